@@ -1,0 +1,749 @@
+/*
+ * wl_oracle.c - CPU restatement of Windlass's quantized-matmul arithmetic.
+ *
+ * TEST INFRASTRUCTURE (the oracle). Loaded only by the tests, the smoke check and the
+ * benchmark's CPU-baseline leg; the product library never links or calls it.
+ *
+ * Build (oracle/Makefile): gcc -O2 -fno-tree-vectorize -ffp-contract=off -fopenmp.
+ * No fast-math and no contraction: every float operation below rounds on its own and in
+ * the order the reference writes it, which is what "bit-exact decode" is measured against.
+ * Each function cites the reference lines it restates.
+ */
+#include "wl_oracle.h"
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------ fp16 (src/Half.cs) */
+
+static float bits_to_float(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static uint32_t float_to_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+/* src/Half.cs:59-90: sign, 5-bit exponent, 10-bit mantissa; subnormals renormalised. */
+float wlo_half_to_float(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h >> 15) << 31;
+    int exp = (h >> 10) & 0x1F;
+    uint32_t mant = h & 0x3FFu;
+    if (exp == 0) {
+        if (mant == 0) return bits_to_float(sign);
+        int shift = 0;
+        while ((mant & 0x400u) == 0) { mant <<= 1; shift++; }
+        /* value = 1.m * 2^(-14 - (shift - 1)) */
+        return bits_to_float(sign | (uint32_t)(127 - 15 - (shift - 1)) << 23 | (mant & 0x3FFu) << 13);
+    }
+    if (exp == 31) return bits_to_float(sign | 0x7F800000u | mant << 13);
+    return bits_to_float(sign | (uint32_t)(exp - 15 + 127) << 23 | mant << 13);
+}
+
+/* src/Half.cs:29-57: NaN keeps a quiet payload bit, overflow -> Inf, RNE everywhere. */
+uint16_t wlo_half_from_float(float value)
+{
+    uint32_t f = float_to_bits(value);
+    uint32_t sign = (f >> 16) & 0x8000u;
+    int e = (int)((f >> 23) & 0xFF);
+    uint32_t m = f & 0x7FFFFFu;
+    if (e == 255) return (uint16_t)(sign | 0x7C00u | (m ? 0x200u : 0u));
+    int ne = e - 127 + 15;
+    if (ne >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (ne <= 0) {
+        if (ne < -10) return (uint16_t)sign;
+        m |= 0x800000u;
+        int shift = 14 - ne;
+        uint32_t hm = m >> shift, rem = m & ((1u << shift) - 1), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (hm & 1u))) hm++;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t h = sign | ((uint32_t)ne << 10) | (m >> 13);
+    uint32_t r = m & 0x1FFFu;
+    if (r > 0x1000u || (r == 0x1000u && (h & 1u))) h++;   /* a carry into the exponent is right */
+    return (uint16_t)h;
+}
+
+float wlo_half_round(float f) { return wlo_half_to_float(wlo_half_from_float(f)); }
+
+void wlo_half_to_float_n(const uint16_t *h, int64_t n, float *out)
+{
+    for (int64_t i = 0; i < n; i++) out[i] = wlo_half_to_float(h[i]);
+}
+
+void wlo_half_from_float_n(const float *f, int64_t n, uint16_t *out)
+{
+    for (int64_t i = 0; i < n; i++) out[i] = wlo_half_from_float(f[i]);
+}
+
+static float H(const uint8_t *p) { return wlo_half_to_float((uint16_t)(p[0] | (p[1] << 8))); }
+static uint32_t U32(const uint8_t *p) { return (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24; }
+
+/* ------------------------------------------------------- Rng (tests/TinyModels.cs:89-97) */
+
+void wlo_rng_init(uint64_t *s, uint64_t seed) { *s = seed * 0x9E3779B97F4A7C15ull + 1; }
+
+uint64_t wlo_rng_next(uint64_t *s)
+{
+    uint64_t v = *s;
+    v ^= v >> 12; v ^= v << 25; v ^= v >> 27;
+    *s = v;
+    return v * 2685821657736338717ull;
+}
+
+static uint8_t rng_byte(uint64_t *s) { return (uint8_t)(wlo_rng_next(s) >> 56); }
+static double rng_uniform(uint64_t *s) { return (double)(wlo_rng_next(s) >> 11) * (1.0 / 9007199254740992.0); }
+static float rng_normal(uint64_t *s)
+{
+    double u = rng_uniform(s), v = rng_uniform(s);
+    if (u < 1e-12) u = 1e-12;
+    return (float)(sqrt(-2 * log(u)) * cos(2 * M_PI * v));
+}
+
+void wlo_rng_bytes(uint64_t *s, int64_t n, uint8_t *out) { for (int64_t i = 0; i < n; i++) out[i] = rng_byte(s); }
+void wlo_rng_uniforms(uint64_t *s, int64_t n, double *out) { for (int64_t i = 0; i < n; i++) out[i] = rng_uniform(s); }
+void wlo_rng_normals(uint64_t *s, int64_t n, float *out) { for (int64_t i = 0; i < n; i++) out[i] = rng_normal(s); }
+
+/* --------------------------------------------------------- layouts (src/Gguf.cs:30-66) */
+
+int wlo_layout(int t, int *be, int *bb)
+{
+    switch (t) {
+    case WLO_F32: *be = 1; *bb = 4; return 1;
+    case WLO_F16: case WLO_BF16: *be = 1; *bb = 2; return 1;
+    case WLO_Q8_0: *be = 32; *bb = 34; return 1;
+    case WLO_Q4_K: *be = 256; *bb = 144; return 1;
+    case WLO_Q6_K: *be = 256; *bb = 210; return 1;
+    case WLO_IQ2_XXS: *be = 256; *bb = 66; return 1;
+    case WLO_IQ4_XS: *be = 256; *bb = 136; return 1;
+    }
+    *be = 0; *bb = 0;
+    return 0;
+}
+
+int wlo_can_decode(int t)
+{
+    int be, bb;
+    return wlo_layout(t, &be, &bb);
+}
+
+int wlo_can_dot(int t)
+{
+    return t == WLO_F32 || t == WLO_F16 || t == WLO_BF16 || t == WLO_Q8_0 || t == WLO_Q4_K || t == WLO_Q6_K;
+}
+
+/* ------------------------------------------------------ I-quant tables (src/IqTables.cs) */
+
+/* kvalues_iq4nl (src/IqTables.cs:22). */
+static const int8_t KVALUES[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
+
+/* iq2xxs_grid (src/IqTables.cs:23-57), stored as 2-bit codes per byte: 0 -> 0x08, 1 -> 0x19,
+ * 2 -> 0x2b (the only byte values the grid holds); byte j of entry i is code bits 2j..2j+1. */
+static const uint16_t IQ2XXS_CODES[256] = {
+    0x0000, 0x0002, 0x0005, 0x0008, 0x000a, 0x0011, 0x0014, 0x0020, 0x0022, 0x0028, 0x002a, 0x0041, 0x0044, 0x0050, 0x0058, 0x0061,
+    0x0064, 0x0080, 0x0082, 0x008a, 0x00a2, 0x0101, 0x0104, 0x0110, 0x0115, 0x0140, 0x0184, 0x0198, 0x0200, 0x0202, 0x0222, 0x0282,
+    0x0401, 0x0404, 0x0410, 0x0421, 0x0424, 0x0440, 0x0442, 0x0448, 0x0460, 0x0481, 0x0484, 0x0490, 0x04a4, 0x0500, 0x0502, 0x0508,
+    0x0520, 0x0546, 0x0569, 0x0580, 0x0591, 0x0609, 0x0610, 0x0640, 0x0684, 0x06a4, 0x0800, 0x0805, 0x0808, 0x0814, 0x0828, 0x0841,
+    0x0844, 0x0850, 0x0852, 0x0888, 0x0904, 0x0940, 0x0a02, 0x0a14, 0x1001, 0x1004, 0x1010, 0x1021, 0x1040, 0x1060, 0x1084, 0x1090,
+    0x1095, 0x1100, 0x1108, 0x1120, 0x1150, 0x115a, 0x1180, 0x1224, 0x1245, 0x1400, 0x1408, 0x1420, 0x1425, 0x1449, 0x1480, 0x1518,
+    0x1562, 0x1600, 0x1616, 0x1801, 0x1804, 0x1810, 0x1840, 0x1881, 0x1900, 0x1905, 0x19a0, 0x1a51, 0x2000, 0x2002, 0x200a, 0x2044,
+    0x2061, 0x2080, 0x2082, 0x2129, 0x2148, 0x2200, 0x2202, 0x2401, 0x2404, 0x2410, 0x2440, 0x2456, 0x2500, 0x2541, 0x2564, 0x2690,
+    0x2808, 0x2820, 0x2894, 0x2a44, 0x4001, 0x4004, 0x4010, 0x4018, 0x4021, 0x4024, 0x4040, 0x4048, 0x4056, 0x4060, 0x4081, 0x4084,
+    0x4090, 0x4100, 0x4120, 0x4161, 0x4180, 0x4185, 0x4201, 0x4210, 0x4248, 0x4256, 0x4268, 0x4400, 0x4408, 0x4420, 0x4480, 0x4499,
+    0x4512, 0x4524, 0x4600, 0x4801, 0x4804, 0x4810, 0x4840, 0x4845, 0x4900, 0x4958, 0x4961, 0x4982, 0x4a45, 0x4a90, 0x5000, 0x5008,
+    0x5011, 0x5019, 0x5020, 0x5080, 0x5088, 0x5104, 0x5142, 0x51a4, 0x5291, 0x5490, 0x5492, 0x550a, 0x5601, 0x5654, 0x5800, 0x5811,
+    0x5819, 0x5864, 0x5940, 0x5a08, 0x6004, 0x6010, 0x6040, 0x6068, 0x6100, 0x6155, 0x6218, 0x6260, 0x6400, 0x6405, 0x6510, 0x6512,
+    0x6584, 0x6842, 0x8000, 0x8002, 0x800a, 0x8041, 0x8082, 0x8104, 0x8118, 0x8140, 0x8211, 0x8401, 0x8404, 0x8410, 0x8415, 0x8440,
+    0x8460, 0x8500, 0x8546, 0x8594, 0x8609, 0x8640, 0x8660, 0x8802, 0x8904, 0x8a11, 0x9004, 0x9010, 0x9024, 0x9040, 0x90a1, 0x9116,
+    0x9180, 0x9245, 0x9400, 0x9422, 0x9444, 0x9551, 0x9881, 0x9920, 0xa002, 0xa050, 0xa085, 0xa109, 0xa200, 0xa418, 0xa850, 0xa904,
+};
+
+static uint64_t IQ2XXS_GRID[256];
+static uint8_t KSIGNS[128];
+
+static void tables_init(void)
+{
+    static const uint8_t vals[3] = { 0x08, 0x19, 0x2b };
+    if (IQ2XXS_GRID[0]) return;
+    for (int i = 0; i < 128; i++) {
+        /* ksigns_iq2xs[i]: i plus an eighth bit that makes the bit count even (src/IqTables.cs:10-21). */
+        KSIGNS[i] = (uint8_t)(i | ((__builtin_popcount(i) & 1) << 7));
+    }
+    for (int i = 0; i < 256; i++) {
+        uint64_t g = 0;
+        for (int j = 0; j < 8; j++) g |= (uint64_t)vals[(IQ2XXS_CODES[i] >> (2 * j)) & 3] << (8 * j);
+        IQ2XXS_GRID[i] = g;
+    }
+}
+
+const uint64_t *wlo_iq2xxs_grid(void) { tables_init(); return IQ2XXS_GRID; }
+const uint8_t *wlo_ksigns_iq2xs(void) { tables_init(); return KSIGNS; }
+const int8_t *wlo_kvalues_iq4nl(void) { return KVALUES; }
+
+/* ------------------------------------------------------------ decoders (src/Quants.cs) */
+
+/* get_scale_min_k4 (src/Quants.cs:321-330). */
+static void scale_min_k4(int j, const uint8_t *q, int *sc, int *m)
+{
+    if (j < 4) { *sc = q[j] & 63; *m = q[j + 4] & 63; }
+    else {
+        *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* src/Quants.cs:251-259: y = q * d. */
+static void dec_q8_0(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 32; i++, b += 34, y += 32) {
+        float d = H(b);
+        const int8_t *q = (const int8_t *)(b + 2);
+        for (int j = 0; j < 32; j++) y[j] = (float)q[j] * d;
+    }
+}
+
+/* src/Quants.cs:332-350: d1 = d*s, m1 = dmin*m, y = d1*nibble - m1. */
+static void dec_q4_k(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 256; i++, b += 144) {
+        float d = H(b), min = H(b + 2);
+        const uint8_t *sc = b + 4, *q = b + 16;
+        for (int j = 0, idx = 0; j < 256; j += 64, q += 32, idx += 2) {
+            int s, m;
+            scale_min_k4(idx, sc, &s, &m);
+            float d1 = d * (float)s, m1 = min * (float)m;
+            scale_min_k4(idx + 1, sc, &s, &m);
+            float d2 = d * (float)s, m2 = min * (float)m;
+            for (int l = 0; l < 32; l++) *y++ = d1 * (float)(q[l] & 0xF) - m1;
+            for (int l = 0; l < 32; l++) *y++ = d2 * (float)(q[l] >> 4) - m2;
+        }
+    }
+}
+
+/* src/Quants.cs:372-396: y = (d * sc) * (q6 - 32). */
+static void dec_q6_k(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 256; i++, b += 210) {
+        float d = H(b + 208);
+        const uint8_t *ql = b, *qh = b + 128;
+        const int8_t *sc = (const int8_t *)(b + 192);
+        for (int k = 0; k < 256; k += 128, y += 128, ql += 64, qh += 32, sc += 8) {
+            for (int l = 0; l < 32; l++) {
+                int s = l / 16;
+                int q1 = ((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                int q2 = ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                y[l] = d * (float)sc[s] * (float)q1;
+                y[l + 32] = d * (float)sc[s + 2] * (float)q2;
+                y[l + 64] = d * (float)sc[s + 4] * (float)q3;
+                y[l + 96] = d * (float)sc[s + 6] * (float)q4;
+            }
+        }
+    }
+}
+
+/* src/IQuants.cs:60-80: ls = low4 | high2 << 4, dl = d * (ls - 32), y = dl * kvalues[nibble]. */
+static void dec_iq4_xs(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 256; i++, b += 136) {
+        float d = H(b);
+        int scales_h = b[2] | (b[3] << 8);
+        const uint8_t *scales_l = b + 4, *q = b + 8;
+        for (int ib = 0; ib < 8; ib++, q += 16, y += 32) {
+            int ls = ((scales_l[ib / 2] >> (4 * (ib % 2))) & 0xF) | (((scales_h >> (2 * ib)) & 3) << 4);
+            float dl = d * (float)(ls - 32);
+            for (int j = 0; j < 16; j++) {
+                y[j] = dl * (float)KVALUES[q[j] & 0xF];
+                y[j + 16] = dl * (float)KVALUES[q[j] >> 4];
+            }
+        }
+    }
+}
+
+/* src/IQuants.cs:147-170: db = d * (0.5 + scale4) * 0.25, y = db * gridbyte * sign. */
+static void dec_iq2_xxs(const uint8_t *b, int64_t n, float *y)
+{
+    tables_init();
+    for (int64_t i = 0; i < n / 256; i++, b += 66) {
+        float d = H(b);
+        const uint8_t *qs = b + 2;
+        for (int ib32 = 0; ib32 < 8; ib32++) {
+            uint32_t aux0 = U32(qs + 8 * ib32), aux1 = U32(qs + 8 * ib32 + 4);
+            float db = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
+            for (int l = 0; l < 4; l++) {
+                uint64_t g = IQ2XXS_GRID[(aux0 >> (8 * l)) & 0xFF];
+                int signs = KSIGNS[(aux1 >> (7 * l)) & 127];
+                for (int j = 0; j < 8; j++)
+                    y[j] = db * (float)(uint8_t)(g >> (8 * j)) * ((signs & (1 << j)) ? -1.0f : 1.0f);
+                y += 8;
+            }
+        }
+    }
+}
+
+static float bf16_to_float(uint16_t v) { return bits_to_float((uint32_t)v << 16); }
+
+/* Quants.DecodeRow dispatch (src/Quants.cs:32-52; src/IQuants.cs:27-42). */
+int wlo_decode_row(int t, const uint8_t *src, int64_t n, float *dst)
+{
+    switch (t) {
+    case WLO_F32: memcpy(dst, src, (size_t)n * 4); return 0;
+    case WLO_F16: for (int64_t i = 0; i < n; i++) dst[i] = H(src + 2 * i); return 0;
+    case WLO_BF16: for (int64_t i = 0; i < n; i++) dst[i] = bf16_to_float((uint16_t)(src[2 * i] | src[2 * i + 1] << 8)); return 0;
+    case WLO_Q8_0: dec_q8_0(src, n, dst); return 0;
+    case WLO_Q4_K: dec_q4_k(src, n, dst); return 0;
+    case WLO_Q6_K: dec_q6_k(src, n, dst); return 0;
+    case WLO_IQ4_XS: dec_iq4_xs(src, n, dst); return 0;
+    case WLO_IQ2_XXS: dec_iq2_xxs(src, n, dst); return 0;
+    }
+    return -1;
+}
+
+/* ---------------------------------------------------------- fused dots (src/Quants.cs) */
+
+/* Transformer.Dot (src/Transformer.cs:466-477): four partial chains, then (s0+s1)+(s2+s3). */
+static float dot_f32(const float *a, const float *b, int n)
+{
+    float s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+        s0 += a[i] * b[i]; s1 += a[i + 1] * b[i + 1];
+        s2 += a[i + 2] * b[i + 2]; s3 += a[i + 3] * b[i + 3];
+    }
+    for (; i < n; i++) s0 += a[i] * b[i];
+    return (s0 + s1) + (s2 + s3);
+}
+
+/* Quants.DotRow (src/Quants.cs:67-187). */
+int wlo_dot_row(int t, const uint8_t *b, const float *x, int n, float *out)
+{
+    switch (t) {
+    case WLO_F32:
+        /* DotRow hands the row to Transformer.Dot as a float pointer (src/Quants.cs:71). */
+        *out = dot_f32((const float *)b, x, n);
+        return 0;
+    case WLO_F16: case WLO_BF16: {          /* src/Quants.cs:72-85 */
+        float s0 = 0, s1 = 0;
+        for (int i = 0; i < n; i += 2) {
+            uint16_t h0 = (uint16_t)(b[2 * i] | b[2 * i + 1] << 8), h1 = (uint16_t)(b[2 * i + 2] | b[2 * i + 3] << 8);
+            float w0 = t == WLO_F16 ? wlo_half_to_float(h0) : bf16_to_float(h0);
+            float w1 = t == WLO_F16 ? wlo_half_to_float(h1) : bf16_to_float(h1);
+            s0 += w0 * x[i]; s1 += w1 * x[i + 1];
+        }
+        *out = s0 + s1;
+        return 0;
+    }
+    case WLO_Q8_0: {                          /* src/Quants.cs:86-97 */
+        float sum = 0;
+        for (int i = 0; i < n / 32; i++, b += 34, x += 32) {
+            const int8_t *q = (const int8_t *)(b + 2);
+            float s0 = 0, s1 = 0;
+            for (int j = 0; j < 32; j += 2) { s0 += (float)q[j] * x[j]; s1 += (float)q[j + 1] * x[j + 1]; }
+            sum += H(b) * (s0 + s1);
+        }
+        *out = sum;
+        return 0;
+    }
+    case WLO_Q4_K: {                          /* src/Quants.cs:110-133 */
+        float sum = 0;
+        for (int i = 0; i < n / 256; i++, b += 144) {
+            float d = H(b), min = H(b + 2);
+            const uint8_t *sc = b + 4, *q = b + 16;
+            for (int j = 0; j < 4; j++, q += 32, x += 64) {
+                int s1, m1, s2, m2;
+                scale_min_k4(2 * j, sc, &s1, &m1);
+                scale_min_k4(2 * j + 1, sc, &s2, &m2);
+                float a1 = 0, a2 = 0, x1 = 0, x2 = 0;
+                for (int l = 0; l < 32; l++) {
+                    float xl = x[l], xh = x[l + 32];
+                    a1 += (float)(q[l] & 0xF) * xl; x1 += xl;
+                    a2 += (float)(q[l] >> 4) * xh; x2 += xh;
+                }
+                sum += d * ((float)s1 * a1 + (float)s2 * a2) - min * ((float)m1 * x1 + (float)m2 * x2);
+            }
+        }
+        *out = sum;
+        return 0;
+    }
+    case WLO_Q6_K: {                          /* src/Quants.cs:159-184 */
+        float sum = 0, acc[8];
+        for (int i = 0; i < n / 256; i++, b += 210) {
+            float d = H(b + 208);
+            const uint8_t *ql = b, *qh = b + 128;
+            const int8_t *sc = (const int8_t *)(b + 192);
+            for (int k = 0; k < 2; k++, ql += 64, qh += 32, sc += 8, x += 128) {
+                for (int g = 0; g < 8; g++) acc[g] = 0;
+                for (int l = 0; l < 32; l++) {
+                    int s = l >> 4;
+                    acc[s] += (float)(((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32) * x[l];
+                    acc[s + 2] += (float)(((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32) * x[l + 32];
+                    acc[s + 4] += (float)(((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32) * x[l + 64];
+                    acc[s + 6] += (float)(((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32) * x[l + 96];
+                }
+                float part = 0;
+                for (int g = 0; g < 8; g++) part += (float)sc[g] * acc[g];
+                sum += d * part;
+            }
+        }
+        *out = sum;
+        return 0;
+    }
+    }
+    return -1;
+}
+
+/* ------------------------------------------------------- FastMath.Block (src/FastMath.cs) */
+
+/* src/FastMath.cs:216-264: one accumulator chain per (row, token), summed in index order;
+ * 4 rows x 2 tokens per pass, then the token tail, then the row tail. */
+void wlo_block(const float *w, int ws, int nr, const float *x, int xs, int nt, int cols, float *y, int ys)
+{
+    int r = 0;
+    for (; r + 4 <= nr; r += 4) {
+        const float *w0 = w + (int64_t)r * ws, *w1 = w0 + ws, *w2 = w1 + ws, *w3 = w2 + ws;
+        int t = 0;
+        for (; t + 2 <= nt; t += 2) {
+            const float *xa = x + (int64_t)t * xs, *xb = xa + xs;
+            float a0 = 0, a1 = 0, a2 = 0, a3 = 0, b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+            for (int i = 0; i < cols; i++) {
+                float va = xa[i], vb = xb[i];
+                float u0 = w0[i], u1 = w1[i], u2 = w2[i], u3 = w3[i];
+                a0 += u0 * va; a1 += u1 * va; a2 += u2 * va; a3 += u3 * va;
+                b0 += u0 * vb; b1 += u1 * vb; b2 += u2 * vb; b3 += u3 * vb;
+            }
+            float *ya = y + (int64_t)t * ys + r, *yb = ya + ys;
+            ya[0] = a0; ya[1] = a1; ya[2] = a2; ya[3] = a3;
+            yb[0] = b0; yb[1] = b1; yb[2] = b2; yb[3] = b3;
+        }
+        for (; t < nt; t++) {
+            const float *xa = x + (int64_t)t * xs;
+            float a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+            for (int i = 0; i < cols; i++) {
+                float va = xa[i];
+                a0 += w0[i] * va; a1 += w1[i] * va; a2 += w2[i] * va; a3 += w3[i] * va;
+            }
+            float *ya = y + (int64_t)t * ys + r;
+            ya[0] = a0; ya[1] = a1; ya[2] = a2; ya[3] = a3;
+        }
+    }
+    for (; r < nr; r++) {
+        const float *wr = w + (int64_t)r * ws;
+        for (int t = 0; t < nt; t++) {
+            const float *xa = x + (int64_t)t * xs;
+            float s = 0;
+            for (int i = 0; i < cols; i++) s += wr[i] * xa[i];
+            y[(int64_t)t * ys + r] = s;
+        }
+    }
+}
+
+/* ------------------------------------------------- MatMul dispatch (src/Transformer.cs) */
+
+#define ROW_TILE 32   /* src/Transformer.cs:479 */
+
+static int n_threads(int threads)
+{
+#ifdef _OPENMP
+    return threads > 0 ? threads : omp_get_max_threads();
+#else
+    (void)threads;
+    return 1;
+#endif
+}
+
+/* Transformer.MatMul (src/Transformer.cs:483-537) without --int-dot, plus MatMulEach
+ * (src/Transformer.cs:544-561) when each_token is set. Tiles of 32 rows run in parallel. */
+int wlo_matmul(int type, const uint8_t *data, int rows, int cols, int64_t row_bytes,
+               const float *x, int T, float *y, int each_token, int threads)
+{
+    if (!wlo_can_decode(type)) return -1;
+    int tiles = (rows + ROW_TILE - 1) / ROW_TILE;
+    int nth = n_threads(threads);
+    if ((T == 1 || each_token) && wlo_can_dot(type)) {
+        /* T == 1: DotRow per row (:494-502); each_token: DotRow per (row, token) (:551-560). */
+        #pragma omp parallel for schedule(dynamic, 1) num_threads(nth)
+        for (int tile = 0; tile < tiles; tile++) {
+            int r0 = tile * ROW_TILE, r1 = r0 + ROW_TILE < rows ? r0 + ROW_TILE : rows;
+            for (int r = r0; r < r1; r++)
+                for (int t = 0; t < T; t++)
+                    wlo_dot_row(type, data + (int64_t)r * row_bytes, x + (int64_t)t * cols, cols, y + (int64_t)t * rows + r);
+        }
+        return 0;
+    }
+    /* Decode a 32-row tile, then Block (:526-536). */
+    #pragma omp parallel num_threads(nth)
+    {
+        float *scratch = (float *)malloc(sizeof(float) * ROW_TILE * (size_t)cols);
+        #pragma omp for schedule(dynamic, 1)
+        for (int tile = 0; tile < tiles; tile++) {
+            int r0 = tile * ROW_TILE, r1 = r0 + ROW_TILE < rows ? r0 + ROW_TILE : rows;
+            for (int r = r0; r < r1; r++)
+                wlo_decode_row(type, data + (int64_t)r * row_bytes, cols, scratch + (int64_t)(r - r0) * cols);
+            wlo_block(scratch, cols, r1 - r0, x, cols, T, cols, y + r0, rows);
+        }
+        free(scratch);
+    }
+    return 0;
+}
+
+static int64_t row_bytes_of(int type, int cols)
+{
+    int be, bb;
+    if (!wlo_layout(type, &be, &bb)) return -1;
+    return (int64_t)(cols / be) * bb;
+}
+
+/* SwiGlu (src/Transformer.cs:241-251). The exponential is .NET Math.Exp on a double, cast
+ * to float; libm exp stands in for it. */
+int wlo_swiglu(int gtype, const uint8_t *gate, int64_t grb, int utype, const uint8_t *up, int64_t urb,
+               int dtype, const uint8_t *down, int64_t drb, int ff, int embd,
+               const float *x, int T, float *out, int each_token, int threads)
+{
+    float *g = (float *)malloc(sizeof(float) * (size_t)T * ff);
+    float *u = (float *)malloc(sizeof(float) * (size_t)T * ff);
+    int rc = wlo_matmul(gtype, gate, ff, embd, grb, x, T, g, each_token, threads);
+    if (!rc) rc = wlo_matmul(utype, up, ff, embd, urb, x, T, u, each_token, threads);
+    if (!rc) {
+        for (int64_t i = 0; i < (int64_t)T * ff; i++) {
+            float a = g[i];
+            g[i] = a / (1.0f + (float)exp((double)(-a))) * u[i];
+        }
+        rc = wlo_matmul(dtype, down, embd, ff, drb, g, T, out, each_token, threads);
+    }
+    free(g); free(u);
+    return rc;
+}
+
+#define MIN_EXPERT_WEIGHT_SUM 6.103515625e-5f   /* src/Transformer.cs:253 */
+
+/* Route (src/Transformer.cs:315-340): softmax with a double denominator, top-k with ties to
+ * the lower id, optional renormalisation clamped at the smallest fp16 normal. */
+void wlo_route(const float *logits, int n, int k, int renorm, int *sel, float *wts, int *count)
+{
+    float max = -INFINITY;
+    for (int i = 0; i < n; i++) if (logits[i] > max) max = logits[i];
+    float *p = (float *)malloc(sizeof(float) * (size_t)n);
+    char *taken = (char *)calloc((size_t)n, 1);
+    double sum = 0;
+    for (int i = 0; i < n; i++) { p[i] = (float)exp((double)(logits[i] - max)); sum += p[i]; }
+    float inv = (float)(1.0 / sum);
+    for (int i = 0; i < n; i++) p[i] *= inv;
+    float chosen = 0;
+    for (int j = 0; j < k; j++) {
+        int best = -1;
+        for (int i = 0; i < n; i++) if (!taken[i] && (best < 0 || p[i] > p[best])) best = i;
+        taken[best] = 1;
+        sel[j] = best; wts[j] = p[best];
+        chosen += p[best];
+        if (count) count[best]++;
+    }
+    if (renorm) {
+        float div = chosen > MIN_EXPERT_WEIGHT_SUM ? chosen : MIN_EXPERT_WEIGHT_SUM;
+        for (int j = 0; j < k; j++) wts[j] /= div;
+    }
+    free(p); free(taken);
+}
+
+/* MoeFfn (src/Transformer.cs:259-294) after the router MatMul: route every token, then for
+ * each expert in ascending id gather its tokens, run SwiGlu on the expert's slices and
+ * scatter-add the weighted rows. */
+int wlo_moe_ffn(const float *logits, int ne, int k, int renorm,
+                int gtype, const uint8_t *gate, int utype, const uint8_t *up,
+                int dtype, const uint8_t *down, int ff, int embd,
+                const float *x, int T, float *out, int each_token, int threads, int *expert_runs)
+{
+    int64_t grb = row_bytes_of(gtype, embd), urb = row_bytes_of(utype, embd), drb = row_bytes_of(dtype, ff);
+    if (grb < 0 || urb < 0 || drb < 0) return -1;
+    int *sel = (int *)malloc(sizeof(int) * (size_t)T * k);
+    float *wts = (float *)malloc(sizeof(float) * (size_t)T * k);
+    int *count = (int *)calloc((size_t)ne, sizeof(int));
+    for (int t = 0; t < T; t++) wlo_route(logits + (int64_t)t * ne, ne, k, renorm, sel + t * k, wts + t * k, count);
+    memset(out, 0, sizeof(float) * (size_t)T * embd);
+    int rc = 0, runs = 0;
+    for (int e = 0; e < ne && !rc; e++) {
+        int n = count[e];
+        if (!n) continue;
+        int *toks = (int *)malloc(sizeof(int) * (size_t)n);
+        float *w = (float *)malloc(sizeof(float) * (size_t)n);
+        float *xe = (float *)malloc(sizeof(float) * (size_t)n * embd);
+        float *ye = (float *)malloc(sizeof(float) * (size_t)n * embd);
+        int at = 0;
+        for (int t = 0; t < T; t++)
+            for (int j = 0; j < k; j++)
+                if (sel[t * k + j] == e) {
+                    toks[at] = t; w[at] = wts[t * k + j];
+                    memcpy(xe + (int64_t)at * embd, x + (int64_t)t * embd, sizeof(float) * (size_t)embd);
+                    at++;
+                }
+        runs++;
+        rc = wlo_swiglu(gtype, gate + (int64_t)e * ff * grb, grb, utype, up + (int64_t)e * ff * urb, urb,
+                        dtype, down + (int64_t)e * embd * drb, drb, ff, embd, xe, n, ye, each_token, threads);
+        for (int i = 0; i < n && !rc; i++) {
+            float *o = out + (int64_t)toks[i] * embd;
+            const float *r = ye + (int64_t)i * embd;
+            for (int d = 0; d < embd; d++) o[d] += w[i] * r[d];
+        }
+        free(toks); free(w); free(xe); free(ye);
+    }
+    if (expert_runs) *expert_runs = runs;
+    free(sel); free(wts); free(count);
+    return rc;
+}
+
+/* ---------------------------------------------- test matrices (tests/TinyModels.cs) */
+
+/* Offsets of the fp16 scale fields per type (tests/TinyModels.cs:314-329). */
+static int scale_fields(int t, int *f)
+{
+    switch (t) {
+    case WLO_Q8_0: case WLO_IQ4_XS: case WLO_IQ2_XXS: f[0] = 0; return 1;
+    case WLO_Q4_K: f[0] = 0; f[1] = 2; return 2;
+    case WLO_Q6_K: f[0] = 208; return 1;
+    }
+    return 0;
+}
+
+/* TinyModels.Matrix (tests/TinyModels.cs:344-381). */
+int wlo_matrix(uint64_t *rng, int t, int rows, int cols, float rms, uint8_t *data)
+{
+    int be, bb;
+    if (!wlo_layout(t, &be, &bb)) return -1;
+    int64_t n = (int64_t)rows * cols;
+    int64_t nbytes = n / be * bb;
+    if (t == WLO_F32 || t == WLO_F16 || t == WLO_BF16) {
+        for (int64_t i = 0; i < n; i++) {
+            float v = rms * rng_normal(rng);
+            if (t == WLO_F32) memcpy(data + 4 * i, &v, 4);
+            else {
+                uint16_t h = t == WLO_F16 ? wlo_half_from_float(v) : (uint16_t)(float_to_bits(v) >> 16);
+                data[2 * i] = (uint8_t)h; data[2 * i + 1] = (uint8_t)(h >> 8);
+            }
+        }
+        return 0;
+    }
+    for (int64_t i = 0; i < nbytes; i++) data[i] = rng_byte(rng);
+    int fields[2];
+    int nf = scale_fields(t, fields);
+    if (!nf) return -1;
+    int64_t blocks = nbytes / bb;
+    float tmp[256];
+    uint16_t one = wlo_half_from_float(1.0f);
+    for (int64_t b = 0; b < blocks; b++) {
+        uint8_t *o = data + b * bb;
+        for (int i = 0; i < nf; i++) { o[fields[i]] = (uint8_t)one; o[fields[i] + 1] = (uint8_t)(one >> 8); }
+        double sum = 0;
+        wlo_decode_row(t, o, be, tmp);
+        for (int i = 0; i < be; i++) { float v2 = tmp[i] * tmp[i]; sum += v2; }
+        double ms = sum / be;
+        float scale = (float)(rms / sqrt(ms > 1e-12 ? ms : 1e-12));
+        scale *= (float)(0.75 + 0.5 * rng_uniform(rng));
+        uint16_t h = wlo_half_from_float(scale);
+        for (int i = 0; i < nf; i++) { o[fields[i]] = (uint8_t)h; o[fields[i] + 1] = (uint8_t)(h >> 8); }
+    }
+    return 0;
+}
+
+/* ------------------------------------------- integer dots (src/FastMath.cs:35-214) */
+
+/* C# Math.Round(v, MidpointRounding.AwayFromZero) and Math.Round(v) (to even), on doubles. */
+static double round_away(double v) { return v < 0 ? -floor(-v + 0.5) : floor(v + 0.5); }
+static double round_even(double v) { return nearbyint(v); }
+
+void wlo_quantize_row(const float *x, int cols, int k, int8_t *q, float *d, int16_t *bsums)
+{
+    int bs = k ? 256 : 32, nb = cols / bs;
+    for (int b = 0; b < nb; b++) {
+        const float *xb = x + b * bs;
+        int8_t *qb = q + b * bs;
+        if (!k) {                                             /* src/FastMath.cs:54-61 */
+            float amax = 0;
+            for (int j = 0; j < 32; j++) { float ax = fabsf(xb[j]); if (ax > amax) amax = ax; }
+            float dd = amax / 127.0f, id = dd != 0 ? 1.0f / dd : 0.0f;
+            for (int j = 0; j < 32; j++) qb[j] = (int8_t)(int)round_away((double)(xb[j] * id));
+            d[b] = wlo_half_round(dd);
+        } else {                                              /* src/FastMath.cs:62-86 */
+            float max = 0, amax = 0;
+            for (int j = 0; j < 256; j++) { float ax = fabsf(xb[j]); if (ax > amax) { amax = ax; max = xb[j]; } }
+            if (amax == 0) {
+                d[b] = 0;
+                memset(qb, 0, 256);
+                for (int j = 0; j < 16; j++) bsums[b * 16 + j] = 0;
+                continue;
+            }
+            float iscale = -127.0f / max;
+            for (int j = 0; j < 256; j++) {
+                int v = (int)round_even((double)(iscale * xb[j]));
+                qb[j] = (int8_t)(v > 127 ? 127 : v);
+            }
+            for (int j = 0; j < 16; j++) {
+                int s = 0;
+                for (int l = 0; l < 16; l++) s += qb[j * 16 + l];
+                bsums[b * 16 + j] = (int16_t)s;
+            }
+            d[b] = 1.0f / iscale;
+        }
+    }
+}
+
+int wlo_int_dot(int t, const uint8_t *b, const int8_t *q, const float *d, const int16_t *bsums, int n, float *out)
+{
+    switch (t) {
+    case WLO_Q8_0: {                                          /* src/FastMath.cs:111-122 */
+        float sum = 0;
+        for (int i = 0; i < n / 32; i++, b += 34, q += 32) {
+            const int8_t *w = (const int8_t *)(b + 2);
+            int s0 = 0, s1 = 0;
+            for (int j = 0; j < 32; j += 2) { s0 += w[j] * q[j]; s1 += w[j + 1] * q[j + 1]; }
+            sum += H(b) * d[i] * (float)(s0 + s1);
+        }
+        *out = sum;
+        return 0;
+    }
+    case WLO_Q4_K: {                                          /* src/FastMath.cs:135-157 */
+        float sum = 0;
+        for (int i = 0; i < n / 256; i++, b += 144, q += 256, bsums += 16) {
+            float dd = H(b), dmin = H(b + 2);
+            const uint8_t *sc = b + 4, *w = b + 16;
+            int sumi = 0, summ = 0;
+            for (int j = 0; j < 4; j++, w += 32) {
+                int s1, m1, s2, m2;
+                scale_min_k4(2 * j, sc, &s1, &m1);
+                scale_min_k4(2 * j + 1, sc, &s2, &m2);
+                const int8_t *qa = q + 64 * j, *qb = qa + 32;
+                int a1 = 0, a2 = 0;
+                for (int l = 0; l < 32; l++) { a1 += (w[l] & 0xF) * qa[l]; a2 += (w[l] >> 4) * qb[l]; }
+                sumi += s1 * a1 + s2 * a2;
+                summ += m1 * (bsums[4 * j] + bsums[4 * j + 1]) + m2 * (bsums[4 * j + 2] + bsums[4 * j + 3]);
+            }
+            sum += d[i] * (dd * (float)sumi - dmin * (float)summ);
+        }
+        *out = sum;
+        return 0;
+    }
+    case WLO_Q6_K: {                                          /* src/FastMath.cs:185-211 */
+        float sum = 0;
+        int acc[8];
+        for (int i = 0; i < n / 256; i++, b += 210, q += 256) {
+            float dd = H(b + 208);
+            const uint8_t *ql = b, *qh = b + 128;
+            const int8_t *sc = (const int8_t *)(b + 192), *x = q;
+            for (int k = 0; k < 2; k++, ql += 64, qh += 32, sc += 8, x += 128) {
+                for (int g = 0; g < 8; g++) acc[g] = 0;
+                for (int l = 0; l < 32; l++) {
+                    int s = l >> 4;
+                    acc[s] += (((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32) * x[l];
+                    acc[s + 2] += (((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32) * x[l + 32];
+                    acc[s + 4] += (((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32) * x[l + 64];
+                    acc[s + 6] += (((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32) * x[l + 96];
+                }
+                int part = 0;
+                for (int g = 0; g < 8; g++) part += sc[g] * acc[g];
+                sum += d[i] * dd * (float)part;
+            }
+        }
+        *out = sum;
+        return 0;
+    }
+    }
+    return -1;
+}

@@ -1,0 +1,100 @@
+"""Writes tests/golden/reference_pins.json: the known answers the reference's own tests hold
+for this path, transcribed by hand from those tests (the C# cannot run here).
+
+Every entry names the reference test it comes from. Run from the repository root:
+    python tests/golden/make_golden.py
+The output is data (inputs and expected outputs); nothing here executes reference code.
+"""
+import json
+import math
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def iq2xxs_hand_block():
+    # tests/IQuantTests.cs:330-351: d = 1 (0x3C00); sub-block 0 uses grid words 0..3, sign
+    # indices 0, 1, 2, 127 and scale nibble 3 (db = 0.875); every other byte is zero.
+    blk = [0] * 66
+    blk[0], blk[1] = 0x00, 0x3C
+    blk[2], blk[3], blk[4], blk[5] = 0, 1, 2, 3
+    aux1 = (3 << 28) | (0 << 0) | (1 << 7) | (2 << 14) | (127 << 21)
+    for i in range(4):
+        blk[6 + i] = (aux1 >> (8 * i)) & 0xFF
+    want = [0.0] * 256
+    for j in range(8):
+        want[j] = 0.875 * 8                                              # group 0: +7.0
+        want[8 + j] = 0.875 * (43 if j == 0 else 8) * (-1 if j in (0, 7) else 1)
+        want[16 + j] = 0.875 * (25 if j < 2 else 8) * (-1 if j in (1, 7) else 1)
+        want[24 + j] = -0.875 * (43 if j == 1 else 8)
+    for e in range(32, 256):
+        want[e] = 1.0                                                    # db = 0.125, grid byte 8
+    return {"source": "tests/IQuantTests.cs:330-351", "block": blk, "want": want}
+
+
+def route_cases():
+    # tests/MoeTests.cs:116-149 (RoutingMath).
+    z = math.exp(1) + math.exp(3) + math.exp(2) + 1
+    p1, p2 = math.exp(3) / z, math.exp(2) / z
+    return {
+        "source": "tests/MoeTests.cs:116-149",
+        "tol": 1e-6,
+        "cases": [
+            {"logits": [1, 3, 2, 0], "k": 2, "renorm": False, "sel": [1, 2], "wts": [p1, p2],
+             "count": [0, 1, 1, 0]},
+            {"logits": [1, 3, 2, 0], "k": 2, "renorm": True, "sel": [1, 2],
+             "wts": [p1 / (p1 + p2), p2 / (p1 + p2)], "count": [0, 1, 1, 0]},
+            {"logits": [2, 2, 2, 2], "k": 2, "renorm": False, "sel": [0, 1], "wts": [0.25, 0.25],
+             "count": [1, 1, 0, 0]},
+            {"logits": [2, 2, 2, 2], "k": 2, "renorm": True, "sel": [0, 1], "wts": [0.5, 0.5],
+             "count": [1, 1, 0, 0]},
+            {"logits": [1, 3, 2, 0], "k": 4, "renorm": True, "sel": [1, 2, 0, 3], "wts_sum": 1.0,
+             "count": [1, 1, 1, 1]},
+            {"logits": [0, 5, 0, 0], "k": 1, "renorm": True, "sel": [1], "wts": [1.0], "exact": True,
+             "count": [0, 1, 0, 0]},
+            {"logits": [9, 0, 0, 0], "k": 1, "renorm": True, "sel": [0], "wts": [1.0], "exact": True,
+             "count": [1, 0, 0, 0]},
+        ],
+    }
+
+
+def tables():
+    # tests/IQuantTests.cs:251-317 (Tables) and src/Gguf.cs:19-66 (ids and layouts).
+    return {
+        "source": "tests/IQuantTests.cs:51,251-317",
+        "kmask": [1 << i for i in range(8)],
+        "kvalues": [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113],
+        "iq2xxs_grid_fnv1a64": "0xbb4ee025b5ac6e8e",
+        "iq2xxs_grid_spots": {"0": "0x0808080808080808", "1": "0x080808080808082b",
+                              "3": "0x0808080808082b08"},
+        "iq2xxs_grid_bytes": [8, 0x19, 0x2B],
+        "ids": {"f32": 0, "f16": 1, "q8_0": 8, "q4_K": 12, "q6_K": 14, "iq2_xxs": 16, "iq4_xs": 23,
+                "bf16": 30},
+        "layouts": {"q8_0": [32, 34], "q4_K": [256, 144], "q6_K": [256, 210],
+                    "iq2_xxs": [256, 66], "iq4_xs": [256, 136], "f32": [1, 4], "f16": [1, 2],
+                    "bf16": [1, 2]},
+        "layout_source": "src/Gguf.cs:30-66; tests/IQuantTests.cs:375-380",
+    }
+
+
+def quantizer_pins():
+    # tests/FastMathTests.cs:44-69 (ActivationQuantizers): x = (i-16)*0.5, amax 8.
+    return {
+        "source": "tests/FastMathTests.cs:44-69",
+        "q8_0_x": [(i - 16) * 0.5 for i in range(32)],
+        "q8_0_q0": -127, "q8_0_q16": 0,
+        "q8_k_x": [6.0 if i == 10 else float((i % 7) - 3) for i in range(256)],
+        "q8_k_q10": -127, "q8_k_dq10": 6.0, "q8_k_tol": 1e-5,
+    }
+
+
+def main():
+    out = {"iq2xxs_hand": iq2xxs_hand_block(), "route": route_cases(), "tables": tables(),
+           "quantizers": quantizer_pins()}
+    with open(os.path.join(HERE, "reference_pins.json"), "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+
+
+if __name__ == "__main__":
+    main()

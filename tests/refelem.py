@@ -1,0 +1,124 @@
+"""Independent element-by-element decoders used to pin the oracle's decoders.
+
+Each function computes element e of a block straight from the block layout (byte offsets of
+the fields), in the style of the reference's own ``RefElement`` (tests/IQuantTests.cs:89-194):
+no loops over sub-blocks, no shared helpers with the oracle. ``exact=True`` evaluates the
+float32 operation sequence the reference writes for that element (each op rounded), so the
+result can be compared bit for bit; ``exact=False`` evaluates in float64 for the tolerance
+checks of the reference's tests.
+"""
+import numpy as np
+
+KVALUES = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+
+
+def fp16(bits):
+    """IEEE half -> float64 from the bit fields (independent of any table)."""
+    bits = int(bits)
+    sign, exp, man = (bits >> 15) & 1, (bits >> 10) & 31, bits & 1023
+    if exp == 0:
+        v = man / 1024.0 * 2.0 ** -14
+    elif exp == 31:
+        v = float("inf") if man == 0 else float("nan")
+    else:
+        v = (1 + man / 1024.0) * 2.0 ** (exp - 15)
+    return -v if sign else v
+
+
+def u16(b, o):
+    return int(b[o]) | int(b[o + 1]) << 8
+
+
+def u32(b, o):
+    return int(b[o]) | int(b[o + 1]) << 8 | int(b[o + 2]) << 16 | int(b[o + 3]) << 24
+
+
+def sign_byte(idx7):
+    return idx7 | ((bin(idx7).count("1") & 1) << 7)
+
+
+def _f(v, exact):
+    return np.float32(v) if exact else float(v)
+
+
+def q8_0(b, o, e, exact):
+    d = fp16(u16(b, o))
+    q = int(np.int8(np.uint8(b[o + 2 + e])))
+    return np.float32(q) * np.float32(d) if exact else q * d
+
+
+def q4_k(b, o, e, exact):
+    d, dmin = fp16(u16(b, o)), fp16(u16(b, o + 2))
+    sub = e // 32                       # sub-block 0..7
+    pair, high = sub // 2, sub % 2      # 64-element group and which nibble
+    byte = b[o + 16 + 32 * pair + e % 32]
+    q = (byte >> 4) if high else (byte & 15)
+    sc = b[o + 4: o + 16]
+    if sub < 4:
+        s, m = sc[sub] & 63, sc[sub + 4] & 63
+    else:
+        s = (sc[sub + 4] & 15) | ((sc[sub - 4] >> 6) << 4)
+        m = (sc[sub + 4] >> 4) | ((sc[sub] >> 6) << 4)
+    if exact:
+        d1 = np.float32(d) * np.float32(s)
+        m1 = np.float32(dmin) * np.float32(m)
+        return d1 * np.float32(q) - m1
+    return d * s * q - dmin * m
+
+
+def q6_k(b, o, e, exact):
+    d = fp16(u16(b, o + 208))
+    half, r = e // 128, e % 128         # 128-element half, position inside it
+    quarter, l = r // 32, r % 32        # which of the four 32-runs, index l
+    ql = b[o + 64 * half + l + (32 if quarter in (1, 3) else 0)]
+    low4 = (ql >> 4) if quarter >= 2 else (ql & 15)
+    qh = b[o + 128 + 32 * half + l]
+    high2 = (qh >> (2 * quarter)) & 3
+    q = (low4 | (high2 << 4)) - 32
+    sc = int(np.int8(np.uint8(b[o + 192 + 8 * half + l // 16 + 2 * quarter])))
+    if exact:
+        return np.float32(d) * np.float32(sc) * np.float32(q)
+    return d * sc * q
+
+
+def iq4_xs(b, o, e, exact):
+    d = fp16(u16(b, o))
+    sub = e // 32
+    low4 = (b[o + 4 + sub // 2] >> (4 * (sub % 2))) & 15
+    high2 = (u16(b, o + 2) >> (2 * sub)) & 3
+    ls = low4 | (high2 << 4)
+    within = e % 32
+    qb = b[o + 8 + 16 * sub + within % 16]
+    nib = (qb & 15) if within < 16 else (qb >> 4)
+    if exact:
+        return np.float32(d) * np.float32(ls - 32) * np.float32(KVALUES[nib])
+    return d * (ls - 32) * KVALUES[nib]
+
+
+def iq2_xxs(b, o, e, exact, grid):
+    d = fp16(u16(b, o))
+    sub, group, within = e // 32, (e // 8) % 4, e % 8
+    packed = u32(b, o + 2 + 8 * sub + 4)
+    gidx = b[o + 2 + 8 * sub + group]
+    g = (int(grid[gidx]) >> (8 * within)) & 0xFF
+    sgn = -1.0 if (sign_byte((packed >> (7 * group)) & 127) >> within) & 1 else 1.0
+    if exact:
+        db = np.float32(d) * (np.float32(0.5) + np.float32(packed >> 28)) * np.float32(0.25)
+        return db * np.float32(g) * np.float32(sgn)
+    return d * (0.5 + (packed >> 28)) * 0.25 * g * sgn
+
+
+def decode_blocks(t, data, nblocks, exact, grid=None):
+    """All elements of nblocks consecutive blocks of type t (oracle type ids)."""
+    fn = {8: q8_0, 12: q4_k, 14: q6_k, 23: iq4_xs}
+    be, bb = {8: (32, 34), 12: (256, 144), 14: (256, 210), 16: (256, 66), 23: (256, 136)}[t]
+    out = np.empty(nblocks * be, np.float32 if exact else np.float64)
+    data = [int(v) for v in data]
+    for k in range(nblocks):
+        for e in range(be):
+            if t == 16:
+                v = iq2_xxs(data, k * bb, e, exact, grid)
+            else:
+                v = fn[t](data, k * bb, e, exact)
+            out[k * be + e] = v
+    return out
