@@ -1,0 +1,216 @@
+"""Benchmark: Q4_K GEMV HBM GB/s (% of peak) + ms/layer at Llama-3.3-70B shapes, batch 1.
+
+One step = one decoder layer's seven GEMVs of a Llama-3.3-70B Q4_K_M model at batch 1 (hidden
+8192, FFN 28672, 64 query / 8 KV heads of 128): q, k (Q4_K) and v (Q6_K) in one fused launch,
+o (Q4_K), gate+up (Q4_K) in one launch with the SiLU epilogue, down (Q6_K). Synthetic seeded
+blocks (fp16 d, dmin = |N(0,1)|*0.01; uniform 6-bit scales and 4/6-bit quants), random x. The
+weights of 4 distinct layer copies rotate (2.2 GB) so the 256 MB Infinity Cache cannot serve a
+repeat; activations stay in HBM for the whole timed region.
+
+Prints one JSON line. value = algorithmic bytes of the layer (weights + 4*T*(cols+rows) per
+GEMV) / measured time per layer, in GB/s.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "Q4_K GEMV HBM GB/s (% of peak) + ms/layer at 70B shapes, batch 1"
+
+HIDDEN, FFN, HEADS, KV_HEADS, HEAD_DIM, LAYERS = 8192, 28672, 64, 8, 128, 80
+Q4_K, Q6_K = 12, 14
+# name, type, rows, cols
+LAYER = [("q", Q4_K, HEADS * HEAD_DIM, HIDDEN), ("k", Q4_K, KV_HEADS * HEAD_DIM, HIDDEN),
+         ("v", Q6_K, KV_HEADS * HEAD_DIM, HIDDEN), ("o", Q4_K, HIDDEN, HEADS * HEAD_DIM),
+         ("gate", Q4_K, FFN, HIDDEN), ("up", Q4_K, FFN, HIDDEN), ("down", Q6_K, HIDDEN, FFN)]
+
+
+def row_bytes(t, cols):
+    return cols // 256 * (144 if t == Q4_K else 210)
+
+
+def algo_bytes(mats, T):
+    return sum(r * row_bytes(t, c) + 4 * T * (c + r) for _, t, r, c in mats)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--batch", type=int, default=1, help="tokens per step (1..8)")
+    ap.add_argument("--copies", type=int, default=4, help="distinct layer copies to rotate")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return ap.parse_args()
+
+
+class Layer:
+    def __init__(self, ctx, host):
+        self.w = {n: ctx.upload(t, host[n], r, c, name=n) for n, t, r, c in LAYER}
+
+    def free(self):
+        for w in self.w.values():
+            w.free()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build runs the hot path on a single MI355X "
+              "(--gpus %d requested)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+    T = args.batch
+    if not 1 <= T <= 8:
+        sys.exit("--batch must be 1..8")
+
+    import torch
+    import windlass_amd
+    from windlass_amd import synth
+    from windlass_amd._lib import check
+    from windlass_amd.backend import Context
+
+    L = windlass_amd.load()
+    rng = np.random.default_rng(0x57494E44 + 3000)
+    host = {n: synth.blocks(t, r, c, rng) for n, t, r, c in LAYER}
+    ctx = Context(0)
+    layers = [Layer(ctx, host) for _ in range(args.copies)]
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(synth.activations(rng, T, HIDDEN)).to(dev)
+    yq = torch.empty((T, HEADS * HEAD_DIM), device=dev)
+    yk = torch.empty((T, KV_HEADS * HEAD_DIM), device=dev)
+    yv = torch.empty((T, KV_HEADS * HEAD_DIM), device=dev)
+    yo = torch.empty((T, HIDDEN), device=dev)
+    h = torch.empty((T, FFN), device=dev)
+    out = torch.empty((T, HIDDEN), device=dev)
+    stream = torch.cuda.ExternalStream(ctx.stream, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def qkv(ly):
+        ws = (ctypes.c_void_p * 3)(ly.w["q"].handle.value, ly.w["k"].handle.value, ly.w["v"].handle.value)
+        ys = (ctypes.c_void_p * 3)(yq.data_ptr(), yk.data_ptr(), yv.data_ptr())
+        check(L.wl_matmul_multi_dev(ctx.handle, 3, ws, P(x), T, ys))
+
+    def o_proj(ly):   # the attention output stands in as yq (attention is not on this path)
+        check(L.wl_matmul_dev(ctx.handle, ly.w["o"].handle, -1, P(yq), T, P(yo)))
+
+    def gate_up(ly):
+        check(L.wl_gate_up_dev(ctx.handle, ly.w["gate"].handle, ly.w["up"].handle, -1, P(yo), T, P(h)))
+
+    def down(ly):
+        check(L.wl_matmul_dev(ctx.handle, ly.w["down"].handle, -1, P(h), T, P(out)))
+
+    def step(i):
+        ly = layers[i % len(layers)]
+        qkv(ly); o_proj(ly); gate_up(ly); down(ly)
+
+    # warmup, then exactly K timed steps between events on the launch stream
+    for i in range(args.warmup):
+        step(i)
+    ctx.sync()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(args.steps):
+            step(i)
+        e1.record(stream)
+    e1.synchronize()
+    torch.cuda.synchronize()
+    ms_layer = e0.elapsed_time(e1) / args.steps
+    layer_bytes = algo_bytes(LAYER, T)
+    gbs = layer_bytes / (ms_layer * 1e-3) / 1e9
+
+    # per-launch durations (HIP events on the same stream), rotating copies
+    def time_launch(fn, reps=200):
+        with torch.cuda.stream(stream):
+            for i in range(10):
+                fn(layers[i % len(layers)])
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for i in range(reps):
+                fn(layers[i % len(layers)])
+            b.record(stream)
+        b.synchronize()
+        return a.elapsed_time(b) / reps
+
+    per = {"qkv": time_launch(qkv), "o": time_launch(o_proj), "gate_up": time_launch(gate_up),
+           "down": time_launch(down)}
+    launch_bytes = {"qkv": algo_bytes(LAYER[0:3], T), "o": algo_bytes(LAYER[3:4], T),
+                    "gate_up": algo_bytes(LAYER[4:6], T), "down": algo_bytes(LAYER[6:7], T)}
+    dom = max(per, key=per.get)
+    ach = launch_bytes[dom] / (per[dom] * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("%s_T%d" % (dom, T))
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(host, T, rng, args.cpu_seconds)
+
+    for ly in layers:
+        ly.free()
+    ctx.close()
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_layer, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic seeded GGUF blocks (Q4_K/Q6_K), x ~ N(0,1)",
+        "config": {"workload": "Llama-3.3-70B Q4_K_M decoder layer, 7 GEMVs (q,k,o,gate,up Q4_K; v,down Q6_K)",
+                   "hidden": HIDDEN, "ffn": FFN, "heads": HEADS, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM,
+                   "batch": T, "layer_copies": args.copies, "launches_per_layer": 4},
+        "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "ms_per_layer": round(ms_layer, 5),
+        "tokens_per_s_80_layers": round(1000.0 / (LAYERS * ms_layer), 2),
+        "layer_algorithmic_bytes": layer_bytes,
+        "per_launch_ms": {k: round(v, 5) for k, v in per.items()},
+        "per_launch_gbs": {k: round(launch_bytes[k] / (per[k] * 1e-3) / 1e9, 1) for k in per},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(host, T, rng, budget_s):
+    """The oracle (C restatement of the reference's CPU MatMul: DotRow per row in a parallel
+    loop over 32-row tiles) on the host cores: best of repeated whole layers within budget."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    x = rng.standard_normal((T, HIDDEN), dtype=np.float32)
+    xf = rng.standard_normal((T, FFN), dtype=np.float32)
+    best, reps, t_start = float("inf"), 0, time.perf_counter()
+    while reps < 3 or (time.perf_counter() - t_start < budget_s and reps < 50):
+        t0 = time.perf_counter()
+        for n, t, r, c in LAYER:
+            oracle.matmul(t, host[n], r, c, xf if c == FFN else x, T, each_token=True, threads=threads)
+        best = min(best, time.perf_counter() - t0)
+        reps += 1
+    gbs = algo_bytes(LAYER, T) / best / 1e9
+    return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_layer": round(best * 1e3, 2),
+            "sample": "whole 70B layer (7 GEMVs) at batch %d, best of %d reps, C restatement of "
+                      "Transformer.MatMul/DotRow (-O2, scalar, -ffp-contract=off), %d threads" % (T, reps, threads)}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,142 @@
+/*
+ * windlass_hip.h - C ABI of the MI355X (gfx950) quantized-matmul library.
+ *
+ * The library takes raw GGUF weight blocks unchanged into one GPU's HBM and runs the
+ * matrix-vector / matrix-matrix products of Windlass's decoder layer on hand-written
+ * HIP kernels. Every entry point replaces one operator of the reference's CPU path; the
+ * comment above each names the reference interface (file:line) it stands in for.
+ *
+ * Conventions
+ *  - Return 0 (WL_OK) on success, a negative WL_E_* code otherwise; wl_last_error()
+ *    gives the message (thread-local).
+ *  - Activations are fp32 row-major: x is [T][cols], y is [T][rows], exactly the layout of
+ *    Transformer.MatMul (src/Transformer.cs:483-486).
+ *  - A context may be used by one thread at a time (the reference's engine holds
+ *    lock(_run) around every model call, src/Engine.cs:138). Distinct contexts are
+ *    independent.
+ *  - Host-pointer entry points are synchronous. *_dev entry points take device pointers,
+ *    are enqueued on wl_stream(ctx) and return before the GPU finishes.
+ */
+#ifndef WINDLASS_HIP_H
+#define WINDLASS_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error codes and the reference exception each maps to. */
+#define WL_OK 0
+#define WL_E_UNSUPPORTED (-1) /* NotSupportedException (src/Quants.cs:51,186) */
+#define WL_E_SHAPE (-2)       /* ArgumentException "MatMul shape mismatch" (src/Transformer.cs:486) */
+#define WL_E_DEVICE (-3)      /* HIP runtime failure; the server's BackendException 500 (src/Server.cs:756-761) */
+#define WL_E_ARG (-4)         /* ArgumentOutOfRangeException / null argument (src/LayerStream.cs:28) */
+#define WL_E_NOMEM (-5)       /* device allocation failed */
+
+/* ggml type ids (enum GgmlType, src/Gguf.cs:19-25). */
+#define WL_TYPE_F32 0
+#define WL_TYPE_F16 1
+#define WL_TYPE_Q8_0 8
+#define WL_TYPE_Q4_K 12
+#define WL_TYPE_Q6_K 14
+#define WL_TYPE_IQ2_XXS 16
+#define WL_TYPE_IQ4_XS 23
+#define WL_TYPE_BF16 30
+
+typedef struct wl_ctx wl_ctx;       /* one per model: a HIP stream plus scratch buffers */
+typedef struct wl_weight wl_weight; /* raw GGUF blocks of one tensor in HBM (WeightView, src/LayerStream.cs:15-35) */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int wl_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *wl_last_error(void);
+
+/* Quants.CanDecode (src/Quants.cs:11-21): 1 when wl_dequant_f32 handles the type. */
+int wl_can_decode(int ggml_type);
+
+/* Quants.CanDot (src/Quants.cs:56-65) widened to every type the GPU multiplies: 1 when
+ * wl_matmul handles the type (the I-quants included, which the CPU path decodes first). */
+int wl_can_matmul(int ggml_type);
+
+/* Block geometry, GgmlTypes.TryGetLayout (src/Gguf.cs:30-66). Returns 1 when known. */
+int wl_type_layout(int ggml_type, int *block_elems, int *block_bytes);
+
+/* New context on HIP device `device` (the model's Transformer/LayerStream pair owns one;
+ * src/Engine.cs:55-91). */
+int wl_create(int device, wl_ctx **out);
+void wl_destroy(wl_ctx *ctx);
+
+/* The hipStream_t the context launches on, as void*. */
+void *wl_stream(wl_ctx *ctx);
+
+/* Waits for every launch queued on the context. */
+int wl_sync(wl_ctx *ctx);
+
+/* Copies raw GGUF blocks unchanged to HBM: LayerStream.Bind's view of one tensor
+ * (src/LayerStream.cs:182-203). `rows` is per expert; `experts` stacked expert tensors
+ * follow each other (src/Gguf.cs:97-101), 1 for an ordinary matrix. row_bytes must equal
+ * cols/block*blockBytes. The host buffer stays the caller's. */
+int wl_upload(wl_ctx *ctx, int ggml_type, const void *blocks, int64_t rows, int64_t cols,
+              int64_t row_bytes, int32_t experts, wl_weight **out);
+
+/* Releases a weight's device memory. */
+int wl_weight_free(wl_ctx *ctx, wl_weight *w);
+
+/* Transformer.MatMul (src/Transformer.cs:483-537), with ForwardBatch's MatMulEach
+ * (:544-561) built in: y[t][r] = dot(W[r], x[t]) for T rows of x; `expert` >= 0 selects
+ * WeightView.Slice(expert) (src/LayerStream.cs:26-34), -1 the whole tensor.
+ * T <= 8 runs the fp32 decode GEMV, whose result for a token does not depend on T (bit for
+ * bit); T > 8 runs the MFMA GEMM (bf16 operands, fp32 accumulation). Synchronous. */
+int wl_matmul(wl_ctx *ctx, const wl_weight *w, int32_t expert, const float *x, int32_t T, float *y);
+
+/* Quants.DecodeRow (src/Quants.cs:32-52; src/IQuants.cs:27-42) for rows row0..row0+nrows-1
+ * of the whole tensor (experts stacked), bit-exact: dst is [nrows][cols] fp32. */
+int wl_dequant_f32(wl_ctx *ctx, const wl_weight *w, int64_t row0, int64_t nrows, float *dst);
+
+/* SwiGlu (src/Transformer.cs:241-251): out = down(silu(gate x) * (up x)); x [T][embd],
+ * out [T][down rows]. `expert` as in wl_matmul, applied to all three. Synchronous. */
+int wl_swiglu(wl_ctx *ctx, const wl_weight *gate, const wl_weight *up, const wl_weight *down,
+              int32_t expert, const float *x, int32_t T, float *out);
+
+/* Route (src/Transformer.cs:313-340) for T tokens: softmax over n logits per token, the k
+ * largest (ties to the lower id), renormalised when asked. sel/wts are [T][k]. */
+int wl_route(wl_ctx *ctx, const float *logits, int32_t T, int32_t n, int32_t k, int32_t renorm,
+             int32_t *sel, float *wts);
+
+/* MoeFfn (src/Transformer.cs:259-294) given the router logits [T][n_expert]: route, run each
+ * chosen expert's SwiGLU on its tokens, weighted sum. gate/up/down are stacked expert tensors
+ * ([n_expert][ff][embd], [n_expert][ff][embd], [n_expert][embd][ff]). expert_runs (may be
+ * NULL) receives the number of distinct experts computed (Transformer.ExpertRuns, :27). */
+int wl_moe_ffn(wl_ctx *ctx, const float *logits, int32_t k, int32_t renorm,
+               const wl_weight *gate_exps, const wl_weight *up_exps, const wl_weight *down_exps,
+               const float *x, int32_t T, float *out, int32_t *expert_runs);
+
+/* ---- device-pointer variants (activations resident in HBM), asynchronous ---------- */
+
+/* wl_matmul on device buffers d_x [T][cols], d_y [T][rows]. */
+int wl_matmul_dev(wl_ctx *ctx, const wl_weight *w, int32_t expert, const float *d_x, int32_t T,
+                  float *d_y);
+
+/* Several matrices that read the same x in ONE launch (Layer's q, k and v,
+ * src/Transformer.cs:186-188): d_ys[i] is [T][rows_i]. n <= 4; types may differ. */
+int wl_matmul_multi_dev(wl_ctx *ctx, int32_t n, const wl_weight *const *ws, const float *d_x,
+                        int32_t T, float *const *d_ys);
+
+/* The SwiGLU gate/up half in one launch: d_h [T][ff] = silu(gate x) * (up x)
+ * (src/Transformer.cs:245-247). gate and up must share a type. */
+int wl_gate_up_dev(wl_ctx *ctx, const wl_weight *gate, const wl_weight *up, int32_t expert,
+                   const float *d_x, int32_t T, float *d_h);
+
+/* wl_dequant_f32 into a device buffer. */
+int wl_dequant_dev(wl_ctx *ctx, const wl_weight *w, int64_t row0, int64_t nrows, float *d_dst);
+
+/* wl_moe_ffn on device buffers (logits, x, out in HBM). */
+int wl_moe_ffn_dev(wl_ctx *ctx, const float *d_logits, int32_t k, int32_t renorm,
+                   const wl_weight *gate_exps, const wl_weight *up_exps,
+                   const wl_weight *down_exps, const float *d_x, int32_t T, float *d_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

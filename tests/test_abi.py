@@ -1,0 +1,81 @@
+"""The C-ABI library (CPU side only, no GPU needed): it loads, exports every function that
+include/windlass_hip.h declares, and its host-only entry points behave."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import windlass_amd
+from windlass_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "windlass_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    names = declared_functions()
+    assert names, "no declarations found"
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = windlass_amd.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_nm_dynamic_symbols():
+    # the exported names are plain C symbols (no C++ mangling)
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", windlass_amd.library_path()],
+                         capture_output=True, text=True, check=True).stdout
+    syms = set(line.split()[-1] for line in out.splitlines() if line.strip())
+    for name in declared_functions():
+        assert name in syms, name
+
+
+def test_type_queries_match_reference_layouts():
+    L = windlass_amd.load()
+    # src/Gguf.cs:30-66
+    want = {0: (1, 4), 1: (1, 2), 30: (1, 2), 8: (32, 34), 12: (256, 144), 14: (256, 210),
+            16: (256, 66), 23: (256, 136)}
+    for t, lay in want.items():
+        assert windlass_amd.layout(t) == lay
+        assert L.wl_can_decode(t) == 1
+    for t in (8, 12, 14, 16, 23):
+        assert L.wl_can_matmul(t) == 1
+    for t in (2, 3, 6, 7, 10, 11, 13, 15, 17, 18, 19, 20, 21, 22, 29):
+        assert L.wl_can_decode(t) == 0 and L.wl_can_matmul(t) == 0
+    assert windlass_amd.Quants.CanDecode(windlass_amd.GgmlType.Q4_K)
+    assert L.wl_version() >= 100
+
+
+def test_null_arguments_are_refused_without_touching_a_device():
+    L = windlass_amd.load()
+    assert L.wl_create(0, None) == _lib.WL_E_ARG
+    assert b"null" in L.wl_last_error()
+    assert L.wl_sync(None) == _lib.WL_E_ARG
+    assert L.wl_matmul(None, None, -1, None, 1, None) == _lib.WL_E_ARG
+    with pytest.raises(windlass_amd.ArgumentOutOfRangeError):
+        _lib.check(L.wl_matmul(None, None, -1, None, 1, None))
+
+
+def test_error_codes_map_to_reference_exceptions():
+    assert issubclass(windlass_amd.NotSupportedError, NotImplementedError)
+    assert issubclass(windlass_amd.ShapeError, ValueError)
+    assert _lib._EXC[_lib.WL_E_UNSUPPORTED] is windlass_amd.NotSupportedError
+    assert _lib._EXC[_lib.WL_E_SHAPE] is windlass_amd.ShapeError
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "HERE", str(tmp_path))
+    with pytest.raises(windlass_amd.BackendError):
+        _lib.load()

@@ -1,0 +1,93 @@
+"""GPU decode GEMV (Transformer.MatMul T <= 8, src/Transformer.cs:483-561) against the oracle.
+
+Bar (tests/Tests.cs:297-299): |y - exact| <= 1e-5 * sum|w*x| + 1e-6, exact computed in float64
+from the bit-exact decoded weights; the oracle's own DotRow/MatMulEach result must meet the same
+bar (so GPU and oracle agree to within it). Batch invariance: every token of a T-token call
+equals the same token alone, bit for bit (MatMulEach / ForwardBatch, src/Transformer.cs:127-131).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from gpu_common import QTYPES, blocks, decoded, tol_check
+from windlass_amd import Transformer
+from windlass_amd.backend import Context, GgmlType
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(5, 512), (37, 1024), (300, 2048), (1000, 4096)]
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = Context(0)
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "%dx%d" % s)
+@pytest.mark.parametrize("T", [1, 3, 8])
+def test_gemv_within_tolerance(ctx, t, shape, T):
+    rows, cols = shape
+    data = blocks(t, rows, cols, seed=rows + cols + int(t))
+    x = np.random.default_rng(T).standard_normal((T, cols), dtype=np.float32)
+    w = ctx.upload(t, data, rows, cols)
+    y = Transformer.MatMul(w, x, T)
+    wd = decoded(t, data, rows, cols)
+    tol_check(y, x, wd, what="gpu %s T=%d" % (t.name, T))
+    # the oracle (DotRow / MatMulEach / decode+Block) meets the same bar on the same inputs
+    yo = oracle.matmul(int(t), data, rows, cols, x, T, each_token=True)
+    tol_check(yo, x, wd, what="oracle %s T=%d" % (t.name, T))
+    w.free()
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
+def test_batch_rows_equal_single_token_bitwise(ctx, t):
+    rows, cols = 300, 2048
+    data = blocks(t, rows, cols, seed=77)
+    w = ctx.upload(t, data, rows, cols)
+    x = np.random.default_rng(3).standard_normal((8, cols), dtype=np.float32)
+    y1 = np.stack([Transformer.MatMul(w, x[i:i + 1], 1)[0] for i in range(8)])
+    for T in (2, 3, 4, 5, 8):
+        yb = Transformer.MatMul(w, x[:T], T)
+        assert np.array_equal(yb.view(np.uint32), y1[:T].view(np.uint32)), T
+    w.free()
+
+
+def test_more_than_eight_tokens(ctx):
+    t, rows, cols, T = GgmlType.Q4_K, 64, 1024, 19
+    data = blocks(t, rows, cols, seed=1)
+    w = ctx.upload(t, data, rows, cols)
+    x = np.random.default_rng(2).standard_normal((T, cols), dtype=np.float32)
+    y = Transformer.MatMul(w, x, T)
+    tol_check(y, x, decoded(t, data, rows, cols), rel=1e-5, what="T=19")
+    w.free()
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
+def test_expert_slices(ctx, t):
+    ne, rows, cols = 4, 40, 512
+    data = blocks(t, ne * rows, cols, seed=11)
+    w = ctx.upload(t, data, rows, cols, experts=ne)
+    x = np.random.default_rng(4).standard_normal((2, cols), dtype=np.float32)
+    wd = decoded(t, data, ne * rows, cols).reshape(ne, rows, cols)
+    for e in range(ne):
+        y = Transformer.MatMul(w.Slice(e), x, 2)
+        tol_check(y, x, wd[e], what="expert %d" % e)
+    w.free()
+
+
+def test_errors(ctx):
+    import windlass_amd
+    data = blocks(GgmlType.Q4_K, 4, 256, seed=0)
+    w = ctx.upload(GgmlType.Q4_K, data, 4, 256)
+    with pytest.raises(windlass_amd.ShapeError):
+        Transformer.MatMul(w, np.zeros(300, np.float32), 1)
+    with pytest.raises(windlass_amd.ArgumentOutOfRangeError):
+        w.Slice(1)
+    with pytest.raises(windlass_amd.NotSupportedError):
+        ctx.upload(11, np.zeros(110, np.uint8), 1, 256)   # Q3_K: not on this path
+    with pytest.raises(windlass_amd.ShapeError):
+        ctx.upload(GgmlType.Q4_K, np.zeros(144, np.uint8), 1, 300)
+    w.free()

@@ -1,0 +1,80 @@
+"""GPU routing and routed experts (Route / MoeFfn, src/Transformer.cs:253-340) against the
+oracle and the reference's own routing known answers (tests/MoeTests.cs:116-149)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from gpu_common import blocks
+from windlass_amd import Transformer
+from windlass_amd.backend import Context, GgmlType
+
+pytestmark = pytest.mark.gpu
+
+PINS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_pins.json")))
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def test_route_known_answers(ctx):
+    for c in PINS["route"]["cases"]:
+        lg = np.array(c["logits"], np.float32)
+        sel, wts = Transformer.Route(ctx, lg, lg.size, c["k"], c["renorm"])
+        assert list(sel[0]) == c["sel"], c
+        if "wts" in c:
+            if c.get("exact"):
+                assert list(wts[0]) == c["wts"]
+            else:
+                assert np.all(np.abs(wts[0] - np.array(c["wts"])) < PINS["route"]["tol"])
+
+
+@pytest.mark.parametrize("n,k", [(128, 8), (64, 4), (8, 2)])
+def test_route_vs_oracle(ctx, n, k):
+    T = 16
+    lg = np.random.default_rng(n + k).standard_normal((T, n), dtype=np.float32)
+    sel, wts = Transformer.Route(ctx, lg, n, k, True)
+    for t in range(T):
+        osel, owts, _ = oracle.route(lg[t], k, True)
+        assert list(sel[t]) == list(osel)
+        assert np.all(np.abs(wts[t] - owts) <= 1e-6 * np.abs(owts))
+
+
+@pytest.mark.parametrize("T", [1, 8, 11])
+@pytest.mark.parametrize("types", [(12, 12), (12, 14)])
+def test_moe_ffn_vs_oracle(ctx, T, types):
+    ne, k, embd, ff = 16, 4, 512, 256
+    gt, dt = types
+    gate = blocks(gt, ne * ff, embd, seed=1)
+    up = blocks(gt, ne * ff, embd, seed=2)
+    down = blocks(dt, ne * embd, ff, seed=3)
+    x = np.random.default_rng(4).standard_normal((T, embd), dtype=np.float32)
+    logits = np.random.default_rng(5).standard_normal((T, ne), dtype=np.float32)
+    wg = ctx.upload(gt, gate, ff, embd, experts=ne)
+    wu = ctx.upload(gt, up, ff, embd, experts=ne)
+    wd = ctx.upload(dt, down, embd, ff, experts=ne)
+    got, runs = Transformer.MoeFfn(logits, wg, wu, wd, x, T, k, True)
+    want, oruns = oracle.moe_ffn(logits, k, True, gt, gate, gt, up, dt, down, ff, embd, x, T, each_token=True)
+    if T <= 8:
+        assert runs == oruns
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.std(want)
+    for w in (wg, wu, wd):
+        w.free()
+
+
+def test_one_expert_equals_dense(ctx):
+    # tests/MoeTests.cs:151-162: a one-expert MoE is its dense twin (weight 1 after renorm)
+    embd, ff, T = 512, 256, 3
+    g, u, d = blocks(12, ff, embd, 1), blocks(12, ff, embd, 2), blocks(12, embd, ff, 3)
+    wg, wu, wd = ctx.upload(12, g, ff, embd, 1), ctx.upload(12, u, ff, embd, 1), ctx.upload(12, d, embd, ff, 1)
+    x = np.random.default_rng(0).standard_normal((T, embd), dtype=np.float32)
+    moe, runs = Transformer.MoeFfn(np.zeros((T, 1), np.float32), wg, wu, wd, x, T, 1, True)
+    dense = Transformer.SwiGlu(wg, wu, wd, x, T)
+    assert runs == 1
+    assert np.array_equal(moe.view(np.uint32), dense.view(np.uint32))

@@ -1,0 +1,24 @@
+"""windlass_amd - MI355X (gfx950) quantized-matmul backend for Windlass.
+
+Host-side mirror of the reference's operator interface for this path, over the C ABI of
+libwindlass_hip.so (include/windlass_hip.h):
+
+- ``GgmlType``                    enum GgmlType (src/Gguf.cs:19-25)
+- ``Quants.CanDecode/CanDot``     src/Quants.cs:11-21, 56-65
+- ``WeightView`` / ``Slice``      src/LayerStream.cs:15-35 (here: raw blocks resident in HBM)
+- ``Transformer.MatMul``          src/Transformer.cs:483-537 (+ MatMulEach, :544-561)
+- ``Transformer.SwiGlu``          src/Transformer.cs:241-251
+- ``Transformer.Route``           src/Transformer.cs:315-340
+- ``Transformer.MoeFfn``          src/Transformer.cs:259-294 (router logits given)
+
+Errors map to the reference's exception kinds: ``NotSupportedError`` (NotSupportedException),
+``ShapeError`` (ArgumentException), ``ArgumentOutOfRangeError``, ``BackendError`` (device
+failure). There is no CPU fallback: without the built library every call raises.
+"""
+from ._lib import (ArgumentOutOfRangeError, BackendError, NotSupportedError, ShapeError,
+                   library_path, load)
+from .backend import Context, GgmlType, Quants, Transformer, WeightView, layout
+
+__all__ = ["ArgumentOutOfRangeError", "BackendError", "NotSupportedError", "ShapeError",
+           "library_path", "load", "Context", "GgmlType", "Quants", "Transformer",
+           "WeightView", "layout"]

@@ -1,0 +1,85 @@
+"""ctypes binding of libwindlass_hip.so (include/windlass_hip.h)."""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_NAME = "libwindlass_hip.so"
+
+# Every symbol include/windlass_hip.h declares, with (restype, argtypes).
+P, I32, I64, F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+PP = ctypes.POINTER(ctypes.c_void_p)
+SIGNATURES = {
+    "wl_version": (ctypes.c_int, []),
+    "wl_last_error": (ctypes.c_char_p, []),
+    "wl_can_decode": (ctypes.c_int, [ctypes.c_int]),
+    "wl_can_matmul": (ctypes.c_int, [ctypes.c_int]),
+    "wl_type_layout": (ctypes.c_int, [ctypes.c_int, P, P]),
+    "wl_create": (ctypes.c_int, [ctypes.c_int, PP]),
+    "wl_destroy": (None, [P]),
+    "wl_stream": (P, [P]),
+    "wl_sync": (ctypes.c_int, [P]),
+    "wl_upload": (ctypes.c_int, [P, ctypes.c_int, P, I64, I64, I64, I32, PP]),
+    "wl_weight_free": (ctypes.c_int, [P, P]),
+    "wl_matmul": (ctypes.c_int, [P, P, I32, P, I32, P]),
+    "wl_dequant_f32": (ctypes.c_int, [P, P, I64, I64, P]),
+    "wl_swiglu": (ctypes.c_int, [P, P, P, P, I32, P, I32, P]),
+    "wl_route": (ctypes.c_int, [P, P, I32, I32, I32, I32, P, P]),
+    "wl_moe_ffn": (ctypes.c_int, [P, P, I32, I32, P, P, P, P, I32, P, P]),
+    "wl_matmul_dev": (ctypes.c_int, [P, P, I32, P, I32, P]),
+    "wl_matmul_multi_dev": (ctypes.c_int, [P, I32, P, P, I32, P]),
+    "wl_gate_up_dev": (ctypes.c_int, [P, P, P, I32, P, I32, P]),
+    "wl_dequant_dev": (ctypes.c_int, [P, P, I64, I64, P]),
+    "wl_moe_ffn_dev": (ctypes.c_int, [P, P, I32, I32, P, P, P, P, I32, P]),
+}
+
+WL_E_UNSUPPORTED, WL_E_SHAPE, WL_E_DEVICE, WL_E_ARG, WL_E_NOMEM = -1, -2, -3, -4, -5
+
+
+class BackendError(RuntimeError):
+    """A HIP runtime failure (the server reports it as a 500 server_error)."""
+
+
+class NotSupportedError(NotImplementedError):
+    """NotSupportedException: a type the GPU path cannot decode or multiply."""
+
+
+class ShapeError(ValueError):
+    """ArgumentException: operand shapes that do not match."""
+
+
+class ArgumentOutOfRangeError(IndexError):
+    """ArgumentOutOfRangeException: an expert or row range outside the tensor."""
+
+
+_EXC = {WL_E_UNSUPPORTED: NotSupportedError, WL_E_SHAPE: ShapeError, WL_E_DEVICE: BackendError,
+        WL_E_ARG: ArgumentOutOfRangeError, WL_E_NOMEM: BackendError}
+
+_lib = None
+
+
+def library_path():
+    return os.path.join(HERE, _LIB_NAME)
+
+
+def load():
+    """Loads libwindlass_hip.so; raises when it has not been built (no CPU fallback)."""
+    global _lib
+    if _lib is None:
+        path = library_path()
+        if not os.path.exists(path):
+            raise BackendError("%s is not built: run `python -m windlass_amd.build` "
+                               "(or __graft_entry__.build())" % path)
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        msg = load().wl_last_error().decode(errors="replace")
+        raise _EXC.get(rc, BackendError)(msg or "error %d" % rc)
+    return rc

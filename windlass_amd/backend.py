@@ -1,0 +1,201 @@
+"""The reference's operator interface for the quantized-matmul path, on the GPU.
+
+Mirrors the names and argument meaning of Windlass's C# (file:line on each member) so a caller
+of ``Transformer.MatMul(w, x, T, y)`` finds the same operation here. Arrays are numpy float32
+(host) buffers in the reference's layout: x is [T][cols], y is [T][rows].
+"""
+import ctypes
+from enum import IntEnum
+
+import numpy as np
+
+from ._lib import ArgumentOutOfRangeError, NotSupportedError, ShapeError, check, load
+
+
+class GgmlType(IntEnum):
+    """enum GgmlType (src/Gguf.cs:19-25), the ids this backend handles."""
+    F32 = 0
+    F16 = 1
+    Q8_0 = 8
+    Q4_K = 12
+    Q6_K = 14
+    IQ2_XXS = 16
+    IQ4_XS = 23
+    BF16 = 30
+
+
+def layout(t):
+    """(elements, bytes) per block, GgmlTypes.TryGetLayout (src/Gguf.cs:30-66)."""
+    be, bb = ctypes.c_int(), ctypes.c_int()
+    if not load().wl_type_layout(int(t), ctypes.byref(be), ctypes.byref(bb)):
+        raise ValueError("unknown ggml type %d" % int(t))
+    return be.value, bb.value
+
+
+class Quants:
+    """Type capability checks (src/Quants.cs:11-21, 56-65)."""
+
+    @staticmethod
+    def CanDecode(t):
+        return bool(load().wl_can_decode(int(t)))
+
+    @staticmethod
+    def CanDot(t):
+        return bool(load().wl_can_matmul(int(t)))
+
+
+def _ptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+class Context:
+    """One GPU context per model (a HIP stream plus scratch), wl_create/wl_destroy."""
+
+    def __init__(self, device=0):
+        self._lib = load()
+        h = ctypes.c_void_p()
+        check(self._lib.wl_create(device, ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            self._lib.wl_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self):
+        return self._lib.wl_stream(self.handle)
+
+    def sync(self):
+        check(self._lib.wl_sync(self.handle))
+
+    def upload(self, t, blocks, rows, cols, experts=1, name="weight"):
+        """Raw GGUF blocks to HBM, unchanged (LayerStream.Bind, src/LayerStream.cs:182-203)."""
+        return WeightView(self, t, blocks, rows, cols, experts, name)
+
+
+class WeightView:
+    """A tensor's raw blocks in HBM: {Name, Type, Rows, Cols, RowBytes, Experts}
+    (src/LayerStream.cs:15-24). Rows counts one expert's rows for stacked tensors."""
+
+    def __init__(self, ctx, t, blocks, rows, cols, experts=1, name="weight", _parent=None, _expert=-1):
+        self.ctx = ctx
+        self.Name = name
+        if int(t) not in GgmlType._value2member_map_ or not Quants.CanDecode(t):
+            raise NotSupportedError("Windlass cannot decode type %d weights on the GPU." % int(t))
+        self.Type = GgmlType(int(t))
+        self.Rows = int(rows)
+        self.Cols = int(cols)
+        self.Experts = int(experts)
+        be, bb = layout(self.Type)
+        if self.Cols % be:
+            raise ShapeError("%s has %d columns, not whole %s blocks" % (name, cols, self.Type.name))
+        self.RowBytes = self.Cols // be * bb
+        self._expert = _expert
+        self._parent = _parent
+        if _parent is not None:
+            self.handle = _parent.handle
+            return
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+        if blocks.size != self.Rows * self.Experts * self.RowBytes:
+            raise ShapeError("%s: %d bytes for %d x %d x %d %s values" % (
+                name, blocks.size, self.Experts, self.Rows, self.Cols, self.Type.name))
+        h = ctypes.c_void_p()
+        check(load().wl_upload(ctx.handle, int(self.Type), _ptr(blocks), self.Rows, self.Cols,
+                               self.RowBytes, self.Experts, ctypes.byref(h)))
+        self.handle = h
+
+    def Slice(self, expert):
+        """Expert e of a stacked tensor as an ordinary matrix (src/LayerStream.cs:26-34)."""
+        if expert < 0 or expert >= self.Experts:
+            raise ArgumentOutOfRangeError("Expert %d is outside 0..%d of %s." % (
+                expert, self.Experts - 1, self.Name))
+        return WeightView(self.ctx, self.Type, None, self.Rows, self.Cols, 1,
+                          "%s[%d]" % (self.Name, expert), _parent=self, _expert=expert)
+
+    @property
+    def matrix_rows(self):
+        """Rows of the operand (a slice's rows, or every expert's rows of a stacked tensor)."""
+        return self.Rows if self._expert >= 0 else self.Rows * self.Experts
+
+    def free(self):
+        if self._parent is None and self.handle:
+            check(load().wl_weight_free(self.ctx.handle, self.handle))
+            self.handle = None
+
+    def decode(self, row0=0, nrows=None):
+        """Quants.DecodeRow over rows row0.. of the whole tensor, bit-exact fp32."""
+        total = self.Rows * self.Experts
+        if self._expert >= 0:
+            row0 += self._expert * self.Rows
+            total = (self._expert + 1) * self.Rows
+        nrows = total - row0 if nrows is None else nrows
+        out = np.empty((nrows, self.Cols), np.float32)
+        check(load().wl_dequant_f32(self.ctx.handle, self.handle, row0, nrows, _ptr(out)))
+        return out
+
+
+class Transformer:
+    """The static operators of src/Transformer.cs that this path replaces."""
+
+    @staticmethod
+    def MatMul(w, x, T, y=None):
+        """y[t][r] = dot(W[r], x[t]) (src/Transformer.cs:483-537). T <= 8 rows give every
+        token the bits it gets alone (MatMulEach, :544-561)."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        rows = w.matrix_rows
+        if x.size != w.Cols * T or (y is not None and y.size < rows * T):
+            raise ShapeError("MatMul shape mismatch for %s." % w.Name)
+        out = np.empty(T * rows, np.float32) if y is None else y
+        check(load().wl_matmul(w.ctx.handle, w.handle, w._expert, _ptr(x), T, _ptr(out)))
+        return out.reshape(T, rows) if y is None else y
+
+    @staticmethod
+    def SwiGlu(gate, up, down, xn, T):
+        """down(silu(gate x) * (up x)) for T rows of xn (src/Transformer.cs:241-251)."""
+        xn = np.ascontiguousarray(xn, np.float32).reshape(-1)
+        if xn.size != gate.Cols * T:
+            raise ShapeError("MatMul shape mismatch for %s." % gate.Name)
+        out = np.empty((T, down.matrix_rows), np.float32)
+        expert = gate._expert
+        if not (gate._expert == up._expert == down._expert):
+            raise ShapeError("SwiGlu slices of different experts")
+        check(load().wl_swiglu(gate.ctx.handle, gate.handle, up.handle, down.handle, expert,
+                               _ptr(xn), T, _ptr(out)))
+        return out
+
+    @staticmethod
+    def Route(ctx, logits, n, k, renorm):
+        """Per-token routing (src/Transformer.cs:315-340): softmax, top-k (ties to the lower
+        id), optional renormalisation. logits is [T][n]; returns (sel [T][k], wts [T][k])."""
+        logits = np.ascontiguousarray(logits, np.float32).reshape(-1, n)
+        T = logits.shape[0]
+        sel = np.empty((T, k), np.int32)
+        wts = np.empty((T, k), np.float32)
+        check(load().wl_route(ctx.handle, _ptr(logits), T, n, k, int(bool(renorm)), _ptr(sel), _ptr(wts)))
+        return sel, wts
+
+    @staticmethod
+    def MoeFfn(logits, gate_exps, up_exps, down_exps, xn, T, k, renorm):
+        """The routed experts of MoeFfn (src/Transformer.cs:259-294) given router logits
+        [T][n_expert]. Returns (out [T][embd], expert runs)."""
+        logits = np.ascontiguousarray(logits, np.float32).reshape(-1)
+        xn = np.ascontiguousarray(xn, np.float32).reshape(-1)
+        out = np.empty((T, gate_exps.Cols), np.float32)
+        runs = ctypes.c_int32()
+        check(load().wl_moe_ffn(gate_exps.ctx.handle, _ptr(logits), k, int(bool(renorm)),
+                                gate_exps.handle, up_exps.handle, down_exps.handle, _ptr(xn), T,
+                                _ptr(out), ctypes.byref(runs)))
+        return out, runs.value

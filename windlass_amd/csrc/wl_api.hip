@@ -1,0 +1,517 @@
+// wl_api.hip - the C ABI (include/windlass_hip.h): contexts, weight upload, operator dispatch.
+//
+// Host-side only; the kernels live in wl_gemv.hip, wl_dequant.hip, wl_gemm.hip and wl_moe.hip.
+// Every entry point validates shapes on the host before anything is launched, so a kernel
+// never sees an operand that does not match its grid.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/windlass_hip.h"
+#include "wl_dequant.h"
+#include "wl_gemm.h"
+#include "wl_gemv.h"
+#include "wl_moe.h"
+
+// Bytes of padding after every weight buffer: the GEMV reads the aligned dwords around
+// 2-byte-aligned fields and may touch up to 16 bytes past the last block.
+static constexpr size_t kWeightPad = 256;
+
+struct wl_weight {
+  int type;
+  int64_t rows;  // per expert
+  int64_t cols;
+  int64_t row_bytes;
+  int32_t experts;
+  uint8_t *dev;
+  size_t bytes;  // rows * experts * row_bytes
+};
+
+struct wl_ctx {
+  int device;
+  hipStream_t stream;
+  // growable scratch (device)
+  void *buf[6];
+  size_t cap[6];
+};
+
+enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX };
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char *fmt, ...) {
+  char msg[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(msg, sizeof msg, fmt, ap);
+  va_end(ap);
+  g_err = msg;
+  return code;
+}
+
+static int hip_fail(hipError_t e, const char *what) {
+  return fail(WL_E_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define WL_HIP(call, what)                                 \
+  do {                                                     \
+    hipError_t e_ = (call);                                \
+    if (e_ != hipSuccess) return hip_fail(e_, what);       \
+  } while (0)
+
+static const char *type_name(int t) {
+  switch (t) {
+    case WL_TYPE_F32: return "f32";
+    case WL_TYPE_F16: return "f16";
+    case WL_TYPE_BF16: return "bf16";
+    case WL_TYPE_Q8_0: return "q8_0";
+    case WL_TYPE_Q4_K: return "q4_K";
+    case WL_TYPE_Q6_K: return "q6_K";
+    case WL_TYPE_IQ2_XXS: return "iq2_xxs";
+    case WL_TYPE_IQ4_XS: return "iq4_xs";
+  }
+  return "type";
+}
+
+extern "C" int wl_type_layout(int t, int *be, int *bb) {
+  int e = 0, b = 0;
+  switch (t) {
+    case WL_TYPE_F32: e = 1; b = 4; break;
+    case WL_TYPE_F16: case WL_TYPE_BF16: e = 1; b = 2; break;
+    case WL_TYPE_Q8_0: e = 32; b = 34; break;
+    case WL_TYPE_Q4_K: e = 256; b = 144; break;
+    case WL_TYPE_Q6_K: e = 256; b = 210; break;
+    case WL_TYPE_IQ2_XXS: e = 256; b = 66; break;
+    case WL_TYPE_IQ4_XS: e = 256; b = 136; break;
+  }
+  if (be) *be = e;
+  if (bb) *bb = b;
+  return e != 0;
+}
+
+extern "C" int wl_version(void) { return 100; }
+
+extern "C" const char *wl_last_error(void) { return g_err.c_str(); }
+
+extern "C" int wl_can_decode(int t) { return wl::dequant_supports(t) ? 1 : 0; }
+
+extern "C" int wl_can_matmul(int t) { return wl::gemv_supports(t) ? 1 : 0; }
+
+static int ensure(wl_ctx *c, int slot, size_t bytes) {
+  if (c->cap[slot] >= bytes) return WL_OK;
+  if (c->buf[slot]) {
+    hipStreamSynchronize(c->stream);
+    hipFree(c->buf[slot]);
+    c->buf[slot] = nullptr;
+    c->cap[slot] = 0;
+  }
+  size_t want = bytes < 4096 ? 4096 : bytes;
+  if (hipMalloc(&c->buf[slot], want) != hipSuccess) {
+    c->buf[slot] = nullptr;
+    return fail(WL_E_NOMEM, "cannot allocate %zu bytes of device scratch", want);
+  }
+  c->cap[slot] = want;
+  return WL_OK;
+}
+
+extern "C" int wl_create(int device, wl_ctx **out) {
+  if (!out) return fail(WL_E_ARG, "wl_create: out is null");
+  *out = nullptr;
+  int n = 0;
+  WL_HIP(hipGetDeviceCount(&n), "hipGetDeviceCount");
+  if (device < 0 || device >= n) return fail(WL_E_ARG, "device %d is outside 0..%d", device, n - 1);
+  WL_HIP(hipSetDevice(device), "hipSetDevice");
+  wl_ctx *c = new wl_ctx();
+  c->device = device;
+  hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_fail(e, "hipStreamCreate");
+  }
+  *out = c;
+  return WL_OK;
+}
+
+extern "C" void wl_destroy(wl_ctx *c) {
+  if (!c) return;
+  hipSetDevice(c->device);
+  hipStreamSynchronize(c->stream);
+  for (void *&b : c->buf)
+    if (b) hipFree(b);
+  hipStreamDestroy(c->stream);
+  delete c;
+}
+
+extern "C" void *wl_stream(wl_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+extern "C" int wl_sync(wl_ctx *c) {
+  if (!c) return fail(WL_E_ARG, "context is null");
+  WL_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return WL_OK;
+}
+
+extern "C" int wl_upload(wl_ctx *c, int type, const void *blocks, int64_t rows, int64_t cols, int64_t row_bytes,
+                         int32_t experts, wl_weight **out) {
+  if (!c || !out || !blocks) return fail(WL_E_ARG, "wl_upload: null argument");
+  *out = nullptr;
+  int be, bb;
+  if (!wl_type_layout(type, &be, &bb) || !wl::dequant_supports(type))
+    return fail(WL_E_UNSUPPORTED, "Windlass cannot decode %s weights on the GPU.", type_name(type));
+  if (rows <= 0 || cols <= 0 || experts <= 0) return fail(WL_E_SHAPE, "wl_upload: empty shape");
+  if (cols % be) return fail(WL_E_SHAPE, "%s rows of %lld values are not whole blocks of %d", type_name(type),
+                             (long long)cols, be);
+  if (row_bytes != cols / be * bb)
+    return fail(WL_E_SHAPE, "row_bytes %lld does not match %lld %s values (%lld)", (long long)row_bytes,
+                (long long)cols, type_name(type), (long long)(cols / be * bb));
+  if (cols > (1 << 30) || rows > (1 << 30)) return fail(WL_E_SHAPE, "wl_upload: dimension too large");
+  WL_HIP(hipSetDevice(c->device), "hipSetDevice");
+  wl_weight *w = new wl_weight();
+  w->type = type;
+  w->rows = rows;
+  w->cols = cols;
+  w->row_bytes = row_bytes;
+  w->experts = experts;
+  w->bytes = (size_t)rows * (size_t)experts * (size_t)row_bytes;
+  if (hipMalloc(&w->dev, w->bytes + kWeightPad) != hipSuccess) {
+    delete w;
+    return fail(WL_E_NOMEM, "cannot allocate %zu bytes for a %s weight", (size_t)(rows * experts * row_bytes),
+                type_name(type));
+  }
+  hipError_t e = hipMemcpyAsync(w->dev, blocks, w->bytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(w->dev + w->bytes, 0, kWeightPad, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    hipFree(w->dev);
+    delete w;
+    return hip_fail(e, "weight upload");
+  }
+  *out = w;
+  return WL_OK;
+}
+
+extern "C" int wl_weight_free(wl_ctx *c, wl_weight *w) {
+  if (!w) return WL_OK;
+  if (c) hipStreamSynchronize(c->stream);
+  hipFree(w->dev);
+  delete w;
+  return WL_OK;
+}
+
+// ------------------------------------------------------------------------------ matmul
+
+static int check_expert(const wl_weight *w, int32_t expert) {
+  if (expert < -1 || expert >= w->experts)
+    return fail(WL_E_ARG, "Expert %d is outside 0..%d.", expert, w->experts - 1);
+  return WL_OK;
+}
+
+// rows and base pointer of the operand WeightView (whole tensor or one expert's slice)
+static void operand(const wl_weight *w, int32_t expert, const uint8_t **base, int64_t *rows) {
+  if (expert < 0) {
+    *base = w->dev;
+    *rows = w->rows * w->experts;
+  } else {
+    *base = w->dev + (int64_t)expert * w->rows * w->row_bytes;
+    *rows = w->rows;
+  }
+}
+
+static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float *d_x, int32_t T, float *d_y) {
+  if (!c || !w || !d_x || !d_y) return fail(WL_E_ARG, "matmul: null argument");
+  int rc = check_expert(w, expert);
+  if (rc) return rc;
+  if (T <= 0) return fail(WL_E_SHAPE, "MatMul shape mismatch: T = %d", T);
+  if (!wl::gemv_supports(w->type) && !wl::gemm_supports(w->type))
+    return fail(WL_E_UNSUPPORTED, "No GPU matmul for %s.", type_name(w->type));
+  const uint8_t *base;
+  int64_t rows;
+  operand(w, expert, &base, &rows);
+  if (T > 8 && wl::gemm_supports(w->type)) {
+    WL_HIP(wl::gemm_launch(w->type, base, w->row_bytes, (int)rows, (int)w->cols, d_x, T, d_y, c->stream), "gemm launch");
+    return WL_OK;
+  }
+  // decode GEMV in passes of up to 8 tokens (a token's result does not depend on its pass)
+  for (int t0 = 0; t0 < T; t0 += 8) {
+    wl::GemvParams p{};
+    p.nseg = 1;
+    p.seg[0].w = base;
+    p.seg[0].row_bytes = w->row_bytes;
+    p.seg[0].rows = (int)rows;
+    p.seg[0].y = d_y + (int64_t)t0 * rows;
+    p.seg[0].ldy = (int)rows;
+    p.seg[0].type = w->type;
+    p.x = d_x + (int64_t)t0 * w->cols;
+    p.ldx = (int)w->cols;
+    p.cols = (int)w->cols;
+    p.T = T - t0 < 8 ? T - t0 : 8;
+    WL_HIP(wl::gemv_launch(w->type, 1, p, c->stream), "gemv launch");
+  }
+  return WL_OK;
+}
+
+extern "C" int wl_matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float *d_x, int32_t T,
+                             float *d_y) {
+  return matmul_dev(c, w, expert, d_x, T, d_y);
+}
+
+extern "C" int wl_matmul(wl_ctx *c, const wl_weight *w, int32_t expert, const float *x, int32_t T, float *y) {
+  if (!c || !w || !x || !y) return fail(WL_E_ARG, "wl_matmul: null argument");
+  int rc = check_expert(w, expert);
+  if (rc) return rc;
+  if (T <= 0) return fail(WL_E_SHAPE, "MatMul shape mismatch: T = %d", T);
+  const uint8_t *base;
+  int64_t rows;
+  operand(w, expert, &base, &rows);
+  const size_t xb = (size_t)T * w->cols * 4, yb = (size_t)T * rows * 4;
+  if ((rc = ensure(c, S_X, xb)) || (rc = ensure(c, S_Y, yb))) return rc;
+  WL_HIP(hipMemcpyAsync(c->buf[S_X], x, xb, hipMemcpyHostToDevice, c->stream), "copy x");
+  if ((rc = matmul_dev(c, w, expert, (const float *)c->buf[S_X], T, (float *)c->buf[S_Y]))) return rc;
+  WL_HIP(hipMemcpyAsync(y, c->buf[S_Y], yb, hipMemcpyDeviceToHost, c->stream), "copy y");
+  WL_HIP(hipStreamSynchronize(c->stream), "matmul");
+  return WL_OK;
+}
+
+extern "C" int wl_matmul_multi_dev(wl_ctx *c, int32_t n, const wl_weight *const *ws, const float *d_x, int32_t T,
+                                   float *const *d_ys) {
+  if (!c || !ws || !d_x || !d_ys) return fail(WL_E_ARG, "wl_matmul_multi_dev: null argument");
+  if (n <= 0 || n > wl::GEMV_MAX_SEGS) return fail(WL_E_ARG, "wl_matmul_multi_dev: n = %d outside 1..%d", n,
+                                                   wl::GEMV_MAX_SEGS);
+  if (T <= 0 || T > 8) return fail(WL_E_SHAPE, "wl_matmul_multi_dev: T = %d outside 1..8", T);
+  bool same = true, mixed_ok = true;
+  for (int i = 0; i < n; i++) {
+    if (!ws[i] || !d_ys[i]) return fail(WL_E_ARG, "wl_matmul_multi_dev: null weight or output %d", i);
+    if (ws[i]->cols != ws[0]->cols) return fail(WL_E_SHAPE, "MatMul shape mismatch: fused matrices read different x");
+    if (!wl::gemv_supports(ws[i]->type)) return fail(WL_E_UNSUPPORTED, "No GPU matmul for %s.", type_name(ws[i]->type));
+    same = same && ws[i]->type == ws[0]->type;
+    mixed_ok = mixed_ok && wl::gemv_mixed_supports(ws[i]->type);
+  }
+  if (!same && !mixed_ok) {
+    for (int i = 0; i < n; i++) {
+      int rc = matmul_dev(c, ws[i], -1, d_x, T, d_ys[i]);
+      if (rc) return rc;
+    }
+    return WL_OK;
+  }
+  wl::GemvParams p{};
+  p.nseg = n;
+  for (int i = 0; i < n; i++) {
+    const wl_weight *w = ws[i];
+    p.seg[i].w = w->dev;
+    p.seg[i].row_bytes = w->row_bytes;
+    p.seg[i].rows = (int)(w->rows * w->experts);
+    p.seg[i].y = d_ys[i];
+    p.seg[i].ldy = p.seg[i].rows;
+    p.seg[i].type = w->type;
+  }
+  p.x = d_x;
+  p.ldx = (int)ws[0]->cols;
+  p.cols = (int)ws[0]->cols;
+  p.T = T;
+  if (same) WL_HIP(wl::gemv_launch(ws[0]->type, 1, p, c->stream), "gemv launch");
+  else WL_HIP(wl::gemv_launch_mixed(p, c->stream), "gemv launch");
+  return WL_OK;
+}
+
+extern "C" int wl_gate_up_dev(wl_ctx *c, const wl_weight *gate, const wl_weight *up, int32_t expert,
+                              const float *d_x, int32_t T, float *d_h) {
+  if (!c || !gate || !up || !d_x || !d_h) return fail(WL_E_ARG, "wl_gate_up_dev: null argument");
+  int rc = check_expert(gate, expert);
+  if (!rc) rc = check_expert(up, expert);
+  if (rc) return rc;
+  if (gate->type != up->type) return fail(WL_E_UNSUPPORTED, "gate and up must share a type for the fused launch");
+  if (gate->rows != up->rows || gate->cols != up->cols || gate->experts != up->experts)
+    return fail(WL_E_SHAPE, "MatMul shape mismatch: gate and up differ in shape");
+  if (!wl::gemv_supports(gate->type)) return fail(WL_E_UNSUPPORTED, "No GPU matmul for %s.", type_name(gate->type));
+  if (T <= 0) return fail(WL_E_SHAPE, "MatMul shape mismatch: T = %d", T);
+  const uint8_t *gb, *ub;
+  int64_t rows;
+  operand(gate, expert, &gb, &rows);
+  operand(up, expert, &ub, &rows);
+  for (int t0 = 0; t0 < T; t0 += 8) {
+    wl::GemvParams p{};
+    p.nseg = 1;
+    p.seg[0].w = gb;
+    p.seg[0].w2 = ub;
+    p.seg[0].row_bytes = gate->row_bytes;
+    p.seg[0].rows = (int)rows;
+    p.seg[0].y = d_h + (int64_t)t0 * rows;
+    p.seg[0].ldy = (int)rows;
+    p.seg[0].type = gate->type;
+    p.x = d_x + (int64_t)t0 * gate->cols;
+    p.ldx = (int)gate->cols;
+    p.cols = (int)gate->cols;
+    p.T = T - t0 < 8 ? T - t0 : 8;
+    WL_HIP(wl::gemv_launch(gate->type, 2, p, c->stream), "gemv launch");
+  }
+  return WL_OK;
+}
+
+extern "C" int wl_swiglu(wl_ctx *c, const wl_weight *gate, const wl_weight *up, const wl_weight *down,
+                         int32_t expert, const float *x, int32_t T, float *out) {
+  if (!c || !gate || !up || !down || !x || !out) return fail(WL_E_ARG, "wl_swiglu: null argument");
+  if (T <= 0) return fail(WL_E_SHAPE, "MatMul shape mismatch: T = %d", T);
+  if (down->cols != gate->rows) return fail(WL_E_SHAPE, "MatMul shape mismatch for the down projection");
+  int rc = check_expert(down, expert);
+  if (rc) return rc;
+  const int64_t ff = gate->rows * (expert < 0 ? gate->experts : 1);
+  const int64_t embd = down->rows * (expert < 0 ? down->experts : 1);
+  const size_t xb = (size_t)T * gate->cols * 4, hb = (size_t)T * ff * 4, ob = (size_t)T * embd * 4;
+  if ((rc = ensure(c, S_X, xb)) || (rc = ensure(c, S_H, hb)) || (rc = ensure(c, S_OUT, ob))) return rc;
+  WL_HIP(hipMemcpyAsync(c->buf[S_X], x, xb, hipMemcpyHostToDevice, c->stream), "copy x");
+  if (gate->type == up->type) {
+    rc = wl_gate_up_dev(c, gate, up, expert, (const float *)c->buf[S_X], T, (float *)c->buf[S_H]);
+  } else {
+    rc = fail(WL_E_UNSUPPORTED, "gate and up of different types are not fused");
+  }
+  if (rc) return rc;
+  if ((rc = matmul_dev(c, down, expert, (const float *)c->buf[S_H], T, (float *)c->buf[S_OUT]))) return rc;
+  WL_HIP(hipMemcpyAsync(out, c->buf[S_OUT], ob, hipMemcpyDeviceToHost, c->stream), "copy out");
+  WL_HIP(hipStreamSynchronize(c->stream), "swiglu");
+  return WL_OK;
+}
+
+// ----------------------------------------------------------------------------- dequant
+
+extern "C" int wl_dequant_dev(wl_ctx *c, const wl_weight *w, int64_t row0, int64_t nrows, float *d_dst) {
+  if (!c || !w || !d_dst) return fail(WL_E_ARG, "wl_dequant_dev: null argument");
+  const int64_t total = w->rows * w->experts;
+  if (row0 < 0 || nrows < 0 || row0 + nrows > total)
+    return fail(WL_E_ARG, "rows %lld..%lld are outside the tensor's %lld rows", (long long)row0,
+                (long long)(row0 + nrows), (long long)total);
+  WL_HIP(wl::dequant_launch(w->type, w->dev, w->row_bytes, row0, nrows, w->cols, d_dst, c->stream), "dequant launch");
+  return WL_OK;
+}
+
+extern "C" int wl_dequant_f32(wl_ctx *c, const wl_weight *w, int64_t row0, int64_t nrows, float *dst) {
+  if (!c || !w || !dst) return fail(WL_E_ARG, "wl_dequant_f32: null argument");
+  const size_t bytes = (size_t)nrows * w->cols * 4;
+  int rc = ensure(c, S_Y, bytes ? bytes : 4);
+  if (rc) return rc;
+  if ((rc = wl_dequant_dev(c, w, row0, nrows, (float *)c->buf[S_Y]))) return rc;
+  WL_HIP(hipMemcpyAsync(dst, c->buf[S_Y], bytes, hipMemcpyDeviceToHost, c->stream), "copy dst");
+  WL_HIP(hipStreamSynchronize(c->stream), "dequant");
+  return WL_OK;
+}
+
+// --------------------------------------------------------------------------------- MoE
+
+// scratch layout in S_MOE: sel | wts | prob | plan | h | yd
+struct MoeScratch {
+  size_t sel, wts, prob, plan, h, yd, total;
+};
+
+static MoeScratch moe_layout(int T, int k, int ne, int ff, int embd) {
+  auto al = [](size_t v) { return (v + 255) & ~size_t(255); };
+  MoeScratch s{};
+  size_t o = 0;
+  s.sel = o; o = al(o + (size_t)T * k * 4);
+  s.wts = o; o = al(o + (size_t)T * k * 4);
+  s.prob = o; o = al(o + (size_t)T * ne * 4);
+  s.plan = o; o = al(o + sizeof(wl::MoePlan));
+  s.h = o; o = al(o + (size_t)T * k * ff * 4);
+  s.yd = o; o = al(o + (size_t)T * k * embd * 4);
+  s.total = o;
+  return s;
+}
+
+extern "C" int wl_route(wl_ctx *c, const float *logits, int32_t T, int32_t n, int32_t k, int32_t renorm,
+                        int32_t *sel, float *wts) {
+  if (!c || !logits || !sel || !wts) return fail(WL_E_ARG, "wl_route: null argument");
+  if (T <= 0 || n <= 0 || k <= 0 || k > n) return fail(WL_E_ARG, "wl_route: bad sizes T=%d n=%d k=%d", T, n, k);
+  const size_t lb = (size_t)T * n * 4, kb = (size_t)T * k * 4;
+  int rc;
+  if ((rc = ensure(c, S_AUX, 2 * lb + 2 * kb + 1024))) return rc;
+  uint8_t *base = (uint8_t *)c->buf[S_AUX];
+  float *d_l = (float *)base;
+  float *d_p = (float *)(base + lb);
+  int *d_sel = (int *)(base + 2 * lb);
+  float *d_w = (float *)(base + 2 * lb + kb);
+  WL_HIP(hipMemcpyAsync(d_l, logits, lb, hipMemcpyHostToDevice, c->stream), "copy logits");
+  WL_HIP(wl::route_launch(d_l, T, n, k, renorm, d_sel, d_w, d_p, c->stream), "route launch");
+  WL_HIP(hipMemcpyAsync(sel, d_sel, kb, hipMemcpyDeviceToHost, c->stream), "copy sel");
+  WL_HIP(hipMemcpyAsync(wts, d_w, kb, hipMemcpyDeviceToHost, c->stream), "copy wts");
+  WL_HIP(hipStreamSynchronize(c->stream), "route");
+  return WL_OK;
+}
+
+static int moe_check(const wl_weight *g, const wl_weight *u, const wl_weight *d, int32_t k) {
+  if (!g || !u || !d) return fail(WL_E_ARG, "moe: null expert tensor");
+  if (g->type != u->type) return fail(WL_E_UNSUPPORTED, "moe: gate and up must share a type");
+  if (!wl::moe_supports(g->type) || !wl::moe_supports(d->type))
+    return fail(WL_E_UNSUPPORTED, "No GPU expert matmul for %s / %s.", type_name(g->type), type_name(d->type));
+  if (g->experts != u->experts || g->experts != d->experts || g->rows != u->rows || g->cols != u->cols ||
+      d->cols != g->rows || d->rows != g->cols)
+    return fail(WL_E_SHAPE, "MatMul shape mismatch between the expert tensors");
+  if (k <= 0 || k > wl::MOE_MAX_K || k > g->experts) return fail(WL_E_ARG, "moe: k = %d outside 1..%d", k,
+                                                                  g->experts < wl::MOE_MAX_K ? g->experts : wl::MOE_MAX_K);
+  return WL_OK;
+}
+
+static int moe_dev(wl_ctx *c, const float *d_logits, int32_t k, int32_t renorm, const wl_weight *g,
+                   const wl_weight *u, const wl_weight *d, const float *d_x, int32_t T, float *d_out) {
+  int rc = moe_check(g, u, d, k);
+  if (rc) return rc;
+  const int ne = g->experts, ff = (int)g->rows, embd = (int)g->cols;
+  for (int t0 = 0; t0 < T; t0 += wl::MOE_MAX_T) {
+    const int Tc = T - t0 < wl::MOE_MAX_T ? T - t0 : wl::MOE_MAX_T;
+    MoeScratch s = moe_layout(Tc, k, ne, ff, embd);
+    if ((rc = ensure(c, S_MOE, s.total))) return rc;
+    uint8_t *b = (uint8_t *)c->buf[S_MOE];
+    wl::MoeLaunch m{};
+    m.logits = d_logits + (int64_t)t0 * ne;
+    m.T = Tc; m.ne = ne; m.k = k; m.renorm = renorm;
+    m.gu_type = g->type; m.d_type = d->type;
+    m.gate = g->dev; m.up = u->dev; m.down = d->dev;
+    m.gu_row_bytes = g->row_bytes; m.d_row_bytes = d->row_bytes;
+    m.ff = ff; m.embd = embd;
+    m.x = d_x + (int64_t)t0 * embd;
+    m.out = d_out + (int64_t)t0 * embd;
+    m.sel = (int *)(b + s.sel); m.wts = (float *)(b + s.wts); m.prob = (float *)(b + s.prob);
+    m.plan = (wl::MoePlan *)(b + s.plan); m.h = (float *)(b + s.h); m.yd = (float *)(b + s.yd);
+    WL_HIP(wl::moe_launch(m, c->stream), "moe launch");
+  }
+  return WL_OK;
+}
+
+extern "C" int wl_moe_ffn_dev(wl_ctx *c, const float *d_logits, int32_t k, int32_t renorm, const wl_weight *g,
+                              const wl_weight *u, const wl_weight *d, const float *d_x, int32_t T, float *d_out) {
+  if (!c || !d_logits || !d_x || !d_out) return fail(WL_E_ARG, "wl_moe_ffn_dev: null argument");
+  if (T <= 0) return fail(WL_E_SHAPE, "MatMul shape mismatch: T = %d", T);
+  return moe_dev(c, d_logits, k, renorm, g, u, d, d_x, T, d_out);
+}
+
+extern "C" int wl_moe_ffn(wl_ctx *c, const float *logits, int32_t k, int32_t renorm, const wl_weight *g,
+                          const wl_weight *u, const wl_weight *d, const float *x, int32_t T, float *out,
+                          int32_t *expert_runs) {
+  if (!c || !logits || !x || !out) return fail(WL_E_ARG, "wl_moe_ffn: null argument");
+  if (T <= 0) return fail(WL_E_SHAPE, "MatMul shape mismatch: T = %d", T);
+  int rc = moe_check(g, u, d, k);
+  if (rc) return rc;
+  const int ne = g->experts, embd = (int)g->cols;
+  const size_t lb = (size_t)T * ne * 4, xb = (size_t)T * embd * 4;
+  if ((rc = ensure(c, S_AUX, lb)) || (rc = ensure(c, S_X, xb)) || (rc = ensure(c, S_OUT, xb))) return rc;
+  WL_HIP(hipMemcpyAsync(c->buf[S_AUX], logits, lb, hipMemcpyHostToDevice, c->stream), "copy logits");
+  WL_HIP(hipMemcpyAsync(c->buf[S_X], x, xb, hipMemcpyHostToDevice, c->stream), "copy x");
+  int runs = 0;
+  for (int t0 = 0; t0 < T; t0 += wl::MOE_MAX_T) {
+    const int Tc = T - t0 < wl::MOE_MAX_T ? T - t0 : wl::MOE_MAX_T;
+    if ((rc = moe_dev(c, (const float *)c->buf[S_AUX] + (int64_t)t0 * ne, k, renorm, g, u, d,
+                      (const float *)c->buf[S_X] + (int64_t)t0 * embd, Tc, (float *)c->buf[S_OUT] + (int64_t)t0 * embd)))
+      return rc;
+    if (expert_runs) {
+      MoeScratch s = moe_layout(Tc, k, ne, (int)g->rows, embd);
+      int ns = 0;
+      WL_HIP(hipMemcpyAsync(&ns, (uint8_t *)c->buf[S_MOE] + s.plan + offsetof(wl::MoePlan, nslots), sizeof(int),
+                            hipMemcpyDeviceToHost, c->stream), "copy runs");
+      WL_HIP(hipStreamSynchronize(c->stream), "moe");
+      runs += ns;
+    }
+  }
+  WL_HIP(hipMemcpyAsync(out, c->buf[S_OUT], xb, hipMemcpyDeviceToHost, c->stream), "copy out");
+  WL_HIP(hipStreamSynchronize(c->stream), "moe");
+  if (expert_runs) *expert_runs = runs;
+  return WL_OK;
+}

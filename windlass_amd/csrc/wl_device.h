@@ -1,0 +1,102 @@
+// wl_device.h - device-side building blocks shared by the kernels: fp16 decoding, aligned
+// loads of 2-byte-aligned GGUF fields, and the fp16-denormal multiply-add used by the GEMVs.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wl {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// Exact fp16 -> fp32 from the bit fields (sign, 5-bit exponent, 10-bit mantissa), including
+// subnormals, Inf and NaN payloads, as the reference's table decode does
+// (src/Half.cs:59-90). Used where the result must be bit-exact (dequantization).
+__device__ __forceinline__ float half_bits_exact(uint32_t h) {
+  uint32_t sign = (h >> 15) << 31;
+  uint32_t exp = (h >> 10) & 0x1F;
+  uint32_t mant = h & 0x3FF;
+  uint32_t bits;
+  if (exp == 0) {
+    if (mant == 0) {
+      bits = sign;
+    } else {
+      // normalise: the leading one of mant moves to bit 10
+      uint32_t lz = __builtin_clz(mant) - 21;  // shifts needed, 1..10
+      mant = (mant << lz) & 0x3FF;
+      bits = sign | ((113u - lz) << 23) | (mant << 13);
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7F800000u | (mant << 13);
+  } else {
+    bits = sign | ((exp + 112u) << 23) | (mant << 13);
+  }
+  return __uint_as_float(bits);
+}
+
+// Hardware fp16 -> fp32 (exact for every finite value; used inside the GEMVs).
+__device__ __forceinline__ float half_lo(uint32_t w) {
+  return (float)__builtin_bit_cast(half2_t, w).x;
+}
+__device__ __forceinline__ float half_hi(uint32_t w) {
+  return (float)__builtin_bit_cast(half2_t, w).y;
+}
+
+// acc + f16(pair.lo/hi) * x in one v_fma_mix_f32. With a small integer n in the low bits of
+// a half (no exponent bits), the half is the subnormal n * 2^-24, so this is an exact
+// integer-to-float conversion fused into the multiply-add, scaled by a power of two that
+// the caller folds back into the block scale.
+__device__ __forceinline__ float fma_lo(uint32_t pair, float x, float acc) {
+  return __builtin_fmaf(half_lo(pair), x, acc);
+}
+__device__ __forceinline__ float fma_hi(uint32_t pair, float x, float acc) {
+  return __builtin_fmaf(half_hi(pair), x, acc);
+}
+
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {
+  return *reinterpret_cast<const uint4 *>(p);
+}
+__device__ __forceinline__ uint32_t ld4(const uint8_t *p) {
+  return *reinterpret_cast<const uint32_t *>(p);
+}
+
+// 8 bytes at a 2-byte-aligned address, from the three aligned dwords that cover them. Reads
+// up to 4 bytes past p+8: every weight buffer carries padding after its last block.
+__device__ __forceinline__ uint2 ld8_a2(const uint8_t *p) {
+  const uint32_t *a = reinterpret_cast<const uint32_t *>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
+  uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3) * 8;
+  uint32_t w0 = a[0], w1 = a[1], w2 = a[2];
+  return make_uint2(__builtin_amdgcn_alignbit(w1, w0, sh), __builtin_amdgcn_alignbit(w2, w1, sh));
+}
+
+// The fp16 at a 2-byte-aligned address.
+__device__ __forceinline__ uint32_t ld_half_a2(const uint8_t *p) {
+  uint32_t w = *reinterpret_cast<const uint32_t *>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
+  return (reinterpret_cast<uintptr_t>(p) & 2) ? (w >> 16) : (w & 0xFFFF);
+}
+
+__device__ __forceinline__ void ld_x16(const float *p, float *v) {
+  const float4 *q = reinterpret_cast<const float4 *>(p);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float4 f = q[i];
+    v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+  }
+}
+
+__device__ __forceinline__ void ld_x8(const float *p, float *v) {
+  const float4 *q = reinterpret_cast<const float4 *>(p);
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    float4 f = q[i];
+    v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+  }
+}
+
+// Sum over the 64 lanes of a wave, the same tree on every lane and every call.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+}  // namespace wl

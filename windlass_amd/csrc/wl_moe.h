@@ -1,0 +1,59 @@
+// wl_moe.h - host-side interface of the routed MoE launches.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wl {
+
+constexpr int MOE_MAX_T = 8;   // tokens per pass (larger batches run in passes of 8)
+constexpr int MOE_MAX_K = 16;  // experts per token
+constexpr int MOE_MAX_PAIRS = MOE_MAX_T * MOE_MAX_K;
+
+// Device-resident routing plan, written by plan_kernel.
+struct MoePlan {
+  int nslots;                              // distinct experts chosen (ExpertRuns)
+  int slot_expert[MOE_MAX_PAIRS];          // ascending expert ids
+  int slot_ntok[MOE_MAX_PAIRS];
+  int slot_tok[MOE_MAX_PAIRS][MOE_MAX_T];  // tokens of the slot, ascending
+  int slot_pair[MOE_MAX_PAIRS][MOE_MAX_T]; // their pair (hidden/out row) indices
+  int tok_pair[MOE_MAX_T][MOE_MAX_K];      // pair of (token, j-th choice)
+  float tok_w[MOE_MAX_T][MOE_MAX_K];
+  int comb_pair[MOE_MAX_T][MOE_MAX_K];     // a token's pairs, ascending expert id
+  float comb_w[MOE_MAX_T][MOE_MAX_K];
+};
+
+struct MoeGemvArgs {
+  const MoePlan *plan;
+  const uint8_t *w, *w2;
+  int64_t row_bytes;
+  int rows, cols;
+  const float *x;
+  int64_t ldx;
+  int x_by_pair;  // x rows indexed by pair (down) or by token (gate/up)
+  float *y;
+  int64_t ldy;
+};
+
+struct MoeLaunch {
+  const float *logits;  // [T][ne]
+  int T, ne, k, renorm;
+  int gu_type, d_type;
+  const uint8_t *gate, *up, *down;  // stacked expert tensors
+  int64_t gu_row_bytes, d_row_bytes;
+  int ff, embd;
+  const float *x;  // [T][embd]
+  float *out;      // [T][embd]
+  // scratch
+  int *sel;
+  float *wts, *prob;  // [T][k], [T][k], [T][ne]
+  MoePlan *plan;
+  float *h;   // [pairs][ff]
+  float *yd;  // [pairs][embd]
+};
+
+bool moe_supports(int type);
+hipError_t route_launch(const float *logits, int T, int n, int k, int renorm, int *sel, float *wts, float *prob,
+                        hipStream_t st);
+hipError_t moe_launch(const MoeLaunch &m, hipStream_t st);
+
+}  // namespace wl

@@ -1,0 +1,36 @@
+"""Synthetic, seeded GGUF blocks at the benchmark configurations.
+
+Block contents follow the workload definitions: fp16 scales d (and dmin) = |N(0,1)| * 0.01
+encoded round-to-nearest-even; Q4_K 6-bit scales/mins and 4-bit quants uniform (random bytes
+make every packed field uniform and independent); Q6_K int8 scales uniform over all bytes and
+6-bit quants uniform; Q8_0 int8 quants uniform in [-127, 127]; IQ4_XS / IQ2_XXS random payload.
+"""
+import numpy as np
+
+from .backend import GgmlType, layout
+
+# offsets of the fp16 scale fields per block
+_SCALE_FIELDS = {GgmlType.Q8_0: (0,), GgmlType.Q4_K: (0, 2), GgmlType.Q6_K: (208,),
+                 GgmlType.IQ4_XS: (0,), GgmlType.IQ2_XXS: (0,)}
+
+
+def half_scales(rng, n):
+    """fp16 bit patterns of |N(0,1)| * 0.01 (RNE)."""
+    return (np.abs(rng.standard_normal(n, dtype=np.float32)) * np.float32(0.01)).astype(np.float16).view(np.uint16)
+
+
+def blocks(t, rows, cols, rng):
+    """rows x cols values of type t as raw blocks (uint8, rows * row_bytes)."""
+    t = GgmlType(int(t))
+    be, bb = layout(t)
+    nb = rows * cols // be
+    data = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    if t == GgmlType.Q8_0:
+        data[:, 2:] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int16).astype(np.int8).view(np.uint8)
+    for off in _SCALE_FIELDS[t]:
+        data[:, off:off + 2] = half_scales(rng, nb).view(np.uint8).reshape(nb, 2)
+    return data.reshape(-1)
+
+
+def activations(rng, T, cols):
+    return rng.standard_normal((T, cols), dtype=np.float32)
