@@ -32,6 +32,7 @@ struct wl_weight {
 
 struct wl_ctx {
   int device;
+  int num_cu;
   hipStream_t stream;
   // growable scratch (device)
   void *buf[6];
@@ -126,6 +127,9 @@ extern "C" int wl_create(int device, wl_ctx **out) {
   WL_HIP(hipSetDevice(device), "hipSetDevice");
   wl_ctx *c = new wl_ctx();
   c->device = device;
+  hipDeviceProp_t prop;
+  c->num_cu = hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0
+                  ? prop.multiProcessorCount : 256;
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete c;
@@ -247,7 +251,7 @@ static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float
     p.ldx = (int)w->cols;
     p.cols = (int)w->cols;
     p.T = T - t0 < 8 ? T - t0 : 8;
-    WL_HIP(wl::gemv_launch(w->type, 1, p, c->stream), "gemv launch");
+    WL_HIP(wl::gemv_launch(w->type, 1, p, c->num_cu, c->stream), "gemv launch");
   }
   return WL_OK;
 }
@@ -310,8 +314,8 @@ extern "C" int wl_matmul_multi_dev(wl_ctx *c, int32_t n, const wl_weight *const 
   p.ldx = (int)ws[0]->cols;
   p.cols = (int)ws[0]->cols;
   p.T = T;
-  if (same) WL_HIP(wl::gemv_launch(ws[0]->type, 1, p, c->stream), "gemv launch");
-  else WL_HIP(wl::gemv_launch_mixed(p, c->stream), "gemv launch");
+  if (same) WL_HIP(wl::gemv_launch(ws[0]->type, 1, p, c->num_cu, c->stream), "gemv launch");
+  else WL_HIP(wl::gemv_launch_mixed(p, c->num_cu, c->stream), "gemv launch");
   return WL_OK;
 }
 
@@ -344,7 +348,7 @@ extern "C" int wl_gate_up_dev(wl_ctx *c, const wl_weight *gate, const wl_weight 
     p.ldx = (int)gate->cols;
     p.cols = (int)gate->cols;
     p.T = T - t0 < 8 ? T - t0 : 8;
-    WL_HIP(wl::gemv_launch(gate->type, 2, p, c->stream), "gemv launch");
+    WL_HIP(wl::gemv_launch(gate->type, 2, p, c->num_cu, c->stream), "gemv launch");
   }
   return WL_OK;
 }
@@ -471,7 +475,7 @@ static int moe_dev(wl_ctx *c, const float *d_logits, int32_t k, int32_t renorm, 
     m.out = d_out + (int64_t)t0 * embd;
     m.sel = (int *)(b + s.sel); m.wts = (float *)(b + s.wts); m.prob = (float *)(b + s.prob);
     m.plan = (wl::MoePlan *)(b + s.plan); m.h = (float *)(b + s.h); m.yd = (float *)(b + s.yd);
-    WL_HIP(wl::moe_launch(m, c->stream), "moe launch");
+    WL_HIP(wl::moe_launch(m, c->num_cu, c->stream), "moe launch");
   }
   return WL_OK;
 }

@@ -1,14 +1,22 @@
 // wl_codecs.h - per-format lane codecs for the decode GEMV.
 //
-// A wave64 walks a group of weight rows; in each step every lane owns one fixed slice of one
-// GGUF block (LPB lanes per block, 64/LPB consecutive blocks per step) and the matching slice
-// of x. A codec knows, for its block format:
-//   Xs     - the x slice of a lane for one token (values plus the sums the format needs),
-//   W      - one row's block slice unpacked into registers (done once, reused for every token),
-//   load_x - read the x slice,  decode - read and unpack the weight slice,
-//   dot    - the lane's partial sum of W * x for one token.
+// Every lane of a wave owns one fixed slice of one block column (LPB lanes per block, 64/LPB
+// consecutive blocks per wave, i.e. 2048 columns per wave for every format). A codec knows,
+// for its block format:
+//   Lane   - the lane's constant offsets and masks (from its slice index `sub`),
+//   Xs     - the lane's x slice for one token, pre-scaled so the unpacked quants can enter the
+//            multiply-add as fp16 subnormals (load_x also forms the sums the format needs),
+//   Raw    - one row's block slice as loaded (load: memory reads only),
+//   W      - that slice unpacked into registers (unpack; reused for every token),
+//   dot    - the lane's partial sum of W * x for one token, in the reference's units.
+//   R1     - rows per group at one token (bounded by the registers a row's Raw takes).
 // The partial of a lane is a fixed sequence of fp32 operations on that lane's slice, the same
 // for every token count, so a token's result never depends on how many tokens run with it.
+//
+// Integer quants enter v_fma_mix_f32 as the fp16 subnormal n * 2^-24 (n in the low bits of a
+// half, no exponent bits): an exact integer-to-float conversion fused into the multiply-add.
+// The 2^24 is folded into x once (an exact power-of-two scaling), so the products are the
+// reference's n * x.
 //
 // Block layouts (ggml-common.h, restated in src/Quants.cs and src/IQuants.cs):
 //   Q8_0    34 B / 32:  d f16 | q int8[32]                                (src/Quants.cs:251-259)
@@ -22,6 +30,9 @@
 
 namespace wl {
 
+constexpr float kTwo24 = 16777216.f;
+constexpr float kTwo20 = 1048576.f;
+
 // LDS tables some codecs use; filled once per workgroup by init_lds.
 struct Lds {
   uint32_t grid16[256][4];   // IQ2_XXS grid entries as four fp16-subnormal byte pairs
@@ -32,45 +43,62 @@ struct Lds {
 // Lane slice: 16 bytes of qs, i.e. 16 low nibbles of sub-block 2j (x[64j+16h .. +16]) and
 // 16 high nibbles of sub-block 2j+1 (x[64j+32+16h .. +16]), with j = sub/2, h = sub%2.
 struct Q4K {
-  static constexpr int BLOCK = 256, BYTES = 144, LPB = 8, NEED_LDS = 0;
+  static constexpr int BLOCK = 256, BYTES = 144, LPB = 8, NEED_LDS = 0, R1 = 8;
+  struct Lane {
+    int j, h, sh;
+    bool jlo;
+    uint32_t m1, m2;
+  };
   struct Xs { float lo[16], hi[16], slo, shi; };
-  struct W { uint32_t m[16]; float ds1, ds2, dm1, dm2; };
+  struct Raw { uint4 hdr, q; };
+  struct W { uint32_t m[16]; float fs1, fs2, fm1, fm2, d, dmin; };
 
-  __device__ static void load_x(const float *xb, int sub, Xs &x) {
-    const int j = sub >> 1, h = sub & 1;
-    ld_x16(xb + 64 * j + 16 * h, x.lo);
-    ld_x16(xb + 64 * j + 32 + 16 * h, x.hi);
+  __device__ static Lane lane(int sub) {
+    Lane L;
+    L.j = sub >> 1;
+    L.h = sub & 1;
+    L.sh = 16 * (L.j & 1);
+    L.jlo = L.j < 2;
+    L.m1 = L.jlo ? 0x3F3F3F3Fu : 0x0F0F0F0Fu;
+    L.m2 = L.jlo ? 0u : 0x30303030u;
+    return L;
+  }
+
+  __device__ static void load_x(const float *xb, const Lane &L, Xs &x) {
+    ld_x16(xb + 64 * L.j + 16 * L.h, x.lo);
+    ld_x16(xb + 64 * L.j + 32 + 16 * L.h, x.hi);
     float a = 0.f, b = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; i++) { a += x.lo[i]; b += x.hi[i]; }
-    x.slo = a; x.shi = b;
+    x.slo = a;
+    x.shi = b;
+    // low nibbles enter as n*2^-24, high nibbles (kept in bits 4-7) as n*2^-20
+#pragma unroll
+    for (int i = 0; i < 16; i++) { x.lo[i] *= kTwo24; x.hi[i] *= kTwo20; }
   }
 
-  __device__ static void decode(const uint8_t *blk, int sub, const Lds &, W &w) {
-    const uint4 hdr = ld16(blk);
-    const uint4 q = ld16(blk + 16 + 16 * sub);
-    const int j = sub >> 1;
-    // The 6-bit scales and mins of all eight sub-blocks as bytes (get_scale_min_k4,
-    // src/Quants.cs:321-330): sub-blocks 0-3 from bytes 0-7, 4-7 from bytes 8-11 plus the
-    // top two bits of bytes 0-7.
-    uint32_t S, M;
-    if (j < 2) {
-      S = hdr.y & 0x3F3F3F3Fu;
-      M = hdr.z & 0x3F3F3F3Fu;
-    } else {
-      S = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
-      M = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
-    }
-    const int sh = (j & 1) * 16;
-    const float s1 = (float)((S >> sh) & 0xFF), s2 = (float)((S >> (sh + 8)) & 0xFF);
-    const float m1 = (float)((M >> sh) & 0xFF), m2 = (float)((M >> (sh + 8)) & 0xFF);
-    const float d = half_lo(hdr.x), dmin = half_hi(hdr.x);
-    // Low nibbles enter as n*2^-24, high nibbles (kept in bits 4-7) as n*2^-20.
-    w.ds1 = d * (s1 * 16777216.f);
-    w.ds2 = d * (s2 * 1048576.f);
-    w.dm1 = dmin * m1;
-    w.dm2 = dmin * m2;
-    const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+  __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
+    r.hdr = ld16(blk);
+    r.q = ld16(blk + 16 + 16 * (2 * L.j + L.h));
+  }
+
+  __device__ static void unpack(const Raw &r, const Lane &L, const Lds &, W &w) {
+    const uint4 h = r.hdr;
+    // The 6-bit scale and min of sub-blocks 2j and 2j+1 (get_scale_min_k4,
+    // src/Quants.cs:321-330): sub-blocks 0-3 are the low 6 bits of bytes 0-7; 4-7 take their
+    // low 4 bits from bytes 8-11 and the top two from the top of bytes 0-7. The lane's j is
+    // fixed, so both cases are one masked form with lane-constant masks.
+    const uint32_t P = L.jlo ? h.y : h.w;
+    const uint32_t Q = L.jlo ? h.z : (h.w >> 4);
+    const uint32_t S = ((P & L.m1) | ((h.y >> 2) & L.m2)) >> L.sh;
+    const uint32_t M = ((Q & L.m1) | ((h.z >> 2) & L.m2)) >> L.sh;
+    w.fs1 = (float)(S & 0xFF);
+    w.fs2 = (float)((S >> 8) & 0xFF);
+    w.fm1 = (float)(M & 0xFF);
+    w.fm2 = (float)((M >> 8) & 0xFF);
+    w.d = half_lo(h.x);
+    w.dmin = half_hi(h.x);
+    const uint32_t qq[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const uint32_t v = qq[i], v8 = v >> 8;
@@ -95,9 +123,9 @@ struct Q4K {
       b = fma_hi(w.m[4 * i + 3], x.hi[4 * i + 3], b);
     }
     // d*(s1*a1 + s2*a2) - dmin*(m1*x1 + m2*x2)   (src/Quants.cs:129)
-    float mins = __builtin_fmaf(w.dm2, x.shi, w.dm1 * x.slo);
-    float r = __builtin_fmaf(w.ds2, b, w.ds1 * a);
-    return r - mins;
+    const float sc = __builtin_fmaf(w.fs2, b, w.fs1 * a);
+    const float mn = __builtin_fmaf(w.fm2, x.shi, w.fm1 * x.slo);
+    return __builtin_fmaf(w.d, sc, -(w.dmin * mn));
   }
 };
 
@@ -105,13 +133,23 @@ struct Q4K {
 // Lane slice: half hh = sub/4 of the block (128 values) and l = 8g..8g+7 with g = sub%4:
 // the four values l, l+32, l+64, l+96 of each l (scales sc[l/16 + 0,2,4,6]).
 struct Q6K {
-  static constexpr int BLOCK = 256, BYTES = 210, LPB = 8, NEED_LDS = 0;
+  static constexpr int BLOCK = 256, BYTES = 210, LPB = 8, NEED_LDS = 0, R1 = 4;
+  struct Lane { int hh, g, s; };
   struct Xs { float v[4][8]; float s[4]; };
-  struct W { uint32_t p[4][4]; float dq[4], dz[4]; };
+  // the aligned dwords around each 2-byte-aligned field, and the byte shift (0 or 16)
+  struct Raw { uint32_t l1[3], l2[3], h[3], sc[3], dw; uint32_t sh; };
+  struct W { uint32_t p[4][4]; float dq[4]; };
 
-  __device__ static void load_x(const float *xb, int sub, Xs &x) {
-    const int hh = sub >> 2, g = sub & 3;
-    const float *base = xb + 128 * hh + 8 * g;
+  __device__ static Lane lane(int sub) {
+    Lane L;
+    L.hh = sub >> 2;
+    L.g = sub & 3;
+    L.s = L.g >> 1;
+    return L;
+  }
+
+  __device__ static void load_x(const float *xb, const Lane &L, Xs &x) {
+    const float *base = xb + 128 * L.hh + 8 * L.g;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       ld_x8(base + 32 * k, x.v[k]);
@@ -119,27 +157,41 @@ struct Q6K {
 #pragma unroll
       for (int i = 0; i < 8; i++) s += x.v[k][i];
       x.s[k] = s;
+#pragma unroll
+      for (int i = 0; i < 8; i++) x.v[k][i] *= kTwo24;
     }
   }
 
-  __device__ static void decode(const uint8_t *blk, int sub, const Lds &, W &w) {
-    const int hh = sub >> 2, g = sub & 3;
-    const uint2 ql1 = ld8_a2(blk + 64 * hh + 8 * g);
-    const uint2 ql2 = ld8_a2(blk + 64 * hh + 32 + 8 * g);
-    const uint2 qh = ld8_a2(blk + 128 + 32 * hh + 8 * g);
-    const uint2 sc = ld8_a2(blk + 192 + 8 * hh);
-    const float d = half_lo(ld_half_a2(blk + 208));
-    const int s = g >> 1;
-    // signed scale bytes s, s+2 (first dword) and s+4, s+6 (second dword)
-    const float sc0 = (float)(int8_t)(sc.x >> (8 * s)), sc1 = (float)(int8_t)(sc.x >> (8 * s + 16));
-    const float sc2 = (float)(int8_t)(sc.y >> (8 * s)), sc3 = (float)(int8_t)(sc.y >> (8 * s + 16));
-    const float scs[4] = {sc0, sc1, sc2, sc3};
+  __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
+    // every field offset below is a multiple of 8, so all share the block's alignment
+    const uintptr_t base = reinterpret_cast<uintptr_t>(blk);
+    const uint32_t *a = reinterpret_cast<const uint32_t *>(base & ~uintptr_t(3));
+    r.sh = (uint32_t)(base & 3) * 8;
+    const int o1 = (64 * L.hh + 8 * L.g) / 4, o2 = (64 * L.hh + 32 + 8 * L.g) / 4,
+              oh = (128 + 32 * L.hh + 8 * L.g) / 4, os = (192 + 8 * L.hh) / 4;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const float dk = d * scs[k];
-      w.dq[k] = dk * 16777216.f;  // the 6-bit values enter as q*2^-24
-      w.dz[k] = dk * 32.f;        // the -32 offset, applied to the sum of x
+    for (int i = 0; i < 3; i++) {
+      r.l1[i] = a[o1 + i];
+      r.l2[i] = a[o2 + i];
+      r.h[i] = a[oh + i];
+      r.sc[i] = a[os + i];
     }
+    r.dw = a[208 / 4];  // d: low half (aligned block) or high half (block at 2 mod 4)
+  }
+
+  __device__ static uint2 field(const uint32_t (&f)[3], uint32_t sh) {
+    return make_uint2(__builtin_amdgcn_alignbit(f[1], f[0], sh), __builtin_amdgcn_alignbit(f[2], f[1], sh));
+  }
+
+  __device__ static void unpack(const Raw &r, const Lane &L, const Lds &, W &w) {
+    const uint2 ql1 = field(r.l1, r.sh), ql2 = field(r.l2, r.sh), qh = field(r.h, r.sh), sc = field(r.sc, r.sh);
+    const float d = half_lo(r.sh ? (r.dw >> 16) : r.dw);
+    // signed scale bytes s, s+2 (first dword) and s+4, s+6 (second dword)
+    const int s = L.s;
+    const float scs[4] = {(float)(int8_t)(sc.x >> (8 * s)), (float)(int8_t)(sc.x >> (8 * s + 16)),
+                          (float)(int8_t)(sc.y >> (8 * s)), (float)(int8_t)(sc.y >> (8 * s + 16))};
+#pragma unroll
+    for (int k = 0; k < 4; k++) w.dq[k] = d * scs[k];
     const uint32_t L1[2] = {ql1.x, ql1.y}, L2[2] = {ql2.x, ql2.y}, QH[2] = {qh.x, qh.y};
 #pragma unroll
     for (int i = 0; i < 2; i++) {
@@ -170,9 +222,8 @@ struct Q6K {
         a = fma_lo(w.p[k][2 * i + 1], x.v[k][4 * i + 1], a);
         a = fma_hi(w.p[k][2 * i + 1], x.v[k][4 * i + 3], a);
       }
-      // (d*sc) * sum((q-32)*x) = dq*a - dz*sum(x)   (src/Quants.cs:173-180)
-      r = __builtin_fmaf(w.dq[k], a, r);
-      r = __builtin_fmaf(-w.dz[k], x.s[k], r);
+      // (d*sc) * sum((q-32)*x) = (d*sc) * (sum(q*x) - 32*sum(x))   (src/Quants.cs:173-180)
+      r = __builtin_fmaf(w.dq[k], __builtin_fmaf(-32.f, x.s[k], a), r);
     }
     return r;
   }
@@ -181,36 +232,45 @@ struct Q6K {
 // ---------------------------------------------------------------------------- Q8_0
 // Lane slice: one whole 32-value block (blocks start 2-byte aligned).
 struct Q80 {
-  static constexpr int BLOCK = 32, BYTES = 34, LPB = 1, NEED_LDS = 0;
+  static constexpr int BLOCK = 32, BYTES = 34, LPB = 1, NEED_LDS = 0, R1 = 4;
+  struct Lane {};
   struct Xs { float v[32]; float s; };
-  struct W { uint32_t p[16]; float dq, dz; };
+  // the 10 aligned dwords covering the block and the byte shift (0 or 16)
+  struct Raw { uint32_t win[10]; uint32_t sh; };
+  struct W { uint32_t p[16]; float d; };
 
-  __device__ static void load_x(const float *xb, int, Xs &x) {
+  __device__ static Lane lane(int) { return Lane{}; }
+
+  __device__ static void load_x(const float *xb, const Lane &, Xs &x) {
     ld_x16(xb, x.v);
     ld_x16(xb + 16, x.v + 16);
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; i++) s += x.v[i];
     x.s = s;
+#pragma unroll
+    for (int i = 0; i < 32; i++) x.v[i] *= kTwo24;
   }
 
-  __device__ static void decode(const uint8_t *blk, int, const Lds &, W &w) {
-    const float d = half_lo(ld_half_a2(blk));
-    const uint8_t *q = blk + 2;
-    const uint32_t *a = reinterpret_cast<const uint32_t *>(reinterpret_cast<uintptr_t>(q) & ~uintptr_t(3));
-    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(q) & 3) * 8;
-    uint32_t win[9];
+  __device__ static void load(const uint8_t *blk, const Lane &, Raw &r) {
+    const uint32_t *a = reinterpret_cast<const uint32_t *>(reinterpret_cast<uintptr_t>(blk) & ~uintptr_t(3));
+    r.sh = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3) * 8;
 #pragma unroll
-    for (int i = 0; i < 9; i++) win[i] = a[i];
+    for (int i = 0; i < 10; i++) r.win[i] = a[i];
+  }
+
+  __device__ static void unpack(const Raw &r, const Lane &, const Lds &, W &w) {
+    // d: bytes 0-1 of the block; q: bytes 2..33, i.e. the window shifted by sh + 16 bits
+    w.d = half_lo(__builtin_amdgcn_alignbit(r.win[1], r.win[0], r.sh));
 #pragma unroll
     for (int i = 0; i < 8; i++) {
+      const uint32_t lo = __builtin_amdgcn_alignbit(r.win[i + 1], r.win[i], r.sh);
+      const uint32_t hi = __builtin_amdgcn_alignbit(r.win[i + 2], r.win[i + 1], r.sh);
       // int8 q + 128 as an unsigned byte, then bytes 0,2 / 1,3 as subnormal halves
-      const uint32_t v = __builtin_amdgcn_alignbit(win[i + 1], win[i], sh) ^ 0x80808080u;
+      const uint32_t v = __builtin_amdgcn_alignbit(hi, lo, 16) ^ 0x80808080u;
       w.p[2 * i] = v & 0x00FF00FFu;
       w.p[2 * i + 1] = (v >> 8) & 0x00FF00FFu;
     }
-    w.dq = d * 16777216.f;
-    w.dz = d * 128.f;
   }
 
   __device__ static float dot(const W &w, const Xs &x) {
@@ -222,25 +282,38 @@ struct Q80 {
       a = fma_lo(w.p[2 * i + 1], x.v[4 * i + 1], a);
       a = fma_hi(w.p[2 * i + 1], x.v[4 * i + 3], a);
     }
-    // d * sum(q*x) = dq*sum((q+128)*x*2^-24) - 128*d*sum(x)   (src/Quants.cs:93-94)
-    return __builtin_fmaf(w.dq, a, -(w.dz * x.s));
+    // d * sum(q*x) = d * (sum((q+128)*x) - 128*sum(x))   (src/Quants.cs:93-94)
+    return w.d * __builtin_fmaf(-128.f, x.s, a);
   }
 };
 
 // -------------------------------------------------------------------------- IQ4_XS
 // Lane slice: sub-block ib = sub (32 values, 16 bytes of qs).
 struct IQ4XS {
-  static constexpr int BLOCK = 256, BYTES = 136, LPB = 8, NEED_LDS = 0;
+  static constexpr int BLOCK = 256, BYTES = 136, LPB = 8, NEED_LDS = 0, R1 = 8;
+  struct Lane { int ib; };
   struct Xs { float v[32]; float s; };
-  struct W { uint32_t p[16]; float dq, dz; };
+  struct Raw { uint2 hdr, q01, q23; };
+  struct W { uint32_t p[16]; float dl; };
 
-  __device__ static void load_x(const float *xb, int sub, Xs &x) {
-    ld_x16(xb + 32 * sub, x.v);
-    ld_x16(xb + 32 * sub + 16, x.v + 16);
+  __device__ static Lane lane(int sub) { return Lane{sub}; }
+
+  __device__ static void load_x(const float *xb, const Lane &L, Xs &x) {
+    ld_x16(xb + 32 * L.ib, x.v);
+    ld_x16(xb + 32 * L.ib + 16, x.v + 16);
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; i++) s += x.v[i];
     x.s = s;
+#pragma unroll
+    for (int i = 0; i < 32; i++) x.v[i] *= kTwo24;
+  }
+
+  // blocks are 8-byte aligned (136 = 8*17): 8-byte loads for the header and the 16 qs bytes
+  __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
+    r.hdr = *reinterpret_cast<const uint2 *>(blk);  // d | scales_h | scales_l[4]
+    r.q01 = *reinterpret_cast<const uint2 *>(blk + 8 + 16 * L.ib);
+    r.q23 = *reinterpret_cast<const uint2 *>(blk + 16 + 16 * L.ib);
   }
 
   // kvalues_iq4nl + 128 (all in 1..241) as bytes: table index n -> byte n.
@@ -264,19 +337,14 @@ struct IQ4XS {
     return (hi & m) | (lo & ~m);
   }
 
-  __device__ static void decode(const uint8_t *blk, int sub, const Lds &, W &w) {
-    // blocks are 8-byte aligned (136 = 8*17): two 8-byte loads for the 16 bytes of qs
-    const uint2 hdr = *reinterpret_cast<const uint2 *>(blk);  // d | scales_h | scales_l[4]
-    const uint2 q01 = *reinterpret_cast<const uint2 *>(blk + 8 + 16 * sub);
-    const uint2 q23 = *reinterpret_cast<const uint2 *>(blk + 16 + 16 * sub);
+  __device__ static void unpack(const Raw &r, const Lane &L, const Lds &, W &w) {
+    const uint2 hdr = r.hdr;
+    const int ib = L.ib;
     const float d = half_lo(hdr.x);
     const uint32_t scales_h = hdr.x >> 16;
-    const int ls = (int)((hdr.y >> (8 * (sub >> 1) + 4 * (sub & 1))) & 0xF) |
-                   (int)(((scales_h >> (2 * sub)) & 3) << 4);
-    const float dl = d * (float)(ls - 32);  // src/IQuants.cs:71-72
-    w.dq = dl * 16777216.f;
-    w.dz = dl * 128.f;
-    const uint32_t qq[4] = {q01.x, q01.y, q23.x, q23.y};
+    const int ls = (int)((hdr.y >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xF) | (int)(((scales_h >> (2 * ib)) & 3) << 4);
+    w.dl = d * (float)(ls - 32);  // src/IQuants.cs:71-72
+    const uint32_t qq[4] = {r.q01.x, r.q01.y, r.q23.x, r.q23.y};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       // qs byte 4i+k: low nibble -> value 4i+k, high nibble -> value 16+4i+k
@@ -301,7 +369,8 @@ struct IQ4XS {
         a = fma_lo(w.p[8 * h + 2 * i + 1], xv[1], a);
         a = fma_hi(w.p[8 * h + 2 * i + 1], xv[3], a);
       }
-    return __builtin_fmaf(w.dq, a, -(w.dz * x.s));
+    // dl * sum(kv*x) = dl * (sum((kv+128)*x) - 128*sum(x))
+    return w.dl * __builtin_fmaf(-128.f, x.s, a);
   }
 };
 
@@ -309,21 +378,38 @@ struct IQ4XS {
 // Lane slice: sub-block ib32 = sub: four groups of 8 values, each a grid entry (8 bytes of
 // 8/25/43) with eight signs from a 7-bit index plus a parity bit.
 struct IQ2XXS {
-  static constexpr int BLOCK = 256, BYTES = 66, LPB = 8, NEED_LDS = 1;
+  static constexpr int BLOCK = 256, BYTES = 66, LPB = 8, NEED_LDS = 1, R1 = 8;
+  struct Lane { int ib; };
   struct Xs { float v[32]; };
+  struct Raw { uint32_t dw, a[3]; uint32_t dsh, sh; };
   struct W { uint32_t p[16]; float db; };
 
-  __device__ static void load_x(const float *xb, int sub, Xs &x) {
-    ld_x16(xb + 32 * sub, x.v);
-    ld_x16(xb + 32 * sub + 16, x.v + 16);
+  __device__ static Lane lane(int sub) { return Lane{sub}; }
+
+  __device__ static void load_x(const float *xb, const Lane &L, Xs &x) {
+    ld_x16(xb + 32 * L.ib, x.v);
+    ld_x16(xb + 32 * L.ib + 16, x.v + 16);
+#pragma unroll
+    for (int i = 0; i < 32; i++) x.v[i] *= kTwo24;
   }
 
-  __device__ static void decode(const uint8_t *blk, int sub, const Lds &lds, W &w) {
-    const float d = half_lo(ld_half_a2(blk));
-    const uint2 aux = ld8_a2(blk + 2 + 8 * sub);
-    // db = d * (0.5 + scale4) * 0.25; grid bytes enter as n*2^-24   (src/IQuants.cs:159)
-    const float db = d * (0.5f + (float)(aux.y >> 28)) * 0.25f;
-    w.db = db * 16777216.f;
+  __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
+    const uintptr_t pd = reinterpret_cast<uintptr_t>(blk), pa = pd + 2 + 8 * L.ib;
+    r.dw = *reinterpret_cast<const uint32_t *>(pd & ~uintptr_t(3));
+    r.dsh = (uint32_t)(pd & 2);
+    const uint32_t *a = reinterpret_cast<const uint32_t *>(pa & ~uintptr_t(3));
+    r.sh = (uint32_t)(pa & 3) * 8;
+    r.a[0] = a[0];
+    r.a[1] = a[1];
+    r.a[2] = a[2];
+  }
+
+  __device__ static void unpack(const Raw &r, const Lane &, const Lds &lds, W &w) {
+    const float d = half_lo(r.dsh ? (r.dw >> 16) : r.dw);
+    const uint2 aux = make_uint2(__builtin_amdgcn_alignbit(r.a[1], r.a[0], r.sh),
+                                 __builtin_amdgcn_alignbit(r.a[2], r.a[1], r.sh));
+    // db = d * (0.5 + scale4) * 0.25   (src/IQuants.cs:159)
+    w.db = d * (0.5f + (float)(aux.y >> 28)) * 0.25f;
 #pragma unroll
     for (int l = 0; l < 4; l++) {
       const uint32_t gi = (aux.x >> (8 * l)) & 0xFF;

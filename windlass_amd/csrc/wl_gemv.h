@@ -16,6 +16,7 @@ struct GemvSeg {
   int rows;
   int ldy;
   int wg_begin;  // first workgroup of this segment (set by the launcher)
+  int nwg;       // workgroups of this segment (set by the launcher)
   int type;
 };
 
@@ -30,8 +31,11 @@ struct GemvParams {
 
 bool gemv_supports(int type);
 bool gemv_mixed_supports(int type);
-// nm = 1: y = W x. nm = 2: y = silu(W x) * (W2 x) (the SwiGLU gate/up pair).
-hipError_t gemv_launch(int type, int nm, GemvParams &p, hipStream_t st);
-hipError_t gemv_launch_mixed(GemvParams &p, hipStream_t st);
+// nm = 1: y = W x. nm = 2: y = silu(W x) * (W2 x) (the SwiGLU gate/up pair). num_cu sizes
+// the grid (a few waves per SIMD across the device).
+hipError_t gemv_launch(int type, int nm, GemvParams &p, int num_cu, hipStream_t st);
+hipError_t gemv_launch_mixed(GemvParams &p, int num_cu, hipStream_t st);
+// Waves per workgroup for a row of `cols` values.
+int gemv_waves(int cols);
 
 }  // namespace wl

@@ -1,8 +1,35 @@
-// wl_gemv_impl.h - the wave-level decode GEMV body shared by the dense and the MoE launches.
+// wl_gemv_impl.h - the column-stationary decode GEMV body shared by every GEMV launch.
+//
+// Work decomposition. A row of nb blocks is covered by P passes of NWV waves (P = ceil(nb /
+// (8*BPW)), NWV = ceil(nb / (P*BPW)) <= 8, BPW = blocks per wave); in pass p, wave w, lane l
+// owns block column b = (p*NWV + w)*BPW + l/LPB, slice l%LPB, of EVERY row. For one token and
+// at most two passes (cols <= 32768) the lane's x slices are read once for the whole launch
+// and stay in registers. The workgroup walks row groups of R rows with a stride of gridDim; for
+// each group every lane reads its slice of the R rows (one coalesced read per row and wave),
+// forms its partial dot per (row, token), the wave folds its 64 partials with one fixed
+// exchange butterfly, and wave 0 adds the waves' results in wave order.
+//
+// Summation order of y[t][r] (fixed, independent of T, R and the launch's other rows):
+//   lane partial  = sum over passes of the codec's dot on that lane's slice
+//   wave partial  = pairwise tree over lanes (i, i^32), then (i, i^16), ..., (i, i^1)
+//   y             = ((wave 0 + wave 1) + wave 2) + ...
+// so a token's result is bit-identical whatever the token count or row grouping.
 #pragma once
 #include "wl_codecs.h"
 
 namespace wl {
+
+constexpr int kColsPerWave = 2048;  // every codec: 64/LPB blocks of BLOCK values per wave
+constexpr int kMaxWaves = 8;        // waves per workgroup (the kernels' launch bound is 512)
+
+// Passes and waves for a row of `cols` values (the same for every token count).
+__host__ __device__ inline void cs_shape(int cols, int *passes, int *waves) {
+  const int units = (cols + kColsPerWave - 1) / kColsPerWave;  // wave-columns needed
+  const int p = (units + kMaxWaves - 1) / kMaxWaves;
+  *passes = p < 1 ? 1 : p;
+  *waves = (units + *passes - 1) / *passes;
+  if (*waves < 1) *waves = 1;
+}
 
 // SiLU(g) * u as src/Transformer.cs:247 writes it: g / (1 + exp(-g)) * u, the exponential in
 // double (Math.Exp) cast to float. Compiled without contraction by every includer.
@@ -10,67 +37,174 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + (float)exp((double)(-g))) * u;
 }
 
-// Rows row0..row0+R-1 of w (and of w2 when NM == 2) times T <= TM activation rows.
-//   x row of token t:  x + (xrow ? xrow[t] : t) * ldx
-//   y of (token t, row r): y[(yrow ? yrow[t] : t) * ldy + r]
-// NM == 2 stores silu(w x) * (w2 x) instead (the SwiGLU gate/up pair).
+// Folds V = 2^k values per lane over the 64 lanes. Lane l returns the full sum of value
+// index (l >> (6-k)): the first k levels exchange halves of the value set between lane pairs
+// (l, l^32), (l, l^16), ...; the rest are a plain butterfly. Every value meets the same
+// pairwise tree as a plain 64-lane butterfly, whatever V is.
+template <int V, int BIT>
+__device__ __forceinline__ float exch_reduce(const float *v, int lane) {
+  if constexpr (V == 1) {
+    float q = v[0];
+    if constexpr (BIT >= 0) {
+#pragma unroll
+      for (int m = 1 << BIT; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+    }
+    return q;
+  } else {
+    const bool hi = (lane >> BIT) & 1;
+    float u[V / 2];
+#pragma unroll
+    for (int k = 0; k < V / 2; k++) {
+      const float send = hi ? v[k] : v[k + V / 2];
+      const float keep = hi ? v[k + V / 2] : v[k];
+      u[k] = keep + __shfl_xor(send, 1 << BIT, 64);
+    }
+    return exch_reduce<V / 2, BIT - 1>(u, lane);
+  }
+}
+
+constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
+
+// One matrix set of a launch: rows of w (and of w2 for the SwiGLU pair, NM == 2).
+struct CsRows {
+  const uint8_t *w, *w2;
+  int64_t row_bytes;
+  int rows;
+};
+
+// Activations: token t reads x + (xrow ? xrow[t] : t) * ldx; results go to
+// y[(yrow ? yrow[t] : t) * ldy + r].
+struct CsIO {
+  const float *x;
+  const int *xrow;
+  int64_t ldx;
+  float *y;
+  const int *yrow;
+  int64_t ldy;
+  int T;
+};
+
+// Dynamic LDS of a launch: the codec tables, then the double-buffered wave partials.
 template <class C, int TM, int R, int NM>
-__device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, const uint8_t *__restrict__ w2,
-                                          int64_t row_bytes, int rows, int row0,
-                                          const float *__restrict__ x, const int *xrow, int64_t ldx,
-                                          int cols, int T, float *__restrict__ y, const int *yrow,
-                                          int64_t ldy, const Lds &lds) {
-  const int lane = threadIdx.x & 63;
-  const int sub = lane % C::LPB;
-  const int bslot = lane / C::LPB;
+inline size_t cs_lds_bytes(int nwv) {
+  return (C::NEED_LDS ? sizeof(Lds) : 0) + sizeof(float) * 2 * nwv * NM * R * TM;
+}
+
+// SP: passes whose x slices stay in registers (0: x read per row group; 1 or 2 only for TM 1).
+template <class C, int TM, int R, int NM, int SP>
+__device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int cols, int g0, int gstride,
+                                        uint8_t *lds_raw) {
+  constexpr int V = NM * R * TM;
+  constexpr int LOW = 6 - ilog2(V);
+  static_assert((1 << ilog2(V)) == V && V <= 64, "partials per lane must be a power of two <= 64");
+  static_assert(SP == 0 || TM == 1, "stationary x slices are for one token");
   constexpr int BPW = 64 / C::LPB;
+  const Lds &lds = *reinterpret_cast<const Lds *>(lds_raw);
+  float *part = reinterpret_cast<float *>(lds_raw + (C::NEED_LDS ? sizeof(Lds) : 0));
+  if constexpr (C::NEED_LDS) {
+    C::init_lds(*reinterpret_cast<Lds *>(lds_raw));
+    __syncthreads();
+  }
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  const int sub = lane % C::LPB, bslot = lane / C::LPB;
+  const typename C::Lane L = C::lane(sub);
   const int nb = cols / C::BLOCK;
-  const uint8_t *wm[2] = {w, w2};
+  const int npass = (nb + nwv * BPW - 1) / (nwv * BPW);
+  const int ngroups = (W.rows + R - 1) / R;
+  const uint8_t *wm[2] = {W.w, W.w2};
 
   const float *xr[TM];
 #pragma unroll
-  for (int t = 0; t < TM; t++) xr[t] = x + (int64_t)(xrow ? xrow[t < T ? t : 0] : t) * ldx;
+  for (int t = 0; t < TM; t++) xr[t] = io.x + (int64_t)(io.xrow ? io.xrow[t < io.T ? t : 0] : t) * io.ldx;
 
-  // Rows past the end re-read the last row (valid memory); their results are dropped.
-  int64_t roff[R];
+  // x slices of the stationary passes, read once
+  typename C::Xs xs0[SP > 0 ? SP : 1];
 #pragma unroll
-  for (int r = 0; r < R; r++) roff[r] = (int64_t)min(row0 + r, rows - 1) * row_bytes;
+  for (int p = 0; p < SP; p++) {
+    const int b = (p * nwv + wv) * BPW + bslot;
+    if (b < nb) C::load_x(xr[0] + (int64_t)b * C::BLOCK, L, xs0[p]);
+  }
 
-  float acc[NM][R][TM];
-#pragma unroll
-  for (int m = 0; m < NM; m++)
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-      for (int t = 0; t < TM; t++) acc[m][r][t] = 0.f;
-
-  for (int b = bslot; b < nb; b += BPW) {
-    typename C::W wr[NM][R];
+  int buf = 0;
+  for (int g = g0; g < ngroups; g += gstride, buf ^= 1) {
+    float acc[NM][R][TM];
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
-      for (int r = 0; r < R; r++) C::decode(wm[m] + roff[r] + (int64_t)b * C::BYTES, sub, lds, wr[m][r]);
+      for (int r = 0; r < R; r++)
 #pragma unroll
-    for (int t = 0; t < TM; t++) {
-      if (t < T) {
-        typename C::Xs xs;
-        C::load_x(xr[t] + (int64_t)b * C::BLOCK, sub, xs);
+        for (int t = 0; t < TM; t++) acc[m][r][t] = 0.f;
+
+    for (int p = 0; p < npass; p++) {
+      const int b = (p * nwv + wv) * BPW + bslot;
+      if (b < nb) {
+        typename C::Raw raw[NM][R];
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
-          for (int r = 0; r < R; r++) acc[m][r][t] += C::dot(wr[m][r], xs);
+          for (int r = 0; r < R; r++) {
+            // rows past the end re-read the last row (valid memory); their results are dropped
+            const int row = min(g * R + r, W.rows - 1);
+            C::load(wm[m] + (int64_t)row * W.row_bytes + (int64_t)b * C::BYTES, L, raw[m][r]);
+          }
+        if constexpr (TM == 1) {
+          typename C::Xs xs;
+          if constexpr (SP == 1) xs = xs0[0];
+          else if constexpr (SP == 2) xs = p == 0 ? xs0[0] : xs0[1];
+          else C::load_x(xr[0] + (int64_t)b * C::BLOCK, L, xs);
+#pragma unroll
+          for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+              typename C::W w;
+              C::unpack(raw[m][r], L, lds, w);
+              acc[m][r][0] += C::dot(w, xs);
+            }
+        } else {
+          typename C::W w[NM][R];
+#pragma unroll
+          for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int r = 0; r < R; r++) C::unpack(raw[m][r], L, lds, w[m][r]);
+#pragma unroll
+          for (int t = 0; t < TM; t++) {
+            if (t < io.T) {
+              typename C::Xs xs;
+              C::load_x(xr[t] + (int64_t)b * C::BLOCK, L, xs);
+#pragma unroll
+              for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[m][r][t] += C::dot(w[m][r], xs);
+            }
+          }
+        }
       }
     }
-  }
 
+    // value index v = (m*TM + t)*R + r
+    float vals[V];
 #pragma unroll
-  for (int r = 0; r < R; r++) {
+    for (int m = 0; m < NM; m++)
 #pragma unroll
-    for (int t = 0; t < TM; t++) {
-      if (t < T) {
-        float v = wave_sum(acc[0][r][t]);
-        if (NM == 2) v = silu_mul(v, wave_sum(acc[NM - 1][r][t]));
-        if (lane == 0 && row0 + r < rows) y[(int64_t)(yrow ? yrow[t] : t) * ldy + row0 + r] = v;
+      for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int r = 0; r < R; r++) vals[(m * TM + t) * R + r] = acc[m][r][t];
+    const float q = exch_reduce<V, 5>(vals, lane);
+    if ((lane & ((1 << LOW) - 1)) == 0) part[(buf * nwv + wv) * V + (lane >> LOW)] = q;
+    __syncthreads();
+    if (wv == 0 && lane < R * TM) {
+      const int r = lane % R, t = lane / R;
+      const int row = g * R + r;
+      if (t < io.T && row < W.rows) {
+        const float *pb = part + buf * nwv * V;
+        float s = pb[t * R + r];
+        for (int w = 1; w < nwv; w++) s += pb[w * V + t * R + r];
+        if constexpr (NM == 2) {
+          float s1 = pb[(TM + t) * R + r];
+          for (int w = 1; w < nwv; w++) s1 += pb[w * V + (TM + t) * R + r];
+          s = silu_mul(s, s1);
+        }
+        io.y[(int64_t)(io.yrow ? io.yrow[t] : t) * io.ldy + row] = s;
       }
     }
   }

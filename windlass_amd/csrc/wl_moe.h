@@ -54,6 +54,6 @@ struct MoeLaunch {
 bool moe_supports(int type);
 hipError_t route_launch(const float *logits, int T, int n, int k, int renorm, int *sel, float *wts, float *prob,
                         hipStream_t st);
-hipError_t moe_launch(const MoeLaunch &m, hipStream_t st);
+hipError_t moe_launch(const MoeLaunch &m, int num_cu, hipStream_t st);
 
 }  // namespace wl

@@ -12,6 +12,7 @@
 //   5. combine_kernel  out[t] = sum over t's experts, ascending, of w * y (:289-293).
 // Only the chosen experts are read (tests/MoeTests.cs:164-181).
 #include "wl_moe.h"
+#include "wl_gemv.h"
 #include "wl_gemv_impl.h"
 
 #pragma clang fp contract(off)
@@ -94,25 +95,18 @@ __global__ void plan_kernel(const int *__restrict__ sel, const float *__restrict
 
 extern "C" __shared__ uint8_t wl_moe_dyn_lds[];
 
-// blockIdx.y = slot; rows of the slot's expert in blockIdx.x row groups.
-template <class C, int TM, int R, int NM>
-__global__ __launch_bounds__(256) void moe_gemv_kernel(MoeGemvArgs a) {
-  Lds &lds = *reinterpret_cast<Lds *>(wl_moe_dyn_lds);
-  if constexpr (C::NEED_LDS) {
-    C::init_lds(lds);
-    __syncthreads();
-  }
+// blockIdx.y = slot (one chosen expert); the slot's workgroups stride over the expert's rows.
+template <class C, int TM, int R, int NM, int SP>
+__global__ __launch_bounds__(512) void moe_gemv_kernel(MoeGemvArgs a) {
   const MoePlan *plan = a.plan;
   const int s = blockIdx.y;
-  if (s >= plan->nslots) return;
+  if (s >= plan->nslots) return;  // uniform over the workgroup
   const int e = plan->slot_expert[s];
-  const int n = plan->slot_ntok[s];
-  const int row0 = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * R;
-  if (row0 >= a.rows) return;
   const int64_t eoff = (int64_t)e * a.rows * a.row_bytes;
-  const int *xrow = a.x_by_pair ? plan->slot_pair[s] : plan->slot_tok[s];
-  gemv_rows<C, TM, R, NM>(a.w + eoff, NM == 2 ? a.w2 + eoff : nullptr, a.row_bytes, a.rows, row0, a.x, xrow,
-                          a.ldx, a.cols, n, a.y, plan->slot_pair[s], a.ldy, lds);
+  const CsRows W{a.w + eoff, NM == 2 ? a.w2 + eoff : nullptr, a.row_bytes, a.rows};
+  const CsIO io{a.x, a.x_by_pair ? plan->slot_pair[s] : plan->slot_tok[s], a.ldx, a.y, plan->slot_pair[s],
+                a.ldy, plan->slot_ntok[s]};
+  cs_gemv<C, TM, R, NM, SP>(W, io, a.cols, (int)blockIdx.x, (int)gridDim.x, wl_moe_dyn_lds);
 }
 
 __global__ void combine_kernel(const MoePlan *__restrict__ plan, const float *__restrict__ yd, int T, int k,
@@ -126,30 +120,39 @@ __global__ void combine_kernel(const MoePlan *__restrict__ plan, const float *__
 }
 
 template <class C, int TM, int NM>
-static hipError_t launch_moe_gemv(const MoeGemvArgs &a, int max_slots, hipStream_t st) {
-  constexpr int R = NM == 2 ? 2 : 4;
-  const int nwg = (a.rows + 4 * R - 1) / (4 * R);
-  const size_t smem = C::NEED_LDS ? sizeof(Lds) : 0;
-  hipLaunchKernelGGL((moe_gemv_kernel<C, TM, R, NM>), dim3(nwg, max_slots), dim3(256), smem, st, a);
+static hipError_t launch_moe_gemv(const MoeGemvArgs &a, int max_slots, int num_cu, hipStream_t st) {
+  constexpr int R = TM == 1 ? (NM == 1 ? C::R1 : C::R1 / 2) : (NM == 1 ? 4 : 2);
+  int passes, nwv;
+  cs_shape(a.cols, &passes, &nwv);
+  const int groups = (a.rows + R - 1) / R;
+  // about 16 waves per CU over all slots
+  int gx = (num_cu * 16 / nwv + max_slots - 1) / max_slots;
+  if (gx < 1) gx = 1;
+  if (gx > groups) gx = groups;
+  const size_t smem = cs_lds_bytes<C, TM, R, NM>(nwv);
+  if (TM == 1 && passes == 1)
+    hipLaunchKernelGGL((moe_gemv_kernel<C, TM, R, NM, TM == 1 ? 1 : 0>), dim3(gx, max_slots), dim3(64 * nwv), smem, st, a);
+  else
+    hipLaunchKernelGGL((moe_gemv_kernel<C, TM, R, NM, 0>), dim3(gx, max_slots), dim3(64 * nwv), smem, st, a);
   return hipGetLastError();
 }
 
 template <class C, int NM>
-static hipError_t launch_moe_tm(const MoeGemvArgs &a, int T, int max_slots, hipStream_t st) {
-  if (T <= 1) return launch_moe_gemv<C, 1, NM>(a, max_slots, st);
-  if (T <= 2) return launch_moe_gemv<C, 2, NM>(a, max_slots, st);
-  if (T <= 4) return launch_moe_gemv<C, 4, NM>(a, max_slots, st);
-  return launch_moe_gemv<C, 8, NM>(a, max_slots, st);
+static hipError_t launch_moe_tm(const MoeGemvArgs &a, int T, int max_slots, int num_cu, hipStream_t st) {
+  if (T <= 1) return launch_moe_gemv<C, 1, NM>(a, max_slots, num_cu, st);
+  if (T <= 2) return launch_moe_gemv<C, 2, NM>(a, max_slots, num_cu, st);
+  if (T <= 4) return launch_moe_gemv<C, 4, NM>(a, max_slots, num_cu, st);
+  return launch_moe_gemv<C, 8, NM>(a, max_slots, num_cu, st);
 }
 
 template <int NM>
-static hipError_t launch_moe_type(int type, const MoeGemvArgs &a, int T, int max_slots, hipStream_t st) {
+static hipError_t launch_moe_type(int type, const MoeGemvArgs &a, int T, int max_slots, int num_cu, hipStream_t st) {
   switch (type) {
-    case 12: return launch_moe_tm<Q4K, NM>(a, T, max_slots, st);
-    case 14: return launch_moe_tm<Q6K, NM>(a, T, max_slots, st);
-    case 8: return launch_moe_tm<Q80, NM>(a, T, max_slots, st);
-    case 23: return launch_moe_tm<IQ4XS, NM>(a, T, max_slots, st);
-    case 16: return launch_moe_tm<IQ2XXS, NM>(a, T, max_slots, st);
+    case 12: return launch_moe_tm<Q4K, NM>(a, T, max_slots, num_cu, st);
+    case 14: return launch_moe_tm<Q6K, NM>(a, T, max_slots, num_cu, st);
+    case 8: return launch_moe_tm<Q80, NM>(a, T, max_slots, num_cu, st);
+    case 23: return launch_moe_tm<IQ4XS, NM>(a, T, max_slots, num_cu, st);
+    case 16: return launch_moe_tm<IQ2XXS, NM>(a, T, max_slots, num_cu, st);
   }
   return hipErrorInvalidValue;
 }
@@ -160,7 +163,7 @@ hipError_t route_launch(const float *logits, int T, int n, int k, int renorm, in
   return hipGetLastError();
 }
 
-hipError_t moe_launch(const MoeLaunch &m, hipStream_t st) {
+hipError_t moe_launch(const MoeLaunch &m, int num_cu, hipStream_t st) {
   hipError_t err = route_launch(m.logits, m.T, m.ne, m.k, m.renorm, m.sel, m.wts, m.prob, st);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(64), 0, st, m.sel, m.wts, m.T, m.k, m.ne, m.plan);
@@ -170,12 +173,12 @@ hipError_t moe_launch(const MoeLaunch &m, hipStream_t st) {
   gu.plan = m.plan;
   gu.w = m.gate; gu.w2 = m.up; gu.row_bytes = m.gu_row_bytes; gu.rows = m.ff; gu.cols = m.embd;
   gu.x = m.x; gu.ldx = m.embd; gu.x_by_pair = 0; gu.y = m.h; gu.ldy = m.ff;
-  if ((err = launch_moe_type<2>(m.gu_type, gu, m.T, max_slots, st)) != hipSuccess) return err;
+  if ((err = launch_moe_type<2>(m.gu_type, gu, m.T, max_slots, num_cu, st)) != hipSuccess) return err;
   MoeGemvArgs dn{};
   dn.plan = m.plan;
   dn.w = m.down; dn.w2 = nullptr; dn.row_bytes = m.d_row_bytes; dn.rows = m.embd; dn.cols = m.ff;
   dn.x = m.h; dn.ldx = m.ff; dn.x_by_pair = 1; dn.y = m.yd; dn.ldy = m.embd;
-  if ((err = launch_moe_type<1>(m.d_type, dn, m.T, max_slots, st)) != hipSuccess) return err;
+  if ((err = launch_moe_type<1>(m.d_type, dn, m.T, max_slots, num_cu, st)) != hipSuccess) return err;
   const int64_t total = (int64_t)m.T * m.embd;
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, m.plan, m.yd, m.T,
                      m.k, m.embd, m.out);
