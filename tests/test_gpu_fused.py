@@ -33,8 +33,8 @@ def _p(t):
 
 @pytest.mark.parametrize("types", [(12, 12, 14), (12, 12, 12), (14, 8, 12)])
 @pytest.mark.parametrize("T", [1, 8])
-def test_multi_matmul_equals_separate(ctx, types, T):
-    cols = 2048
+@pytest.mark.parametrize("cols", [2048, 16384])
+def test_multi_matmul_equals_separate(ctx, types, T, cols):
     shapes = [512, 128, 128]
     ws, datas = [], []
     for i, (t, r) in enumerate(zip(types, shapes)):
@@ -59,8 +59,9 @@ def test_multi_matmul_equals_separate(ctx, types, T):
 
 @pytest.mark.parametrize("t", [GgmlType.Q4_K, GgmlType.Q6_K, GgmlType.IQ4_XS], ids=lambda t: t.name)
 @pytest.mark.parametrize("T", [1, 4])
-def test_gate_up_epilogue(ctx, t, T):
-    ff, embd = 768, 2048
+@pytest.mark.parametrize("embd", [2048, 12288])
+def test_gate_up_epilogue(ctx, t, T, embd):
+    ff = 768
     g = blocks(t, ff, embd, seed=1)
     u = blocks(t, ff, embd, seed=2)
     wg, wu = ctx.upload(t, g, ff, embd), ctx.upload(t, u, ff, embd)

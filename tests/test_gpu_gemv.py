@@ -15,7 +15,10 @@ from windlass_amd.backend import Context, GgmlType
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(5, 512), (37, 1024), (300, 2048), (1000, 4096)]
+# 10240: one pass of five waves; 12288, 16384, 18432, 28672: rows cut along K into 2, 2, 3
+# and 7 chunks added in chunk order; 34816: three passes of a prime width
+SHAPES = [(5, 512), (37, 1024), (300, 2048), (1000, 4096), (24, 10240), (64, 12288), (48, 16384),
+          (16, 18432), (40, 28672), (9, 34816)]
 
 
 @pytest.fixture(scope="module")
@@ -43,8 +46,9 @@ def test_gemv_within_tolerance(ctx, t, shape, T):
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
-def test_batch_rows_equal_single_token_bitwise(ctx, t):
-    rows, cols = 300, 2048
+@pytest.mark.parametrize("cols", [2048, 28672])
+def test_batch_rows_equal_single_token_bitwise(ctx, t, cols):
+    rows = 300 if cols == 2048 else 40
     data = blocks(t, rows, cols, seed=77)
     w = ctx.upload(t, data, rows, cols)
     x = np.random.default_rng(3).standard_normal((8, cols), dtype=np.float32)

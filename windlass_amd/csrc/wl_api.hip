@@ -35,11 +35,12 @@ struct wl_ctx {
   int num_cu;
   hipStream_t stream;
   // growable scratch (device)
-  void *buf[6];
-  size_t cap[6];
+  void *buf[7];
+  size_t cap[7];
 };
 
-enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX };
+// S_PART holds the K-chunk partials of split GEMV rows.
+enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART };
 
 static thread_local std::string g_err;
 
@@ -223,6 +224,17 @@ static void operand(const wl_weight *w, int32_t expert, const uint8_t **base, in
   }
 }
 
+// One GEMV launch (plus its combine when rows are split along K) on the context's stream.
+static int gemv(wl_ctx *c, const wl::GemvMat *mats, int nmat, int nm, const float *d_x, int cols, int T) {
+  const int64_t nf = wl::gemv_scratch_floats(mats, nmat, nm, cols, T);
+  int rc;
+  if (nf > 0 && (rc = ensure(c, S_PART, (size_t)nf * sizeof(float)))) return rc;
+  WL_HIP(wl::gemv_run(mats, nmat, nm, d_x, cols, cols, T, nf > 0 ? (float *)c->buf[S_PART] : nullptr, c->num_cu,
+                      c->stream),
+         "gemv launch");
+  return WL_OK;
+}
+
 static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float *d_x, int32_t T, float *d_y) {
   if (!c || !w || !d_x || !d_y) return fail(WL_E_ARG, "matmul: null argument");
   int rc = check_expert(w, expert);
@@ -239,19 +251,9 @@ static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float
   }
   // decode GEMV in passes of up to 8 tokens (a token's result does not depend on its pass)
   for (int t0 = 0; t0 < T; t0 += 8) {
-    wl::GemvParams p{};
-    p.nseg = 1;
-    p.seg[0].w = base;
-    p.seg[0].row_bytes = w->row_bytes;
-    p.seg[0].rows = (int)rows;
-    p.seg[0].y = d_y + (int64_t)t0 * rows;
-    p.seg[0].ldy = (int)rows;
-    p.seg[0].type = w->type;
-    p.x = d_x + (int64_t)t0 * w->cols;
-    p.ldx = (int)w->cols;
-    p.cols = (int)w->cols;
-    p.T = T - t0 < 8 ? T - t0 : 8;
-    WL_HIP(wl::gemv_launch(w->type, 1, p, c->num_cu, c->stream), "gemv launch");
+    const wl::GemvMat m{base, nullptr, w->row_bytes, (int)rows, w->type, d_y + (int64_t)t0 * rows, (int)rows};
+    const int Tp = T - t0 < 8 ? T - t0 : 8;
+    if ((rc = gemv(c, &m, 1, 1, d_x + (int64_t)t0 * w->cols, (int)w->cols, Tp))) return rc;
   }
   return WL_OK;
 }
@@ -281,8 +283,8 @@ extern "C" int wl_matmul(wl_ctx *c, const wl_weight *w, int32_t expert, const fl
 extern "C" int wl_matmul_multi_dev(wl_ctx *c, int32_t n, const wl_weight *const *ws, const float *d_x, int32_t T,
                                    float *const *d_ys) {
   if (!c || !ws || !d_x || !d_ys) return fail(WL_E_ARG, "wl_matmul_multi_dev: null argument");
-  if (n <= 0 || n > wl::GEMV_MAX_SEGS) return fail(WL_E_ARG, "wl_matmul_multi_dev: n = %d outside 1..%d", n,
-                                                   wl::GEMV_MAX_SEGS);
+  if (n <= 0 || n > wl::GEMV_MAX_MATS) return fail(WL_E_ARG, "wl_matmul_multi_dev: n = %d outside 1..%d", n,
+                                                   wl::GEMV_MAX_MATS);
   if (T <= 0 || T > 8) return fail(WL_E_SHAPE, "wl_matmul_multi_dev: T = %d outside 1..8", T);
   bool same = true, mixed_ok = true;
   for (int i = 0; i < n; i++) {
@@ -299,24 +301,13 @@ extern "C" int wl_matmul_multi_dev(wl_ctx *c, int32_t n, const wl_weight *const 
     }
     return WL_OK;
   }
-  wl::GemvParams p{};
-  p.nseg = n;
+  wl::GemvMat mats[wl::GEMV_MAX_MATS];
   for (int i = 0; i < n; i++) {
     const wl_weight *w = ws[i];
-    p.seg[i].w = w->dev;
-    p.seg[i].row_bytes = w->row_bytes;
-    p.seg[i].rows = (int)(w->rows * w->experts);
-    p.seg[i].y = d_ys[i];
-    p.seg[i].ldy = p.seg[i].rows;
-    p.seg[i].type = w->type;
+    const int rows = (int)(w->rows * w->experts);
+    mats[i] = wl::GemvMat{w->dev, nullptr, w->row_bytes, rows, w->type, d_ys[i], rows};
   }
-  p.x = d_x;
-  p.ldx = (int)ws[0]->cols;
-  p.cols = (int)ws[0]->cols;
-  p.T = T;
-  if (same) WL_HIP(wl::gemv_launch(ws[0]->type, 1, p, c->num_cu, c->stream), "gemv launch");
-  else WL_HIP(wl::gemv_launch_mixed(p, c->num_cu, c->stream), "gemv launch");
-  return WL_OK;
+  return gemv(c, mats, n, 1, d_x, (int)ws[0]->cols, T);
 }
 
 extern "C" int wl_gate_up_dev(wl_ctx *c, const wl_weight *gate, const wl_weight *up, int32_t expert,
@@ -335,20 +326,9 @@ extern "C" int wl_gate_up_dev(wl_ctx *c, const wl_weight *gate, const wl_weight 
   operand(gate, expert, &gb, &rows);
   operand(up, expert, &ub, &rows);
   for (int t0 = 0; t0 < T; t0 += 8) {
-    wl::GemvParams p{};
-    p.nseg = 1;
-    p.seg[0].w = gb;
-    p.seg[0].w2 = ub;
-    p.seg[0].row_bytes = gate->row_bytes;
-    p.seg[0].rows = (int)rows;
-    p.seg[0].y = d_h + (int64_t)t0 * rows;
-    p.seg[0].ldy = (int)rows;
-    p.seg[0].type = gate->type;
-    p.x = d_x + (int64_t)t0 * gate->cols;
-    p.ldx = (int)gate->cols;
-    p.cols = (int)gate->cols;
-    p.T = T - t0 < 8 ? T - t0 : 8;
-    WL_HIP(wl::gemv_launch(gate->type, 2, p, c->num_cu, c->stream), "gemv launch");
+    const wl::GemvMat m{gb, ub, gate->row_bytes, (int)rows, gate->type, d_h + (int64_t)t0 * rows, (int)rows};
+    const int Tp = T - t0 < 8 ? T - t0 : 8;
+    if ((rc = gemv(c, &m, 1, 2, d_x + (int64_t)t0 * gate->cols, (int)gate->cols, Tp))) return rc;
   }
   return WL_OK;
 }

@@ -10,6 +10,7 @@
 //   W      - that slice unpacked into registers (unpack; reused for every token),
 //   dot    - the lane's partial sum of W * x for one token, in the reference's units.
 //   R1     - rows per group at one token (bounded by the registers a row's Raw takes).
+//   SP2    - whether rows of two passes keep both x slices in registers (1) or re-read them.
 // The partial of a lane is a fixed sequence of fp32 operations on that lane's slice, the same
 // for every token count, so a token's result never depends on how many tokens run with it.
 //
@@ -42,8 +43,11 @@ struct Lds {
 // ---------------------------------------------------------------------------- Q4_K
 // Lane slice: 16 bytes of qs, i.e. 16 low nibbles of sub-block 2j (x[64j+16h .. +16]) and
 // 16 high nibbles of sub-block 2j+1 (x[64j+32+16h .. +16]), with j = sub/2, h = sub%2.
+#ifndef WL_Q4K_R1
+#define WL_Q4K_R1 8
+#endif
 struct Q4K {
-  static constexpr int BLOCK = 256, BYTES = 144, LPB = 8, NEED_LDS = 0, R1 = 8;
+  static constexpr int BLOCK = 256, BYTES = 144, LPB = 8, NEED_LDS = 0, R1 = WL_Q4K_R1, SP2 = 1;
   struct Lane {
     int j, h, sh;
     bool jlo;
@@ -132,8 +136,14 @@ struct Q4K {
 // ---------------------------------------------------------------------------- Q6_K
 // Lane slice: half hh = sub/4 of the block (128 values) and l = 8g..8g+7 with g = sub%4:
 // the four values l, l+32, l+64, l+96 of each l (scales sc[l/16 + 0,2,4,6]).
+#ifndef WL_Q6K_R1
+#define WL_Q6K_R1 4
+#endif
+#ifndef WL_Q6K_SP2
+#define WL_Q6K_SP2 1
+#endif
 struct Q6K {
-  static constexpr int BLOCK = 256, BYTES = 210, LPB = 8, NEED_LDS = 0, R1 = 4;
+  static constexpr int BLOCK = 256, BYTES = 210, LPB = 8, NEED_LDS = 0, R1 = WL_Q6K_R1, SP2 = WL_Q6K_SP2;
   struct Lane { int hh, g, s; };
   struct Xs { float v[4][8]; float s[4]; };
   // the aligned dwords around each 2-byte-aligned field, and the byte shift (0 or 16)
@@ -164,9 +174,8 @@ struct Q6K {
 
   __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
     // every field offset below is a multiple of 8, so all share the block's alignment
-    const uintptr_t base = reinterpret_cast<uintptr_t>(blk);
-    const uint32_t *a = reinterpret_cast<const uint32_t *>(base & ~uintptr_t(3));
-    r.sh = (uint32_t)(base & 3) * 8;
+    gu32 *a = align4_down(blk);
+    r.sh = misalign4(blk) * 8;
     const int o1 = (64 * L.hh + 8 * L.g) / 4, o2 = (64 * L.hh + 32 + 8 * L.g) / 4,
               oh = (128 + 32 * L.hh + 8 * L.g) / 4, os = (192 + 8 * L.hh) / 4;
 #pragma unroll
@@ -232,7 +241,7 @@ struct Q6K {
 // ---------------------------------------------------------------------------- Q8_0
 // Lane slice: one whole 32-value block (blocks start 2-byte aligned).
 struct Q80 {
-  static constexpr int BLOCK = 32, BYTES = 34, LPB = 1, NEED_LDS = 0, R1 = 4;
+  static constexpr int BLOCK = 32, BYTES = 34, LPB = 1, NEED_LDS = 0, R1 = 4, SP2 = 1;
   struct Lane {};
   struct Xs { float v[32]; float s; };
   // the 10 aligned dwords covering the block and the byte shift (0 or 16)
@@ -253,8 +262,8 @@ struct Q80 {
   }
 
   __device__ static void load(const uint8_t *blk, const Lane &, Raw &r) {
-    const uint32_t *a = reinterpret_cast<const uint32_t *>(reinterpret_cast<uintptr_t>(blk) & ~uintptr_t(3));
-    r.sh = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3) * 8;
+    gu32 *a = align4_down(blk);
+    r.sh = misalign4(blk) * 8;
 #pragma unroll
     for (int i = 0; i < 10; i++) r.win[i] = a[i];
   }
@@ -290,7 +299,7 @@ struct Q80 {
 // -------------------------------------------------------------------------- IQ4_XS
 // Lane slice: sub-block ib = sub (32 values, 16 bytes of qs).
 struct IQ4XS {
-  static constexpr int BLOCK = 256, BYTES = 136, LPB = 8, NEED_LDS = 0, R1 = 8;
+  static constexpr int BLOCK = 256, BYTES = 136, LPB = 8, NEED_LDS = 0, R1 = 8, SP2 = 1;
   struct Lane { int ib; };
   struct Xs { float v[32]; float s; };
   struct Raw { uint2 hdr, q01, q23; };
@@ -378,7 +387,7 @@ struct IQ4XS {
 // Lane slice: sub-block ib32 = sub: four groups of 8 values, each a grid entry (8 bytes of
 // 8/25/43) with eight signs from a 7-bit index plus a parity bit.
 struct IQ2XXS {
-  static constexpr int BLOCK = 256, BYTES = 66, LPB = 8, NEED_LDS = 1, R1 = 8;
+  static constexpr int BLOCK = 256, BYTES = 66, LPB = 8, NEED_LDS = 1, R1 = 8, SP2 = 1;
   struct Lane { int ib; };
   struct Xs { float v[32]; };
   struct Raw { uint32_t dw, a[3]; uint32_t dsh, sh; };
@@ -394,11 +403,11 @@ struct IQ2XXS {
   }
 
   __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
-    const uintptr_t pd = reinterpret_cast<uintptr_t>(blk), pa = pd + 2 + 8 * L.ib;
-    r.dw = *reinterpret_cast<const uint32_t *>(pd & ~uintptr_t(3));
-    r.dsh = (uint32_t)(pd & 2);
-    const uint32_t *a = reinterpret_cast<const uint32_t *>(pa & ~uintptr_t(3));
-    r.sh = (uint32_t)(pa & 3) * 8;
+    const uint8_t *pa = blk + 2 + 8 * L.ib;
+    r.dw = *align4_down(blk);
+    r.dsh = misalign4(blk) & 2;
+    gu32 *a = align4_down(pa);
+    r.sh = misalign4(pa) * 8;
     r.a[0] = a[0];
     r.a[1] = a[1];
     r.a[2] = a[2];

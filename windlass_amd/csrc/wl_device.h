@@ -59,19 +59,18 @@ __device__ __forceinline__ uint32_t ld4(const uint8_t *p) {
   return *reinterpret_cast<const uint32_t *>(p);
 }
 
-// 8 bytes at a 2-byte-aligned address, from the three aligned dwords that cover them. Reads
-// up to 4 bytes past p+8: every weight buffer carries padding after its last block.
-__device__ __forceinline__ uint2 ld8_a2(const uint8_t *p) {
-  const uint32_t *a = reinterpret_cast<const uint32_t *>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
-  uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3) * 8;
-  uint32_t w0 = a[0], w1 = a[1], w2 = a[2];
-  return make_uint2(__builtin_amdgcn_alignbit(w1, w0, sh), __builtin_amdgcn_alignbit(w2, w1, sh));
+// Byte offset of p within its dword.
+__device__ __forceinline__ uint32_t misalign4(const void *p) {
+  return (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3);
 }
 
-// The fp16 at a 2-byte-aligned address.
-__device__ __forceinline__ uint32_t ld_half_a2(const uint8_t *p) {
-  uint32_t w = *reinterpret_cast<const uint32_t *>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
-  return (reinterpret_cast<uintptr_t>(p) & 2) ? (w >> 16) : (w & 0xFFFF);
+// Weight and activation buffers live in global memory; loads through this pointer type are
+// global loads (a generic pointer rebuilt from an integer would otherwise become a flat load).
+typedef const __attribute__((address_space(1))) uint32_t gu32;
+
+// The dword-aligned address at or below p, in the global address space.
+__device__ __forceinline__ gu32 *align4_down(const uint8_t *p) {
+  return (gu32 *)(p - misalign4(p));
 }
 
 __device__ __forceinline__ void ld_x16(const float *p, float *v) {

@@ -4,38 +4,56 @@
 
 namespace wl {
 
-constexpr int GEMV_MAX_SEGS = 4;
+constexpr int GEMV_MAX_MATS = 4;   // matrices that share x in one launch (q, k, v)
+constexpr int GEMV_MAX_SEGS = 16;  // (matrix, K-chunk) segments of one launch
 
-// One matrix of a launch: rows [0, rows) of w (and of w2 when two matrices share the rows),
-// results to y[t * ldy + r].
+// One matrix of a launch: y[t * ldy + r] = W[r] . x[t] (nm = 2: silu(W x) * (W2 x)).
+struct GemvMat {
+  const uint8_t *w;
+  const uint8_t *w2;
+  int64_t row_bytes;
+  int rows;
+  int type;
+  float *y;
+  int ldy;
+};
+
+// One segment: a K-chunk [col0, col0 + cols) of one matrix, written to out (the result, or a
+// partial the combine kernel adds when the row is split).
 struct GemvSeg {
   const uint8_t *w;
   const uint8_t *w2;
   int64_t row_bytes;
-  float *y;
+  float *out;
+  int64_t ldo;
   int rows;
-  int ldy;
-  int wg_begin;  // first workgroup of this segment (set by the launcher)
-  int nwg;       // workgroups of this segment (set by the launcher)
+  int col0;
   int type;
+  int wg_begin;
+  int nwg;
 };
 
 struct GemvParams {
   GemvSeg seg[GEMV_MAX_SEGS];
   int nseg;
-  const float *x;  // [T][ldx]
+  int cols;  // columns of every segment
+  const float *x;
   int ldx;
-  int cols;
   int T;
 };
 
 bool gemv_supports(int type);
 bool gemv_mixed_supports(int type);
-// nm = 1: y = W x. nm = 2: y = silu(W x) * (W2 x) (the SwiGLU gate/up pair). num_cu sizes
-// the grid (a few waves per SIMD across the device).
-hipError_t gemv_launch(int type, int nm, GemvParams &p, int num_cu, hipStream_t st);
-hipError_t gemv_launch_mixed(GemvParams &p, int num_cu, hipStream_t st);
-// Waves per workgroup for a row of `cols` values.
-int gemv_waves(int cols);
+
+// K-chunks a row of `cols` values is split into when nmat matrices share a launch (1: no split).
+int gemv_chunks(int nmat, int cols);
+// Scratch floats a launch needs for partials (0 without a split).
+int64_t gemv_scratch_floats(const GemvMat *mats, int nmat, int nm, int cols, int T);
+
+// y = W x for nmat matrices sharing x [T][ldx] (T <= 8), in one launch (plus one combine
+// launch when rows are split along K). Types may differ only among Q4_K / Q6_K / Q8_0.
+// scratch holds gemv_scratch_floats(...) floats. num_cu sizes the grid.
+hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int ldx, int cols, int T,
+                    float *scratch, int num_cu, hipStream_t st);
 
 }  // namespace wl

@@ -4,6 +4,12 @@
 // Quants.DotRow per row) and MatMulEach (:544-561, one DotRow per (row, token)), plus the
 // decode-then-Block path the I-quants take (:526-536). The kernel body is cs_gemv
 // (wl_gemv_impl.h): column-stationary lanes, each weight byte read once per launch.
+//
+// Rows wider than four wave-columns (8192 values) are cut along K into equal chunks of 2-4
+// wave-columns; every chunk is a segment of the same launch whose lanes keep their x slices in
+// registers, the chunks' partial sums go to scratch, and a combine launch adds them in chunk
+// order: y = ((chunk 0 + chunk 1) + chunk 2) + ... The cut depends only on the row length and
+// the number of matrices, so a token's bits do not depend on how many tokens share the launch.
 #include "wl_gemv.h"
 #include "wl_gemv_impl.h"
 
@@ -21,64 +27,106 @@ __device__ __forceinline__ int find_seg(const GemvParams &p) {
   return si;
 }
 
+// split: the segment writes partials; for the SwiGLU pair the up partial follows the gate
+// partial at out + T * ldo.
 template <class C, int TM, int R, int NM, int SP>
-__device__ __forceinline__ void run_seg(const GemvParams &p, const GemvSeg &s) {
+__device__ __forceinline__ void run_seg(const GemvParams &p, const GemvSeg &s, int split) {
   const CsRows W{s.w, s.w2, s.row_bytes, s.rows};
-  const CsIO io{p.x, nullptr, p.ldx, s.y, nullptr, s.ldy, p.T};
+  float *y2 = (NM == 2 && split) ? s.out + (int64_t)p.T * s.ldo : nullptr;
+  const CsIO io{p.x + s.col0, nullptr, p.ldx, s.out, nullptr, s.ldo, p.T, y2};
   cs_gemv<C, TM, R, NM, SP>(W, io, p.cols, (int)blockIdx.x - s.wg_begin, s.nwg, wl_dyn_lds);
 }
 
 template <class C, int TM, int R, int NM, int SP>
-__global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
-  run_seg<C, TM, R, NM, SP>(p, p.seg[find_seg(p)]);
+__global__ __launch_bounds__(64 * kMaxWaves) void gemv_kernel(GemvParams p, int split) {
+  run_seg<C, TM, R, NM, SP>(p, p.seg[find_seg(p)], split);
 }
 
-// Segments of different formats in one launch (q/k Q4_K with v Q6_K): the codec is chosen
-// per workgroup; every segment's workgroups stay on that segment.
 // Rows per group: V = NM*R*TM partials per lane go through the exchange butterfly.
 template <class C, int TM, int NM>
 constexpr int rows_per_group() {
   return TM == 1 ? (NM == 1 ? C::R1 : C::R1 / 2) : (NM == 1 ? 4 : 2);
 }
 
+static int rows_per_group_rt(int type, int tm, int nm) {
+  if (tm > 1) return nm == 1 ? 4 : 2;
+  const int r1 = type == 12 ? Q4K::R1 : type == 14 ? Q6K::R1 : type == 8 ? Q80::R1 : type == 23 ? IQ4XS::R1
+                                                                                                    : IQ2XXS::R1;
+  return nm == 1 ? r1 : r1 / 2;
+}
+
+// Segments of different formats in one launch (q/k Q4_K with v Q6_K): the codec is chosen
+// per workgroup; every segment's workgroups stay on that segment.
 template <int TM, int SP>
-__global__ __launch_bounds__(512) void gemv_mixed_kernel(GemvParams p) {
+__global__ __launch_bounds__(64 * kMaxWaves) void gemv_mixed_kernel(GemvParams p, int split) {
   const GemvSeg &s = p.seg[find_seg(p)];
   switch (s.type) {
-    case 12: run_seg<Q4K, TM, rows_per_group<Q4K, TM, 1>(), 1, SP>(p, s); break;
-    case 14: run_seg<Q6K, TM, rows_per_group<Q6K, TM, 1>(), 1, SP>(p, s); break;
-    case 8: run_seg<Q80, TM, rows_per_group<Q80, TM, 1>(), 1, SP>(p, s); break;
+    case 12: run_seg<Q4K, TM, rows_per_group<Q4K, TM, 1>(), 1, SP>(p, s, split); break;
+    case 14: run_seg<Q6K, TM, rows_per_group<Q6K, TM, 1>(), 1, SP>(p, s, split); break;
+    case 8: run_seg<Q80, TM, rows_per_group<Q80, TM, 1>(), 1, SP>(p, s, split); break;
     default: break;
   }
 }
 
-int gemv_waves(int cols) {
-  int passes, waves;
-  cs_shape(cols, &passes, &waves);
-  return waves;
+// y = the chunk partials added in chunk order (SwiGLU pair: silu(gate sum) * (up sum)).
+struct CombineParams {
+  const float *part[GEMV_MAX_MATS];  // per matrix: [S][NM][T][rows]
+  float *y[GEMV_MAX_MATS];
+  int ldy[GEMV_MAX_MATS];
+  int rows[GEMV_MAX_MATS];
+  int S, NM, T;
+};
+
+__global__ __launch_bounds__(256) void combine_kernel(CombineParams cp) {
+  const int m = blockIdx.y;
+  const int rows = cp.rows[m];
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)cp.T * rows) return;
+  const int t = (int)(i / rows), r = (int)(i % rows);
+  const int64_t plane = (int64_t)cp.T * rows;
+  const float *p = cp.part[m] + (int64_t)t * rows + r;
+  float g = p[0];
+  for (int c = 1; c < cp.S; c++) g += p[(int64_t)c * cp.NM * plane];
+  if (cp.NM == 2) {
+    float u = p[plane];
+    for (int c = 1; c < cp.S; c++) u += p[(int64_t)c * 2 * plane + plane];
+    g = silu_mul(g, u);
+  }
+  cp.y[m][(int64_t)t * cp.ldy[m] + r] = g;
 }
 
-static int gemv_passes(int cols) {
-  int passes, waves;
-  cs_shape(cols, &passes, &waves);
-  return passes;
+int gemv_chunks(int nmat, int cols) {
+  if (cols % kColsPerWave) return 1;
+  const int u = cols / kColsPerWave;
+  if (u <= 4) return 1;
+  for (int w = 4; w >= 2; w--)
+    if (u % w == 0) return nmat * (u / w) <= GEMV_MAX_SEGS ? u / w : 1;
+  return 1;  // prime widths run unsplit (one or more passes)
 }
 
-// Split the grid over the segments in proportion to their row groups: about 16 waves per CU.
-// rows_of(i) gives segment i's rows per group.
-template <class RowsPerGroup>
-static int plan_grid(GemvParams &p, RowsPerGroup rows_of, int nwv, int num_cu) {
-  int total_groups = 0;
-  for (int i = 0; i < p.nseg; i++) total_groups += (p.seg[i].rows + rows_of(i) - 1) / rows_of(i);
-  if (total_groups == 0) return 0;
-  const int target = (num_cu * 16 + nwv - 1) / nwv;
+int64_t gemv_scratch_floats(const GemvMat *mats, int nmat, int nm, int cols, int T) {
+  const int S = gemv_chunks(nmat, cols);
+  if (S == 1) return 0;
+  int64_t n = 0;
+  for (int i = 0; i < nmat; i++) n += (int64_t)S * nm * T * mats[i].rows;
+  return n;
+}
+
+// Grid: about kWavesPerCu waves per CU, split over the segments in proportion to their groups.
+static int plan_grid(GemvParams &p, int tm, int nm, int nwv, int num_cu) {
+  int total = 0, groups[GEMV_MAX_SEGS];
+  for (int i = 0; i < p.nseg; i++) {
+    const int R = rows_per_group_rt(p.seg[i].type, tm, nm);
+    groups[i] = (p.seg[i].rows + R - 1) / R;
+    total += groups[i];
+  }
+  if (total == 0) return 0;
+  const int target = (num_cu * kWavesPerCu + nwv - 1) / nwv;
   int nwg = 0;
   for (int i = 0; i < p.nseg; i++) {
-    const int R = rows_of(i);
-    const int groups = (p.seg[i].rows + R - 1) / R;
-    int n = (int)(((int64_t)target * groups + total_groups - 1) / total_groups);
+    int n = (int)(((int64_t)target * groups[i] + total - 1) / total);
     if (n < 1) n = 1;
-    if (n > groups) n = groups;
+    if (n > groups[i]) n = groups[i];
     p.seg[i].wg_begin = nwg;
     p.seg[i].nwg = n;
     nwg += n;
@@ -87,75 +135,128 @@ static int plan_grid(GemvParams &p, RowsPerGroup rows_of, int nwv, int num_cu) {
 }
 
 template <class C, int TM, int NM>
-static hipError_t launch_one(GemvParams &p, int num_cu, hipStream_t st) {
+static hipError_t launch_one(GemvParams &p, int split, int num_cu, hipStream_t st) {
   constexpr int R = rows_per_group<C, TM, NM>();
-  const int nwv = gemv_waves(p.cols), passes = gemv_passes(p.cols);
-  const int nwg = plan_grid(p, [](int) { return R; }, nwv, num_cu);
+  int passes, nwv;
+  cs_shape(p.cols, &passes, &nwv);
+  const int nwg = plan_grid(p, TM, NM, nwv, num_cu);
   if (nwg == 0) return hipSuccess;
   const size_t smem = cs_lds_bytes<C, TM, R, NM>(nwv);
   if (TM == 1 && passes == 1)
-    hipLaunchKernelGGL((gemv_kernel<C, TM, R, NM, TM == 1 ? 1 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p);
-  else if (TM == 1 && passes == 2)
-    hipLaunchKernelGGL((gemv_kernel<C, TM, R, NM, TM == 1 ? 2 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p);
+    hipLaunchKernelGGL((gemv_kernel<C, TM, R, NM, TM == 1 ? 1 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
+  else if (TM == 1 && passes == 2 && C::SP2)
+    hipLaunchKernelGGL((gemv_kernel<C, TM, R, NM, TM == 1 ? 2 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
   else
-    hipLaunchKernelGGL((gemv_kernel<C, TM, R, NM, 0>), dim3(nwg), dim3(64 * nwv), smem, st, p);
+    hipLaunchKernelGGL((gemv_kernel<C, TM, R, NM, 0>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
   return hipGetLastError();
 }
 
 template <class C, int NM>
-static hipError_t launch_tm(GemvParams &p, int num_cu, hipStream_t st) {
-  if (p.T <= 1) return launch_one<C, 1, NM>(p, num_cu, st);
-  if (p.T <= 2) return launch_one<C, 2, NM>(p, num_cu, st);
-  if (p.T <= 4) return launch_one<C, 4, NM>(p, num_cu, st);
-  return launch_one<C, 8, NM>(p, num_cu, st);
+static hipError_t launch_tm(GemvParams &p, int split, int num_cu, hipStream_t st) {
+  if (p.T <= 1) return launch_one<C, 1, NM>(p, split, num_cu, st);
+  if (p.T <= 2) return launch_one<C, 2, NM>(p, split, num_cu, st);
+  if (p.T <= 4) return launch_one<C, 4, NM>(p, split, num_cu, st);
+  return launch_one<C, 8, NM>(p, split, num_cu, st);
 }
 
-hipError_t gemv_launch(int type, int nm, GemvParams &p, int num_cu, hipStream_t st) {
-  if (nm == 1) {
-    switch (type) {
-      case 12: return launch_tm<Q4K, 1>(p, num_cu, st);
-      case 14: return launch_tm<Q6K, 1>(p, num_cu, st);
-      case 8: return launch_tm<Q80, 1>(p, num_cu, st);
-      case 23: return launch_tm<IQ4XS, 1>(p, num_cu, st);
-      case 16: return launch_tm<IQ2XXS, 1>(p, num_cu, st);
-    }
-  } else {
-    switch (type) {
-      case 12: return launch_tm<Q4K, 2>(p, num_cu, st);
-      case 14: return launch_tm<Q6K, 2>(p, num_cu, st);
-      case 8: return launch_tm<Q80, 2>(p, num_cu, st);
-      case 23: return launch_tm<IQ4XS, 2>(p, num_cu, st);
-      case 16: return launch_tm<IQ2XXS, 2>(p, num_cu, st);
-    }
+template <int NM>
+static hipError_t launch_type(int type, GemvParams &p, int split, int num_cu, hipStream_t st) {
+  switch (type) {
+    case 12: return launch_tm<Q4K, NM>(p, split, num_cu, st);
+    case 14: return launch_tm<Q6K, NM>(p, split, num_cu, st);
+    case 8: return launch_tm<Q80, NM>(p, split, num_cu, st);
+    case 23: return launch_tm<IQ4XS, NM>(p, split, num_cu, st);
+    case 16: return launch_tm<IQ2XXS, NM>(p, split, num_cu, st);
   }
   return hipErrorInvalidValue;
 }
 
-static int mixed_rows(int type, int tm) {
-  if (tm > 1) return 4;
-  return type == 12 ? Q4K::R1 : type == 14 ? Q6K::R1 : Q80::R1;
-}
-
 template <int TM>
-static hipError_t launch_mixed_tm(GemvParams &p, int num_cu, hipStream_t st) {
-  const int nwv = gemv_waves(p.cols), passes = gemv_passes(p.cols);
-  const int nwg = plan_grid(p, [&](int i) { return mixed_rows(p.seg[i].type, TM); }, nwv, num_cu);
+static hipError_t launch_mixed_tm(GemvParams &p, int split, int num_cu, hipStream_t st) {
+  int passes, nwv;
+  cs_shape(p.cols, &passes, &nwv);
+  const int nwg = plan_grid(p, TM, 1, nwv, num_cu);
   if (nwg == 0) return hipSuccess;
   const size_t smem = sizeof(float) * 2 * nwv * 8 * TM;  // the largest R*TM of the three codecs
   if (TM == 1 && passes == 1)
-    hipLaunchKernelGGL((gemv_mixed_kernel<TM, TM == 1 ? 1 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p);
+    hipLaunchKernelGGL((gemv_mixed_kernel<TM, TM == 1 ? 1 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
   else if (TM == 1 && passes == 2)
-    hipLaunchKernelGGL((gemv_mixed_kernel<TM, TM == 1 ? 2 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p);
+    hipLaunchKernelGGL((gemv_mixed_kernel<TM, TM == 1 ? 2 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
   else
-    hipLaunchKernelGGL((gemv_mixed_kernel<TM, 0>), dim3(nwg), dim3(64 * nwv), smem, st, p);
+    hipLaunchKernelGGL((gemv_mixed_kernel<TM, 0>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
   return hipGetLastError();
 }
 
-hipError_t gemv_launch_mixed(GemvParams &p, int num_cu, hipStream_t st) {
-  if (p.T <= 1) return launch_mixed_tm<1>(p, num_cu, st);
-  if (p.T <= 2) return launch_mixed_tm<2>(p, num_cu, st);
-  if (p.T <= 4) return launch_mixed_tm<4>(p, num_cu, st);
-  return launch_mixed_tm<8>(p, num_cu, st);
+static int block_bytes(int type) {
+  return type == 12 ? 144 : type == 14 ? 210 : type == 8 ? 34 : type == 23 ? 136 : 66;
+}
+
+hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int ldx, int cols, int T,
+                    float *scratch, int num_cu, hipStream_t st) {
+  if (nmat < 1 || nmat > GEMV_MAX_MATS || T < 1 || T > 8 || (nm != 1 && nm != 2)) return hipErrorInvalidValue;
+  bool same = true;
+  for (int i = 1; i < nmat; i++) same = same && mats[i].type == mats[0].type;
+  if (!same && nm != 1) return hipErrorInvalidValue;
+  const int S = gemv_chunks(nmat, cols);
+  if (S > 1 && !scratch) return hipErrorInvalidValue;
+  GemvParams p{};
+  p.cols = cols / S;
+  p.x = x;
+  p.ldx = ldx;
+  p.T = T;
+  CombineParams cp{};
+  cp.S = S;
+  cp.NM = nm;
+  cp.T = T;
+  float *part = scratch;
+  int maxrows = 0;
+  for (int i = 0; i < nmat; i++) {
+    const GemvMat &m = mats[i];
+    const int be = m.type == 8 ? 32 : 256;
+    const int64_t chunk_bytes = (int64_t)(p.cols / be) * block_bytes(m.type);
+    for (int c = 0; c < S; c++) {
+      GemvSeg &s = p.seg[p.nseg++];
+      s.w = m.w + c * chunk_bytes;
+      s.w2 = m.w2 ? m.w2 + c * chunk_bytes : nullptr;
+      s.row_bytes = m.row_bytes;
+      s.rows = m.rows;
+      s.col0 = c * p.cols;
+      s.type = m.type;
+      if (S == 1) {
+        s.out = m.y;
+        s.ldo = m.ldy;
+      } else {
+        s.out = part + (int64_t)c * nm * T * m.rows;
+        s.ldo = m.rows;
+      }
+    }
+    if (S > 1) {
+      cp.part[i] = part;
+      cp.y[i] = m.y;
+      cp.ldy[i] = m.ldy;
+      cp.rows[i] = m.rows;
+      part += (int64_t)S * nm * T * m.rows;
+    }
+    maxrows = m.rows > maxrows ? m.rows : maxrows;
+  }
+  const int split = S > 1;
+  hipError_t e;
+  if (same) {
+    e = nm == 1 ? launch_type<1>(mats[0].type, p, split, num_cu, st)
+                : launch_type<2>(mats[0].type, p, split, num_cu, st);
+  } else if (T <= 1) {
+    e = launch_mixed_tm<1>(p, split, num_cu, st);
+  } else if (T <= 2) {
+    e = launch_mixed_tm<2>(p, split, num_cu, st);
+  } else if (T <= 4) {
+    e = launch_mixed_tm<4>(p, split, num_cu, st);
+  } else {
+    e = launch_mixed_tm<8>(p, split, num_cu, st);
+  }
+  if (e != hipSuccess || !split || maxrows == 0) return e;
+  const int64_t n = (int64_t)T * maxrows;
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256), nmat), dim3(256), 0, st, cp);
+  return hipGetLastError();
 }
 
 bool gemv_supports(int type) { return type == 12 || type == 14 || type == 8 || type == 23 || type == 16; }

@@ -19,8 +19,15 @@
 
 namespace wl {
 
-constexpr int kColsPerWave = 2048;  // every codec: 64/LPB blocks of BLOCK values per wave
-constexpr int kMaxWaves = 8;        // waves per workgroup (the kernels' launch bound is 512)
+#ifndef WL_GEMV_MAX_WAVES
+#define WL_GEMV_MAX_WAVES 8
+#endif
+#ifndef WL_GEMV_WAVES_PER_CU
+#define WL_GEMV_WAVES_PER_CU 16
+#endif
+constexpr int kColsPerWave = 2048;                // every codec: 64/LPB blocks of BLOCK values per wave
+constexpr int kMaxWaves = WL_GEMV_MAX_WAVES;      // waves per workgroup (the kernels' launch bound)
+constexpr int kWavesPerCu = WL_GEMV_WAVES_PER_CU;  // grid target: resident waves per CU
 
 // Passes and waves for a row of `cols` values (the same for every token count).
 __host__ __device__ inline void cs_shape(int cols, int *passes, int *waves) {
@@ -73,7 +80,8 @@ struct CsRows {
 };
 
 // Activations: token t reads x + (xrow ? xrow[t] : t) * ldx; results go to
-// y[(yrow ? yrow[t] : t) * ldy + r].
+// y[(yrow ? yrow[t] : t) * ldy + r]. For the SwiGLU pair, y2 non-null keeps the two sums
+// apart (gate to y, up to y2, same indexing) for a later combine instead of applying SiLU.
 struct CsIO {
   const float *x;
   const int *xrow;
@@ -82,6 +90,7 @@ struct CsIO {
   const int *yrow;
   int64_t ldy;
   int T;
+  float *y2;
 };
 
 // Dynamic LDS of a launch: the codec tables, then the double-buffered wave partials.
@@ -199,12 +208,17 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
         const float *pb = part + buf * nwv * V;
         float s = pb[t * R + r];
         for (int w = 1; w < nwv; w++) s += pb[w * V + t * R + r];
+        const int64_t o = (int64_t)(io.yrow ? io.yrow[t] : t) * io.ldy + row;
         if constexpr (NM == 2) {
           float s1 = pb[(TM + t) * R + r];
           for (int w = 1; w < nwv; w++) s1 += pb[w * V + (TM + t) * R + r];
-          s = silu_mul(s, s1);
+          if (io.y2) {
+            io.y2[o] = s1;
+          } else {
+            s = silu_mul(s, s1);
+          }
         }
-        io.y[(int64_t)(io.yrow ? io.yrow[t] : t) * io.ldy + row] = s;
+        io.y[o] = s;
       }
     }
   }

@@ -97,7 +97,7 @@ extern "C" __shared__ uint8_t wl_moe_dyn_lds[];
 
 // blockIdx.y = slot (one chosen expert); the slot's workgroups stride over the expert's rows.
 template <class C, int TM, int R, int NM, int SP>
-__global__ __launch_bounds__(512) void moe_gemv_kernel(MoeGemvArgs a) {
+__global__ __launch_bounds__(64 * kMaxWaves) void moe_gemv_kernel(MoeGemvArgs a) {
   const MoePlan *plan = a.plan;
   const int s = blockIdx.y;
   if (s >= plan->nslots) return;  // uniform over the workgroup
@@ -126,7 +126,7 @@ static hipError_t launch_moe_gemv(const MoeGemvArgs &a, int max_slots, int num_c
   cs_shape(a.cols, &passes, &nwv);
   const int groups = (a.rows + R - 1) / R;
   // about 16 waves per CU over all slots
-  int gx = (num_cu * 16 / nwv + max_slots - 1) / max_slots;
+  int gx = (num_cu * kWavesPerCu / nwv + max_slots - 1) / max_slots;
   if (gx < 1) gx = 1;
   if (gx > groups) gx = groups;
   const size_t smem = cs_lds_bytes<C, TM, R, NM>(nwv);
