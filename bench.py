@@ -50,6 +50,9 @@ def parse():
     ap.add_argument("--copies", type=int, default=4, help="distinct layer copies to rotate")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate", type=int, default=0, metavar="MIB",
+                    help="before warm-up, run a plain elementwise copy (torch.neg) of MIB MiB three "
+                         "times, untimed: the HBM counters of a kernel of known traffic")
     return ap.parse_args()
 
 
@@ -111,6 +114,14 @@ def main():
     def step(i):
         ly = layers[i % len(layers)]
         qkv(ly); o_proj(ly); gate_up(ly); down(ly)
+
+    if args.calibrate > 0:
+        src = torch.ones(args.calibrate << 18, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     # warmup, then exactly K timed steps between events on the launch stream
     for i in range(args.warmup):
