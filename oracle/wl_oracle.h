@@ -33,7 +33,10 @@ float wlo_half_round(float f);
 void wlo_half_to_float_n(const uint16_t *h, int64_t n, float *out);
 void wlo_half_from_float_n(const float *f, int64_t n, uint16_t *out);
 
-/* xorshift64* Rng of tests/TinyModels.cs:89-97. The state is one uint64. */
+/* xorshift64* Rng of tests/TinyModels.cs:89-97. The state is one uint64.
+ * Parity unpinned: the reference's tests hold no vector of this stream, and Normal() uses
+ * libm log/cos/sqrt where the reference uses .NET Math. It only generates seeded test data;
+ * every check reads the same generated data on both of its sides. */
 void wlo_rng_init(uint64_t *state, uint64_t seed);
 uint64_t wlo_rng_next(uint64_t *state);
 void wlo_rng_bytes(uint64_t *state, int64_t n, uint8_t *out);      /* Rng.Byte() n times */
@@ -76,7 +79,8 @@ int wlo_moe_ffn(const float *logits, int n_expert, int k, int renorm,
                 int *expert_runs);
 
 /* TinyModels.Matrix (tests/TinyModels.cs:342-381): random block bytes whose scale fields
- * are then set so the decoded RMS is about rms. out holds rows*cols/block*bytes bytes. */
+ * are then set so the decoded RMS is about rms. out holds rows*cols/block*bytes bytes.
+ * Parity unpinned (the scale fields depend on Rng.Normal, above); test data only. */
 int wlo_matrix(uint64_t *rng_state, int type, int rows, int cols, float rms, uint8_t *out);
 
 /* FastMath.Quantize (src/FastMath.cs:35-91) for one activation row.
