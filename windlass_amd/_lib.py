@@ -58,7 +58,8 @@ _lib = None
 
 
 def library_path():
-    return os.path.join(HERE, _LIB_NAME)
+    """The in-tree build, or the file WINDLASS_HIP_LIB names (another build of the same library)."""
+    return os.environ.get("WINDLASS_HIP_LIB") or os.path.join(HERE, _LIB_NAME)
 
 
 def load():

@@ -82,8 +82,8 @@ struct Q4K {
   }
 
   __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
-    r.hdr = ld16(blk);
-    r.q = ld16(blk + 16 + 16 * (2 * L.j + L.h));
+    r.hdr = ldw16(blk);
+    r.q = ldw16(blk + 16 + 16 * (2 * L.j + L.h));
   }
 
   __device__ static void unpack(const Raw &r, const Lane &L, const Lds &, W &w) {
@@ -180,12 +180,12 @@ struct Q6K {
               oh = (128 + 32 * L.hh + 8 * L.g) / 4, os = (192 + 8 * L.hh) / 4;
 #pragma unroll
     for (int i = 0; i < 3; i++) {
-      r.l1[i] = a[o1 + i];
-      r.l2[i] = a[o2 + i];
-      r.h[i] = a[oh + i];
-      r.sc[i] = a[os + i];
+      r.l1[i] = ldw4(a + o1 + i);
+      r.l2[i] = ldw4(a + o2 + i);
+      r.h[i] = ldw4(a + oh + i);
+      r.sc[i] = ldw4(a + os + i);
     }
-    r.dw = a[208 / 4];  // d: low half (aligned block) or high half (block at 2 mod 4)
+    r.dw = ldw4(a + 208 / 4);  // d: low half (aligned block) or high half (block at 2 mod 4)
   }
 
   __device__ static uint2 field(const uint32_t (&f)[3], uint32_t sh) {
@@ -265,7 +265,7 @@ struct Q80 {
     gu32 *a = align4_down(blk);
     r.sh = misalign4(blk) * 8;
 #pragma unroll
-    for (int i = 0; i < 10; i++) r.win[i] = a[i];
+    for (int i = 0; i < 10; i++) r.win[i] = ldw4(a + i);
   }
 
   __device__ static void unpack(const Raw &r, const Lane &, const Lds &, W &w) {
@@ -320,9 +320,9 @@ struct IQ4XS {
 
   // blocks are 8-byte aligned (136 = 8*17): 8-byte loads for the header and the 16 qs bytes
   __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
-    r.hdr = *reinterpret_cast<const uint2 *>(blk);  // d | scales_h | scales_l[4]
-    r.q01 = *reinterpret_cast<const uint2 *>(blk + 8 + 16 * L.ib);
-    r.q23 = *reinterpret_cast<const uint2 *>(blk + 16 + 16 * L.ib);
+    r.hdr = ldw8(blk);  // d | scales_h | scales_l[4]
+    r.q01 = ldw8(blk + 8 + 16 * L.ib);
+    r.q23 = ldw8(blk + 16 + 16 * L.ib);
   }
 
   // kvalues_iq4nl + 128 (all in 1..241) as bytes: table index n -> byte n.
@@ -404,13 +404,13 @@ struct IQ2XXS {
 
   __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
     const uint8_t *pa = blk + 2 + 8 * L.ib;
-    r.dw = *align4_down(blk);
+    r.dw = ldw4(align4_down(blk));
     r.dsh = misalign4(blk) & 2;
     gu32 *a = align4_down(pa);
     r.sh = misalign4(pa) * 8;
-    r.a[0] = a[0];
-    r.a[1] = a[1];
-    r.a[2] = a[2];
+    r.a[0] = ldw4(a);
+    r.a[1] = ldw4(a + 1);
+    r.a[2] = ldw4(a + 2);
   }
 
   __device__ static void unpack(const Raw &r, const Lane &, const Lds &lds, W &w) {

@@ -85,13 +85,22 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams cp) {
   const int t = (int)(i / rows), r = (int)(i % rows);
   const int64_t plane = (int64_t)cp.T * rows;
   const float *p = cp.part[m] + (int64_t)t * rows + r;
-  float g = p[0];
-  for (int c = 1; c < cp.S; c++) g += p[(int64_t)c * cp.NM * plane];
-  if (cp.NM == 2) {
-    float u = p[plane];
-    for (int c = 1; c < cp.S; c++) u += p[(int64_t)c * 2 * plane + plane];
-    g = silu_mul(g, u);
+  // every chunk's partial is loaded before the in-order sum, so the loads overlap
+  float pg[GEMV_MAX_SEGS], pu[GEMV_MAX_SEGS];
+#pragma unroll
+  for (int c = 0; c < GEMV_MAX_SEGS; c++) {
+    pg[c] = c < cp.S ? p[(int64_t)c * cp.NM * plane] : 0.f;
+    pu[c] = c < cp.S && cp.NM == 2 ? p[(int64_t)c * 2 * plane + plane] : 0.f;
   }
+  float g = pg[0], u = pu[0];
+#pragma unroll
+  for (int c = 1; c < GEMV_MAX_SEGS; c++) {
+    if (c < cp.S) {
+      g += pg[c];
+      u += pu[c];
+    }
+  }
+  if (cp.NM == 2) g = silu_mul(g, u);
   cp.y[m][(int64_t)t * cp.ldy[m] + r] = g;
 }
 

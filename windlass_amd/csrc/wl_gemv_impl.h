@@ -23,7 +23,7 @@ namespace wl {
 #define WL_GEMV_MAX_WAVES 8
 #endif
 #ifndef WL_GEMV_WAVES_PER_CU
-#define WL_GEMV_WAVES_PER_CU 16
+#define WL_GEMV_WAVES_PER_CU 32
 #endif
 constexpr int kColsPerWave = 2048;                // every codec: 64/LPB blocks of BLOCK values per wave
 constexpr int kMaxWaves = WL_GEMV_MAX_WAVES;      // waves per workgroup (the kernels' launch bound)
