@@ -29,3 +29,15 @@ def tol_check(got, x, w, rel=1e-5, absol=1e-6, what=""):
     assert not bad.any(), "%s: %d of %d outside tolerance, worst %.3g (mag %.3g)" % (
         what, int(bad.sum()), bad.size, float(err.max()), float(mag[np.unravel_index(err.argmax(), err.shape)]))
     return float((err / (mag + 1e-30)).max())
+
+
+def bf16_round(a):
+    """float32 -> nearest-even bfloat16, returned as float32 (finite inputs)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32).reshape(np.shape(a))
+
+
+# The GEMM's stated bound against the fp32 reference: each product of bf16-rounded operands is
+# within (1 + 2^-9)^2 - 1 < 2^-8 of the exact product, and fp32 accumulation adds far less.
+GEMM_REL = 2.0 ** -8

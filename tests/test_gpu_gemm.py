@@ -1,0 +1,57 @@
+"""GPU prefill GEMM (Transformer.MatMul with T > 8, src/Transformer.cs:526-536) against the oracle.
+
+The GEMM multiplies on the bf16 matrix cores: weights are decoded exactly in fp32 and rounded to
+bfloat16, x is rounded to bfloat16, products and sums are fp32. Two bars:
+  - against the same bf16-rounded operands multiplied exactly (float64): 1e-5 * sum|w*x| + 1e-6,
+    the fp32-accumulation bar of tests/Tests.cs:297-299 (this pins the tiling and lane layout);
+  - against the fp32 reference path (the oracle's decode + Block): 2^-8 * sum|w*x| + 1e-6, the
+    stated bf16 bound.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from gpu_common import GEMM_REL, QTYPES, bf16_round, blocks, decoded, tol_check
+from windlass_amd import Transformer
+from windlass_amd.backend import Context, GgmlType
+
+pytestmark = pytest.mark.gpu
+
+# rows x cols x T: tile edges in rows (128) and tokens (128), K from one 256-block up
+SHAPES = [(128, 256, 128), (200, 1024, 37), (300, 2048, 9), (64, 512, 300), (1000, 4096, 129)]
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = Context(0)
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "%dx%dxT%d" % s)
+def test_gemm_bars(ctx, t, shape):
+    rows, cols, T = shape
+    data = blocks(t, rows, cols, seed=rows * 7 + cols + int(t))
+    x = np.random.default_rng(T).standard_normal((T, cols), dtype=np.float32)
+    w = ctx.upload(t, data, rows, cols)
+    y = Transformer.MatMul(w, x, T)
+    wd = decoded(t, data, rows, cols)
+    tol_check(y, bf16_round(x), bf16_round(wd), rel=1e-5, what="%s bf16 operands" % t.name)
+    tol_check(y, x, wd, rel=GEMM_REL, what="%s vs fp32" % t.name)
+    yo = oracle.matmul(int(t), data, rows, cols, x, T)  # the reference's batch path (decode + Block)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(wd.astype(np.float64)).T
+    assert np.all(np.abs(y.astype(np.float64) - yo) <= GEMM_REL * mag + 1e-6)
+    w.free()
+
+
+def test_gemm_expert_slice(ctx):
+    t, ne, rows, cols, T = GgmlType.Q4_K, 3, 96, 512, 40
+    data = blocks(t, ne * rows, cols, seed=5)
+    w = ctx.upload(t, data, rows, cols, experts=ne)
+    x = np.random.default_rng(6).standard_normal((T, cols), dtype=np.float32)
+    wd = decoded(t, data, ne * rows, cols).reshape(ne, rows, cols)
+    for e in range(ne):
+        y = Transformer.MatMul(w.Slice(e), x, T)
+        tol_check(y, bf16_round(x), bf16_round(wd[e]), rel=1e-5, what="expert %d" % e)
+    w.free()

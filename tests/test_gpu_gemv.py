@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
-from gpu_common import QTYPES, blocks, decoded, tol_check
+from gpu_common import GEMM_REL, QTYPES, blocks, decoded, tol_check
 from windlass_amd import Transformer
 from windlass_amd.backend import Context, GgmlType
 
@@ -60,12 +60,13 @@ def test_batch_rows_equal_single_token_bitwise(ctx, t, cols):
 
 
 def test_more_than_eight_tokens(ctx):
+    # T > 8 runs the bf16 MFMA GEMM: within the stated bf16 bound of the fp32 result
     t, rows, cols, T = GgmlType.Q4_K, 64, 1024, 19
     data = blocks(t, rows, cols, seed=1)
     w = ctx.upload(t, data, rows, cols)
     x = np.random.default_rng(2).standard_normal((T, cols), dtype=np.float32)
     y = Transformer.MatMul(w, x, T)
-    tol_check(y, x, decoded(t, data, rows, cols), rel=1e-5, what="T=19")
+    tol_check(y, x, decoded(t, data, rows, cols), rel=GEMM_REL, what="T=19")
     w.free()
 
 

@@ -35,12 +35,12 @@ struct wl_ctx {
   int num_cu;
   hipStream_t stream;
   // growable scratch (device)
-  void *buf[7];
-  size_t cap[7];
+  void *buf[8];
+  size_t cap[8];
 };
 
-// S_PART holds the K-chunk partials of split GEMV rows.
-enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART };
+// S_PART holds the K-chunk partials of split GEMV rows, S_XB the bf16 copy of x for the GEMM.
+enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB };
 
 static thread_local std::string g_err;
 
@@ -246,7 +246,10 @@ static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float
   int64_t rows;
   operand(w, expert, &base, &rows);
   if (T > 8 && wl::gemm_supports(w->type)) {
-    WL_HIP(wl::gemm_launch(w->type, base, w->row_bytes, (int)rows, (int)w->cols, d_x, T, d_y, c->stream), "gemm launch");
+    if ((rc = ensure(c, S_XB, (size_t)wl::gemm_scratch_bytes(T, (int)w->cols)))) return rc;
+    WL_HIP(wl::gemm_launch(w->type, base, w->row_bytes, (int)rows, (int)w->cols, d_x, T, d_y, (int)rows,
+                           c->buf[S_XB], c->stream),
+           "gemm launch");
     return WL_OK;
   }
   // decode GEMV in passes of up to 8 tokens (a token's result does not depend on its pass)
