@@ -17,8 +17,11 @@ from windlass_amd.backend import Context, GgmlType
 
 pytestmark = pytest.mark.gpu
 
-# rows x cols x T: tile edges in rows (128) and tokens (128), K from one 256-block up
-SHAPES = [(128, 256, 128), (200, 1024, 37), (300, 2048, 9), (64, 512, 300), (1000, 4096, 129)]
+# rows x cols x T: tile edges in rows (128) and tokens (256), K from one 256-block up. Launches
+# with fewer output tiles than CUs split K into chunks (all but the first two shapes below on a
+# 256-CU device); 4224 x 512 x 2000 has 264 tiles and runs unsplit.
+SHAPES = [(128, 256, 128), (4224, 512, 2000), (200, 1024, 37), (300, 2048, 9), (64, 512, 300),
+          (1000, 4096, 129)]
 
 
 @pytest.fixture(scope="module")

@@ -246,9 +246,9 @@ static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float
   int64_t rows;
   operand(w, expert, &base, &rows);
   if (T > 8 && wl::gemm_supports(w->type)) {
-    if ((rc = ensure(c, S_XB, (size_t)wl::gemm_scratch_bytes(T, (int)w->cols)))) return rc;
+    if ((rc = ensure(c, S_XB, (size_t)wl::gemm_scratch_bytes((int)rows, (int)w->cols, T, c->num_cu)))) return rc;
     WL_HIP(wl::gemm_launch(w->type, base, w->row_bytes, (int)rows, (int)w->cols, d_x, T, d_y, (int)rows,
-                           c->buf[S_XB], c->stream),
+                           c->buf[S_XB], c->num_cu, c->stream),
            "gemm launch");
     return WL_OK;
   }

@@ -7,14 +7,16 @@ namespace wl {
 
 bool gemm_supports(int type);
 
-// Bytes of scratch gemm_launch needs for T rows of x of `cols` values (x as bf16).
-inline int64_t gemm_scratch_bytes(int T, int cols) { return (int64_t)T * cols * 2; }
+// K-chunks of a launch (1 when the output tiles alone fill the device).
+int gemm_chunks(int rows, int cols, int T, int num_cu);
+// Bytes of scratch gemm_launch needs: x as bf16, then the chunk partials when K is split.
+int64_t gemm_scratch_bytes(int rows, int cols, int T, int num_cu);
 
 // y[t * ldy + r] = sum_k W[r][k] * x[t][k] for T rows of x (x is [T][cols] fp32), W rows x cols
 // raw blocks of `type`. The operands enter the matrix cores as bf16 (weights decoded exactly in
 // fp32, then rounded to nearest even; x rounded the same way into `scratch`); products and sums
-// are fp32.
+// are fp32. A split K adds the chunk partials in chunk order, so results are deterministic.
 hipError_t gemm_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, int cols, const float *x, int T,
-                       float *y, int ldy, void *scratch, hipStream_t st);
+                       float *y, int ldy, void *scratch, int num_cu, hipStream_t st);
 
 }  // namespace wl
