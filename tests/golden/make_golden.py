@@ -88,12 +88,40 @@ def quantizer_pins():
     }
 
 
+# Tiny models whose weights use this path's formats (TinyModels.StandardSpecs, tests/TinyModels.cs:166-177).
+TINY_KEYS = ["llama-q4_K", "llama-q6_K", "llama-q8_0", "llama-q8_0-spm", "qwen2-q8_0", "qwen3-q4_K",
+             "qwen2-q6_K-tied"]
+LLAMA_CPP_FIXTURE = "/root/reference/tests/fixtures/llama-cpp-reference.txt"
+
+
+def llama_cpp_rows():
+    """The 'argmax' and 'last' rows of the reference's llama.cpp fixture for TINY_KEYS: the top
+    token at each of the 12 probe positions and the last position's logits (4 decimals), which
+    tests/Tests.cs:250-278 compares against."""
+    rows, key = {}, None
+    with open(LLAMA_CPP_FIXTURE, encoding="utf-8") as f:
+        for line in f:
+            parts = line.split()
+            if not parts:
+                continue
+            if parts[0] == "model":
+                key = parts[1]
+            elif key in TINY_KEYS and parts[0] in ("argmax", "last"):
+                vals = [int(v) for v in parts[1:]] if parts[0] == "argmax" else [float(v) for v in parts[1:]]
+                rows.setdefault(key, {})[parts[0]] = vals
+    return {"source": "tests/fixtures/llama-cpp-reference.txt (llama-cpp-python 0.3.36, CPU)", "models": rows}
+
+
 def main():
     out = {"iq2xxs_hand": iq2xxs_hand_block(), "route": route_cases(), "tables": tables(),
            "quantizers": quantizer_pins()}
     with open(os.path.join(HERE, "reference_pins.json"), "w") as f:
         json.dump(out, f, indent=1)
         f.write("\n")
+    if os.path.exists(LLAMA_CPP_FIXTURE):
+        with open(os.path.join(HERE, "llama_cpp_tiny.json"), "w") as f:
+            json.dump(llama_cpp_rows(), f)
+            f.write("\n")
 
 
 if __name__ == "__main__":

@@ -1,0 +1,97 @@
+"""Tiny seeded models end to end (tests/Tests.cs:250-278, LogitsMatchLlamaCpp).
+
+CPU: the forward pass on the oracle's matrix products matches llama.cpp's outputs for the same
+models (the reference's own bar: max |logit - llama.cpp| <= 0.2 * std of llama.cpp's last logits,
+top token equal at >= 11 of 12 probe positions). This pins the model builder, the norms, the
+feed-forward and the head that the GPU test below reuses; attention moves the logits of these
+random models little except in the qwen2 models (zeroing the attention output shifts qwen2 by
+about 3 std of the logits, llama by 0.035), so it is pinned there only.
+
+GPU: with every matrix product on the GPU library, the model gives the same greedy tokens as the
+CPU backend (prompt in chunks of 8 tokens, so every product runs the fp32 decode GEMV, then 8
+greedy steps), and the whole-prompt pass (T = 12: the bf16 GEMM) meets the llama.cpp bar.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from tiny_model import PROBE, SPECS, Model, oracle_matmul
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LLAMA_CPP = json.load(open(os.path.join(HERE, "golden", "llama_cpp_tiny.json")))["models"]
+KEYS = sorted(SPECS)
+
+
+def llama_cpp_bar(key, all_logits):
+    ref = LLAMA_CPP[key]
+    last = np.array(ref["last"], np.float64)
+    std = last.std()
+    diff = np.abs(all_logits[-1].astype(np.float64) - last).max()
+    agree = sum(int(np.argmax(all_logits[t]) == ref["argmax"][t]) for t in range(len(PROBE)))
+    return diff / std, agree
+
+
+@pytest.mark.parametrize("key", KEYS)
+def test_cpu_forward_matches_llama_cpp(key):
+    m = Model(key, oracle_matmul)
+    logits = m.forward(PROBE, 0)
+    rel, agree = llama_cpp_bar(key, logits)
+    assert rel <= 0.2 and agree >= len(PROBE) - 1, "%s: max diff %.4f std, %d/12 argmax" % (key, rel, agree)
+
+
+def test_bar_rejects_broken_products():
+    """The bar is not vacuous: a negated down projection (llama) or a zeroed attention output
+    (qwen2) fails it."""
+    def negated_down(name, w, x):
+        y = oracle_matmul(name, w, x)
+        return -y if name.endswith("ffn_down") else y
+
+    def no_attention(name, w, x):
+        y = oracle_matmul(name, w, x)
+        return 0 * y if name.endswith("attn_output") else y
+
+    for key, mm in (("llama-q4_K", negated_down), ("qwen2-q6_K-tied", no_attention)):
+        rel, agree = llama_cpp_bar(key, Model(key, mm).forward(PROBE, 0))
+        assert rel > 0.2 or agree < len(PROBE) - 1, key
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    from windlass_amd.backend import Context
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def gpu_matmul(ctx):
+    from windlass_amd import Transformer
+    cache = {}
+
+    def mm(name, w, x):
+        key = id(w)
+        if key not in cache:
+            cache[key] = ctx.upload(w.type, w.data, w.rows, w.cols, name=name)
+        x = np.ascontiguousarray(x, np.float32)
+        return Transformer.MatMul(cache[key], x, x.shape[0])
+
+    return mm, cache
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("key", KEYS)
+def test_gpu_greedy_tokens_match_cpu(gpu, key):
+    mm, cache = gpu_matmul(gpu)
+    cpu, dev = Model(key, oracle_matmul), Model(key, mm)
+    want, want_logits = cpu.greedy(PROBE, 8, chunk=8)
+    got, got_logits = dev.greedy(PROBE, 8, chunk=8)
+    for a, b in zip(want_logits, got_logits):
+        assert np.abs(a - b).max() <= 1e-3 * np.std(a), "%s: logits drift from the CPU backend" % key
+    assert got == want, "%s: greedy tokens %s, CPU backend %s" % (key, got, want)
+    # the whole prompt at once (T = 12) runs the bf16 GEMM: llama.cpp's bar still holds
+    dev.reset()
+    rel, agree = llama_cpp_bar(key, dev.forward(PROBE, 0))
+    assert rel <= 0.2 and agree >= len(PROBE) - 1, "%s: max diff %.4f std, %d/12 argmax" % (key, rel, agree)
+    for w in cache.values():
+        w.free()
