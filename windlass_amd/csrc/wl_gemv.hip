@@ -186,7 +186,7 @@ static hipError_t launch_mixed_tm(GemvParams &p, int split, int num_cu, hipStrea
   cs_shape(p.cols, &passes, &nwv);
   const int nwg = plan_grid(p, TM, 1, nwv, num_cu);
   if (nwg == 0) return hipSuccess;
-  const size_t smem = sizeof(float) * 2 * nwv * 8 * TM;  // the largest R*TM of the three codecs
+  const size_t smem = sizeof(float) * 2 * GS * nwv * 8 * TM;  // the largest R*TM of the three codecs
   if (TM == 1 && passes == 1)
     hipLaunchKernelGGL((gemv_mixed_kernel<TM, TM == 1 ? 1 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
   else if (TM == 1 && passes == 2)

@@ -93,10 +93,16 @@ struct CsIO {
   float *y2;
 };
 
+// Row groups whose wave results are buffered in LDS between two barriers.
+#ifndef WL_GEMV_GROUPS_PER_SYNC
+#define WL_GEMV_GROUPS_PER_SYNC 4
+#endif
+constexpr int GS = WL_GEMV_GROUPS_PER_SYNC;
+
 // Dynamic LDS of a launch: the codec tables, then the double-buffered wave partials.
 template <class C, int TM, int R, int NM>
 inline size_t cs_lds_bytes(int nwv) {
-  return (C::NEED_LDS ? sizeof(Lds) : 0) + sizeof(float) * 2 * nwv * NM * R * TM;
+  return (C::NEED_LDS ? sizeof(Lds) : 0) + sizeof(float) * 2 * GS * nwv * NM * R * TM;
 }
 
 // SP: passes whose x slices stay in registers (0: x read per row group; 1 or 2 only for TM 1).
@@ -110,10 +116,6 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
   constexpr int BPW = 64 / C::LPB;
   const Lds &lds = *reinterpret_cast<const Lds *>(lds_raw);
   float *part = reinterpret_cast<float *>(lds_raw + (C::NEED_LDS ? sizeof(Lds) : 0));
-  if constexpr (C::NEED_LDS) {
-    C::init_lds(*reinterpret_cast<Lds *>(lds_raw));
-    __syncthreads();
-  }
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
   const int sub = lane % C::LPB, bslot = lane / C::LPB;
   const typename C::Lane L = C::lane(sub);
@@ -134,8 +136,16 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
     if (b < nb) C::load_x(xr[0] + (int64_t)b * C::BLOCK, L, xs0[p]);
   }
 
-  int buf = 0;
-  for (int g = g0; g < ngroups; g += gstride, buf ^= 1) {
+  if constexpr (C::NEED_LDS) {
+    C::init_lds(*reinterpret_cast<Lds *>(lds_raw));
+    __syncthreads();
+  }
+
+  // Reduced group results go to LDS slot `slot` of buffer `buf`; every GS groups (and after the
+  // last) one barrier, then wave 0 finishes the buffered groups while the other waves go on
+  // into the other buffer.
+  int buf = 0, slot = 0, gfirst = g0;
+  for (int g = g0; g < ngroups; g += gstride) {
     float acc[NM][R][TM];
 #pragma unroll
     for (int m = 0; m < NM; m++)
@@ -199,28 +209,38 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
 #pragma unroll
         for (int r = 0; r < R; r++) vals[(m * TM + t) * R + r] = acc[m][r][t];
     const float q = exch_reduce<V, 5>(vals, lane);
-    if ((lane & ((1 << LOW) - 1)) == 0) part[(buf * nwv + wv) * V + (lane >> LOW)] = q;
+    if ((lane & ((1 << LOW) - 1)) == 0) part[((buf * GS + slot) * nwv + wv) * V + (lane >> LOW)] = q;
+    if (slot + 1 < GS && g + gstride < ngroups) {  // uniform over the workgroup
+      slot++;
+      continue;
+    }
     __syncthreads();
-    if (wv == 0 && lane < R * TM) {
-      const int r = lane % R, t = lane / R;
-      const int row = g * R + r;
-      if (t < io.T && row < W.rows) {
-        const float *pb = part + buf * nwv * V;
-        float s = pb[t * R + r];
-        for (int w = 1; w < nwv; w++) s += pb[w * V + t * R + r];
-        const int64_t o = (int64_t)(io.yrow ? io.yrow[t] : t) * io.ldy + row;
-        if constexpr (NM == 2) {
-          float s1 = pb[(TM + t) * R + r];
-          for (int w = 1; w < nwv; w++) s1 += pb[w * V + (TM + t) * R + r];
-          if (io.y2) {
-            io.y2[o] = s1;
-          } else {
-            s = silu_mul(s, s1);
+    if (wv == 0) {
+      for (int i = lane; i < (slot + 1) * R * TM; i += 64) {
+        const int sl = i / (R * TM), rt = i % (R * TM);
+        const int r = rt % R, t = rt / R;
+        const int row = (gfirst + sl * gstride) * R + r;
+        if (t < io.T && row < W.rows) {
+          const float *pb = part + (buf * GS + sl) * nwv * V;
+          float s = pb[t * R + r];
+          for (int w = 1; w < nwv; w++) s += pb[w * V + t * R + r];
+          const int64_t o = (int64_t)(io.yrow ? io.yrow[t] : t) * io.ldy + row;
+          if constexpr (NM == 2) {
+            float s1 = pb[(TM + t) * R + r];
+            for (int w = 1; w < nwv; w++) s1 += pb[w * V + (TM + t) * R + r];
+            if (io.y2) {
+              io.y2[o] = s1;
+            } else {
+              s = silu_mul(s, s1);
+            }
           }
+          io.y[o] = s;
         }
-        io.y[o] = s;
       }
     }
+    buf ^= 1;
+    slot = 0;
+    gfirst = g + gstride;
   }
 }
 
