@@ -35,7 +35,8 @@ def test_route_known_answers(ctx):
                 assert np.all(np.abs(wts[0] - np.array(c["wts"])) < PINS["route"]["tol"])
 
 
-@pytest.mark.parametrize("n,k", [(128, 8), (64, 4), (8, 2)])
+# n <= 2048 (and k <= 64) runs one wave per token; 3000 experts or 70 choices the serial kernel
+@pytest.mark.parametrize("n,k", [(128, 8), (64, 4), (8, 2), (300, 8), (2048, 16), (3000, 4), (200, 70)])
 def test_route_vs_oracle(ctx, n, k):
     T = 16
     lg = np.random.default_rng(n + k).standard_normal((T, n), dtype=np.float32)
@@ -46,10 +47,33 @@ def test_route_vs_oracle(ctx, n, k):
         assert np.all(np.abs(wts[t] - owts) <= 1e-6 * np.abs(owts))
 
 
+@pytest.mark.parametrize("n", [100, 3000])
+def test_route_ties_and_nan_vs_oracle(ctx, n):
+    """Repeated logits pick the lower id; a NaN logit follows the reference's sequential scan
+    (a NaN first-untaken entry is kept, a later NaN never wins)."""
+    rng = np.random.default_rng(n)
+    T, k = 6, 4
+    lg = np.round(rng.standard_normal((T, n)), 1).astype(np.float32)  # many exact ties
+    lg[1, 7] = np.nan
+    lg[2, 0] = np.nan
+    lg[3, :] = 0.5  # all equal
+    lg[4, 3:9] = np.inf
+    sel, wts = Transformer.Route(ctx, lg, n, k, True)
+    for t in range(T):
+        osel, owts, _ = oracle.route(lg[t], k, True)
+        assert list(sel[t]) == list(osel), t
+        ok = np.isclose(wts[t], owts, rtol=1e-6, atol=0, equal_nan=True)
+        assert ok.all(), (t, wts[t], owts)
+
+
+# (ne, k, embd, ff): 128 experts top-8 is the qwen3moe routing shape; 2100 experts route on the
+# serial kernel and plan separately
 @pytest.mark.parametrize("T", [1, 8, 11])
 @pytest.mark.parametrize("types", [(12, 12), (12, 14)])
-def test_moe_ffn_vs_oracle(ctx, T, types):
-    ne, k, embd, ff = 16, 4, 512, 256
+@pytest.mark.parametrize("shape", [(16, 4, 512, 256), (128, 8, 512, 256), (2100, 2, 256, 256)],
+                         ids=lambda s: "ne%d_k%d" % s[:2])
+def test_moe_ffn_vs_oracle(ctx, T, types, shape):
+    ne, k, embd, ff = shape
     gt, dt = types
     gate = blocks(gt, ne * ff, embd, seed=1)
     up = blocks(gt, ne * ff, embd, seed=2)

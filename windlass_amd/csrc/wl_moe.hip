@@ -1,10 +1,10 @@
 // wl_moe.hip - routed mixture-of-experts FFN on the GPU.
 //
 // Restates MoeFfn + Route (src/Transformer.cs:253-340) without a host round trip:
-//   1. route_kernel    one thread per token runs the reference's sequential routing: softmax
+//   1. route + plan    one workgroup: wave t runs the reference's routing of token t (softmax
 //                      with a double denominator, k largest with ties to the lower id,
-//                      renormalisation clamped at 6.103515625e-5 (:315-340);
-//   2. plan_kernel     one thread orders the (expert, token) pairs: experts ascending, tokens
+//                      renormalisation clamped at 6.103515625e-5, :315-340), then one thread per
+//                      (token, choice) pair numbers the pairs: experts ascending, tokens
 //                      ascending within an expert (the gather order of :271-286);
 //   3. moe_gate_up     grouped decode GEMV over the chosen experts' gate/up slices
 //                      (WeightView.Slice, src/LayerStream.cs:26-34), SiLU epilogue;
@@ -21,8 +21,9 @@ namespace wl {
 
 #define WL_MIN_EXPERT_WEIGHT_SUM 6.103515625e-5f  // src/Transformer.cs:253
 
-__global__ void route_kernel(const float *__restrict__ logits, int T, int n, int k, int renorm,
-                             int *__restrict__ sel, float *__restrict__ wts, float *__restrict__ prob) {
+// Serial routing, one thread per token (expert counts above kRouteWaveMax).
+__global__ void route_serial_kernel(const float *__restrict__ logits, int T, int n, int k, int renorm,
+                                    int *__restrict__ sel, float *__restrict__ wts, float *__restrict__ prob) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= T) return;
   const float *l = logits + (int64_t)t * n;
@@ -55,42 +56,166 @@ __global__ void route_kernel(const float *__restrict__ logits, int T, int n, int
   }
 }
 
-__global__ void plan_kernel(const int *__restrict__ sel, const float *__restrict__ wts, int T, int k, int ne,
-                            MoePlan *__restrict__ plan) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int ns = 0, np = 0;
-  for (int e = 0; e < ne; e++) {
-    int n = 0;
-    for (int t = 0; t < T; t++)
-      for (int j = 0; j < k; j++)
-        if (sel[t * k + j] == e) {
-          plan->slot_tok[ns][n] = t;
-          plan->slot_pair[ns][n] = np;
-          plan->tok_pair[t][j] = np;
-          plan->tok_w[t][j] = wts[t * k + j];
-          n++;
-          np++;
+// Routing of one token per wave (n <= 64 * PER experts, k <= 64): lane l holds probabilities l, l + 64,
+// ...; the same values as route_serial_kernel. The maximum ignores NaN like the reference's `>`
+// scan; the softmax denominator is summed in double in index order (values read lane by lane);
+// each of the k rounds picks what the reference's sequential scan picks: the first untaken entry
+// when it is NaN, else the largest untaken non-NaN value, ties to the lower id.
+constexpr int kRouteWaveMax = 64 * 32;
+
+__device__ __forceinline__ bool route_better(float v, int i, float bv, int bi) {
+  return bi < 0 || v > bv || (v == bv && i < bi);
+}
+
+template <int PER>
+__device__ __forceinline__ void route_wave(const float *__restrict__ l, int n, int k, int renorm,
+                                           int *__restrict__ sel, float *__restrict__ wts) {
+  const int lane = threadIdx.x & 63;
+  float v[PER];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int m = 0; m < PER; m++) {
+    const int i = lane + 64 * m;
+    v[m] = i < n ? l[i] : -INFINITY;
+    if (v[m] > mx) mx = v[m];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float u = __shfl_xor(mx, o, 64);
+    if (u > mx) mx = u;
+  }
+#pragma unroll
+  for (int m = 0; m < PER; m++)
+    if (lane + 64 * m < n) v[m] = (float)exp((double)(v[m] - mx));
+  double sum = 0;  // in index order: entry 64m + j lives in lane j
+#pragma unroll
+  for (int m = 0; m < PER; m++) {
+    const int cnt = n - 64 * m < 64 ? n - 64 * m : 64;
+    for (int j = 0; j < cnt; j++) sum += (double)__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[m]), j));
+  }
+  const float inv = (float)(1.0 / sum);
+#pragma unroll
+  for (int m = 0; m < PER; m++) v[m] *= inv;
+  uint32_t taken = 0;  // bit m: entry lane + 64m chosen
+  float chosen = 0, mine_w = 0.f;  // lane j keeps choice j
+  int mine = 0;
+  for (int j = 0; j < k; j++) {
+    int first = 0x7FFFFFFF, bi = -1;
+    float bv = 0.f;
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+      const int i = lane + 64 * m;
+      if (i < n && !((taken >> m) & 1)) {
+        if (i < first) first = i;
+        if (v[m] == v[m] && route_better(v[m], i, bv, bi)) {
+          bv = v[m];
+          bi = i;
         }
-    if (n) {
-      plan->slot_expert[ns] = e;
-      plan->slot_ntok[ns] = n;
-      ns++;
-    }
-  }
-  plan->nslots = ns;
-  // each token's pairs in ascending expert order: sort its k entries by the chosen expert id
-  for (int t = 0; t < T; t++) {
-    int ord[MOE_MAX_K];
-    for (int j = 0; j < k; j++) ord[j] = j;
-    for (int a = 1; a < k; a++)
-      for (int b = a; b > 0 && sel[t * k + ord[b]] < sel[t * k + ord[b - 1]]; b--) {
-        int tmp = ord[b]; ord[b] = ord[b - 1]; ord[b - 1] = tmp;
       }
-    for (int j = 0; j < k; j++) {
-      plan->comb_pair[t][j] = plan->tok_pair[t][ord[j]];
-      plan->comb_w[t][j] = plan->tok_w[t][ord[j]];
     }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const int f2 = __shfl_xor(first, o, 64);
+      const int i2 = __shfl_xor(bi, o, 64);
+      const float v2 = __shfl_xor(bv, o, 64);
+      if (f2 < first) first = f2;
+      if (i2 >= 0 && route_better(v2, i2, bv, bi)) {
+        bv = v2;
+        bi = i2;
+      }
+    }
+    // the first untaken entry is a NaN: the reference's scan keeps it
+    float firstv = 0.f;
+#pragma unroll
+    for (int m = 0; m < PER; m++)
+      if (lane + 64 * m == first) firstv = v[m];
+    firstv = __shfl(firstv, first & 63, 64);
+    const int best = (firstv != firstv) ? first : bi;
+    const float bw = best == first ? firstv : bv;
+#pragma unroll
+    for (int m = 0; m < PER; m++)
+      if (lane + 64 * m == best) taken |= 1u << m;
+    if (lane == j) {
+      mine = best;
+      mine_w = bw;
+    }
+    chosen += bw;
   }
+  if (lane < k) {
+    if (renorm) {
+      const float div = chosen > WL_MIN_EXPERT_WEIGHT_SUM ? chosen : WL_MIN_EXPERT_WEIGHT_SUM;
+      mine_w /= div;
+    }
+    sel[lane] = mine;
+    wts[lane] = mine_w;
+  }
+}
+
+template <int PER>
+__global__ __launch_bounds__(64) void route_wave_kernel(const float *__restrict__ logits, int n, int k, int renorm,
+                                                        int *__restrict__ sel, float *__restrict__ wts) {
+  const int t = blockIdx.x;
+  route_wave<PER>(logits + (int64_t)t * n, n, k, renorm, sel + t * k, wts + t * k);
+}
+
+// The routing plan from T tokens' k choices, one thread per (token, choice) pair. Pairs are
+// numbered experts ascending, tokens ascending within an expert (the gather order of
+// src/Transformer.cs:271-286); each token's pairs are listed again in ascending expert order for
+// the combine (:289-293).
+__device__ __forceinline__ void plan_pairs(const int *__restrict__ sel, const float *__restrict__ wts, int T, int k,
+                                           MoePlan *__restrict__ plan) {
+  __shared__ int se[MOE_MAX_PAIRS];
+  __shared__ int first_of[MOE_MAX_PAIRS];  // pair a is the lowest-index pair of its expert
+  const int P = T * k, i = threadIdx.x;
+  if (i < P) se[i] = sel[i];
+  __syncthreads();
+  if (i < P) {
+    int f = 1;
+    for (int b = 0; b < i; b++)
+      if (se[b] == se[i]) f = 0;
+    first_of[i] = f;
+  }
+  __syncthreads();
+  if (i >= P) return;
+  const int e = se[i], t = i / k, j = i % k;
+  int rank = 0, before = 0, same = 0, slot = 0, pos = 0, nslots = 0;
+  for (int a = 0; a < P; a++) {
+    const int ea = se[a], ta = a / k;
+    if (ea < e || (ea == e && ta < t)) rank++;
+    if (ea == e) {
+      same++;
+      if (ta < t) before++;
+    }
+    if (first_of[a]) {
+      nslots++;
+      if (ea < e) slot++;
+    }
+    if (ta == t && ea < e) pos++;
+  }
+  plan->slot_tok[slot][before] = t;
+  plan->slot_pair[slot][before] = rank;
+  plan->tok_pair[t][j] = rank;
+  plan->tok_w[t][j] = wts[i];
+  plan->comb_pair[t][pos] = rank;
+  plan->comb_w[t][pos] = wts[i];
+  if (before == 0) {
+    plan->slot_expert[slot] = e;
+    plan->slot_ntok[slot] = same;
+  }
+  if (i == 0) plan->nslots = nslots;
+}
+
+// Routing and plan in one workgroup of T waves: wave t routes token t (unless `route` is 0 and
+// sel/wts already hold the choices), then the pairs are numbered (after the barrier every choice
+// is visible to the workgroup).
+template <int PER>
+__global__ __launch_bounds__(64 * MOE_MAX_T) void route_plan_kernel(const float *__restrict__ logits, int T, int n,
+                                                                    int k, int renorm, int route, int *__restrict__ sel,
+                                                                    float *__restrict__ wts, MoePlan *__restrict__ plan) {
+  const int t = threadIdx.x >> 6;
+  if (route && t < T) route_wave<PER>(logits + (int64_t)t * n, n, k, renorm, sel + t * k, wts + t * k);
+  __syncthreads();
+  plan_pairs(sel, wts, T, k, plan);
 }
 
 extern "C" __shared__ uint8_t wl_moe_dyn_lds[];
@@ -157,17 +282,52 @@ static hipError_t launch_moe_type(int type, const MoeGemvArgs &a, int T, int max
   return hipErrorInvalidValue;
 }
 
+static int route_per(int n) { return n <= 64 ? 1 : n <= 128 ? 2 : n <= 256 ? 4 : n <= 512 ? 8 : n <= 1024 ? 16 : 32; }
+
 hipError_t route_launch(const float *logits, int T, int n, int k, int renorm, int *sel, float *wts, float *prob,
                         hipStream_t st) {
-  hipLaunchKernelGGL(route_kernel, dim3((T + 63) / 64), dim3(64), 0, st, logits, T, n, k, renorm, sel, wts, prob);
+  if (n > kRouteWaveMax || k > 64) {  // the wave kernel keeps choice j in lane j
+    hipLaunchKernelGGL(route_serial_kernel, dim3((T + 63) / 64), dim3(64), 0, st, logits, T, n, k, renorm, sel, wts,
+                       prob);
+    return hipGetLastError();
+  }
+  switch (route_per(n)) {
+    case 1: hipLaunchKernelGGL(route_wave_kernel<1>, dim3(T), dim3(64), 0, st, logits, n, k, renorm, sel, wts); break;
+    case 2: hipLaunchKernelGGL(route_wave_kernel<2>, dim3(T), dim3(64), 0, st, logits, n, k, renorm, sel, wts); break;
+    case 4: hipLaunchKernelGGL(route_wave_kernel<4>, dim3(T), dim3(64), 0, st, logits, n, k, renorm, sel, wts); break;
+    case 8: hipLaunchKernelGGL(route_wave_kernel<8>, dim3(T), dim3(64), 0, st, logits, n, k, renorm, sel, wts); break;
+    case 16: hipLaunchKernelGGL(route_wave_kernel<16>, dim3(T), dim3(64), 0, st, logits, n, k, renorm, sel, wts); break;
+    default: hipLaunchKernelGGL(route_wave_kernel<32>, dim3(T), dim3(64), 0, st, logits, n, k, renorm, sel, wts); break;
+  }
+  return hipGetLastError();
+}
+
+static hipError_t route_plan_launch(const MoeLaunch &m, hipStream_t st) {
+  if (m.ne > kRouteWaveMax) {
+    hipError_t e = route_launch(m.logits, m.T, m.ne, m.k, m.renorm, m.sel, m.wts, m.prob, st);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(route_plan_kernel<1>, dim3(1), dim3(64 * MOE_MAX_T), 0, st, m.logits, m.T, m.ne, m.k, m.renorm,
+                       0, m.sel, m.wts, m.plan);
+    return hipGetLastError();
+  }
+#define WL_RP(P)                                                                                                  \
+  hipLaunchKernelGGL(route_plan_kernel<P>, dim3(1), dim3(64 * MOE_MAX_T), 0, st, m.logits, m.T, m.ne, m.k, m.renorm, \
+                     1, m.sel, m.wts, m.plan)
+  switch (route_per(m.ne)) {
+    case 1: WL_RP(1); break;
+    case 2: WL_RP(2); break;
+    case 4: WL_RP(4); break;
+    case 8: WL_RP(8); break;
+    case 16: WL_RP(16); break;
+    default: WL_RP(32); break;
+  }
+#undef WL_RP
   return hipGetLastError();
 }
 
 hipError_t moe_launch(const MoeLaunch &m, int num_cu, hipStream_t st) {
-  hipError_t err = route_launch(m.logits, m.T, m.ne, m.k, m.renorm, m.sel, m.wts, m.prob, st);
+  hipError_t err = route_plan_launch(m, st);
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(64), 0, st, m.sel, m.wts, m.T, m.k, m.ne, m.plan);
-  if ((err = hipGetLastError()) != hipSuccess) return err;
   const int max_slots = m.T * m.k < m.ne ? m.T * m.k : m.ne;
   MoeGemvArgs gu{};
   gu.plan = m.plan;
