@@ -36,8 +36,8 @@ constexpr float kTwo20 = 1048576.f;
 
 // LDS tables some codecs use; filled once per workgroup by init_lds.
 struct Lds {
-  uint32_t grid16[256][4];   // IQ2_XXS grid entries as four fp16-subnormal byte pairs
-  uint32_t signs16[128][4];  // IQ2_XXS sign patterns as fp16 sign-bit masks, same pairing
+  uint2 grid8[256];   // IQ2_XXS grid entries: 8 value bytes (8, 25 or 43)
+  uint2 signs8[128];  // IQ2_XXS sign patterns: 8 bytes, 0x80 where the value is negated
 };
 
 // ---------------------------------------------------------------------------- Q4_K
@@ -423,12 +423,13 @@ struct IQ2XXS {
     for (int l = 0; l < 4; l++) {
       const uint32_t gi = (aux.x >> (8 * l)) & 0xFF;
       const uint32_t si = (aux.y >> (7 * l)) & 127;
-      const uint4 g = *reinterpret_cast<const uint4 *>(lds.grid16[gi]);
-      const uint4 s = *reinterpret_cast<const uint4 *>(lds.signs16[si]);
-      w.p[4 * l + 0] = g.x | s.x;
-      w.p[4 * l + 1] = g.y | s.y;
-      w.p[4 * l + 2] = g.z | s.z;
-      w.p[4 * l + 3] = g.w | s.w;
+      const uint2 g = lds.grid8[gi], sg = lds.signs8[si];
+      // fp16 pairs (value bytes a, b as subnormals, sign bytes as their high bytes):
+      // bytes [g_a, s_a, g_b, s_b] for the pairs (0,2) (1,3) of each half
+      w.p[4 * l + 0] = __builtin_amdgcn_perm(sg.x, g.x, 0x06020400u);
+      w.p[4 * l + 1] = __builtin_amdgcn_perm(sg.x, g.x, 0x07030501u);
+      w.p[4 * l + 2] = __builtin_amdgcn_perm(sg.y, g.y, 0x06020400u);
+      w.p[4 * l + 3] = __builtin_amdgcn_perm(sg.y, g.y, 0x07030501u);
     }
   }
 
@@ -450,25 +451,19 @@ struct IQ2XXS {
     return w.db * a;
   }
 
-  // Grid entries as subnormal-half pairs (bytes 0,2 | 1,3 | 4,6 | 5,7) and the 128 sign
-  // patterns (ksigns_iq2xs: index plus an even-parity bit) as sign-bit masks on the same pairs.
+  // The grid entries as their 8 value bytes and the 128 sign patterns (ksigns_iq2xs: index plus
+  // an even-parity bit) as 8 bytes of 0x80 / 0x00; unpack merges them into fp16 pairs.
   __device__ static void init_lds(Lds &lds) {
     for (int i = threadIdx.x; i < 256; i += blockDim.x) {
       uint32_t b[8];
       for (int j = 0; j < 8; j++) b[j] = iq2_code_byte((kIq2xxsCodes[i] >> (2 * j)) & 3);
-      lds.grid16[i][0] = b[0] | b[2] << 16;
-      lds.grid16[i][1] = b[1] | b[3] << 16;
-      lds.grid16[i][2] = b[4] | b[6] << 16;
-      lds.grid16[i][3] = b[5] | b[7] << 16;
+      lds.grid8[i] = make_uint2(b[0] | b[1] << 8 | b[2] << 16 | b[3] << 24, b[4] | b[5] << 8 | b[6] << 16 | b[7] << 24);
     }
     for (int i = threadIdx.x; i < 128; i += blockDim.x) {
-      const uint32_t s = (uint32_t)i | ((uint32_t)(__builtin_popcount(i) & 1) << 7);
+      const uint32_t sg = (uint32_t)i | ((uint32_t)(__builtin_popcount(i) & 1) << 7);
       uint32_t m[8];
-      for (int j = 0; j < 8; j++) m[j] = ((s >> j) & 1) ? 0x8000u : 0u;
-      lds.signs16[i][0] = m[0] | m[2] << 16;
-      lds.signs16[i][1] = m[1] | m[3] << 16;
-      lds.signs16[i][2] = m[4] | m[6] << 16;
-      lds.signs16[i][3] = m[5] | m[7] << 16;
+      for (int j = 0; j < 8; j++) m[j] = ((sg >> j) & 1) ? 0x80u : 0u;
+      lds.signs8[i] = make_uint2(m[0] | m[1] << 8 | m[2] << 16 | m[3] << 24, m[4] | m[5] << 8 | m[6] << 16 | m[7] << 24);
     }
   }
 };
