@@ -38,6 +38,7 @@ constexpr float kTwo20 = 1048576.f;
 struct Lds {
   uint2 grid8[256];   // IQ2_XXS grid entries: 8 value bytes (8, 25 or 43)
   uint2 signs8[128];  // IQ2_XXS sign patterns: 8 bytes, 0x80 where the value is negated
+  uint32_t iq4[256];  // IQ4_XS qs byte -> (kvalue[low nibble] + 128, kvalue[high nibble] + 128) as fp16 pair
 };
 
 // ---------------------------------------------------------------------------- Q4_K
@@ -298,8 +299,11 @@ struct Q80 {
 
 // -------------------------------------------------------------------------- IQ4_XS
 // Lane slice: sub-block ib = sub (32 values, 16 bytes of qs).
+#ifndef WL_IQ4XS_LDS
+#define WL_IQ4XS_LDS 1
+#endif
 struct IQ4XS {
-  static constexpr int BLOCK = 256, BYTES = 136, LPB = 8, NEED_LDS = 0, R1 = 8, SP2 = 1;
+  static constexpr int BLOCK = 256, BYTES = 136, LPB = 8, NEED_LDS = WL_IQ4XS_LDS, R1 = 8, SP2 = 1;
   struct Lane { int ib; };
   struct Xs { float v[32]; float s; };
   struct Raw { uint2 hdr, q01, q23; };
@@ -346,7 +350,7 @@ struct IQ4XS {
     return (hi & m) | (lo & ~m);
   }
 
-  __device__ static void unpack(const Raw &r, const Lane &L, const Lds &, W &w) {
+  __device__ static void unpack(const Raw &r, const Lane &L, const Lds &lds, W &w) {
     const uint2 hdr = r.hdr;
     const int ib = L.ib;
     const float d = half_lo(hdr.x);
@@ -354,32 +358,52 @@ struct IQ4XS {
     const int ls = (int)((hdr.y >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xF) | (int)(((scales_h >> (2 * ib)) & 3) << 4);
     w.dl = d * (float)(ls - 32);  // src/IQuants.cs:71-72
     const uint32_t qq[4] = {r.q01.x, r.q01.y, r.q23.x, r.q23.y};
+    if constexpr (NEED_LDS) {
+      // qs byte k: its low nibble is value k, its high nibble value 16+k; one table read gives both
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      // qs byte 4i+k: low nibble -> value 4i+k, high nibble -> value 16+4i+k
-      const uint32_t lo = lookup(qq[i] & 0x0F0F0F0Fu);
-      const uint32_t hi = lookup((qq[i] >> 4) & 0x0F0F0F0Fu);
-      w.p[2 * i] = lo & 0x00FF00FFu;
-      w.p[2 * i + 1] = (lo >> 8) & 0x00FF00FFu;
-      w.p[8 + 2 * i] = hi & 0x00FF00FFu;
-      w.p[8 + 2 * i + 1] = (hi >> 8) & 0x00FF00FFu;
+      for (int k = 0; k < 16; k++) w.p[k] = lds.iq4[(qq[k >> 2] >> (8 * (k & 3))) & 0xFF];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        // qs byte 4i+k: low nibble -> value 4i+k, high nibble -> value 16+4i+k
+        const uint32_t lo = lookup(qq[i] & 0x0F0F0F0Fu);
+        const uint32_t hi = lookup((qq[i] >> 4) & 0x0F0F0F0Fu);
+        w.p[2 * i] = lo & 0x00FF00FFu;
+        w.p[2 * i + 1] = (lo >> 8) & 0x00FF00FFu;
+        w.p[8 + 2 * i] = hi & 0x00FF00FFu;
+        w.p[8 + 2 * i + 1] = (hi >> 8) & 0x00FF00FFu;
+      }
     }
   }
 
   __device__ static float dot(const W &w, const Xs &x) {
     float a = 0.f;
+    if constexpr (NEED_LDS) {
 #pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float *xv = x.v + 16 * h + 4 * i;
-        a = fma_lo(w.p[8 * h + 2 * i], xv[0], a);
-        a = fma_hi(w.p[8 * h + 2 * i], xv[2], a);
-        a = fma_lo(w.p[8 * h + 2 * i + 1], xv[1], a);
-        a = fma_hi(w.p[8 * h + 2 * i + 1], xv[3], a);
+      for (int k = 0; k < 16; k++) {
+        a = fma_lo(w.p[k], x.v[k], a);
+        a = fma_hi(w.p[k], x.v[16 + k], a);
       }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float *xv = x.v + 16 * h + 4 * i;
+          a = fma_lo(w.p[8 * h + 2 * i], xv[0], a);
+          a = fma_hi(w.p[8 * h + 2 * i], xv[2], a);
+          a = fma_lo(w.p[8 * h + 2 * i + 1], xv[1], a);
+          a = fma_hi(w.p[8 * h + 2 * i + 1], xv[3], a);
+        }
+    }
     // dl * sum(kv*x) = dl * (sum((kv+128)*x) - 128*sum(x))
     return w.dl * __builtin_fmaf(-128.f, x.s, a);
+  }
+
+  // byte b -> fp16 pair (kvalues[b & 15] + 128, kvalues[b >> 4] + 128) as subnormals
+  __device__ static void init_lds(Lds &lds) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x)
+      lds.iq4[i] = (uint32_t)(kKvaluesIq4nl[i & 15] + 128) | (uint32_t)(kKvaluesIq4nl[i >> 4] + 128) << 16;
   }
 };
 
