@@ -105,12 +105,83 @@ inline size_t cs_lds_bytes(int nwv) {
   return (C::NEED_LDS ? sizeof(Lds) : 0) + sizeof(float) * 2 * GS * nwv * NM * R * TM;
 }
 
+// The weights of row group g for block column b: R rows of each of the NM matrices. Rows past
+// the end re-read the last row (valid memory); their results are dropped.
+template <class C, int R, int NM>
+__device__ __forceinline__ void cs_load(const CsRows &W, int g, int b, const typename C::Lane &L,
+                                        typename C::Raw (&raw)[NM][R]) {
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int row = min(g * R + r, W.rows - 1);
+      C::load((m ? W.w2 : W.w) + (int64_t)row * W.row_bytes + (int64_t)b * C::BYTES, L, raw[m][r]);
+    }
+}
+
+// Where the wave results of the buffered groups go, and which group the buffer starts at.
+struct CsSlots {
+  int buf, slot, gfirst;
+};
+
+// Folds row group g's lane partials over the wave into LDS slot `slot` of buffer `buf`. Every
+// GS groups (and after the last) one barrier, then wave 0 finishes the buffered groups while
+// the other waves go on into the other buffer. g and the slot state are uniform over the
+// workgroup, so every wave takes the same branches.
+template <int TM, int R, int NM>
+__device__ __forceinline__ void cs_finish(const float (&acc)[NM][R][TM], int g, int gstride, int ngroups,
+                                          CsSlots &st, float *part, const CsRows &W, const CsIO &io) {
+  constexpr int V = NM * R * TM;
+  constexpr int LOW = 6 - ilog2(V);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  // value index v = (m*TM + t)*R + r
+  float vals[V];
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+      for (int r = 0; r < R; r++) vals[(m * TM + t) * R + r] = acc[m][r][t];
+  const float q = exch_reduce<V, 5>(vals, lane);
+  if ((lane & ((1 << LOW) - 1)) == 0) part[((st.buf * GS + st.slot) * nwv + wv) * V + (lane >> LOW)] = q;
+  if (st.slot + 1 < GS && g + gstride < ngroups) {
+    st.slot++;
+    return;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    for (int i = lane; i < (st.slot + 1) * R * TM; i += 64) {
+      const int sl = i / (R * TM), rt = i % (R * TM);
+      const int r = rt % R, t = rt / R;
+      const int row = (st.gfirst + sl * gstride) * R + r;
+      if (t < io.T && row < W.rows) {
+        const float *pb = part + (st.buf * GS + sl) * nwv * V;
+        float s = pb[t * R + r];
+        for (int w = 1; w < nwv; w++) s += pb[w * V + t * R + r];
+        const int64_t o = (int64_t)(io.yrow ? io.yrow[t] : t) * io.ldy + row;
+        if constexpr (NM == 2) {
+          float s1 = pb[(TM + t) * R + r];
+          for (int w = 1; w < nwv; w++) s1 += pb[w * V + (TM + t) * R + r];
+          if (io.y2) {
+            io.y2[o] = s1;
+          } else {
+            s = silu_mul(s, s1);
+          }
+        }
+        io.y[o] = s;
+      }
+    }
+  }
+  st.buf ^= 1;
+  st.slot = 0;
+  st.gfirst = g + gstride;
+}
+
 // SP: passes whose x slices stay in registers (0: x read per row group; 1 or 2 only for TM 1).
 template <class C, int TM, int R, int NM, int SP>
 __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int cols, int g0, int gstride,
                                         uint8_t *lds_raw) {
   constexpr int V = NM * R * TM;
-  constexpr int LOW = 6 - ilog2(V);
   static_assert((1 << ilog2(V)) == V && V <= 64, "partials per lane must be a power of two <= 64");
   static_assert(SP == 0 || TM == 1, "stationary x slices are for one token");
   constexpr int BPW = 64 / C::LPB;
@@ -122,11 +193,12 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
   const int nb = cols / C::BLOCK;
   const int npass = (nb + nwv * BPW - 1) / (nwv * BPW);
   const int ngroups = (W.rows + R - 1) / R;
-  const uint8_t *wm[2] = {W.w, W.w2};
 
   const float *xr[TM];
 #pragma unroll
   for (int t = 0; t < TM; t++) xr[t] = io.x + (int64_t)(io.xrow ? io.xrow[t < io.T ? t : 0] : t) * io.ldx;
+
+  CsSlots st{0, 0, g0};
 
   // x slices of the stationary passes, read once
   typename C::Xs xs0[SP > 0 ? SP : 1];
@@ -141,10 +213,6 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
     __syncthreads();
   }
 
-  // Reduced group results go to LDS slot `slot` of buffer `buf`; every GS groups (and after the
-  // last) one barrier, then wave 0 finishes the buffered groups while the other waves go on
-  // into the other buffer.
-  int buf = 0, slot = 0, gfirst = g0;
   for (int g = g0; g < ngroups; g += gstride) {
     float acc[NM][R][TM];
 #pragma unroll
@@ -158,14 +226,7 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
       const int b = (p * nwv + wv) * BPW + bslot;
       if (b < nb) {
         typename C::Raw raw[NM][R];
-#pragma unroll
-        for (int m = 0; m < NM; m++)
-#pragma unroll
-          for (int r = 0; r < R; r++) {
-            // rows past the end re-read the last row (valid memory); their results are dropped
-            const int row = min(g * R + r, W.rows - 1);
-            C::load(wm[m] + (int64_t)row * W.row_bytes + (int64_t)b * C::BYTES, L, raw[m][r]);
-          }
+        cs_load<C, R, NM>(W, g, b, L, raw);
         if constexpr (TM == 1) {
           typename C::Xs xs;
           if constexpr (SP == 1) xs = xs0[0];
@@ -199,48 +260,7 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
         }
       }
     }
-
-    // value index v = (m*TM + t)*R + r
-    float vals[V];
-#pragma unroll
-    for (int m = 0; m < NM; m++)
-#pragma unroll
-      for (int t = 0; t < TM; t++)
-#pragma unroll
-        for (int r = 0; r < R; r++) vals[(m * TM + t) * R + r] = acc[m][r][t];
-    const float q = exch_reduce<V, 5>(vals, lane);
-    if ((lane & ((1 << LOW) - 1)) == 0) part[((buf * GS + slot) * nwv + wv) * V + (lane >> LOW)] = q;
-    if (slot + 1 < GS && g + gstride < ngroups) {  // uniform over the workgroup
-      slot++;
-      continue;
-    }
-    __syncthreads();
-    if (wv == 0) {
-      for (int i = lane; i < (slot + 1) * R * TM; i += 64) {
-        const int sl = i / (R * TM), rt = i % (R * TM);
-        const int r = rt % R, t = rt / R;
-        const int row = (gfirst + sl * gstride) * R + r;
-        if (t < io.T && row < W.rows) {
-          const float *pb = part + (buf * GS + sl) * nwv * V;
-          float s = pb[t * R + r];
-          for (int w = 1; w < nwv; w++) s += pb[w * V + t * R + r];
-          const int64_t o = (int64_t)(io.yrow ? io.yrow[t] : t) * io.ldy + row;
-          if constexpr (NM == 2) {
-            float s1 = pb[(TM + t) * R + r];
-            for (int w = 1; w < nwv; w++) s1 += pb[w * V + (TM + t) * R + r];
-            if (io.y2) {
-              io.y2[o] = s1;
-            } else {
-              s = silu_mul(s, s1);
-            }
-          }
-          io.y[o] = s;
-        }
-      }
-    }
-    buf ^= 1;
-    slot = 0;
-    gfirst = g + gstride;
+    cs_finish<TM, R, NM>(acc, g, gstride, ngroups, st, part, W, io);
   }
 }
 
