@@ -59,6 +59,10 @@ int wl_can_decode(int ggml_type);
  * wl_matmul handles the type (the I-quants included, which the CPU path decodes first). */
 int wl_can_matmul(int ggml_type);
 
+/* FastMath.CanIntDot (src/FastMath.cs:27-30) for the formats this library has: 1 for Q8_0,
+ * Q4_K and Q6_K (the reference also lists Q4_0 and Q5_K, which this build does not carry). */
+int wl_can_int_dot(int ggml_type);
+
 /* Block geometry, GgmlTypes.TryGetLayout (src/Gguf.cs:30-66). Returns 1 when known. */
 int wl_type_layout(int ggml_type, int *block_elems, int *block_bytes);
 
@@ -112,7 +116,27 @@ int wl_moe_ffn(wl_ctx *ctx, const float *logits, int32_t k, int32_t renorm,
                const wl_weight *gate_exps, const wl_weight *up_exps, const wl_weight *down_exps,
                const float *x, int32_t T, float *out, int32_t *expert_runs);
 
+/* Transformer.IntDot (src/Transformer.cs:23), set from --int-dot (src/Program.cs:50,215;
+ * EngineOptions.IntDot, src/Engine.cs:22,70). Off by default. When on, wl_matmul(_dev), the
+ * fused q/k/v entry and the SwiGLU entries multiply wl_can_int_dot weights whose rows are whole
+ * activation blocks (FastMath.Fits, src/FastMath.cs:34) with the integer branch of MatMul
+ * (src/Transformer.cs:504-524): the T rows of x are quantized once (FastMath.Quantize), then
+ * y[t][r] = FastMath.IntDot(W[r], activations of t) (src/FastMath.cs:105-214), bit-identical to
+ * the reference for every T. MoE experts keep the float path. */
+int wl_set_int_dot(wl_ctx *ctx, int on);
+
+/* FastMath.Quantize (src/FastMath.cs:35-91) of x [T][cols], bit-identical: k = 0 gives Q8_0
+ * activations (q int8 [T][cols], d [T][cols/32] rounded through fp16; bsums unused, may be
+ * NULL), k = 1 Q8_K (d [T][cols/256], bsums int16 [T][cols/16], the sums of every 16 quants).
+ * cols must be whole blocks. Synchronous. */
+int wl_quantize(wl_ctx *ctx, const float *x, int32_t T, int32_t cols, int32_t k, int8_t *q, float *d,
+                int16_t *bsums);
+
 /* ---- device-pointer variants (activations resident in HBM), asynchronous ---------- */
+
+/* wl_quantize on device buffers. */
+int wl_quantize_dev(wl_ctx *ctx, const float *d_x, int32_t T, int32_t cols, int32_t k, int8_t *d_q,
+                    float *d_d, int16_t *d_bsums);
 
 /* wl_matmul on device buffers d_x [T][cols], d_y [T][rows]. */
 int wl_matmul_dev(wl_ctx *ctx, const wl_weight *w, int32_t expert, const float *d_x, int32_t T,

@@ -10,6 +10,9 @@ libwindlass_hip.so (include/windlass_hip.h):
 - ``Transformer.SwiGlu``          src/Transformer.cs:241-251
 - ``Transformer.Route``           src/Transformer.cs:315-340
 - ``Transformer.MoeFfn``          src/Transformer.cs:259-294 (router logits given)
+- ``Context.IntDot``              Transformer.IntDot (src/Transformer.cs:23), the integer branch
+                                  of MatMul (src/Transformer.cs:504-524)
+- ``FastMath``                    CanIntDot/NeedsK/Fits/Quantize (src/FastMath.cs:27-91)
 
 Errors map to the reference's exception kinds: ``NotSupportedError`` (NotSupportedException),
 ``ShapeError`` (ArgumentException), ``ArgumentOutOfRangeError``, ``BackendError`` (device
@@ -17,8 +20,8 @@ failure). There is no CPU fallback: without the built library every call raises.
 """
 from ._lib import (ArgumentOutOfRangeError, BackendError, NotSupportedError, ShapeError,
                    library_path, load)
-from .backend import Context, GgmlType, Quants, Transformer, WeightView, layout
+from .backend import Context, FastMath, GgmlType, QActs, Quants, Transformer, WeightView, layout
 
 __all__ = ["ArgumentOutOfRangeError", "BackendError", "NotSupportedError", "ShapeError",
-           "library_path", "load", "Context", "GgmlType", "Quants", "Transformer",
-           "WeightView", "layout"]
+           "library_path", "load", "Context", "FastMath", "GgmlType", "QActs", "Quants",
+           "Transformer", "WeightView", "layout"]

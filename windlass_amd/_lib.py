@@ -13,6 +13,7 @@ SIGNATURES = {
     "wl_last_error": (ctypes.c_char_p, []),
     "wl_can_decode": (ctypes.c_int, [ctypes.c_int]),
     "wl_can_matmul": (ctypes.c_int, [ctypes.c_int]),
+    "wl_can_int_dot": (ctypes.c_int, [ctypes.c_int]),
     "wl_type_layout": (ctypes.c_int, [ctypes.c_int, P, P]),
     "wl_create": (ctypes.c_int, [ctypes.c_int, PP]),
     "wl_destroy": (None, [P]),
@@ -25,6 +26,9 @@ SIGNATURES = {
     "wl_swiglu": (ctypes.c_int, [P, P, P, P, I32, P, I32, P]),
     "wl_route": (ctypes.c_int, [P, P, I32, I32, I32, I32, P, P]),
     "wl_moe_ffn": (ctypes.c_int, [P, P, I32, I32, P, P, P, P, I32, P, P]),
+    "wl_set_int_dot": (ctypes.c_int, [P, ctypes.c_int]),
+    "wl_quantize": (ctypes.c_int, [P, P, I32, I32, I32, P, P, P]),
+    "wl_quantize_dev": (ctypes.c_int, [P, P, I32, I32, I32, P, P, P]),
     "wl_matmul_dev": (ctypes.c_int, [P, P, I32, P, I32, P]),
     "wl_matmul_multi_dev": (ctypes.c_int, [P, I32, P, P, I32, P]),
     "wl_gate_up_dev": (ctypes.c_int, [P, P, P, I32, P, I32, P]),

@@ -48,6 +48,47 @@ def _ptr(a):
     return ctypes.c_void_p(a.ctypes.data)
 
 
+class QActs:
+    """Quantized activations of Rows x Cols values (FastMath.QActs, src/FastMath.cs:17-23)."""
+
+    def __init__(self, k, rows, cols, q, d, bsums):
+        self.K, self.Rows, self.Cols, self.Q, self.D, self.Bsums = k, rows, cols, q, d, bsums
+
+
+class FastMath:
+    """The integer-dot helpers of src/FastMath.cs (activation quantizers and type checks)."""
+
+    @staticmethod
+    def CanIntDot(t):
+        """src/FastMath.cs:27-30, for the formats this library carries (Q8_0, Q4_K, Q6_K)."""
+        return bool(load().wl_can_int_dot(int(t)))
+
+    @staticmethod
+    def NeedsK(t):
+        """src/FastMath.cs:32: the weights take Q8_K activations."""
+        return int(t) in (GgmlType.Q4_K, GgmlType.Q6_K)
+
+    @staticmethod
+    def Fits(t, cols):
+        """src/FastMath.cs:34: a row is whole activation blocks."""
+        return cols % (256 if FastMath.NeedsK(t) else 32) == 0
+
+    @staticmethod
+    def Quantize(ctx, x, rows, cols, k):
+        """src/FastMath.cs:35-91 on the GPU: x [rows][cols] to Q8_0 (k False) or Q8_K (k True)
+        activations, bit-identical to the reference."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        bs = 256 if k else 32
+        if x.size != rows * cols or cols % bs:
+            raise ShapeError("Quantize: %d values are not %d rows of whole %d-value blocks" % (x.size, rows, bs))
+        q = np.empty(rows * cols, np.int8)
+        d = np.empty(rows * (cols // bs), np.float32)
+        bsums = np.empty(rows * (cols // 16), np.int16) if k else None
+        check(load().wl_quantize(ctx.handle, _ptr(x), rows, cols, int(bool(k)), _ptr(q), _ptr(d),
+                                 _ptr(bsums) if k else None))
+        return QActs(bool(k), rows, cols, q, d, bsums)
+
+
 class Context:
     """One GPU context per model (a HIP stream plus scratch), wl_create/wl_destroy."""
 
@@ -80,6 +121,17 @@ class Context:
 
     def sync(self):
         check(self._lib.wl_sync(self.handle))
+
+    @property
+    def IntDot(self):
+        """Transformer.IntDot (src/Transformer.cs:23): integer dot products with 8-bit
+        activations for the matrices that have an integer kernel. Off by default."""
+        return getattr(self, "_int_dot", False)
+
+    @IntDot.setter
+    def IntDot(self, on):
+        check(self._lib.wl_set_int_dot(self.handle, int(bool(on))))
+        self._int_dot = bool(on)
 
     def upload(self, t, blocks, rows, cols, experts=1, name="weight"):
         """Raw GGUF blocks to HBM, unchanged (LayerStream.Bind, src/LayerStream.cs:182-203)."""

@@ -14,6 +14,7 @@
 #include "wl_dequant.h"
 #include "wl_gemm.h"
 #include "wl_gemv.h"
+#include "wl_intdot.h"
 #include "wl_moe.h"
 
 // Bytes of padding after every weight buffer: the GEMV reads the aligned dwords around
@@ -30,17 +31,20 @@ struct wl_weight {
   size_t bytes;  // rows * experts * row_bytes
 };
 
+// S_PART holds the K-chunk partials of split GEMV rows, S_XB the bf16 copy of x for the GEMM,
+// S_QA the 8-bit activations of the integer path, S_TERMS its per-block terms and S_U the up
+// projection of an integer SwiGLU.
+enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB, S_QA, S_TERMS, S_U, S_COUNT };
+
 struct wl_ctx {
   int device;
   int num_cu;
   hipStream_t stream;
+  int int_dot;  // Transformer.IntDot (src/Transformer.cs:23)
   // growable scratch (device)
-  void *buf[8];
-  size_t cap[8];
+  void *buf[S_COUNT];
+  size_t cap[S_COUNT];
 };
-
-// S_PART holds the K-chunk partials of split GEMV rows, S_XB the bf16 copy of x for the GEMM.
-enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB };
 
 static thread_local std::string g_err;
 
@@ -101,6 +105,8 @@ extern "C" const char *wl_last_error(void) { return g_err.c_str(); }
 extern "C" int wl_can_decode(int t) { return wl::dequant_supports(t) ? 1 : 0; }
 
 extern "C" int wl_can_matmul(int t) { return wl::gemv_supports(t) ? 1 : 0; }
+
+extern "C" int wl_can_int_dot(int t) { return wl::intdot_supports(t) ? 1 : 0; }
 
 static int ensure(wl_ctx *c, int slot, size_t bytes) {
   if (c->cap[slot] >= bytes) return WL_OK;
@@ -235,6 +241,36 @@ static int gemv(wl_ctx *c, const wl::GemvMat *mats, int nmat, int nm, const floa
   return WL_OK;
 }
 
+// The integer path runs when it is switched on and the weight has an integer kernel whose
+// activation blocks fit the row (src/Transformer.cs:493).
+static bool int_path(const wl_ctx *c, const wl_weight *w) {
+  return c->int_dot && wl::intdot_supports(w->type) && wl::intdot_fits(w->type, (int)w->cols);
+}
+
+// Transformer.MatMul's integer branch (src/Transformer.cs:504-524): quantize the T rows of x
+// once, then every (row, token) is FastMath.IntDot, in passes of up to 8 tokens.
+static int intdot_matmul(wl_ctx *c, const wl_weight *w, const uint8_t *base, int64_t rows, const float *d_x, int T,
+                         float *d_y) {
+  const int cols = (int)w->cols, k = wl::intdot_needs_k(w->type) ? 1 : 0;
+  int rc;
+  if ((rc = ensure(c, S_QA, (size_t)wl::qacts_bytes(T, cols, k)))) return rc;
+  const int tp = T < 8 ? T : 8;
+  if ((rc = ensure(c, S_TERMS, (size_t)wl::intdot_terms_floats(w->type, (int)rows, cols, tp) * sizeof(float))))
+    return rc;
+  const wl::QActsDev qa = wl::qacts_at(c->buf[S_QA], T, cols, k);
+  WL_HIP(wl::quantize_launch(d_x, T, cols, k, qa, c->stream), "quantize launch");
+  const int ab = k ? 256 : 32;
+  for (int t0 = 0; t0 < T; t0 += 8) {
+    const int n = T - t0 < 8 ? T - t0 : 8;
+    const wl::QActsDev at{qa.q + (int64_t)t0 * cols, qa.d + (int64_t)t0 * (cols / ab),
+                          qa.bsums ? qa.bsums + (int64_t)t0 * (cols / 16) : nullptr};
+    WL_HIP(wl::intdot_launch(w->type, base, w->row_bytes, (int)rows, cols, at, n, (float *)c->buf[S_TERMS],
+                             d_y + (int64_t)t0 * rows, (int)rows, c->num_cu, c->stream),
+           "int dot launch");
+  }
+  return WL_OK;
+}
+
 static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float *d_x, int32_t T, float *d_y) {
   if (!c || !w || !d_x || !d_y) return fail(WL_E_ARG, "matmul: null argument");
   int rc = check_expert(w, expert);
@@ -245,6 +281,7 @@ static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float
   const uint8_t *base;
   int64_t rows;
   operand(w, expert, &base, &rows);
+  if (int_path(c, w)) return intdot_matmul(c, w, base, rows, d_x, T, d_y);
   if (T > 8 && wl::gemm_supports(w->type)) {
     if ((rc = ensure(c, S_XB, (size_t)wl::gemm_scratch_bytes((int)rows, (int)w->cols, T, c->num_cu)))) return rc;
     WL_HIP(wl::gemm_launch(w->type, base, w->row_bytes, (int)rows, (int)w->cols, d_x, T, d_y, (int)rows,
@@ -297,7 +334,9 @@ extern "C" int wl_matmul_multi_dev(wl_ctx *c, int32_t n, const wl_weight *const 
     same = same && ws[i]->type == ws[0]->type;
     mixed_ok = mixed_ok && wl::gemv_mixed_supports(ws[i]->type);
   }
-  if (!same && !mixed_ok) {
+  bool any_int = false;
+  for (int i = 0; i < n; i++) any_int = any_int || int_path(c, ws[i]);
+  if (any_int || (!same && !mixed_ok)) {
     for (int i = 0; i < n; i++) {
       int rc = matmul_dev(c, ws[i], -1, d_x, T, d_ys[i]);
       if (rc) return rc;
@@ -328,6 +367,15 @@ extern "C" int wl_gate_up_dev(wl_ctx *c, const wl_weight *gate, const wl_weight 
   int64_t rows;
   operand(gate, expert, &gb, &rows);
   operand(up, expert, &ub, &rows);
+  if (int_path(c, gate)) {
+    // SwiGlu on the integer kernels: g = gate x, u = up x, then g / (1 + exp(-g)) * u
+    if ((rc = ensure(c, S_U, (size_t)T * rows * sizeof(float)))) return rc;
+    float *d_u = (float *)c->buf[S_U];
+    if ((rc = intdot_matmul(c, gate, gb, rows, d_x, T, d_h)) || (rc = intdot_matmul(c, up, ub, rows, d_x, T, d_u)))
+      return rc;
+    WL_HIP(wl::silu_mul_launch(d_h, d_u, (int64_t)T * rows, c->stream), "silu launch");
+    return WL_OK;
+  }
   for (int t0 = 0; t0 < T; t0 += 8) {
     const wl::GemvMat m{gb, ub, gate->row_bytes, (int)rows, gate->type, d_h + (int64_t)t0 * rows, (int)rows};
     const int Tp = T - t0 < 8 ? T - t0 : 8;
@@ -500,5 +548,44 @@ extern "C" int wl_moe_ffn(wl_ctx *c, const float *logits, int32_t k, int32_t ren
   WL_HIP(hipMemcpyAsync(out, c->buf[S_OUT], xb, hipMemcpyDeviceToHost, c->stream), "copy out");
   WL_HIP(hipStreamSynchronize(c->stream), "moe");
   if (expert_runs) *expert_runs = runs;
+  return WL_OK;
+}
+
+// ----------------------------------------------------------------------------- integer path
+
+extern "C" int wl_set_int_dot(wl_ctx *c, int on) {
+  if (!c) return fail(WL_E_ARG, "wl_set_int_dot: null context");
+  c->int_dot = on ? 1 : 0;
+  return WL_OK;
+}
+
+extern "C" int wl_quantize_dev(wl_ctx *c, const float *d_x, int32_t T, int32_t cols, int32_t k, int8_t *d_q,
+                               float *d_d, int16_t *d_bsums) {
+  if (!c || !d_x || !d_q || !d_d || (k && !d_bsums)) return fail(WL_E_ARG, "wl_quantize_dev: null argument");
+  if (T < 0 || cols <= 0 || cols % (k ? 256 : 32))
+    return fail(WL_E_SHAPE, "Quantize: %d columns are not whole %d-value blocks", cols, k ? 256 : 32);
+  WL_HIP(wl::quantize_launch(d_x, T, cols, k ? 1 : 0, wl::QActsDev{d_q, d_d, d_bsums}, c->stream), "quantize launch");
+  return WL_OK;
+}
+
+extern "C" int wl_quantize(wl_ctx *c, const float *x, int32_t T, int32_t cols, int32_t k, int8_t *q, float *d,
+                           int16_t *bsums) {
+  if (!c || !x || !q || !d || (k && !bsums)) return fail(WL_E_ARG, "wl_quantize: null argument");
+  if (T < 0 || cols <= 0 || cols % (k ? 256 : 32))
+    return fail(WL_E_SHAPE, "Quantize: %d columns are not whole %d-value blocks", cols, k ? 256 : 32);
+  if (T == 0) return WL_OK;
+  const int kk = k ? 1 : 0, bs = kk ? 256 : 32;
+  const size_t xb = (size_t)T * cols * 4;
+  int rc;
+  if ((rc = ensure(c, S_X, xb)) || (rc = ensure(c, S_QA, (size_t)wl::qacts_bytes(T, cols, kk)))) return rc;
+  const wl::QActsDev qa = wl::qacts_at(c->buf[S_QA], T, cols, kk);
+  WL_HIP(hipMemcpyAsync(c->buf[S_X], x, xb, hipMemcpyHostToDevice, c->stream), "copy x");
+  WL_HIP(wl::quantize_launch((const float *)c->buf[S_X], T, cols, kk, qa, c->stream), "quantize launch");
+  WL_HIP(hipMemcpyAsync(q, qa.q, (size_t)T * cols, hipMemcpyDeviceToHost, c->stream), "copy q");
+  WL_HIP(hipMemcpyAsync(d, qa.d, (size_t)T * (cols / bs) * 4, hipMemcpyDeviceToHost, c->stream), "copy d");
+  if (kk)
+    WL_HIP(hipMemcpyAsync(bsums, qa.bsums, (size_t)T * (cols / 16) * 2, hipMemcpyDeviceToHost, c->stream),
+           "copy bsums");
+  WL_HIP(hipStreamSynchronize(c->stream), "quantize");
   return WL_OK;
 }

@@ -1,0 +1,444 @@
+// wl_intdot.hip - the integer-dot path of Transformer.MatMul (src/Transformer.cs:504-524).
+//
+// Quantize: one wave per 256 activations (four per lane). Q8_0 takes the block's |x| maximum
+// over 8 lanes; Q8_K finds the value of largest magnitude, the first one on ties as the
+// reference's strict scan does, by a wave-wide (|x| descending, index ascending) selection.
+// The roundings are the reference's: x * id rounded half away from zero (Q8_0), iscale * x
+// rounded half to even and clamped at 127 (Q8_K), d = amax / 127 rounded through fp16, d =
+// 1 / iscale (correctly rounded divisions).
+//
+// Dot products: the float GEMV's lane slices and block loads (wl_codecs.h), with v_dot4_i32_i8
+// on the quant bytes and the 8-bit activations. A block's integer sums are exact whatever the
+// order, so its lanes add their partials with a butterfly; the block's leader lane forms the
+// block's float term with the reference's operations and writes it. A second launch adds each
+// row's terms in block order, which is the reference's `sum +=` loop, so y is bit-identical to
+// FastMath.IntDot. Waves never exchange data, so there is no barrier.
+#include "wl_intdot.h"
+
+#include "wl_codecs.h"
+#include "wl_gemv_impl.h"
+
+#pragma clang fp contract(off)
+
+namespace wl {
+
+bool intdot_supports(int t) { return t == 8 || t == 12 || t == 14; }
+bool intdot_needs_k(int t) { return t == 12 || t == 14; }
+bool intdot_fits(int t, int cols) { return cols > 0 && cols % (intdot_needs_k(t) ? 256 : 32) == 0; }
+
+static int64_t up16(int64_t n) { return (n + 15) / 16 * 16; }
+
+int64_t qacts_bytes(int T, int cols, int k) {
+  const int bs = k ? 256 : 32;
+  return up16((int64_t)T * cols) + up16((int64_t)T * (cols / bs) * 4) + (k ? (int64_t)T * (cols / 16) * 2 : 0);
+}
+
+QActsDev qacts_at(void *buf, int T, int cols, int k) {
+  const int bs = k ? 256 : 32;
+  uint8_t *p = static_cast<uint8_t *>(buf);
+  QActsDev a;
+  a.q = reinterpret_cast<int8_t *>(p);
+  p += up16((int64_t)T * cols);
+  a.d = reinterpret_cast<float *>(p);
+  p += up16((int64_t)T * (cols / bs) * 4);
+  a.bsums = k ? reinterpret_cast<int16_t *>(p) : nullptr;
+  return a;
+}
+
+// ------------------------------------------------------------------------------ quantize
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)(d & 0xFF) << 24);
+}
+
+// Wave w of the grid quantizes activations [256 c, 256 c + 256) of token t (w = t * nchunk + c).
+__global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__ x, int T, int cols, int k,
+                                                       int8_t *__restrict__ q, float *__restrict__ d,
+                                                       int16_t *__restrict__ bsums) {
+  const int lane = threadIdx.x & 63;
+  const int nchunk = (cols + 255) / 256;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gw >= (int64_t)T * nchunk) return;  // the whole wave
+  const int t = (int)(gw / nchunk), c = (int)(gw % nchunk);
+  const int base = 256 * c + 4 * lane;  // cols is a multiple of 32, so a lane's 4 values are all in or all out
+  const bool in = base < cols;
+  const float *xr = x + (int64_t)t * cols;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (in) {
+    const float4 f = *reinterpret_cast<const float4 *>(xr + base);
+    v[0] = f.x;
+    v[1] = f.y;
+    v[2] = f.z;
+    v[3] = f.w;
+  }
+  uint32_t *qw = reinterpret_cast<uint32_t *>(q + (int64_t)t * cols + base);
+  if (k == 0) {
+    // quantize_row_q8_0 (src/FastMath.cs:54-61): a block of 32 is 8 lanes
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float ax = fabsf(v[i]);
+      if (ax > amax) amax = ax;
+    }
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    const float dd = amax / 127.f, id = dd != 0.f ? 1.f / dd : 0.f;
+    int qi[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) qi[i] = (int)roundf(v[i] * id);  // Math.Round(.., AwayFromZero)
+    if (in) {
+      *qw = pack4(qi[0], qi[1], qi[2], qi[3]);
+      if ((lane & 7) == 0) d[(int64_t)t * (cols / 32) + base / 32] = (float)(_Float16)dd;  // Half.Round
+    }
+    return;
+  }
+  // quantize_row_q8_K (src/FastMath.cs:62-86): the first value of largest magnitude
+  float am = 0.f, mv = 0.f;
+  int mi = 0x7FFFFFFF;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float ax = fabsf(v[i]);
+    if (ax > am) {
+      am = ax;
+      mv = v[i];
+      mi = base + i;
+    }
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const float oa = __shfl_xor(am, m, 64), om = __shfl_xor(mv, m, 64);
+    const int oi = __shfl_xor(mi, m, 64);
+    if (oa > am || (oa == am && oi < mi)) {
+      am = oa;
+      mv = om;
+      mi = oi;
+    }
+  }
+  int qi[4] = {0, 0, 0, 0};
+  float iscale = 0.f;
+  if (am != 0.f) {
+    iscale = -127.f / mv;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r = (int)rintf(iscale * v[i]);  // Math.Round (to even)
+      qi[i] = r > 127 ? 127 : r;
+    }
+  }
+  int s = qi[0] + qi[1] + qi[2] + qi[3];  // bsums: 16 quants = 4 lanes
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  *qw = pack4(qi[0], qi[1], qi[2], qi[3]);
+  if ((lane & 3) == 0) bsums[(int64_t)t * (cols / 16) + base / 16] = (int16_t)s;
+  if (lane == 0) d[(int64_t)t * (cols / 256) + c] = am != 0.f ? 1.f / iscale : 0.f;
+}
+
+hipError_t quantize_launch(const float *x, int T, int cols, int k, QActsDev a, hipStream_t st) {
+  if (T <= 0 || cols <= 0) return hipSuccess;
+  if (cols % (k ? 256 : 32)) return hipErrorInvalidValue;
+  const int64_t waves = (int64_t)T * ((cols + 255) / 256);
+  hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, T, cols, k, a.q, a.d,
+                     a.bsums);
+  return hipGetLastError();
+}
+
+// ----------------------------------------------------------------------------- dot codecs
+// Per format, on the float codec's lane slice (Lane, Raw, load): Xq is the lane's share of one
+// token's activations; part() gives the lane's integer partials of one row's block (si, and
+// sm where the format has a min term); the block's lanes add them; term() is the leader's float.
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Q4_K (src/FastMath.cs:135-157). Lane (j, h): qs bytes 32j + 16h .. +16; low nibbles are
+// values 64j + 16h + i of sub-block 2j, high nibbles 64j + 32 + 16h + i of sub-block 2j+1.
+struct IQ4K {
+  using C = Q4K;
+  static constexpr int TERMS = 1;
+  struct Xq {
+    uint32_t a[4], b[4];
+    int B1, B2;  // bsums of the two sub-blocks (lane h = 0 only; 0 on h = 1 so the pair counts them once)
+    float d;
+  };
+  __device__ static void load_x(const int8_t *q, const float *d, const int16_t *bs, int blk, const C::Lane &L,
+                                Xq &x) {
+    const int8_t *qb = q + (int64_t)blk * 256 + 64 * L.j + 16 * L.h;
+    const uint4 a = *reinterpret_cast<const uint4 *>(qb);
+    const uint4 b = *reinterpret_cast<const uint4 *>(qb + 32);
+    x.a[0] = a.x, x.a[1] = a.y, x.a[2] = a.z, x.a[3] = a.w;
+    x.b[0] = b.x, x.b[1] = b.y, x.b[2] = b.z, x.b[3] = b.w;
+    const int16_t *s = bs + (int64_t)blk * 16 + 4 * L.j;
+    x.B1 = L.h ? 0 : s[0] + s[1];
+    x.B2 = L.h ? 0 : s[2] + s[3];
+    x.d = d[blk];
+  }
+  __device__ static void part(const C::Raw &r, const C::Lane &L, const Xq &x, int &si, int &sm) {
+    // the 6-bit scales and mins of sub-blocks 2j, 2j+1 (get_scale_min_k4, src/Quants.cs:321-330),
+    // decoded as in the float codec
+    const uint4 h = r.hdr;
+    const uint32_t P = L.jlo ? h.y : h.w;
+    const uint32_t Q = L.jlo ? h.z : (h.w >> 4);
+    const uint32_t S = ((P & L.m1) | ((h.y >> 2) & L.m2)) >> L.sh;
+    const uint32_t M = ((Q & L.m1) | ((h.z >> 2) & L.m2)) >> L.sh;
+    const uint32_t qq[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    int a1 = 0, a2 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      a1 = dot4(qq[i] & 0x0F0F0F0Fu, x.a[i], a1);
+      a2 = dot4((qq[i] >> 4) & 0x0F0F0F0Fu, x.b[i], a2);
+    }
+    si = (int)(S & 0xFF) * a1 + (int)((S >> 8) & 0xFF) * a2;
+    sm = (int)(M & 0xFF) * x.B1 + (int)((M >> 8) & 0xFF) * x.B2;
+  }
+  __device__ static void reduce(int &si, int &sm) {
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+      si += __shfl_xor(si, m, 64);
+      sm += __shfl_xor(sm, m, 64);
+    }
+  }
+  __device__ static bool leader(const C::Lane &L) { return L.j == 0 && L.h == 0; }
+  __device__ static int term_index(const C::Lane &) { return 0; }
+  __device__ static float term(const C::Raw &r, int si, int sm, const Xq &x) {
+    const float dd = half_lo(r.hdr.x), dmin = half_hi(r.hdr.x);
+    return x.d * (dd * (float)si - dmin * (float)sm);  // src/FastMath.cs:155
+  }
+};
+
+// Q6_K (src/FastMath.cs:185-211). Lane (hh, g): values 128 hh + 8g + 32k + (0..7), k < 4, of
+// scale group 2k + g/2 of half hh; that group's other 8 values are on lane g^1.
+struct IQ6K {
+  using C = Q6K;
+  static constexpr int TERMS = 2;  // one per half, in order
+  struct Xq {
+    uint32_t v[4][2];
+    int bsum[4];  // the group sums (lanes with even g only)
+    float d;
+  };
+  __device__ static void load_x(const int8_t *q, const float *d, const int16_t *bs, int blk, const C::Lane &L,
+                                Xq &x) {
+    const int8_t *qb = q + (int64_t)blk * 256 + 128 * L.hh + 8 * L.g;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint2 u = *reinterpret_cast<const uint2 *>(qb + 32 * k);
+      x.v[k][0] = u.x;
+      x.v[k][1] = u.y;
+      x.bsum[k] = (L.g & 1) ? 0 : bs[(int64_t)blk * 16 + 8 * L.hh + L.s + 2 * k];
+    }
+    x.d = d[blk];
+  }
+  __device__ static void part(const C::Raw &r, const C::Lane &L, const Xq &x, int &si, int &sm) {
+    const uint2 ql1 = C::field(r.l1, r.sh), ql2 = C::field(r.l2, r.sh), qh = C::field(r.h, r.sh),
+                sc = C::field(r.sc, r.sh);
+    const int s = L.s;
+    const int scs[4] = {(int)(int8_t)(sc.x >> (8 * s)), (int)(int8_t)(sc.x >> (8 * s + 16)),
+                        (int)(int8_t)(sc.y >> (8 * s)), (int)(int8_t)(sc.y >> (8 * s + 16))};
+    const uint32_t L1[2] = {ql1.x, ql1.y}, L2[2] = {ql2.x, ql2.y}, QH[2] = {qh.x, qh.y};
+    int p[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      // the 6-bit quants q (0..63) of values l, l+32, l+64, l+96 (src/Quants.cs:384-387)
+      const uint32_t a = (L1[i] & 0x0F0F0F0Fu) | ((QH[i] << 4) & 0x30303030u);
+      const uint32_t b = (L2[i] & 0x0F0F0F0Fu) | ((QH[i] << 2) & 0x30303030u);
+      const uint32_t c = ((L1[i] >> 4) & 0x0F0F0F0Fu) | (QH[i] & 0x30303030u);
+      const uint32_t e = ((L2[i] >> 4) & 0x0F0F0F0Fu) | ((QH[i] >> 2) & 0x30303030u);
+      p[0] = dot4(a, x.v[0][i], p[0]);
+      p[1] = dot4(b, x.v[1][i], p[1]);
+      p[2] = dot4(c, x.v[2][i], p[2]);
+      p[3] = dot4(e, x.v[3][i], p[3]);
+    }
+    // sum over the group of (q - 32) * x = sum(q * x) - 32 * (sum of the group's x quants)
+    int v = 0, w = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      v += scs[k] * p[k];
+      w += scs[k] * x.bsum[k];
+    }
+    si = v - 32 * w;
+    sm = 0;
+  }
+  __device__ static void reduce(int &si, int &) {
+    si += __shfl_xor(si, 1, 64);
+    si += __shfl_xor(si, 2, 64);
+  }
+  __device__ static bool leader(const C::Lane &L) { return L.g == 0; }
+  __device__ static int term_index(const C::Lane &L) { return L.hh; }
+  __device__ static float term(const C::Raw &r, int si, int, const Xq &x) {
+    const float dd = half_lo(r.sh ? (r.dw >> 16) : r.dw);
+    return x.d * dd * (float)si;  // src/FastMath.cs:209
+  }
+};
+
+// Q8_0 (src/FastMath.cs:111-122): one lane per 32-value block.
+struct IQ80 {
+  using C = Q80;
+  static constexpr int TERMS = 1;
+  struct Xq {
+    uint32_t v[8];
+    float d;
+  };
+  __device__ static void load_x(const int8_t *q, const float *d, const int16_t *, int blk, const C::Lane &, Xq &x) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(q + (int64_t)blk * 32);
+    const uint4 a = p[0], b = p[1];
+    x.v[0] = a.x, x.v[1] = a.y, x.v[2] = a.z, x.v[3] = a.w;
+    x.v[4] = b.x, x.v[5] = b.y, x.v[6] = b.z, x.v[7] = b.w;
+    x.d = d[blk];
+  }
+  __device__ static void part(const C::Raw &r, const C::Lane &, const Xq &x, int &si, int &sm) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      // quant bytes 4i..4i+3: the window shifted past the 2-byte scale
+      const uint32_t lo = __builtin_amdgcn_alignbit(r.win[i + 1], r.win[i], r.sh);
+      const uint32_t hi = __builtin_amdgcn_alignbit(r.win[i + 2], r.win[i + 1], r.sh);
+      s = dot4(__builtin_amdgcn_alignbit(hi, lo, 16), x.v[i], s);
+    }
+    si = s;
+    sm = 0;
+  }
+  __device__ static void reduce(int &, int &) {}
+  __device__ static bool leader(const C::Lane &) { return true; }
+  __device__ static int term_index(const C::Lane &) { return 0; }
+  __device__ static float term(const C::Raw &r, int si, int, const Xq &x) {
+    const float h = half_lo(__builtin_amdgcn_alignbit(r.win[1], r.win[0], r.sh));
+    return h * x.d * (float)si;  // src/FastMath.cs:120
+  }
+};
+
+struct IntArgs {
+  const uint8_t *w;
+  int64_t row_bytes;
+  int rows, cols;
+  const int8_t *q;  // token 0's quants; token t at q + t * cols
+  const float *d;   // token t at d + t * (cols / activation block)
+  const int16_t *bs;
+  int T;
+  float *terms;  // [T][rows][nterm]
+  int nterm;
+};
+
+constexpr int kIntRows = 4;  // rows per group
+
+// blockIdx.y: a run of 4 wave-columns (4 * 64/LPB blocks); blockIdx.x: row groups with a
+// stride of gridDim.x. A wave keeps its lanes' activation slices in registers for every row.
+template <class IC, int TM>
+__global__ __launch_bounds__(256) void intdot_kernel(IntArgs a) {
+  using C = typename IC::C;
+  constexpr int BPW = 64 / C::LPB, R = kIntRows;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int nb = a.cols / C::BLOCK;
+  const int b0 = (blockIdx.y * 4 + wv) * BPW;
+  if (b0 >= nb) return;  // the whole wave: waves never synchronise
+  const int sub = lane % C::LPB, b = b0 + lane / C::LPB;
+  const bool live = b < nb;
+  const typename C::Lane L = C::lane(sub);
+  constexpr int ab = C::BLOCK;  // activation blocks match the weight blocks (32 for Q8_0, 256 for the K-quants)
+  typename IC::Xq xs[TM];
+#pragma unroll
+  for (int t = 0; t < TM; t++)
+    if (t < a.T && live)
+      IC::load_x(a.q + (int64_t)t * a.cols, a.d + (int64_t)t * (a.cols / ab),
+                 a.bs ? a.bs + (int64_t)t * (a.cols / 16) : nullptr, b, L, xs[t]);
+  const int ngroups = (a.rows + R - 1) / R;
+  for (int g = blockIdx.x; g < ngroups; g += gridDim.x) {
+    typename C::Raw raw[R];
+    if (live) {
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        // rows past the end re-read the last row (valid memory); their terms are not written
+        const int row = min(g * R + r, a.rows - 1);
+        C::load(a.w + (int64_t)row * a.row_bytes + (int64_t)b * C::BYTES, L, raw[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int row = g * R + r;
+#pragma unroll
+      for (int t = 0; t < TM; t++) {
+        if (t < a.T) {
+          int si = 0, sm = 0;
+          if (live) IC::part(raw[r], L, xs[t], si, sm);
+          IC::reduce(si, sm);  // every lane takes part (uniform over the wave)
+          if (live && IC::leader(L) && row < a.rows)
+            a.terms[((int64_t)t * a.rows + row) * a.nterm + b * IC::TERMS + IC::term_index(L)] =
+                IC::term(raw[r], si, sm, xs[t]);
+        }
+      }
+    }
+  }
+}
+
+// y[t][r] = the row's terms added in order, from 0 (the reference's `float sum = 0; sum += ...`).
+__global__ __launch_bounds__(256) void intdot_sum_kernel(const float *__restrict__ terms, int nterm, int rows, int T,
+                                                         float *__restrict__ y, int ldy) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)T * rows) return;
+  const int t = (int)(i / rows), r = (int)(i % rows);
+  const float *p = terms + i * nterm;
+  float s = 0.f;
+  for (int j = 0; j < nterm; j++) s += p[j];
+  y[(int64_t)t * ldy + r] = s;
+}
+
+static int nterm_of(int type, int cols) {
+  return type == 8 ? cols / 32 : type == 14 ? 2 * (cols / 256) : cols / 256;
+}
+
+int64_t intdot_terms_floats(int type, int rows, int cols, int T) {
+  return (int64_t)T * rows * nterm_of(type, cols);
+}
+
+template <class IC, int TM>
+static void launch_int(const IntArgs &a, int num_cu, hipStream_t st) {
+  using C = typename IC::C;
+  const int nb = a.cols / C::BLOCK, bpw = 64 / C::LPB;
+  const int gy = (nb + 4 * bpw - 1) / (4 * bpw);
+  const int ngroups = (a.rows + kIntRows - 1) / kIntRows;
+  int gx = (num_cu * 8 + gy - 1) / gy;  // about 8 workgroups (32 waves) per CU
+  if (gx > ngroups) gx = ngroups;
+  if (gx < 1) gx = 1;
+  hipLaunchKernelGGL((intdot_kernel<IC, TM>), dim3(gx, gy), dim3(256), 0, st, a);
+}
+
+template <class IC>
+static void launch_int_tm(const IntArgs &a, int num_cu, hipStream_t st) {
+  if (a.T <= 1) launch_int<IC, 1>(a, num_cu, st);
+  else if (a.T <= 2) launch_int<IC, 2>(a, num_cu, st);
+  else if (a.T <= 4) launch_int<IC, 4>(a, num_cu, st);
+  else launch_int<IC, 8>(a, num_cu, st);
+}
+
+hipError_t intdot_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, int cols, QActsDev qa, int T,
+                         float *terms, float *y, int ldy, int num_cu, hipStream_t st) {
+  if (rows <= 0 || T <= 0) return hipSuccess;
+  if (T > 8 || !intdot_supports(type) || !intdot_fits(type, cols)) return hipErrorInvalidValue;
+  IntArgs a{w, row_bytes, rows, cols, qa.q, qa.d, qa.bsums, T, terms, nterm_of(type, cols)};
+  switch (type) {
+    case 12: launch_int_tm<IQ4K>(a, num_cu, st); break;
+    case 14: launch_int_tm<IQ6K>(a, num_cu, st); break;
+    default: launch_int_tm<IQ80>(a, num_cu, st); break;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t n = (int64_t)T * rows;
+  hipLaunchKernelGGL(intdot_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, terms, a.nterm, rows, T,
+                     y, ldy);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------ SwiGLU step
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ g, const float *__restrict__ u, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    g[i] = silu_mul(g[i], u[i]);
+}
+
+hipError_t silu_mul_launch(float *g, const float *u, int64_t n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, st, g, u, n);
+  return hipGetLastError();
+}
+
+}  // namespace wl
