@@ -50,6 +50,9 @@ def parse():
     ap.add_argument("--copies", type=int, default=4, help="distinct layer copies to rotate")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--int-dot", action="store_true",
+                    help="the integer-dot kernels (Transformer.IntDot, --int-dot): 8-bit activations, "
+                         "FastMath.IntDot per row; no CPU baseline")
     ap.add_argument("--calibrate", type=int, default=0, metavar="MIB",
                     help="before warm-up, run a plain elementwise copy (torch.neg) of MIB MiB three "
                          "times, untimed: the HBM counters of a kernel of known traffic")
@@ -85,6 +88,7 @@ def main():
     rng = np.random.default_rng(0x57494E44 + 3000)
     host = {n: synth.blocks(t, r, c, rng) for n, t, r, c in LAYER}
     ctx = Context(0)
+    ctx.IntDot = args.int_dot
     layers = [Layer(ctx, host) for _ in range(args.copies)]
     dev = torch.device("cuda:0")
     x = torch.from_numpy(synth.activations(rng, T, HIDDEN)).to(dev)
@@ -162,10 +166,10 @@ def main():
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("%s_T%d" % (dom, T))
+        traffic = json.load(open(tpath)).get("%s_T%d%s" % (dom, T, "_int" if args.int_dot else ""))
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not args.int_dot:
         cpu = cpu_baseline(host, T, rng, args.cpu_seconds)
 
     for ly in layers:
@@ -183,11 +187,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "int8 x q-blocks -> int32, f32 terms" if args.int_dot else "f32",
         "data": "synthetic seeded GGUF blocks (Q4_K/Q6_K), x ~ N(0,1)",
         "config": {"workload": "Llama-3.3-70B Q4_K_M decoder layer, 7 GEMVs (q,k,o,gate,up Q4_K; v,down Q6_K)",
                    "hidden": HIDDEN, "ffn": FFN, "heads": HEADS, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM,
-                   "batch": T, "layer_copies": args.copies, "launches_per_layer": 4},
+                   "batch": T, "layer_copies": args.copies, "launches_per_layer": 4,
+                   "kernels": "int-dot (8-bit activations)" if args.int_dot else "fp32 decode GEMV"},
         "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "ms_per_layer": round(ms_layer, 5),
         "tokens_per_s_80_layers": round(1000.0 / (LAYERS * ms_layer), 2),

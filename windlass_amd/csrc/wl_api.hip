@@ -32,9 +32,8 @@ struct wl_weight {
 };
 
 // S_PART holds the K-chunk partials of split GEMV rows, S_XB the bf16 copy of x for the GEMM,
-// S_QA the 8-bit activations of the integer path, S_TERMS its per-block terms and S_U the up
-// projection of an integer SwiGLU.
-enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB, S_QA, S_TERMS, S_U, S_COUNT };
+// S_QA the 8-bit activations of the integer path.
+enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB, S_QA, S_COUNT };
 
 struct wl_ctx {
   int device;
@@ -247,28 +246,62 @@ static bool int_path(const wl_ctx *c, const wl_weight *w) {
   return c->int_dot && wl::intdot_supports(w->type) && wl::intdot_fits(w->type, (int)w->cols);
 }
 
-// Transformer.MatMul's integer branch (src/Transformer.cs:504-524): quantize the T rows of x
-// once, then every (row, token) is FastMath.IntDot, in passes of up to 8 tokens.
-static int intdot_matmul(wl_ctx *c, const wl_weight *w, const uint8_t *base, int64_t rows, const float *d_x, int T,
-                         float *d_y) {
-  const int cols = (int)w->cols, k = wl::intdot_needs_k(w->type) ? 1 : 0;
+// FastMath.Quantize of x [T][cols] into S_QA (Q8_K when k, else Q8_0).
+static int int_quantize(wl_ctx *c, const float *d_x, int T, int cols, int k, wl::QActsDev *qa) {
   int rc;
   if ((rc = ensure(c, S_QA, (size_t)wl::qacts_bytes(T, cols, k)))) return rc;
-  const int tp = T < 8 ? T : 8;
-  if ((rc = ensure(c, S_TERMS, (size_t)wl::intdot_terms_floats(w->type, (int)rows, cols, tp) * sizeof(float))))
-    return rc;
-  const wl::QActsDev qa = wl::qacts_at(c->buf[S_QA], T, cols, k);
-  WL_HIP(wl::quantize_launch(d_x, T, cols, k, qa, c->stream), "quantize launch");
+  *qa = wl::qacts_at(c->buf[S_QA], T, cols, k);
+  WL_HIP(wl::quantize_launch(d_x, T, cols, k, *qa, c->stream), "quantize launch");
+  return WL_OK;
+}
+
+// The activations of tokens t0.. within qa.
+static wl::QActsDev int_tokens(const wl::QActsDev &qa, int t0, int cols, int k) {
   const int ab = k ? 256 : 32;
-  for (int t0 = 0; t0 < T; t0 += 8) {
-    const int n = T - t0 < 8 ? T - t0 : 8;
-    const wl::QActsDev at{qa.q + (int64_t)t0 * cols, qa.d + (int64_t)t0 * (cols / ab),
-                          qa.bsums ? qa.bsums + (int64_t)t0 * (cols / 16) : nullptr};
-    WL_HIP(wl::intdot_launch(w->type, base, w->row_bytes, (int)rows, cols, at, n, (float *)c->buf[S_TERMS],
-                             d_y + (int64_t)t0 * rows, (int)rows, c->num_cu, c->stream),
-           "int dot launch");
+  return wl::QActsDev{qa.q + (int64_t)t0 * cols, qa.d + (int64_t)t0 * (cols / ab),
+                      qa.bsums ? qa.bsums + (int64_t)t0 * (cols / 16) : nullptr};
+}
+
+// Activations quantized for the integer kernels, made at most once per call and kind.
+struct IntActs {
+  wl::QActsDev qa[2];  // [k]: Q8_0, Q8_K
+  bool made[2] = {false, false};
+};
+
+// Transformer.MatMul's integer branch (src/Transformer.cs:504-524): every (row, token) is
+// FastMath.IntDot, in passes of as many tokens as a launch takes, on the activations of x
+// (quantized once per call and kind). With up (same type and shape), y = silu(gate) * up per
+// (row, token) instead (SwiGlu).
+static int int_run(wl_ctx *c, const wl_weight *w, const uint8_t *base, const uint8_t *up_base, int64_t rows,
+                   const float *d_x, IntActs &acts, int T, float *d_y) {
+  const int cols = (int)w->cols, k = wl::intdot_needs_k(w->type) ? 1 : 0;
+  const int tp = wl::intdot_max_tokens(w->type, cols, up_base ? 2 : 1);
+  if (tp < 1) return fail(WL_E_UNSUPPORTED, "integer dot: rows of %d values are too wide", cols);
+  int rc;
+  if (!acts.made[k]) {
+    if ((rc = int_quantize(c, d_x, T, cols, k, &acts.qa[k]))) return rc;
+    acts.made[k] = true;
+  }
+  for (int t0 = 0; t0 < T; t0 += tp) {
+    const int n = T - t0 < tp ? T - t0 : tp;
+    const wl::QActsDev at = int_tokens(acts.qa[k], t0, cols, k);
+    float *y = d_y + (int64_t)t0 * rows;
+    if (up_base)
+      WL_HIP(wl::intdot_swiglu_launch(w->type, base, up_base, w->row_bytes, (int)rows, cols, at, n, y, (int)rows,
+                                      c->num_cu, c->stream),
+             "int dot launch");
+    else
+      WL_HIP(wl::intdot_launch(w->type, base, w->row_bytes, (int)rows, cols, at, n, y, (int)rows, c->num_cu,
+                               c->stream),
+             "int dot launch");
   }
   return WL_OK;
+}
+
+static int intdot_matmul(wl_ctx *c, const wl_weight *w, const uint8_t *base, int64_t rows, const float *d_x, int T,
+                         float *d_y) {
+  IntActs acts;
+  return int_run(c, w, base, nullptr, rows, d_x, acts, T, d_y);
 }
 
 static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float *d_x, int32_t T, float *d_y) {
@@ -336,7 +369,18 @@ extern "C" int wl_matmul_multi_dev(wl_ctx *c, int32_t n, const wl_weight *const 
   }
   bool any_int = false;
   for (int i = 0; i < n; i++) any_int = any_int || int_path(c, ws[i]);
-  if (any_int || (!same && !mixed_ok)) {
+  if (any_int) {
+    // the integer matrices share the activations; the others take the float path one by one
+    IntActs acts;
+    for (int i = 0; i < n; i++) {
+      int rc = int_path(c, ws[i]) ? int_run(c, ws[i], ws[i]->dev, nullptr, ws[i]->rows * ws[i]->experts, d_x, acts,
+                                            T, d_ys[i])
+                                  : matmul_dev(c, ws[i], -1, d_x, T, d_ys[i]);
+      if (rc) return rc;
+    }
+    return WL_OK;
+  }
+  if (!same && !mixed_ok) {
     for (int i = 0; i < n; i++) {
       int rc = matmul_dev(c, ws[i], -1, d_x, T, d_ys[i]);
       if (rc) return rc;
@@ -368,13 +412,10 @@ extern "C" int wl_gate_up_dev(wl_ctx *c, const wl_weight *gate, const wl_weight 
   operand(gate, expert, &gb, &rows);
   operand(up, expert, &ub, &rows);
   if (int_path(c, gate)) {
-    // SwiGlu on the integer kernels: g = gate x, u = up x, then g / (1 + exp(-g)) * u
-    if ((rc = ensure(c, S_U, (size_t)T * rows * sizeof(float)))) return rc;
-    float *d_u = (float *)c->buf[S_U];
-    if ((rc = intdot_matmul(c, gate, gb, rows, d_x, T, d_h)) || (rc = intdot_matmul(c, up, ub, rows, d_x, T, d_u)))
-      return rc;
-    WL_HIP(wl::silu_mul_launch(d_h, d_u, (int64_t)T * rows, c->stream), "silu launch");
-    return WL_OK;
+    // SwiGlu on the integer kernels: g = gate x, u = up x on the same activations, then
+    // g / (1 + exp(-g)) * u once each row's terms are added
+    IntActs acts;
+    return int_run(c, gate, gb, ub, rows, d_x, acts, T, d_h);
   }
   for (int t0 = 0; t0 < T; t0 += 8) {
     const wl::GemvMat m{gb, ub, gate->row_bytes, (int)rows, gate->type, d_h + (int64_t)t0 * rows, (int)rows};

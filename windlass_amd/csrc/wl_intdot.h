@@ -27,17 +27,20 @@ QActsDev qacts_at(void *buf, int T, int cols, int k);
 // through fp16), k = 1 Q8_K (blocks of 256, float d, sums of every 16 quants). Bit-identical.
 hipError_t quantize_launch(const float *x, int T, int cols, int k, QActsDev a, hipStream_t st);
 
-// Floats of scratch one intdot_launch needs for its per-block terms (T <= 8 tokens).
-int64_t intdot_terms_floats(int type, int rows, int cols, int T);
+// Tokens one launch can take for a row of `cols` (the staged terms fit the workgroup's LDS);
+// nm = 2 for the SwiGLU pair. 0 when not even one fits.
+int intdot_max_tokens(int type, int cols, int nm);
 
 // y[t * ldy + r] = FastMath.IntDot(W[r], the activations of token t) (src/FastMath.cs:105-214)
-// for T <= 8 tokens whose activations start at a (token 0). Bit-identical to the reference: each
-// block's integer sums are exact, its float term is formed with the reference's operations,
-// and a row's terms are added in block order by a second launch.
+// for T <= intdot_max_tokens tokens whose activations start at a (token 0). Bit-identical to
+// the reference: each block's integer sums are exact, its float term is formed with the
+// reference's operations, and a row's terms are added in block order.
 hipError_t intdot_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, int cols, QActsDev a, int T,
-                         float *terms, float *y, int ldy, int num_cu, hipStream_t st);
+                         float *y, int ldy, int num_cu, hipStream_t st);
 
-// h[i] = silu(g[i]) * u[i] (SwiGlu's elementwise step, src/Transformer.cs:247), in place on g.
-hipError_t silu_mul_launch(float *g, const float *u, int64_t n, hipStream_t st);
+// SwiGlu's gate/up half on the integer kernels, one launch: y = silu(IntDot(gate)) * IntDot(up)
+// per (row, token) (src/Transformer.cs:245-247), both products on the same activations a.
+hipError_t intdot_swiglu_launch(int type, const uint8_t *wg, const uint8_t *wu, int64_t row_bytes, int rows,
+                                int cols, QActsDev a, int T, float *y, int ldy, int num_cu, hipStream_t st);
 
 }  // namespace wl

@@ -10,9 +10,9 @@
 // Dot products: the float GEMV's lane slices and block loads (wl_codecs.h), with v_dot4_i32_i8
 // on the quant bytes and the 8-bit activations. A block's integer sums are exact whatever the
 // order, so its lanes add their partials with a butterfly; the block's leader lane forms the
-// block's float term with the reference's operations and writes it. A second launch adds each
-// row's terms in block order, which is the reference's `sum +=` loop, so y is bit-identical to
-// FastMath.IntDot. Waves never exchange data, so there is no barrier.
+// block's float term with the reference's operations and stages it in LDS. A workgroup covers
+// whole rows, so after one barrier a lane per (row, token) adds the row's terms in block order,
+// which is the reference's `sum +=` loop: y is bit-identical to FastMath.IntDot.
 #include "wl_intdot.h"
 
 #include "wl_codecs.h"
@@ -306,139 +306,187 @@ struct IQ80 {
 };
 
 struct IntArgs {
-  const uint8_t *w;
+  const uint8_t *w, *w2;  // w2: the up matrix of the SwiGLU pair (NM = 2)
   int64_t row_bytes;
   int rows, cols;
   const int8_t *q;  // token 0's quants; token t at q + t * cols
   const float *d;   // token t at d + t * (cols / activation block)
   const int16_t *bs;
   int T;
-  float *terms;  // [T][rows][nterm]
-  int nterm;
+  float *y;
+  int ldy;
+  int nterm;  // float terms per row
 };
 
-constexpr int kIntRows = 4;  // rows per group
+constexpr int kIntRows = 4;        // rows per group (of each matrix: 4 / NM)
+constexpr int kIntMaxWaves = 8;    // waves per workgroup
+constexpr int kIntLds = 65536;     // bytes of terms a workgroup may stage
 
-// blockIdx.y: a run of 4 wave-columns (4 * 64/LPB blocks); blockIdx.x: row groups with a
-// stride of gridDim.x. A wave keeps its lanes' activation slices in registers for every row.
-template <class IC, int TM>
-__global__ __launch_bounds__(256) void intdot_kernel(IntArgs a) {
+// The terms of one row added in order, from 0 (the reference's `float sum = 0; sum += ...`);
+// p is 16-byte aligned.
+__device__ __forceinline__ float sum_in_order(const float *p, int n) {
+  float s = 0.f;
+  int j = 0;
+  for (; j + 4 <= n; j += 4) {
+    const float4 v = *reinterpret_cast<const float4 *>(p + j);
+    s += v.x;
+    s += v.y;
+    s += v.z;
+    s += v.w;
+  }
+  for (; j < n; j++) s += p[j];
+  return s;
+}
+
+// A workgroup of NWV waves covers whole rows: in pass p wave w owns the blocks
+// (p * NWV + w) * BPW .. +BPW, lane l block l/LPB of those, slice l%LPB, of every row. For each
+// group of R rows the block terms of every (matrix, row, token) go to LDS; after one barrier
+// wave 0 adds each row's terms in block order (and applies SiLU to the SwiGLU pair) while the
+// other waves go on into the other LDS buffer. SP: one pass, activations kept in registers.
+template <class IC, int TM, int NM, bool SP>
+__global__ __launch_bounds__(64 * kIntMaxWaves) void intdot_kernel(IntArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float wl_int_lds[];
   using C = typename IC::C;
-  constexpr int BPW = 64 / C::LPB, R = kIntRows;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int nb = a.cols / C::BLOCK;
-  const int b0 = (blockIdx.y * 4 + wv) * BPW;
-  if (b0 >= nb) return;  // the whole wave: waves never synchronise
-  const int sub = lane % C::LPB, b = b0 + lane / C::LPB;
-  const bool live = b < nb;
-  const typename C::Lane L = C::lane(sub);
+  constexpr int BPW = 64 / C::LPB, R = kIntRows / NM, TT = IC::TERMS;
   constexpr int ab = C::BLOCK;  // activation blocks match the weight blocks (32 for Q8_0, 256 for the K-quants)
-  typename IC::Xq xs[TM];
-#pragma unroll
-  for (int t = 0; t < TM; t++)
-    if (t < a.T && live)
-      IC::load_x(a.q + (int64_t)t * a.cols, a.d + (int64_t)t * (a.cols / ab),
-                 a.bs ? a.bs + (int64_t)t * (a.cols / 16) : nullptr, b, L, xs[t]);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  const int nb = a.cols / C::BLOCK;
+  const int npass = SP ? 1 : (nb + nwv * BPW - 1) / (nwv * BPW);
+  const int sub = lane % C::LPB, bslot = lane / C::LPB;
+  const typename C::Lane L = C::lane(sub);
   const int ngroups = (a.rows + R - 1) / R;
-  for (int g = blockIdx.x; g < ngroups; g += gridDim.x) {
-    typename C::Raw raw[R];
-    if (live) {
+  const int ld = (a.nterm + 3) & ~3;        // LDS row stride: 16-byte aligned rows
+  const int slab = NM * R * TM * ld;          // floats of one LDS buffer
+  const uint8_t *wm[2] = {a.w, a.w2};
+
+  auto load_xs = [&](int b, typename IC::Xq(&xs)[TM]) {
 #pragma unroll
-      for (int r = 0; r < R; r++) {
-        // rows past the end re-read the last row (valid memory); their terms are not written
-        const int row = min(g * R + r, a.rows - 1);
-        C::load(a.w + (int64_t)row * a.row_bytes + (int64_t)b * C::BYTES, L, raw[r]);
+    for (int t = 0; t < TM; t++)
+      if (t < a.T)
+        IC::load_x(a.q + (int64_t)t * a.cols, a.d + (int64_t)t * (a.cols / ab),
+                   a.bs ? a.bs + (int64_t)t * (a.cols / 16) : nullptr, b, L, xs[t]);
+  };
+  typename IC::Xq xs0[TM];
+  if (SP && wv * BPW + bslot < nb) load_xs(wv * BPW + bslot, xs0);
+
+  int buf = 0;
+  for (int g = blockIdx.x; g < ngroups; g += gridDim.x, buf ^= 1) {
+    float *pb = wl_int_lds + buf * slab;
+    for (int p = 0; p < npass; p++) {
+      const int b = (p * nwv + wv) * BPW + bslot;
+      const bool live = b < nb;
+      typename IC::Xq xsp[TM];
+      if (!SP && live) load_xs(b, xsp);
+      const typename IC::Xq(&xs)[TM] = SP ? xs0 : xsp;
+      typename C::Raw raw[NM][R];
+      if (live) {
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            // rows past the end re-read the last row (valid memory); their sums are not stored
+            const int row = min(g * R + r, a.rows - 1);
+            C::load(wm[m] + (int64_t)row * a.row_bytes + (int64_t)b * C::BYTES, L, raw[m][r]);
+          }
       }
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+          for (int t = 0; t < TM; t++) {
+            if (t < a.T) {
+              int si = 0, sm = 0;
+              if (live) IC::part(raw[m][r], L, xs[t], si, sm);
+              IC::reduce(si, sm);  // every lane takes part (uniform over the wave)
+              if (live && IC::leader(L))
+                pb[((m * R + r) * TM + t) * ld + b * TT + IC::term_index(L)] = IC::term(raw[m][r], si, sm, xs[t]);
+            }
+          }
     }
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      const int row = g * R + r;
-#pragma unroll
-      for (int t = 0; t < TM; t++) {
-        if (t < a.T) {
-          int si = 0, sm = 0;
-          if (live) IC::part(raw[r], L, xs[t], si, sm);
-          IC::reduce(si, sm);  // every lane takes part (uniform over the wave)
-          if (live && IC::leader(L) && row < a.rows)
-            a.terms[((int64_t)t * a.rows + row) * a.nterm + b * IC::TERMS + IC::term_index(L)] =
-                IC::term(raw[r], si, sm, xs[t]);
+    __syncthreads();
+    if (wv == 0) {
+      for (int i = lane; i < R * TM; i += 64) {
+        const int r = i % R, t = i / R, row = g * R + r;
+        if (t < a.T && row < a.rows) {
+          float s = sum_in_order(pb + (r * TM + t) * ld, a.nterm);
+          if constexpr (NM == 2) s = silu_mul(s, sum_in_order(pb + ((R + r) * TM + t) * ld, a.nterm));
+          a.y[(int64_t)t * a.ldy + row] = s;
         }
       }
     }
   }
 }
 
-// y[t][r] = the row's terms added in order, from 0 (the reference's `float sum = 0; sum += ...`).
-__global__ __launch_bounds__(256) void intdot_sum_kernel(const float *__restrict__ terms, int nterm, int rows, int T,
-                                                         float *__restrict__ y, int ldy) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)T * rows) return;
-  const int t = (int)(i / rows), r = (int)(i % rows);
-  const float *p = terms + i * nterm;
-  float s = 0.f;
-  for (int j = 0; j < nterm; j++) s += p[j];
-  y[(int64_t)t * ldy + r] = s;
-}
-
 static int nterm_of(int type, int cols) {
   return type == 8 ? cols / 32 : type == 14 ? 2 * (cols / 256) : cols / 256;
 }
 
-int64_t intdot_terms_floats(int type, int rows, int cols, int T) {
-  return (int64_t)T * rows * nterm_of(type, cols);
+static size_t lds_of(int nm, int tm, int nterm) {
+  return sizeof(float) * 2 * kIntRows * tm * ((nterm + 3) & ~3);  // nm matrices of kIntRows / nm rows
 }
 
-template <class IC, int TM>
-static void launch_int(const IntArgs &a, int num_cu, hipStream_t st) {
+template <class IC, int TM, int NM>
+static hipError_t launch_int(const IntArgs &a, int num_cu, hipStream_t st) {
   using C = typename IC::C;
-  const int nb = a.cols / C::BLOCK, bpw = 64 / C::LPB;
-  const int gy = (nb + 4 * bpw - 1) / (4 * bpw);
-  const int ngroups = (a.rows + kIntRows - 1) / kIntRows;
-  int gx = (num_cu * 8 + gy - 1) / gy;  // about 8 workgroups (32 waves) per CU
-  if (gx > ngroups) gx = ngroups;
-  if (gx < 1) gx = 1;
-  hipLaunchKernelGGL((intdot_kernel<IC, TM>), dim3(gx, gy), dim3(256), 0, st, a);
+  const int bpw = 64 / C::LPB, nb = a.cols / C::BLOCK;
+  const int units = (nb + bpw - 1) / bpw;
+  const int passes = (units + kIntMaxWaves - 1) / kIntMaxWaves;
+  const int nwv = (units + passes - 1) / passes;
+  const int ngroups = (a.rows + kIntRows / NM - 1) / (kIntRows / NM);
+  int nwg = (num_cu * 32 + nwv - 1) / nwv;  // about 32 waves per CU
+  if (nwg > ngroups) nwg = ngroups;
+  const size_t smem = lds_of(NM, TM, a.nterm);
+  if (passes == 1)
+    hipLaunchKernelGGL((intdot_kernel<IC, TM, NM, true>), dim3(nwg), dim3(64 * nwv), smem, st, a);
+  else
+    hipLaunchKernelGGL((intdot_kernel<IC, TM, NM, false>), dim3(nwg), dim3(64 * nwv), smem, st, a);
+  return hipGetLastError();
 }
 
-template <class IC>
-static void launch_int_tm(const IntArgs &a, int num_cu, hipStream_t st) {
-  if (a.T <= 1) launch_int<IC, 1>(a, num_cu, st);
-  else if (a.T <= 2) launch_int<IC, 2>(a, num_cu, st);
-  else if (a.T <= 4) launch_int<IC, 4>(a, num_cu, st);
-  else launch_int<IC, 8>(a, num_cu, st);
+template <class IC, int NM>
+static hipError_t launch_int_tm(const IntArgs &a, int num_cu, hipStream_t st) {
+  if (a.T <= 1) return launch_int<IC, 1, NM>(a, num_cu, st);
+  if (a.T <= 2) return launch_int<IC, 2, NM>(a, num_cu, st);
+  if (a.T <= 4) return launch_int<IC, 4, NM>(a, num_cu, st);
+  return launch_int<IC, 8, NM>(a, num_cu, st);
+}
+
+template <int NM>
+static hipError_t launch_type(int type, const IntArgs &a, int num_cu, hipStream_t st) {
+  switch (type) {
+    case 12: return launch_int_tm<IQ4K, NM>(a, num_cu, st);
+    case 14: return launch_int_tm<IQ6K, NM>(a, num_cu, st);
+    default: return launch_int_tm<IQ80, NM>(a, num_cu, st);
+  }
+}
+
+int intdot_max_tokens(int type, int cols, int nm) {
+  const int nterm = nterm_of(type, cols);
+  for (int tm = 8; tm >= 1; tm /= 2)
+    if (lds_of(nm, tm, nterm) <= (size_t)kIntLds) return tm;
+  return 0;
+}
+
+static hipError_t run(int type, const uint8_t *w, const uint8_t *w2, int64_t row_bytes, int rows, int cols,
+                      QActsDev qa, int T, float *y, int ldy, int num_cu, hipStream_t st) {
+  if (rows <= 0 || T <= 0) return hipSuccess;
+  const int nm = w2 ? 2 : 1;
+  if (!intdot_supports(type) || !intdot_fits(type, cols) || T > intdot_max_tokens(type, cols, nm))
+    return hipErrorInvalidValue;
+  if (!qa.q || !qa.d || (intdot_needs_k(type) && !qa.bsums)) return hipErrorInvalidValue;
+  const IntArgs a{w, w2, row_bytes, rows, cols, qa.q, qa.d, qa.bsums, T, y, ldy, nterm_of(type, cols)};
+  return nm == 2 ? launch_type<2>(type, a, num_cu, st) : launch_type<1>(type, a, num_cu, st);
 }
 
 hipError_t intdot_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, int cols, QActsDev qa, int T,
-                         float *terms, float *y, int ldy, int num_cu, hipStream_t st) {
-  if (rows <= 0 || T <= 0) return hipSuccess;
-  if (T > 8 || !intdot_supports(type) || !intdot_fits(type, cols)) return hipErrorInvalidValue;
-  IntArgs a{w, row_bytes, rows, cols, qa.q, qa.d, qa.bsums, T, terms, nterm_of(type, cols)};
-  switch (type) {
-    case 12: launch_int_tm<IQ4K>(a, num_cu, st); break;
-    case 14: launch_int_tm<IQ6K>(a, num_cu, st); break;
-    default: launch_int_tm<IQ80>(a, num_cu, st); break;
-  }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const int64_t n = (int64_t)T * rows;
-  hipLaunchKernelGGL(intdot_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, terms, a.nterm, rows, T,
-                     y, ldy);
-  return hipGetLastError();
+                         float *y, int ldy, int num_cu, hipStream_t st) {
+  return run(type, w, nullptr, row_bytes, rows, cols, qa, T, y, ldy, num_cu, st);
 }
 
-// ------------------------------------------------------------------------------ SwiGLU step
-
-__global__ __launch_bounds__(256) void silu_mul_kernel(float *__restrict__ g, const float *__restrict__ u, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-    g[i] = silu_mul(g[i], u[i]);
-}
-
-hipError_t silu_mul_launch(float *g, const float *u, int64_t n, hipStream_t st) {
-  if (n <= 0) return hipSuccess;
-  int64_t blocks = (n + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, st, g, u, n);
-  return hipGetLastError();
+hipError_t intdot_swiglu_launch(int type, const uint8_t *wg, const uint8_t *wu, int64_t row_bytes, int rows,
+                                int cols, QActsDev qa, int T, float *y, int ldy, int num_cu, hipStream_t st) {
+  return run(type, wg, wu, row_bytes, rows, cols, qa, T, y, ldy, num_cu, st);
 }
 
 }  // namespace wl
