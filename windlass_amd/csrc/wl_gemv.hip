@@ -113,12 +113,28 @@ int gemv_chunks(int nmat, int cols) {
   return 1;  // prime widths run unsplit (one or more passes)
 }
 
+// The wave-columns a one-token launch splits a row into (S chunks of W waves, one pass each), or
+// 0 when a row needs more than one pass (then tokens run the per-group path below).
+static int batch_columns(int nmat, int cols, int *S_out, int *W_out) {
+  const int S = gemv_chunks(nmat, cols);
+  int passes, nwv;
+  cs_shape(cols / S, &passes, &nwv);
+  if (passes != 1) return 0;
+  *S_out = S;
+  *W_out = nwv;
+  return S * nwv;
+}
+
 int64_t gemv_scratch_floats(const GemvMat *mats, int nmat, int nm, int cols, int T) {
   const int S = gemv_chunks(nmat, cols);
-  if (S == 1) return 0;
   int64_t n = 0;
-  for (int i = 0; i < nmat; i++) n += (int64_t)S * nm * T * mats[i].rows;
-  return n;
+  if (S > 1)
+    for (int i = 0; i < nmat; i++) n += (int64_t)S * nm * T * mats[i].rows;
+  int bs, bw;
+  const int u = T > 1 ? batch_columns(nmat, cols, &bs, &bw) : 0;
+  int64_t nb = 0;
+  for (int i = 0; i < nmat; i++) nb += (int64_t)u * nm * T * mats[i].rows;
+  return n > nb ? n : nb;
 }
 
 // Grid: about kWavesPerCu waves per CU, split over the segments in proportion to their groups.
@@ -200,12 +216,222 @@ static int block_bytes(int type) {
   return type == 12 ? 144 : type == 14 ? 210 : type == 8 ? 34 : type == 23 ? 136 : 66;
 }
 
+// ------------------------------------------------------------------ batched tokens (T >= 2)
+// The one-token launch's decomposition, kept bit for bit, with the tokens' x slices staged in
+// LDS once per workgroup: a workgroup owns ONE wave-column c (blocks c*BPW .. +BPW: the slices a
+// wave of the one-token launch owns) for a stripe of row groups; its waves walk row groups
+// independently (no barrier after staging). Per (matrix, token, row) a lane forms the codec's
+// dot on its slice, the 64 lanes fold it with the same exchange butterfly, and the wave-column's
+// result goes to part[m][t][row][c]. batch_combine_kernel then adds the wave-columns as the
+// one-token launch does: in wave order within each K-chunk, then in chunk order, SiLU last for
+// the SwiGLU pair. So every token's bits equal its one-token result.
+struct BatchArgs {
+  const uint8_t *w, *w2;
+  int64_t row_bytes;
+  int rows, cols;
+  const float *x;
+  int ldx, T;
+  float *part;  // [NM][T][rows][u]
+  int u;        // wave-columns
+};
+
+template <class C>
+constexpr int xs_u4() {
+  return (int)((sizeof(typename C::Xs) + 15) / 16);
+}
+
+template <class C, int TM>
+__host__ __device__ constexpr size_t batch_lds_bytes() {
+  return (C::NEED_LDS ? sizeof(Lds) : 0) + (size_t)TM * xs_u4<C>() * 64 * 16;
+}
+
+template <class C, int TM, int R, int NM>
+__global__ __launch_bounds__(256) void gemv_batch_kernel(BatchArgs a) {
+  constexpr int V = NM * R * TM, LOW = 6 - ilog2(V), BPW = 64 / C::LPB, NX = xs_u4<C>();
+  static_assert((1 << ilog2(V)) == V && V <= 64, "partials per lane must be a power of two <= 64");
+  const Lds &lds = *reinterpret_cast<const Lds *>(wl_dyn_lds);
+  uint4 *xl = reinterpret_cast<uint4 *>(wl_dyn_lds + (C::NEED_LDS ? sizeof(Lds) : 0));  // [TM][NX][64]
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int c = blockIdx.y, nb = a.cols / C::BLOCK;
+  const int sub = lane % C::LPB, b = c * BPW + lane / C::LPB;
+  const bool live = b < nb;
+  const typename C::Lane L = C::lane(sub);
+  if constexpr (C::NEED_LDS) C::init_lds(*reinterpret_cast<Lds *>(wl_dyn_lds));
+  // stage: wave w prepares tokens w, w+4, ... exactly as the one-token launch prepares its slice
+  for (int t = wv; t < TM; t += 4) {
+    if (t < a.T && live) {
+      typename C::Xs xs;
+      C::load_x(a.x + (int64_t)t * a.ldx + (int64_t)b * C::BLOCK, L, xs);
+      uint4 v[NX] = {};
+      __builtin_memcpy(v, &xs, sizeof(xs));
+#pragma unroll
+      for (int i = 0; i < NX; i++) xl[(t * NX + i) * 64 + lane] = v[i];
+    }
+  }
+  __syncthreads();
+  const uint8_t *wm[2] = {a.w, a.w2};
+  const int ngroups = (a.rows + R - 1) / R;
+  for (int g = blockIdx.x * 4 + wv; g < ngroups; g += gridDim.x * 4) {
+    float acc[NM][R][TM];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int t = 0; t < TM; t++) acc[m][r][t] = 0.f;
+    if (live) {
+      typename C::Raw raw[NM][R];
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          // rows past the end re-read the last row (valid memory); their results are dropped
+          const int row = min(g * R + r, a.rows - 1);
+          C::load(wm[m] + (int64_t)row * a.row_bytes + (int64_t)b * C::BYTES, L, raw[m][r]);
+        }
+      typename C::W w[NM][R];
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int r = 0; r < R; r++) C::unpack(raw[m][r], L, lds, w[m][r]);
+#pragma unroll
+      for (int t = 0; t < TM; t++) {
+        if (t < a.T) {
+          uint4 v[NX];
+#pragma unroll
+          for (int i = 0; i < NX; i++) v[i] = xl[(t * NX + i) * 64 + lane];
+          typename C::Xs xs;
+          __builtin_memcpy(&xs, v, sizeof(xs));
+#pragma unroll
+          for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[m][r][t] += C::dot(w[m][r], xs);
+        }
+      }
+    }
+    // value index v = (m*TM + t)*R + r, as the one-token launch folds it
+    float vals[V];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int r = 0; r < R; r++) vals[(m * TM + t) * R + r] = acc[m][r][t];
+    const float q = exch_reduce<V, 5>(vals, lane);
+    if ((lane & ((1 << LOW) - 1)) == 0) {
+      const int v = lane >> LOW, r = v % R, t = (v / R) % TM, m = v / (R * TM);
+      const int row = g * R + r;
+      if (t < a.T && row < a.rows) a.part[(((int64_t)m * a.T + t) * a.rows + row) * a.u + c] = q;
+    }
+  }
+}
+
+// y[t][r] from the wave-column partials: waves in order within each of S chunks of W, then the
+// chunks in order (the one-token launch's wave-0 sum and chunk combine); SiLU for the pair.
+__device__ __forceinline__ float batch_sum(const float *p, int S, int W) {
+  float y = 0.f;
+  for (int c = 0; c < S; c++) {
+    float s = p[c * W];
+    for (int k = 1; k < W; k++) s += p[c * W + k];
+    y = c == 0 ? s : y + s;
+  }
+  return y;
+}
+
+__global__ __launch_bounds__(256) void batch_combine_kernel(const float *__restrict__ part, int NM, int T, int rows,
+                                                            int S, int W, float *__restrict__ y, int ldy) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)T * rows) return;
+  const int t = (int)(i / rows), r = (int)(i % rows);
+  const int u = S * W;
+  float s = batch_sum(part + i * u, S, W);
+  if (NM == 2) s = silu_mul(s, batch_sum(part + ((int64_t)T * rows + i) * u, S, W));
+  y[(int64_t)t * ldy + r] = s;
+}
+
+#ifndef WL_BATCH_R1
+#define WL_BATCH_R1 4  // rows per group of a single matrix (2 for the SwiGLU pair)
+#endif
+#ifndef WL_BATCH_WGS
+#define WL_BATCH_WGS 4  // workgroups per CU the grid aims at (two rounds at eight tokens)
+#endif
+
+template <class C, int TM, int NM>
+static hipError_t launch_batch_tm(const BatchArgs &a, int S, int W, float *y, int ldy, int num_cu, hipStream_t st) {
+  constexpr int R = NM == 1 ? WL_BATCH_R1 : 2;
+  const size_t smem = batch_lds_bytes<C, TM>();
+  static bool raised = false;
+  if (smem > 65536 && !raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_batch_kernel<C, TM, R, NM>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+      return hipErrorInvalidConfiguration;
+    raised = true;
+  }
+  const int ngroups = (a.rows + R - 1) / R;
+  int gx = (num_cu * WL_BATCH_WGS + a.u - 1) / a.u;
+  if (gx * 4 > ngroups) gx = (ngroups + 3) / 4;
+  if (gx < 1) gx = 1;
+  hipLaunchKernelGGL((gemv_batch_kernel<C, TM, R, NM>), dim3(gx, a.u), dim3(256), smem, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t n = (int64_t)a.T * a.rows;
+  hipLaunchKernelGGL(batch_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.part, NM, a.T,
+                     a.rows, S, W, y, ldy);
+  return hipGetLastError();
+}
+
+template <class C, int NM>
+static hipError_t launch_batch(const BatchArgs &a, int S, int W, float *y, int ldy, int num_cu, hipStream_t st) {
+  if (a.T <= 2) return launch_batch_tm<C, 2, NM>(a, S, W, y, ldy, num_cu, st);
+  if (a.T <= 4) return launch_batch_tm<C, 4, NM>(a, S, W, y, ldy, num_cu, st);
+  return launch_batch_tm<C, 8, NM>(a, S, W, y, ldy, num_cu, st);
+}
+
+template <int NM>
+static hipError_t launch_batch_type(int type, const BatchArgs &a, int S, int W, float *y, int ldy, int num_cu,
+                                    hipStream_t st) {
+  switch (type) {
+    case 12: return launch_batch<Q4K, NM>(a, S, W, y, ldy, num_cu, st);
+    case 14: return launch_batch<Q6K, NM>(a, S, W, y, ldy, num_cu, st);
+    case 8: return launch_batch<Q80, NM>(a, S, W, y, ldy, num_cu, st);
+    case 23: return launch_batch<IQ4XS, NM>(a, S, W, y, ldy, num_cu, st);
+    case 16: return launch_batch<IQ2XXS, NM>(a, S, W, y, ldy, num_cu, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+#ifndef WL_GEMV_BATCH
+#define WL_GEMV_BATCH 1
+#endif
+
+// The batched path for every matrix of a launch of T >= 2 tokens, when the one-token launch runs
+// its rows in single passes. Returns hipErrorNotSupported when it does not apply.
+static hipError_t gemv_batch_run(const GemvMat *mats, int nmat, int nm, const float *x, int ldx, int cols, int T,
+                                 float *scratch, int num_cu, hipStream_t st) {
+  if (!WL_GEMV_BATCH || T < 2 || !scratch) return hipErrorNotSupported;
+  int S, W;
+  const int u = batch_columns(nmat, cols, &S, &W);
+  if (u == 0) return hipErrorNotSupported;
+  for (int i = 0; i < nmat; i++) {
+    const GemvMat &m = mats[i];
+    const BatchArgs a{m.w, m.w2, m.row_bytes, m.rows, cols, x, ldx, T, scratch, u};
+    const hipError_t e = nm == 2 ? launch_batch_type<2>(m.type, a, S, W, m.y, m.ldy, num_cu, st)
+                                 : launch_batch_type<1>(m.type, a, S, W, m.y, m.ldy, num_cu, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int ldx, int cols, int T,
                     float *scratch, int num_cu, hipStream_t st) {
   if (nmat < 1 || nmat > GEMV_MAX_MATS || T < 1 || T > 8 || (nm != 1 && nm != 2)) return hipErrorInvalidValue;
   bool same = true;
   for (int i = 1; i < nmat; i++) same = same && mats[i].type == mats[0].type;
   if (!same && nm != 1) return hipErrorInvalidValue;
+  {
+    const hipError_t e = gemv_batch_run(mats, nmat, nm, x, ldx, cols, T, scratch, num_cu, st);
+    if (e != hipErrorNotSupported) return e;
+  }
   const int S = gemv_chunks(nmat, cols);
   if (S > 1 && !scratch) return hipErrorInvalidValue;
   GemvParams p{};
