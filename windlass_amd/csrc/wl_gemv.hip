@@ -219,20 +219,29 @@ static int block_bytes(int type) {
 // ------------------------------------------------------------------ batched tokens (T >= 2)
 // The one-token launch's decomposition, kept bit for bit, with the tokens' x slices staged in
 // LDS once per workgroup: a workgroup owns ONE wave-column c (blocks c*BPW .. +BPW: the slices a
-// wave of the one-token launch owns) for a stripe of row groups; its waves walk row groups
-// independently (no barrier after staging). Per (matrix, token, row) a lane forms the codec's
-// dot on its slice, the 64 lanes fold it with the same exchange butterfly, and the wave-column's
-// result goes to part[m][t][row][c]. batch_combine_kernel then adds the wave-columns as the
-// one-token launch does: in wave order within each K-chunk, then in chunk order, SiLU last for
-// the SwiGLU pair. So every token's bits equal its one-token result.
-struct BatchArgs {
+// wave of the one-token launch owns) for a stripe of row groups of one matrix; its waves walk
+// row groups independently (no barrier after staging). Per (matrix, token, row) a lane forms the
+// codec's dot on its slice, the 64 lanes fold it with the same exchange butterfly, and the
+// wave-column's result goes to part[m][t][row][c]. batch_combine_kernel then adds the
+// wave-columns as the one-token launch does: in wave order within each K-chunk, then in chunk
+// order, SiLU last for the SwiGLU pair. So every token's bits equal its one-token result.
+// All matrices of a call (q, k, v) share one launch and one combine launch.
+struct BatchMat {
   const uint8_t *w, *w2;
   int64_t row_bytes;
-  int rows, cols;
+  float *part;  // [NM][T][rows][u]
+  float *y;
+  int ldy, rows, type;
+  int wg_begin;  // first blockIdx.x of this matrix
+};
+
+struct BatchArgs {
+  BatchMat m[GEMV_MAX_MATS];
+  int nmat, cols;
   const float *x;
   int ldx, T;
-  float *part;  // [NM][T][rows][u]
-  int u;        // wave-columns
+  int u;     // wave-columns
+  int S, W;  // the one-token launch's K-chunks and waves per chunk (u = S * W)
 };
 
 template <class C>
@@ -245,8 +254,22 @@ __host__ __device__ constexpr size_t batch_lds_bytes() {
   return (C::NEED_LDS ? sizeof(Lds) : 0) + (size_t)TM * xs_u4<C>() * 64 * 16;
 }
 
+#ifndef WL_BATCH_WAVES
+#define WL_BATCH_WAVES 8  // waves per workgroup of the batched kernel
+#endif
+constexpr int kBatchWaves = WL_BATCH_WAVES;
+
+__device__ __forceinline__ int batch_mat(const BatchArgs &a) {
+  int mi = 0;
+#pragma unroll
+  for (int i = 1; i < GEMV_MAX_MATS; i++)
+    if (i < a.nmat && (int)blockIdx.x >= a.m[i].wg_begin) mi = i;
+  return mi;
+}
+
+// wgx: this workgroup's index among the matrix's nwg workgroups of column blockIdx.y.
 template <class C, int TM, int R, int NM>
-__global__ __launch_bounds__(256) void gemv_batch_kernel(BatchArgs a) {
+__device__ __forceinline__ void batch_body(const BatchArgs &a, const BatchMat &M, int wgx, int nwg) {
   constexpr int V = NM * R * TM, LOW = 6 - ilog2(V), BPW = 64 / C::LPB, NX = xs_u4<C>();
   static_assert((1 << ilog2(V)) == V && V <= 64, "partials per lane must be a power of two <= 64");
   const Lds &lds = *reinterpret_cast<const Lds *>(wl_dyn_lds);
@@ -257,8 +280,8 @@ __global__ __launch_bounds__(256) void gemv_batch_kernel(BatchArgs a) {
   const bool live = b < nb;
   const typename C::Lane L = C::lane(sub);
   if constexpr (C::NEED_LDS) C::init_lds(*reinterpret_cast<Lds *>(wl_dyn_lds));
-  // stage: wave w prepares tokens w, w+4, ... exactly as the one-token launch prepares its slice
-  for (int t = wv; t < TM; t += 4) {
+  // stage: wave w prepares tokens w, w + kBatchWaves, ... as the one-token launch prepares its slice
+  for (int t = wv; t < TM; t += kBatchWaves) {
     if (t < a.T && live) {
       typename C::Xs xs;
       C::load_x(a.x + (int64_t)t * a.ldx + (int64_t)b * C::BLOCK, L, xs);
@@ -269,9 +292,9 @@ __global__ __launch_bounds__(256) void gemv_batch_kernel(BatchArgs a) {
     }
   }
   __syncthreads();
-  const uint8_t *wm[2] = {a.w, a.w2};
-  const int ngroups = (a.rows + R - 1) / R;
-  for (int g = blockIdx.x * 4 + wv; g < ngroups; g += gridDim.x * 4) {
+  const uint8_t *wm[2] = {M.w, M.w2};
+  const int ngroups = (M.rows + R - 1) / R;
+  for (int g = wgx * kBatchWaves + wv; g < ngroups; g += nwg * kBatchWaves) {
     float acc[NM][R][TM];
 #pragma unroll
     for (int m = 0; m < NM; m++)
@@ -286,8 +309,8 @@ __global__ __launch_bounds__(256) void gemv_batch_kernel(BatchArgs a) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
           // rows past the end re-read the last row (valid memory); their results are dropped
-          const int row = min(g * R + r, a.rows - 1);
-          C::load(wm[m] + (int64_t)row * a.row_bytes + (int64_t)b * C::BYTES, L, raw[m][r]);
+          const int row = min(g * R + r, M.rows - 1);
+          C::load(wm[m] + (int64_t)row * M.row_bytes + (int64_t)b * C::BYTES, L, raw[m][r]);
         }
       typename C::W w[NM][R];
 #pragma unroll
@@ -321,8 +344,57 @@ __global__ __launch_bounds__(256) void gemv_batch_kernel(BatchArgs a) {
     if ((lane & ((1 << LOW) - 1)) == 0) {
       const int v = lane >> LOW, r = v % R, t = (v / R) % TM, m = v / (R * TM);
       const int row = g * R + r;
-      if (t < a.T && row < a.rows) a.part[(((int64_t)m * a.T + t) * a.rows + row) * a.u + c] = q;
+      if (t < a.T && row < M.rows) M.part[(((int64_t)m * a.T + t) * M.rows + row) * a.u + c] = q;
     }
+  }
+}
+
+__device__ __forceinline__ int batch_nwg(const BatchArgs &a, int mi) {
+  return (mi + 1 < a.nmat ? a.m[mi + 1].wg_begin : (int)gridDim.x) - a.m[mi].wg_begin;
+}
+
+// Waves per SIMD the register budget is cut for: four (two resident workgroups of eight waves
+// per CU, at most 128 VGPRs), except where that would spill (the Q6_K SwiGLU pair).
+template <class C, int NM>
+constexpr int batch_occupancy() {
+  return NM == 2 && C::BYTES == 210 ? 2 : 4;
+}
+
+template <class C, int TM, int R, int NM>
+__global__ __launch_bounds__(64 * kBatchWaves) __attribute__((amdgpu_waves_per_eu(batch_occupancy<C, NM>())))
+void gemv_batch_kernel(BatchArgs a) {
+  const int mi = batch_mat(a);
+  batch_body<C, TM, R, NM>(a, a.m[mi], (int)blockIdx.x - a.m[mi].wg_begin, batch_nwg(a, mi));
+}
+
+#ifndef WL_BATCH_R1
+#define WL_BATCH_R1 2  // rows per group of a single matrix
+#endif
+#ifndef WL_BATCH_R2
+#define WL_BATCH_R2 1  // rows per group of the SwiGLU pair
+#endif
+#ifndef WL_BATCH_WPC
+#define WL_BATCH_WPC 64  // waves per CU the grid aims at (about four rounds of resident workgroups)
+#endif
+constexpr int kBatchR1 = WL_BATCH_R1, kBatchR2 = WL_BATCH_R2;
+
+#ifndef WL_BATCH_MIXED_OCC
+#define WL_BATCH_MIXED_OCC 4
+#endif
+
+// Matrices of different formats in one launch (q/k Q4_K with v Q6_K): the codec is chosen per
+// workgroup, every workgroup stays on one matrix.
+template <int TM>
+__global__ __launch_bounds__(64 * kBatchWaves) __attribute__((amdgpu_waves_per_eu(WL_BATCH_MIXED_OCC)))
+void gemv_batch_mixed_kernel(BatchArgs a) {
+  const int mi = batch_mat(a);
+  const BatchMat &M = a.m[mi];
+  const int wgx = (int)blockIdx.x - M.wg_begin, nwg = batch_nwg(a, mi);
+  switch (M.type) {
+    case 12: batch_body<Q4K, TM, kBatchR1, 1>(a, M, wgx, nwg); break;
+    case 14: batch_body<Q6K, TM, kBatchR1, 1>(a, M, wgx, nwg); break;
+    case 8: batch_body<Q80, TM, kBatchR1, 1>(a, M, wgx, nwg); break;
+    default: break;
   }
 }
 
@@ -338,64 +410,98 @@ __device__ __forceinline__ float batch_sum(const float *p, int S, int W) {
   return y;
 }
 
-__global__ __launch_bounds__(256) void batch_combine_kernel(const float *__restrict__ part, int NM, int T, int rows,
-                                                            int S, int W, float *__restrict__ y, int ldy) {
+// blockIdx.y: the matrix.
+template <int NM>
+__global__ __launch_bounds__(256) void batch_combine_kernel(BatchArgs a) {
+  const BatchMat &M = a.m[blockIdx.y];
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)T * rows) return;
-  const int t = (int)(i / rows), r = (int)(i % rows);
-  const int u = S * W;
-  float s = batch_sum(part + i * u, S, W);
-  if (NM == 2) s = silu_mul(s, batch_sum(part + ((int64_t)T * rows + i) * u, S, W));
-  y[(int64_t)t * ldy + r] = s;
+  if (i >= (int64_t)a.T * M.rows) return;
+  const int t = (int)(i / M.rows), r = (int)(i % M.rows);
+  float s = batch_sum(M.part + i * a.u, a.S, a.W);
+  if constexpr (NM == 2) s = silu_mul(s, batch_sum(M.part + ((int64_t)a.T * M.rows + i) * a.u, a.S, a.W));
+  M.y[(int64_t)t * M.ldy + r] = s;
 }
 
-#ifndef WL_BATCH_R1
-#define WL_BATCH_R1 4  // rows per group of a single matrix (2 for the SwiGLU pair)
-#endif
-#ifndef WL_BATCH_WGS
-#define WL_BATCH_WGS 4  // workgroups per CU the grid aims at (two rounds at eight tokens)
-#endif
+// Workgroups per matrix along x: about WL_BATCH_WPC waves per CU over all columns, split over
+// the matrices in proportion to their row groups. Returns the grid's x size.
+static int plan_batch(BatchArgs &a, int R, int num_cu) {
+  int total = 0;
+  for (int i = 0; i < a.nmat; i++) total += (a.m[i].rows + R - 1) / R;
+  const int target = (num_cu * WL_BATCH_WPC / kBatchWaves + a.u - 1) / a.u;
+  int gx = 0;
+  for (int i = 0; i < a.nmat; i++) {
+    const int groups = (a.m[i].rows + R - 1) / R;
+    int n = (int)(((int64_t)target * groups + total - 1) / total);
+    const int most = (groups + kBatchWaves - 1) / kBatchWaves;
+    if (n > most) n = most;
+    if (n < 1) n = 1;
+    a.m[i].wg_begin = gx;
+    gx += n;
+  }
+  return gx;
+}
 
-template <class C, int TM, int NM>
-static hipError_t launch_batch_tm(const BatchArgs &a, int S, int W, float *y, int ldy, int num_cu, hipStream_t st) {
-  constexpr int R = NM == 1 ? WL_BATCH_R1 : 2;
-  const size_t smem = batch_lds_bytes<C, TM>();
-  static bool raised = false;
+template <class K>
+static hipError_t raise_lds(K *kernel, size_t smem, bool &raised) {
   if (smem > 65536 && !raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_batch_kernel<C, TM, R, NM>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)smem) != hipSuccess)
       return hipErrorInvalidConfiguration;
     raised = true;
   }
-  const int ngroups = (a.rows + R - 1) / R;
-  int gx = (num_cu * WL_BATCH_WGS + a.u - 1) / a.u;
-  if (gx * 4 > ngroups) gx = (ngroups + 3) / 4;
-  if (gx < 1) gx = 1;
-  hipLaunchKernelGGL((gemv_batch_kernel<C, TM, R, NM>), dim3(gx, a.u), dim3(256), smem, st, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const int64_t n = (int64_t)a.T * a.rows;
-  hipLaunchKernelGGL(batch_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.part, NM, a.T,
-                     a.rows, S, W, y, ldy);
-  return hipGetLastError();
-}
-
-template <class C, int NM>
-static hipError_t launch_batch(const BatchArgs &a, int S, int W, float *y, int ldy, int num_cu, hipStream_t st) {
-  if (a.T <= 2) return launch_batch_tm<C, 2, NM>(a, S, W, y, ldy, num_cu, st);
-  if (a.T <= 4) return launch_batch_tm<C, 4, NM>(a, S, W, y, ldy, num_cu, st);
-  return launch_batch_tm<C, 8, NM>(a, S, W, y, ldy, num_cu, st);
+  return hipSuccess;
 }
 
 template <int NM>
-static hipError_t launch_batch_type(int type, const BatchArgs &a, int S, int W, float *y, int ldy, int num_cu,
-                                    hipStream_t st) {
+static hipError_t launch_batch_combine(const BatchArgs &a, hipStream_t st) {
+  int most = 0;
+  for (int i = 0; i < a.nmat; i++) most = a.m[i].rows > most ? a.m[i].rows : most;
+  const int64_t n = (int64_t)a.T * most;
+  hipLaunchKernelGGL(batch_combine_kernel<NM>, dim3((unsigned)((n + 255) / 256), a.nmat), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+template <class C, int TM, int NM>
+static hipError_t launch_batch_tm(BatchArgs a, int num_cu, hipStream_t st) {
+  constexpr int R = NM == 1 ? kBatchR1 : kBatchR2;
+  const size_t smem = batch_lds_bytes<C, TM>();
+  static bool raised = false;
+  hipError_t e = raise_lds(&gemv_batch_kernel<C, TM, R, NM>, smem, raised);
+  if (e != hipSuccess) return e;
+  const int gx = plan_batch(a, R, num_cu);
+  hipLaunchKernelGGL((gemv_batch_kernel<C, TM, R, NM>), dim3(gx, a.u), dim3(64 * kBatchWaves), smem, st, a);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  return launch_batch_combine<NM>(a, st);
+}
+
+template <int TM>
+static hipError_t launch_batch_mixed_tm(BatchArgs a, int num_cu, hipStream_t st) {
+  constexpr size_t s1 = batch_lds_bytes<Q4K, TM>(), s2 = batch_lds_bytes<Q6K, TM>(), s3 = batch_lds_bytes<Q80, TM>();
+  constexpr size_t smem = s1 > s2 ? (s1 > s3 ? s1 : s3) : (s2 > s3 ? s2 : s3);
+  static bool raised = false;
+  hipError_t e = raise_lds(&gemv_batch_mixed_kernel<TM>, smem, raised);
+  if (e != hipSuccess) return e;
+  const int gx = plan_batch(a, kBatchR1, num_cu);
+  hipLaunchKernelGGL((gemv_batch_mixed_kernel<TM>), dim3(gx, a.u), dim3(64 * kBatchWaves), smem, st, a);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  return launch_batch_combine<1>(a, st);
+}
+
+template <class C, int NM>
+static hipError_t launch_batch(const BatchArgs &a, int num_cu, hipStream_t st) {
+  if (a.T <= 2) return launch_batch_tm<C, 2, NM>(a, num_cu, st);
+  if (a.T <= 4) return launch_batch_tm<C, 4, NM>(a, num_cu, st);
+  return launch_batch_tm<C, 8, NM>(a, num_cu, st);
+}
+
+template <int NM>
+static hipError_t launch_batch_type(int type, const BatchArgs &a, int num_cu, hipStream_t st) {
   switch (type) {
-    case 12: return launch_batch<Q4K, NM>(a, S, W, y, ldy, num_cu, st);
-    case 14: return launch_batch<Q6K, NM>(a, S, W, y, ldy, num_cu, st);
-    case 8: return launch_batch<Q80, NM>(a, S, W, y, ldy, num_cu, st);
-    case 23: return launch_batch<IQ4XS, NM>(a, S, W, y, ldy, num_cu, st);
-    case 16: return launch_batch<IQ2XXS, NM>(a, S, W, y, ldy, num_cu, st);
+    case 12: return launch_batch<Q4K, NM>(a, num_cu, st);
+    case 14: return launch_batch<Q6K, NM>(a, num_cu, st);
+    case 8: return launch_batch<Q80, NM>(a, num_cu, st);
+    case 23: return launch_batch<IQ4XS, NM>(a, num_cu, st);
+    case 16: return launch_batch<IQ2XXS, NM>(a, num_cu, st);
   }
   return hipErrorInvalidValue;
 }
@@ -409,17 +515,29 @@ static hipError_t launch_batch_type(int type, const BatchArgs &a, int S, int W, 
 static hipError_t gemv_batch_run(const GemvMat *mats, int nmat, int nm, const float *x, int ldx, int cols, int T,
                                  float *scratch, int num_cu, hipStream_t st) {
   if (!WL_GEMV_BATCH || T < 2 || !scratch) return hipErrorNotSupported;
-  int S, W;
-  const int u = batch_columns(nmat, cols, &S, &W);
-  if (u == 0) return hipErrorNotSupported;
+  BatchArgs a{};
+  a.u = batch_columns(nmat, cols, &a.S, &a.W);
+  if (a.u == 0) return hipErrorNotSupported;
+  a.nmat = nmat;
+  a.cols = cols;
+  a.x = x;
+  a.ldx = ldx;
+  a.T = T;
+  bool same = true;
+  float *part = scratch;
   for (int i = 0; i < nmat; i++) {
     const GemvMat &m = mats[i];
-    const BatchArgs a{m.w, m.w2, m.row_bytes, m.rows, cols, x, ldx, T, scratch, u};
-    const hipError_t e = nm == 2 ? launch_batch_type<2>(m.type, a, S, W, m.y, m.ldy, num_cu, st)
-                                 : launch_batch_type<1>(m.type, a, S, W, m.y, m.ldy, num_cu, st);
-    if (e != hipSuccess) return e;
+    a.m[i] = BatchMat{m.w, m.w2, m.row_bytes, part, m.y, m.ldy, m.rows, m.type, 0};
+    part += (int64_t)a.u * nm * T * m.rows;
+    same = same && m.type == mats[0].type;
   }
-  return hipSuccess;
+  if (same) return nm == 2 ? launch_batch_type<2>(mats[0].type, a, num_cu, st)
+                           : launch_batch_type<1>(mats[0].type, a, num_cu, st);
+  for (int i = 0; i < nmat; i++)
+    if (!gemv_mixed_supports(mats[i].type)) return hipErrorNotSupported;
+  if (T <= 2) return launch_batch_mixed_tm<2>(a, num_cu, st);
+  if (T <= 4) return launch_batch_mixed_tm<4>(a, num_cu, st);
+  return launch_batch_mixed_tm<8>(a, num_cu, st);
 }
 
 hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int ldx, int cols, int T,
