@@ -44,28 +44,50 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + (float)exp((double)(-g))) * u;
 }
 
+// The partner exchanges of the folding tree. Bits 5 and 4 pair lane l with l^32 and l^16
+// through the permlane swaps, which deliver both partners' values in one instruction; bits 3..0
+// use DPP: l^8 (row_ror:8), l^7 within each eight lanes (row_half_mirror), l^2 and l^1
+// (quad_perm). Every partner flips the level's bit, so bit BIT of a lane still says which half
+// of the values it keeps.
+template <int BIT>
+__device__ __forceinline__ float dpp_partner(float x) {
+  constexpr int ctrl = BIT == 3 ? 0x128 : BIT == 2 ? 0x141 : BIT == 1 ? 0x4E : 0xB1;
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xF, 0xF, false));
+}
+
+// Lanes with bit BIT clear return a + (partner's a), the others b + (partner's b).
+template <int BIT>
+__device__ __forceinline__ float exch_pair(float a, float b, int lane) {
+  if constexpr (BIT == 5) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if constexpr (BIT == 4) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    const bool hi = (lane >> BIT) & 1;
+    const float send = hi ? a : b, keep = hi ? b : a;
+    return keep + dpp_partner<BIT>(send);
+  }
+}
+
 // Folds V = 2^k values per lane over the 64 lanes. Lane l returns the full sum of value
-// index (l >> (6-k)): the first k levels exchange halves of the value set between lane pairs
-// (l, l^32), (l, l^16), ...; the rest are a plain butterfly. Every value meets the same
-// pairwise tree as a plain 64-lane butterfly, whatever V is.
+// index (l >> (6-k)): the first k levels exchange halves of the value set between partner
+// lanes (bits 5, 4, ...), the rest fold the one remaining value. Every value is added over the
+// same pairwise tree (one pair per level), whatever V is.
 template <int V, int BIT>
 __device__ __forceinline__ float exch_reduce(const float *v, int lane) {
   if constexpr (V == 1) {
     float q = v[0];
     if constexpr (BIT >= 0) {
-#pragma unroll
-      for (int m = 1 << BIT; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+      q = exch_pair<BIT>(q, q, lane);
+      return exch_reduce<1, BIT - 1>(&q, lane);
     }
     return q;
   } else {
-    const bool hi = (lane >> BIT) & 1;
     float u[V / 2];
 #pragma unroll
-    for (int k = 0; k < V / 2; k++) {
-      const float send = hi ? v[k] : v[k + V / 2];
-      const float keep = hi ? v[k + V / 2] : v[k];
-      u[k] = keep + __shfl_xor(send, 1 << BIT, 64);
-    }
+    for (int k = 0; k < V / 2; k++) u[k] = exch_pair<BIT>(v[k], v[k + V / 2], lane);
     return exch_reduce<V / 2, BIT - 1>(u, lane);
   }
 }
