@@ -191,11 +191,11 @@ def main():
         "data": "synthetic seeded GGUF blocks (Q4_K/Q6_K), x ~ N(0,1)",
         "config": {"workload": "Llama-3.3-70B Q4_K_M decoder layer, 7 GEMVs (q,k,o,gate,up Q4_K; v,down Q6_K)",
                    "hidden": HIDDEN, "ffn": FFN, "heads": HEADS, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM,
-                   "batch": T, "layer_copies": args.copies, "launches_per_layer": 4,
+                   "batch": T, "layer_copies": args.copies, "matrix_calls_per_layer": 4,
                    "kernels": "int-dot (8-bit activations)" if args.int_dot else "fp32 decode GEMV"},
         "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "ms_per_layer": round(ms_layer, 5),
-        "tokens_per_s_80_layers": round(1000.0 / (LAYERS * ms_layer), 2),
+        "tokens_per_s_80_layers": round(1000.0 * T / (LAYERS * ms_layer), 2),
         "layer_algorithmic_bytes": layer_bytes,
         "per_launch_ms": {k: round(v, 5) for k, v in per.items()},
         "per_launch_gbs": {k: round(launch_bytes[k] / (per[k] * 1e-3) / 1e9, 1) for k in per},
