@@ -110,10 +110,18 @@ int wlo_layout(int t, int *be, int *bb)
     switch (t) {
     case WLO_F32: *be = 1; *bb = 4; return 1;
     case WLO_F16: case WLO_BF16: *be = 1; *bb = 2; return 1;
+    case WLO_Q4_0: *be = 32; *bb = 18; return 1;
+    case WLO_Q4_1: *be = 32; *bb = 20; return 1;
+    case WLO_Q5_0: *be = 32; *bb = 22; return 1;
+    case WLO_Q5_1: *be = 32; *bb = 24; return 1;
     case WLO_Q8_0: *be = 32; *bb = 34; return 1;
+    case WLO_Q2_K: *be = 256; *bb = 84; return 1;
+    case WLO_Q3_K: *be = 256; *bb = 110; return 1;
     case WLO_Q4_K: *be = 256; *bb = 144; return 1;
+    case WLO_Q5_K: *be = 256; *bb = 176; return 1;
     case WLO_Q6_K: *be = 256; *bb = 210; return 1;
     case WLO_IQ2_XXS: *be = 256; *bb = 66; return 1;
+    case WLO_IQ4_NL: *be = 32; *bb = 18; return 1;
     case WLO_IQ4_XS: *be = 256; *bb = 136; return 1;
     }
     *be = 0; *bb = 0;
@@ -128,7 +136,8 @@ int wlo_can_decode(int t)
 
 int wlo_can_dot(int t)
 {
-    return t == WLO_F32 || t == WLO_F16 || t == WLO_BF16 || t == WLO_Q8_0 || t == WLO_Q4_K || t == WLO_Q6_K;
+    return t == WLO_F32 || t == WLO_F16 || t == WLO_BF16 || t == WLO_Q4_0 || t == WLO_Q8_0 || t == WLO_Q4_K ||
+           t == WLO_Q5_K || t == WLO_Q6_K;
 }
 
 /* ------------------------------------------------------ I-quant tables (src/IqTables.cs) */
@@ -219,6 +228,155 @@ static void dec_q4_k(const uint8_t *b, int64_t n, float *y)
     }
 }
 
+/* src/Quants.cs:189-200: y = (nibble - 8) * d; low nibbles give values 0-15, high 16-31. */
+static void dec_q4_0(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 32; i++, b += 18, y += 32) {
+        float d = H(b);
+        const uint8_t *q = b + 2;
+        for (int j = 0; j < 16; j++) {
+            y[j] = (float)((q[j] & 0xF) - 8) * d;
+            y[j + 16] = (float)((q[j] >> 4) - 8) * d;
+        }
+    }
+}
+
+/* src/Quants.cs:202-214: y = nibble * d + m. */
+static void dec_q4_1(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 32; i++, b += 20, y += 32) {
+        float d = H(b), m = H(b + 2);
+        const uint8_t *q = b + 4;
+        for (int j = 0; j < 16; j++) {
+            y[j] = (float)(q[j] & 0xF) * d + m;
+            y[j + 16] = (float)(q[j] >> 4) * d + m;
+        }
+    }
+}
+
+/* src/Quants.cs:216-231: the fifth bit of value j is bit j of qh (value j + 16: bit j + 16);
+ * y = (q5 - 16) * d. */
+static void dec_q5_0(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 32; i++, b += 22, y += 32) {
+        float d = H(b);
+        uint32_t qh = U32(b + 2);
+        const uint8_t *q = b + 6;
+        for (int j = 0; j < 16; j++) {
+            int h0 = (int)(((qh >> j) << 4) & 0x10), h1 = (int)((qh >> (j + 12)) & 0x10);
+            y[j] = (float)(((q[j] & 0xF) | h0) - 16) * d;
+            y[j + 16] = (float)(((q[j] >> 4) | h1) - 16) * d;
+        }
+    }
+}
+
+/* src/Quants.cs:233-249: y = q5 * d + m. */
+static void dec_q5_1(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 32; i++, b += 24, y += 32) {
+        float d = H(b), m = H(b + 2);
+        uint32_t qh = U32(b + 4);
+        const uint8_t *q = b + 8;
+        for (int j = 0; j < 16; j++) {
+            int h0 = (int)(((qh >> j) << 4) & 0x10), h1 = (int)((qh >> (j + 12)) & 0x10);
+            y[j] = (float)((q[j] & 0xF) | h0) * d + m;
+            y[j + 16] = (float)((q[j] >> 4) | h1) * d + m;
+        }
+    }
+}
+
+/* src/Quants.cs:261-285: block = scales[16] | qs[64] | d | dmin. Each 128-value half reads
+ * 32 qs bytes four times (2-bit fields at shifts 0, 2, 4, 6); each run of 16 values takes
+ * one scale byte: dl = d * (s & 15), ml = dmin * (s >> 4), y = dl * q2 - ml. */
+static void dec_q2_k(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 256; i++, b += 84) {
+        const uint8_t *sc = b, *q = b + 16;
+        float d = H(b + 80), min = H(b + 82);
+        int idx = 0;
+        for (int k = 0; k < 256; k += 128, q += 32) {
+            for (int j = 0, shift = 0; j < 4; j++, shift += 2) {
+                for (int half = 0; half < 2; half++) {
+                    int s = sc[idx++];
+                    float dl = d * (float)(s & 0xF), ml = min * (float)(s >> 4);
+                    for (int l = 0; l < 16; l++) *y++ = dl * (float)((q[l + 16 * half] >> shift) & 3) - ml;
+                }
+            }
+        }
+    }
+}
+
+/* The sixteen 6-bit Q3_K scales from their 12 packed bytes, by the reference's kmask shuffle
+ * (src/Quants.cs:295-301): the low four bits of scale i are the low nibble of byte i (i < 8)
+ * or the high nibble of byte i - 8; the top two bits are bits 2*(i/4)..+1 of byte 8 + i%4. */
+static void q3k_scales(const uint8_t *s12, int *scales)
+{
+    uint32_t a0 = U32(s12), a1 = U32(s12 + 4), tmp = U32(s12 + 8);
+    uint32_t aux[4];
+    const uint32_t kmask1 = 0x03030303u, kmask2 = 0x0f0f0f0fu;
+    aux[2] = ((a0 >> 4) & kmask2) | (((tmp >> 4) & kmask1) << 4);
+    aux[3] = ((a1 >> 4) & kmask2) | (((tmp >> 6) & kmask1) << 4);
+    aux[0] = (a0 & kmask2) | (((tmp >> 0) & kmask1) << 4);
+    aux[1] = (a1 & kmask2) | (((tmp >> 2) & kmask1) << 4);
+    for (int i = 0; i < 16; i++) scales[i] = (int)(int8_t)(uint8_t)(aux[i / 4] >> (8 * (i % 4)));
+}
+
+/* src/Quants.cs:287-319: block = hmask[32] | qs[64] | scales[12] | d. Runs of 16 values as in
+ * Q2_K; the high bit of value l of run (k, j) is bit 4*(k/128) + j of hmask[l], and a clear
+ * bit subtracts 4: y = (d * (sc - 32)) * (q2 - (h ? 0 : 4)). */
+static void dec_q3_k(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 256; i++, b += 110) {
+        const uint8_t *hm = b, *q = b + 32;
+        float dall = H(b + 108);
+        int scales[16];
+        q3k_scales(b + 96, scales);
+        int idx = 0, m = 1;
+        for (int k = 0; k < 256; k += 128, q += 32) {
+            for (int j = 0, shift = 0; j < 4; j++, shift += 2, m <<= 1) {
+                for (int half = 0; half < 2; half++) {
+                    float dl = dall * (float)(scales[idx++] - 32);
+                    for (int l = 16 * half; l < 16 * half + 16; l++)
+                        *y++ = dl * (float)(((q[l] >> shift) & 3) - ((hm[l] & m) ? 0 : 4));
+                }
+            }
+        }
+    }
+}
+
+/* src/Quants.cs:352-370: as Q4_K with a fifth bit per value from qh[l] (bit 2j for the low
+ * nibbles of group j, bit 2j+1 for the high ones): y = d1 * q5 - m1. */
+static void dec_q5_k(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 256; i++, b += 176) {
+        float d = H(b), min = H(b + 2);
+        const uint8_t *sc = b + 4, *qh = b + 16, *ql = b + 48;
+        int idx = 0, u1 = 1, u2 = 2;
+        for (int j = 0; j < 256; j += 64, ql += 32, idx += 2, u1 <<= 2, u2 <<= 2) {
+            int s, m;
+            scale_min_k4(idx, sc, &s, &m);
+            float d1 = d * (float)s, m1 = min * (float)m;
+            scale_min_k4(idx + 1, sc, &s, &m);
+            float d2 = d * (float)s, m2 = min * (float)m;
+            for (int l = 0; l < 32; l++) *y++ = d1 * (float)((ql[l] & 0xF) + ((qh[l] & u1) ? 16 : 0)) - m1;
+            for (int l = 0; l < 32; l++) *y++ = d2 * (float)((ql[l] >> 4) + ((qh[l] & u2) ? 16 : 0)) - m2;
+        }
+    }
+}
+
+/* src/IQuants.cs:45-58: y = d * kvalues[nibble]; low nibbles give values 0-15, high 16-31. */
+static void dec_iq4_nl(const uint8_t *b, int64_t n, float *y)
+{
+    for (int64_t i = 0; i < n / 32; i++, b += 18, y += 32) {
+        float d = H(b);
+        const uint8_t *q = b + 2;
+        for (int j = 0; j < 16; j++) {
+            y[j] = d * (float)KVALUES[q[j] & 0xF];
+            y[j + 16] = d * (float)KVALUES[q[j] >> 4];
+        }
+    }
+}
+
 /* src/Quants.cs:372-396: y = (d * sc) * (q6 - 32). */
 static void dec_q6_k(const uint8_t *b, int64_t n, float *y)
 {
@@ -290,9 +448,17 @@ int wlo_decode_row(int t, const uint8_t *src, int64_t n, float *dst)
     case WLO_F32: memcpy(dst, src, (size_t)n * 4); return 0;
     case WLO_F16: for (int64_t i = 0; i < n; i++) dst[i] = H(src + 2 * i); return 0;
     case WLO_BF16: for (int64_t i = 0; i < n; i++) dst[i] = bf16_to_float((uint16_t)(src[2 * i] | src[2 * i + 1] << 8)); return 0;
+    case WLO_Q4_0: dec_q4_0(src, n, dst); return 0;
+    case WLO_Q4_1: dec_q4_1(src, n, dst); return 0;
+    case WLO_Q5_0: dec_q5_0(src, n, dst); return 0;
+    case WLO_Q5_1: dec_q5_1(src, n, dst); return 0;
     case WLO_Q8_0: dec_q8_0(src, n, dst); return 0;
+    case WLO_Q2_K: dec_q2_k(src, n, dst); return 0;
+    case WLO_Q3_K: dec_q3_k(src, n, dst); return 0;
     case WLO_Q4_K: dec_q4_k(src, n, dst); return 0;
+    case WLO_Q5_K: dec_q5_k(src, n, dst); return 0;
     case WLO_Q6_K: dec_q6_k(src, n, dst); return 0;
+    case WLO_IQ4_NL: dec_iq4_nl(src, n, dst); return 0;
     case WLO_IQ4_XS: dec_iq4_xs(src, n, dst); return 0;
     case WLO_IQ2_XXS: dec_iq2_xxs(src, n, dst); return 0;
     }
@@ -340,6 +506,39 @@ int wlo_dot_row(int t, const uint8_t *b, const float *x, int n, float *out)
             float s0 = 0, s1 = 0;
             for (int j = 0; j < 32; j += 2) { s0 += (float)q[j] * x[j]; s1 += (float)q[j + 1] * x[j + 1]; }
             sum += H(b) * (s0 + s1);
+        }
+        *out = sum;
+        return 0;
+    }
+    case WLO_Q4_0: {                          /* src/Quants.cs:98-109 */
+        float sum = 0;
+        for (int i = 0; i < n / 32; i++, b += 18, x += 32) {
+            const uint8_t *q = b + 2;
+            float s0 = 0, s1 = 0;
+            for (int j = 0; j < 16; j++) { s0 += (float)((q[j] & 0xF) - 8) * x[j]; s1 += (float)((q[j] >> 4) - 8) * x[j + 16]; }
+            sum += H(b) * (s0 + s1);
+        }
+        *out = sum;
+        return 0;
+    }
+    case WLO_Q5_K: {                          /* src/Quants.cs:134-158 */
+        float sum = 0;
+        for (int i = 0; i < n / 256; i++, b += 176) {
+            float d = H(b), min = H(b + 2);
+            const uint8_t *sc = b + 4, *qh = b + 16, *ql = b + 48;
+            int u1 = 1, u2 = 2;
+            for (int j = 0; j < 4; j++, ql += 32, x += 64, u1 <<= 2, u2 <<= 2) {
+                int s1, m1, s2, m2;
+                scale_min_k4(2 * j, sc, &s1, &m1);
+                scale_min_k4(2 * j + 1, sc, &s2, &m2);
+                float a1 = 0, a2 = 0, x1 = 0, x2 = 0;
+                for (int l = 0; l < 32; l++) {
+                    float xl = x[l], xh = x[l + 32];
+                    a1 += (float)((ql[l] & 0xF) + ((qh[l] & u1) ? 16 : 0)) * xl; x1 += xl;
+                    a2 += (float)((ql[l] >> 4) + ((qh[l] & u2) ? 16 : 0)) * xh; x2 += xh;
+                }
+                sum += d * ((float)s1 * a1 + (float)s2 * a2) - min * ((float)m1 * x1 + (float)m2 * x2);
+            }
         }
         *out = sum;
         return 0;
@@ -596,8 +795,11 @@ int wlo_moe_ffn(const float *logits, int ne, int k, int renorm,
 static int scale_fields(int t, int *f)
 {
     switch (t) {
-    case WLO_Q8_0: case WLO_IQ4_XS: case WLO_IQ2_XXS: f[0] = 0; return 1;
-    case WLO_Q4_K: f[0] = 0; f[1] = 2; return 2;
+    case WLO_Q4_0: case WLO_Q5_0: case WLO_Q8_0: case WLO_IQ4_NL: case WLO_IQ4_XS: case WLO_IQ2_XXS:
+        f[0] = 0; return 1;
+    case WLO_Q4_1: case WLO_Q5_1: case WLO_Q4_K: case WLO_Q5_K: f[0] = 0; f[1] = 2; return 2;
+    case WLO_Q2_K: f[0] = 80; f[1] = 82; return 2;
+    case WLO_Q3_K: f[0] = 108; return 1;
     case WLO_Q6_K: f[0] = 208; return 1;
     }
     return 0;
@@ -695,6 +897,41 @@ int wlo_int_dot(int t, const uint8_t *b, const int8_t *q, const float *d, const 
             int s0 = 0, s1 = 0;
             for (int j = 0; j < 32; j += 2) { s0 += w[j] * q[j]; s1 += w[j + 1] * q[j + 1]; }
             sum += H(b) * d[i] * (float)(s0 + s1);
+        }
+        *out = sum;
+        return 0;
+    }
+    case WLO_Q4_0: {                                          /* src/FastMath.cs:123-134 */
+        float sum = 0;
+        for (int i = 0; i < n / 32; i++, b += 18, q += 32) {
+            const uint8_t *w = b + 2;
+            int s0 = 0, s1 = 0;
+            for (int j = 0; j < 16; j++) { s0 += ((w[j] & 0xF) - 8) * q[j]; s1 += ((w[j] >> 4) - 8) * q[j + 16]; }
+            sum += H(b) * d[i] * (float)(s0 + s1);
+        }
+        *out = sum;
+        return 0;
+    }
+    case WLO_Q5_K: {                                          /* src/FastMath.cs:158-184 */
+        float sum = 0;
+        for (int i = 0; i < n / 256; i++, b += 176, q += 256, bsums += 16) {
+            float dd = H(b), dmin = H(b + 2);
+            const uint8_t *sc = b + 4, *qh = b + 16, *ql = b + 48;
+            int sumi = 0, summ = 0, u1 = 1, u2 = 2;
+            for (int j = 0; j < 4; j++, ql += 32, u1 <<= 2, u2 <<= 2) {
+                int s1, m1, s2, m2;
+                scale_min_k4(2 * j, sc, &s1, &m1);
+                scale_min_k4(2 * j + 1, sc, &s2, &m2);
+                const int8_t *qa = q + 64 * j, *qb = qa + 32;
+                int a1 = 0, a2 = 0;
+                for (int l = 0; l < 32; l++) {
+                    a1 += ((ql[l] & 0xF) + ((qh[l] & u1) ? 16 : 0)) * qa[l];
+                    a2 += ((ql[l] >> 4) + ((qh[l] & u2) ? 16 : 0)) * qb[l];
+                }
+                sumi += s1 * a1 + s2 * a2;
+                summ += m1 * (bsums[4 * j] + bsums[4 * j + 1]) + m2 * (bsums[4 * j + 2] + bsums[4 * j + 3]);
+            }
+            sum += d[i] * (dd * (float)sumi - dmin * (float)summ);
         }
         *out = sum;
         return 0;

@@ -20,8 +20,9 @@ extern "C" {
 
 /* ggml type ids (src/Gguf.cs:19-25). Only the ones this path decodes are named. */
 enum {
-    WLO_F32 = 0, WLO_F16 = 1, WLO_Q8_0 = 8, WLO_Q4_K = 12, WLO_Q6_K = 14,
-    WLO_IQ2_XXS = 16, WLO_IQ4_XS = 23, WLO_BF16 = 30
+    WLO_F32 = 0, WLO_F16 = 1, WLO_Q4_0 = 2, WLO_Q4_1 = 3, WLO_Q5_0 = 6, WLO_Q5_1 = 7,
+    WLO_Q8_0 = 8, WLO_Q2_K = 10, WLO_Q3_K = 11, WLO_Q4_K = 12, WLO_Q5_K = 13, WLO_Q6_K = 14,
+    WLO_IQ2_XXS = 16, WLO_IQ4_NL = 20, WLO_IQ4_XS = 23, WLO_BF16 = 30
 };
 
 /* fp16 -> fp32, exact incl. subnormals, Inf and NaN payloads (src/Half.cs:59-90). */

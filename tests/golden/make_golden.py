@@ -90,7 +90,8 @@ def quantizer_pins():
 
 # Tiny models whose weights use this path's formats (TinyModels.StandardSpecs, tests/TinyModels.cs:166-177).
 TINY_KEYS = ["llama-q4_K", "llama-q6_K", "llama-q8_0", "llama-q8_0-spm", "qwen2-q8_0", "qwen3-q4_K",
-             "qwen2-q6_K-tied"]
+             "qwen2-q6_K-tied", "llama-f32", "llama-f16", "llama-bf16", "llama-q4_0", "llama-q4_1",
+             "llama-q5_0", "llama-q5_1", "llama-q2_K", "llama-q3_K", "llama-q5_K"]
 LLAMA_CPP_FIXTURE = "/root/reference/tests/fixtures/llama-cpp-reference.txt"
 
 

@@ -108,10 +108,95 @@ def iq2_xxs(b, o, e, exact, grid):
     return d * (0.5 + (packed >> 28)) * 0.25 * g * sgn
 
 
+def _nibble(b, qs, e):
+    """Value e (0..31) of a 32-block's 16 nibble bytes at qs: low nibbles first, then high."""
+    byte = b[qs + e % 16]
+    return (byte & 15) if e < 16 else (byte >> 4)
+
+
+def q4_0(b, o, e, exact):
+    d, q = fp16(u16(b, o)), _nibble(b, o + 2, e) - 8
+    return np.float32(q) * np.float32(d) if exact else q * d
+
+
+def q4_1(b, o, e, exact):
+    d, m, q = fp16(u16(b, o)), fp16(u16(b, o + 2)), _nibble(b, o + 4, e)
+    return np.float32(q) * np.float32(d) + np.float32(m) if exact else q * d + m
+
+
+def q5_0(b, o, e, exact):
+    # the fifth bit of value e is bit e of the 32-bit qh field
+    d = fp16(u16(b, o))
+    q = (_nibble(b, o + 6, e) | (((u32(b, o + 2) >> e) & 1) << 4)) - 16
+    return np.float32(q) * np.float32(d) if exact else q * d
+
+
+def q5_1(b, o, e, exact):
+    d, m = fp16(u16(b, o)), fp16(u16(b, o + 2))
+    q = _nibble(b, o + 8, e) | (((u32(b, o + 4) >> e) & 1) << 4)
+    return np.float32(q) * np.float32(d) + np.float32(m) if exact else q * d + m
+
+
+def q2_k(b, o, e, exact):
+    # 128-value halves; in each, four 32-value runs read the half's 32 qs bytes at shifts 0, 2,
+    # 4, 6; every 16 values take one scale byte (low nibble scale, high nibble min)
+    half, r = e // 128, e % 128
+    j, l = r // 32, r % 32
+    q = (b[o + 16 + 32 * half + l] >> (2 * j)) & 3
+    s = b[o + 8 * half + 2 * j + l // 16]
+    d, dmin = fp16(u16(b, o + 80)), fp16(u16(b, o + 82))
+    if exact:
+        return np.float32(d) * np.float32(s & 15) * np.float32(q) - np.float32(dmin) * np.float32(s >> 4)
+    return d * (s & 15) * q - dmin * (s >> 4)
+
+
+def q3_k(b, o, e, exact):
+    # as Q2_K for the two low bits; the third bit of value (half, j, l) is bit 4*half + j of
+    # hmask[l] and a clear bit subtracts 4; the 6-bit scales are packed in 12 bytes at 96
+    half, r = e // 128, e % 128
+    j, l = r // 32, r % 32
+    q = ((b[o + 32 + 32 * half + l] >> (2 * j)) & 3) - (0 if (b[o + l] >> (4 * half + j)) & 1 else 4)
+    i = 8 * half + 2 * j + l // 16
+    low4 = (b[o + 96 + i] & 15) if i < 8 else (b[o + 96 + i - 8] >> 4)
+    high2 = (b[o + 104 + i % 4] >> (2 * (i // 4))) & 3
+    sc = (low4 | (high2 << 4)) - 32
+    d = fp16(u16(b, o + 108))
+    if exact:
+        return np.float32(d) * np.float32(sc) * np.float32(q)
+    return d * sc * q
+
+
+def q5_k(b, o, e, exact):
+    d, dmin = fp16(u16(b, o)), fp16(u16(b, o + 2))
+    sub = e // 32
+    pair, high = sub // 2, sub % 2
+    byte = b[o + 48 + 32 * pair + e % 32]
+    q = ((byte >> 4) if high else (byte & 15)) + 16 * ((b[o + 16 + e % 32] >> sub) & 1)
+    sc = b[o + 4: o + 16]
+    if sub < 4:
+        s, m = sc[sub] & 63, sc[sub + 4] & 63
+    else:
+        s = (sc[sub + 4] & 15) | ((sc[sub - 4] >> 6) << 4)
+        m = (sc[sub + 4] >> 4) | ((sc[sub] >> 6) << 4)
+    if exact:
+        return np.float32(d) * np.float32(s) * np.float32(q) - np.float32(dmin) * np.float32(m)
+    return d * s * q - dmin * m
+
+
+def iq4_nl(b, o, e, exact):
+    d, kv = fp16(u16(b, o)), KVALUES[_nibble(b, o + 2, e)]
+    return np.float32(d) * np.float32(kv) if exact else d * kv
+
+
+LAYOUT = {2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34), 10: (256, 84), 11: (256, 110),
+          12: (256, 144), 13: (256, 176), 14: (256, 210), 16: (256, 66), 20: (32, 18), 23: (256, 136)}
+
+
 def decode_blocks(t, data, nblocks, exact, grid=None):
     """All elements of nblocks consecutive blocks of type t (oracle type ids)."""
-    fn = {8: q8_0, 12: q4_k, 14: q6_k, 23: iq4_xs}
-    be, bb = {8: (32, 34), 12: (256, 144), 14: (256, 210), 16: (256, 66), 23: (256, 136)}[t]
+    fn = {2: q4_0, 3: q4_1, 6: q5_0, 7: q5_1, 8: q8_0, 10: q2_k, 11: q3_k, 12: q4_k, 13: q5_k,
+          14: q6_k, 20: iq4_nl, 23: iq4_xs}
+    be, bb = LAYOUT[t]
     out = np.empty(nblocks * be, np.float32 if exact else np.float64)
     data = [int(v) for v in data]
     for k in range(nblocks):

@@ -20,10 +20,12 @@ import oracle
 import refelem
 
 PINS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_pins.json")))
-TYPES = [oracle.Q8_0, oracle.Q4_K, oracle.Q6_K, oracle.IQ4_XS, oracle.IQ2_XXS]
+TYPES = [oracle.Q4_0, oracle.Q4_1, oracle.Q5_0, oracle.Q5_1, oracle.Q8_0, oracle.Q2_K, oracle.Q3_K,
+         oracle.Q4_K, oracle.Q5_K, oracle.Q6_K, oracle.IQ4_NL, oracle.IQ4_XS, oracle.IQ2_XXS]
 DBITS = [0x3A00, 0x3E00, 0x3800, 0xB400, 0x3C00]    # 0.75, 1.5, 0.5, -0.25, 1 (exact halves)
-D_FIELDS = {oracle.Q8_0: [0], oracle.Q4_K: [0, 2], oracle.Q6_K: [208], oracle.IQ4_XS: [0],
-            oracle.IQ2_XXS: [0]}
+D_FIELDS = {oracle.Q4_0: [0], oracle.Q4_1: [0, 2], oracle.Q5_0: [0], oracle.Q5_1: [0, 2], oracle.Q8_0: [0],
+            oracle.Q2_K: [80, 82], oracle.Q3_K: [108], oracle.Q4_K: [0, 2], oracle.Q5_K: [0, 2],
+            oracle.Q6_K: [208], oracle.IQ4_NL: [0], oracle.IQ4_XS: [0], oracle.IQ2_XXS: [0]}
 
 
 def random_blocks(t, nblocks, seed, dbits=None):
@@ -86,6 +88,78 @@ def test_q6k_hand_block():
         ql = b[64 * h + l + (32 if qd % 2 else 0)]
         q = ((ql >> 4) if qd >= 2 else (ql & 15)) | (((b[128 + 32 * h + l] >> (2 * qd)) & 3) << 4)
         assert y[e] == q - 32
+
+
+def test_q4_0_and_q4_1_hand_blocks():
+    # nibble j = j (low), 15 - j (high); Q4_0: d = 2 -> y = 2 (q - 8); Q4_1: d = 1, m = -0.5
+    qs = np.array([j | ((15 - j) << 4) for j in range(16)], np.uint8)
+    q = np.array(list(range(16)) + [15 - j for j in range(16)], np.float32)
+    b0 = np.concatenate([np.array([0x00, 0x40], np.uint8), qs])
+    assert np.array_equal(oracle.decode(oracle.Q4_0, b0, 32), 2 * (q - 8))
+    b1 = np.concatenate([np.array([0x00, 0x3C, 0x00, 0xB8], np.uint8), qs])
+    assert np.array_equal(oracle.decode(oracle.Q4_1, b1, 32), q - 0.5)
+
+
+def test_q5_hand_blocks():
+    # qh = 0xAAAA5555: value e has its fifth bit set when bit e of qh is set
+    qs = np.array([j | ((15 - j) << 4) for j in range(16)], np.uint8)
+    qh = 0xAAAA5555
+    q = np.array([(j if e < 16 else 15 - (e - 16)) | (((qh >> e) & 1) << 4)
+                  for e, j in zip(range(32), list(range(16)) * 2)], np.float32)
+    qhb = np.frombuffer(np.uint32(qh).tobytes(), np.uint8)
+    b0 = np.concatenate([np.array([0x00, 0x3C], np.uint8), qhb, qs])
+    assert np.array_equal(oracle.decode(oracle.Q5_0, b0, 32), q - 16)
+    b1 = np.concatenate([np.array([0x00, 0x38, 0x00, 0x3C], np.uint8), qhb, qs])   # d = 0.5, m = 1
+    assert np.array_equal(oracle.decode(oracle.Q5_1, b1, 32), 0.5 * q + 1)
+
+
+def test_q2k_q3k_hand_blocks():
+    # Q2_K: d = 1, dmin = 0.5, scale byte i = s | m << 4 with s = i % 7 + 1, m = i % 3:
+    # every run gives y = s * q2 - 0.5 * m
+    rng = oracle.Rng(9)
+    b = rng.bytes(84)
+    b[0:16] = [(i % 7 + 1) | ((i % 3) << 4) for i in range(16)]
+    b[80:84] = [0x00, 0x3C, 0x00, 0x38]
+    y = oracle.decode(oracle.Q2_K, b, 256)
+    for e in range(256):
+        h, r = e // 128, e % 128
+        j, l = r // 32, r % 32
+        q = (int(b[16 + 32 * h + l]) >> (2 * j)) & 3
+        i = 8 * h + 2 * j + l // 16
+        assert y[e] == (i % 7 + 1) * q - 0.5 * (i % 3), e
+    # Q3_K: d = 1, every scale 33 (6-bit 33 -> 33 - 32 = 1): y = q2 - (hbit ? 0 : 4)
+    c = rng.bytes(110)
+    c[96:104] = 0x11                   # low nibbles of all 16 scales = 1
+    c[104:108] = 0b10101010            # every 2-bit top field = 2: scale = 1 | 2 << 4 = 33
+    c[108:110] = [0x00, 0x3C]
+    y = oracle.decode(oracle.Q3_K, c, 256)
+    for e in range(256):
+        h, r = e // 128, e % 128
+        j, l = r // 32, r % 32
+        q2 = (int(c[32 + 32 * h + l]) >> (2 * j)) & 3
+        hb = (int(c[l]) >> (4 * h + j)) & 1
+        assert y[e] == q2 - (0 if hb else 4), e
+
+
+def test_q5k_hand_block():
+    # d = 1, dmin = 0; scales j + 1; qs nibbles from the pattern; qh bit sub of byte l set
+    # when (l + sub) is even: y = (j + 1) * (nibble + 16 * bit)
+    b = np.zeros(176, np.uint8)
+    b[0:2] = [0x00, 0x3C]
+    s = [j + 1 for j in range(8)]
+    for j in range(4):
+        b[4 + j] = s[j] | ((s[j + 4] >> 4) << 6)
+        b[12 + j] = s[j + 4] & 15
+    for l in range(32):
+        b[16 + l] = sum(1 << sub for sub in range(8) if (l + sub) % 2 == 0)
+    for l in range(128):
+        b[48 + l] = (l % 16) | ((15 - l % 16) << 4)
+    y = oracle.decode(oracle.Q5_K, b, 256)
+    for e in range(256):
+        sub, l = e // 32, e % 32
+        nib = (l % 16) if sub % 2 == 0 else 15 - (l % 16)
+        q = nib + 16 * ((l + sub) % 2 == 0)
+        assert y[e] == s[sub] * q, e
 
 
 def test_q8_0_hand_block():

@@ -12,14 +12,14 @@ import pytest
 
 import oracle
 
-DOT_TYPES = [oracle.F32, oracle.F16, oracle.BF16, oracle.Q8_0, oracle.Q4_K, oracle.Q6_K]
-ALL_TYPES = DOT_TYPES + [oracle.IQ4_XS, oracle.IQ2_XXS]
+# Quants.CanDot (src/Quants.cs:56-65)
+DOT_TYPES = [oracle.F32, oracle.F16, oracle.BF16, oracle.Q4_0, oracle.Q8_0, oracle.Q4_K, oracle.Q5_K,
+             oracle.Q6_K]
+ALL_TYPES = DOT_TYPES + [oracle.Q4_1, oracle.Q5_0, oracle.Q5_1, oracle.Q2_K, oracle.Q3_K, oracle.IQ4_NL,
+                         oracle.IQ4_XS, oracle.IQ2_XXS]
 
 
 def _mat(t, rows, cols, seed, rms=0.5):
-    if t in (oracle.IQ4_XS, oracle.IQ2_XXS):
-        # Matrix() has no scale-field rule for them beyond d at offset 0, which it supports.
-        pass
     return oracle.matrix(oracle.Rng(seed), t, rows, cols, rms)
 
 
@@ -105,11 +105,11 @@ def test_block_is_one_chain_in_index_order():
 def test_int_dot_matches_dequantized_activation_reference():
     # tests/FastMathTests.cs:74-111: the integer kernel equals decode x dequantized activations
     # in double at 1e-4*mag + 1e-5, and stays within 0.03*mag of the float dot.
-    for t in (oracle.Q8_0, oracle.Q4_K, oracle.Q6_K):
+    for t in (oracle.Q8_0, oracle.Q4_0, oracle.Q4_K, oracle.Q5_K, oracle.Q6_K):   # FastMath.CanIntDot
         cols, rows, T = 512, 4, 3
         data = oracle.matrix(oracle.Rng(5), t, rows, cols, 0.5)
         x = oracle.Rng(11).normals(T * cols).reshape(T, cols)
-        k = t != oracle.Q8_0
+        k = t not in (oracle.Q8_0, oracle.Q4_0)
         bs = 256 if k else 32
         rb = oracle.row_bytes(t, cols)
         for r in range(rows):

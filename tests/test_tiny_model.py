@@ -57,6 +57,28 @@ def test_bar_rejects_broken_products():
         assert rel > 0.2 or agree < len(PROBE) - 1, key
 
 
+# A dropped term of each newer format's decode, planted in the block bytes: (block bytes, first
+# byte, end byte, mask kept). Q5_0/Q5_K: the fifth bits; Q3_K: the high-bit mask (every value
+# then loses 4); Q4_1: the high nibbles; Q2_K: the 2-bit fields above shift 0.
+DROPPED = {"llama-q5_0": (22, 2, 6, 0x00), "llama-q5_K": (176, 16, 48, 0x00), "llama-q3_K": (110, 0, 32, 0x00),
+           "llama-q4_1": (20, 4, 20, 0x0F), "llama-q2_K": (84, 16, 80, 0x03)}
+
+
+@pytest.mark.parametrize("key", sorted(DROPPED))
+def test_bar_rejects_a_dropped_term(key):
+    """The llama.cpp bar pins the newer decoders: the same model with one field of every block
+    masked before the products fails it."""
+    bb, lo, hi, keep = DROPPED[key]
+
+    def dropped(name, w, x):
+        data = w.data.copy().reshape(-1, bb)
+        data[:, lo:hi] &= keep
+        return oracle_matmul(name, type(w)(w.type, w.rows, w.cols, data.reshape(-1)), x)
+
+    rel, agree = llama_cpp_bar(key, Model(key, dropped).forward(PROBE, 0))
+    assert rel > 0.2 or agree < len(PROBE) - 1, (key, rel, agree)
+
+
 @pytest.fixture(scope="module")
 def gpu():
     from windlass_amd.backend import Context
@@ -79,8 +101,14 @@ def gpu_matmul(ctx):
     return mm, cache
 
 
+def _gpu_keys():
+    """The models whose weight format the library multiplies (wl_can_matmul runs on the host)."""
+    from windlass_amd._lib import load
+    return [k for k in KEYS if load().wl_can_matmul(SPECS[k][1])]
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("key", KEYS)
+@pytest.mark.parametrize("key", _gpu_keys())
 def test_gpu_greedy_tokens_match_cpu(gpu, key):
     mm, cache = gpu_matmul(gpu)
     cpu, dev = Model(key, oracle_matmul), Model(key, mm)

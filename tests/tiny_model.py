@@ -18,6 +18,16 @@ F32 = np.float32
 # TinySpec defaults (tests/TinyModels.cs:105-115) and the keys of TinyModels.StandardSpecs on this
 # path's formats (:166-177)
 SPECS = {
+    "llama-f32": ("llama", 0, False, False),
+    "llama-f16": ("llama", 1, False, False),
+    "llama-bf16": ("llama", 30, False, False),
+    "llama-q4_0": ("llama", 2, False, False),
+    "llama-q4_1": ("llama", 3, False, False),
+    "llama-q5_0": ("llama", 6, False, False),
+    "llama-q5_1": ("llama", 7, False, False),
+    "llama-q2_K": ("llama", 10, False, False),
+    "llama-q3_K": ("llama", 11, False, False),
+    "llama-q5_K": ("llama", 13, False, False),
     "llama-q4_K": ("llama", 12, False, False),
     "llama-q6_K": ("llama", 14, False, False),
     "llama-q8_0": ("llama", 8, False, False),
