@@ -68,11 +68,13 @@ def tables():
         "iq2xxs_grid_spots": {"0": "0x0808080808080808", "1": "0x080808080808082b",
                               "3": "0x0808080808082b08"},
         "iq2xxs_grid_bytes": [8, 0x19, 0x2B],
-        "ids": {"f32": 0, "f16": 1, "q8_0": 8, "q4_K": 12, "q6_K": 14, "iq2_xxs": 16, "iq4_xs": 23,
+        "ids": {"f32": 0, "f16": 1, "q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q8_0": 8, "q2_K": 10,
+                "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14, "iq2_xxs": 16, "iq4_nl": 20, "iq4_xs": 23,
                 "bf16": 30},
-        "layouts": {"q8_0": [32, 34], "q4_K": [256, 144], "q6_K": [256, 210],
-                    "iq2_xxs": [256, 66], "iq4_xs": [256, 136], "f32": [1, 4], "f16": [1, 2],
-                    "bf16": [1, 2]},
+        "layouts": {"q4_0": [32, 18], "q4_1": [32, 20], "q5_0": [32, 22], "q5_1": [32, 24],
+                    "q8_0": [32, 34], "q2_K": [256, 84], "q3_K": [256, 110], "q4_K": [256, 144],
+                    "q5_K": [256, 176], "q6_K": [256, 210], "iq2_xxs": [256, 66], "iq4_nl": [32, 18],
+                    "iq4_xs": [256, 136], "f32": [1, 4], "f16": [1, 2], "bf16": [1, 2]},
         "layout_source": "src/Gguf.cs:30-66; tests/IQuantTests.cs:375-380",
     }
 
