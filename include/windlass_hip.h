@@ -36,10 +36,18 @@ extern "C" {
 /* ggml type ids (enum GgmlType, src/Gguf.cs:19-25). */
 #define WL_TYPE_F32 0
 #define WL_TYPE_F16 1
+#define WL_TYPE_Q4_0 2
+#define WL_TYPE_Q4_1 3
+#define WL_TYPE_Q5_0 6
+#define WL_TYPE_Q5_1 7
 #define WL_TYPE_Q8_0 8
+#define WL_TYPE_Q2_K 10
+#define WL_TYPE_Q3_K 11
 #define WL_TYPE_Q4_K 12
+#define WL_TYPE_Q5_K 13
 #define WL_TYPE_Q6_K 14
 #define WL_TYPE_IQ2_XXS 16
+#define WL_TYPE_IQ4_NL 20
 #define WL_TYPE_IQ4_XS 23
 #define WL_TYPE_BF16 30
 

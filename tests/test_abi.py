@@ -44,14 +44,16 @@ def test_nm_dynamic_symbols():
 def test_type_queries_match_reference_layouts():
     L = windlass_amd.load()
     # src/Gguf.cs:30-66
-    want = {0: (1, 4), 1: (1, 2), 30: (1, 2), 8: (32, 34), 12: (256, 144), 14: (256, 210),
-            16: (256, 66), 23: (256, 136)}
+    want = {0: (1, 4), 1: (1, 2), 30: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24),
+            8: (32, 34), 10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210),
+            16: (256, 66), 20: (32, 18), 23: (256, 136)}
     for t, lay in want.items():
         assert windlass_amd.layout(t) == lay
         assert L.wl_can_decode(t) == 1
     for t in (8, 12, 14, 16, 23):
         assert L.wl_can_matmul(t) == 1
-    for t in (2, 3, 6, 7, 10, 11, 13, 15, 17, 18, 19, 20, 21, 22, 29):
+    # Q8_1, Q8_K (activation formats) and the I-quants whose grids have no source here
+    for t in (9, 15, 17, 18, 19, 21, 22, 29):
         assert L.wl_can_decode(t) == 0 and L.wl_can_matmul(t) == 0
     assert windlass_amd.Quants.CanDecode(windlass_amd.GgmlType.Q4_K)
     assert L.wl_version() >= 100

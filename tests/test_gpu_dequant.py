@@ -5,7 +5,8 @@ import numpy as np
 import pytest
 
 import oracle
-from gpu_common import QTYPES, blocks
+from gpu_common import ALLQ, FLOATS, blocks
+from windlass_amd.synth import scale_fields
 from windlass_amd.backend import Context, GgmlType, layout
 
 pytestmark = pytest.mark.gpu
@@ -27,7 +28,7 @@ def _bits(a):
     return b
 
 
-@pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
+@pytest.mark.parametrize("t", ALLQ + FLOATS, ids=lambda t: t.name)
 @pytest.mark.parametrize("shape", [(1, 256), (7, 1024), (300, 2048)])
 def test_random_blocks_bit_exact(ctx, t, shape):
     rows, cols = shape
@@ -43,7 +44,7 @@ def test_random_blocks_bit_exact(ctx, t, shape):
     w.free()
 
 
-@pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
+@pytest.mark.parametrize("t", ALLQ, ids=lambda t: t.name)
 def test_every_fp16_scale_class(ctx, t):
     # one block per interesting fp16 pattern in every scale field
     specials = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x8201, 0x0400, 0x3C00, 0xBC00, 0x7BFF,
@@ -52,8 +53,7 @@ def test_every_fp16_scale_class(ctx, t):
     nblk = len(specials)
     cols = be * nblk
     data = blocks(t, 1, cols, seed=5).reshape(nblk, bb)
-    fields = {GgmlType.Q8_0: [0], GgmlType.Q4_K: [0, 2], GgmlType.Q6_K: [208],
-              GgmlType.IQ4_XS: [0], GgmlType.IQ2_XXS: [0]}[t]
+    fields = scale_fields(t)
     for i, h in enumerate(specials):
         for k, f in enumerate(fields):
             hv = int(specials[(i + 3 * k) % nblk])
@@ -67,16 +67,16 @@ def test_every_fp16_scale_class(ctx, t):
     w.free()
 
 
-@pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
+@pytest.mark.parametrize("t", ALLQ, ids=lambda t: t.name)
 @pytest.mark.parametrize("fill", [0x00, 0xFF])
 def test_payload_fills(ctx, t, fill):
     be, bb = layout(t)
     data = np.full((4, bb), fill, np.uint8)
     data.reshape(-1)[:] = fill
     for i, h in enumerate([0x3A00, 0x3E00, 0x0001, 0xB400]):
-        off = 208 if t == GgmlType.Q6_K else 0
-        data[i, off] = h & 0xFF
-        data[i, off + 1] = h >> 8
+        for off in scale_fields(t):
+            data[i, off] = h & 0xFF
+            data[i, off + 1] = h >> 8
     data = data.reshape(-1)
     w = ctx.upload(t, data, 1, 4 * be)
     got = w.decode()

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle
-from gpu_common import GEMM_REL, QTYPES, bf16_round, blocks, decoded, tol_check
+from gpu_common import FLOATS, GEMM_REL, NEWQ, QTYPES, bf16_round, blocks, decoded, tol_check
 from windlass_amd import Transformer
 from windlass_amd.backend import Context, GgmlType
 
@@ -31,8 +31,12 @@ def ctx():
     c.close()
 
 
-@pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
-@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "%dx%dxT%d" % s)
+# the other formats on three shapes: a single tile, a split-K launch and a 9-token tail
+CASES = [(t, s) for t in QTYPES for s in SHAPES] + [
+    (t, s) for t in NEWQ + FLOATS for s in [(128, 256, 128), (200, 1024, 37), (300, 2048, 9)]]
+
+
+@pytest.mark.parametrize("t,shape", CASES, ids=lambda v: v.name if hasattr(v, "name") else "%dx%dxT%d" % v)
 def test_gemm_bars(ctx, t, shape):
     rows, cols, T = shape
     data = blocks(t, rows, cols, seed=rows * 7 + cols + int(t))

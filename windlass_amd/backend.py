@@ -16,10 +16,18 @@ class GgmlType(IntEnum):
     """enum GgmlType (src/Gguf.cs:19-25), the ids this backend handles."""
     F32 = 0
     F16 = 1
+    Q4_0 = 2
+    Q4_1 = 3
+    Q5_0 = 6
+    Q5_1 = 7
     Q8_0 = 8
+    Q2_K = 10
+    Q3_K = 11
     Q4_K = 12
+    Q5_K = 13
     Q6_K = 14
     IQ2_XXS = 16
+    IQ4_NL = 20
     IQ4_XS = 23
     BF16 = 30
 

@@ -72,10 +72,18 @@ static const char *type_name(int t) {
     case WL_TYPE_F32: return "f32";
     case WL_TYPE_F16: return "f16";
     case WL_TYPE_BF16: return "bf16";
+    case WL_TYPE_Q4_0: return "q4_0";
+    case WL_TYPE_Q4_1: return "q4_1";
+    case WL_TYPE_Q5_0: return "q5_0";
+    case WL_TYPE_Q5_1: return "q5_1";
     case WL_TYPE_Q8_0: return "q8_0";
+    case WL_TYPE_Q2_K: return "q2_K";
+    case WL_TYPE_Q3_K: return "q3_K";
     case WL_TYPE_Q4_K: return "q4_K";
+    case WL_TYPE_Q5_K: return "q5_K";
     case WL_TYPE_Q6_K: return "q6_K";
     case WL_TYPE_IQ2_XXS: return "iq2_xxs";
+    case WL_TYPE_IQ4_NL: return "iq4_nl";
     case WL_TYPE_IQ4_XS: return "iq4_xs";
   }
   return "type";
@@ -86,10 +94,18 @@ extern "C" int wl_type_layout(int t, int *be, int *bb) {
   switch (t) {
     case WL_TYPE_F32: e = 1; b = 4; break;
     case WL_TYPE_F16: case WL_TYPE_BF16: e = 1; b = 2; break;
+    case WL_TYPE_Q4_0: e = 32; b = 18; break;
+    case WL_TYPE_Q4_1: e = 32; b = 20; break;
+    case WL_TYPE_Q5_0: e = 32; b = 22; break;
+    case WL_TYPE_Q5_1: e = 32; b = 24; break;
     case WL_TYPE_Q8_0: e = 32; b = 34; break;
+    case WL_TYPE_Q2_K: e = 256; b = 84; break;
+    case WL_TYPE_Q3_K: e = 256; b = 110; break;
     case WL_TYPE_Q4_K: e = 256; b = 144; break;
+    case WL_TYPE_Q5_K: e = 256; b = 176; break;
     case WL_TYPE_Q6_K: e = 256; b = 210; break;
     case WL_TYPE_IQ2_XXS: e = 256; b = 66; break;
+    case WL_TYPE_IQ4_NL: e = 32; b = 18; break;
     case WL_TYPE_IQ4_XS: e = 256; b = 136; break;
   }
   if (be) *be = e;

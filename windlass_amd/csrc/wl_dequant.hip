@@ -6,6 +6,7 @@
 // the fp16 scales are decoded from their bit fields (subnormals, Inf and NaN payloads exact).
 #include "wl_dequant.h"
 
+#include "wl_blocks.h"
 #include "wl_device.h"
 #include "wl_tables.h"
 
@@ -130,6 +131,20 @@ struct DqBF16 {
   }
 };
 
+// The formats of wl_blocks.h: one work item = 16 values of a block.
+template <class B>
+struct DqBlk {
+  static constexpr int BLOCK = B::BLOCK, BYTES = B::BYTES, CHUNKS = B::BLOCK / 16;
+  __device__ static void run(const uint8_t *b, int c, float *y) {
+    typename B::Raw r;
+    B::load(b, 16 * c, r);
+    float v[16];
+    B::dec(r, 16 * c, v);
+#pragma unroll
+    for (int j = 0; j < 16; j++) y[16 * c + j] = v[j];
+  }
+};
+
 template <class D>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
                                                       int64_t row0, int64_t nrows, int64_t cols,
@@ -159,7 +174,8 @@ static hipError_t launch(const uint8_t *w, int64_t row_bytes, int64_t row0, int6
 
 bool dequant_supports(int type) {
   switch (type) {
-    case 0: case 1: case 30: case 8: case 12: case 14: case 23: case 16: return true;
+    case 0: case 1: case 30: case 8: case 12: case 14: case 23: case 16:
+    case 2: case 3: case 6: case 7: case 10: case 11: case 13: case 20: return true;
   }
   return false;
 }
@@ -175,6 +191,14 @@ hipError_t dequant_launch(int type, const uint8_t *w, int64_t row_bytes, int64_t
     case 14: return launch<DqQ6K>(w, row_bytes, row0, nrows, cols, dst, st);
     case 23: return launch<DqIQ4XS>(w, row_bytes, row0, nrows, cols, dst, st);
     case 16: return launch<DqIQ2XXS>(w, row_bytes, row0, nrows, cols, dst, st);
+    case 2: return launch<DqBlk<BQ40>>(w, row_bytes, row0, nrows, cols, dst, st);
+    case 3: return launch<DqBlk<BQ41>>(w, row_bytes, row0, nrows, cols, dst, st);
+    case 6: return launch<DqBlk<BQ50>>(w, row_bytes, row0, nrows, cols, dst, st);
+    case 7: return launch<DqBlk<BQ51>>(w, row_bytes, row0, nrows, cols, dst, st);
+    case 10: return launch<DqBlk<BQ2K>>(w, row_bytes, row0, nrows, cols, dst, st);
+    case 11: return launch<DqBlk<BQ3K>>(w, row_bytes, row0, nrows, cols, dst, st);
+    case 13: return launch<DqBlk<BQ5K>>(w, row_bytes, row0, nrows, cols, dst, st);
+    case 20: return launch<DqBlk<BIQ4NL>>(w, row_bytes, row0, nrows, cols, dst, st);
   }
   return hipErrorInvalidValue;
 }

@@ -105,6 +105,23 @@ __device__ __forceinline__ uint32_t ldw4(gu32 *p) {
   else return *p;
 }
 
+// N (multiple of 4) bytes starting at a 2-byte aligned address: the dword window holding them
+// (N/4 + 1 dwords) and the bit offset of the first byte.
+template <int N>
+struct Win {
+  uint32_t w[N / 4 + 1];
+  uint32_t sh;
+  __device__ void load(const uint8_t *p) {
+    gu32 *a = align4_down(p);
+    sh = misalign4(p) * 8;
+#pragma unroll
+    for (int i = 0; i <= N / 4; i++) w[i] = a[i];
+  }
+  // dword i of the N bytes, and byte i
+  __device__ uint32_t dw(int i) const { return __builtin_amdgcn_alignbit(w[i + 1], w[i], sh); }
+  __device__ uint32_t byte(int i) const { return (dw(i / 4) >> (8 * (i % 4))) & 0xFFu; }
+};
+
 __device__ __forceinline__ void ld_x16(const float *p, float *v) {
   const float4 *q = reinterpret_cast<const float4 *>(p);
 #pragma unroll

@@ -14,6 +14,7 @@
 // With A = weights and B = tokens, a lane's four results are four consecutive rows of one token.
 #include "wl_gemm.h"
 
+#include "wl_blocks.h"
 #include "wl_device.h"
 #include "wl_codecs.h"
 #include "wl_tables.h"
@@ -35,21 +36,6 @@ constexpr int LDK = BK + 8;
 #ifndef WL_GEMM_WPE
 #define WL_GEMM_WPE 2  // waves per SIMD the register budget must allow
 #endif
-
-// n (multiple of 4) bytes starting at a 2-byte aligned address: the dword window holding them
-// (N/4 + 1 dwords) and the bit offset of the first byte.
-template <int N>
-struct Win {
-  uint32_t w[N / 4 + 1];
-  uint32_t sh;
-  __device__ void load(const uint8_t *p) {
-    gu32 *a = align4_down(p);
-    sh = misalign4(p) * 8;
-#pragma unroll
-    for (int i = 0; i <= N / 4; i++) w[i] = a[i];
-  }
-  __device__ uint32_t dw(int i) const { return __builtin_amdgcn_alignbit(w[i + 1], w[i], sh); }
-};
 
 __device__ __forceinline__ uint32_t half_at(uint32_t dword, uint32_t byte_off) { return (dword >> (8 * byte_off)) & 0xFFFFu; }
 
@@ -218,6 +204,21 @@ struct GIQ2XXS {
 };
 
 // x [T][cols] fp32 -> xb [T][cols] bf16.
+// The formats of wl_blocks.h: their exact fp32 values rounded to bf16.
+template <class B>
+struct GBlk {
+  struct Raw { typename B::Raw r; };
+  __device__ static void load(const uint8_t *row, int k, Raw &r) {
+    B::load(row + (k / B::BLOCK) * B::BYTES, k % B::BLOCK, r.r);
+  }
+  __device__ static void dec(const Raw &r, int k, uint32_t *o) {
+    float y[16];
+    B::dec(r.r, k % B::BLOCK, y);
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = pk(y[2 * i], y[2 * i + 1]);
+  }
+};
+
 __global__ __launch_bounds__(256) void to_bf16_kernel(const float *__restrict__ x, int64_t n4,
                                                       uint2 *__restrict__ xb) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
@@ -400,7 +401,13 @@ static hipError_t launch(const uint8_t *w, int64_t row_bytes, int rows, int cols
   return hipGetLastError();
 }
 
-bool gemm_supports(int type) { return type == 8 || type == 12 || type == 14 || type == 23 || type == 16; }
+bool gemm_supports(int type) {
+  switch (type) {
+    case 0: case 1: case 2: case 3: case 6: case 7: case 8: case 10: case 11: case 12: case 13: case 14: case 16:
+    case 20: case 23: case 30: return true;
+  }
+  return false;
+}
 
 hipError_t gemm_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, int cols, const float *x, int T,
                        float *y, int ldy, void *scratch, int num_cu, hipStream_t st) {
@@ -422,6 +429,17 @@ hipError_t gemm_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, 
     case 14: return launch<GQ6K>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
     case 23: return launch<GIQ4XS>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
     case 16: return launch<GIQ2XXS>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 0: return launch<GBlk<BF32>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 1: return launch<GBlk<BF16h>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 30: return launch<GBlk<BBF16>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 2: return launch<GBlk<BQ40>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 3: return launch<GBlk<BQ41>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 6: return launch<GBlk<BQ50>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 7: return launch<GBlk<BQ51>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 10: return launch<GBlk<BQ2K>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 11: return launch<GBlk<BQ3K>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 13: return launch<GBlk<BQ5K>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 20: return launch<GBlk<BIQ4NL>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
   }
   return hipErrorInvalidValue;
 }
