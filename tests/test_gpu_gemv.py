@@ -92,7 +92,7 @@ def test_errors(ctx):
     with pytest.raises(windlass_amd.ArgumentOutOfRangeError):
         w.Slice(1)
     with pytest.raises(windlass_amd.NotSupportedError):
-        ctx.upload(11, np.zeros(110, np.uint8), 1, 256)   # Q3_K: not on this path
+        ctx.upload(18, np.zeros(98, np.uint8), 1, 256)    # IQ3_XXS: its grid has no source here
     with pytest.raises(windlass_amd.ShapeError):
         ctx.upload(GgmlType.Q4_K, np.zeros(144, np.uint8), 1, 300)
     w.free()

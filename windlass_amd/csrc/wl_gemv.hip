@@ -10,49 +10,16 @@
 // registers, the chunks' partial sums go to scratch, and a combine launch adds them in chunk
 // order: y = ((chunk 0 + chunk 1) + chunk 2) + ... The cut depends only on the row length and
 // the number of matrices, so a token's bits do not depend on how many tokens share the launch.
-#include "wl_gemv.h"
-#include "wl_gemv_impl.h"
+#include "wl_gemv_launch.h"
 
-#pragma clang fp contract(off)
+extern "C" int wl_type_layout(int ggml_type, int *block_elems, int *block_bytes);
 
 namespace wl {
 
-extern "C" __shared__ uint8_t wl_dyn_lds[];
-
-__device__ __forceinline__ int find_seg(const GemvParams &p) {
-  int si = 0;
-#pragma unroll
-  for (int i = 1; i < GEMV_MAX_SEGS; i++)
-    if (i < p.nseg && (int)blockIdx.x >= p.seg[i].wg_begin) si = i;
-  return si;
-}
-
-// split: the segment writes partials; for the SwiGLU pair the up partial follows the gate
-// partial at out + T * ldo.
-template <class C, int TM, int R, int NM, int SP>
-__device__ __forceinline__ void run_seg(const GemvParams &p, const GemvSeg &s, int split) {
-  const CsRows W{s.w, s.w2, s.row_bytes, s.rows};
-  float *y2 = (NM == 2 && split) ? s.out + (int64_t)p.T * s.ldo : nullptr;
-  const CsIO io{p.x + s.col0, nullptr, p.ldx, s.out, nullptr, s.ldo, p.T, y2};
-  cs_gemv<C, TM, R, NM, SP>(W, io, p.cols, (int)blockIdx.x - s.wg_begin, s.nwg, wl_dyn_lds);
-}
-
-template <class C, int TM, int R, int NM, int SP>
-__global__ __launch_bounds__(64 * kMaxWaves) void gemv_kernel(GemvParams p, int split) {
-  run_seg<C, TM, R, NM, SP>(p, p.seg[find_seg(p)], split);
-}
-
-// Rows per group: V = NM*R*TM partials per lane go through the exchange butterfly.
-template <class C, int TM, int NM>
-constexpr int rows_per_group() {
-  return TM == 1 ? (NM == 1 ? C::R1 : C::R1 / 2) : (NM == 1 ? 4 : 2);
-}
-
-static int rows_per_group_rt(int type, int tm, int nm) {
-  if (tm > 1) return nm == 1 ? 4 : 2;
-  const int r1 = type == 12 ? Q4K::R1 : type == 14 ? Q6K::R1 : type == 8 ? Q80::R1 : type == 23 ? IQ4XS::R1
-                                                                                                    : IQ2XXS::R1;
-  return nm == 1 ? r1 : r1 / 2;
+// Rows per group of the mixed kernel's codecs.
+static int mixed_rows_per_group(int type, int tm) {
+  if (tm > 1) return 4;
+  return type == 12 ? Q4K::R1 : type == 14 ? Q6K::R1 : Q80::R1;
 }
 
 // Segments of different formats in one launch (q/k Q4_K with v Q6_K): the codec is chosen
@@ -67,6 +34,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_mixed_kernel(GemvParams p
     default: break;
   }
 }
+
 
 // y = the chunk partials added in chunk order (SwiGLU pair: silu(gate sum) * (up sum)).
 struct CombineParams {
@@ -137,70 +105,11 @@ int64_t gemv_scratch_floats(const GemvMat *mats, int nmat, int nm, int cols, int
   return n > nb ? n : nb;
 }
 
-// Grid: about kWavesPerCu waves per CU, split over the segments in proportion to their groups.
-static int plan_grid(GemvParams &p, int tm, int nm, int nwv, int num_cu) {
-  int total = 0, groups[GEMV_MAX_SEGS];
-  for (int i = 0; i < p.nseg; i++) {
-    const int R = rows_per_group_rt(p.seg[i].type, tm, nm);
-    groups[i] = (p.seg[i].rows + R - 1) / R;
-    total += groups[i];
-  }
-  if (total == 0) return 0;
-  const int target = (num_cu * kWavesPerCu + nwv - 1) / nwv;
-  int nwg = 0;
-  for (int i = 0; i < p.nseg; i++) {
-    int n = (int)(((int64_t)target * groups[i] + total - 1) / total);
-    if (n < 1) n = 1;
-    if (n > groups[i]) n = groups[i];
-    p.seg[i].wg_begin = nwg;
-    p.seg[i].nwg = n;
-    nwg += n;
-  }
-  return nwg;
-}
-
-template <class C, int TM, int NM>
-static hipError_t launch_one(GemvParams &p, int split, int num_cu, hipStream_t st) {
-  constexpr int R = rows_per_group<C, TM, NM>();
-  int passes, nwv;
-  cs_shape(p.cols, &passes, &nwv);
-  const int nwg = plan_grid(p, TM, NM, nwv, num_cu);
-  if (nwg == 0) return hipSuccess;
-  const size_t smem = cs_lds_bytes<C, TM, R, NM>(nwv);
-  if (TM == 1 && passes == 1)
-    hipLaunchKernelGGL((gemv_kernel<C, TM, R, NM, TM == 1 ? 1 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
-  else if (TM == 1 && passes == 2 && C::SP2)
-    hipLaunchKernelGGL((gemv_kernel<C, TM, R, NM, TM == 1 ? 2 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
-  else
-    hipLaunchKernelGGL((gemv_kernel<C, TM, R, NM, 0>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
-  return hipGetLastError();
-}
-
-template <class C, int NM>
-static hipError_t launch_tm(GemvParams &p, int split, int num_cu, hipStream_t st) {
-  if (p.T <= 1) return launch_one<C, 1, NM>(p, split, num_cu, st);
-  if (p.T <= 2) return launch_one<C, 2, NM>(p, split, num_cu, st);
-  if (p.T <= 4) return launch_one<C, 4, NM>(p, split, num_cu, st);
-  return launch_one<C, 8, NM>(p, split, num_cu, st);
-}
-
-template <int NM>
-static hipError_t launch_type(int type, GemvParams &p, int split, int num_cu, hipStream_t st) {
-  switch (type) {
-    case 12: return launch_tm<Q4K, NM>(p, split, num_cu, st);
-    case 14: return launch_tm<Q6K, NM>(p, split, num_cu, st);
-    case 8: return launch_tm<Q80, NM>(p, split, num_cu, st);
-    case 23: return launch_tm<IQ4XS, NM>(p, split, num_cu, st);
-    case 16: return launch_tm<IQ2XXS, NM>(p, split, num_cu, st);
-  }
-  return hipErrorInvalidValue;
-}
-
 template <int TM>
 static hipError_t launch_mixed_tm(GemvParams &p, int split, int num_cu, hipStream_t st) {
   int passes, nwv;
   cs_shape(p.cols, &passes, &nwv);
-  const int nwg = plan_grid(p, TM, 1, nwv, num_cu);
+  const int nwg = plan_grid(p, [](int type) { return mixed_rows_per_group(type, TM); }, nwv, num_cu);
   if (nwg == 0) return hipSuccess;
   const size_t smem = sizeof(float) * 2 * GS * nwv * 8 * TM;  // the largest R*TM of the three codecs
   if (TM == 1 && passes == 1)
@@ -212,175 +121,10 @@ static hipError_t launch_mixed_tm(GemvParams &p, int split, int num_cu, hipStrea
   return hipGetLastError();
 }
 
-static int block_bytes(int type) {
-  return type == 12 ? 144 : type == 14 ? 210 : type == 8 ? 34 : type == 23 ? 136 : 66;
-}
-
-// ------------------------------------------------------------------ batched tokens (T >= 2)
-// The one-token launch's decomposition, kept bit for bit, with the tokens' x slices staged in
-// LDS once per workgroup: a workgroup owns ONE wave-column c (blocks c*BPW .. +BPW: the slices a
-// wave of the one-token launch owns) for a stripe of row groups of one matrix; its waves walk
-// row groups independently (no barrier after staging). Per (matrix, token, row) a lane forms the
-// codec's dot on its slice, the 64 lanes fold it with the same exchange butterfly, and the
-// wave-column's result goes to part[m][t][row][c]. batch_combine_kernel then adds the
-// wave-columns as the one-token launch does: in wave order within each K-chunk, then in chunk
-// order, SiLU last for the SwiGLU pair. So every token's bits equal its one-token result.
-// All matrices of a call (q, k, v) share one launch and one combine launch.
-struct BatchMat {
-  const uint8_t *w, *w2;
-  int64_t row_bytes;
-  float *part;  // [NM][T][rows][u]
-  float *y;
-  int ldy, rows, type;
-  int wg_begin;  // first blockIdx.x of this matrix
-};
-
-struct BatchArgs {
-  BatchMat m[GEMV_MAX_MATS];
-  int nmat, cols;
-  const float *x;
-  int ldx, T;
-  int u;     // wave-columns
-  int S, W;  // the one-token launch's K-chunks and waves per chunk (u = S * W)
-};
-
-template <class C>
-constexpr int xs_u4() {
-  return (int)((sizeof(typename C::Xs) + 15) / 16);
-}
-
-template <class C, int TM>
-__host__ __device__ constexpr size_t batch_lds_bytes() {
-  return (C::NEED_LDS ? sizeof(Lds) : 0) + (size_t)TM * xs_u4<C>() * 64 * 16;
-}
-
-#ifndef WL_BATCH_WAVES
-#define WL_BATCH_WAVES 8  // waves per workgroup of the batched kernel
-#endif
-constexpr int kBatchWaves = WL_BATCH_WAVES;
-
-__device__ __forceinline__ int batch_mat(const BatchArgs &a) {
-  int mi = 0;
-#pragma unroll
-  for (int i = 1; i < GEMV_MAX_MATS; i++)
-    if (i < a.nmat && (int)blockIdx.x >= a.m[i].wg_begin) mi = i;
-  return mi;
-}
-
-// wgx: this workgroup's index among the matrix's nwg workgroups of column blockIdx.y.
-template <class C, int TM, int R, int NM>
-__device__ __forceinline__ void batch_body(const BatchArgs &a, const BatchMat &M, int wgx, int nwg) {
-  constexpr int V = NM * R * TM, LOW = 6 - ilog2(V), BPW = 64 / C::LPB, NX = xs_u4<C>();
-  static_assert((1 << ilog2(V)) == V && V <= 64, "partials per lane must be a power of two <= 64");
-  const Lds &lds = *reinterpret_cast<const Lds *>(wl_dyn_lds);
-  uint4 *xl = reinterpret_cast<uint4 *>(wl_dyn_lds + (C::NEED_LDS ? sizeof(Lds) : 0));  // [TM][NX][64]
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int c = blockIdx.y, nb = a.cols / C::BLOCK;
-  const int sub = lane % C::LPB, b = c * BPW + lane / C::LPB;
-  const bool live = b < nb;
-  const typename C::Lane L = C::lane(sub);
-  if constexpr (C::NEED_LDS) C::init_lds(*reinterpret_cast<Lds *>(wl_dyn_lds));
-  // stage: wave w prepares tokens w, w + kBatchWaves, ... as the one-token launch prepares its slice
-  for (int t = wv; t < TM; t += kBatchWaves) {
-    if (t < a.T && live) {
-      typename C::Xs xs;
-      C::load_x(a.x + (int64_t)t * a.ldx + (int64_t)b * C::BLOCK, L, xs);
-      uint4 v[NX] = {};
-      __builtin_memcpy(v, &xs, sizeof(xs));
-#pragma unroll
-      for (int i = 0; i < NX; i++) xl[(t * NX + i) * 64 + lane] = v[i];
-    }
-  }
-  __syncthreads();
-  const uint8_t *wm[2] = {M.w, M.w2};
-  const int ngroups = (M.rows + R - 1) / R;
-  for (int g = wgx * kBatchWaves + wv; g < ngroups; g += nwg * kBatchWaves) {
-    float acc[NM][R][TM];
-#pragma unroll
-    for (int m = 0; m < NM; m++)
-#pragma unroll
-      for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int t = 0; t < TM; t++) acc[m][r][t] = 0.f;
-    if (live) {
-      typename C::Raw raw[NM][R];
-#pragma unroll
-      for (int m = 0; m < NM; m++)
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-          // rows past the end re-read the last row (valid memory); their results are dropped
-          const int row = min(g * R + r, M.rows - 1);
-          C::load(wm[m] + (int64_t)row * M.row_bytes + (int64_t)b * C::BYTES, L, raw[m][r]);
-        }
-      typename C::W w[NM][R];
-#pragma unroll
-      for (int m = 0; m < NM; m++)
-#pragma unroll
-        for (int r = 0; r < R; r++) C::unpack(raw[m][r], L, lds, w[m][r]);
-#pragma unroll
-      for (int t = 0; t < TM; t++) {
-        if (t < a.T) {
-          uint4 v[NX];
-#pragma unroll
-          for (int i = 0; i < NX; i++) v[i] = xl[(t * NX + i) * 64 + lane];
-          typename C::Xs xs;
-          __builtin_memcpy(&xs, v, sizeof(xs));
-#pragma unroll
-          for (int m = 0; m < NM; m++)
-#pragma unroll
-            for (int r = 0; r < R; r++) acc[m][r][t] += C::dot(w[m][r], xs);
-        }
-      }
-    }
-    // value index v = (m*TM + t)*R + r, as the one-token launch folds it
-    float vals[V];
-#pragma unroll
-    for (int m = 0; m < NM; m++)
-#pragma unroll
-      for (int t = 0; t < TM; t++)
-#pragma unroll
-        for (int r = 0; r < R; r++) vals[(m * TM + t) * R + r] = acc[m][r][t];
-    const float q = exch_reduce<V, 5>(vals, lane);
-    if ((lane & ((1 << LOW) - 1)) == 0) {
-      const int v = lane >> LOW, r = v % R, t = (v / R) % TM, m = v / (R * TM);
-      const int row = g * R + r;
-      if (t < a.T && row < M.rows) M.part[(((int64_t)m * a.T + t) * M.rows + row) * a.u + c] = q;
-    }
-  }
-}
-
-__device__ __forceinline__ int batch_nwg(const BatchArgs &a, int mi) {
-  return (mi + 1 < a.nmat ? a.m[mi + 1].wg_begin : (int)gridDim.x) - a.m[mi].wg_begin;
-}
-
-// Waves per SIMD the register budget is cut for: four (two resident workgroups of eight waves
-// per CU, at most 128 VGPRs), except where that would spill (the Q6_K SwiGLU pair).
-template <class C, int NM>
-constexpr int batch_occupancy() {
-  return NM == 2 && C::BYTES == 210 ? 2 : 4;
-}
-
-template <class C, int TM, int R, int NM>
-__global__ __launch_bounds__(64 * kBatchWaves) __attribute__((amdgpu_waves_per_eu(batch_occupancy<C, NM>())))
-void gemv_batch_kernel(BatchArgs a) {
-  const int mi = batch_mat(a);
-  batch_body<C, TM, R, NM>(a, a.m[mi], (int)blockIdx.x - a.m[mi].wg_begin, batch_nwg(a, mi));
-}
-
-#ifndef WL_BATCH_R1
-#define WL_BATCH_R1 2  // rows per group of a single matrix
-#endif
-#ifndef WL_BATCH_R2
-#define WL_BATCH_R2 1  // rows per group of the SwiGLU pair
-#endif
-#ifndef WL_BATCH_WPC
-#define WL_BATCH_WPC 64  // waves per CU the grid aims at (about four rounds of resident workgroups)
-#endif
-constexpr int kBatchR1 = WL_BATCH_R1, kBatchR2 = WL_BATCH_R2;
-
 #ifndef WL_BATCH_MIXED_OCC
 #define WL_BATCH_MIXED_OCC 4
 #endif
+
 
 // Matrices of different formats in one launch (q/k Q4_K with v Q6_K): the codec is chosen per
 // workgroup, every workgroup stays on one matrix.
@@ -398,81 +142,6 @@ void gemv_batch_mixed_kernel(BatchArgs a) {
   }
 }
 
-// y[t][r] from the wave-column partials: waves in order within each of S chunks of W, then the
-// chunks in order (the one-token launch's wave-0 sum and chunk combine); SiLU for the pair.
-__device__ __forceinline__ float batch_sum(const float *p, int S, int W) {
-  float y = 0.f;
-  for (int c = 0; c < S; c++) {
-    float s = p[c * W];
-    for (int k = 1; k < W; k++) s += p[c * W + k];
-    y = c == 0 ? s : y + s;
-  }
-  return y;
-}
-
-// blockIdx.y: the matrix.
-template <int NM>
-__global__ __launch_bounds__(256) void batch_combine_kernel(BatchArgs a) {
-  const BatchMat &M = a.m[blockIdx.y];
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)a.T * M.rows) return;
-  const int t = (int)(i / M.rows), r = (int)(i % M.rows);
-  float s = batch_sum(M.part + i * a.u, a.S, a.W);
-  if constexpr (NM == 2) s = silu_mul(s, batch_sum(M.part + ((int64_t)a.T * M.rows + i) * a.u, a.S, a.W));
-  M.y[(int64_t)t * M.ldy + r] = s;
-}
-
-// Workgroups per matrix along x: about WL_BATCH_WPC waves per CU over all columns, split over
-// the matrices in proportion to their row groups. Returns the grid's x size.
-static int plan_batch(BatchArgs &a, int R, int num_cu) {
-  int total = 0;
-  for (int i = 0; i < a.nmat; i++) total += (a.m[i].rows + R - 1) / R;
-  const int target = (num_cu * WL_BATCH_WPC / kBatchWaves + a.u - 1) / a.u;
-  int gx = 0;
-  for (int i = 0; i < a.nmat; i++) {
-    const int groups = (a.m[i].rows + R - 1) / R;
-    int n = (int)(((int64_t)target * groups + total - 1) / total);
-    const int most = (groups + kBatchWaves - 1) / kBatchWaves;
-    if (n > most) n = most;
-    if (n < 1) n = 1;
-    a.m[i].wg_begin = gx;
-    gx += n;
-  }
-  return gx;
-}
-
-template <class K>
-static hipError_t raise_lds(K *kernel, size_t smem, bool &raised) {
-  if (smem > 65536 && !raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)smem) != hipSuccess)
-      return hipErrorInvalidConfiguration;
-    raised = true;
-  }
-  return hipSuccess;
-}
-
-template <int NM>
-static hipError_t launch_batch_combine(const BatchArgs &a, hipStream_t st) {
-  int most = 0;
-  for (int i = 0; i < a.nmat; i++) most = a.m[i].rows > most ? a.m[i].rows : most;
-  const int64_t n = (int64_t)a.T * most;
-  hipLaunchKernelGGL(batch_combine_kernel<NM>, dim3((unsigned)((n + 255) / 256), a.nmat), dim3(256), 0, st, a);
-  return hipGetLastError();
-}
-
-template <class C, int TM, int NM>
-static hipError_t launch_batch_tm(BatchArgs a, int num_cu, hipStream_t st) {
-  constexpr int R = NM == 1 ? kBatchR1 : kBatchR2;
-  const size_t smem = batch_lds_bytes<C, TM>();
-  static bool raised = false;
-  hipError_t e = raise_lds(&gemv_batch_kernel<C, TM, R, NM>, smem, raised);
-  if (e != hipSuccess) return e;
-  const int gx = plan_batch(a, R, num_cu);
-  hipLaunchKernelGGL((gemv_batch_kernel<C, TM, R, NM>), dim3(gx, a.u), dim3(64 * kBatchWaves), smem, st, a);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  return launch_batch_combine<NM>(a, st);
-}
 
 template <int TM>
 static hipError_t launch_batch_mixed_tm(BatchArgs a, int num_cu, hipStream_t st) {
@@ -487,23 +156,25 @@ static hipError_t launch_batch_mixed_tm(BatchArgs a, int num_cu, hipStream_t st)
   return launch_batch_combine<1>(a, st);
 }
 
-template <class C, int NM>
-static hipError_t launch_batch(const BatchArgs &a, int num_cu, hipStream_t st) {
-  if (a.T <= 2) return launch_batch_tm<C, 2, NM>(a, num_cu, st);
-  if (a.T <= 4) return launch_batch_tm<C, 4, NM>(a, num_cu, st);
-  return launch_batch_tm<C, 8, NM>(a, num_cu, st);
+// The codecs of this unit and the lookup over every unit.
+const GemvOps *gemv_ops_base(int type) {
+  static constexpr GemvOps q4k = gemv_ops_of<Q4K>(), q6k = gemv_ops_of<Q6K>(), q80 = gemv_ops_of<Q80>(),
+                           iq4xs = gemv_ops_of<IQ4XS>(), iq2xxs = gemv_ops_of<IQ2XXS>();
+  switch (type) {
+    case 12: return &q4k;
+    case 14: return &q6k;
+    case 8: return &q80;
+    case 23: return &iq4xs;
+    case 16: return &iq2xxs;
+  }
+  return nullptr;
 }
 
-template <int NM>
-static hipError_t launch_batch_type(int type, const BatchArgs &a, int num_cu, hipStream_t st) {
-  switch (type) {
-    case 12: return launch_batch<Q4K, NM>(a, num_cu, st);
-    case 14: return launch_batch<Q6K, NM>(a, num_cu, st);
-    case 8: return launch_batch<Q80, NM>(a, num_cu, st);
-    case 23: return launch_batch<IQ4XS, NM>(a, num_cu, st);
-    case 16: return launch_batch<IQ2XXS, NM>(a, num_cu, st);
-  }
-  return hipErrorInvalidValue;
+static const GemvOps *gemv_ops(int type) {
+  if (const GemvOps *o = gemv_ops_base(type)) return o;
+  if (const GemvOps *o = gemv_ops_k(type)) return o;
+  if (const GemvOps *o = gemv_ops_32(type)) return o;
+  return gemv_ops_f(type);
 }
 
 #ifndef WL_GEMV_BATCH
@@ -531,8 +202,10 @@ static hipError_t gemv_batch_run(const GemvMat *mats, int nmat, int nm, const fl
     part += (int64_t)a.u * nm * T * m.rows;
     same = same && m.type == mats[0].type;
   }
-  if (same) return nm == 2 ? launch_batch_type<2>(mats[0].type, a, num_cu, st)
-                           : launch_batch_type<1>(mats[0].type, a, num_cu, st);
+  if (same) {
+    const GemvOps *o = gemv_ops(mats[0].type);
+    return o ? o->batch[nm - 1](a, num_cu, st) : hipErrorInvalidValue;
+  }
   for (int i = 0; i < nmat; i++)
     if (!gemv_mixed_supports(mats[i].type)) return hipErrorNotSupported;
   if (T <= 2) return launch_batch_mixed_tm<2>(a, num_cu, st);
@@ -565,8 +238,9 @@ hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int l
   int maxrows = 0;
   for (int i = 0; i < nmat; i++) {
     const GemvMat &m = mats[i];
-    const int be = m.type == 8 ? 32 : 256;
-    const int64_t chunk_bytes = (int64_t)(p.cols / be) * block_bytes(m.type);
+    int be = 0, bb = 0;
+    if (!wl_type_layout(m.type, &be, &bb)) return hipErrorInvalidValue;
+    const int64_t chunk_bytes = (int64_t)(p.cols / be) * bb;
     for (int c = 0; c < S; c++) {
       GemvSeg &s = p.seg[p.nseg++];
       s.w = m.w + c * chunk_bytes;
@@ -595,8 +269,8 @@ hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int l
   const int split = S > 1;
   hipError_t e;
   if (same) {
-    e = nm == 1 ? launch_type<1>(mats[0].type, p, split, num_cu, st)
-                : launch_type<2>(mats[0].type, p, split, num_cu, st);
+    const GemvOps *o = gemv_ops(mats[0].type);
+    e = o ? o->launch[nm - 1](p, split, num_cu, st) : hipErrorInvalidValue;
   } else if (T <= 1) {
     e = launch_mixed_tm<1>(p, split, num_cu, st);
   } else if (T <= 2) {
@@ -612,7 +286,7 @@ hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int l
   return hipGetLastError();
 }
 
-bool gemv_supports(int type) { return type == 12 || type == 14 || type == 8 || type == 23 || type == 16; }
+bool gemv_supports(int type) { return gemv_ops(type) != nullptr; }
 
 bool gemv_mixed_supports(int type) { return type == 12 || type == 14 || type == 8; }
 
