@@ -31,7 +31,7 @@ def _p(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
-@pytest.mark.parametrize("types", [(12, 12, 14), (12, 12, 12), (14, 8, 12)])
+@pytest.mark.parametrize("types", [(12, 12, 14), (12, 12, 12), (14, 8, 12), (13, 13, 14), (13, 13, 13), (2, 8, 2)])
 @pytest.mark.parametrize("T", [1, 8])
 @pytest.mark.parametrize("cols", [2048, 16384])
 def test_multi_matmul_equals_separate(ctx, types, T, cols):

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
-from gpu_common import GEMM_REL, QTYPES, blocks, decoded, tol_check
+from gpu_common import FLOATS, GEMM_REL, NEWQ, QTYPES, blocks, decoded, tol_check
 from windlass_amd import Transformer
 from windlass_amd.backend import Context, GgmlType
 
@@ -28,8 +28,13 @@ def ctx():
     c.close()
 
 
-@pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
-@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "%dx%d" % s)
+# the other formats: one shape per launch structure (single pass, K-split in 7 chunks, three
+# passes of a prime width, a row narrower than a wave)
+NEW_SHAPES = [(37, 1024), (40, 28672), (9, 34816), (300, 2048)]
+CASES = [(t, s) for t in QTYPES for s in SHAPES] + [(t, s) for t in NEWQ + FLOATS for s in NEW_SHAPES]
+
+
+@pytest.mark.parametrize("t,shape", CASES, ids=lambda v: v.name if hasattr(v, "name") else "%dx%d" % v)
 @pytest.mark.parametrize("T", [1, 3, 8])
 def test_gemv_within_tolerance(ctx, t, shape, T):
     rows, cols = shape
@@ -45,7 +50,7 @@ def test_gemv_within_tolerance(ctx, t, shape, T):
     w.free()
 
 
-@pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
+@pytest.mark.parametrize("t", QTYPES + NEWQ + FLOATS, ids=lambda t: t.name)
 @pytest.mark.parametrize("cols", [2048, 28672])
 def test_batch_rows_equal_single_token_bitwise(ctx, t, cols):
     rows = 300 if cols == 2048 else 40
@@ -70,7 +75,7 @@ def test_more_than_eight_tokens(ctx):
     w.free()
 
 
-@pytest.mark.parametrize("t", QTYPES, ids=lambda t: t.name)
+@pytest.mark.parametrize("t", QTYPES + NEWQ + FLOATS, ids=lambda t: t.name)
 def test_expert_slices(ctx, t):
     ne, rows, cols = 4, 40, 512
     data = blocks(t, ne * rows, cols, seed=11)

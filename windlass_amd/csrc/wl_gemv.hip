@@ -35,7 +35,6 @@ __global__ __launch_bounds__(64 * kMaxWaves) void gemv_mixed_kernel(GemvParams p
   }
 }
 
-
 // y = the chunk partials added in chunk order (SwiGLU pair: silu(gate sum) * (up sum)).
 struct CombineParams {
   const float *part[GEMV_MAX_MATS];  // per matrix: [S][NM][T][rows]
@@ -93,7 +92,25 @@ static int batch_columns(int nmat, int cols, int *S_out, int *W_out) {
   return S * nwv;
 }
 
+// Matrices of different formats that the mixed kernels do not hold run one launch each.
+static bool per_matrix(const GemvMat *mats, int nmat) {
+  bool same = true, mixable = true;
+  for (int i = 0; i < nmat; i++) {
+    same = same && mats[i].type == mats[0].type;
+    mixable = mixable && gemv_mixed_supports(mats[i].type);
+  }
+  return !same && !mixable;
+}
+
 int64_t gemv_scratch_floats(const GemvMat *mats, int nmat, int nm, int cols, int T) {
+  if (nmat > 1 && per_matrix(mats, nmat)) {
+    int64_t most = 0;
+    for (int i = 0; i < nmat; i++) {
+      const int64_t f = gemv_scratch_floats(&mats[i], 1, nm, cols, T);
+      most = f > most ? f : most;
+    }
+    return most;
+  }
   const int S = gemv_chunks(nmat, cols);
   int64_t n = 0;
   if (S > 1)
@@ -125,7 +142,6 @@ static hipError_t launch_mixed_tm(GemvParams &p, int split, int num_cu, hipStrea
 #define WL_BATCH_MIXED_OCC 4
 #endif
 
-
 // Matrices of different formats in one launch (q/k Q4_K with v Q6_K): the codec is chosen per
 // workgroup, every workgroup stays on one matrix.
 template <int TM>
@@ -141,7 +157,6 @@ void gemv_batch_mixed_kernel(BatchArgs a) {
     default: break;
   }
 }
-
 
 template <int TM>
 static hipError_t launch_batch_mixed_tm(BatchArgs a, int num_cu, hipStream_t st) {
@@ -219,6 +234,15 @@ hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int l
   bool same = true;
   for (int i = 1; i < nmat; i++) same = same && mats[i].type == mats[0].type;
   if (!same && nm != 1) return hipErrorInvalidValue;
+  if (per_matrix(mats, nmat)) {
+    // formats the mixed kernels do not hold: one launch per matrix (each needs less scratch
+    // than the whole set)
+    for (int i = 0; i < nmat; i++) {
+      const hipError_t e = gemv_run(&mats[i], 1, nm, x, ldx, cols, T, scratch, num_cu, st);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
   {
     const hipError_t e = gemv_batch_run(mats, nmat, nm, x, ldx, cols, T, scratch, num_cu, st);
     if (e != hipErrorNotSupported) return e;
