@@ -53,6 +53,9 @@ def parse():
     ap.add_argument("--int-dot", action="store_true",
                     help="the integer-dot kernels (Transformer.IntDot, --int-dot): 8-bit activations, "
                          "FastMath.IntDot per row; no CPU baseline")
+    ap.add_argument("--formats", action="store_true",
+                    help="instead of the layer: the decode GEMV of every GGUF format at the 70B FFN "
+                         "shapes (28672x8192 and 8192x28672), one token and eight, one JSON line")
     ap.add_argument("--calibrate", type=int, default=0, metavar="MIB",
                     help="before warm-up, run a plain elementwise copy (torch.neg) of MIB MiB three "
                          "times, untimed: the HBM counters of a kernel of known traffic")
@@ -74,6 +77,8 @@ def main():
         print("bench.py measures one GPU only: this build runs the hot path on a single MI355X "
               "(--gpus %d requested)" % args.gpus, file=sys.stderr)
         sys.exit(2)
+    if args.formats:
+        return run_formats(args)
     T = args.batch
     if not 1 <= T <= 8:
         sys.exit("--batch must be 1..8")
@@ -203,6 +208,65 @@ def main():
                      "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
     }
+    print(json.dumps(line), flush=True)
+
+
+# ggml type id -> name, for --formats
+FORMATS = {12: "q4_K", 13: "q5_K", 14: "q6_K", 10: "q2_K", 11: "q3_K", 2: "q4_0", 3: "q4_1", 6: "q5_0",
+           7: "q5_1", 8: "q8_0", 20: "iq4_nl", 23: "iq4_xs", 16: "iq2_xxs", 1: "f16", 30: "bf16", 0: "f32"}
+
+
+def run_formats(args):
+    """The decode GEMV of every format at the 70B FFN shapes: gate/up-shaped 28672 x 8192 and
+    down-shaped 8192 x 28672, at one token and eight. Four weight copies rotate (each at least
+    117 MB for the 2-bit formats), HIP events on the library's stream, 200 launches per figure."""
+    import torch
+    import windlass_amd
+    from windlass_amd import synth
+    from windlass_amd._lib import check
+    from windlass_amd.backend import Context, layout
+
+    L = windlass_amd.load()
+    ctx = Context(0)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.ExternalStream(ctx.stream, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    rng = np.random.default_rng(0x57494E44 + 5000)
+    results = {}
+    for t, name in FORMATS.items():
+        be, bb = layout(t)
+        for rows, cols in ((FFN, HIDDEN), (HIDDEN, FFN)):
+            host = synth.blocks(t, rows, cols, rng)
+            ws = [ctx.upload(t, host, rows, cols) for _ in range(args.copies)]
+            for T in (1, 8):
+                x = torch.from_numpy(synth.activations(rng, T, cols)).to(dev)
+                y = torch.empty((T, rows), device=dev)
+
+                def run(i):
+                    check(L.wl_matmul_dev(ctx.handle, ws[i % len(ws)].handle, -1, P(x), T, P(y)))
+
+                with torch.cuda.stream(stream):
+                    for i in range(10):
+                        run(i)
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record(stream)
+                    for i in range(200):
+                        run(i)
+                    b.record(stream)
+                b.synchronize()
+                ms = a.elapsed_time(b) / 200
+                byt = rows * (cols // be * bb) + 4 * T * (rows + cols)
+                results["%s_%dx%d_T%d" % (name, rows, cols, T)] = {
+                    "us": round(ms * 1e3, 2), "gbs": round(byt / (ms * 1e-3) / 1e9, 1)}
+            for w in ws:
+                w.free()
+    ctx.close()
+    q4 = results["q4_K_%dx%d_T1" % (FFN, HIDDEN)]["gbs"]
+    line = {"metric": "decode GEMV HBM GB/s per GGUF format at 70B FFN shapes", "value": q4, "unit": "GB/s",
+            "n_gpus": 1, "higher_is_better": True, "dtype": "f32", "data": "synthetic seeded blocks, x ~ N(0,1)",
+            "config": {"workload": "one matrix per launch: 28672x8192 and 8192x28672, batch 1 and 8",
+                       "layer_copies": args.copies},
+            "value_is": "q4_K 28672x8192 at batch 1", "per_format": results}
     print(json.dumps(line), flush=True)
 
 

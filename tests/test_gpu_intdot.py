@@ -26,7 +26,7 @@ pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PINS = json.load(open(os.path.join(HERE, "golden", "reference_pins.json")))
-ITYPES = [GgmlType.Q8_0, GgmlType.Q4_K, GgmlType.Q6_K]
+ITYPES = [GgmlType.Q8_0, GgmlType.Q4_0, GgmlType.Q4_K, GgmlType.Q5_K, GgmlType.Q6_K]  # FastMath.CanIntDot
 
 
 @pytest.fixture(scope="module")

@@ -69,7 +69,9 @@ def test_route_ties_and_nan_vs_oracle(ctx, n):
 # (ne, k, embd, ff): 128 experts top-8 is the qwen3moe routing shape; 2100 experts route on the
 # serial kernel and plan separately
 @pytest.mark.parametrize("T", [1, 8, 11])
-@pytest.mark.parametrize("types", [(12, 12), (12, 14)])
+# (gate/up, down) formats; Q5_0 and Q3_K experts are the reference's own MoE cases
+# (tests/MoeTests.cs:73-77)
+@pytest.mark.parametrize("types", [(12, 12), (12, 14), (6, 6), (11, 11), (13, 14), (2, 8), (1, 30)])
 @pytest.mark.parametrize("shape", [(16, 4, 512, 256), (128, 8, 512, 256), (2100, 2, 256, 256)],
                          ids=lambda s: "ne%d_k%d" % s[:2])
 def test_moe_ffn_vs_oracle(ctx, T, types, shape):

@@ -68,13 +68,13 @@ class FastMath:
 
     @staticmethod
     def CanIntDot(t):
-        """src/FastMath.cs:27-30, for the formats this library carries (Q8_0, Q4_K, Q6_K)."""
+        """src/FastMath.cs:27-30: Q8_0, Q4_0, Q4_K, Q5_K, Q6_K."""
         return bool(load().wl_can_int_dot(int(t)))
 
     @staticmethod
     def NeedsK(t):
         """src/FastMath.cs:32: the weights take Q8_K activations."""
-        return int(t) in (GgmlType.Q4_K, GgmlType.Q6_K)
+        return int(t) in (GgmlType.Q4_K, GgmlType.Q5_K, GgmlType.Q6_K)
 
     @staticmethod
     def Fits(t, cols):

@@ -15,15 +15,16 @@
 // which is the reference's `sum +=` loop: y is bit-identical to FastMath.IntDot.
 #include "wl_intdot.h"
 
-#include "wl_codecs.h"
+#include "wl_codecs2.h"
 #include "wl_gemv_impl.h"
 
 #pragma clang fp contract(off)
 
 namespace wl {
 
-bool intdot_supports(int t) { return t == 8 || t == 12 || t == 14; }
-bool intdot_needs_k(int t) { return t == 12 || t == 14; }
+// FastMath.CanIntDot / NeedsK (src/FastMath.cs:27-32)
+bool intdot_supports(int t) { return t == 8 || t == 2 || t == 12 || t == 13 || t == 14; }
+bool intdot_needs_k(int t) { return t == 12 || t == 13 || t == 14; }
 bool intdot_fits(int t, int cols) { return cols > 0 && cols % (intdot_needs_k(t) ? 256 : 32) == 0; }
 
 static int64_t up16(int64_t n) { return (n + 15) / 16 * 16; }
@@ -205,6 +206,33 @@ struct IQ4K {
   }
 };
 
+// Q5_K (src/FastMath.cs:158-184): Q4_K's lanes and terms with the fifth bit of every quant from
+// qh (bit 2j of qh[l] for the low nibbles, 2j+1 for the high ones).
+struct IQ5K : IQ4K {
+  using C = Q5K;
+  __device__ static void part(const C::Raw &r, const C::Lane &L, const Xq &x, int &si, int &sm) {
+    const uint4 h = r.hdr;
+    const uint32_t P = L.jlo ? h.y : h.w;
+    const uint32_t Q = L.jlo ? h.z : (h.w >> 4);
+    const uint32_t S = ((P & L.m1) | ((h.y >> 2) & L.m2)) >> L.sh;
+    const uint32_t M = ((Q & L.m1) | ((h.z >> 2) & L.m2)) >> L.sh;
+    const uint32_t qq[4] = {r.q.x, r.q.y, r.q.z, r.q.w}, qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    int a1 = 0, a2 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t hs = qh[i] >> (2 * L.j);
+      a1 = dot4((qq[i] & 0x0F0F0F0Fu) | ((hs & 0x01010101u) << 4), x.a[i], a1);
+      a2 = dot4(((qq[i] >> 4) & 0x0F0F0F0Fu) | (((hs >> 1) & 0x01010101u) << 4), x.b[i], a2);
+    }
+    si = (int)(S & 0xFF) * a1 + (int)((S >> 8) & 0xFF) * a2;
+    sm = (int)(M & 0xFF) * x.B1 + (int)((M >> 8) & 0xFF) * x.B2;
+  }
+  __device__ static float term(const C::Raw &r, int si, int sm, const Xq &x) {
+    const float dd = half_lo(r.hdr.x), dmin = half_hi(r.hdr.x);
+    return x.d * (dd * (float)si - dmin * (float)sm);  // src/FastMath.cs:182
+  }
+};
+
 // Q6_K (src/FastMath.cs:185-211). Lane (hh, g): values 128 hh + 8g + 32k + (0..7), k < 4, of
 // scale group 2k + g/2 of half hh; that group's other 8 values are on lane g^1.
 struct IQ6K {
@@ -302,6 +330,47 @@ struct IQ80 {
   __device__ static float term(const C::Raw &r, int si, int, const Xq &x) {
     const float h = half_lo(__builtin_amdgcn_alignbit(r.win[1], r.win[0], r.sh));
     return h * x.d * (float)si;  // src/FastMath.cs:120
+  }
+};
+
+// Q4_0 (src/FastMath.cs:123-134): one lane per 32-value block; the reference's s0 + s1 is
+// sum((n - 8) * q) = sum(n * q) - 8 * sum(q), the activations' sum formed once per token.
+struct IQ40 {
+  using C = Q40;
+  static constexpr int TERMS = 1;
+  struct Xq {
+    uint32_t v[8];
+    int sq;
+    float d;
+  };
+  __device__ static void load_x(const int8_t *q, const float *d, const int16_t *, int blk, const C::Lane &, Xq &x) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(q + (int64_t)blk * 32);
+    const uint4 a = p[0], b = p[1];
+    x.v[0] = a.x, x.v[1] = a.y, x.v[2] = a.z, x.v[3] = a.w;
+    x.v[4] = b.x, x.v[5] = b.y, x.v[6] = b.z, x.v[7] = b.w;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) s = dot4(0x01010101u, x.v[i], s);
+    x.sq = s;
+    x.d = d[blk];
+  }
+  __device__ static void part(const C::Raw &r, const C::Lane &, const Xq &x, int &si, int &sm) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      // qs dword i: values 4i..4i+3 (low nibbles) and 16+4i.. (high nibbles)
+      const uint32_t v = r.at(2, i);
+      s = dot4(v & 0x0F0F0F0Fu, x.v[i], s);
+      s = dot4((v >> 4) & 0x0F0F0F0Fu, x.v[4 + i], s);
+    }
+    si = s - 8 * x.sq;
+    sm = 0;
+  }
+  __device__ static void reduce(int &, int &) {}
+  __device__ static bool leader(const C::Lane &) { return true; }
+  __device__ static int term_index(const C::Lane &) { return 0; }
+  __device__ static float term(const C::Raw &r, int si, int, const Xq &x) {
+    return half_lo(r.w.dw(0)) * x.d * (float)si;  // src/FastMath.cs:132
   }
 };
 
@@ -419,7 +488,7 @@ __global__ __launch_bounds__(64 * kIntMaxWaves) void intdot_kernel(IntArgs a) {
 }
 
 static int nterm_of(int type, int cols) {
-  return type == 8 ? cols / 32 : type == 14 ? 2 * (cols / 256) : cols / 256;
+  return type == 8 || type == 2 ? cols / 32 : type == 14 ? 2 * (cols / 256) : cols / 256;
 }
 
 static size_t lds_of(int nm, int tm, int nterm) {
@@ -456,7 +525,9 @@ template <int NM>
 static hipError_t launch_type(int type, const IntArgs &a, int num_cu, hipStream_t st) {
   switch (type) {
     case 12: return launch_int_tm<IQ4K, NM>(a, num_cu, st);
+    case 13: return launch_int_tm<IQ5K, NM>(a, num_cu, st);
     case 14: return launch_int_tm<IQ6K, NM>(a, num_cu, st);
+    case 2: return launch_int_tm<IQ40, NM>(a, num_cu, st);
     default: return launch_int_tm<IQ80, NM>(a, num_cu, st);
   }
 }

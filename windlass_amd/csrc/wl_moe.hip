@@ -11,9 +11,7 @@
 //   4. moe_down        grouped decode GEMV of each pair's hidden row with its expert's down;
 //   5. combine_kernel  out[t] = sum over t's experts, ascending, of w * y (:289-293).
 // Only the chosen experts are read (tests/MoeTests.cs:164-181).
-#include "wl_moe.h"
-#include "wl_gemv.h"
-#include "wl_gemv_impl.h"
+#include "wl_moe_launch.h"
 
 #pragma clang fp contract(off)
 
@@ -218,22 +216,6 @@ __global__ __launch_bounds__(64 * MOE_MAX_T) void route_plan_kernel(const float 
   plan_pairs(sel, wts, T, k, plan);
 }
 
-extern "C" __shared__ uint8_t wl_moe_dyn_lds[];
-
-// blockIdx.y = slot (one chosen expert); the slot's workgroups stride over the expert's rows.
-template <class C, int TM, int R, int NM, int SP>
-__global__ __launch_bounds__(64 * kMaxWaves) void moe_gemv_kernel(MoeGemvArgs a) {
-  const MoePlan *plan = a.plan;
-  const int s = blockIdx.y;
-  if (s >= plan->nslots) return;  // uniform over the workgroup
-  const int e = plan->slot_expert[s];
-  const int64_t eoff = (int64_t)e * a.rows * a.row_bytes;
-  const CsRows W{a.w + eoff, NM == 2 ? a.w2 + eoff : nullptr, a.row_bytes, a.rows};
-  const CsIO io{a.x, a.x_by_pair ? plan->slot_pair[s] : plan->slot_tok[s], a.ldx, a.y, plan->slot_pair[s],
-                a.ldy, plan->slot_ntok[s]};
-  cs_gemv<C, TM, R, NM, SP>(W, io, a.cols, (int)blockIdx.x, (int)gridDim.x, wl_moe_dyn_lds);
-}
-
 __global__ void combine_kernel(const MoePlan *__restrict__ plan, const float *__restrict__ yd, int T, int k,
                                int embd, float *__restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -244,42 +226,31 @@ __global__ void combine_kernel(const MoePlan *__restrict__ plan, const float *__
   out[i] = o;
 }
 
-template <class C, int TM, int NM>
-static hipError_t launch_moe_gemv(const MoeGemvArgs &a, int max_slots, int num_cu, hipStream_t st) {
-  constexpr int R = TM == 1 ? (NM == 1 ? C::R1 : C::R1 / 2) : (NM == 1 ? 4 : 2);
-  int passes, nwv;
-  cs_shape(a.cols, &passes, &nwv);
-  const int groups = (a.rows + R - 1) / R;
-  // about 16 waves per CU over all slots
-  int gx = (num_cu * kWavesPerCu / nwv + max_slots - 1) / max_slots;
-  if (gx < 1) gx = 1;
-  if (gx > groups) gx = groups;
-  const size_t smem = cs_lds_bytes<C, TM, R, NM>(nwv);
-  if (TM == 1 && passes == 1)
-    hipLaunchKernelGGL((moe_gemv_kernel<C, TM, R, NM, TM == 1 ? 1 : 0>), dim3(gx, max_slots), dim3(64 * nwv), smem, st, a);
-  else
-    hipLaunchKernelGGL((moe_gemv_kernel<C, TM, R, NM, 0>), dim3(gx, max_slots), dim3(64 * nwv), smem, st, a);
-  return hipGetLastError();
+// The codecs of this unit and the lookup over every unit.
+const MoeOps *moe_ops_base(int type) {
+  static constexpr MoeOps q4k = moe_ops_of<Q4K>(), q6k = moe_ops_of<Q6K>(), q80 = moe_ops_of<Q80>(),
+                          iq4xs = moe_ops_of<IQ4XS>(), iq2xxs = moe_ops_of<IQ2XXS>();
+  switch (type) {
+    case 12: return &q4k;
+    case 14: return &q6k;
+    case 8: return &q80;
+    case 23: return &iq4xs;
+    case 16: return &iq2xxs;
+  }
+  return nullptr;
 }
 
-template <class C, int NM>
-static hipError_t launch_moe_tm(const MoeGemvArgs &a, int T, int max_slots, int num_cu, hipStream_t st) {
-  if (T <= 1) return launch_moe_gemv<C, 1, NM>(a, max_slots, num_cu, st);
-  if (T <= 2) return launch_moe_gemv<C, 2, NM>(a, max_slots, num_cu, st);
-  if (T <= 4) return launch_moe_gemv<C, 4, NM>(a, max_slots, num_cu, st);
-  return launch_moe_gemv<C, 8, NM>(a, max_slots, num_cu, st);
+static const MoeOps *moe_ops(int type) {
+  if (const MoeOps *o = moe_ops_base(type)) return o;
+  if (const MoeOps *o = moe_ops_k(type)) return o;
+  if (const MoeOps *o = moe_ops_32(type)) return o;
+  return moe_ops_f(type);
 }
 
 template <int NM>
 static hipError_t launch_moe_type(int type, const MoeGemvArgs &a, int T, int max_slots, int num_cu, hipStream_t st) {
-  switch (type) {
-    case 12: return launch_moe_tm<Q4K, NM>(a, T, max_slots, num_cu, st);
-    case 14: return launch_moe_tm<Q6K, NM>(a, T, max_slots, num_cu, st);
-    case 8: return launch_moe_tm<Q80, NM>(a, T, max_slots, num_cu, st);
-    case 23: return launch_moe_tm<IQ4XS, NM>(a, T, max_slots, num_cu, st);
-    case 16: return launch_moe_tm<IQ2XXS, NM>(a, T, max_slots, num_cu, st);
-  }
-  return hipErrorInvalidValue;
+  const MoeOps *o = moe_ops(type);
+  return o ? o->launch[NM - 1](a, T, max_slots, num_cu, st) : hipErrorInvalidValue;
 }
 
 static int route_per(int n) { return n <= 64 ? 1 : n <= 128 ? 2 : n <= 256 ? 4 : n <= 512 ? 8 : n <= 1024 ? 16 : 32; }
@@ -345,6 +316,6 @@ hipError_t moe_launch(const MoeLaunch &m, int num_cu, hipStream_t st) {
   return hipGetLastError();
 }
 
-bool moe_supports(int type) { return type == 12 || type == 14 || type == 8 || type == 23 || type == 16; }
+bool moe_supports(int type) { return moe_ops(type) != nullptr; }
 
 }  // namespace wl
