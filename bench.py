@@ -56,6 +56,7 @@ def parse():
     ap.add_argument("--formats", action="store_true",
                     help="instead of the layer: the decode GEMV of every GGUF format at the 70B FFN "
                          "shapes (28672x8192 and 8192x28672), one token and eight, one JSON line")
+    ap.add_argument("--only", default="", help="with --formats: comma-separated format names")
     ap.add_argument("--calibrate", type=int, default=0, metavar="MIB",
                     help="before warm-up, run a plain elementwise copy (torch.neg) of MIB MiB three "
                          "times, untimed: the HBM counters of a kernel of known traffic")
@@ -233,7 +234,10 @@ def run_formats(args):
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     rng = np.random.default_rng(0x57494E44 + 5000)
     results = {}
+    only = [n for n in args.only.split(",") if n]
     for t, name in FORMATS.items():
+        if only and name not in only:
+            continue
         be, bb = layout(t)
         for rows, cols in ((FFN, HIDDEN), (HIDDEN, FFN)):
             host = synth.blocks(t, rows, cols, rng)
@@ -261,7 +265,7 @@ def run_formats(args):
             for w in ws:
                 w.free()
     ctx.close()
-    q4 = results["q4_K_%dx%d_T1" % (FFN, HIDDEN)]["gbs"]
+    q4 = results.get("q4_K_%dx%d_T1" % (FFN, HIDDEN), {}).get("gbs")
     line = {"metric": "decode GEMV HBM GB/s per GGUF format at 70B FFN shapes", "value": q4, "unit": "GB/s",
             "n_gpus": 1, "higher_is_better": True, "dtype": "f32", "data": "synthetic seeded blocks, x ~ N(0,1)",
             "config": {"workload": "one matrix per launch: 28672x8192 and 8192x28672, batch 1 and 8",

@@ -179,13 +179,10 @@ struct Q6K {
     r.sh = misalign4(blk) * 8;
     const int o1 = (64 * L.hh + 8 * L.g) / 4, o2 = (64 * L.hh + 32 + 8 * L.g) / 4,
               oh = (128 + 32 * L.hh + 8 * L.g) / 4, os = (192 + 8 * L.hh) / 4;
-#pragma unroll
-    for (int i = 0; i < 3; i++) {
-      r.l1[i] = ldw4(a + o1 + i);
-      r.l2[i] = ldw4(a + o2 + i);
-      r.h[i] = ldw4(a + oh + i);
-      r.sc[i] = ldw4(a + os + i);
-    }
+    ldw12(a + o1, r.l1);
+    ldw12(a + o2, r.l2);
+    ldw12(a + oh, r.h);
+    ldw12(a + os, r.sc);
     r.dw = ldw4(a + 208 / 4);  // d: low half (aligned block) or high half (block at 2 mod 4)
   }
 

@@ -199,9 +199,16 @@ __device__ __forceinline__ void dot_k2(const uint32_t (&p)[16], const XsK2 &x, f
   }
 }
 
+#ifndef WL_Q2K_R1
+#define WL_Q2K_R1 4
+#endif
+#ifndef WL_Q3K_R1
+#define WL_Q3K_R1 4
+#endif
+
 // Q2_K (src/Quants.cs:261-285): y = d*(s & 15) * q2 - dmin*(s >> 4). Blocks are 4-byte aligned.
 struct Q2K {
-  static constexpr int BLOCK = 256, BYTES = 84, LPB = 8, NEED_LDS = 0, R1 = 8, SP2 = 1;
+  static constexpr int BLOCK = 256, BYTES = 84, LPB = 8, NEED_LDS = 0, R1 = WL_Q2K_R1, SP2 = 1;
   typedef LaneK2 Lane;
   typedef XsK2 Xs;
   struct Raw { uint32_t q[8], sc, d; };
@@ -211,8 +218,19 @@ struct Q2K {
   __device__ static void load_x(const float *xb, const Lane &L, Xs &x) { load_x_k2(xb, 4 * L.kk + L.j, x); }
   __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
     gu32 *a = align4_down(blk);  // aligned: 84 = 4 * 21
+    if constexpr (WL_WIDE_LOADS) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) r.q[i] = ldw4(a + 4 + 8 * L.kk + i);
+      for (int i = 0; i < 8; i += 4) {
+        const u32x4a4_t v = *reinterpret_cast<gu32x4 *>(a + 4 + 8 * L.kk + i);
+        r.q[i] = v.x;
+        r.q[i + 1] = v.y;
+        r.q[i + 2] = v.z;
+        r.q[i + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) r.q[i] = ldw4(a + 4 + 8 * L.kk + i);
+    }
     r.sc = ldw4(a + (8 * L.kk + 2 * L.j) / 4);
     r.d = ldw4(a + 20);
   }
@@ -240,7 +258,7 @@ struct Q2K {
 // Q3_K (src/Quants.cs:287-319): y = d*(sc - 32) * (q2 - (h ? 0 : 4)), h = bit 4kk + j of
 // hmask[l]; q2 + 4h enters as a 3-bit field and 4 * sum(x) is taken off.
 struct Q3K {
-  static constexpr int BLOCK = 256, BYTES = 110, LPB = 8, NEED_LDS = 0, R1 = 4, SP2 = 1;
+  static constexpr int BLOCK = 256, BYTES = 110, LPB = 8, NEED_LDS = 0, R1 = WL_Q3K_R1, SP2 = 1;
   typedef LaneK2 Lane;
   typedef XsK2 Xs;
   struct Raw { Win<32> q, hm; Win<12> sc; Win<4> d; };

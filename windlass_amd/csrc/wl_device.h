@@ -105,6 +105,27 @@ __device__ __forceinline__ uint32_t ldw4(gu32 *p) {
   else return *p;
 }
 
+// Three consecutive weight dwords at a dword-aligned address in one load instruction (the
+// hardware takes dword-aligned multi-dword global loads). WL_WIDE_LOADS = 0 issues three.
+#ifndef WL_WIDE_LOADS
+#define WL_WIDE_LOADS 1
+#endif
+typedef uint32_t u32x3a4_t __attribute__((ext_vector_type(3), aligned(4)));
+typedef const __attribute__((address_space(1))) u32x3a4_t gu32x3;
+typedef uint32_t u32x4a4_t __attribute__((ext_vector_type(4), aligned(4)));
+typedef const __attribute__((address_space(1))) u32x4a4_t gu32x4;
+__device__ __forceinline__ void ldw12(gu32 *p, uint32_t (&o)[3]) {
+  if constexpr (WL_WIDE_LOADS) {
+    const u32x3a4_t v = *reinterpret_cast<gu32x3 *>(p);
+    o[0] = v.x;
+    o[1] = v.y;
+    o[2] = v.z;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 3; i++) o[i] = ldw4(p + i);
+  }
+}
+
 // N (multiple of 4) bytes starting at a 2-byte aligned address: the dword window holding them
 // (N/4 + 1 dwords) and the bit offset of the first byte.
 template <int N>
@@ -114,8 +135,23 @@ struct Win {
   __device__ void load(const uint8_t *p) {
     gu32 *a = align4_down(p);
     sh = misalign4(p) * 8;
+    constexpr int n = N / 4 + 1;
+    if constexpr (WL_WIDE_LOADS) {
+      // groups of four dwords in one instruction each, then the rest
 #pragma unroll
-    for (int i = 0; i <= N / 4; i++) w[i] = a[i];
+      for (int i = 0; i + 4 <= n; i += 4) {
+        const u32x4a4_t v = *reinterpret_cast<gu32x4 *>(a + i);
+        w[i] = v.x;
+        w[i + 1] = v.y;
+        w[i + 2] = v.z;
+        w[i + 3] = v.w;
+      }
+#pragma unroll
+      for (int i = n / 4 * 4; i < n; i++) w[i] = a[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < n; i++) w[i] = a[i];
+    }
   }
   // dword i of the N bytes, and byte i
   __device__ uint32_t dw(int i) const { return __builtin_amdgcn_alignbit(w[i + 1], w[i], sh); }
