@@ -414,4 +414,79 @@ struct F32Row {
 typedef F32Row<false> F32c;
 typedef F32Row<true> BF16c;
 
+// Float rows whose length is a multiple of 2048, read coalesced: the whole wave-column is one
+// "block" (LPB = 64) and lane `sub` owns the 16-byte pieces at 1024k + 16*sub of it (k < 4 for
+// 2-byte values, k < 8 for F32), so every load instruction of a wave reads 1 KB contiguous. (The
+// 32-value runs above give each lane 64 or 128 contiguous bytes, which a wave reads 16 bytes per
+// lane at a 64- or 128-byte stride.) KIND: 0 F32, 1 F16, 2 BF16.
+template <int KIND>
+struct FWide {
+  static constexpr int E = KIND == 0 ? 4 : 2;            // bytes per value
+  static constexpr int NQ = KIND == 0 ? 8 : 4;           // 16-byte pieces per lane
+  static constexpr int PER = 16 / E;                     // values per piece
+  static constexpr int BLOCK = 2048, BYTES = 2048 * E, LPB = 64, NEED_LDS = 0, R1 = KIND == 1 ? 4 : 2, SP2 = 0;
+  struct Lane { int sub; };
+  struct Xs { float v[32]; };
+  struct Raw { uint4 q[NQ]; };
+  struct W { uint32_t p[KIND == 1 ? 16 : 32]; };
+
+  __device__ static Lane lane(int sub) { return Lane{sub}; }
+  // piece k holds values (1024k + 16 sub) / E .. + PER of the wave-column
+  __device__ static void load_x(const float *xb, const Lane &L, Xs &x) {
+#pragma unroll
+    for (int k = 0; k < NQ; k++) {
+      const float4 *q = reinterpret_cast<const float4 *>(xb + (1024 * k + 16 * L.sub) / E);
+#pragma unroll
+      for (int i = 0; i < PER / 4; i++) {
+        const float4 f = q[i];
+        x.v[PER * k + 4 * i] = f.x;
+        x.v[PER * k + 4 * i + 1] = f.y;
+        x.v[PER * k + 4 * i + 2] = f.z;
+        x.v[PER * k + 4 * i + 3] = f.w;
+      }
+    }
+  }
+  __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
+#pragma unroll
+    for (int k = 0; k < NQ; k++) r.q[k] = ldw16(blk + 1024 * k + 16 * L.sub);
+  }
+  __device__ static void unpack(const Raw &r, const Lane &, const Lds &, W &w) {
+#pragma unroll
+    for (int k = 0; k < NQ; k++) {
+      const uint32_t u[4] = {r.q[k].x, r.q[k].y, r.q[k].z, r.q[k].w};
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        if constexpr (KIND == 1) {
+          w.p[4 * k + c] = u[c];  // two fp16 values, used as they are
+        } else if constexpr (KIND == 2) {
+          w.p[8 * k + 2 * c] = u[c] << 16;  // Quants.Bf16 (src/Quants.cs:23-27)
+          w.p[8 * k + 2 * c + 1] = u[c] & 0xFFFF0000u;
+        } else {
+          w.p[4 * k + c] = u[c];
+        }
+      }
+    }
+  }
+  __device__ static float dot(const W &w, const Xs &x) {
+    float a = 0.f, b = 0.f;
+    if constexpr (KIND == 1) {
+#pragma unroll
+      for (int k = 0; k < 16; k++) {
+        a = fma_lo(w.p[k], x.v[2 * k], a);
+        b = fma_hi(w.p[k], x.v[2 * k + 1], b);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; k++) {
+        a = __builtin_fmaf(__uint_as_float(w.p[2 * k]), x.v[2 * k], a);
+        b = __builtin_fmaf(__uint_as_float(w.p[2 * k + 1]), x.v[2 * k + 1], b);
+      }
+    }
+    return a + b;
+  }
+};
+typedef FWide<0> F32w;
+typedef FWide<1> F16w;
+typedef FWide<2> BF16w;
+
 }  // namespace wl
