@@ -67,8 +67,7 @@ int wl_can_decode(int ggml_type);
  * wl_matmul handles the type (the I-quants included, which the CPU path decodes first). */
 int wl_can_matmul(int ggml_type);
 
-/* FastMath.CanIntDot (src/FastMath.cs:27-30) for the formats this library has: 1 for Q8_0,
- * Q4_K and Q6_K (the reference also lists Q4_0 and Q5_K, which this build does not carry). */
+/* FastMath.CanIntDot (src/FastMath.cs:27-30): 1 for Q8_0, Q4_0, Q4_K, Q5_K and Q6_K. */
 int wl_can_int_dot(int ggml_type);
 
 /* Block geometry, GgmlTypes.TryGetLayout (src/Gguf.cs:30-66). Returns 1 when known. */
@@ -92,8 +91,41 @@ int wl_sync(wl_ctx *ctx);
 int wl_upload(wl_ctx *ctx, int ggml_type, const void *blocks, int64_t rows, int64_t cols,
               int64_t row_bytes, int32_t experts, wl_weight **out);
 
-/* Releases a weight's device memory. */
+/* Releases a weight's device memory (a stage view: only the handle). */
 int wl_weight_free(wl_ctx *ctx, wl_weight *w);
+
+/* ---- Stages: LayerStream's slots in HBM (src/LayerStream.cs:36-264) ----
+ * A stage is one slot of device memory holding a layer's tensors at 64-byte aligned offsets,
+ * as LayerStream.Bind lays them out (:182-203). Resident mode (--cache-gb covering the model,
+ * :110-124) uploads every stage once; streaming mode keeps two slots and uploads stage N+1 on
+ * the context's copy stream while stage N computes (StartPrefetch / Acquire / WaitSlot,
+ * :127-181). Ordering is explicit, as the slot tasks make it there:
+ *   wl_stage_upload_async  queue host -> slot copies (host memory from wl_host_alloc copies at
+ *                          link speed and must stay unchanged until the copies are done);
+ *                          they wait for the slot's last wl_stage_release;
+ *   wl_stage_ready         the compute stream waits for the slot's queued copies (Acquire);
+ *   wl_stage_release       the compute queued so far is the slot's last reader (WaitSlot);
+ *   wl_stage_sync          the host waits for the slot's copies. */
+typedef struct wl_stage wl_stage;
+
+/* Pinned host memory (LayerStream's slot buffers, Marshal.AllocHGlobal at :104-108). */
+int wl_host_alloc(int64_t bytes, void **out);
+int wl_host_free(void *p);
+
+/* A slot of `bytes` (Stage.Bytes with its padding, :88-94). */
+int wl_stage_create(wl_ctx *ctx, int64_t bytes, wl_stage **out);
+int wl_stage_free(wl_ctx *ctx, wl_stage *stage);
+
+/* LayerStream.Read into the slot (:206-235): `bytes` of host memory to `offset`, asynchronous. */
+int wl_stage_upload_async(wl_ctx *ctx, wl_stage *stage, const void *host, int64_t offset, int64_t bytes);
+int wl_stage_ready(wl_ctx *ctx, wl_stage *stage);
+int wl_stage_release(wl_ctx *ctx, wl_stage *stage);
+int wl_stage_sync(wl_ctx *ctx, wl_stage *stage);
+
+/* Bind's WeightView of one tensor in the slot (:188-200): no copy, the arguments of wl_upload
+ * at a 64-byte aligned offset. The view reads whatever the slot holds when a call runs. */
+int wl_stage_weight(wl_ctx *ctx, wl_stage *stage, int64_t offset, int ggml_type, int64_t rows, int64_t cols,
+                    int64_t row_bytes, int32_t experts, wl_weight **out);
 
 /* Transformer.MatMul (src/Transformer.cs:483-537), with ForwardBatch's MatMulEach
  * (:544-561) built in: y[t][r] = dot(W[r], x[t]) for T rows of x; `expert` >= 0 selects

@@ -21,6 +21,15 @@ SIGNATURES = {
     "wl_sync": (ctypes.c_int, [P]),
     "wl_upload": (ctypes.c_int, [P, ctypes.c_int, P, I64, I64, I64, I32, PP]),
     "wl_weight_free": (ctypes.c_int, [P, P]),
+    "wl_host_alloc": (ctypes.c_int, [I64, PP]),
+    "wl_host_free": (ctypes.c_int, [P]),
+    "wl_stage_create": (ctypes.c_int, [P, I64, PP]),
+    "wl_stage_free": (ctypes.c_int, [P, P]),
+    "wl_stage_upload_async": (ctypes.c_int, [P, P, P, I64, I64]),
+    "wl_stage_ready": (ctypes.c_int, [P, P]),
+    "wl_stage_release": (ctypes.c_int, [P, P]),
+    "wl_stage_sync": (ctypes.c_int, [P, P]),
+    "wl_stage_weight": (ctypes.c_int, [P, P, I64, ctypes.c_int, I64, I64, I64, I32, PP]),
     "wl_matmul": (ctypes.c_int, [P, P, I32, P, I32, P]),
     "wl_dequant_f32": (ctypes.c_int, [P, P, I64, I64, P]),
     "wl_swiglu": (ctypes.c_int, [P, P, P, P, I32, P, I32, P]),

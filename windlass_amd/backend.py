@@ -145,12 +145,72 @@ class Context:
         """Raw GGUF blocks to HBM, unchanged (LayerStream.Bind, src/LayerStream.cs:182-203)."""
         return WeightView(self, t, blocks, rows, cols, experts, name)
 
+    def stage(self, nbytes):
+        """A LayerStream slot of nbytes in HBM (src/LayerStream.cs:36-124)."""
+        return Stage(self, nbytes)
+
+
+class HostBuffer:
+    """Pinned host memory as a uint8 numpy array (the slot buffers LayerStream reads stages
+    into, src/LayerStream.cs:104-108): copies from it run at link speed."""
+
+    def __init__(self, nbytes):
+        p = ctypes.c_void_p()
+        check(load().wl_host_alloc(int(nbytes), ctypes.byref(p)))
+        self._p = p
+        self.array = np.ctypeslib.as_array((ctypes.c_uint8 * int(nbytes)).from_address(p.value))
+
+    def free(self):
+        if self._p:
+            self.array = None
+            check(load().wl_host_free(self._p))
+            self._p = None
+
+
+class Stage:
+    """One stage slot in HBM: a layer's tensors at 64-byte aligned offsets, filled by
+    asynchronous copies on the context's copy stream (LayerStream.Read / StartPrefetch,
+    src/LayerStream.cs:127-235). ready() makes later calls wait for the copies (Acquire),
+    release() marks the calls queued so far as the slot's last readers (WaitSlot)."""
+
+    def __init__(self, ctx, nbytes):
+        self.ctx = ctx
+        self.Bytes = int(nbytes)
+        h = ctypes.c_void_p()
+        check(load().wl_stage_create(ctx.handle, self.Bytes, ctypes.byref(h)))
+        self.handle = h
+
+    def upload_async(self, host, offset=0):
+        """Queue a copy of host (uint8, kept unchanged until the copy is done) to offset."""
+        host = np.ascontiguousarray(host, dtype=np.uint8).reshape(-1)
+        check(load().wl_stage_upload_async(self.ctx.handle, self.handle, _ptr(host), int(offset), host.size))
+        return host
+
+    def ready(self):
+        check(load().wl_stage_ready(self.ctx.handle, self.handle))
+
+    def release(self):
+        check(load().wl_stage_release(self.ctx.handle, self.handle))
+
+    def sync(self):
+        check(load().wl_stage_sync(self.ctx.handle, self.handle))
+
+    def weight(self, offset, t, rows, cols, experts=1, name="weight"):
+        """Bind's WeightView of the tensor at offset (src/LayerStream.cs:188-200), no copy."""
+        return WeightView(self.ctx, t, None, rows, cols, experts, name, _stage=self, _offset=offset)
+
+    def free(self):
+        if self.handle:
+            check(load().wl_stage_free(self.ctx.handle, self.handle))
+            self.handle = None
+
 
 class WeightView:
     """A tensor's raw blocks in HBM: {Name, Type, Rows, Cols, RowBytes, Experts}
     (src/LayerStream.cs:15-24). Rows counts one expert's rows for stacked tensors."""
 
-    def __init__(self, ctx, t, blocks, rows, cols, experts=1, name="weight", _parent=None, _expert=-1):
+    def __init__(self, ctx, t, blocks, rows, cols, experts=1, name="weight", _parent=None, _expert=-1,
+                 _stage=None, _offset=0):
         self.ctx = ctx
         self.Name = name
         if int(t) not in GgmlType._value2member_map_ or not Quants.CanDecode(t):
@@ -167,6 +227,12 @@ class WeightView:
         self._parent = _parent
         if _parent is not None:
             self.handle = _parent.handle
+            return
+        if _stage is not None:
+            h = ctypes.c_void_p()
+            check(load().wl_stage_weight(ctx.handle, _stage.handle, int(_offset), int(self.Type), self.Rows,
+                                         self.Cols, self.RowBytes, self.Experts, ctypes.byref(h)))
+            self.handle = h
             return
         blocks = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
         if blocks.size != self.Rows * self.Experts * self.RowBytes:

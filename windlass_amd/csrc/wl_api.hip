@@ -29,6 +29,17 @@ struct wl_weight {
   int32_t experts;
   uint8_t *dev;
   size_t bytes;  // rows * experts * row_bytes
+  bool owned;    // false for a view into a stage (wl_stage_weight): the stage owns the memory
+};
+
+// One LayerStream stage slot in HBM (src/LayerStream.cs:36-59, 62-124): its tensors at their
+// 64-byte aligned offsets. `copied` marks the end of the copies queued into it, `released` the
+// last compute that reads it (the next copy into the slot waits for that).
+struct wl_stage {
+  uint8_t *dev;
+  size_t bytes;
+  hipEvent_t copied, released;
+  bool has_release;
 };
 
 // S_PART holds the K-chunk partials of split GEMV rows, S_XB the bf16 copy of x for the GEMM,
@@ -39,6 +50,7 @@ struct wl_ctx {
   int device;
   int num_cu;
   hipStream_t stream;
+  hipStream_t copy;  // stage uploads (default priority), created on first use
   int int_dot;  // Transformer.IntDot (src/Transformer.cs:23)
   // growable scratch (device)
   void *buf[S_COUNT];
@@ -168,6 +180,10 @@ extern "C" void wl_destroy(wl_ctx *c) {
   for (void *&b : c->buf)
     if (b) hipFree(b);
   hipStreamDestroy(c->stream);
+  if (c->copy) {
+    hipStreamSynchronize(c->copy);
+    hipStreamDestroy(c->copy);
+  }
   delete c;
 }
 
@@ -201,6 +217,7 @@ extern "C" int wl_upload(wl_ctx *c, int type, const void *blocks, int64_t rows, 
   w->row_bytes = row_bytes;
   w->experts = experts;
   w->bytes = (size_t)rows * (size_t)experts * (size_t)row_bytes;
+  w->owned = true;
   if (hipMalloc(&w->dev, w->bytes + kWeightPad) != hipSuccess) {
     delete w;
     return fail(WL_E_NOMEM, "cannot allocate %zu bytes for a %s weight", (size_t)(rows * experts * row_bytes),
@@ -221,8 +238,128 @@ extern "C" int wl_upload(wl_ctx *c, int type, const void *blocks, int64_t rows, 
 extern "C" int wl_weight_free(wl_ctx *c, wl_weight *w) {
   if (!w) return WL_OK;
   if (c) hipStreamSynchronize(c->stream);
-  hipFree(w->dev);
+  if (w->owned) hipFree(w->dev);
   delete w;
+  return WL_OK;
+}
+
+// ------------------------------------------------------------------------------ stages
+
+extern "C" int wl_host_alloc(int64_t bytes, void **out) {
+  if (!out || bytes <= 0) return fail(WL_E_ARG, "wl_host_alloc: bad argument");
+  *out = nullptr;
+  if (hipHostMalloc(out, (size_t)bytes, hipHostMallocDefault) != hipSuccess) {
+    *out = nullptr;
+    return fail(WL_E_NOMEM, "cannot allocate %lld bytes of pinned host memory", (long long)bytes);
+  }
+  return WL_OK;
+}
+
+extern "C" int wl_host_free(void *p) {
+  if (p) WL_HIP(hipHostFree(p), "hipHostFree");
+  return WL_OK;
+}
+
+extern "C" int wl_stage_create(wl_ctx *c, int64_t bytes, wl_stage **out) {
+  if (!c || !out) return fail(WL_E_ARG, "wl_stage_create: null argument");
+  *out = nullptr;
+  if (bytes <= 0) return fail(WL_E_SHAPE, "wl_stage_create: empty stage");
+  WL_HIP(hipSetDevice(c->device), "hipSetDevice");
+  if (!c->copy) WL_HIP(hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking), "copy stream");
+  wl_stage *s = new wl_stage();
+  s->bytes = (size_t)bytes;
+  if (hipMalloc(&s->dev, s->bytes + kWeightPad) != hipSuccess) {
+    delete s;
+    return fail(WL_E_NOMEM, "cannot allocate a stage of %lld bytes", (long long)bytes);
+  }
+  hipError_t e = hipEventCreateWithFlags(&s->copied, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&s->released, hipEventDisableTiming);
+  // the padding after the slot is read by the kernels' aligned windows: keep it defined
+  if (e == hipSuccess) e = hipMemsetAsync(s->dev + s->bytes, 0, kWeightPad, c->copy);
+  if (e == hipSuccess) e = hipEventRecord(s->copied, c->copy);
+  if (e != hipSuccess) {
+    hipFree(s->dev);
+    delete s;
+    return hip_fail(e, "stage setup");
+  }
+  *out = s;
+  return WL_OK;
+}
+
+extern "C" int wl_stage_free(wl_ctx *c, wl_stage *s) {
+  if (!s) return WL_OK;
+  if (c) {
+    hipStreamSynchronize(c->stream);
+    if (c->copy) hipStreamSynchronize(c->copy);
+  }
+  hipEventDestroy(s->copied);
+  hipEventDestroy(s->released);
+  hipFree(s->dev);
+  delete s;
+  return WL_OK;
+}
+
+extern "C" int wl_stage_upload_async(wl_ctx *c, wl_stage *s, const void *host, int64_t offset, int64_t bytes) {
+  if (!c || !s || !host) return fail(WL_E_ARG, "wl_stage_upload_async: null argument");
+  if (offset < 0 || bytes < 0 || (size_t)(offset + bytes) > s->bytes)
+    return fail(WL_E_ARG, "stage upload of %lld bytes at %lld is outside the %zu-byte slot", (long long)bytes,
+                (long long)offset, s->bytes);
+  if (bytes == 0) return WL_OK;
+  // the slot is overwritten only after the compute that read it last (LayerStream.WaitSlot)
+  if (s->has_release) WL_HIP(hipStreamWaitEvent(c->copy, s->released, 0), "wait for the slot's release");
+  WL_HIP(hipMemcpyAsync(s->dev + offset, host, (size_t)bytes, hipMemcpyHostToDevice, c->copy), "stage copy");
+  WL_HIP(hipEventRecord(s->copied, c->copy), "stage copy event");
+  return WL_OK;
+}
+
+extern "C" int wl_stage_ready(wl_ctx *c, wl_stage *s) {
+  if (!c || !s) return fail(WL_E_ARG, "wl_stage_ready: null argument");
+  WL_HIP(hipStreamWaitEvent(c->stream, s->copied, 0), "wait for the stage's copies");
+  return WL_OK;
+}
+
+extern "C" int wl_stage_release(wl_ctx *c, wl_stage *s) {
+  if (!c || !s) return fail(WL_E_ARG, "wl_stage_release: null argument");
+  WL_HIP(hipEventRecord(s->released, c->stream), "stage release event");
+  s->has_release = true;
+  return WL_OK;
+}
+
+extern "C" int wl_stage_sync(wl_ctx *c, wl_stage *s) {
+  if (!c || !s) return fail(WL_E_ARG, "wl_stage_sync: null argument");
+  WL_HIP(hipEventSynchronize(s->copied), "stage copies");
+  return WL_OK;
+}
+
+extern "C" int wl_stage_weight(wl_ctx *c, wl_stage *s, int64_t offset, int type, int64_t rows, int64_t cols,
+                               int64_t row_bytes, int32_t experts, wl_weight **out) {
+  if (!c || !s || !out) return fail(WL_E_ARG, "wl_stage_weight: null argument");
+  *out = nullptr;
+  int be, bb;
+  if (!wl_type_layout(type, &be, &bb) || !wl::dequant_supports(type))
+    return fail(WL_E_UNSUPPORTED, "Windlass cannot decode %s weights on the GPU.", type_name(type));
+  if (rows <= 0 || cols <= 0 || experts <= 0) return fail(WL_E_SHAPE, "wl_stage_weight: empty shape");
+  if (cols % be) return fail(WL_E_SHAPE, "%s rows of %lld values are not whole blocks of %d", type_name(type),
+                             (long long)cols, be);
+  if (row_bytes != cols / be * bb)
+    return fail(WL_E_SHAPE, "row_bytes %lld does not match %lld %s values (%lld)", (long long)row_bytes,
+                (long long)cols, type_name(type), (long long)(cols / be * bb));
+  if (cols > (1 << 30) || rows > (1 << 30)) return fail(WL_E_SHAPE, "wl_stage_weight: dimension too large");
+  const size_t bytes = (size_t)rows * (size_t)experts * (size_t)row_bytes;
+  // LayerStream lays tensors out at 64-byte aligned offsets (src/LayerStream.cs:64,195-201)
+  if (offset < 0 || offset % 64 || (size_t)offset + bytes > s->bytes)
+    return fail(WL_E_ARG, "a %zu-byte tensor at offset %lld does not fit the %zu-byte stage at 64-byte alignment",
+                bytes, (long long)offset, s->bytes);
+  wl_weight *w = new wl_weight();
+  w->type = type;
+  w->rows = rows;
+  w->cols = cols;
+  w->row_bytes = row_bytes;
+  w->experts = experts;
+  w->dev = s->dev + offset;
+  w->bytes = bytes;
+  w->owned = false;
+  *out = w;
   return WL_OK;
 }
 
