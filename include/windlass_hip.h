@@ -200,6 +200,63 @@ int wl_moe_ffn_dev(wl_ctx *ctx, const float *d_logits, int32_t k, int32_t renorm
                    const wl_weight *gate_exps, const wl_weight *up_exps,
                    const wl_weight *down_exps, const float *d_x, int32_t T, float *d_out);
 
+/* ---- The rest of a decoder layer on device-resident activations ----
+ * Transformer.Layer's other operations (src/Transformer.cs:177-232), stream-ordered on the
+ * context like the *_dev products, so a whole decode step runs with its activations in HBM.
+ * Pointers are device memory. */
+
+/* RmsNormRows (src/Transformer.cs:446-457): y[r] = x[r] / sqrt(mean(x[r]^2) + eps) * w, the sum
+ * of squares in double; in place allowed. */
+int wl_rms_norm_dev(wl_ctx *ctx, const float *d_x, int64_t rows, int64_t dim, const float *d_w, float eps,
+                    float *d_y);
+
+/* RopeTable + Rope (src/Transformer.cs:396-431) on T rows of `heads` heads, in place: the
+ * first rope_dims values of each head rotate by the angles (pos * freq_scale) * base^(-2i/n),
+ * pairs (2i, 2i+1), or (i, i + n/2) when neox. Row t's position is d_pos[t], or pos0 + t when
+ * d_pos is null. */
+int wl_rope_dev(wl_ctx *ctx, float *d_x, int32_t T, int32_t heads, int32_t head_dim, int32_t rope_dims,
+                int32_t neox, int32_t pos0, const int32_t *d_pos, double base, double freq_scale);
+
+/* ToHalf (src/Transformer.cs:342-348): rows pos0..pos0+T-1 of the fp16 K and V caches. */
+int wl_kv_store_dev(wl_ctx *ctx, const float *d_k, const float *d_v, int32_t T, int32_t kv_dim, uint16_t *d_K,
+                    uint16_t *d_V, int32_t pos0);
+
+/* Attention (src/Transformer.cs:351-393): row t attends to positions 0..pos0+t of the fp16
+ * caches; softmax with exp and the denominator in double; grouped KV heads. */
+int wl_attention_dev(wl_ctx *ctx, const float *d_q, int32_t T, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                     const uint16_t *d_K, const uint16_t *d_V, int32_t pos0, float scale, float *d_out);
+
+/* The residual add of Layer (src/Transformer.cs:224,231): x += o * rs. */
+int wl_residual_dev(wl_ctx *ctx, float *d_x, const float *d_o, int64_t n, float rs);
+
+/* Greedy sampling (src/Engine.cs:356-360): the first index of each row's largest logit. */
+int wl_argmax_dev(wl_ctx *ctx, const float *d_logits, int32_t rows, int64_t n, int32_t *d_out);
+
+/* LayerStream.EmbedRow (src/LayerStream.cs:238-257): the decoded embedding rows of T tokens
+ * (token ids on the host) into d_x [T][cols]. */
+int wl_embed_dev(wl_ctx *ctx, const wl_weight *embd, const int32_t *tokens, int32_t T, float *d_x);
+
+/* One decoder layer: the weights and vectors Transformer.Layer reads from its stage
+ * (src/Transformer.cs:177-232) and the model constants it uses (ModelConfig). Vectors are
+ * device fp32 arrays; the optional ones are null when the architecture has none (biases: qwen2;
+ * q/k norms per head: qwen3). Zero scales mean the defaults (1/sqrt(head_dim), 1). */
+typedef struct wl_layer_desc {
+  const wl_weight *attn_q, *attn_k, *attn_v, *attn_output, *ffn_gate, *ffn_up, *ffn_down;
+  const float *d_attn_norm, *d_ffn_norm;
+  const float *d_q_bias, *d_k_bias, *d_v_bias;
+  const float *d_q_norm, *d_k_norm;
+  int32_t embd, heads, kv_heads, head_dim, rope_dims, neox;
+  double rope_base, rope_freq_scale;
+  float eps, attention_scale, residual_scale;
+} wl_layer_desc;
+
+/* Transformer.Layer (src/Transformer.cs:177-232) for T tokens at positions pos0.. of one
+ * sequence: x [T][embd] (device) is updated in place and the tokens' keys and values go to
+ * rows pos0.. of the fp16 caches d_K / d_V [positions][kv_heads * head_dim]. Every activation
+ * stays in HBM (the context's scratch); stream-ordered, no host wait. */
+int wl_layer_dev(wl_ctx *ctx, const wl_layer_desc *layer, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
+                 uint16_t *d_V);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,6 +14,7 @@ libwindlass_hip.so (include/windlass_hip.h):
                                   of MatMul (src/Transformer.cs:504-524)
 - ``FastMath``                    CanIntDot/NeedsK/Fits/Quantize (src/FastMath.cs:27-91)
 - ``Stage`` / ``HostBuffer``      LayerStream's slots and their reads (src/LayerStream.cs:36-264), in HBM
+- ``LayerDesc`` + wl_layer_dev    Transformer.Layer (src/Transformer.cs:177-232) on device-resident activations
 
 Errors map to the reference's exception kinds: ``NotSupportedError`` (NotSupportedException),
 ``ShapeError`` (ArgumentException), ``ArgumentOutOfRangeError``, ``BackendError`` (device
@@ -21,9 +22,9 @@ failure). There is no CPU fallback: without the built library every call raises.
 """
 from ._lib import (ArgumentOutOfRangeError, BackendError, NotSupportedError, ShapeError,
                    library_path, load)
-from .backend import (Context, FastMath, GgmlType, HostBuffer, QActs, Quants, Stage, Transformer, WeightView,
-                      layout)
+from .backend import (Context, FastMath, GgmlType, HostBuffer, LayerDesc, QActs, Quants, Stage, Transformer,
+                      WeightView, layout)
 
 __all__ = ["ArgumentOutOfRangeError", "BackendError", "NotSupportedError", "ShapeError",
-           "library_path", "load", "Context", "FastMath", "GgmlType", "HostBuffer", "QActs", "Quants", "Stage",
+           "library_path", "load", "Context", "FastMath", "GgmlType", "HostBuffer", "LayerDesc", "QActs", "Quants", "Stage",
            "Transformer", "WeightView", "layout"]

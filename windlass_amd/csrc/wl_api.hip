@@ -15,6 +15,7 @@
 #include "wl_gemm.h"
 #include "wl_gemv.h"
 #include "wl_intdot.h"
+#include "wl_layer.h"
 #include "wl_moe.h"
 
 // Bytes of padding after every weight buffer: the GEMV reads the aligned dwords around
@@ -44,7 +45,9 @@ struct wl_stage {
 
 // S_PART holds the K-chunk partials of split GEMV rows, S_XB the bf16 copy of x for the GEMM,
 // S_QA the 8-bit activations of the integer path.
-enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB, S_QA, S_COUNT };
+// S_L* are wl_layer_dev's activations.
+enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB, S_QA, S_ROPE, S_ATT,
+       S_LXN, S_LQ, S_LK, S_LV, S_LATT, S_LO, S_LG, S_LU, S_COUNT };
 
 struct wl_ctx {
   int device;
@@ -781,5 +784,142 @@ extern "C" int wl_quantize(wl_ctx *c, const float *x, int32_t T, int32_t cols, i
     WL_HIP(hipMemcpyAsync(bsums, qa.bsums, (size_t)T * (cols / 16) * 2, hipMemcpyDeviceToHost, c->stream),
            "copy bsums");
   WL_HIP(hipStreamSynchronize(c->stream), "quantize");
+  return WL_OK;
+}
+
+// ----------------------------------------------------------------- the rest of a layer
+
+extern "C" int wl_rms_norm_dev(wl_ctx *c, const float *d_x, int64_t rows, int64_t dim, const float *d_w, float eps,
+                               float *d_y) {
+  if (!c || !d_x || !d_w || !d_y) return fail(WL_E_ARG, "wl_rms_norm_dev: null argument");
+  if (rows < 0 || dim <= 0) return fail(WL_E_SHAPE, "wl_rms_norm_dev: %lld rows of %lld", (long long)rows,
+                                        (long long)dim);
+  WL_HIP(wl::rms_norm_launch(d_x, rows, dim, d_w, eps, d_y, c->stream), "rms norm");
+  return WL_OK;
+}
+
+extern "C" int wl_rope_dev(wl_ctx *c, float *d_x, int32_t T, int32_t heads, int32_t head_dim, int32_t rope_dims,
+                           int32_t neox, int32_t pos0, const int32_t *d_pos, double base, double freq_scale) {
+  if (!c || !d_x) return fail(WL_E_ARG, "wl_rope_dev: null argument");
+  if (T < 0 || heads <= 0 || head_dim <= 0 || rope_dims <= 0 || rope_dims > head_dim || rope_dims % 2)
+    return fail(WL_E_SHAPE, "wl_rope_dev: %d rotated of %d per head", rope_dims, head_dim);
+  int rc = ensure(c, S_ROPE, (size_t)T * rope_dims * sizeof(float));
+  if (rc) return rc;
+  WL_HIP(wl::rope_launch(d_x, (int64_t)heads * head_dim, T, heads, head_dim, rope_dims, neox, d_pos, pos0, base,
+                         freq_scale, (float *)c->buf[S_ROPE], c->stream),
+         "rope");
+  return WL_OK;
+}
+
+extern "C" int wl_kv_store_dev(wl_ctx *c, const float *d_k, const float *d_v, int32_t T, int32_t kv_dim,
+                               uint16_t *d_K, uint16_t *d_V, int32_t pos0) {
+  if (!c || !d_k || !d_v || !d_K || !d_V) return fail(WL_E_ARG, "wl_kv_store_dev: null argument");
+  if (T < 0 || kv_dim <= 0 || pos0 < 0) return fail(WL_E_SHAPE, "wl_kv_store_dev: bad shape");
+  const int64_t off = (int64_t)pos0 * kv_dim;
+  WL_HIP(wl::kv_store_launch(d_k, d_v, (int64_t)T * kv_dim, d_K + off, d_V + off, c->stream), "kv store");
+  return WL_OK;
+}
+
+extern "C" int wl_attention_dev(wl_ctx *c, const float *d_q, int32_t T, int32_t heads, int32_t kv_heads,
+                                int32_t head_dim, const uint16_t *d_K, const uint16_t *d_V, int32_t pos0, float scale,
+                                float *d_out) {
+  if (!c || !d_q || !d_K || !d_V || !d_out) return fail(WL_E_ARG, "wl_attention_dev: null argument");
+  if (T < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || head_dim <= 0 || pos0 < 0)
+    return fail(WL_E_SHAPE, "wl_attention_dev: %d heads over %d KV heads", heads, kv_heads);
+  int rc = ensure(c, S_ATT, (size_t)T * heads * (pos0 + T) * sizeof(float));
+  if (rc) return rc;
+  const int64_t qd = (int64_t)heads * head_dim;
+  WL_HIP(wl::attention_launch(d_q, qd, T, d_K, d_V, kv_heads * head_dim, heads, kv_heads, head_dim, pos0, scale,
+                              (float *)c->buf[S_ATT], d_out, qd, c->stream),
+         "attention");
+  return WL_OK;
+}
+
+extern "C" int wl_residual_dev(wl_ctx *c, float *d_x, const float *d_o, int64_t n, float rs) {
+  if (!c || !d_x || !d_o) return fail(WL_E_ARG, "wl_residual_dev: null argument");
+  WL_HIP(wl::residual_launch(d_x, d_o, n, rs, c->stream), "residual");
+  return WL_OK;
+}
+
+extern "C" int wl_argmax_dev(wl_ctx *c, const float *d_logits, int32_t rows, int64_t n, int32_t *d_out) {
+  if (!c || !d_logits || !d_out) return fail(WL_E_ARG, "wl_argmax_dev: null argument");
+  if (rows < 0 || n <= 0) return fail(WL_E_SHAPE, "wl_argmax_dev: bad shape");
+  WL_HIP(wl::argmax_launch(d_logits, rows, n, d_out, c->stream), "argmax");
+  return WL_OK;
+}
+
+extern "C" int wl_embed_dev(wl_ctx *c, const wl_weight *embd, const int32_t *tokens, int32_t T, float *d_x) {
+  if (!c || !embd || !tokens || !d_x) return fail(WL_E_ARG, "wl_embed_dev: null argument");
+  for (int t = 0; t < T; t++) {
+    if (tokens[t] < 0 || tokens[t] >= embd->rows * embd->experts)
+      return fail(WL_E_ARG, "Token id %d is outside the vocabulary.", tokens[t]);
+    WL_HIP(wl::dequant_launch(embd->type, embd->dev, embd->row_bytes, tokens[t], 1, embd->cols,
+                              d_x + (int64_t)t * embd->cols, c->stream),
+           "embedding row");
+  }
+  return WL_OK;
+}
+
+// Transformer.Layer (src/Transformer.cs:177-232) with every activation in HBM.
+extern "C" int wl_layer_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
+                            uint16_t *d_V) {
+  if (!c || !L || !d_x || !d_K || !d_V) return fail(WL_E_ARG, "wl_layer_dev: null argument");
+  if (!L->attn_q || !L->attn_k || !L->attn_v || !L->attn_output || !L->ffn_gate || !L->ffn_up || !L->ffn_down ||
+      !L->d_attn_norm || !L->d_ffn_norm)
+    return fail(WL_E_ARG, "wl_layer_dev: a required tensor is missing");
+  const int E = L->embd, H = L->heads, KH = L->kv_heads, HD = L->head_dim;
+  if (T <= 0 || pos0 < 0 || E <= 0 || H <= 0 || KH <= 0 || H % KH || HD <= 0)
+    return fail(WL_E_SHAPE, "wl_layer_dev: bad shape");
+  const int QD = H * HD, KD = KH * HD;
+  const int64_t FF = L->ffn_gate->rows;
+  if (L->attn_q->cols != E || L->attn_q->rows != QD || L->attn_k->rows != KD || L->attn_v->rows != KD ||
+      L->attn_output->cols != QD || L->attn_output->rows != E || L->ffn_gate->cols != E || L->ffn_up->rows != FF ||
+      L->ffn_down->cols != FF || L->ffn_down->rows != E)
+    return fail(WL_E_SHAPE, "wl_layer_dev: tensor shapes do not match the layer");
+  int rc;
+  if ((rc = ensure(c, S_LXN, (size_t)T * E * 4)) || (rc = ensure(c, S_LQ, (size_t)T * QD * 4)) ||
+      (rc = ensure(c, S_LK, (size_t)T * KD * 4)) || (rc = ensure(c, S_LV, (size_t)T * KD * 4)) ||
+      (rc = ensure(c, S_LATT, (size_t)T * QD * 4)) || (rc = ensure(c, S_LO, (size_t)T * E * 4)) ||
+      (rc = ensure(c, S_LG, (size_t)T * FF * 4)) || (rc = ensure(c, S_LU, (size_t)T * FF * 4)))
+    return rc;
+  float *xn = (float *)c->buf[S_LXN], *q = (float *)c->buf[S_LQ], *k = (float *)c->buf[S_LK],
+        *v = (float *)c->buf[S_LV], *att = (float *)c->buf[S_LATT], *o = (float *)c->buf[S_LO],
+        *g = (float *)c->buf[S_LG], *u = (float *)c->buf[S_LU];
+  const float rs = L->residual_scale != 0.f ? L->residual_scale : 1.f;
+  // attention block
+  if ((rc = wl_rms_norm_dev(c, d_x, T, E, L->d_attn_norm, L->eps, xn))) return rc;
+  if (T <= 8) {
+    const wl_weight *ws[3] = {L->attn_q, L->attn_k, L->attn_v};
+    float *ys[3] = {q, k, v};
+    if ((rc = wl_matmul_multi_dev(c, 3, ws, xn, T, ys))) return rc;
+  } else if ((rc = matmul_dev(c, L->attn_q, -1, xn, T, q)) || (rc = matmul_dev(c, L->attn_k, -1, xn, T, k)) ||
+             (rc = matmul_dev(c, L->attn_v, -1, xn, T, v))) {
+    return rc;
+  }
+  if (L->d_q_bias) WL_HIP(wl::bias_launch(q, L->d_q_bias, T, QD, c->stream), "q bias");
+  if (L->d_k_bias) WL_HIP(wl::bias_launch(k, L->d_k_bias, T, KD, c->stream), "k bias");
+  if (L->d_v_bias) WL_HIP(wl::bias_launch(v, L->d_v_bias, T, KD, c->stream), "v bias");
+  if (L->d_q_norm && (rc = wl_rms_norm_dev(c, q, (int64_t)T * H, HD, L->d_q_norm, L->eps, q))) return rc;
+  if (L->d_k_norm && (rc = wl_rms_norm_dev(c, k, (int64_t)T * KH, HD, L->d_k_norm, L->eps, k))) return rc;
+  const int rd = L->rope_dims > 0 ? L->rope_dims : HD;
+  const double fs = L->rope_freq_scale != 0.0 ? L->rope_freq_scale : 1.0;
+  if ((rc = wl_rope_dev(c, q, T, H, HD, rd, L->neox, pos0, nullptr, L->rope_base, fs)) ||
+      (rc = wl_rope_dev(c, k, T, KH, HD, rd, L->neox, pos0, nullptr, L->rope_base, fs)) ||
+      (rc = wl_kv_store_dev(c, k, v, T, KD, d_K, d_V, pos0)))
+    return rc;
+  const float scale = L->attention_scale != 0.f ? L->attention_scale : 1.0f / (float)sqrt((double)HD);
+  if ((rc = wl_attention_dev(c, q, T, H, KH, HD, d_K, d_V, pos0, scale, att))) return rc;
+  if ((rc = matmul_dev(c, L->attn_output, -1, att, T, o)) || (rc = wl_residual_dev(c, d_x, o, (int64_t)T * E, rs)))
+    return rc;
+  // feed-forward block
+  if ((rc = wl_rms_norm_dev(c, d_x, T, E, L->d_ffn_norm, L->eps, xn))) return rc;
+  if (L->ffn_gate->type == L->ffn_up->type) {
+    if ((rc = wl_gate_up_dev(c, L->ffn_gate, L->ffn_up, -1, xn, T, g))) return rc;
+  } else {
+    if ((rc = matmul_dev(c, L->ffn_gate, -1, xn, T, g)) || (rc = matmul_dev(c, L->ffn_up, -1, xn, T, u))) return rc;
+    WL_HIP(wl::silu_mul_launch(g, u, (int64_t)T * FF, c->stream), "silu");
+  }
+  if ((rc = matmul_dev(c, L->ffn_down, -1, g, T, o)) || (rc = wl_residual_dev(c, d_x, o, (int64_t)T * E, rs)))
+    return rc;
   return WL_OK;
 }
