@@ -212,10 +212,12 @@ int wl_rms_norm_dev(wl_ctx *ctx, const float *d_x, int64_t rows, int64_t dim, co
 
 /* RopeTable + Rope (src/Transformer.cs:396-431) on T rows of `heads` heads, in place: the
  * first rope_dims values of each head rotate by the angles (pos * freq_scale) * base^(-2i/n),
+ * each divided by d_freqs[i] when d_freqs (rope_freqs.weight, n/2 device floats) is given;
  * pairs (2i, 2i+1), or (i, i + n/2) when neox. Row t's position is d_pos[t], or pos0 + t when
  * d_pos is null. */
 int wl_rope_dev(wl_ctx *ctx, float *d_x, int32_t T, int32_t heads, int32_t head_dim, int32_t rope_dims,
-                int32_t neox, int32_t pos0, const int32_t *d_pos, double base, double freq_scale);
+                int32_t neox, int32_t pos0, const int32_t *d_pos, double base, double freq_scale,
+                const float *d_freqs);
 
 /* ToHalf (src/Transformer.cs:342-348): rows pos0..pos0+T-1 of the fp16 K and V caches. */
 int wl_kv_store_dev(wl_ctx *ctx, const float *d_k, const float *d_v, int32_t T, int32_t kv_dim, uint16_t *d_K,
@@ -239,12 +241,14 @@ int wl_embed_dev(wl_ctx *ctx, const wl_weight *embd, const int32_t *tokens, int3
 /* One decoder layer: the weights and vectors Transformer.Layer reads from its stage
  * (src/Transformer.cs:177-232) and the model constants it uses (ModelConfig). Vectors are
  * device fp32 arrays; the optional ones are null when the architecture has none (biases: qwen2;
- * q/k norms per head: qwen3). Zero scales mean the defaults (1/sqrt(head_dim), 1). */
+ * q/k norms per head: qwen3; RoPE frequency factors: rope_freqs.weight of Llama 3.1 and later,
+ * shared by every layer, src/Transformer.cs:37). Zero scales mean the defaults (1/sqrt(head_dim),
+ * 1). */
 typedef struct wl_layer_desc {
   const wl_weight *attn_q, *attn_k, *attn_v, *attn_output, *ffn_gate, *ffn_up, *ffn_down;
   const float *d_attn_norm, *d_ffn_norm;
   const float *d_q_bias, *d_k_bias, *d_v_bias;
-  const float *d_q_norm, *d_k_norm;
+  const float *d_q_norm, *d_k_norm, *d_rope_freqs;
   int32_t embd, heads, kv_heads, head_dim, rope_dims, neox;
   double rope_base, rope_freq_scale;
   float eps, attention_scale, residual_scale;

@@ -25,6 +25,39 @@ def test_header_and_binding_agree():
     assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
 
 
+def declared_arity():
+    """Each declared function's parameter count, from the header's text."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(wl_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_binding_argument_counts_match_header():
+    arity = declared_arity()
+    assert set(arity) == set(_lib.SIGNATURES)
+    for name, (_, args) in _lib.SIGNATURES.items():
+        assert len(args) == arity[name], (name, len(args), arity[name])
+
+
+def test_layer_desc_layout_matches_header(tmp_path):
+    """ctypes' LayerDesc has wl_layer_desc's offsets and size, as gcc lays the struct out."""
+    import subprocess
+    from windlass_amd.backend import LayerDesc
+    names = [f[0] for f in LayerDesc._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "windlass_hip.h"\nint main(void) {\n'
+                   + "".join('  printf("%%zu\\n", offsetof(wl_layer_desc, %s));\n' % n for n in names)
+                   + '  printf("%zu\\n", sizeof(wl_layer_desc));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [getattr(LayerDesc, n).offset for n in names] + [ctypes.sizeof(LayerDesc)]
+    assert got == want, list(zip(names + ["sizeof"], got, want))
+
+
 def test_library_exports_every_declared_symbol():
     lib = windlass_amd.load()
     for name in declared_functions():

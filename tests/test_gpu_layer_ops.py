@@ -1,0 +1,207 @@
+"""The rest of a decoder layer on device-resident activations, one operation at a time, against
+numpy restatements that follow src/Transformer.cs's operation order:
+
+- RmsNormRows (:446-457): double sum of squares, float mean, float scale;
+- RopeTable + Rope (:396-431): running double angle, frequency factors, partial rotation,
+  both pair layouts, explicit positions;
+- ToHalf (:342-348): fp16 round-to-nearest-even into rows pos0.. of the caches;
+- Attention (:351-393): four partial score sums, exp in double, in-order value sums;
+- the residual add (:224,231) and Sampler's greedy pick (src/Engine.cs:356-360);
+- LayerStream.EmbedRow (src/LayerStream.cs:238-257) against the oracle's row decode.
+
+Tolerances: the integer and elementwise operations (fp16 store, residual, argmax, embed) are
+bit-exact. RMSNorm, RoPE and attention take one double sum or a double cos/sin/exp that the
+device computes in another order or with another library; they are held to 1 ulp (RMSNorm,
+RoPE) and to 2e-6 of the row's largest value (attention, whose softmax denominator is a tree
+sum on the device)."""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_common import blocks
+from layer_ref import attention_ref, fp16_cache, greedy_ref, rms_norm_ref, rope_ref, to_half_ref
+from windlass_amd._lib import ArgumentOutOfRangeError, ShapeError, check, load
+from windlass_amd.backend import Context, GgmlType
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+DEV = torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def P(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def dev(a):
+    """A device copy; the caller keeps the tensor alive until the library's queued work ends."""
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    torch.cuda.synchronize()  # the library's stream does not wait for torch's
+    return t
+
+
+def host(ctx, t):
+    ctx.sync()
+    return t.cpu().numpy()
+
+
+def ulps(a, b):
+    """Distance in units in the last place between two float32 arrays of finite values."""
+    ia = np.asarray(a, F32).view(np.int32).astype(np.int64)
+    ib = np.asarray(b, F32).view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, -(ia & 0x7fffffff), ia)
+    ib = np.where(ib < 0, -(ib & 0x7fffffff), ib)
+    return np.abs(ia - ib)
+
+
+# ---------------------------------------------------------------- tests
+
+
+@pytest.mark.parametrize("rows,dim,eps", [(5, 300, 1e-5), (1, 8192, 1e-6), (7, 64, 1e-5), (3, 1, 1e-5)])
+def test_rms_norm(ctx, rows, dim, eps):
+    rng = np.random.default_rng(dim)
+    x = (rng.standard_normal((rows, dim), dtype=F32) * F32(3)).astype(F32)
+    w = (F32(1) + F32(0.2) * rng.standard_normal(dim, dtype=F32)).astype(F32)
+    dx, dw, dy = dev(x), dev(w), torch.empty((rows, dim), device=DEV)
+    check(load().wl_rms_norm_dev(ctx.handle, P(dx), rows, dim, P(dw), eps, P(dy)))
+    got, want = host(ctx, dy), rms_norm_ref(x, w, eps)
+    assert ulps(got, want).max() <= 1
+    # in place (the per-head q/k norms run with x == y)
+    check(load().wl_rms_norm_dev(ctx.handle, P(dx), rows, dim, P(dw), eps, P(dx)))
+    assert np.array_equal(host(ctx, dx), got)
+
+
+@pytest.mark.parametrize("neox", [0, 1])
+@pytest.mark.parametrize("heads,hd,n,base,fs,factors,positions", [
+    (4, 64, 64, 500000.0, 1.0, False, None),            # llama: every value rotates
+    (2, 128, 128, 1000000.0, 1.0, True, [0, 7, 8191]),  # rope_freqs factors, explicit positions
+    (3, 64, 32, 10000.0, 0.25, False, None),            # partial rotation, linear scaling
+])
+def test_rope(ctx, neox, heads, hd, n, base, fs, factors, positions):
+    rng = np.random.default_rng(hd + n)
+    T, pos0 = 3, 41
+    pos = positions if positions is not None else [pos0 + t for t in range(T)]
+    x = rng.standard_normal((T, heads * hd), dtype=F32)
+    freqs = (F32(1) + F32(7) * rng.random(n // 2, dtype=F32)).astype(F32) if factors else None
+    dx = dev(x)
+    dpos = dev(np.asarray(pos, np.int32)) if positions is not None else None
+    dfr = dev(freqs) if factors else None
+    check(load().wl_rope_dev(ctx.handle, P(dx), T, heads, hd, n, neox, pos0, P(dpos) if dpos is not None else None,
+                             base, fs, P(dfr) if dfr is not None else None))
+    got, want = host(ctx, dx), rope_ref(x, heads, hd, n, neox, pos, base, fs, freqs)
+    assert ulps(got, want).max() <= 1
+    if n < hd:  # values past rope_dims are untouched
+        r = got.reshape(T, heads, hd)[:, :, n:]
+        assert np.array_equal(r, x.reshape(T, heads, hd)[:, :, n:])
+
+
+def test_kv_store_rounds_to_nearest_even(ctx):
+    rng = np.random.default_rng(3)
+    kd, T, pos0, cap = 96, 5, 11, 20
+    k = rng.standard_normal((T, kd), dtype=F32) * F32(100)
+    v = rng.standard_normal((T, kd), dtype=F32) * F32(1e-6)   # fp16 subnormals
+    k[0, :4] = [70000.0, -65520.0, 65519.0, 2.0 ** -25]      # overflow, the rounding edge, underflow
+    v[1, :3] = [1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, -0.0]  # ties go to even
+    k[2, :3] = [np.nan, -np.nan, -np.inf]
+    sentinel = np.full((cap, kd), 0x7bcd, np.int16)
+    dK, dV = dev(sentinel), dev(sentinel)
+    dk, dv = dev(k), dev(v)  # held until the queued kernel has read them
+    check(load().wl_kv_store_dev(ctx.handle, P(dk), P(dv), T, kd, P(dK), P(dV), pos0))
+    K, V = host(ctx, dK), host(ctx, dV)
+    for got, src in ((K[pos0:pos0 + T], k), (V[pos0:pos0 + T], v)):
+        want = to_half_ref(src).view(np.int16)
+        bad = np.argwhere(got != want)
+        assert bad.size == 0, [(tuple(b), float(src[tuple(b)]), hex(int(got[tuple(b)]) & 0xffff),
+                               hex(int(want[tuple(b)]) & 0xffff)) for b in bad[:8]]
+    for c in (K, V):  # rows outside pos0..pos0+T-1 untouched
+        assert np.array_equal(c[:pos0], sentinel[:pos0]) and np.array_equal(c[pos0 + T:], sentinel[pos0 + T:])
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd,T,pos0", [
+    (4, 2, 64, 3, 5),      # grouped heads, a prefill chunk after cached positions
+    (8, 1, 70, 1, 300),    # one KV head; head_dim with a tail past the four partial sums; > 256 positions
+    (2, 2, 128, 9, 0),     # a prompt from position 0
+])
+def test_attention(ctx, heads, kv_heads, hd, T, pos0):
+    rng = np.random.default_rng(hd * 7 + T)
+    kd, n = kv_heads * hd, pos0 + T
+    K, V = fp16_cache(rng, n, kd), fp16_cache(rng, n, kd)
+    q = rng.standard_normal((T, heads * hd), dtype=F32)
+    scale = F32(1) / F32(math.sqrt(hd))
+    out = torch.empty((T, heads * hd), device=DEV)
+    dq, dK, dV = dev(q), dev(K.view(np.int16)), dev(V.view(np.int16))
+    check(load().wl_attention_dev(ctx.handle, P(dq), T, heads, kv_heads, hd, P(dK), P(dV), pos0, float(scale),
+                                  P(out)))
+    got = host(ctx, out)
+    want = attention_ref(q, K.astype(F32), V.astype(F32), heads, kv_heads, hd, pos0, scale)
+    err = np.abs(got - want).max(axis=1)
+    assert (err <= 2e-6 * np.abs(want).max(axis=1)).all(), err
+
+
+def test_residual(ctx):
+    rng = np.random.default_rng(5)
+    x, o = rng.standard_normal(1001, dtype=F32), rng.standard_normal(1001, dtype=F32)
+    dx = dev(x)
+    do = dev(o)
+    check(load().wl_residual_dev(ctx.handle, P(dx), P(do), x.size, 0.75))
+    assert np.array_equal(host(ctx, dx), (x + (o * F32(0.75)).astype(F32)).astype(F32))
+
+
+def test_argmax_first_maximum(ctx):
+    rng = np.random.default_rng(6)
+    n = 32000 + 17
+    rows = rng.standard_normal((8, n), dtype=F32)
+    rows[1, [5, 900, 31000]] = 50.0            # ties: the first index wins
+    rows[2, :] = -np.inf                       # no value beats logits[0]
+    rows[3, 0] = np.nan                        # nothing compares greater than a NaN at 0
+    rows[4, [3, 10]] = [np.nan, 99.0]          # a NaN later is skipped
+    rows[5, n - 1] = np.inf
+    rows[6, :] = 0.0
+    rows[6, 77] = -0.0
+    rows[7, 12345] = rows[7].max() + F32(1e-3)
+    out = torch.empty(8, dtype=torch.int32, device=DEV)
+    dr = dev(rows)
+    check(load().wl_argmax_dev(ctx.handle, P(dr), 8, n, P(out)))
+    assert host(ctx, out).tolist() == [greedy_ref(r) for r in rows]
+
+
+@pytest.mark.parametrize("t", [GgmlType.Q4_K, GgmlType.Q8_0, GgmlType.Q6_K, GgmlType.F16, GgmlType.BF16])
+def test_embed_rows(ctx, t):
+    vocab, cols = 97, 512
+    data = blocks(t, vocab, cols, seed=int(t))
+    w = ctx.upload(t, data, vocab, cols)
+    toks = [0, 96, 5, 5, 40]
+    ids = (ctypes.c_int32 * len(toks))(*toks)
+    out = torch.empty((len(toks), cols), device=DEV)
+    check(load().wl_embed_dev(ctx.handle, w.handle, ids, len(toks), P(out)))
+    got = host(ctx, out)
+    rb = data.size // vocab
+    want = np.stack([oracle.decode(int(t), data[i * rb:(i + 1) * rb], cols) for i in toks])
+    assert np.array_equal(got.view(np.uint32), want.astype(F32).view(np.uint32))
+    bad = (ctypes.c_int32 * 1)(vocab)
+    with pytest.raises(ArgumentOutOfRangeError):
+        check(load().wl_embed_dev(ctx.handle, w.handle, bad, 1, P(out)))
+    w.free()
+
+
+def test_shape_errors(ctx):
+    L = load()
+    x = torch.zeros(4096, device=DEV)
+    with pytest.raises(ShapeError):  # heads not a multiple of the KV heads
+        check(L.wl_attention_dev(ctx.handle, P(x), 1, 6, 4, 8, P(x), P(x), 0, 1.0, P(x)))
+    with pytest.raises(ShapeError):  # an odd number of rotated values
+        check(L.wl_rope_dev(ctx.handle, P(x), 1, 2, 8, 7, 0, 0, None, 10000.0, 1.0, None))
+    with pytest.raises(ShapeError):  # more rotated values than a head holds
+        check(L.wl_rope_dev(ctx.handle, P(x), 1, 2, 8, 10, 0, 0, None, 10000.0, 1.0, None))
+    with pytest.raises(ShapeError):
+        check(L.wl_rms_norm_dev(ctx.handle, P(x), 2, 0, P(x), 1e-5, P(x)))

@@ -22,7 +22,7 @@ SIGNATURES = {
     "wl_upload": (ctypes.c_int, [P, ctypes.c_int, P, I64, I64, I64, I32, PP]),
     "wl_weight_free": (ctypes.c_int, [P, P]),
     "wl_rms_norm_dev": (ctypes.c_int, [P, P, I64, I64, P, ctypes.c_float, P]),
-    "wl_rope_dev": (ctypes.c_int, [P, P, I32, I32, I32, I32, I32, I32, P, ctypes.c_double, ctypes.c_double]),
+    "wl_rope_dev": (ctypes.c_int, [P, P, I32, I32, I32, I32, I32, I32, P, ctypes.c_double, ctypes.c_double, P]),
     "wl_kv_store_dev": (ctypes.c_int, [P, P, P, I32, I32, P, P, I32]),
     "wl_attention_dev": (ctypes.c_int, [P, P, I32, I32, I32, I32, P, P, I32, ctypes.c_float, P]),
     "wl_residual_dev": (ctypes.c_int, [P, P, P, I64, ctypes.c_float]),

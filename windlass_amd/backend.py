@@ -278,7 +278,8 @@ class LayerDesc(ctypes.Structure):
     Weight fields take WeightView handles, vector fields device pointers (0 when absent)."""
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down",
-        "d_attn_norm", "d_ffn_norm", "d_q_bias", "d_k_bias", "d_v_bias", "d_q_norm", "d_k_norm")] + [
+        "d_attn_norm", "d_ffn_norm", "d_q_bias", "d_k_bias", "d_v_bias", "d_q_norm", "d_k_norm",
+        "d_rope_freqs")] + [
         ("embd", ctypes.c_int32), ("heads", ctypes.c_int32), ("kv_heads", ctypes.c_int32),
         ("head_dim", ctypes.c_int32), ("rope_dims", ctypes.c_int32), ("neox", ctypes.c_int32),
         ("rope_base", ctypes.c_double), ("rope_freq_scale", ctypes.c_double),

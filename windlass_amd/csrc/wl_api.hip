@@ -799,14 +799,15 @@ extern "C" int wl_rms_norm_dev(wl_ctx *c, const float *d_x, int64_t rows, int64_
 }
 
 extern "C" int wl_rope_dev(wl_ctx *c, float *d_x, int32_t T, int32_t heads, int32_t head_dim, int32_t rope_dims,
-                           int32_t neox, int32_t pos0, const int32_t *d_pos, double base, double freq_scale) {
+                           int32_t neox, int32_t pos0, const int32_t *d_pos, double base, double freq_scale,
+                           const float *d_freqs) {
   if (!c || !d_x) return fail(WL_E_ARG, "wl_rope_dev: null argument");
   if (T < 0 || heads <= 0 || head_dim <= 0 || rope_dims <= 0 || rope_dims > head_dim || rope_dims % 2)
     return fail(WL_E_SHAPE, "wl_rope_dev: %d rotated of %d per head", rope_dims, head_dim);
   int rc = ensure(c, S_ROPE, (size_t)T * rope_dims * sizeof(float));
   if (rc) return rc;
   WL_HIP(wl::rope_launch(d_x, (int64_t)heads * head_dim, T, heads, head_dim, rope_dims, neox, d_pos, pos0, base,
-                         freq_scale, (float *)c->buf[S_ROPE], c->stream),
+                         freq_scale, d_freqs, (float *)c->buf[S_ROPE], c->stream),
          "rope");
   return WL_OK;
 }
@@ -903,8 +904,8 @@ extern "C" int wl_layer_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32
   if (L->d_k_norm && (rc = wl_rms_norm_dev(c, k, (int64_t)T * KH, HD, L->d_k_norm, L->eps, k))) return rc;
   const int rd = L->rope_dims > 0 ? L->rope_dims : HD;
   const double fs = L->rope_freq_scale != 0.0 ? L->rope_freq_scale : 1.0;
-  if ((rc = wl_rope_dev(c, q, T, H, HD, rd, L->neox, pos0, nullptr, L->rope_base, fs)) ||
-      (rc = wl_rope_dev(c, k, T, KH, HD, rd, L->neox, pos0, nullptr, L->rope_base, fs)) ||
+  if ((rc = wl_rope_dev(c, q, T, H, HD, rd, L->neox, pos0, nullptr, L->rope_base, fs, L->d_rope_freqs)) ||
+      (rc = wl_rope_dev(c, k, T, KH, HD, rd, L->neox, pos0, nullptr, L->rope_base, fs, L->d_rope_freqs)) ||
       (rc = wl_kv_store_dev(c, k, v, T, KD, d_K, d_V, pos0)))
     return rc;
   const float scale = L->attention_scale != 0.f ? L->attention_scale : 1.0f / (float)sqrt((double)HD);

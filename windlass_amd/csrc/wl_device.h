@@ -33,6 +33,34 @@ __device__ __forceinline__ float half_bits_exact(uint32_t h) {
   return __uint_as_float(bits);
 }
 
+// binary32 -> binary16 as Half.FromFloat gives it (src/Half.cs:29-57): round to nearest even
+// through the subnormals, overflow to infinity, a NaN to the quiet NaN 0x7e00 with its sign.
+// Integer arithmetic, so the bits do not depend on the hardware conversion's rounding mode or
+// its handling of fp16 subnormals.
+__device__ __forceinline__ uint16_t to_half(float v) {
+  const uint32_t f = __builtin_bit_cast(uint32_t, v);
+  const uint32_t sign = (f >> 16) & 0x8000u, fe = (f >> 23) & 0xffu;
+  uint32_t m = f & 0x7fffffu;
+  if (fe == 0xffu) return (uint16_t)(sign | 0x7c00u | (m ? 0x200u : 0u));
+  const int e = (int)fe - 112;  // the binary16 biased exponent
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  uint32_t h, rem, halfway;
+  if (e <= 0) {  // subnormal result: the implicit bit joins the shifted significand
+    if (e < -10) return (uint16_t)sign;
+    m |= 0x800000u;
+    const int sh = 14 - e;
+    h = m >> sh;
+    rem = m & ((1u << sh) - 1u);
+    halfway = 1u << (sh - 1);
+  } else {
+    h = ((uint32_t)e << 10) | (m >> 13);
+    rem = m & 0x1fffu;
+    halfway = 0x1000u;
+  }
+  h += (rem > halfway || (rem == halfway && (h & 1u))) ? 1u : 0u;  // a carry may reach the exponent
+  return (uint16_t)(sign | h);
+}
+
 // Hardware fp16 -> fp32 (exact for every finite value; used inside the GEMVs).
 __device__ __forceinline__ float half_lo(uint32_t w) {
   return (float)__builtin_bit_cast(half2_t, w).x;

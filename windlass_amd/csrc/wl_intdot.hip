@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__
     for (int i = 0; i < 4; i++) qi[i] = (int)roundf(v[i] * id);  // Math.Round(.., AwayFromZero)
     if (in) {
       *qw = pack4(qi[0], qi[1], qi[2], qi[3]);
-      if ((lane & 7) == 0) d[(int64_t)t * (cols / 32) + base / 32] = (float)(_Float16)dd;  // Half.Round
+      if ((lane & 7) == 0) d[(int64_t)t * (cols / 32) + base / 32] = half_bits_exact(to_half(dd));  // Half.Round
     }
     return;
   }

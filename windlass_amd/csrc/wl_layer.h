@@ -9,7 +9,7 @@ hipError_t rms_norm_launch(const float *x, int64_t rows, int64_t dim, const floa
                            hipStream_t st);
 // cs: T * n floats of scratch for the cos/sin table
 hipError_t rope_launch(float *x, int64_t ldx, int T, int heads, int hd, int n, int neox, const int *pos, int pos0,
-                       double base, double freq_scale, float *cs, hipStream_t st);
+                       double base, double freq_scale, const float *freqs, float *cs, hipStream_t st);
 hipError_t kv_store_launch(const float *k, const float *v, int64_t n, uint16_t *K, uint16_t *V, hipStream_t st);
 // scores: T * heads * (pos0 + T) floats of scratch
 hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *K, const uint16_t *V, int kv_dim,

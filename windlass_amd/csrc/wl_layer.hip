@@ -11,6 +11,8 @@
 // softmax denominator) are tree sums here, so their last bit can differ.
 #include "wl_layer.h"
 
+#include "wl_device.h"
+
 #include <math.h>
 
 #pragma clang fp contract(off)
@@ -57,16 +59,18 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, int64_t d
 }
 
 // RopeTable (src/Transformer.cs:396-414): cos/sin per rotated pair at each row's position,
-// the angle a running product in double as there. One thread per row.
+// the angle a running product in double as there, divided by the pair's frequency factor when
+// the model has them (rope_freqs.weight). One thread per row.
 __global__ void rope_table_kernel(const int *__restrict__ pos, int pos0, int T, int n, double theta_scale,
-                                  double freq_scale, float *__restrict__ cs) {
+                                  double freq_scale, const float *__restrict__ freqs, float *__restrict__ cs) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= T) return;
   double theta = (double)(pos ? pos[t] : pos0 + t) * freq_scale;
   float *c = cs + (int64_t)t * n;
   for (int i = 0; i < n / 2; i++) {
-    c[2 * i] = (float)cos(theta);
-    c[2 * i + 1] = (float)sin(theta);
+    const double a = freqs ? theta / (double)freqs[i] : theta;
+    c[2 * i] = (float)cos(a);
+    c[2 * i + 1] = (float)sin(a);
     theta *= theta_scale;
   }
 }
@@ -88,14 +92,13 @@ __global__ void rope_kernel(float *__restrict__ x, int64_t ldx, int heads, int h
   o[b] = x0 * s + x1 * c;
 }
 
-// ToHalf (src/Transformer.cs:342-348): Half.FromFloat rounds to nearest even, as the hardware
-// conversion does.
+// ToHalf (src/Transformer.cs:342-348) of one token's keys and values.
 __global__ void kv_store_kernel(const float *__restrict__ k, const float *__restrict__ v, int64_t n,
                                 uint16_t *__restrict__ K, uint16_t *__restrict__ V) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  K[i] = __builtin_bit_cast(uint16_t, (_Float16)k[i]);
-  V[i] = __builtin_bit_cast(uint16_t, (_Float16)v[i]);
+  K[i] = to_half(k[i]);
+  V[i] = to_half(v[i]);
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
@@ -158,6 +161,8 @@ __global__ void residual_kernel(float *__restrict__ x, const float *__restrict__
 }
 
 // Greedy sampling (src/Engine.cs:356-360): the first index of the largest logit of each row.
+// NaNs never win a comparison, so they are skipped, except at index 0: the reference starts
+// from index 0 and nothing compares greater than a NaN there, so such a row gives 0.
 __global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int64_t n,
                                                      int *__restrict__ out) {
   __shared__ float sv[256];
@@ -186,7 +191,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ l
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) out[blockIdx.x] = si[0] == 0x7fffffff ? 0 : si[0];
+  if (threadIdx.x == 0) out[blockIdx.x] = (si[0] == 0x7fffffff || l[0] != l[0]) ? 0 : si[0];
 }
 
 // AddBias (src/Transformer.cs:433-443): y[t][i] += b[i].
@@ -227,10 +232,10 @@ hipError_t rms_norm_launch(const float *x, int64_t rows, int64_t dim, const floa
 }
 
 hipError_t rope_launch(float *x, int64_t ldx, int T, int heads, int hd, int n, int neox, const int *pos, int pos0,
-                       double base, double freq_scale, float *cs, hipStream_t st) {
+                       double base, double freq_scale, const float *freqs, float *cs, hipStream_t st) {
   if (T <= 0) return hipSuccess;
   hipLaunchKernelGGL(rope_table_kernel, dim3(blocks_of(T, 64)), dim3(64), 0, st, pos, pos0, T, n,
-                     pow(base, -2.0 / n), freq_scale, cs);
+                     pow(base, -2.0 / n), freq_scale, freqs, cs);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(rope_kernel, dim3(blocks_of((int64_t)heads * (n / 2), 256), T), dim3(256), 0, st, x, ldx, heads,
