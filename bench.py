@@ -60,6 +60,12 @@ def parse():
     ap.add_argument("--stream", action="store_true",
                     help="instead of the resident layer: the layer streamed from pinned host memory "
                          "through two HBM stage slots (copy of layer N+1 beside the compute of N)")
+    ap.add_argument("--decode", action="store_true",
+                    help="instead of the layer: whole-token greedy decode of the 70B model with every "
+                         "layer, the embedding, the head and the KV cache resident in HBM")
+    ap.add_argument("--layers", type=int, default=LAYERS, help="with --decode: decoder layers")
+    ap.add_argument("--prompt", type=int, default=128, help="with --decode: prompt tokens before decoding")
+    ap.add_argument("--tokens", type=int, default=64, help="with --decode: timed greedy tokens")
     ap.add_argument("--calibrate", type=int, default=0, metavar="MIB",
                     help="before warm-up, run a plain elementwise copy (torch.neg) of MIB MiB three "
                          "times, untimed: the HBM counters of a kernel of known traffic")
@@ -85,6 +91,8 @@ def main():
         return run_formats(args)
     if args.stream:
         return run_stream(args)
+    if args.decode:
+        return run_decode(args)
     T = args.batch
     if not 1 <= T <= 8:
         sys.exit("--batch must be 1..8")
@@ -318,6 +326,90 @@ def run_stream(args):
             "overlap": round(max(copy_s, compute_s) / stream_s, 3),
             "resident_note": "with every stage resident (288 GB HBM holds the 42.5 GB file) a layer takes the compute time"}
     print(json.dumps(line), flush=True)
+
+
+VOCAB = 128256
+
+
+def run_decode(args):
+    """Whole-token greedy decode of Llama-3.3-70B Q4_K_M on one GPU with every tensor resident
+    (windlass_amd.DeviceTransformer: Transformer.Forward, src/Transformer.cs:83-125, and the greedy
+    loop, src/Engine.cs:356-360). 80 distinct layers in HBM (each its own copy of one synthetic
+    layer's blocks), a Q4_K embedding and a Q6_K head of 128256 rows, fp16 KV caches. The prompt
+    runs as one prefill pass (the MFMA GEMMs), then --warmup greedy tokens untimed and --tokens
+    timed; each token's id is read back to the host before the next step, as the engine does."""
+    import torch
+    import windlass_amd
+    from windlass_amd import DeviceTransformer, ModelConfig, synth
+    from windlass_amd.backend import Context
+
+    rng = np.random.default_rng(0x57494E44 + 4000)
+    host = {n: synth.blocks(t, r, c, rng) for n, t, r, c in LAYER}
+    names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate",
+             "up": "ffn_up", "down": "ffn_down"}
+    windlass_amd.load()
+    ctx = Context(0)
+    dev = torch.device("cuda:0")
+
+    def vocab_blocks(t):  # 1/8 of the rows synthesised, repeated (content does not change the timing)
+        return np.tile(synth.blocks(t, VOCAB // 8, HIDDEN, rng), 8)
+
+    def norm():
+        return torch.from_numpy((1 + 0.2 * rng.standard_normal(HIDDEN)).astype(np.float32)).to(dev)
+
+    t0 = time.perf_counter()
+    weights = {"token_embd": ctx.upload(Q4_K, vocab_blocks(Q4_K), VOCAB, HIDDEN, name="token_embd"),
+               "output": ctx.upload(Q6_K, vocab_blocks(Q6_K), VOCAB, HIDDEN, name="output")}
+    vectors = {"output_norm": norm()}
+    for l in range(args.layers):
+        for n, t, r, c in LAYER:
+            key = "blk.%d.%s" % (l, names[n])
+            weights[key] = ctx.upload(t, host[n], r, c, name=key)
+        vectors["blk.%d.attn_norm" % l], vectors["blk.%d.ffn_norm" % l] = norm(), norm()
+    load_s = time.perf_counter() - t0
+    cfg = ModelConfig(layers=args.layers, embd=HIDDEN, heads=HEADS, kv_heads=KV_HEADS, head_dim=HEAD_DIM,
+                      rope_base=500000.0, eps=1e-5)
+    ctxlen = args.prompt + args.warmup + args.tokens
+    m = DeviceTransformer(ctx, cfg, weights, vectors, ctxlen)
+    prompt = [int(v) for v in rng.integers(0, VOCAB, args.prompt)]
+    ctx.sync()
+    t0 = time.perf_counter()
+    m.forward(prompt, 0)
+    tok = m.sample()
+    prefill_s = time.perf_counter() - t0
+    pos = args.prompt
+    for _ in range(args.warmup):
+        m.forward([tok], pos)
+        tok = m.sample()
+        pos += 1
+    t0 = time.perf_counter()
+    for _ in range(args.tokens):
+        m.forward([tok], pos)
+        tok = m.sample()
+        pos += 1
+    decode_s = time.perf_counter() - t0
+    per_tok = decode_s / args.tokens
+    wbytes = sum(w.Rows * w.RowBytes for k, w in weights.items() if k != "token_embd") + HIDDEN * 2 * 4 * args.layers
+    emb_row = HIDDEN // 256 * 144
+    kv_bytes = args.layers * 2 * 2 * KV_HEADS * HEAD_DIM * (args.prompt + args.warmup + args.tokens / 2)
+    line = {"metric": "70B Q4_K_M whole-token greedy decode, every tensor resident in HBM",
+            "value": round(1.0 / per_tok, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.tokens,
+            "warmup": args.warmup, "ms_per_step": round(per_tok * 1e3, 3), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "fp32 accumulate over Q4_K/Q6_K blocks",
+            "data": "synthetic seeded GGUF blocks; random prompt ids; random-init norms",
+            "config": {"workload": "Llama-3.3-70B Q4_K_M: %d layers (hidden 8192, FFN 28672, 64/8 heads of 128), "
+                                   "vocab 128256, prompt %d then %d timed tokens"
+                                   % (args.layers, args.prompt, args.tokens), "batch": 1},
+            "ms_per_layer": round(per_tok * 1e3 / args.layers, 4),
+            "weights_read_per_token_bytes": int(wbytes + emb_row),
+            "kv_read_per_token_bytes_mean": int(kv_bytes),
+            "effective_GBps": round((wbytes + emb_row + kv_bytes) / per_tok / 1e9, 1),
+            "prefill_tokens_per_s": round(args.prompt / prefill_s, 1), "prefill_s": round(prefill_s, 4),
+            "load_s": round(load_s, 2)}
+    print(json.dumps(line), flush=True)
+    for w in weights.values():
+        w.free()
+    ctx.close()
 
 
 # ggml type id -> name, for --formats

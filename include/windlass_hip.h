@@ -182,6 +182,13 @@ int wl_quantize_dev(wl_ctx *ctx, const float *d_x, int32_t T, int32_t cols, int3
 int wl_matmul_dev(wl_ctx *ctx, const wl_weight *w, int32_t expert, const float *d_x, int32_t T,
                   float *d_y);
 
+/* MatMul followed by Layer's residual add (src/Transformer.cs:224,231): d_y [T][rows] +=
+ * (W x) * rs, the product rounded to float first and the add as two roundings, so the bits
+ * equal wl_matmul_dev then wl_residual_dev. Up to 8 tokens the add is the GEMV's own store (no
+ * extra launch). */
+int wl_matmul_add_dev(wl_ctx *ctx, const wl_weight *w, int32_t expert, const float *d_x, int32_t T,
+                      float *d_y, float rs);
+
 /* Several matrices that read the same x in ONE launch (Layer's q, k and v,
  * src/Transformer.cs:186-188): d_ys[i] is [T][rows_i]. n <= 4; types may differ. */
 int wl_matmul_multi_dev(wl_ctx *ctx, int32_t n, const wl_weight *const *ws, const float *d_x,

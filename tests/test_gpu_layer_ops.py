@@ -131,6 +131,9 @@ def test_kv_store_rounds_to_nearest_even(ctx):
     (4, 2, 64, 3, 5),      # grouped heads, a prefill chunk after cached positions
     (8, 1, 70, 1, 300),    # one KV head; head_dim with a tail past the four partial sums; > 256 positions
     (2, 2, 128, 9, 0),     # a prompt from position 0
+    (2, 1, 128, 3, 254),   # rows of 255, 256 and 257 positions: one chunk, then two
+    (8, 2, 128, 2, 600),   # three chunks of 256 positions
+    (4, 4, 64, 1, 1000),   # four chunks, head dim 64
 ])
 def test_attention(ctx, heads, kv_heads, hd, T, pos0):
     rng = np.random.default_rng(hd * 7 + T)
@@ -205,3 +208,92 @@ def test_shape_errors(ctx):
         check(L.wl_rope_dev(ctx.handle, P(x), 1, 2, 8, 10, 0, 0, None, 10000.0, 1.0, None))
     with pytest.raises(ShapeError):
         check(L.wl_rms_norm_dev(ctx.handle, P(x), 2, 0, P(x), 1e-5, P(x)))
+
+
+def test_layer_equals_its_operations(ctx):
+    """wl_layer_dev is the operations above in Transformer.Layer's order (src/Transformer.cs:177-232):
+    the same layer run one operation at a time through the C ABI gives the same bits, with every
+    option the tiny models leave out (partial RoPE, frequency factors, biases, per-head q/k
+    norms, residual and attention scales) and cached positions before the rows."""
+    from windlass_amd import LayerDesc
+    L, h = load(), ctx.handle
+    rng = np.random.default_rng(11)
+    E, H, KH, HD, FF, T, pos0, cap = 256, 4, 2, 64, 512, 3, 5, 16
+    QD, KD, rd, rs, asc = H * HD, KH * HD, 32, 0.5, 0.1
+    mats = {"attn_q": (GgmlType.Q4_K, QD, E), "attn_k": (GgmlType.Q8_0, KD, E), "attn_v": (GgmlType.Q6_K, KD, E),
+            "attn_output": (GgmlType.Q4_K, E, QD), "ffn_gate": (GgmlType.Q4_K, FF, E),
+            "ffn_up": (GgmlType.Q4_K, FF, E), "ffn_down": (GgmlType.Q6_K, E, FF)}
+    w = {n: ctx.upload(t, blocks(t, r, c, seed=i), r, c, name=n) for i, (n, (t, r, c)) in enumerate(mats.items())}
+    vec = lambda n, s=0.2, base=1.0: dev((base + s * rng.standard_normal(n)).astype(F32))  # noqa: E731
+    v = {"attn_norm": vec(E), "ffn_norm": vec(E), "q_bias": vec(QD, 0.1, 0.0), "k_bias": vec(KD, 0.1, 0.0),
+         "v_bias": vec(KD, 0.1, 0.0), "q_norm": vec(HD), "k_norm": vec(HD),
+         "freqs": dev((1 + 3 * rng.random(rd // 2)).astype(F32))}
+    x0 = rng.standard_normal((T, E), dtype=F32)
+    cache = rng.standard_normal((cap, KD), dtype=F32).astype(np.float16).view(np.int16)
+    d = LayerDesc()
+    for n in mats:
+        setattr(d, n, w[n].handle.value)
+    d.d_attn_norm, d.d_ffn_norm = v["attn_norm"].data_ptr(), v["ffn_norm"].data_ptr()
+    d.d_q_bias, d.d_k_bias, d.d_v_bias = (v[k].data_ptr() for k in ("q_bias", "k_bias", "v_bias"))
+    d.d_q_norm, d.d_k_norm, d.d_rope_freqs = v["q_norm"].data_ptr(), v["k_norm"].data_ptr(), v["freqs"].data_ptr()
+    d.embd, d.heads, d.kv_heads, d.head_dim, d.rope_dims, d.neox = E, H, KH, HD, rd, 1
+    d.rope_base, d.rope_freq_scale, d.eps, d.attention_scale, d.residual_scale = 10000.0, 0.5, 1e-6, asc, rs
+    xa, Ka, Va = dev(x0), dev(cache), dev(cache)
+    check(L.wl_layer_dev(h, ctypes.byref(d), P(xa), T, pos0, P(Ka), P(Va)))
+    # the same, one operation at a time
+    xb, Kb, Vb = dev(x0), dev(cache), dev(cache)
+    xn = torch.empty((T, E), device=DEV)
+    q, k, vv = (torch.empty((T, n), device=DEV) for n in (QD, KD, KD))
+    att, o = torch.empty((T, QD), device=DEV), torch.empty((T, E), device=DEV)
+    g = torch.empty((T, FF), device=DEV)
+    c = ctypes.c_float
+    check(L.wl_rms_norm_dev(h, P(xb), T, E, P(v["attn_norm"]), c(1e-6), P(xn)))
+    ws = (ctypes.c_void_p * 3)(*(w[n].handle.value for n in ("attn_q", "attn_k", "attn_v")))
+    ys = (ctypes.c_void_p * 3)(q.data_ptr(), k.data_ptr(), vv.data_ptr())
+    check(L.wl_matmul_multi_dev(h, 3, ws, P(xn), T, ys))
+    ctx.sync()
+    q += v["q_bias"]
+    k += v["k_bias"]
+    vv += v["v_bias"]
+    torch.cuda.synchronize()
+    check(L.wl_rms_norm_dev(h, P(q), T * H, HD, P(v["q_norm"]), c(1e-6), P(q)))
+    check(L.wl_rms_norm_dev(h, P(k), T * KH, HD, P(v["k_norm"]), c(1e-6), P(k)))
+    for y, nh in ((q, H), (k, KH)):
+        check(L.wl_rope_dev(h, P(y), T, nh, HD, rd, 1, pos0, None, 10000.0, 0.5, P(v["freqs"])))
+    check(L.wl_kv_store_dev(h, P(k), P(vv), T, KD, P(Kb), P(Vb), pos0))
+    check(L.wl_attention_dev(h, P(q), T, H, KH, HD, P(Kb), P(Vb), pos0, c(asc), P(att)))
+    check(L.wl_matmul_dev(h, w["attn_output"].handle, -1, P(att), T, P(o)))
+    check(L.wl_residual_dev(h, P(xb), P(o), T * E, c(rs)))
+    check(L.wl_rms_norm_dev(h, P(xb), T, E, P(v["ffn_norm"]), c(1e-6), P(xn)))
+    check(L.wl_gate_up_dev(h, w["ffn_gate"].handle, w["ffn_up"].handle, -1, P(xn), T, P(g)))
+    check(L.wl_matmul_dev(h, w["ffn_down"].handle, -1, P(g), T, P(o)))
+    check(L.wl_residual_dev(h, P(xb), P(o), T * E, c(rs)))
+    for a, b in ((xa, xb), (Ka, Kb), (Va, Vb)):
+        assert np.array_equal(host(ctx, a).view(np.uint32 if a.dtype == torch.float32 else np.uint16),
+                              host(ctx, b).view(np.uint32 if b.dtype == torch.float32 else np.uint16))
+    assert not np.array_equal(host(ctx, Ka)[pos0:pos0 + T], cache[pos0:pos0 + T])  # the rows were written
+    for x in w.values():
+        x.free()
+
+
+@pytest.mark.parametrize("t", [GgmlType.Q4_K, GgmlType.Q6_K, GgmlType.Q8_0, GgmlType.Q5_K, GgmlType.IQ4_XS,
+                               GgmlType.F16])
+@pytest.mark.parametrize("rows,cols", [(256, 512), (512, 16384), (300, 2048)])
+@pytest.mark.parametrize("T", [1, 3, 8, 12])
+def test_matmul_add_equals_matmul_then_residual(ctx, t, rows, cols, T):
+    """wl_matmul_add_dev's add in the GEMV's own store (the unsplit one-token store, the K-chunk
+    combine at 16384 columns, the batched combine) and through the residual kernel past 8
+    tokens gives the bits of wl_matmul_dev then wl_residual_dev."""
+    L = load()
+    w = ctx.upload(t, blocks(t, rows, cols, seed=rows + T), rows, cols)
+    rng = np.random.default_rng(cols + T)
+    x = dev(rng.standard_normal((T, cols), dtype=F32))
+    y0 = rng.standard_normal((T, rows), dtype=F32)
+    for rs in (1.0, 0.5):
+        ya, yb = dev(y0), dev(y0)
+        o = torch.empty((T, rows), device=DEV)
+        check(L.wl_matmul_add_dev(ctx.handle, w.handle, -1, P(x), T, P(ya), ctypes.c_float(rs)))
+        check(L.wl_matmul_dev(ctx.handle, w.handle, -1, P(x), T, P(o)))
+        check(L.wl_residual_dev(ctx.handle, P(yb), P(o), T * rows, ctypes.c_float(rs)))
+        assert np.array_equal(host(ctx, ya).view(np.uint32), host(ctx, yb).view(np.uint32)), rs
+    w.free()

@@ -126,103 +126,24 @@ def test_gpu_greedy_tokens_match_cpu(gpu, key):
         w.free()
 
 
-class DeviceModel:
-    """The same model with every activation in HBM: embedding rows, wl_layer_dev per layer
-    (Transformer.Layer, src/Transformer.cs:177-232) over fp16 KV caches on the device, the final
-    norm, the output product and greedy sampling on the device (src/Engine.cs:356-360)."""
-
-    def __init__(self, ctx, key, max_pos=64):
-        import ctypes
-        from tiny_model import EMBD, EPS, HEADS, KV_HEADS, LAYERS, build
-        from windlass_amd import LayerDesc
-        from windlass_amd._lib import load
-        self.ctx, self.L, self.torch = ctx, load(), torch
-        self.arch, t = build(key)
-        self.hd = EMBD // HEADS
-        self.layers, self.embd = LAYERS, EMBD
-        dev = torch.device("cuda:0")
-        self.dev = dev
-        up = lambda w, n: ctx.upload(w.type, w.data, w.rows, w.cols, name=n)  # noqa: E731
-        vec = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)  # noqa: E731
-        self.w, self.v = {}, {}
-        for n, x in t.items():
-            if not isinstance(x, np.ndarray):  # a quantized or float tensor (tiny_model.Tensor)
-                if n not in self.w and not (n == "output" and x is t["token_embd"]):
-                    self.w[n] = up(x, n)
-            else:
-                self.v[n] = vec(x)
-        self.w.setdefault("output", self.w["token_embd"])
-        self.descs = []
-        P = lambda a: a.data_ptr() if a is not None else None  # noqa: E731
-        for l in range(LAYERS):
-            p = "blk.%d." % l
-            d = LayerDesc()
-            for f, n in (("attn_q", "attn_q"), ("attn_k", "attn_k"), ("attn_v", "attn_v"),
-                         ("attn_output", "attn_output"), ("ffn_gate", "ffn_gate"), ("ffn_up", "ffn_up"),
-                         ("ffn_down", "ffn_down")):
-                setattr(d, f, self.w[p + n].handle.value)
-            d.d_attn_norm, d.d_ffn_norm = P(self.v[p + "attn_norm"]), P(self.v[p + "ffn_norm"])
-            d.d_q_bias, d.d_k_bias, d.d_v_bias = (P(self.v.get(p + "attn_%s.bias" % c)) for c in "qkv")
-            d.d_q_norm, d.d_k_norm = P(self.v.get(p + "attn_q_norm")), P(self.v.get(p + "attn_k_norm"))
-            d.embd, d.heads, d.kv_heads, d.head_dim, d.rope_dims = EMBD, HEADS, KV_HEADS, self.hd, self.hd
-            d.neox = int(self.arch != "llama")
-            d.rope_base = 500000.0 if self.arch == "llama" else 1000000.0
-            d.rope_freq_scale, d.eps = 1.0, float(EPS)
-            self.descs.append(d)
-        kd = KV_HEADS * self.hd
-        self.K = torch.zeros((LAYERS, max_pos, kd), dtype=torch.int16, device=dev)
-        self.V = torch.zeros((LAYERS, max_pos, kd), dtype=torch.int16, device=dev)
-        torch.cuda.synchronize()  # the library's stream does not wait for torch's
-        self.ctypes = ctypes
-
-    def forward(self, tokens, pos0):
-        """Logits of the last token (on the device)."""
-        c, torch, L = self.ctypes, self.torch, self.L
-        T = len(tokens)
-        x = torch.empty((T, self.embd), device=self.dev)
-        toks = (c.c_int32 * T)(*tokens)
-        check = __import__("windlass_amd._lib", fromlist=["check"]).check
-        check(L.wl_embed_dev(self.ctx.handle, self.w["token_embd"].handle, toks, T, c.c_void_p(x.data_ptr())))
-        for l, d in enumerate(self.descs):
-            check(L.wl_layer_dev(self.ctx.handle, c.byref(d), c.c_void_p(x.data_ptr()), T, pos0,
-                                 c.c_void_p(self.K[l].data_ptr()), c.c_void_p(self.V[l].data_ptr())))
-        xl = x[T - 1:].contiguous()
-        xn = torch.empty_like(xl)
-        check(L.wl_rms_norm_dev(self.ctx.handle, c.c_void_p(xl.data_ptr()), 1, self.embd,
-                                c.c_void_p(self.v["output_norm"].data_ptr()), c.c_float(1e-5), c.c_void_p(xn.data_ptr())))
-        out = self.w["output"]
-        logits = torch.empty((1, out.Rows), device=self.dev)
-        check(L.wl_matmul_dev(self.ctx.handle, out.handle, -1, c.c_void_p(xn.data_ptr()), 1,
-                              c.c_void_p(logits.data_ptr())))
-        return logits
-
-    def greedy(self, prompt, steps, chunk):
-        c, torch, L = self.ctypes, self.torch, self.L
-        check = __import__("windlass_amd._lib", fromlist=["check"]).check
-        pos, logits = 0, None
-        for i in range(0, len(prompt), chunk):
-            part = prompt[i:i + chunk]
-            logits = self.forward(part, pos)
-            pos += len(part)
-        self.ctx.sync()  # torch reads on its own stream
-        out, seen = [], [logits[0].cpu().numpy()]
-        tok = torch.empty(1, dtype=torch.int32, device=self.dev)
-        for _ in range(steps):
-            check(L.wl_argmax_dev(self.ctx.handle, c.c_void_p(logits.data_ptr()), 1, logits.shape[1],
-                                  c.c_void_p(tok.data_ptr())))
-            self.ctx.sync()
-            t = int(tok.item())
-            out.append(t)
-            logits = self.forward([t], pos)
-            pos += 1
-            self.ctx.sync()
-            seen.append(logits[0].cpu().numpy())
-        return out, seen
-
-    def free(self):
-        for n, w in self.w.items():
-            if n != "output" or w is not self.w["token_embd"]:
-                w.free()
+def device_model(ctx, key, max_positions=64):
+    """The same model with every activation in HBM (windlass_amd.DeviceTransformer): embedding
+    rows, wl_layer_dev per layer (Transformer.Layer, src/Transformer.cs:177-232) over fp16 KV
+    caches on the device, the final norm, the output product and greedy sampling on the device
+    (src/Engine.cs:356-360). Returns the model and the weights to free."""
+    from tiny_model import EMBD, EPS, HEADS, KV_HEADS, LAYERS, build
+    from windlass_amd import DeviceTransformer, ModelConfig
+    arch, t = build(key)
+    dev = torch.device("cuda:0")
+    weights, vectors = {}, {}
+    for n, x in t.items():
+        if isinstance(x, np.ndarray):
+            vectors[n] = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev)
+        elif not (n == "output" and x is t["token_embd"]):  # a tied head reuses token_embd
+            weights[n] = ctx.upload(x.type, x.data, x.rows, x.cols, name=n)
+    cfg = ModelConfig(layers=LAYERS, embd=EMBD, heads=HEADS, kv_heads=KV_HEADS, head_dim=EMBD // HEADS,
+                      neox=arch != "llama", rope_base=500000.0 if arch == "llama" else 1000000.0, eps=float(EPS))
+    return DeviceTransformer(ctx, cfg, weights, vectors, max_positions), weights
 
 
 @pytest.mark.gpu
@@ -232,9 +153,17 @@ def test_gpu_device_resident_greedy_tokens_match_cpu(gpu, key):
     residuals, sampling on the device) gives the CPU backend's greedy tokens."""
     cpu = Model(key, oracle_matmul)
     want, want_logits = cpu.greedy(PROBE, 8, chunk=8)
-    dm = DeviceModel(gpu, key)
-    got, got_logits = dm.greedy(PROBE, 8, chunk=8)
-    dm.free()
+    dm, weights = device_model(gpu, key)
+    got, got_logits = dm.greedy(PROBE, 8, chunk=8, keep_logits=True)
+    # the whole prompt in one pass (T = 12: the bf16 GEMMs and the separate SiLU pass) meets
+    # llama.cpp's bar at the last position
+    dm.forward(PROBE, 0)
+    last = dm.host_logits()
+    for w in weights.values():
+        w.free()
     for a, b in zip(want_logits, got_logits):
         assert np.abs(a - b).max() <= 1e-3 * np.std(a), "%s: logits drift from the CPU backend" % key
     assert got == want, "%s: greedy tokens %s, CPU backend %s" % (key, got, want)
+    ref = np.array(LLAMA_CPP[key]["last"], np.float64)
+    rel = np.abs(last - ref).max() / ref.std()
+    assert rel <= 0.2 and int(np.argmax(last)) == LLAMA_CPP[key]["argmax"][-1], (key, rel)

@@ -15,6 +15,8 @@ libwindlass_hip.so (include/windlass_hip.h):
 - ``FastMath``                    CanIntDot/NeedsK/Fits/Quantize (src/FastMath.cs:27-91)
 - ``Stage`` / ``HostBuffer``      LayerStream's slots and their reads (src/LayerStream.cs:36-264), in HBM
 - ``LayerDesc`` + wl_layer_dev    Transformer.Layer (src/Transformer.cs:177-232) on device-resident activations
+- ``DeviceTransformer``           Transformer.Forward/Head (src/Transformer.cs:83-125) and the greedy
+                                  loop (src/Engine.cs:356-360), every tensor resident in HBM
 
 Errors map to the reference's exception kinds: ``NotSupportedError`` (NotSupportedException),
 ``ShapeError`` (ArgumentException), ``ArgumentOutOfRangeError``, ``BackendError`` (device
@@ -24,7 +26,8 @@ from ._lib import (ArgumentOutOfRangeError, BackendError, NotSupportedError, Sha
                    library_path, load)
 from .backend import (Context, FastMath, GgmlType, HostBuffer, LayerDesc, QActs, Quants, Stage, Transformer,
                       WeightView, layout)
+from .model import DeviceTransformer, ModelConfig
 
 __all__ = ["ArgumentOutOfRangeError", "BackendError", "NotSupportedError", "ShapeError",
            "library_path", "load", "Context", "FastMath", "GgmlType", "HostBuffer", "LayerDesc", "QActs", "Quants", "Stage",
-           "Transformer", "WeightView", "layout"]
+           "Transformer", "WeightView", "layout", "DeviceTransformer", "ModelConfig"]

@@ -47,6 +47,7 @@ SIGNATURES = {
     "wl_quantize": (ctypes.c_int, [P, P, I32, I32, I32, P, P, P]),
     "wl_quantize_dev": (ctypes.c_int, [P, P, I32, I32, I32, P, P, P]),
     "wl_matmul_dev": (ctypes.c_int, [P, P, I32, P, I32, P]),
+    "wl_matmul_add_dev": (ctypes.c_int, [P, P, I32, P, I32, P, ctypes.c_float]),
     "wl_matmul_multi_dev": (ctypes.c_int, [P, I32, P, P, I32, P]),
     "wl_gate_up_dev": (ctypes.c_int, [P, P, P, I32, P, I32, P]),
     "wl_dequant_dev": (ctypes.c_int, [P, P, I64, I64, P]),

@@ -105,6 +105,7 @@ class Context:
         h = ctypes.c_void_p()
         check(self._lib.wl_create(device, ctypes.byref(h)))
         self.handle = h
+        self.device = device
 
     def close(self):
         if self.handle:

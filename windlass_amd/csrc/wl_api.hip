@@ -45,8 +45,9 @@ struct wl_stage {
 
 // S_PART holds the K-chunk partials of split GEMV rows, S_XB the bf16 copy of x for the GEMM,
 // S_QA the 8-bit activations of the integer path.
-// S_L* are wl_layer_dev's activations.
-enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB, S_QA, S_ROPE, S_ATT,
+// S_L* are wl_layer_dev's activations (S_LO: wl_matmul_add_dev's product when the add is not
+// the GEMV's own store).
+enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB, S_QA, S_ATT,
        S_LXN, S_LQ, S_LK, S_LV, S_LATT, S_LO, S_LG, S_LU, S_COUNT };
 
 struct wl_ctx {
@@ -492,6 +493,31 @@ extern "C" int wl_matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, cons
   return matmul_dev(c, w, expert, d_x, T, d_y);
 }
 
+// d_y += (W x) * rs. Up to 8 tokens on the GEMV kernels the add is their final store; otherwise
+// the product goes to scratch and the residual kernel adds it. Either way o = W x is rounded to
+// float first, then x + o * rs as two roundings (src/Transformer.cs:224,231).
+extern "C" int wl_matmul_add_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float *d_x, int32_t T,
+                                 float *d_y, float rs) {
+  if (!c || !w || !d_x || !d_y) return fail(WL_E_ARG, "wl_matmul_add_dev: null argument");
+  int rc = check_expert(w, expert);
+  if (rc) return rc;
+  if (T <= 0) return fail(WL_E_SHAPE, "MatMul shape mismatch: T = %d", T);
+  const uint8_t *base;
+  int64_t rows;
+  operand(w, expert, &base, &rows);
+  if (T <= 8 && wl::gemv_supports(w->type) && !int_path(c, w)) {
+    wl::GemvMat m{base, nullptr, w->row_bytes, (int)rows, w->type, d_y, (int)rows};
+    m.add = 1;
+    m.rs = rs;
+    return gemv(c, &m, 1, 1, d_x, (int)w->cols, T);
+  }
+  if ((rc = ensure(c, S_LO, (size_t)T * rows * sizeof(float)))) return rc;
+  float *o = (float *)c->buf[S_LO];
+  if ((rc = matmul_dev(c, w, expert, d_x, T, o))) return rc;
+  WL_HIP(wl::residual_launch(d_y, o, (int64_t)T * rows, rs, c->stream), "residual");
+  return WL_OK;
+}
+
 extern "C" int wl_matmul(wl_ctx *c, const wl_weight *w, int32_t expert, const float *x, int32_t T, float *y) {
   if (!c || !w || !x || !y) return fail(WL_E_ARG, "wl_matmul: null argument");
   int rc = check_expert(w, expert);
@@ -804,10 +830,8 @@ extern "C" int wl_rope_dev(wl_ctx *c, float *d_x, int32_t T, int32_t heads, int3
   if (!c || !d_x) return fail(WL_E_ARG, "wl_rope_dev: null argument");
   if (T < 0 || heads <= 0 || head_dim <= 0 || rope_dims <= 0 || rope_dims > head_dim || rope_dims % 2)
     return fail(WL_E_SHAPE, "wl_rope_dev: %d rotated of %d per head", rope_dims, head_dim);
-  int rc = ensure(c, S_ROPE, (size_t)T * rope_dims * sizeof(float));
-  if (rc) return rc;
   WL_HIP(wl::rope_launch(d_x, (int64_t)heads * head_dim, T, heads, head_dim, rope_dims, neox, d_pos, pos0, base,
-                         freq_scale, d_freqs, (float *)c->buf[S_ROPE], c->stream),
+                         freq_scale, d_freqs, c->stream),
          "rope");
   return WL_OK;
 }
@@ -827,7 +851,9 @@ extern "C" int wl_attention_dev(wl_ctx *c, const float *d_q, int32_t T, int32_t 
   if (!c || !d_q || !d_K || !d_V || !d_out) return fail(WL_E_ARG, "wl_attention_dev: null argument");
   if (T < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || head_dim <= 0 || pos0 < 0)
     return fail(WL_E_SHAPE, "wl_attention_dev: %d heads over %d KV heads", heads, kv_heads);
-  int rc = ensure(c, S_ATT, (size_t)T * heads * (pos0 + T) * sizeof(float));
+  const int kv_dim = kv_heads * head_dim;
+  int rc = ensure(c, S_ATT,
+                  (size_t)wl::attention_scratch_floats(T, heads, head_dim, kv_dim, pos0, d_K, d_V) * sizeof(float));
   if (rc) return rc;
   const int64_t qd = (int64_t)heads * head_dim;
   WL_HIP(wl::attention_launch(d_q, qd, T, d_K, d_V, kv_heads * head_dim, heads, kv_heads, head_dim, pos0, scale,
@@ -880,11 +906,11 @@ extern "C" int wl_layer_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32
   int rc;
   if ((rc = ensure(c, S_LXN, (size_t)T * E * 4)) || (rc = ensure(c, S_LQ, (size_t)T * QD * 4)) ||
       (rc = ensure(c, S_LK, (size_t)T * KD * 4)) || (rc = ensure(c, S_LV, (size_t)T * KD * 4)) ||
-      (rc = ensure(c, S_LATT, (size_t)T * QD * 4)) || (rc = ensure(c, S_LO, (size_t)T * E * 4)) ||
+      (rc = ensure(c, S_LATT, (size_t)T * QD * 4)) ||
       (rc = ensure(c, S_LG, (size_t)T * FF * 4)) || (rc = ensure(c, S_LU, (size_t)T * FF * 4)))
     return rc;
   float *xn = (float *)c->buf[S_LXN], *q = (float *)c->buf[S_LQ], *k = (float *)c->buf[S_LK],
-        *v = (float *)c->buf[S_LV], *att = (float *)c->buf[S_LATT], *o = (float *)c->buf[S_LO],
+        *v = (float *)c->buf[S_LV], *att = (float *)c->buf[S_LATT],
         *g = (float *)c->buf[S_LG], *u = (float *)c->buf[S_LU];
   const float rs = L->residual_scale != 0.f ? L->residual_scale : 1.f;
   // attention block
@@ -904,23 +930,25 @@ extern "C" int wl_layer_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32
   if (L->d_k_norm && (rc = wl_rms_norm_dev(c, k, (int64_t)T * KH, HD, L->d_k_norm, L->eps, k))) return rc;
   const int rd = L->rope_dims > 0 ? L->rope_dims : HD;
   const double fs = L->rope_freq_scale != 0.0 ? L->rope_freq_scale : 1.0;
-  if ((rc = wl_rope_dev(c, q, T, H, HD, rd, L->neox, pos0, nullptr, L->rope_base, fs, L->d_rope_freqs)) ||
-      (rc = wl_rope_dev(c, k, T, KH, HD, rd, L->neox, pos0, nullptr, L->rope_base, fs, L->d_rope_freqs)) ||
-      (rc = wl_kv_store_dev(c, k, v, T, KD, d_K, d_V, pos0)))
-    return rc;
+  if (rd <= 0 || rd > HD || rd % 2) return fail(WL_E_SHAPE, "wl_layer_dev: %d rotated of %d per head", rd, HD);
+  WL_HIP(wl::rope_kv_launch(q, k, v, T, H, KH, HD, rd, L->neox, pos0, L->rope_base, fs, L->d_rope_freqs, d_K, d_V,
+                            c->stream),
+         "rope and kv store");
   const float scale = L->attention_scale != 0.f ? L->attention_scale : 1.0f / (float)sqrt((double)HD);
   if ((rc = wl_attention_dev(c, q, T, H, KH, HD, d_K, d_V, pos0, scale, att))) return rc;
-  if ((rc = matmul_dev(c, L->attn_output, -1, att, T, o)) || (rc = wl_residual_dev(c, d_x, o, (int64_t)T * E, rs)))
-    return rc;
+  if ((rc = wl_matmul_add_dev(c, L->attn_output, -1, att, T, d_x, rs))) return rc;
   // feed-forward block
   if ((rc = wl_rms_norm_dev(c, d_x, T, E, L->d_ffn_norm, L->eps, xn))) return rc;
-  if (L->ffn_gate->type == L->ffn_up->type) {
+  // up to 8 tokens: gate and up in one GEMV launch with the SiLU epilogue; a prompt: the two
+  // GEMMs, then the SiLU pass
+  const bool fused = L->ffn_gate->type == L->ffn_up->type &&
+                     (T <= 8 || int_path(c, L->ffn_gate) || !wl::gemm_supports(L->ffn_gate->type));
+  if (fused) {
     if ((rc = wl_gate_up_dev(c, L->ffn_gate, L->ffn_up, -1, xn, T, g))) return rc;
   } else {
     if ((rc = matmul_dev(c, L->ffn_gate, -1, xn, T, g)) || (rc = matmul_dev(c, L->ffn_up, -1, xn, T, u))) return rc;
     WL_HIP(wl::silu_mul_launch(g, u, (int64_t)T * FF, c->stream), "silu");
   }
-  if ((rc = matmul_dev(c, L->ffn_down, -1, g, T, o)) || (rc = wl_residual_dev(c, d_x, o, (int64_t)T * E, rs)))
-    return rc;
+  if ((rc = wl_matmul_add_dev(c, L->ffn_down, -1, g, T, d_x, rs))) return rc;
   return WL_OK;
 }

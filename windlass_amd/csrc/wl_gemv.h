@@ -7,7 +7,8 @@ namespace wl {
 constexpr int GEMV_MAX_MATS = 4;   // matrices that share x in one launch (q, k, v)
 constexpr int GEMV_MAX_SEGS = 16;  // (matrix, K-chunk) segments of one launch
 
-// One matrix of a launch: y[t * ldy + r] = W[r] . x[t] (nm = 2: silu(W x) * (W2 x)).
+// One matrix of a launch: y[t * ldy + r] = W[r] . x[t] (nm = 2: silu(W x) * (W2 x)); with add,
+// y[t * ldy + r] += (W[r] . x[t]) * rs instead (the residual add, rounded as two operations).
 struct GemvMat {
   const uint8_t *w;
   const uint8_t *w2;
@@ -16,6 +17,8 @@ struct GemvMat {
   int type;
   float *y;
   int ldy;
+  int add = 0;
+  float rs = 1.f;
 };
 
 // One segment: a K-chunk [col0, col0 + cols) of one matrix, written to out (the result, or a
@@ -31,6 +34,8 @@ struct GemvSeg {
   int type;
   int wg_begin;
   int nwg;
+  int add;  // out += result * rs (unsplit segments only)
+  float rs;
 };
 
 struct GemvParams {

@@ -41,6 +41,8 @@ struct CombineParams {
   float *y[GEMV_MAX_MATS];
   int ldy[GEMV_MAX_MATS];
   int rows[GEMV_MAX_MATS];
+  int add[GEMV_MAX_MATS];  // y += result * rs
+  float rs[GEMV_MAX_MATS];
   int S, NM, T;
 };
 
@@ -68,7 +70,8 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams cp) {
     }
   }
   if (cp.NM == 2) g = silu_mul(g, u);
-  cp.y[m][(int64_t)t * cp.ldy[m] + r] = g;
+  float *y = cp.y[m] + (int64_t)t * cp.ldy[m] + r;
+  *y = cp.add[m] ? add_scaled(*y, g, cp.rs[m]) : g;
 }
 
 int gemv_chunks(int nmat, int cols) {
@@ -213,7 +216,7 @@ static hipError_t gemv_batch_run(const GemvMat *mats, int nmat, int nm, const fl
   float *part = scratch;
   for (int i = 0; i < nmat; i++) {
     const GemvMat &m = mats[i];
-    a.m[i] = BatchMat{m.w, m.w2, m.row_bytes, part, m.y, m.ldy, m.rows, m.type, 0};
+    a.m[i] = BatchMat{m.w, m.w2, m.row_bytes, part, m.y, m.ldy, m.rows, m.type, 0, m.add, m.rs};
     part += (int64_t)a.u * nm * T * m.rows;
     same = same && m.type == mats[0].type;
   }
@@ -273,6 +276,8 @@ hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int l
       s.rows = m.rows;
       s.col0 = c * p.cols;
       s.type = m.type;
+      s.add = m.add;
+      s.rs = m.rs;
       if (S == 1) {
         s.out = m.y;
         s.ldo = m.ldy;
@@ -286,6 +291,8 @@ hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int l
       cp.y[i] = m.y;
       cp.ldy[i] = m.ldy;
       cp.rows[i] = m.rows;
+      cp.add[i] = m.add;
+      cp.rs[i] = m.rs;
       part += (int64_t)S * nm * T * m.rows;
     }
     maxrows = m.rows > maxrows ? m.rows : maxrows;

@@ -44,6 +44,13 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + (float)exp((double)(-g))) * u;
 }
 
+// The residual add x += o * rs (src/Transformer.cs:224,231) on a product's result: a product
+// and a sum, never fused into one rounding.
+__device__ __forceinline__ float add_scaled(float x, float v, float rs) {
+#pragma clang fp contract(off)
+  return x + v * rs;
+}
+
 // The partner exchanges of the folding tree. Bits 5 and 4 pair lane l with l^32 and l^16
 // through the permlane swaps, which deliver both partners' values in one instruction; bits 3..0
 // use DPP: l^8 (row_ror:8), l^7 within each eight lanes (row_half_mirror), l^2 and l^1
@@ -113,6 +120,8 @@ struct CsIO {
   int64_t ldy;
   int T;
   float *y2;
+  int add;  // y += result * rs
+  float rs;
 };
 
 // Row groups whose wave results are buffered in LDS between two barriers.
@@ -190,7 +199,7 @@ __device__ __forceinline__ void cs_finish(const float (&acc)[NM][R][TM], int g, 
             s = silu_mul(s, s1);
           }
         }
-        io.y[o] = s;
+        io.y[o] = io.add ? add_scaled(io.y[o], s, io.rs) : s;
       }
     }
   }

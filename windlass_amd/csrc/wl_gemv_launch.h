@@ -26,7 +26,7 @@ template <class C, int TM, int R, int NM, int SP>
 __device__ __forceinline__ void run_seg(const GemvParams &p, const GemvSeg &s, int split) {
   const CsRows W{s.w, s.w2, s.row_bytes, s.rows};
   float *y2 = (NM == 2 && split) ? s.out + (int64_t)p.T * s.ldo : nullptr;
-  const CsIO io{p.x + s.col0, nullptr, p.ldx, s.out, nullptr, s.ldo, p.T, y2};
+  const CsIO io{p.x + s.col0, nullptr, p.ldx, s.out, nullptr, s.ldo, p.T, y2, split ? 0 : s.add, s.rs};
   cs_gemv<C, TM, R, NM, SP>(W, io, p.cols, (int)blockIdx.x - s.wg_begin, s.nwg, wl_dyn_lds);
 }
 
@@ -107,6 +107,8 @@ struct BatchMat {
   float *y;
   int ldy, rows, type;
   int wg_begin;  // first blockIdx.x of this matrix
+  int add;       // y += result * rs
+  float rs;
 };
 
 struct BatchArgs {
@@ -274,7 +276,8 @@ static __global__ __launch_bounds__(256) void batch_combine_kernel(BatchArgs a) 
   const int t = (int)(i / M.rows), r = (int)(i % M.rows);
   float s = batch_sum(M.part + i * a.u, a.S, a.W);
   if constexpr (NM == 2) s = silu_mul(s, batch_sum(M.part + ((int64_t)a.T * M.rows + i) * a.u, a.S, a.W));
-  M.y[(int64_t)t * M.ldy + r] = s;
+  float *y = M.y + (int64_t)t * M.ldy + r;
+  *y = M.add ? add_scaled(*y, s, M.rs) : s;
 }
 
 // Workgroups per matrix along x: about WL_BATCH_WPC waves per CU over all columns, split over

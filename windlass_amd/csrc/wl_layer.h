@@ -7,13 +7,20 @@ namespace wl {
 
 hipError_t rms_norm_launch(const float *x, int64_t rows, int64_t dim, const float *w, float eps, float *y,
                            hipStream_t st);
-// cs: T * n floats of scratch for the cos/sin table
+// RoPE on T rows of `heads` heads (row t at pos[t], or pos0 + t when pos is null).
 hipError_t rope_launch(float *x, int64_t ldx, int T, int heads, int hd, int n, int neox, const int *pos, int pos0,
-                       double base, double freq_scale, const float *freqs, float *cs, hipStream_t st);
+                       double base, double freq_scale, const float *freqs, hipStream_t st);
+// A layer's RoPE on q [T][H*hd] and k [T][KH*hd] and the fp16 stores of k and v into cache rows
+// pos0.. of Kc / Vc [positions][KH*hd], in one launch.
+hipError_t rope_kv_launch(float *q, float *k, const float *v, int T, int H, int KH, int hd, int n, int neox,
+                          int pos0, double base, double freq_scale, const float *freqs, uint16_t *Kc, uint16_t *Vc,
+                          hipStream_t st);
 hipError_t kv_store_launch(const float *k, const float *v, int64_t n, uint16_t *K, uint16_t *V, hipStream_t st);
-// scores: T * heads * (pos0 + T) floats of scratch
+// Floats of scratch attention_launch needs for these operands.
+int64_t attention_scratch_floats(int T, int heads, int hd, int kv_dim, int pos0, const uint16_t *K,
+                                 const uint16_t *V);
 hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *K, const uint16_t *V, int kv_dim,
-                            int heads, int kv_heads, int hd, int pos0, float scale, float *scores, float *out,
+                            int heads, int kv_heads, int hd, int pos0, float scale, float *scratch, float *out,
                             int64_t ldo, hipStream_t st);
 hipError_t residual_launch(float *x, const float *o, int64_t n, float rs, hipStream_t st);
 hipError_t argmax_launch(const float *logits, int rows, int64_t n, int *out, hipStream_t st);

@@ -19,7 +19,8 @@
 
 namespace wl {
 
-// Block-wide sum of doubles over 256 threads (all threads get the result).
+// Block-wide sum of doubles (blockDim.x a multiple of 64, at most 1024; all threads get the
+// result; sh holds 16 doubles).
 __device__ double block_sum_d(double v, double *sh) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
@@ -44,52 +45,102 @@ __device__ float block_max_f(float v, float *sh) {
   return s;
 }
 
-// RmsNormRows (src/Transformer.cs:446-457): one workgroup per row.
-__global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, int64_t dim, const float *__restrict__ w,
-                                                       float eps, float *y) {  // x == y allowed
-  __shared__ double sh[4];
+// RmsNormRows (src/Transformer.cs:446-457): one workgroup per row. Each thread squares and adds
+// its values in double (float4 loads when the row allows), then a tree over the workgroup.
+// Enough threads that a thread holds a few loads at most: the row's latency is one or two
+// memory round trips, not a chain of them.
+__global__ __launch_bounds__(1024) void rms_norm_kernel(const float *x, int64_t dim, const float *__restrict__ w,
+                                                        float eps, float *y) {  // x == y allowed
+  __shared__ double sh[16];
   const float *xr = x + (int64_t)blockIdx.x * dim;
   float *yr = y + (int64_t)blockIdx.x * dim;
+  const bool vec = (dim & 3) == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0 &&
+                   ((uintptr_t)w & 15) == 0;
   double s = 0.0;
-  for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) s += (double)xr[i] * (double)xr[i];
-  s = block_sum_d(s, sh);
+  if (vec) {
+    for (int64_t i = (int64_t)threadIdx.x * 4; i < dim; i += (int64_t)blockDim.x * 4) {
+      const float4 v = *reinterpret_cast<const float4 *>(xr + i);
+      s += (double)v.x * (double)v.x;
+      s += (double)v.y * (double)v.y;
+      s += (double)v.z * (double)v.z;
+      s += (double)v.w * (double)v.w;
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) s += (double)xr[i] * (double)xr[i];
+  }
+  s = block_sum_d(s, sh);  // every read of x precedes the writes below (in place)
   const float mean = (float)(s / (double)dim);
   const float scale = 1.0f / (float)sqrt((double)(mean + eps));
-  for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) yr[i] = xr[i] * scale * w[i];
-}
-
-// RopeTable (src/Transformer.cs:396-414): cos/sin per rotated pair at each row's position,
-// the angle a running product in double as there, divided by the pair's frequency factor when
-// the model has them (rope_freqs.weight). One thread per row.
-__global__ void rope_table_kernel(const int *__restrict__ pos, int pos0, int T, int n, double theta_scale,
-                                  double freq_scale, const float *__restrict__ freqs, float *__restrict__ cs) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= T) return;
-  double theta = (double)(pos ? pos[t] : pos0 + t) * freq_scale;
-  float *c = cs + (int64_t)t * n;
-  for (int i = 0; i < n / 2; i++) {
-    const double a = freqs ? theta / (double)freqs[i] : theta;
-    c[2 * i] = (float)cos(a);
-    c[2 * i + 1] = (float)sin(a);
-    theta *= theta_scale;
+  if (vec) {
+    for (int64_t i = (int64_t)threadIdx.x * 4; i < dim; i += (int64_t)blockDim.x * 4) {
+      const float4 v = *reinterpret_cast<const float4 *>(xr + i), g = *reinterpret_cast<const float4 *>(w + i);
+      *reinterpret_cast<float4 *>(yr + i) =
+          make_float4(v.x * scale * g.x, v.y * scale * g.y, v.z * scale * g.z, v.w * scale * g.w);
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) yr[i] = xr[i] * scale * w[i];
   }
 }
 
-// Rope (src/Transformer.cs:416-431) on row t's `heads` heads: pairs (2i, 2i+1), or (i, i+half)
-// for the NeoX layout.
-__global__ void rope_kernel(float *__restrict__ x, int64_t ldx, int heads, int hd, int n, int neox,
-                            const float *__restrict__ cs) {
-  const int t = blockIdx.y;
-  const int half = n / 2;
-  const int k = blockIdx.x * blockDim.x + threadIdx.x;  // (head, pair)
-  if (k >= heads * half) return;
-  const int h = k / half, i = k % half;
-  float *o = x + (int64_t)t * ldx + (int64_t)h * hd;
-  const float c = cs[(int64_t)t * n + 2 * i], s = cs[(int64_t)t * n + 2 * i + 1];
-  const int a = neox ? i : 2 * i, b = neox ? i + half : 2 * i + 1;
+// The angle of rotated pair i at a position: RopeTable's running product in double
+// (src/Transformer.cs:396-414) repeated up to pair i, so every thread gets the bits the
+// sequential table has, divided by the pair's frequency factor when the model has them
+// (rope_freqs.weight).
+__device__ __forceinline__ void rope_cs(int p, int i, double theta_scale, double freq_scale,
+                                        const float *__restrict__ freqs, float &c, float &s) {
+  double theta = (double)p * freq_scale;
+  for (int k = 0; k < i; k++) theta *= theta_scale;
+  const double a = freqs ? theta / (double)freqs[i] : theta;
+  c = (float)cos(a);
+  s = (float)sin(a);
+}
+
+// Rope (src/Transformer.cs:416-431) on pair i of one head: (2i, 2i+1), or (i, i + n/2) NeoX.
+__device__ __forceinline__ void rope_pair(float *o, int i, int n, int neox, float c, float s, float &y0,
+                                          float &y1, int &a, int &b) {
+  a = neox ? i : 2 * i;
+  b = neox ? i + n / 2 : 2 * i + 1;
   const float x0 = o[a], x1 = o[b];
-  o[a] = x0 * c - x1 * s;
-  o[b] = x0 * s + x1 * c;
+  y0 = x0 * c - x1 * s;
+  y1 = x0 * s + x1 * c;
+  o[a] = y0;
+  o[b] = y1;
+}
+
+// RoPE on q (H heads) and k (KH heads) of row t, and ToHalf of the row's keys and values into
+// cache row pos0 + t (src/Transformer.cs:204-215,342-348). Work items of a row: one per rotated
+// pair of every q and k head, then one per key/value column (the value's store, and the key's
+// for columns past rope_dims). k, v and the caches are null for RoPE on one tensor.
+__global__ __launch_bounds__(256) void rope_qkv_kernel(float *__restrict__ q, int64_t ldq, int H, float *__restrict__ k,
+                                                       const float *__restrict__ v, int KH, int hd, int n, int neox,
+                                                       const int *__restrict__ pos, int pos0, double theta_scale,
+                                                       double freq_scale, const float *__restrict__ freqs,
+                                                       uint16_t *__restrict__ Kc, uint16_t *__restrict__ Vc) {
+  const int t = blockIdx.y, half = n / 2, KD = KH * hd;
+  const int it = blockIdx.x * blockDim.x + threadIdx.x;
+  const int npairs = (H + KH) * half;
+  const int p = pos ? pos[t] : pos0 + t;
+  const int64_t crow = (int64_t)(pos0 + t) * KD;
+  if (it < npairs) {
+    const int head = it / half, i = it % half;
+    float c, s, y0, y1;
+    int a, b;
+    rope_cs(p, i, theta_scale, freq_scale, freqs, c, s);
+    if (head < H) {
+      rope_pair(q + (int64_t)t * ldq + (int64_t)head * hd, i, n, neox, c, s, y0, y1, a, b);
+    } else {
+      const int kh = head - H;
+      rope_pair(k + (int64_t)t * KD + (int64_t)kh * hd, i, n, neox, c, s, y0, y1, a, b);
+      if (Kc) {
+        Kc[crow + kh * hd + a] = to_half(y0);
+        Kc[crow + kh * hd + b] = to_half(y1);
+      }
+    }
+  } else if (it < npairs + KD && Vc) {
+    const int j = it - npairs;
+    Vc[crow + j] = to_half(v[(int64_t)t * KD + j]);
+    if (j % hd >= n) Kc[crow + j] = to_half(k[(int64_t)t * KD + j]);
+  }
 }
 
 // ToHalf (src/Transformer.cs:342-348) of one token's keys and values.
@@ -151,6 +202,138 @@ __global__ __launch_bounds__(256) void attention_kernel(const float *__restrict_
       o += p * h2f(V[(int64_t)j * kv_dim + (int64_t)kvh * hd + d]);
     }
     op[d] = o;
+  }
+}
+
+// Attention for head dims that are a multiple of 8 (src/Transformer.cs:351-393): one workgroup
+// of 256 threads per (query head, chunk of kAttP positions, row). Thread j holds the key of
+// position j0 + j in registers (uint4 loads) and forms its score with the reference's four
+// partial sums; the chunk's values are staged in LDS meanwhile. When a row's positions fit one
+// chunk the workgroup finishes it with the reference's arithmetic (maximum, exp in double,
+// the double sum, p = e * inv, each output value adding its positions in order). A longer row
+// leaves per-chunk partials (unnormalised sums, chunk maximum, double sum) that
+// attention_combine_kernel rescales and adds in chunk order.
+constexpr int kAttP = 256;
+
+__device__ __forceinline__ float half_lo16(uint32_t w) { return h2f((uint16_t)(w & 0xffffu)); }
+__device__ __forceinline__ float half_hi16(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
+
+template <int HD>
+__global__ __launch_bounds__(256) void attention_chunk_kernel(const float *__restrict__ q, int64_t ldq,
+                                                              const uint16_t *__restrict__ K,
+                                                              const uint16_t *__restrict__ V, int kv_dim, int heads,
+                                                              int kv_heads, int pos0, float scale,
+                                                              float *__restrict__ part, int max_chunks,
+                                                              float *__restrict__ out, int64_t ldo) {
+  constexpr int U = HD / 8;  // uint4 per key row
+  __shared__ uint4 vs4[kAttP * U];
+  __shared__ float qs[HD];
+  __shared__ float es[kAttP];
+  __shared__ float shf[4];
+  __shared__ double shd[16];
+  const int h = blockIdx.x, c = blockIdx.y, t = blockIdx.z;
+  const int kvh = h / (heads / kv_heads);
+  const int n = pos0 + t + 1, j0 = c * kAttP;
+  if (j0 >= n) return;  // uniform over the workgroup
+  const int cnt = n - j0 < kAttP ? n - j0 : kAttP;
+  const int nch = (n + kAttP - 1) / kAttP;
+  const int tid = threadIdx.x;
+  uint4 kr[U], vr[U];  // zeroed first: partly written arrays are otherwise kept in scratch
+#pragma unroll
+  for (int u = 0; u < U; u++) kr[u] = vr[u] = make_uint4(0, 0, 0, 0);
+  if (tid < cnt) {
+    const uint4 *kp = reinterpret_cast<const uint4 *>(K + (int64_t)(j0 + tid) * kv_dim + (int64_t)kvh * HD);
+#pragma unroll
+    for (int u = 0; u < U; u++) kr[u] = kp[u];
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++) {  // the chunk's values: element e of [cnt][U] uint4
+    const int e = u * 256 + tid, row = e / U, col = e % U;
+    if (row < cnt) vr[u] = reinterpret_cast<const uint4 *>(V + (int64_t)(j0 + row) * kv_dim + (int64_t)kvh * HD)[col];
+  }
+  const float *qp = q + (int64_t)t * ldq + (int64_t)h * HD;
+  for (int i = tid; i < HD; i += 256) qs[i] = qp[i];
+  __syncthreads();
+  float d = -INFINITY;
+  if (tid < cnt) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const uint4 w = kr[u];
+      const float *qq = qs + 8 * u;
+      s0 += qq[0] * half_lo16(w.x);
+      s1 += qq[1] * half_hi16(w.x);
+      s2 += qq[2] * half_lo16(w.y);
+      s3 += qq[3] * half_hi16(w.y);
+      s0 += qq[4] * half_lo16(w.z);
+      s1 += qq[5] * half_hi16(w.z);
+      s2 += qq[6] * half_lo16(w.w);
+      s3 += qq[7] * half_hi16(w.w);
+    }
+    d = ((s0 + s1) + (s2 + s3)) * scale;
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const int e = u * 256 + tid;
+    if (e / U < cnt) vs4[e] = vr[u];
+  }
+  const float mx = block_max_f(d, shf);
+  float e = 0.f;
+  double sum = 0.0;
+  if (tid < cnt) {
+    e = (float)exp((double)(d - mx));
+    sum = (double)e;
+  }
+  es[tid] = e;
+  sum = block_sum_d(sum, shd);  // also orders the writes of es and vs4 before the reads below
+  const uint16_t *vs = reinterpret_cast<const uint16_t *>(vs4);
+  if (nch == 1) {
+    const float inv = (float)(1.0 / sum);
+    for (int dd = tid; dd < HD; dd += 256) {
+      float o = 0.f;
+      for (int j = 0; j < cnt; j++) {
+        const float p = es[j] * inv;
+        o += p * h2f(vs[j * HD + dd]);
+      }
+      out[(int64_t)t * ldo + (int64_t)h * HD + dd] = o;
+    }
+    return;
+  }
+  // record: HD unnormalised sums, the chunk maximum, a pad, the double sum
+  float *rec = part + (((int64_t)t * heads + h) * max_chunks + c) * (HD + 4);
+  for (int dd = tid; dd < HD; dd += 256) {
+    float o = 0.f;
+    for (int j = 0; j < cnt; j++) o += es[j] * h2f(vs[j * HD + dd]);
+    rec[dd] = o;
+  }
+  if (tid == 0) {
+    rec[HD] = mx;
+    *reinterpret_cast<double *>(rec + HD + 2) = sum;
+  }
+}
+
+// Rows longer than one chunk: m = the largest chunk maximum, each chunk weighted by
+// exp(m_c - m) (double), the weighted sums over the weighted denominators, chunks in order.
+template <int HD>
+__global__ __launch_bounds__(256) void attention_combine_kernel(const float *__restrict__ part, int max_chunks,
+                                                                int heads, int pos0, float *__restrict__ out,
+                                                                int64_t ldo) {
+  const int h = blockIdx.x, t = blockIdx.y;
+  const int n = pos0 + t + 1, nch = (n + kAttP - 1) / kAttP;
+  if (nch == 1) return;
+  const float *rec = part + ((int64_t)t * heads + h) * max_chunks * (HD + 4);
+  float m = -INFINITY;
+  for (int c = 0; c < nch; c++) m = fmaxf(m, rec[c * (HD + 4) + HD]);
+  double L = 0.0;
+  for (int c = 0; c < nch; c++)
+    L += *reinterpret_cast<const double *>(rec + c * (HD + 4) + HD + 2) * exp((double)(rec[c * (HD + 4) + HD] - m));
+  for (int dd = threadIdx.x; dd < HD; dd += blockDim.x) {
+    float o = 0.f;
+    for (int c = 0; c < nch; c++) {
+      const float wgt = (float)(exp((double)(rec[c * (HD + 4) + HD] - m)) / L);
+      o += rec[c * (HD + 4) + dd] * wgt;
+    }
+    out[(int64_t)t * ldo + (int64_t)h * HD + dd] = o;
   }
 }
 
@@ -227,19 +410,28 @@ hipError_t silu_mul_launch(float *g, const float *u, int64_t n, hipStream_t st) 
 hipError_t rms_norm_launch(const float *x, int64_t rows, int64_t dim, const float *w, float eps, float *y,
                            hipStream_t st) {
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, dim, w, eps, y);
+  int nt = (int)((dim / 4 + 63) / 64 * 64);  // a float4 per thread, 64..1024 threads
+  nt = nt < 64 ? 64 : nt > 1024 ? 1024 : nt;
+  hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)rows), dim3(nt), 0, st, x, dim, w, eps, y);
   return hipGetLastError();
 }
 
 hipError_t rope_launch(float *x, int64_t ldx, int T, int heads, int hd, int n, int neox, const int *pos, int pos0,
-                       double base, double freq_scale, const float *freqs, float *cs, hipStream_t st) {
+                       double base, double freq_scale, const float *freqs, hipStream_t st) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rope_table_kernel, dim3(blocks_of(T, 64)), dim3(64), 0, st, pos, pos0, T, n,
-                     pow(base, -2.0 / n), freq_scale, freqs, cs);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(rope_kernel, dim3(blocks_of((int64_t)heads * (n / 2), 256), T), dim3(256), 0, st, x, ldx, heads,
-                     hd, n, neox, cs);
+  const int64_t items = (int64_t)heads * (n / 2);
+  hipLaunchKernelGGL(rope_qkv_kernel, dim3(blocks_of(items, 256), T), dim3(256), 0, st, x, ldx, heads, nullptr,
+                     nullptr, 0, hd, n, neox, pos, pos0, pow(base, -2.0 / n), freq_scale, freqs, nullptr, nullptr);
+  return hipGetLastError();
+}
+
+hipError_t rope_kv_launch(float *q, float *k, const float *v, int T, int H, int KH, int hd, int n, int neox,
+                          int pos0, double base, double freq_scale, const float *freqs, uint16_t *Kc, uint16_t *Vc,
+                          hipStream_t st) {
+  if (T <= 0) return hipSuccess;
+  const int64_t items = (int64_t)(H + KH) * (n / 2) + (int64_t)KH * hd;
+  hipLaunchKernelGGL(rope_qkv_kernel, dim3(blocks_of(items, 256), T), dim3(256), 0, st, q, (int64_t)H * hd, H, k, v,
+                     KH, hd, n, neox, nullptr, pos0, pow(base, -2.0 / n), freq_scale, freqs, Kc, Vc);
   return hipGetLastError();
 }
 
@@ -249,12 +441,46 @@ hipError_t kv_store_launch(const float *k, const float *v, int64_t n, uint16_t *
   return hipGetLastError();
 }
 
+// The chunked kernel takes head dims of 64 and 128 with 16-byte aligned cache rows; other
+// shapes take attention_kernel.
+static bool attention_chunked(int hd, int kv_dim, const uint16_t *K, const uint16_t *V) {
+  return (hd == 64 || hd == 128) && kv_dim % 8 == 0 && ((uintptr_t)K & 15) == 0 && ((uintptr_t)V & 15) == 0;
+}
+
+int64_t attention_scratch_floats(int T, int heads, int hd, int kv_dim, int pos0, const uint16_t *K,
+                                 const uint16_t *V) {
+  if (T <= 0) return 0;
+  if (!attention_chunked(hd, kv_dim, K, V)) return (int64_t)T * heads * (pos0 + T);
+  const int chunks = (pos0 + T + kAttP - 1) / kAttP;
+  return chunks > 1 ? (int64_t)T * heads * chunks * (hd + 4) : 0;
+}
+
+template <int HD>
+static hipError_t attention_chunked_launch(const float *q, int64_t ldq, int T, const uint16_t *K, const uint16_t *V,
+                                           int kv_dim, int heads, int kv_heads, int pos0, float scale, float *part,
+                                           float *out, int64_t ldo, hipStream_t st) {
+  const int chunks = (pos0 + T + kAttP - 1) / kAttP;
+  hipLaunchKernelGGL(attention_chunk_kernel<HD>, dim3(heads, chunks, T), dim3(256), 0, st, q, ldq, K, V, kv_dim,
+                     heads, kv_heads, pos0, scale, part, chunks, out, ldo);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || chunks == 1) return e;
+  hipLaunchKernelGGL(attention_combine_kernel<HD>, dim3(heads, T), dim3(HD), 0, st, part, chunks, heads, pos0, out,
+                     ldo);
+  return hipGetLastError();
+}
+
 hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *K, const uint16_t *V, int kv_dim,
-                            int heads, int kv_heads, int hd, int pos0, float scale, float *scores, float *out,
+                            int heads, int kv_heads, int hd, int pos0, float scale, float *scratch, float *out,
                             int64_t ldo, hipStream_t st) {
   if (T <= 0) return hipSuccess;
+  if (attention_chunked(hd, kv_dim, K, V)) {
+    return hd == 64 ? attention_chunked_launch<64>(q, ldq, T, K, V, kv_dim, heads, kv_heads, pos0, scale, scratch,
+                                                   out, ldo, st)
+                    : attention_chunked_launch<128>(q, ldq, T, K, V, kv_dim, heads, kv_heads, pos0, scale, scratch,
+                                                    out, ldo, st);
+  }
   hipLaunchKernelGGL(attention_kernel, dim3(heads, T), dim3(256), 0, st, q, ldq, K, V, kv_dim, heads, kv_heads, hd,
-                     pos0, scale, scores, (int64_t)(pos0 + T), out, ldo);
+                     pos0, scale, scratch, (int64_t)(pos0 + T), out, ldo);
   return hipGetLastError();
 }
 

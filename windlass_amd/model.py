@@ -1,0 +1,151 @@
+"""Transformer.Forward with every tensor and activation resident in one GPU's HBM
+(src/Transformer.cs:83-110, Layer :177-232, Head :112-125) and Engine's greedy loop
+(src/Engine.cs:356-360).
+
+The weights are WeightViews (raw GGUF blocks in HBM, uploaded or views into a Stage), the norm
+and bias vectors device float32 tensors, the KV caches fp16 on the device. A decode step is
+wl_embed_dev, one wl_layer_dev per layer, the final RMSNorm, the output product and the device
+argmax; only the sampled token id crosses to the host. All of it is queued on the context's
+stream without a host wait until the token id is read.
+"""
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import ShapeError, check, load
+from .backend import LayerDesc
+
+_LAYER_TENSORS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+
+
+@dataclass
+class ModelConfig:
+    """The constants Forward and Layer read (src/ModelConfig.cs:13-14)."""
+    layers: int
+    embd: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    rope_dims: int = 0            # 0: head_dim
+    neox: bool = False            # RopeNeox: pairs (i, i + n/2) instead of (2i, 2i + 1)
+    rope_base: float = 10000.0
+    rope_freq_scale: float = 1.0
+    eps: float = 1e-5
+    attention_scale: float = 0.0  # 0: 1/sqrt(head_dim)
+    residual_scale: float = 0.0   # 0: 1
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+class DeviceTransformer:
+    """weights: {GGUF tensor name: WeightView} with token_embd, output (absent when tied to
+    token_embd) and blk.N.{attn_q,attn_k,attn_v,attn_output,ffn_gate,ffn_up,ffn_down};
+    vectors: {name: device float32 tensor} with output_norm, blk.N.attn_norm, blk.N.ffn_norm and
+    the optional blk.N.attn_{q,k,v}.bias, blk.N.attn_{q,k}_norm and rope_freqs."""
+
+    def __init__(self, ctx, cfg, weights, vectors, max_positions):
+        import torch
+        self.ctx, self.cfg, self.L, self.torch = ctx, cfg, load(), torch
+        self.w, self.v = weights, vectors
+        self.embd_w = weights["token_embd"]
+        self.head_w = weights.get("output", self.embd_w)
+        if self.embd_w.Cols != cfg.embd or self.head_w.Cols != cfg.embd:
+            raise ShapeError("token_embd/output have %d/%d columns; the model has %d"
+                             % (self.embd_w.Cols, self.head_w.Cols, cfg.embd))
+        self.vocab = self.head_w.Rows
+        self.max_positions = max_positions
+        self.dev = torch.device("cuda:%d" % ctx.device)
+        self.descs = [self._desc(l) for l in range(cfg.layers)]
+        kd = cfg.kv_heads * cfg.head_dim
+        self.K = torch.zeros((cfg.layers, max_positions, kd), dtype=torch.int16, device=self.dev)
+        self.V = torch.zeros((cfg.layers, max_positions, kd), dtype=torch.int16, device=self.dev)
+        self.logits = torch.empty((1, self.vocab), device=self.dev)
+        self._tok = torch.empty(1, dtype=torch.int32, device=self.dev)
+        self._xn = torch.empty((1, cfg.embd), device=self.dev)
+        self._x = {}
+        self.length = 0
+        torch.cuda.synchronize()  # the context's stream does not wait for torch's
+
+    def _desc(self, l):
+        c, p, v = self.cfg, "blk.%d." % l, self.v
+        d = LayerDesc()
+        for f in _LAYER_TENSORS:
+            setattr(d, f, self.w[p + f].handle.value)
+        d.d_attn_norm, d.d_ffn_norm = _ptr(v[p + "attn_norm"]), _ptr(v[p + "ffn_norm"])
+        d.d_q_bias, d.d_k_bias, d.d_v_bias = (_ptr(v.get(p + "attn_%s.bias" % q)) for q in "qkv")
+        d.d_q_norm, d.d_k_norm = _ptr(v.get(p + "attn_q_norm")), _ptr(v.get(p + "attn_k_norm"))
+        d.d_rope_freqs = _ptr(v.get("rope_freqs"))
+        d.embd, d.heads, d.kv_heads, d.head_dim = c.embd, c.heads, c.kv_heads, c.head_dim
+        d.rope_dims, d.neox = c.rope_dims or c.head_dim, int(c.neox)
+        d.rope_base, d.rope_freq_scale = float(c.rope_base), float(c.rope_freq_scale)
+        d.eps, d.attention_scale, d.residual_scale = c.eps, c.attention_scale, c.residual_scale
+        return d
+
+    def _rows(self, T):
+        x = self._x.get(T)
+        if x is None:
+            x = self._x[T] = self.torch.empty((T, self.cfg.embd), device=self.dev)
+        return x
+
+    def forward(self, tokens, pos0):
+        """Forward (src/Transformer.cs:83-110) of tokens at positions pos0..: the KV caches take
+        their keys and values, and self.logits (device, [1][vocab]) the last token's logits.
+        Queued on the context's stream; returns self.logits."""
+        T = len(tokens)
+        if T == 0:
+            raise ShapeError("No tokens to run.")
+        if pos0 > self.length:
+            raise ShapeError("pos0 is past the cached positions.")
+        if pos0 + T > self.max_positions:
+            raise ShapeError("The prompt and reply need %d positions; the context is %d."
+                             % (pos0 + T, self.max_positions))
+        L, h, c = self.L, self.ctx.handle, ctypes.c_void_p
+        x = self._rows(T)
+        toks = (ctypes.c_int32 * T)(*tokens)
+        check(L.wl_embed_dev(h, self.embd_w.handle, toks, T, c(x.data_ptr())))
+        for l, d in enumerate(self.descs):
+            check(L.wl_layer_dev(h, ctypes.byref(d), c(x.data_ptr()), T, pos0, c(self.K[l].data_ptr()),
+                                 c(self.V[l].data_ptr())))
+        self.length = pos0 + T
+        # Head (src/Transformer.cs:112-125) of the last row
+        check(L.wl_rms_norm_dev(h, c(x[T - 1:].data_ptr()), 1, self.cfg.embd, c(self.v["output_norm"].data_ptr()),
+                                ctypes.c_float(self.cfg.eps), c(self._xn.data_ptr())))
+        check(L.wl_matmul_dev(h, self.head_w.handle, -1, c(self._xn.data_ptr()), 1, c(self.logits.data_ptr())))
+        return self.logits
+
+    def sample(self):
+        """Greedy pick of self.logits on the device (src/Engine.cs:356-360); waits for it."""
+        check(self.L.wl_argmax_dev(self.ctx.handle, ctypes.c_void_p(self.logits.data_ptr()), 1, self.vocab,
+                                   ctypes.c_void_p(self._tok.data_ptr())))
+        self.ctx.sync()
+        return int(self._tok.item())
+
+    def greedy(self, prompt, steps, chunk=None, keep_logits=False):
+        """The prompt in chunks of `chunk` tokens (all at once when None), then `steps` greedy
+        tokens. Returns the tokens, and the last position's logits after the prompt and after
+        each token when keep_logits."""
+        chunk = chunk or len(prompt)
+        pos = 0
+        for i in range(0, len(prompt), chunk):
+            part = list(prompt[i:i + chunk])
+            self.forward(part, pos)
+            pos += len(part)
+        seen = []
+        out = []
+        for _ in range(steps):
+            if keep_logits:
+                seen.append(self.host_logits())
+            t = self.sample()
+            out.append(t)
+            self.forward([t], pos)
+            pos += 1
+        if keep_logits:
+            seen.append(self.host_logits())
+        return (out, seen) if keep_logits else out
+
+    def host_logits(self):
+        self.ctx.sync()
+        return self.logits[0].cpu().numpy().astype(np.float32)
