@@ -337,7 +337,8 @@ def run_decode(args):
     loop, src/Engine.cs:356-360). 80 distinct layers in HBM (each its own copy of one synthetic
     layer's blocks), a Q4_K embedding and a Q6_K head of 128256 rows, fp16 KV caches. The prompt
     runs as one prefill pass (the MFMA GEMMs), then --warmup greedy tokens untimed and --tokens
-    timed; each token's id is read back to the host before the next step, as the engine does."""
+    timed with each sampled id fed to the next step on the device (value); then 16 tokens with
+    the host reading every id before the next step (host_synced_tokens_per_s)."""
     import torch
     import windlass_amd
     from windlass_amd import DeviceTransformer, ModelConfig, synth
@@ -369,25 +370,39 @@ def run_decode(args):
     load_s = time.perf_counter() - t0
     cfg = ModelConfig(layers=args.layers, embd=HIDDEN, heads=HEADS, kv_heads=KV_HEADS, head_dim=HEAD_DIM,
                       rope_base=500000.0, eps=1e-5)
-    ctxlen = args.prompt + args.warmup + args.tokens
+    host_tokens = 16
+    ctxlen = args.prompt + args.warmup + args.tokens + host_tokens + 1
     m = DeviceTransformer(ctx, cfg, weights, vectors, ctxlen)
     prompt = [int(v) for v in rng.integers(0, VOCAB, args.prompt)]
     ctx.sync()
     t0 = time.perf_counter()
     m.forward(prompt, 0)
-    tok = m.sample()
+    ctx.sync()
     prefill_s = time.perf_counter() - t0
+    # the greedy loop with each id fed back on the device (the host queues ahead)
+    ids = torch.empty(args.warmup + args.tokens + 1, dtype=torch.int32, device=dev)
+    m.sample_into(ids[0:1])
     pos = args.prompt
-    for _ in range(args.warmup):
-        m.forward([tok], pos)
-        tok = m.sample()
+    for i in range(args.warmup):
+        m.forward_ids(ids[i:i + 1], pos)
+        m.sample_into(ids[i + 1:i + 2])
         pos += 1
+    ctx.sync()
     t0 = time.perf_counter()
-    for _ in range(args.tokens):
+    for i in range(args.warmup, args.warmup + args.tokens):
+        m.forward_ids(ids[i:i + 1], pos)
+        m.sample_into(ids[i + 1:i + 2])
+        pos += 1
+    ctx.sync()
+    decode_s = time.perf_counter() - t0
+    # the same with the host reading every id before the next step (the engine's loop)
+    tok = int(ids[-1].item())
+    t0 = time.perf_counter()
+    for _ in range(host_tokens):
         m.forward([tok], pos)
         tok = m.sample()
         pos += 1
-    decode_s = time.perf_counter() - t0
+    host_s = (time.perf_counter() - t0) / host_tokens
     per_tok = decode_s / args.tokens
     wbytes = sum(w.Rows * w.RowBytes for k, w in weights.items() if k != "token_embd") + HIDDEN * 2 * 4 * args.layers
     emb_row = HIDDEN // 256 * 144
@@ -404,6 +419,7 @@ def run_decode(args):
             "weights_read_per_token_bytes": int(wbytes + emb_row),
             "kv_read_per_token_bytes_mean": int(kv_bytes),
             "effective_GBps": round((wbytes + emb_row + kv_bytes) / per_tok / 1e9, 1),
+            "host_synced_tokens_per_s": round(1.0 / host_s, 2),
             "prefill_tokens_per_s": round(args.prompt / prefill_s, 1), "prefill_s": round(prefill_s, 4),
             "load_s": round(load_s, 2)}
     print(json.dumps(line), flush=True)

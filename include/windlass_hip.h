@@ -245,6 +245,11 @@ int wl_argmax_dev(wl_ctx *ctx, const float *d_logits, int32_t rows, int64_t n, i
  * (token ids on the host) into d_x [T][cols]. */
 int wl_embed_dev(wl_ctx *ctx, const wl_weight *embd, const int32_t *tokens, int32_t T, float *d_x);
 
+/* wl_embed_dev with the token ids in device memory (d_tokens [T], e.g. wl_argmax_dev's output),
+ * so a decode loop feeds each sampled token to the next step without a host round trip. The ids
+ * cannot be checked on the host: an id outside the vocabulary gives a row of zeros. */
+int wl_embed_dev_ids(wl_ctx *ctx, const wl_weight *embd, const int32_t *d_tokens, int32_t T, float *d_x);
+
 /* One decoder layer: the weights and vectors Transformer.Layer reads from its stage
  * (src/Transformer.cs:177-232) and the model constants it uses (ModelConfig). Vectors are
  * device fp32 arrays; the optional ones are null when the architecture has none (biases: qwen2;

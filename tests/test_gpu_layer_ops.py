@@ -191,6 +191,14 @@ def test_embed_rows(ctx, t):
     rb = data.size // vocab
     want = np.stack([oracle.decode(int(t), data[i * rb:(i + 1) * rb], cols) for i in toks])
     assert np.array_equal(got.view(np.uint32), want.astype(F32).view(np.uint32))
+    # the ids in device memory: the same rows; ids outside the vocabulary give zero rows
+    d_ids = dev(np.array(toks + [-1, vocab], np.int32))
+    out2 = torch.full((len(toks) + 2, cols), 7.0, device=DEV)
+    torch.cuda.synchronize()
+    check(load().wl_embed_dev_ids(ctx.handle, w.handle, P(d_ids), len(toks) + 2, P(out2)))
+    got2 = host(ctx, out2)
+    assert np.array_equal(got2[:len(toks)].view(np.uint32), want.astype(F32).view(np.uint32))
+    assert not got2[len(toks):].any()
     bad = (ctypes.c_int32 * 1)(vocab)
     with pytest.raises(ArgumentOutOfRangeError):
         check(load().wl_embed_dev(ctx.handle, w.handle, bad, 1, P(out)))

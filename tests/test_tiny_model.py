@@ -157,6 +157,7 @@ def test_gpu_device_resident_greedy_tokens_match_cpu(gpu, key):
     got, got_logits = dm.greedy(PROBE, 8, chunk=8, keep_logits=True)
     # the whole prompt in one pass (T = 12: the bf16 GEMMs and the separate SiLU pass) meets
     # llama.cpp's bar at the last position
+    assert dm.greedy(PROBE, 8, chunk=8) == got  # the ids fed back on the device
     dm.forward(PROBE, 0)
     last = dm.host_logits()
     for w in weights.values():

@@ -887,6 +887,15 @@ extern "C" int wl_embed_dev(wl_ctx *c, const wl_weight *embd, const int32_t *tok
   return WL_OK;
 }
 
+extern "C" int wl_embed_dev_ids(wl_ctx *c, const wl_weight *embd, const int32_t *d_tokens, int32_t T, float *d_x) {
+  if (!c || !embd || !d_tokens || !d_x) return fail(WL_E_ARG, "wl_embed_dev_ids: null argument");
+  if (T < 0) return fail(WL_E_SHAPE, "wl_embed_dev_ids: T = %d", T);
+  WL_HIP(wl::dequant_rows_launch(embd->type, embd->dev, embd->row_bytes, d_tokens, T, embd->rows * embd->experts,
+                                 embd->cols, d_x, c->stream),
+         "embedding rows");
+  return WL_OK;
+}
+
 // Transformer.Layer (src/Transformer.cs:177-232) with every activation in HBM.
 extern "C" int wl_layer_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
                             uint16_t *d_V) {

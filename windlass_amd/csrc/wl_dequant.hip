@@ -145,10 +145,13 @@ struct DqBlk {
   }
 };
 
+// Rows row0.. of the tensor, or (ids non-null) rows ids[0..nrows): an id outside
+// [0, tensor_rows) gives a row of zeros, never a read outside the tensor.
 template <class D>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
                                                       int64_t row0, int64_t nrows, int64_t cols,
-                                                      float *__restrict__ dst) {
+                                                      float *__restrict__ dst, const int32_t *__restrict__ ids,
+                                                      int64_t tensor_rows) {
   const int64_t nb = cols / D::BLOCK;
   const int64_t per_row = nb * D::CHUNKS;
   const int64_t total = nrows * per_row;
@@ -157,18 +160,25 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict_
     const int64_t r = i / per_row, rem = i % per_row;
     const int64_t b = rem / D::CHUNKS;
     const int c = (int)(rem % D::CHUNKS);
-    D::run(w + (row0 + r) * row_bytes + b * D::BYTES, c, dst + r * cols + b * D::BLOCK);
+    const int64_t row = ids ? (int64_t)ids[r] : row0 + r;
+    float *y = dst + r * cols + b * D::BLOCK;
+    if (ids && (row < 0 || row >= tensor_rows)) {
+      for (int j = c * (D::BLOCK / D::CHUNKS); j < (c + 1) * (D::BLOCK / D::CHUNKS); j++) y[j] = 0.f;
+      continue;
+    }
+    D::run(w + row * row_bytes + b * D::BYTES, c, y);
   }
 }
 
 template <class D>
 static hipError_t launch(const uint8_t *w, int64_t row_bytes, int64_t row0, int64_t nrows, int64_t cols,
-                         float *dst, hipStream_t st) {
+                         float *dst, const int32_t *ids, int64_t tensor_rows, hipStream_t st) {
   const int64_t total = nrows * (cols / D::BLOCK) * D::CHUNKS;
   if (total == 0) return hipSuccess;
   int64_t grid = (total + 255) / 256;
   if (grid > 65536) grid = 65536;
-  hipLaunchKernelGGL((dequant_kernel<D>), dim3((unsigned)grid), dim3(256), 0, st, w, row_bytes, row0, nrows, cols, dst);
+  hipLaunchKernelGGL((dequant_kernel<D>), dim3((unsigned)grid), dim3(256), 0, st, w, row_bytes, row0, nrows, cols, dst,
+                     ids, tensor_rows);
   return hipGetLastError();
 }
 
@@ -180,27 +190,37 @@ bool dequant_supports(int type) {
   return false;
 }
 
-hipError_t dequant_launch(int type, const uint8_t *w, int64_t row_bytes, int64_t row0, int64_t nrows,
-                          int64_t cols, float *dst, hipStream_t st) {
+static hipError_t dequant_any(int type, const uint8_t *w, int64_t row_bytes, int64_t row0, int64_t nrows,
+                              int64_t cols, float *dst, const int32_t *ids, int64_t tensor_rows, hipStream_t st) {
   switch (type) {
-    case 0: return launch<DqF32>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 1: return launch<DqF16>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 30: return launch<DqBF16>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 8: return launch<DqQ80>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 12: return launch<DqQ4K>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 14: return launch<DqQ6K>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 23: return launch<DqIQ4XS>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 16: return launch<DqIQ2XXS>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 2: return launch<DqBlk<BQ40>>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 3: return launch<DqBlk<BQ41>>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 6: return launch<DqBlk<BQ50>>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 7: return launch<DqBlk<BQ51>>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 10: return launch<DqBlk<BQ2K>>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 11: return launch<DqBlk<BQ3K>>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 13: return launch<DqBlk<BQ5K>>(w, row_bytes, row0, nrows, cols, dst, st);
-    case 20: return launch<DqBlk<BIQ4NL>>(w, row_bytes, row0, nrows, cols, dst, st);
+    case 0: return launch<DqF32>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 1: return launch<DqF16>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 30: return launch<DqBF16>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 8: return launch<DqQ80>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 12: return launch<DqQ4K>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 14: return launch<DqQ6K>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 23: return launch<DqIQ4XS>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 16: return launch<DqIQ2XXS>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 2: return launch<DqBlk<BQ40>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 3: return launch<DqBlk<BQ41>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 6: return launch<DqBlk<BQ50>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 7: return launch<DqBlk<BQ51>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 10: return launch<DqBlk<BQ2K>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 11: return launch<DqBlk<BQ3K>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 13: return launch<DqBlk<BQ5K>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 20: return launch<DqBlk<BIQ4NL>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t dequant_launch(int type, const uint8_t *w, int64_t row_bytes, int64_t row0, int64_t nrows,
+                          int64_t cols, float *dst, hipStream_t st) {
+  return dequant_any(type, w, row_bytes, row0, nrows, cols, dst, nullptr, 0, st);
+}
+
+hipError_t dequant_rows_launch(int type, const uint8_t *w, int64_t row_bytes, const int32_t *ids, int64_t nrows,
+                               int64_t tensor_rows, int64_t cols, float *dst, hipStream_t st) {
+  return dequant_any(type, w, row_bytes, 0, nrows, cols, dst, ids, tensor_rows, st);
 }
 
 }  // namespace wl

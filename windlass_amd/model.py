@@ -3,10 +3,11 @@
 (src/Engine.cs:356-360).
 
 The weights are WeightViews (raw GGUF blocks in HBM, uploaded or views into a Stage), the norm
-and bias vectors device float32 tensors, the KV caches fp16 on the device. A decode step is
-wl_embed_dev, one wl_layer_dev per layer, the final RMSNorm, the output product and the device
-argmax; only the sampled token id crosses to the host. All of it is queued on the context's
-stream without a host wait until the token id is read.
+and bias vectors device float32 tensors, the KV caches fp16 on the device. A decode step is the
+embedding rows, one wl_layer_dev per layer, the final RMSNorm, the output product and the device
+argmax, all queued on the context's stream. The greedy loop keeps each sampled id on the device
+and feeds it to the next step's embedding (wl_embed_dev_ids), so the host queues a whole reply
+without waiting and reads the ids once.
 """
 import ctypes
 from dataclasses import dataclass
@@ -95,6 +96,23 @@ class DeviceTransformer:
         their keys and values, and self.logits (device, [1][vocab]) the last token's logits.
         Queued on the context's stream; returns self.logits."""
         T = len(tokens)
+        self._check(T, pos0)
+        x = self._rows(T)
+        toks = (ctypes.c_int32 * T)(*tokens)
+        check(self.L.wl_embed_dev(self.ctx.handle, self.embd_w.handle, toks, T, ctypes.c_void_p(x.data_ptr())))
+        return self._layers_and_head(x, T, pos0)
+
+    def forward_ids(self, d_ids, pos0):
+        """forward() with the token ids in device memory (an int32 tensor, e.g. a sampled token):
+        nothing waits for them on the host."""
+        T = d_ids.numel()
+        self._check(T, pos0)
+        x = self._rows(T)
+        check(self.L.wl_embed_dev_ids(self.ctx.handle, self.embd_w.handle, ctypes.c_void_p(d_ids.data_ptr()), T,
+                                      ctypes.c_void_p(x.data_ptr())))
+        return self._layers_and_head(x, T, pos0)
+
+    def _check(self, T, pos0):
         if T == 0:
             raise ShapeError("No tokens to run.")
         if pos0 > self.length:
@@ -102,10 +120,9 @@ class DeviceTransformer:
         if pos0 + T > self.max_positions:
             raise ShapeError("The prompt and reply need %d positions; the context is %d."
                              % (pos0 + T, self.max_positions))
+
+    def _layers_and_head(self, x, T, pos0):
         L, h, c = self.L, self.ctx.handle, ctypes.c_void_p
-        x = self._rows(T)
-        toks = (ctypes.c_int32 * T)(*tokens)
-        check(L.wl_embed_dev(h, self.embd_w.handle, toks, T, c(x.data_ptr())))
         for l, d in enumerate(self.descs):
             check(L.wl_layer_dev(h, ctypes.byref(d), c(x.data_ptr()), T, pos0, c(self.K[l].data_ptr()),
                                  c(self.V[l].data_ptr())))
@@ -118,10 +135,14 @@ class DeviceTransformer:
 
     def sample(self):
         """Greedy pick of self.logits on the device (src/Engine.cs:356-360); waits for it."""
-        check(self.L.wl_argmax_dev(self.ctx.handle, ctypes.c_void_p(self.logits.data_ptr()), 1, self.vocab,
-                                   ctypes.c_void_p(self._tok.data_ptr())))
+        self.sample_into(self._tok)
         self.ctx.sync()
         return int(self._tok.item())
+
+    def sample_into(self, d_out):
+        """The greedy pick into a device int32 element, queued (no wait)."""
+        check(self.L.wl_argmax_dev(self.ctx.handle, ctypes.c_void_p(self.logits.data_ptr()), 1, self.vocab,
+                                   ctypes.c_void_p(d_out.data_ptr())))
 
     def greedy(self, prompt, steps, chunk=None, keep_logits=False):
         """The prompt in chunks of `chunk` tokens (all at once when None), then `steps` greedy
@@ -133,6 +154,17 @@ class DeviceTransformer:
             part = list(prompt[i:i + chunk])
             self.forward(part, pos)
             pos += len(part)
+        if not keep_logits:
+            # each sampled id stays on the device and feeds the next step: the host queues the
+            # whole reply and reads the ids once
+            ids = self.torch.empty(steps + 1, dtype=self.torch.int32, device=self.dev)
+            self.sample_into(ids[0:1])
+            for i in range(steps):
+                self.forward_ids(ids[i:i + 1], pos)
+                pos += 1
+                self.sample_into(ids[i + 1:i + 2])
+            self.ctx.sync()
+            return [int(v) for v in ids[:steps].cpu().tolist()]
         seen = []
         out = []
         for _ in range(steps):
