@@ -1,0 +1,156 @@
+"""GGUF reader (GgufModelFile, src/Gguf.cs:104-270) and ModelConfig.From for the device forward
+(src/ModelConfig.cs:38-100), on files written by tests/gguf_writer.py. CPU only.
+
+The writer lays the format out from ggml's specification; the byte-level checks below pin the
+header offsets independently of the reader (magic, version, counts at fixed offsets, the
+tensor data at the aligned offset)."""
+import struct
+
+import numpy as np
+import pytest
+
+from gguf_writer import ARR, BOOL, F32, F64, I8, I16, I32, I64, STR, U8, U16, U32, U64, tiny_model_gguf, write_gguf
+from windlass_amd._lib import NotSupportedError
+from windlass_amd.backend import GgmlType
+from windlass_amd.gguf import GgufModelFile, InvalidDataError, model_config
+
+META = [("general.architecture", STR, "llama"), ("u8", U8, 200), ("i8", I8, -5), ("u16", U16, 65000),
+        ("i16", I16, -30000), ("u32", U32, 4000000000), ("i32", I32, -7), ("f32", F32, 1.5), ("b", BOOL, True),
+        ("u64", U64, 1 << 60), ("i64", I64, -(1 << 50)), ("f64", F64, 0.1), ("s", STR, "héllo"),
+        ("strs", ARR, (STR, ["a", "", "ccc"])), ("ints", ARR, (I32, [1, -2, 3])), ("fl", ARR, (F32, [0.5, 2.0])),
+        ("bools", ARR, (BOOL, [True, False]))]
+
+
+def _tensors(rng):
+    q4 = rng.integers(0, 256, 2 * 144, dtype=np.uint8)        # 2 rows of one Q4_K block
+    f32 = rng.standard_normal(100, dtype=np.float32).view(np.uint8)
+    q8 = rng.integers(0, 256, 6 * 2 * 34, dtype=np.uint8)     # [3][2][64] Q8_0: 6 rows of 2 blocks
+    return [("a.weight", [256, 2], int(GgmlType.Q4_K), q4), ("v", [100], 0, f32), ("e", [64, 2, 3], 8, q8)]
+
+
+def test_header_bytes_and_round_trip(tmp_path):
+    rng = np.random.default_rng(0)
+    p = tmp_path / "m.gguf"
+    ts = _tensors(rng)
+    write_gguf(p, META, ts, alignment=64)
+    raw = p.read_bytes()
+    assert raw[:4] == b"GGUF" and struct.unpack_from("<Iqq", raw, 4) == (3, 3, len(META) + 1)
+    g = GgufModelFile.Open(p)
+    md = g.Metadata
+    for k, t, v in META:
+        if t == ARR:
+            got = md[k]
+            assert list(got) == list(v[1]), k
+        elif t == F32:
+            assert md[k] == np.float32(v)
+        else:
+            assert md[k] == v, k
+    assert md["general.alignment"] == 64
+    assert [t.Name for t in g.Tensors] == ["a.weight", "v", "e"]
+    a, v, e = g.Tensors
+    assert (a.Type, a.Rows, a.Cols, a.SizeBytes) == (GgmlType.Q4_K, 2, 256, 288)
+    assert (v.Type, v.Rows, v.Cols, v.SizeBytes) == (GgmlType.F32, 1, 100, 400)
+    assert (e.Rows, e.Cols, e.SizeBytes, e.ElementCount) == (6, 64, 408, 384)
+    for t, (_, _, _, data) in zip(g.Tensors, ts):
+        assert t.FileOffset % 64 == 0
+        assert np.array_equal(g.data(t), data)
+        assert raw[t.FileOffset:t.FileOffset + t.SizeBytes] == data.tobytes()
+
+
+def test_version_2_and_default_alignment(tmp_path):
+    p = tmp_path / "v2.gguf"
+    write_gguf(p, META[:1], _tensors(np.random.default_rng(1))[:1], version=2)
+    g = GgufModelFile.Open(p)
+    assert g.Tensors[0].FileOffset % 32 == 0 and "general.alignment" not in g.Metadata
+
+
+@pytest.mark.parametrize("case", ["magic", "version1", "version4", "alignment", "past_end", "duplicate", "dims0",
+                                  "row", "short"])
+def test_malformed_files_are_refused(tmp_path, case):
+    rng = np.random.default_rng(2)
+    p = tmp_path / "bad.gguf"
+    ts = _tensors(rng)
+    kw = {}
+    if case == "magic":
+        kw["magic"] = b"GGUG"
+    elif case in ("version1", "version4"):
+        kw["version"] = 1 if case == "version1" else 4
+    elif case == "alignment":
+        write_gguf(p, META[:1] + [("general.alignment", U32, 48)], ts)
+    elif case == "duplicate":
+        ts = ts + [ts[1]]
+    elif case == "dims0":
+        ts = [("z", [], 0, np.zeros(0, np.uint8))]
+    elif case == "row":
+        ts = [("r", [100, 1], int(GgmlType.Q4_K), np.zeros(144, np.uint8))]
+    if case != "alignment":
+        write_gguf(p, META[:1], ts, **kw)
+    if case == "past_end":
+        raw = p.read_bytes()
+        p.write_bytes(raw[:-50])
+    if case == "short":
+        p.write_bytes(p.read_bytes()[:40])
+    with pytest.raises(InvalidDataError):
+        GgufModelFile.Open(p)
+
+
+def test_unknown_tensor_type_is_not_supported(tmp_path):
+    p = tmp_path / "t.gguf"
+    write_gguf(p, META[:1], [("x", [32], 99, np.zeros(64, np.uint8))])
+    with pytest.raises(NotSupportedError):
+        GgufModelFile.Open(p)
+
+
+def test_split_model_parts(tmp_path):
+    rng = np.random.default_rng(3)
+    ts = _tensors(rng)
+    base = tmp_path / "m"
+    write_gguf(str(base) + "-00001-of-00002.gguf", META[:2] + [("split.no", U16, 0)], ts[:2])
+    write_gguf(str(base) + "-00002-of-00002.gguf", [("split.no", U16, 1), ("late", U32, 9)], ts[2:])
+    g = GgufModelFile.Open(str(base) + "-00002-of-00002.gguf")  # any part opens the whole model
+    assert [t.Name for t in g.Tensors] == ["a.weight", "v", "e"] and [t.FileIndex for t in g.Tensors] == [0, 0, 1]
+    assert g.Metadata["split.no"] == 0 and g.Metadata["late"] == 9   # the first part's value wins
+    assert np.array_equal(g.data(g.Tensors[2]), ts[2][3])
+    (tmp_path / "m-00002-of-00002.gguf").unlink()
+    with pytest.raises(FileNotFoundError):
+        GgufModelFile.Open(str(base) + "-00001-of-00002.gguf")
+
+
+@pytest.mark.parametrize("key", ["llama-q8_0", "qwen2-q6_K-tied", "qwen3-q4_K"])
+def test_tiny_model_config(tmp_path, key):
+    from tiny_model import EMBD, EPS, HEADS, KV_HEADS, LAYERS, SPECS
+    if key not in SPECS:
+        pytest.skip("no such tiny model")
+    p = tmp_path / "tiny.gguf"
+    arch = tiny_model_gguf(p, key)
+    g = GgufModelFile.Open(p)
+    c = model_config(g)
+    assert (c.layers, c.embd, c.heads, c.kv_heads, c.head_dim, c.rope_dims) == (LAYERS, EMBD, HEADS, KV_HEADS,
+                                                                                  EMBD // HEADS, EMBD // HEADS)
+    assert c.neox == (arch != "llama") and c.eps == float(np.float32(EPS))
+    assert c.rope_base == (500000.0 if arch == "llama" else 1000000.0)
+    assert ("output.weight" in g.TensorsByName) == (not key.endswith("tied"))
+
+
+@pytest.mark.parametrize("md,err", [
+    ([("general.architecture", STR, "gpt2")], "architecture"),
+    ([("general.architecture", STR, "qwen3moe"), ("qwen3moe.expert_count", U32, 8)], "experts"),
+    ([("general.architecture", STR, "llama"), ("llama.embedding_length", U32, 64), ("llama.block_count", U32, 1),
+      ("llama.attention.head_count", U32, 6), ("llama.attention.head_count_kv", U32, 4)], "multiple"),
+    ([("general.architecture", STR, "llama"), ("llama.embedding_length", U32, 64), ("llama.block_count", U32, 1),
+      ("llama.attention.head_count", U32, 4), ("llama.rope.scaling.type", STR, "yarn"),
+      ("llama.rope.scaling.factor", F32, 4.0)], "scaling"),
+])
+def test_model_config_refusals(tmp_path, md, err):
+    p = tmp_path / "c.gguf"
+    write_gguf(p, md, [])
+    with pytest.raises(NotSupportedError, match=err):
+        model_config(GgufModelFile.Open(p))
+
+
+def test_linear_rope_scaling(tmp_path):
+    p = tmp_path / "s.gguf"
+    write_gguf(p, [("general.architecture", STR, "llama"), ("llama.embedding_length", U32, 64),
+                   ("llama.block_count", U32, 1), ("llama.attention.head_count", U32, 4),
+                   ("llama.rope.scaling.type", STR, "linear"), ("llama.rope.scaling.factor", F32, 4.0)], [])
+    assert model_config(GgufModelFile.Open(p)).rope_freq_scale == 0.25

@@ -168,3 +168,21 @@ def test_gpu_device_resident_greedy_tokens_match_cpu(gpu, key):
     ref = np.array(LLAMA_CPP[key]["last"], np.float64)
     rel = np.abs(last - ref).max() / ref.std()
     assert rel <= 0.2 and int(np.argmax(last)) == LLAMA_CPP[key]["argmax"][-1], (key, rel)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("key", _gpu_keys())
+def test_gpu_gguf_file_greedy_tokens_match_cpu(gpu, key, tmp_path):
+    """The tiny model written as a GGUF file and loaded by the reader (GgufModelFile,
+    ModelConfig.From, raw blocks to HBM, vectors decoded on the GPU) gives the CPU backend's
+    greedy tokens, the ids fed back on the device."""
+    from gguf_writer import tiny_model_gguf
+    from windlass_amd.gguf import load_device_model
+    p = tmp_path / "tiny.gguf"
+    tiny_model_gguf(p, key)
+    want, _ = Model(key, oracle_matmul).greedy(PROBE, 8, chunk=8)
+    dm, weights = load_device_model(gpu, p)
+    got = dm.greedy(PROBE, 8, chunk=8)
+    for w in weights.values():
+        w.free()
+    assert got == want, "%s: greedy tokens %s, CPU backend %s" % (key, got, want)

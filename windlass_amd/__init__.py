@@ -17,6 +17,8 @@ libwindlass_hip.so (include/windlass_hip.h):
 - ``LayerDesc`` + wl_layer_dev    Transformer.Layer (src/Transformer.cs:177-232) on device-resident activations
 - ``DeviceTransformer``           Transformer.Forward/Head (src/Transformer.cs:83-125) and the greedy
                                   loop (src/Engine.cs:356-360), every tensor resident in HBM
+- ``gguf.GgufModelFile``          GgufModelFile (src/Gguf.cs:104-270); ``gguf.model_config`` and
+                                  ``gguf.load_device_model``: ModelConfig.From and a file's model in HBM
 
 Errors map to the reference's exception kinds: ``NotSupportedError`` (NotSupportedException),
 ``ShapeError`` (ArgumentException), ``ArgumentOutOfRangeError``, ``BackendError`` (device
