@@ -273,6 +273,14 @@ typedef struct wl_layer_desc {
 int wl_layer_dev(wl_ctx *ctx, const wl_layer_desc *layer, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
                  uint16_t *d_V);
 
+/* Transformer.ForwardBatch's layer (src/Transformer.cs:127-170): N rows, row i the next token
+ * of its own sequence, at position pos[i] of cache slot slot[i] (host arrays, checked: slots
+ * distinct and below `slots`, positions below slot_positions). d_K / d_V are this layer's pools
+ * [slots][slot_positions][kv_heads * head_dim]. Every product runs the GEMV in passes of at most
+ * 8 rows (EachToken), so row i's bits equal wl_layer_dev of that token alone on its sequence. */
+int wl_layer_batch_dev(wl_ctx *ctx, const wl_layer_desc *layer, float *d_x, int32_t N, const int32_t *pos,
+                       const int32_t *slot, int32_t slots, int32_t slot_positions, uint16_t *d_K, uint16_t *d_V);
+
 #ifdef __cplusplus
 }
 #endif

@@ -186,3 +186,38 @@ def test_gpu_gguf_file_greedy_tokens_match_cpu(gpu, key, tmp_path):
     for w in weights.values():
         w.free()
     assert got == want, "%s: greedy tokens %s, CPU backend %s" % (key, got, want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n_seq", [4, 10])
+@pytest.mark.parametrize("key", _gpu_keys())
+def test_gpu_batch_step_rows_equal_single_sequences(gpu, key, n_seq):
+    """ForwardBatch's promise (src/Transformer.cs:127-131): in a stacked step every row is
+    bit-identical to that sequence's own one-token step. Sequences of different lengths in
+    their own KV slots; 10 sequences run the products in passes of 8 rows."""
+    import ctypes
+    from windlass_amd import DeviceBatch
+    from windlass_amd._lib import ArgumentOutOfRangeError, check, load
+    prompts = [PROBE[(3 * i) % 7:(3 * i) % 7 + 3 + (i * 5) % 10] for i in range(n_seq)]
+    dm, weights = device_model(gpu, key, max_positions=32)
+    single = []
+    for p in prompts:
+        dm.length = 0
+        single.append(dm.greedy(p, 4, keep_logits=True))
+    batch = DeviceBatch(dm, slots=n_seq, slot_positions=32)
+    toks, seen = batch.greedy(prompts, 4, keep_logits=True)
+    for i in range(n_seq):
+        assert toks[i] == single[i][0], (i, toks[i], single[i][0])
+        for s in range(5):
+            assert np.array_equal(seen[s][i].view(np.uint32), single[i][1][s].view(np.uint32)), (i, s)
+    # the entry point's checks: one token per sequence per step, positions inside the slot
+    L, c = load(), ctypes.c_void_p
+    x = torch.zeros((2, dm.cfg.embd), device=dm.dev)
+    torch.cuda.synchronize()
+    for pos, slot in (([1, 2], [0, 0]), ([1, 32], [0, 1]), ([1, 2], [0, n_seq])):
+        with pytest.raises(ArgumentOutOfRangeError):
+            check(L.wl_layer_batch_dev(gpu.handle, ctypes.byref(dm.descs[0]), c(x.data_ptr()), 2,
+                                       (ctypes.c_int32 * 2)(*pos), (ctypes.c_int32 * 2)(*slot), n_seq, 32,
+                                       c(batch.K[0].data_ptr()), c(batch.V[0].data_ptr())))
+    for w in weights.values():
+        w.free()

@@ -17,6 +17,8 @@ libwindlass_hip.so (include/windlass_hip.h):
 - ``LayerDesc`` + wl_layer_dev    Transformer.Layer (src/Transformer.cs:177-232) on device-resident activations
 - ``DeviceTransformer``           Transformer.Forward/Head (src/Transformer.cs:83-125) and the greedy
                                   loop (src/Engine.cs:356-360), every tensor resident in HBM
+- ``DeviceBatch``                 Transformer.ForwardBatch (src/Transformer.cs:127-170) and BatchEngine's
+                                  stacked step (src/BatchEngine.cs:127-173): KV slots, one pass per step
 - ``gguf.GgufModelFile``          GgufModelFile (src/Gguf.cs:104-270); ``gguf.model_config`` and
                                   ``gguf.load_device_model``: ModelConfig.From and a file's model in HBM
 
@@ -28,8 +30,8 @@ from ._lib import (ArgumentOutOfRangeError, BackendError, NotSupportedError, Sha
                    library_path, load)
 from .backend import (Context, FastMath, GgmlType, HostBuffer, LayerDesc, QActs, Quants, Stage, Transformer,
                       WeightView, layout)
-from .model import DeviceTransformer, ModelConfig
+from .model import DeviceBatch, DeviceTransformer, ModelConfig
 
 __all__ = ["ArgumentOutOfRangeError", "BackendError", "NotSupportedError", "ShapeError",
            "library_path", "load", "Context", "FastMath", "GgmlType", "HostBuffer", "LayerDesc", "QActs", "Quants", "Stage",
-           "Transformer", "WeightView", "layout", "DeviceTransformer", "ModelConfig"]
+           "Transformer", "WeightView", "layout", "DeviceBatch", "DeviceTransformer", "ModelConfig"]

@@ -28,6 +28,7 @@ SIGNATURES = {
     "wl_residual_dev": (ctypes.c_int, [P, P, P, I64, ctypes.c_float]),
     "wl_argmax_dev": (ctypes.c_int, [P, P, I32, I64, P]),
     "wl_embed_dev_ids": (ctypes.c_int, [P, P, P, I32, P]),
+    "wl_layer_batch_dev": (ctypes.c_int, [P, P, P, I32, P, P, I32, I32, P, P]),
     "wl_embed_dev": (ctypes.c_int, [P, P, P, I32, P]),
     "wl_layer_dev": (ctypes.c_int, [P, P, P, I32, I32, P, P]),
     "wl_host_alloc": (ctypes.c_int, [I64, PP]),

@@ -48,7 +48,7 @@ struct wl_stage {
 // S_L* are wl_layer_dev's activations (S_LO: wl_matmul_add_dev's product when the add is not
 // the GEMV's own store).
 enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB, S_QA, S_ATT,
-       S_LXN, S_LQ, S_LK, S_LV, S_LATT, S_LO, S_LG, S_LU, S_COUNT };
+       S_LXN, S_LQ, S_LK, S_LV, S_LATT, S_LO, S_LG, S_LU, S_ROWS, S_COUNT };
 
 struct wl_ctx {
   int device;
@@ -59,6 +59,14 @@ struct wl_ctx {
   // growable scratch (device)
   void *buf[S_COUNT];
   size_t cap[S_COUNT];
+  // pinned staging of batch-step rows (positions, slots): a ring whose entries are reused only
+  // after their copy has run, so the host may queue ahead
+  static constexpr int kRowRing = 4;
+  int32_t *rows_host = nullptr;
+  size_t rows_ints = 0;  // ints per ring entry
+  hipEvent_t rows_ev[kRowRing] = {};
+  bool rows_used[kRowRing] = {};
+  int rows_next = 0;
 };
 
 static thread_local std::string g_err;
@@ -183,6 +191,9 @@ extern "C" void wl_destroy(wl_ctx *c) {
   hipStreamSynchronize(c->stream);
   for (void *&b : c->buf)
     if (b) hipFree(b);
+  if (c->rows_host) hipHostFree(c->rows_host);
+  for (hipEvent_t &e : c->rows_ev)
+    if (e) hipEventDestroy(e);
   hipStreamDestroy(c->stream);
   if (c->copy) {
     hipStreamSynchronize(c->copy);
@@ -853,11 +864,11 @@ extern "C" int wl_attention_dev(wl_ctx *c, const float *d_q, int32_t T, int32_t 
     return fail(WL_E_SHAPE, "wl_attention_dev: %d heads over %d KV heads", heads, kv_heads);
   const int kv_dim = kv_heads * head_dim;
   int rc = ensure(c, S_ATT,
-                  (size_t)wl::attention_scratch_floats(T, heads, head_dim, kv_dim, pos0, d_K, d_V) * sizeof(float));
+                  (size_t)wl::attention_scratch_floats(T, heads, head_dim, kv_dim, pos0 + T, d_K, d_V) * sizeof(float));
   if (rc) return rc;
   const int64_t qd = (int64_t)heads * head_dim;
   WL_HIP(wl::attention_launch(d_q, qd, T, d_K, d_V, kv_heads * head_dim, heads, kv_heads, head_dim, pos0, scale,
-                              (float *)c->buf[S_ATT], d_out, qd, c->stream),
+                              (float *)c->buf[S_ATT], d_out, qd, wl::RowMap{}, pos0 + T, c->stream),
          "attention");
   return WL_OK;
 }
@@ -896,9 +907,12 @@ extern "C" int wl_embed_dev_ids(wl_ctx *c, const wl_weight *embd, const int32_t 
   return WL_OK;
 }
 
-// Transformer.Layer (src/Transformer.cs:177-232) with every activation in HBM.
-extern "C" int wl_layer_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
-                            uint16_t *d_V) {
+// Transformer.Layer (src/Transformer.cs:177-232) with every activation in HBM. rm/max_n: the
+// rows' positions and cache slots (a batch step) and the most positions a row attends to;
+// each: every product in GEMV passes of at most 8 rows, so a row's bits do not depend on the
+// batch (ForwardBatch's EachToken, src/Transformer.cs:127-170).
+static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
+                     uint16_t *d_V, const wl::RowMap &rm, int max_n, bool each) {
   if (!c || !L || !d_x || !d_K || !d_V) return fail(WL_E_ARG, "wl_layer_dev: null argument");
   if (!L->attn_q || !L->attn_k || !L->attn_v || !L->attn_output || !L->ffn_gate || !L->ffn_up || !L->ffn_down ||
       !L->d_attn_norm || !L->d_ffn_norm)
@@ -912,24 +926,42 @@ extern "C" int wl_layer_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32
       L->attn_output->cols != QD || L->attn_output->rows != E || L->ffn_gate->cols != E || L->ffn_up->rows != FF ||
       L->ffn_down->cols != FF || L->ffn_down->rows != E)
     return fail(WL_E_SHAPE, "wl_layer_dev: tensor shapes do not match the layer");
+  const int rd = L->rope_dims > 0 ? L->rope_dims : HD;
+  if (rd > HD || rd % 2) return fail(WL_E_SHAPE, "wl_layer_dev: %d rotated of %d per head", rd, HD);
   int rc;
   if ((rc = ensure(c, S_LXN, (size_t)T * E * 4)) || (rc = ensure(c, S_LQ, (size_t)T * QD * 4)) ||
       (rc = ensure(c, S_LK, (size_t)T * KD * 4)) || (rc = ensure(c, S_LV, (size_t)T * KD * 4)) ||
       (rc = ensure(c, S_LATT, (size_t)T * QD * 4)) ||
-      (rc = ensure(c, S_LG, (size_t)T * FF * 4)) || (rc = ensure(c, S_LU, (size_t)T * FF * 4)))
+      (rc = ensure(c, S_LG, (size_t)T * FF * 4)) || (rc = ensure(c, S_LU, (size_t)T * FF * 4)) ||
+      (rc = ensure(c, S_ATT, (size_t)wl::attention_scratch_floats(T, H, HD, KD, max_n, d_K, d_V) * 4)))
     return rc;
   float *xn = (float *)c->buf[S_LXN], *q = (float *)c->buf[S_LQ], *k = (float *)c->buf[S_LK],
         *v = (float *)c->buf[S_LV], *att = (float *)c->buf[S_LATT],
         *g = (float *)c->buf[S_LG], *u = (float *)c->buf[S_LU];
   const float rs = L->residual_scale != 0.f ? L->residual_scale : 1.f;
+  // y = W x over the T rows: past 8 rows the GEMM, or with each GEMV passes of 8
+  auto mm = [&](const wl_weight *w, const float *x, float *y, bool add) -> int {
+    const int step = each ? 8 : T;
+    for (int t0 = 0; t0 < T; t0 += step) {
+      const int n = T - t0 < step ? T - t0 : step;
+      const float *xs = x + (int64_t)t0 * w->cols;
+      float *ys = y + (int64_t)t0 * w->rows;
+      const int r = add ? wl_matmul_add_dev(c, w, -1, xs, n, ys, rs) : matmul_dev(c, w, -1, xs, n, ys);
+      if (r) return r;
+    }
+    return WL_OK;
+  };
   // attention block
   if ((rc = wl_rms_norm_dev(c, d_x, T, E, L->d_attn_norm, L->eps, xn))) return rc;
-  if (T <= 8) {
-    const wl_weight *ws[3] = {L->attn_q, L->attn_k, L->attn_v};
-    float *ys[3] = {q, k, v};
-    if ((rc = wl_matmul_multi_dev(c, 3, ws, xn, T, ys))) return rc;
-  } else if ((rc = matmul_dev(c, L->attn_q, -1, xn, T, q)) || (rc = matmul_dev(c, L->attn_k, -1, xn, T, k)) ||
-             (rc = matmul_dev(c, L->attn_v, -1, xn, T, v))) {
+  if (T <= 8 || each) {
+    for (int t0 = 0; t0 < T; t0 += 8) {  // q, k, v in one launch per 8 rows
+      const int n = T - t0 < 8 ? T - t0 : 8;
+      const wl_weight *ws[3] = {L->attn_q, L->attn_k, L->attn_v};
+      float *ys[3] = {q + (int64_t)t0 * QD, k + (int64_t)t0 * KD, v + (int64_t)t0 * KD};
+      if ((rc = wl_matmul_multi_dev(c, 3, ws, xn + (int64_t)t0 * E, n, ys))) return rc;
+    }
+  } else if ((rc = mm(L->attn_q, xn, q, false)) || (rc = mm(L->attn_k, xn, k, false)) ||
+             (rc = mm(L->attn_v, xn, v, false))) {
     return rc;
   }
   if (L->d_q_bias) WL_HIP(wl::bias_launch(q, L->d_q_bias, T, QD, c->stream), "q bias");
@@ -937,27 +969,79 @@ extern "C" int wl_layer_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32
   if (L->d_v_bias) WL_HIP(wl::bias_launch(v, L->d_v_bias, T, KD, c->stream), "v bias");
   if (L->d_q_norm && (rc = wl_rms_norm_dev(c, q, (int64_t)T * H, HD, L->d_q_norm, L->eps, q))) return rc;
   if (L->d_k_norm && (rc = wl_rms_norm_dev(c, k, (int64_t)T * KH, HD, L->d_k_norm, L->eps, k))) return rc;
-  const int rd = L->rope_dims > 0 ? L->rope_dims : HD;
   const double fs = L->rope_freq_scale != 0.0 ? L->rope_freq_scale : 1.0;
-  if (rd <= 0 || rd > HD || rd % 2) return fail(WL_E_SHAPE, "wl_layer_dev: %d rotated of %d per head", rd, HD);
   WL_HIP(wl::rope_kv_launch(q, k, v, T, H, KH, HD, rd, L->neox, pos0, L->rope_base, fs, L->d_rope_freqs, d_K, d_V,
-                            c->stream),
+                            rm, c->stream),
          "rope and kv store");
   const float scale = L->attention_scale != 0.f ? L->attention_scale : 1.0f / (float)sqrt((double)HD);
-  if ((rc = wl_attention_dev(c, q, T, H, KH, HD, d_K, d_V, pos0, scale, att))) return rc;
-  if ((rc = wl_matmul_add_dev(c, L->attn_output, -1, att, T, d_x, rs))) return rc;
+  WL_HIP(wl::attention_launch(q, QD, T, d_K, d_V, KD, H, KH, HD, pos0, scale, (float *)c->buf[S_ATT], att, QD, rm,
+                              max_n, c->stream),
+         "attention");
+  if ((rc = mm(L->attn_output, att, d_x, true))) return rc;
   // feed-forward block
   if ((rc = wl_rms_norm_dev(c, d_x, T, E, L->d_ffn_norm, L->eps, xn))) return rc;
-  // up to 8 tokens: gate and up in one GEMV launch with the SiLU epilogue; a prompt: the two
-  // GEMMs, then the SiLU pass
+  // up to 8 rows (or every row with each): gate and up in one GEMV launch with the SiLU
+  // epilogue; a prompt: the two GEMMs, then the SiLU pass
   const bool fused = L->ffn_gate->type == L->ffn_up->type &&
-                     (T <= 8 || int_path(c, L->ffn_gate) || !wl::gemm_supports(L->ffn_gate->type));
+                     (T <= 8 || each || int_path(c, L->ffn_gate) || !wl::gemm_supports(L->ffn_gate->type));
   if (fused) {
     if ((rc = wl_gate_up_dev(c, L->ffn_gate, L->ffn_up, -1, xn, T, g))) return rc;
   } else {
-    if ((rc = matmul_dev(c, L->ffn_gate, -1, xn, T, g)) || (rc = matmul_dev(c, L->ffn_up, -1, xn, T, u))) return rc;
+    if ((rc = mm(L->ffn_gate, xn, g, false)) || (rc = mm(L->ffn_up, xn, u, false))) return rc;
     WL_HIP(wl::silu_mul_launch(g, u, (int64_t)T * FF, c->stream), "silu");
   }
-  if ((rc = wl_matmul_add_dev(c, L->ffn_down, -1, g, T, d_x, rs))) return rc;
-  return WL_OK;
+  return mm(L->ffn_down, g, d_x, true);
+}
+
+extern "C" int wl_layer_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
+                            uint16_t *d_V) {
+  return layer_run(c, L, d_x, T, pos0, d_K, d_V, wl::RowMap{}, pos0 + T, false);
+}
+
+// Transformer.ForwardBatch's layer (src/Transformer.cs:127-170): N rows, each the next token of
+// its own sequence, at position pos[i] of cache slot slot[i].
+extern "C" int wl_layer_batch_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t N, const int32_t *pos,
+                                  const int32_t *slot, int32_t slots, int32_t slot_positions, uint16_t *d_K,
+                                  uint16_t *d_V) {
+  if (!c || !pos || !slot) return fail(WL_E_ARG, "wl_layer_batch_dev: null argument");
+  if (N <= 0 || slots <= 0 || slot_positions <= 0) return fail(WL_E_SHAPE, "wl_layer_batch_dev: bad shape");
+  int max_n = 0;
+  for (int i = 0; i < N; i++) {
+    if (slot[i] < 0 || slot[i] >= slots)
+      return fail(WL_E_ARG, "Row %d's slot %d is outside 0..%d.", i, slot[i], slots - 1);
+    if (pos[i] < 0 || pos[i] >= slot_positions)
+      return fail(WL_E_ARG, "The prompt and reply need %d positions; the context is %d.", pos[i] + 1, slot_positions);
+    for (int j = 0; j < i; j++)
+      if (slot[j] == slot[i]) return fail(WL_E_ARG, "A sequence can take one token per batch step.");
+    if (pos[i] + 1 > max_n) max_n = pos[i] + 1;
+  }
+  int rc;
+  if ((rc = ensure(c, S_ROWS, (size_t)2 * N * sizeof(int32_t)))) return rc;
+  int32_t *rows = (int32_t *)c->buf[S_ROWS];
+  if ((size_t)2 * N > c->rows_ints) {  // grow the pinned ring (after every queued copy from it)
+    WL_HIP(hipStreamSynchronize(c->stream), "row staging");
+    if (c->rows_host) hipHostFree(c->rows_host);
+    c->rows_host = nullptr;
+    c->rows_ints = 0;
+    const size_t ints = (size_t)2 * N < 1024 ? 1024 : (size_t)2 * N;
+    WL_HIP(hipHostMalloc((void **)&c->rows_host, ints * wl_ctx::kRowRing * sizeof(int32_t), hipHostMallocDefault),
+           "row staging");
+    c->rows_ints = ints;
+    for (bool &u : c->rows_used) u = false;
+  }
+  const int e = c->rows_next;
+  c->rows_next = (e + 1) % wl_ctx::kRowRing;
+  if (!c->rows_ev[e]) WL_HIP(hipEventCreateWithFlags(&c->rows_ev[e], hipEventDisableTiming), "row staging");
+  if (c->rows_used[e]) WL_HIP(hipEventSynchronize(c->rows_ev[e]), "row staging");
+  int32_t *stage = c->rows_host + (size_t)e * c->rows_ints;
+  memcpy(stage, pos, (size_t)N * sizeof(int32_t));
+  memcpy(stage + N, slot, (size_t)N * sizeof(int32_t));
+  WL_HIP(hipMemcpyAsync(rows, stage, (size_t)2 * N * sizeof(int32_t), hipMemcpyHostToDevice, c->stream), "row copy");
+  WL_HIP(hipEventRecord(c->rows_ev[e], c->stream), "row staging");
+  c->rows_used[e] = true;
+  wl::RowMap rm;
+  rm.pos = rows;
+  rm.slot = rows + N;
+  rm.cap = slot_positions;
+  return layer_run(c, L, d_x, N, 0, d_K, d_V, rm, max_n, true);
 }

@@ -5,6 +5,14 @@
 
 namespace wl {
 
+// The rows of a batch step (ForwardBatch): row t is at position pos[t] of cache slot slot[t],
+// slots of cap positions each. All null: the rows of one sequence at pos0, pos0 + 1, ...
+struct RowMap {
+  const int *pos = nullptr;
+  const int *slot = nullptr;
+  int64_t cap = 0;
+};
+
 hipError_t rms_norm_launch(const float *x, int64_t rows, int64_t dim, const float *w, float eps, float *y,
                            hipStream_t st);
 // RoPE on T rows of `heads` heads (row t at pos[t], or pos0 + t when pos is null).
@@ -14,14 +22,15 @@ hipError_t rope_launch(float *x, int64_t ldx, int T, int heads, int hd, int n, i
 // pos0.. of Kc / Vc [positions][KH*hd], in one launch.
 hipError_t rope_kv_launch(float *q, float *k, const float *v, int T, int H, int KH, int hd, int n, int neox,
                           int pos0, double base, double freq_scale, const float *freqs, uint16_t *Kc, uint16_t *Vc,
-                          hipStream_t st);
+                          const RowMap &rm, hipStream_t st);
 hipError_t kv_store_launch(const float *k, const float *v, int64_t n, uint16_t *K, uint16_t *V, hipStream_t st);
-// Floats of scratch attention_launch needs for these operands.
-int64_t attention_scratch_floats(int T, int heads, int hd, int kv_dim, int pos0, const uint16_t *K,
+// Floats of scratch attention_launch needs for these operands; max_n: the most positions a row
+// attends to (pos0 + T for one sequence).
+int64_t attention_scratch_floats(int T, int heads, int hd, int kv_dim, int max_n, const uint16_t *K,
                                  const uint16_t *V);
 hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *K, const uint16_t *V, int kv_dim,
                             int heads, int kv_heads, int hd, int pos0, float scale, float *scratch, float *out,
-                            int64_t ldo, hipStream_t st);
+                            int64_t ldo, const RowMap &rm, int max_n, hipStream_t st);
 hipError_t residual_launch(float *x, const float *o, int64_t n, float rs, hipStream_t st);
 hipError_t argmax_launch(const float *logits, int rows, int64_t n, int *out, hipStream_t st);
 hipError_t bias_launch(float *y, const float *b, int64_t rows, int64_t dim, hipStream_t st);

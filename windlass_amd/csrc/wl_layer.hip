@@ -108,19 +108,21 @@ __device__ __forceinline__ void rope_pair(float *o, int i, int n, int neox, floa
 }
 
 // RoPE on q (H heads) and k (KH heads) of row t, and ToHalf of the row's keys and values into
-// cache row pos0 + t (src/Transformer.cs:204-215,342-348). Work items of a row: one per rotated
-// pair of every q and k head, then one per key/value column (the value's store, and the key's
-// for columns past rope_dims). k, v and the caches are null for RoPE on one tensor.
+// cache row pos0 + t, or row pos[t] of slot slot[t] (slots of cap positions) for a batch step
+// (src/Transformer.cs:204-215,342-348). Work items of a row: one per rotated pair of every q and
+// k head, then one per key/value column (the value's store, and the key's for columns past
+// rope_dims). k, v and the caches are null for RoPE on one tensor.
 __global__ __launch_bounds__(256) void rope_qkv_kernel(float *__restrict__ q, int64_t ldq, int H, float *__restrict__ k,
                                                        const float *__restrict__ v, int KH, int hd, int n, int neox,
                                                        const int *__restrict__ pos, int pos0, double theta_scale,
                                                        double freq_scale, const float *__restrict__ freqs,
-                                                       uint16_t *__restrict__ Kc, uint16_t *__restrict__ Vc) {
+                                                       uint16_t *__restrict__ Kc, uint16_t *__restrict__ Vc,
+                                                       const int *__restrict__ slot, int64_t cap) {
   const int t = blockIdx.y, half = n / 2, KD = KH * hd;
   const int it = blockIdx.x * blockDim.x + threadIdx.x;
   const int npairs = (H + KH) * half;
   const int p = pos ? pos[t] : pos0 + t;
-  const int64_t crow = (int64_t)(pos0 + t) * KD;
+  const int64_t crow = (slot ? (int64_t)slot[t] * cap + p : (int64_t)(pos0 + t)) * KD;
   if (it < npairs) {
     const int head = it / half, i = it % half;
     float c, s, y0, y1;
@@ -162,11 +164,17 @@ __global__ __launch_bounds__(256) void attention_kernel(const float *__restrict_
                                                         const uint16_t *__restrict__ V, int kv_dim, int heads,
                                                         int kv_heads, int hd, int pos0, float scale,
                                                         float *__restrict__ scores, int64_t max_n,
-                                                        float *__restrict__ out, int64_t ldo) {
+                                                        float *__restrict__ out, int64_t ldo,
+                                                        const int *__restrict__ pos, const int *__restrict__ slot,
+                                                        int64_t cap) {
   __shared__ double shd[4];
   __shared__ float shf[4];
   const int t = blockIdx.y, h = blockIdx.x, kvh = h / (heads / kv_heads);
-  const int n = pos0 + t + 1;
+  const int n = pos ? pos[t] + 1 : pos0 + t + 1;
+  if (slot) {  // row t reads its own sequence's slot
+    K += (int64_t)slot[t] * cap * kv_dim;
+    V += (int64_t)slot[t] * cap * kv_dim;
+  }
   const float *qp = q + (int64_t)t * ldq + (int64_t)h * hd;
   float *sp = scores + ((int64_t)t * heads + h) * max_n;
   float mx = -INFINITY;
@@ -224,7 +232,9 @@ __global__ __launch_bounds__(256) void attention_chunk_kernel(const float *__res
                                                               const uint16_t *__restrict__ V, int kv_dim, int heads,
                                                               int kv_heads, int pos0, float scale,
                                                               float *__restrict__ part, int max_chunks,
-                                                              float *__restrict__ out, int64_t ldo) {
+                                                              float *__restrict__ out, int64_t ldo,
+                                                              const int *__restrict__ pos,
+                                                              const int *__restrict__ slot, int64_t cap) {
   constexpr int U = HD / 8;  // uint4 per key row
   __shared__ uint4 vs4[kAttP * U];
   __shared__ float qs[HD];
@@ -233,8 +243,12 @@ __global__ __launch_bounds__(256) void attention_chunk_kernel(const float *__res
   __shared__ double shd[16];
   const int h = blockIdx.x, c = blockIdx.y, t = blockIdx.z;
   const int kvh = h / (heads / kv_heads);
-  const int n = pos0 + t + 1, j0 = c * kAttP;
+  const int n = pos ? pos[t] + 1 : pos0 + t + 1, j0 = c * kAttP;
   if (j0 >= n) return;  // uniform over the workgroup
+  if (slot) {  // row t reads its own sequence's slot
+    K += (int64_t)slot[t] * cap * kv_dim;
+    V += (int64_t)slot[t] * cap * kv_dim;
+  }
   const int cnt = n - j0 < kAttP ? n - j0 : kAttP;
   const int nch = (n + kAttP - 1) / kAttP;
   const int tid = threadIdx.x;
@@ -317,9 +331,9 @@ __global__ __launch_bounds__(256) void attention_chunk_kernel(const float *__res
 template <int HD>
 __global__ __launch_bounds__(256) void attention_combine_kernel(const float *__restrict__ part, int max_chunks,
                                                                 int heads, int pos0, float *__restrict__ out,
-                                                                int64_t ldo) {
+                                                                int64_t ldo, const int *__restrict__ pos) {
   const int h = blockIdx.x, t = blockIdx.y;
-  const int n = pos0 + t + 1, nch = (n + kAttP - 1) / kAttP;
+  const int n = pos ? pos[t] + 1 : pos0 + t + 1, nch = (n + kAttP - 1) / kAttP;
   if (nch == 1) return;
   const float *rec = part + ((int64_t)t * heads + h) * max_chunks * (HD + 4);
   float m = -INFINITY;
@@ -421,17 +435,18 @@ hipError_t rope_launch(float *x, int64_t ldx, int T, int heads, int hd, int n, i
   if (T <= 0) return hipSuccess;
   const int64_t items = (int64_t)heads * (n / 2);
   hipLaunchKernelGGL(rope_qkv_kernel, dim3(blocks_of(items, 256), T), dim3(256), 0, st, x, ldx, heads, nullptr,
-                     nullptr, 0, hd, n, neox, pos, pos0, pow(base, -2.0 / n), freq_scale, freqs, nullptr, nullptr);
+                     nullptr, 0, hd, n, neox, pos, pos0, pow(base, -2.0 / n), freq_scale, freqs, nullptr, nullptr,
+                     nullptr, (int64_t)0);
   return hipGetLastError();
 }
 
 hipError_t rope_kv_launch(float *q, float *k, const float *v, int T, int H, int KH, int hd, int n, int neox,
                           int pos0, double base, double freq_scale, const float *freqs, uint16_t *Kc, uint16_t *Vc,
-                          hipStream_t st) {
+                          const RowMap &rm, hipStream_t st) {
   if (T <= 0) return hipSuccess;
   const int64_t items = (int64_t)(H + KH) * (n / 2) + (int64_t)KH * hd;
   hipLaunchKernelGGL(rope_qkv_kernel, dim3(blocks_of(items, 256), T), dim3(256), 0, st, q, (int64_t)H * hd, H, k, v,
-                     KH, hd, n, neox, nullptr, pos0, pow(base, -2.0 / n), freq_scale, freqs, Kc, Vc);
+                     KH, hd, n, neox, rm.pos, pos0, pow(base, -2.0 / n), freq_scale, freqs, Kc, Vc, rm.slot, rm.cap);
   return hipGetLastError();
 }
 
@@ -447,40 +462,40 @@ static bool attention_chunked(int hd, int kv_dim, const uint16_t *K, const uint1
   return (hd == 64 || hd == 128) && kv_dim % 8 == 0 && ((uintptr_t)K & 15) == 0 && ((uintptr_t)V & 15) == 0;
 }
 
-int64_t attention_scratch_floats(int T, int heads, int hd, int kv_dim, int pos0, const uint16_t *K,
+int64_t attention_scratch_floats(int T, int heads, int hd, int kv_dim, int max_n, const uint16_t *K,
                                  const uint16_t *V) {
   if (T <= 0) return 0;
-  if (!attention_chunked(hd, kv_dim, K, V)) return (int64_t)T * heads * (pos0 + T);
-  const int chunks = (pos0 + T + kAttP - 1) / kAttP;
+  if (!attention_chunked(hd, kv_dim, K, V)) return (int64_t)T * heads * max_n;
+  const int chunks = (max_n + kAttP - 1) / kAttP;
   return chunks > 1 ? (int64_t)T * heads * chunks * (hd + 4) : 0;
 }
 
 template <int HD>
 static hipError_t attention_chunked_launch(const float *q, int64_t ldq, int T, const uint16_t *K, const uint16_t *V,
                                            int kv_dim, int heads, int kv_heads, int pos0, float scale, float *part,
-                                           float *out, int64_t ldo, hipStream_t st) {
-  const int chunks = (pos0 + T + kAttP - 1) / kAttP;
+                                           float *out, int64_t ldo, const RowMap &rm, int max_n, hipStream_t st) {
+  const int chunks = (max_n + kAttP - 1) / kAttP;
   hipLaunchKernelGGL(attention_chunk_kernel<HD>, dim3(heads, chunks, T), dim3(256), 0, st, q, ldq, K, V, kv_dim,
-                     heads, kv_heads, pos0, scale, part, chunks, out, ldo);
+                     heads, kv_heads, pos0, scale, part, chunks, out, ldo, rm.pos, rm.slot, rm.cap);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || chunks == 1) return e;
   hipLaunchKernelGGL(attention_combine_kernel<HD>, dim3(heads, T), dim3(HD), 0, st, part, chunks, heads, pos0, out,
-                     ldo);
+                     ldo, rm.pos);
   return hipGetLastError();
 }
 
 hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *K, const uint16_t *V, int kv_dim,
                             int heads, int kv_heads, int hd, int pos0, float scale, float *scratch, float *out,
-                            int64_t ldo, hipStream_t st) {
+                            int64_t ldo, const RowMap &rm, int max_n, hipStream_t st) {
   if (T <= 0) return hipSuccess;
   if (attention_chunked(hd, kv_dim, K, V)) {
     return hd == 64 ? attention_chunked_launch<64>(q, ldq, T, K, V, kv_dim, heads, kv_heads, pos0, scale, scratch,
-                                                   out, ldo, st)
+                                                   out, ldo, rm, max_n, st)
                     : attention_chunked_launch<128>(q, ldq, T, K, V, kv_dim, heads, kv_heads, pos0, scale, scratch,
-                                                    out, ldo, st);
+                                                    out, ldo, rm, max_n, st);
   }
   hipLaunchKernelGGL(attention_kernel, dim3(heads, T), dim3(256), 0, st, q, ldq, K, V, kv_dim, heads, kv_heads, hd,
-                     pos0, scale, scratch, (int64_t)(pos0 + T), out, ldo);
+                     pos0, scale, scratch, (int64_t)max_n, out, ldo, rm.pos, rm.slot, rm.cap);
   return hipGetLastError();
 }
 

@@ -181,3 +181,101 @@ class DeviceTransformer:
     def host_logits(self):
         self.ctx.sync()
         return self.logits[0].cpu().numpy().astype(np.float32)
+
+
+class DeviceBatch:
+    """Several sequences decoding together on one DeviceTransformer's weights: Transformer.
+    ForwardBatch (src/Transformer.cs:127-170) and BatchEngine's stacked step
+    (src/BatchEngine.cs:127-173). Each sequence owns a slot of the KV pools
+    ([layers][slots][slot_positions][kv_dim], fp16). A prompt runs as its own pass into its slot;
+    a step stacks one token of each given sequence into one pass (wl_layer_batch_dev), so every
+    layer's weights are read once for all of them, and row i's bits equal that sequence's own
+    one-token step."""
+
+    def __init__(self, model, slots, slot_positions):
+        torch = model.torch
+        self.m, self.slots, self.cap = model, slots, slot_positions
+        cfg = model.cfg
+        kd = cfg.kv_heads * cfg.head_dim
+        self.K = torch.zeros((cfg.layers, slots, slot_positions, kd), dtype=torch.int16, device=model.dev)
+        self.V = torch.zeros((cfg.layers, slots, slot_positions, kd), dtype=torch.int16, device=model.dev)
+        self.length = [0] * slots
+        self._bufs = {}
+        torch.cuda.synchronize()
+
+    def _buf(self, kind, rows, cols):
+        """A device float32 buffer kept for the object's life: the library's queued work may still
+        use it when the next call starts, so it is never handed back to torch's allocator."""
+        b = self._bufs.get((kind, rows))
+        if b is None:
+            b = self._bufs[(kind, rows)] = self.m.torch.empty((rows, cols), device=self.m.dev)
+        return b
+
+    def _head(self, x, rows):
+        """Head of `rows` rows of x (norm, then the output product in GEMV passes of 8 rows,
+        EachToken); returns the device logits [rows][vocab]."""
+        m, c = self.m, ctypes.c_void_p
+        lg = self._buf("logits", rows, m.vocab)
+        xn = self._buf("xn", rows, m.cfg.embd)
+        check(m.L.wl_rms_norm_dev(m.ctx.handle, c(x.data_ptr()), rows, m.cfg.embd, c(m.v["output_norm"].data_ptr()),
+                                  ctypes.c_float(m.cfg.eps), c(xn.data_ptr())))
+        for r0 in range(0, rows, 8):
+            n = min(8, rows - r0)
+            check(m.L.wl_matmul_dev(m.ctx.handle, m.head_w.handle, -1, c(xn[r0:].data_ptr()), n,
+                                    c(lg[r0:].data_ptr())))
+        return lg
+
+    def prefill(self, slot, tokens):
+        """The prompt of the sequence in `slot` from its current length (Forward on that
+        sequence's cache); returns the device logits of its last token [1][vocab]."""
+        m, c, T = self.m, ctypes.c_void_p, len(tokens)
+        pos0 = self.length[slot]
+        if T == 0 or pos0 + T > self.cap:
+            raise ShapeError("The prompt and reply need %d positions; the context is %d." % (pos0 + T, self.cap))
+        x = self._buf("x", T, m.cfg.embd)
+        toks = (ctypes.c_int32 * T)(*tokens)
+        check(m.L.wl_embed_dev(m.ctx.handle, m.embd_w.handle, toks, T, c(x.data_ptr())))
+        for l, d in enumerate(m.descs):
+            check(m.L.wl_layer_dev(m.ctx.handle, ctypes.byref(d), c(x.data_ptr()), T, pos0,
+                                   c(self.K[l, slot].data_ptr()), c(self.V[l, slot].data_ptr())))
+        self.length[slot] = pos0 + T
+        return self._head(x[T - 1:], 1)
+
+    def step(self, slots, d_ids):
+        """One stacked decode step: d_ids (device int32 [N]) are the next tokens of the sequences
+        in `slots`; returns the device logits [N][vocab]."""
+        m, c, N = self.m, ctypes.c_void_p, len(slots)
+        pos = (ctypes.c_int32 * N)(*[self.length[s] for s in slots])
+        sl = (ctypes.c_int32 * N)(*slots)
+        x = self._buf("x", N, m.cfg.embd)
+        check(m.L.wl_embed_dev_ids(m.ctx.handle, m.embd_w.handle, c(d_ids.data_ptr()), N, c(x.data_ptr())))
+        for l, d in enumerate(m.descs):
+            check(m.L.wl_layer_batch_dev(m.ctx.handle, ctypes.byref(d), c(x.data_ptr()), N, pos, sl, self.slots,
+                                         self.cap, c(self.K[l].data_ptr()), c(self.V[l].data_ptr())))
+        for s in slots:
+            self.length[s] += 1
+        return self._head(x, N)
+
+    def greedy(self, prompts, steps, keep_logits=False):
+        """Each prompt in its own slot (0, 1, ...), then `steps` stacked greedy steps with the
+        sampled ids fed back on the device. Returns the tokens per sequence (and the host
+        logits [N][vocab] before each step and after the last when keep_logits)."""
+        m, c, N = self.m, ctypes.c_void_p, len(prompts)
+        ids = m.torch.empty((steps + 1, N), dtype=m.torch.int32, device=m.dev)
+        first = m.torch.empty((N, m.vocab), device=m.dev)
+        for i, p in enumerate(prompts):
+            lg = self.prefill(i, list(p))
+            check(m.L.wl_argmax_dev(m.ctx.handle, c(lg.data_ptr()), 1, m.vocab, c(ids[0, i:].data_ptr())))
+            if keep_logits:
+                m.ctx.sync()
+                first[i] = lg[0]
+        seen = [first.cpu().numpy().copy()] if keep_logits else []
+        for s in range(steps):
+            lg = self.step(list(range(N)), ids[s])
+            check(m.L.wl_argmax_dev(m.ctx.handle, c(lg.data_ptr()), N, m.vocab, c(ids[s + 1].data_ptr())))
+            if keep_logits:
+                m.ctx.sync()
+                seen.append(lg.cpu().numpy().copy())
+        m.ctx.sync()
+        toks = ids[:steps].cpu().numpy().T.tolist()
+        return (toks, seen) if keep_logits else toks
