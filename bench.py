@@ -92,7 +92,7 @@ def main():
     if args.stream:
         return run_stream(args)
     if args.decode:
-        return run_decode(args)
+        return run_decode_batch(args) if args.batch > 1 else run_decode(args)
     T = args.batch
     if not 1 <= T <= 8:
         sys.exit("--batch must be 1..8")
@@ -422,6 +422,73 @@ def run_decode(args):
             "host_synced_tokens_per_s": round(1.0 / host_s, 2),
             "prefill_tokens_per_s": round(args.prompt / prefill_s, 1), "prefill_s": round(prefill_s, 4),
             "load_s": round(load_s, 2)}
+    print(json.dumps(line), flush=True)
+    for w in weights.values():
+        w.free()
+    ctx.close()
+
+
+def run_decode_batch(args):
+    """--decode with --batch N: N sequences decoding together on the resident 70B model
+    (DeviceBatch: ForwardBatch's stacked step, src/Transformer.cs:127-170). Each sequence's
+    prompt runs into its own KV slot, then --warmup untimed and --tokens timed stacked steps with
+    the ids fed back on the device. value = tokens of all sequences per second."""
+    import torch
+    import windlass_amd
+    from windlass_amd import DeviceBatch, DeviceTransformer, ModelConfig, synth
+    from windlass_amd._lib import check
+    from windlass_amd.backend import Context
+
+    N = args.batch
+    rng = np.random.default_rng(0x57494E44 + 4000)
+    host = {n: synth.blocks(t, r, c, rng) for n, t, r, c in LAYER}
+    names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate",
+             "up": "ffn_up", "down": "ffn_down"}
+    L = windlass_amd.load()
+    ctx = Context(0)
+    dev = torch.device("cuda:0")
+
+    def norm():
+        return torch.from_numpy((1 + 0.2 * rng.standard_normal(HIDDEN)).astype(np.float32)).to(dev)
+
+    weights = {"token_embd": ctx.upload(Q4_K, np.tile(synth.blocks(Q4_K, VOCAB // 8, HIDDEN, rng), 8), VOCAB, HIDDEN),
+               "output": ctx.upload(Q6_K, np.tile(synth.blocks(Q6_K, VOCAB // 8, HIDDEN, rng), 8), VOCAB, HIDDEN)}
+    vectors = {"output_norm": norm()}
+    for l in range(args.layers):
+        for n, t, r, c in LAYER:
+            key = "blk.%d.%s" % (l, names[n])
+            weights[key] = ctx.upload(t, host[n], r, c, name=key)
+        vectors["blk.%d.attn_norm" % l], vectors["blk.%d.ffn_norm" % l] = norm(), norm()
+    cfg = ModelConfig(layers=args.layers, embd=HIDDEN, heads=HEADS, kv_heads=KV_HEADS, head_dim=HEAD_DIM,
+                      rope_base=500000.0, eps=1e-5)
+    cap = args.prompt + args.warmup + args.tokens + 1
+    m = DeviceTransformer(ctx, cfg, weights, vectors, 1)
+    b = DeviceBatch(m, N, cap)
+    ids = torch.empty((args.warmup + args.tokens + 1, N), dtype=torch.int32, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    for i in range(N):
+        lg = b.prefill(i, [int(v) for v in rng.integers(0, VOCAB, args.prompt)])
+        check(L.wl_argmax_dev(ctx.handle, P(lg), 1, VOCAB, P(ids[0, i:])))
+    seqs = list(range(N))
+    for s in range(args.warmup):
+        lg = b.step(seqs, ids[s])
+        check(L.wl_argmax_dev(ctx.handle, P(lg), N, VOCAB, P(ids[s + 1])))
+    ctx.sync()
+    t0 = time.perf_counter()
+    for s in range(args.warmup, args.warmup + args.tokens):
+        lg = b.step(seqs, ids[s])
+        check(L.wl_argmax_dev(ctx.handle, P(lg), N, VOCAB, P(ids[s + 1])))
+    ctx.sync()
+    per_step = (time.perf_counter() - t0) / args.tokens
+    line = {"metric": "70B Q4_K_M greedy decode of N sequences together, every tensor resident in HBM",
+            "value": round(N / per_step, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.tokens,
+            "warmup": args.warmup, "ms_per_step": round(per_step * 1e3, 3), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "fp32 accumulate over Q4_K/Q6_K blocks",
+            "data": "synthetic seeded GGUF blocks; random prompt ids; random-init norms",
+            "config": {"workload": "Llama-3.3-70B Q4_K_M: %d layers, vocab 128256, %d sequences, prompt %d each, "
+                                   "then %d timed stacked steps" % (args.layers, N, args.prompt, args.tokens),
+                       "batch": N},
+            "tokens_per_s_per_sequence": round(1.0 / per_step, 2), "ms_per_layer": round(per_step * 1e3 / args.layers, 4)}
     print(json.dumps(line), flush=True)
     for w in weights.values():
         w.free()
