@@ -48,7 +48,7 @@ struct wl_stage {
 // S_L* are wl_layer_dev's activations (S_LO: wl_matmul_add_dev's product when the add is not
 // the GEMV's own store).
 enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB, S_QA, S_ATT,
-       S_LXN, S_LQ, S_LK, S_LV, S_LATT, S_LO, S_LG, S_LU, S_ROWS, S_COUNT };
+       S_LXN, S_LQ, S_LK, S_LV, S_LATT, S_LO, S_LG, S_LU, S_ROWS, S_ARG, S_COUNT };
 
 struct wl_ctx {
   int device;
@@ -882,7 +882,9 @@ extern "C" int wl_residual_dev(wl_ctx *c, float *d_x, const float *d_o, int64_t 
 extern "C" int wl_argmax_dev(wl_ctx *c, const float *d_logits, int32_t rows, int64_t n, int32_t *d_out) {
   if (!c || !d_logits || !d_out) return fail(WL_E_ARG, "wl_argmax_dev: null argument");
   if (rows < 0 || n <= 0) return fail(WL_E_SHAPE, "wl_argmax_dev: bad shape");
-  WL_HIP(wl::argmax_launch(d_logits, rows, n, d_out, c->stream), "argmax");
+  int rc = ensure(c, S_ARG, (size_t)2 * (rows > 0 ? rows : 1) * wl::argmax_parts(n) * sizeof(float));
+  if (rc) return rc;
+  WL_HIP(wl::argmax_launch(d_logits, rows, n, d_out, (float *)c->buf[S_ARG], c->stream), "argmax");
   return WL_OK;
 }
 

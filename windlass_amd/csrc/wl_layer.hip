@@ -360,20 +360,10 @@ __global__ void residual_kernel(float *__restrict__ x, const float *__restrict__
 // Greedy sampling (src/Engine.cs:356-360): the first index of the largest logit of each row.
 // NaNs never win a comparison, so they are skipped, except at index 0: the reference starts
 // from index 0 and nothing compares greater than a NaN there, so such a row gives 0.
-__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int64_t n,
-                                                     int *__restrict__ out) {
-  __shared__ float sv[256];
-  __shared__ int si[256];
-  const float *l = logits + (int64_t)blockIdx.x * n;
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-    const float v = l[i];
-    if (v > bv) {  // strictly greater: a thread keeps its first maximum
-      bv = v;
-      bi = (int)i;
-    }
-  }
+// Two launches for long rows: workgroup b of a row reduces the contiguous range
+// [b*len, (b+1)*len) to (largest value, its first index); the second launch reduces the ranges
+// in order. Ties go to the lower index at every step, so the result is the first maximum.
+__device__ __forceinline__ void argmax_block(float bv, int bi, float *sv, int *si) {
   sv[threadIdx.x] = bv;
   si[threadIdx.x] = bi;
   __syncthreads();
@@ -388,7 +378,50 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ l
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) out[blockIdx.x] = (si[0] == 0x7fffffff || l[0] != l[0]) ? 0 : si[0];
+}
+
+__global__ __launch_bounds__(256) void argmax_part_kernel(const float *__restrict__ logits, int64_t n, int64_t len,
+                                                          float *__restrict__ pv, int *__restrict__ pi) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int64_t row = blockIdx.y, lo = (int64_t)blockIdx.x * len;
+  const int64_t hi = lo + len < n ? lo + len : n;
+  const float *l = logits + row * n;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+    const float v = l[i];
+    if (v > bv) {  // strictly greater: a thread keeps its first maximum
+      bv = v;
+      bi = (int)i;
+    }
+  }
+  argmax_block(bv, bi, sv, si);
+  if (threadIdx.x == 0) {
+    pv[row * gridDim.x + blockIdx.x] = sv[0];
+    pi[row * gridDim.x + blockIdx.x] = si[0];
+  }
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float *__restrict__ logits, int64_t n, int parts,
+                                                           const float *__restrict__ pv, const int *__restrict__ pi,
+                                                           int *__restrict__ out) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int64_t row = blockIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int p = threadIdx.x; p < parts; p += blockDim.x) {
+    const float v = pv[row * parts + p];
+    const int i = pi[row * parts + p];
+    if (v > bv || (v == bv && i < bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  argmax_block(bv, bi, sv, si);
+  const float l0 = logits[row * n];
+  if (threadIdx.x == 0) out[row] = (si[0] == 0x7fffffff || l0 != l0) ? 0 : si[0];
 }
 
 // AddBias (src/Transformer.cs:433-443): y[t][i] += b[i].
@@ -505,9 +538,21 @@ hipError_t residual_launch(float *x, const float *o, int64_t n, float rs, hipStr
   return hipGetLastError();
 }
 
-hipError_t argmax_launch(const float *logits, int rows, int64_t n, int *out, hipStream_t st) {
+int argmax_parts(int64_t n) {
+  int64_t p = (n + 2047) / 2048;  // at least 2048 values per workgroup
+  return (int)(p < 1 ? 1 : p > 64 ? 64 : p);
+}
+
+hipError_t argmax_launch(const float *logits, int rows, int64_t n, int *out, float *scratch, hipStream_t st) {
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, st, logits, n, out);
+  const int parts = argmax_parts(n);
+  const int64_t len = (n + parts - 1) / parts;
+  float *pv = scratch;
+  int *pi = reinterpret_cast<int *>(scratch + (int64_t)rows * parts);
+  hipLaunchKernelGGL(argmax_part_kernel, dim3(parts, rows), dim3(256), 0, st, logits, n, len, pv, pi);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(256), 0, st, logits, n, parts, pv, pi, out);
   return hipGetLastError();
 }
 
