@@ -57,6 +57,37 @@ __global__ __launch_bounds__(1024) void rms_norm_kernel(const float *x, int64_t 
   const bool vec = (dim & 3) == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0 &&
                    ((uintptr_t)w & 15) == 0;
   double s = 0.0;
+  if (vec && dim <= (int64_t)blockDim.x * 8) {
+    // at most two float4 per thread: x and w both loaded before the reduction, one round trip
+    const int64_t i0 = (int64_t)threadIdx.x * 4, i1 = i0 + (int64_t)blockDim.x * 4;
+    float4 xa = make_float4(0.f, 0.f, 0.f, 0.f), xb = xa, wa = xa, wb = xa;
+    if (i0 < dim) {
+      xa = *reinterpret_cast<const float4 *>(xr + i0);
+      wa = *reinterpret_cast<const float4 *>(w + i0);
+    }
+    if (i1 < dim) {
+      xb = *reinterpret_cast<const float4 *>(xr + i1);
+      wb = *reinterpret_cast<const float4 *>(w + i1);
+    }
+    s += (double)xa.x * (double)xa.x;
+    s += (double)xa.y * (double)xa.y;
+    s += (double)xa.z * (double)xa.z;
+    s += (double)xa.w * (double)xa.w;
+    s += (double)xb.x * (double)xb.x;
+    s += (double)xb.y * (double)xb.y;
+    s += (double)xb.z * (double)xb.z;
+    s += (double)xb.w * (double)xb.w;
+    s = block_sum_d(s, sh);
+    const float mean = (float)(s / (double)dim);
+    const float scale = 1.0f / (float)sqrt((double)(mean + eps));
+    if (i0 < dim)
+      *reinterpret_cast<float4 *>(yr + i0) =
+          make_float4(xa.x * scale * wa.x, xa.y * scale * wa.y, xa.z * scale * wa.z, xa.w * scale * wa.w);
+    if (i1 < dim)
+      *reinterpret_cast<float4 *>(yr + i1) =
+          make_float4(xb.x * scale * wb.x, xb.y * scale * wb.y, xb.z * scale * wb.z, xb.w * scale * wb.w);
+    return;
+  }
   if (vec) {
     for (int64_t i = (int64_t)threadIdx.x * 4; i < dim; i += (int64_t)blockDim.x * 4) {
       const float4 v = *reinterpret_cast<const float4 *>(xr + i);
