@@ -336,7 +336,8 @@ __global__ __launch_bounds__(256) void attention_chunk_kernel(const float *__res
     const float inv = (float)(1.0 / sum);
     for (int dd = tid; dd < HD; dd += 256) {
       float o = 0.f;
-      for (int j = 0; j < cnt; j++) {
+#pragma unroll 8
+      for (int j = 0; j < cnt; j++) {  // unrolled: eight positions' LDS reads in flight
         const float p = es[j] * inv;
         o += p * h2f(vs[j * HD + dd]);
       }
@@ -348,6 +349,7 @@ __global__ __launch_bounds__(256) void attention_chunk_kernel(const float *__res
   float *rec = part + (((int64_t)t * heads + h) * max_chunks + c) * (HD + 4);
   for (int dd = tid; dd < HD; dd += 256) {
     float o = 0.f;
+#pragma unroll 8
     for (int j = 0; j < cnt; j++) o += es[j] * h2f(vs[j * HD + dd]);
     rec[dd] = o;
   }
