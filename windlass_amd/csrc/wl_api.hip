@@ -888,16 +888,50 @@ extern "C" int wl_argmax_dev(wl_ctx *c, const float *d_logits, int32_t rows, int
   return WL_OK;
 }
 
+// Two host int32 arrays of n values each (the second may be null) copied to S_ROWS on the
+// context's stream through the pinned ring: the host may reuse its arrays on return and queue
+// ahead; a ring entry is rewritten only after its copy has run.
+static int stage_rows(wl_ctx *c, const int32_t *a, const int32_t *b, int n, int32_t **d_rows) {
+  const int words = b ? 2 * n : n;
+  int rc;
+  if ((rc = ensure(c, S_ROWS, (size_t)words * sizeof(int32_t)))) return rc;
+  int32_t *rows = (int32_t *)c->buf[S_ROWS];
+  if ((size_t)words > c->rows_ints) {  // grow the pinned ring (after every queued copy from it)
+    WL_HIP(hipStreamSynchronize(c->stream), "row staging");
+    if (c->rows_host) hipHostFree(c->rows_host);
+    c->rows_host = nullptr;
+    c->rows_ints = 0;
+    const size_t ints = (size_t)words < 1024 ? 1024 : (size_t)words;
+    WL_HIP(hipHostMalloc((void **)&c->rows_host, ints * wl_ctx::kRowRing * sizeof(int32_t), hipHostMallocDefault),
+           "row staging");
+    c->rows_ints = ints;
+    for (bool &u : c->rows_used) u = false;
+  }
+  const int e = c->rows_next;
+  c->rows_next = (e + 1) % wl_ctx::kRowRing;
+  if (!c->rows_ev[e]) WL_HIP(hipEventCreateWithFlags(&c->rows_ev[e], hipEventDisableTiming), "row staging");
+  if (c->rows_used[e]) WL_HIP(hipEventSynchronize(c->rows_ev[e]), "row staging");
+  int32_t *stage = c->rows_host + (size_t)e * c->rows_ints;
+  memcpy(stage, a, (size_t)n * sizeof(int32_t));
+  if (b) memcpy(stage + n, b, (size_t)n * sizeof(int32_t));
+  WL_HIP(hipMemcpyAsync(rows, stage, (size_t)words * sizeof(int32_t), hipMemcpyHostToDevice, c->stream), "row copy");
+  WL_HIP(hipEventRecord(c->rows_ev[e], c->stream), "row staging");
+  c->rows_used[e] = true;
+  *d_rows = rows;
+  return WL_OK;
+}
+
 extern "C" int wl_embed_dev(wl_ctx *c, const wl_weight *embd, const int32_t *tokens, int32_t T, float *d_x) {
   if (!c || !embd || !tokens || !d_x) return fail(WL_E_ARG, "wl_embed_dev: null argument");
-  for (int t = 0; t < T; t++) {
+  if (T < 0) return fail(WL_E_SHAPE, "wl_embed_dev: T = %d", T);
+  for (int t = 0; t < T; t++)
     if (tokens[t] < 0 || tokens[t] >= embd->rows * embd->experts)
       return fail(WL_E_ARG, "Token id %d is outside the vocabulary.", tokens[t]);
-    WL_HIP(wl::dequant_launch(embd->type, embd->dev, embd->row_bytes, tokens[t], 1, embd->cols,
-                              d_x + (int64_t)t * embd->cols, c->stream),
-           "embedding row");
-  }
-  return WL_OK;
+  if (T == 0) return WL_OK;
+  int32_t *d_ids;  // the checked ids, staged to the device: every row in one launch
+  int rc = stage_rows(c, tokens, nullptr, T, &d_ids);
+  if (rc) return rc;
+  return wl_embed_dev_ids(c, embd, d_ids, T, d_x);
 }
 
 extern "C" int wl_embed_dev_ids(wl_ctx *c, const wl_weight *embd, const int32_t *d_tokens, int32_t T, float *d_x) {
@@ -1018,29 +1052,8 @@ extern "C" int wl_layer_batch_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x,
     if (pos[i] + 1 > max_n) max_n = pos[i] + 1;
   }
   int rc;
-  if ((rc = ensure(c, S_ROWS, (size_t)2 * N * sizeof(int32_t)))) return rc;
-  int32_t *rows = (int32_t *)c->buf[S_ROWS];
-  if ((size_t)2 * N > c->rows_ints) {  // grow the pinned ring (after every queued copy from it)
-    WL_HIP(hipStreamSynchronize(c->stream), "row staging");
-    if (c->rows_host) hipHostFree(c->rows_host);
-    c->rows_host = nullptr;
-    c->rows_ints = 0;
-    const size_t ints = (size_t)2 * N < 1024 ? 1024 : (size_t)2 * N;
-    WL_HIP(hipHostMalloc((void **)&c->rows_host, ints * wl_ctx::kRowRing * sizeof(int32_t), hipHostMallocDefault),
-           "row staging");
-    c->rows_ints = ints;
-    for (bool &u : c->rows_used) u = false;
-  }
-  const int e = c->rows_next;
-  c->rows_next = (e + 1) % wl_ctx::kRowRing;
-  if (!c->rows_ev[e]) WL_HIP(hipEventCreateWithFlags(&c->rows_ev[e], hipEventDisableTiming), "row staging");
-  if (c->rows_used[e]) WL_HIP(hipEventSynchronize(c->rows_ev[e]), "row staging");
-  int32_t *stage = c->rows_host + (size_t)e * c->rows_ints;
-  memcpy(stage, pos, (size_t)N * sizeof(int32_t));
-  memcpy(stage + N, slot, (size_t)N * sizeof(int32_t));
-  WL_HIP(hipMemcpyAsync(rows, stage, (size_t)2 * N * sizeof(int32_t), hipMemcpyHostToDevice, c->stream), "row copy");
-  WL_HIP(hipEventRecord(c->rows_ev[e], c->stream), "row staging");
-  c->rows_used[e] = true;
+  int32_t *rows;
+  if ((rc = stage_rows(c, pos, slot, N, &rows))) return rc;
   wl::RowMap rm;
   rm.pos = rows;
   rm.slot = rows + N;
