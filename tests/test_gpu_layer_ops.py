@@ -305,3 +305,17 @@ def test_matmul_add_equals_matmul_then_residual(ctx, t, rows, cols, T):
         check(L.wl_residual_dev(ctx.handle, P(yb), P(o), T * rows, ctypes.c_float(rs)))
         assert np.array_equal(host(ctx, ya).view(np.uint32), host(ctx, yb).view(np.uint32)), rs
     w.free()
+
+
+@pytest.mark.parametrize("t", [GgmlType.F32, GgmlType.F16, GgmlType.BF16])
+def test_float_rows_must_be_runs_of_32(ctx, t):
+    """One-value blocks in GGUF, runs of 32 in the kernels: a 100-value row is refused
+    (NotSupportedException) instead of being cut short."""
+    from windlass_amd._lib import NotSupportedError
+    bb = 4 if t == GgmlType.F32 else 2
+    with pytest.raises(NotSupportedError):
+        ctx.upload(t, np.zeros(2 * 100 * bb, np.uint8), 2, 100)
+    st = ctx.stage(4096)
+    with pytest.raises(NotSupportedError):
+        st.weight(0, t, 2, 100)
+    st.free()

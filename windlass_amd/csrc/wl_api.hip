@@ -210,6 +210,15 @@ extern "C" int wl_sync(wl_ctx *c) {
   return WL_OK;
 }
 
+// F32, F16 and BF16 rows have one-value blocks in GGUF, but the GPU kernels read them in runs
+// of 32 values: other lengths are refused rather than cut short.
+static int float_rows_ok(int type, int64_t cols, const char *who) {
+  if ((type == 0 || type == 1 || type == 30) && cols % 32)
+    return fail(WL_E_UNSUPPORTED, "%s: %s rows of %lld values are not whole runs of 32 for the GPU kernels", who,
+                type_name(type), (long long)cols);
+  return WL_OK;
+}
+
 extern "C" int wl_upload(wl_ctx *c, int type, const void *blocks, int64_t rows, int64_t cols, int64_t row_bytes,
                          int32_t experts, wl_weight **out) {
   if (!c || !out || !blocks) return fail(WL_E_ARG, "wl_upload: null argument");
@@ -224,6 +233,7 @@ extern "C" int wl_upload(wl_ctx *c, int type, const void *blocks, int64_t rows, 
     return fail(WL_E_SHAPE, "row_bytes %lld does not match %lld %s values (%lld)", (long long)row_bytes,
                 (long long)cols, type_name(type), (long long)(cols / be * bb));
   if (cols > (1 << 30) || rows > (1 << 30)) return fail(WL_E_SHAPE, "wl_upload: dimension too large");
+  if (int rc = float_rows_ok(type, cols, "wl_upload")) return rc;
   WL_HIP(hipSetDevice(c->device), "hipSetDevice");
   wl_weight *w = new wl_weight();
   w->type = type;
@@ -360,6 +370,7 @@ extern "C" int wl_stage_weight(wl_ctx *c, wl_stage *s, int64_t offset, int type,
     return fail(WL_E_SHAPE, "row_bytes %lld does not match %lld %s values (%lld)", (long long)row_bytes,
                 (long long)cols, type_name(type), (long long)(cols / be * bb));
   if (cols > (1 << 30) || rows > (1 << 30)) return fail(WL_E_SHAPE, "wl_stage_weight: dimension too large");
+  if (int rc = float_rows_ok(type, cols, "wl_stage_weight")) return rc;
   const size_t bytes = (size_t)rows * (size_t)experts * (size_t)row_bytes;
   // LayerStream lays tensors out at 64-byte aligned offsets (src/LayerStream.cs:64,195-201)
   if (offset < 0 || offset % 64 || (size_t)offset + bytes > s->bytes)
