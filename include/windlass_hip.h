@@ -269,7 +269,9 @@ typedef struct wl_layer_desc {
 /* Transformer.Layer (src/Transformer.cs:177-232) for T tokens at positions pos0.. of one
  * sequence: x [T][embd] (device) is updated in place and the tokens' keys and values go to
  * rows pos0.. of the fp16 caches d_K / d_V [positions][kv_heads * head_dim]. Every activation
- * stays in HBM (the context's scratch); stream-ordered, no host wait. */
+ * stays in HBM (the context's scratch); stream-ordered, no host wait. Up to 8 tokens the
+ * products are the decode GEMVs (o and down add into x in their own store); more tokens take
+ * the GEMMs. The caches must hold pos0 + T positions: the library cannot check their size. */
 int wl_layer_dev(wl_ctx *ctx, const wl_layer_desc *layer, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
                  uint16_t *d_V);
 
