@@ -48,6 +48,8 @@ extern "C" {
 #define WL_TYPE_Q6_K 14
 #define WL_TYPE_IQ2_XXS 16
 #define WL_TYPE_IQ4_NL 20
+#define WL_TYPE_IQ3_S 21
+#define WL_TYPE_IQ2_S 22
 #define WL_TYPE_IQ4_XS 23
 #define WL_TYPE_BF16 30
 

@@ -15,13 +15,15 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 = 0, 1, 2, 3, 6, 7, 8
 Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 10, 11, 12, 13, 14
-IQ2_XXS, IQ4_NL, IQ4_XS, BF16 = 16, 20, 23, 30
+IQ2_XXS, IQ4_NL, IQ3_S, IQ2_S, IQ4_XS, BF16 = 16, 20, 21, 22, 23, 30
 LAYOUT = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22),
           Q5_1: (32, 24), Q8_0: (32, 34), Q2_K: (256, 84), Q3_K: (256, 110), Q4_K: (256, 144),
-          Q5_K: (256, 176), Q6_K: (256, 210), IQ2_XXS: (256, 66), IQ4_NL: (32, 18), IQ4_XS: (256, 136)}
+          Q5_K: (256, 176), Q6_K: (256, 210), IQ2_XXS: (256, 66), IQ4_NL: (32, 18), IQ4_XS: (256, 136),
+          IQ3_S: (256, 110), IQ2_S: (256, 82)}
 NAMES = {F32: "f32", F16: "f16", BF16: "bf16", Q4_0: "q4_0", Q4_1: "q4_1", Q5_0: "q5_0",
          Q5_1: "q5_1", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K",
-         Q6_K: "q6_K", IQ2_XXS: "iq2_xxs", IQ4_NL: "iq4_nl", IQ4_XS: "iq4_xs"}
+         Q6_K: "q6_K", IQ2_XXS: "iq2_xxs", IQ4_NL: "iq4_nl", IQ4_XS: "iq4_xs",
+         IQ3_S: "iq3_s", IQ2_S: "iq2_s"}
 
 _lib = None
 
@@ -62,6 +64,8 @@ def lib():
         L.wlo_quantize_row.argtypes = [P, I, I, P, P, P]
         L.wlo_int_dot.argtypes = [I, P, P, P, P, I, P]
         L.wlo_iq2xxs_grid.restype = ctypes.POINTER(ctypes.c_uint64)
+        L.wlo_iq2s_grid.restype = ctypes.POINTER(ctypes.c_uint64)
+        L.wlo_iq3s_grid.restype = ctypes.POINTER(ctypes.c_uint32)
         L.wlo_ksigns_iq2xs.restype = ctypes.POINTER(ctypes.c_uint8)
         L.wlo_kvalues_iq4nl.restype = ctypes.POINTER(ctypes.c_int8)
         _lib = L
@@ -226,6 +230,14 @@ def int_dot(t, row, q, d, bsums):
 def iq2xxs_grid():
     p = lib().wlo_iq2xxs_grid()
     return np.ctypeslib.as_array(p, shape=(256,)).copy()
+
+
+def iq2s_grid():
+    return np.ctypeslib.as_array(lib().wlo_iq2s_grid(), shape=(1024,)).copy()
+
+
+def iq3s_grid():
+    return np.ctypeslib.as_array(lib().wlo_iq3s_grid(), shape=(512,)).copy()
 
 
 def ksigns():

@@ -22,7 +22,7 @@ extern "C" {
 enum {
     WLO_F32 = 0, WLO_F16 = 1, WLO_Q4_0 = 2, WLO_Q4_1 = 3, WLO_Q5_0 = 6, WLO_Q5_1 = 7,
     WLO_Q8_0 = 8, WLO_Q2_K = 10, WLO_Q3_K = 11, WLO_Q4_K = 12, WLO_Q5_K = 13, WLO_Q6_K = 14,
-    WLO_IQ2_XXS = 16, WLO_IQ4_NL = 20, WLO_IQ4_XS = 23, WLO_BF16 = 30
+    WLO_IQ2_XXS = 16, WLO_IQ4_NL = 20, WLO_IQ3_S = 21, WLO_IQ2_S = 22, WLO_IQ4_XS = 23, WLO_BF16 = 30
 };
 
 /* fp16 -> fp32, exact incl. subnormals, Inf and NaN payloads (src/Half.cs:59-90). */
@@ -93,6 +93,8 @@ int wlo_int_dot(int type, const uint8_t *b, const int8_t *q, const float *d,
 
 /* Table data of src/IqTables.cs:9-57 (kmask, ksigns, kvalues, iq2xxs grid). */
 const uint64_t *wlo_iq2xxs_grid(void);
+const uint64_t *wlo_iq2s_grid(void);
+const uint32_t *wlo_iq3s_grid(void);
 const uint8_t *wlo_ksigns_iq2xs(void);
 const int8_t *wlo_kvalues_iq4nl(void);
 

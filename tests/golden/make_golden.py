@@ -68,14 +68,19 @@ def tables():
         "iq2xxs_grid_spots": {"0": "0x0808080808080808", "1": "0x080808080808082b",
                               "3": "0x0808080808082b08"},
         "iq2xxs_grid_bytes": [8, 0x19, 0x2B],
+        # tests/IQuantTests.cs:263,276,278 (the iq2s and iq3s grids' hashes and iq3s's ends)
+        "iq2s_grid_fnv1a64": "0x123edd38a3b62b90",
+        "iq3s_grid_fnv1a64": "0xfa37020c25b44829",
+        "iq3s_grid_spots": {"0": "0x01010101", "1": "0x01010103", "511": "0x0f0f0101"},
         "ids": {"f32": 0, "f16": 1, "q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q8_0": 8, "q2_K": 10,
-                "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14, "iq2_xxs": 16, "iq4_nl": 20, "iq4_xs": 23,
-                "bf16": 30},
+                "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14, "iq2_xxs": 16, "iq4_nl": 20, "iq3_s": 21,
+                "iq2_s": 22, "iq4_xs": 23, "bf16": 30},
         "layouts": {"q4_0": [32, 18], "q4_1": [32, 20], "q5_0": [32, 22], "q5_1": [32, 24],
                     "q8_0": [32, 34], "q2_K": [256, 84], "q3_K": [256, 110], "q4_K": [256, 144],
                     "q5_K": [256, 176], "q6_K": [256, 210], "iq2_xxs": [256, 66], "iq4_nl": [32, 18],
-                    "iq4_xs": [256, 136], "f32": [1, 4], "f16": [1, 2], "bf16": [1, 2]},
-        "layout_source": "src/Gguf.cs:30-66; tests/IQuantTests.cs:375-380",
+                    "iq4_xs": [256, 136], "f32": [1, 4], "f16": [1, 2], "bf16": [1, 2], "iq3_s": [256, 110],
+                    "iq2_s": [256, 82]},
+        "layout_source": "src/Gguf.cs:30-66; tests/IQuantTests.cs:75-82,375-380",
     }
 
 

@@ -8,7 +8,7 @@ from windlass_amd.backend import GgmlType
 QTYPES = [GgmlType.Q8_0, GgmlType.Q4_K, GgmlType.Q6_K, GgmlType.IQ4_XS, GgmlType.IQ2_XXS]
 # the formats added after the five of the benchmark configurations
 NEWQ = [GgmlType.Q4_0, GgmlType.Q4_1, GgmlType.Q5_0, GgmlType.Q5_1, GgmlType.Q2_K, GgmlType.Q3_K,
-        GgmlType.Q5_K, GgmlType.IQ4_NL]
+        GgmlType.Q5_K, GgmlType.IQ4_NL, GgmlType.IQ3_S, GgmlType.IQ2_S]
 FLOATS = [GgmlType.F32, GgmlType.F16, GgmlType.BF16]
 ALLQ = QTYPES + NEWQ
 NAME = {t: t.name for t in GgmlType}

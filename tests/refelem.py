@@ -188,8 +188,41 @@ def iq4_nl(b, o, e, exact):
     return np.float32(d) * np.float32(kv) if exact else d * kv
 
 
+def iq3_s(b, o, e, exact, grid):
+    """tests/IQuantTests.cs:126-137: sub = 32-value sub-block, l = group of 8 in it; grid
+    index = qs byte 2l (+1 for values 4-7) with bit k of qh[sub] as bit 8; sign byte l."""
+    sub, l, within = e // 32, (e % 32) // 8, e % 8
+    d = fp16(u16(b, o))
+    k = 2 * l + (0 if within < 4 else 1)
+    gi = b[o + 2 + sub * 8 + k] | (((b[o + 66 + sub] >> k) & 1) << 8)
+    gv = (int(grid[gi]) >> (8 * (within % 4))) & 0xFF
+    sign = -1.0 if b[o + 74 + sub * 4 + l] & (1 << within) else 1.0
+    sc = b[o + 106 + sub // 2]
+    nib = sc & 15 if sub % 2 == 0 else sc >> 4
+    if exact:
+        return np.float32(np.float32(d) * np.float32(1 + 2 * nib)) * np.float32(gv) * np.float32(sign)
+    return d * (1 + 2 * nib) * gv * sign
+
+
+def iq2_s(b, o, e, exact, grid):
+    """tests/IQuantTests.cs:156-166: grid index = qs byte of the group plus bits 2l..2l+1 of
+    qh[sub]; the sign bytes follow the 32 grid bytes; two scale nibbles per sub-block."""
+    sub, group, l, within = e // 32, e // 8, (e % 32) // 8, e % 8
+    d = fp16(u16(b, o))
+    gi = b[o + 2 + group] | (((b[o + 66 + sub] >> (2 * l)) & 3) << 8)
+    gv = (int(grid[gi]) >> (8 * within)) & 0xFF
+    sign = -1.0 if b[o + 34 + group] & (1 << within) else 1.0
+    sc = b[o + 74 + sub]
+    nib = sc & 15 if l < 2 else sc >> 4
+    if exact:
+        db = np.float32(np.float32(np.float32(d) * (np.float32(0.5) + np.float32(nib))) * np.float32(0.25))
+        return np.float32(db * np.float32(gv)) * np.float32(sign)
+    return d * (0.5 + nib) * 0.25 * gv * sign
+
+
 LAYOUT = {2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34), 10: (256, 84), 11: (256, 110),
-          12: (256, 144), 13: (256, 176), 14: (256, 210), 16: (256, 66), 20: (32, 18), 23: (256, 136)}
+          12: (256, 144), 13: (256, 176), 14: (256, 210), 16: (256, 66), 20: (32, 18), 23: (256, 136),
+          21: (256, 110), 22: (256, 82)}
 
 
 def decode_blocks(t, data, nblocks, exact, grid=None):
@@ -203,6 +236,8 @@ def decode_blocks(t, data, nblocks, exact, grid=None):
         for e in range(be):
             if t == 16:
                 v = iq2_xxs(data, k * bb, e, exact, grid)
+            elif t in (21, 22):
+                v = (iq3_s if t == 21 else iq2_s)(data, k * bb, e, exact, grid)
             else:
                 v = fn[t](data, k * bb, e, exact)
             out[k * be + e] = v

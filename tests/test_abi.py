@@ -79,14 +79,14 @@ def test_type_queries_match_reference_layouts():
     # src/Gguf.cs:30-66
     want = {0: (1, 4), 1: (1, 2), 30: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24),
             8: (32, 34), 10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210),
-            16: (256, 66), 20: (32, 18), 23: (256, 136)}
+            16: (256, 66), 20: (32, 18), 21: (256, 110), 22: (256, 82), 23: (256, 136)}
     for t, lay in want.items():
         assert windlass_amd.layout(t) == lay
         assert L.wl_can_decode(t) == 1
     for t in want:
         assert L.wl_can_matmul(t) == 1
     # Q8_1, Q8_K (activation formats) and the I-quants whose grids have no source here
-    for t in (9, 15, 17, 18, 19, 21, 22, 29):
+    for t in (9, 15, 17, 18, 19, 29):
         assert L.wl_can_decode(t) == 0 and L.wl_can_matmul(t) == 0
     assert windlass_amd.Quants.CanDecode(windlass_amd.GgmlType.Q4_K)
     assert L.wl_version() >= 100

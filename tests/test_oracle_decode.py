@@ -21,11 +21,13 @@ import refelem
 
 PINS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_pins.json")))
 TYPES = [oracle.Q4_0, oracle.Q4_1, oracle.Q5_0, oracle.Q5_1, oracle.Q8_0, oracle.Q2_K, oracle.Q3_K,
-         oracle.Q4_K, oracle.Q5_K, oracle.Q6_K, oracle.IQ4_NL, oracle.IQ4_XS, oracle.IQ2_XXS]
+         oracle.Q4_K, oracle.Q5_K, oracle.Q6_K, oracle.IQ4_NL, oracle.IQ4_XS, oracle.IQ2_XXS, oracle.IQ3_S,
+         oracle.IQ2_S]
 DBITS = [0x3A00, 0x3E00, 0x3800, 0xB400, 0x3C00]    # 0.75, 1.5, 0.5, -0.25, 1 (exact halves)
 D_FIELDS = {oracle.Q4_0: [0], oracle.Q4_1: [0, 2], oracle.Q5_0: [0], oracle.Q5_1: [0, 2], oracle.Q8_0: [0],
             oracle.Q2_K: [80, 82], oracle.Q3_K: [108], oracle.Q4_K: [0, 2], oracle.Q5_K: [0, 2],
-            oracle.Q6_K: [208], oracle.IQ4_NL: [0], oracle.IQ4_XS: [0], oracle.IQ2_XXS: [0]}
+            oracle.Q6_K: [208], oracle.IQ4_NL: [0], oracle.IQ4_XS: [0], oracle.IQ2_XXS: [0], oracle.IQ3_S: [0],
+            oracle.IQ2_S: [0]}
 
 
 def random_blocks(t, nblocks, seed, dbits=None):
@@ -43,8 +45,9 @@ def random_blocks(t, nblocks, seed, dbits=None):
     return data
 
 
-def grid():
-    return oracle.iq2xxs_grid()
+def grid(t=None):
+    """The codebook the type's decode indexes (pinned by test_oracle_tables)."""
+    return {oracle.IQ3_S: oracle.iq3s_grid, oracle.IQ2_S: oracle.iq2s_grid}.get(t, oracle.iq2xxs_grid)()
 
 
 def test_iq2xxs_hand_block():
@@ -177,7 +180,7 @@ def test_random_blocks_exact_scales(t, seed):
     nb = 16 if be == 32 else 5
     data = random_blocks(t, nb, seed, DBITS)
     got = oracle.decode(t, data, nb * be)
-    want = refelem.decode_blocks(t, data, nb, exact=False, grid=grid())
+    want = refelem.decode_blocks(t, data, nb, exact=False, grid=grid(t))
     assert np.array_equal(got.astype(np.float64), want)
 
 
@@ -187,9 +190,9 @@ def test_random_blocks_random_scales(t):
     nb = 24 if be == 32 else 6
     data = random_blocks(t, nb, 77)
     got = oracle.decode(t, data, nb * be)
-    want32 = refelem.decode_blocks(t, data, nb, exact=True, grid=grid())
+    want32 = refelem.decode_blocks(t, data, nb, exact=True, grid=grid(t))
     assert np.array_equal(got.view(np.uint32), want32.view(np.uint32))
-    want64 = refelem.decode_blocks(t, data, nb, exact=False, grid=grid())
+    want64 = refelem.decode_blocks(t, data, nb, exact=False, grid=grid(t))
     assert np.all(np.abs(got - want64) <= 2e-6 * np.abs(want64) + 1e-9)
 
 
@@ -203,7 +206,7 @@ def test_fills(t, fill):
             data[k * bb + f] = h & 0xFF
             data[k * bb + f + 1] = h >> 8
     got = oracle.decode(t, data, 2 * be)
-    want = refelem.decode_blocks(t, data, 2, exact=False, grid=grid())
+    want = refelem.decode_blocks(t, data, 2, exact=False, grid=grid(t))
     assert np.array_equal(got.astype(np.float64), want)
 
 

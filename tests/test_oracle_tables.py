@@ -32,6 +32,30 @@ def test_iq2xxs_grid_hash_spots_and_bytes():
     assert len(set(int(g) for g in grid)) == 256
 
 
+def _fnv1a64_bytes(words, nbytes):
+    h = 0xcbf29ce484222325
+    for w in words:
+        for j in range(nbytes):
+            h ^= (int(w) >> (8 * j)) & 0xFF
+            h = (h * 0x100000001b3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def test_iq2s_and_iq3s_grids():
+    """The reference test's hashes of Iq2sGrid and Iq3sGrid (tests/IQuantTests.cs:263,276,278)
+    and Iq3sGrid's end entries; every byte in the grids' byte sets."""
+    t = PINS["tables"]
+    g2, g3 = oracle.iq2s_grid(), oracle.iq3s_grid()
+    assert g2.size == 1024 and g3.size == 512
+    assert _fnv1a64_bytes(g2, 8) == int(t["iq2s_grid_fnv1a64"], 16)
+    assert _fnv1a64_bytes(g3, 4) == int(t["iq3s_grid_fnv1a64"], 16)
+    for i, v in t["iq3s_grid_spots"].items():
+        assert int(g3[int(i)]) == int(v, 16)
+    assert all({(int(g) >> (8 * j)) & 0xFF for j in range(8)} <= {8, 0x19, 0x2B} for g in g2)
+    assert all({(int(g) >> (8 * j)) & 0xFF for j in range(4)} <= set(range(1, 16, 2)) for g in g3)
+    assert len(set(int(g) for g in g2)) == 1024 and len(set(int(g) for g in g3)) == 512
+
+
 def test_ksigns_parity_and_kvalues():
     ks = oracle.ksigns()
     for i in range(128):
@@ -48,7 +72,7 @@ def test_layouts():
         assert oracle.LAYOUT[tid] == (be, bb)
         assert oracle.lib().wlo_can_decode(tid) == 1
     # types outside this path are refused (src/Quants.cs:51)
-    for tid in (9, 15, 17, 18, 19, 21, 22, 29):
+    for tid in (9, 15, 17, 18, 19, 29):
         assert oracle.lib().wlo_can_decode(tid) == 0
         x = np.zeros(256, np.float32)
         try:

@@ -28,6 +28,8 @@ class GgmlType(IntEnum):
     Q6_K = 14
     IQ2_XXS = 16
     IQ4_NL = 20
+    IQ3_S = 21
+    IQ2_S = 22
     IQ4_XS = 23
     BF16 = 30
 

@@ -108,6 +108,8 @@ static const char *type_name(int t) {
     case WL_TYPE_Q6_K: return "q6_K";
     case WL_TYPE_IQ2_XXS: return "iq2_xxs";
     case WL_TYPE_IQ4_NL: return "iq4_nl";
+    case WL_TYPE_IQ3_S: return "iq3_s";
+    case WL_TYPE_IQ2_S: return "iq2_s";
     case WL_TYPE_IQ4_XS: return "iq4_xs";
   }
   return "type";
@@ -130,6 +132,8 @@ extern "C" int wl_type_layout(int t, int *be, int *bb) {
     case WL_TYPE_Q6_K: e = 256; b = 210; break;
     case WL_TYPE_IQ2_XXS: e = 256; b = 66; break;
     case WL_TYPE_IQ4_NL: e = 32; b = 18; break;
+    case WL_TYPE_IQ3_S: e = 256; b = 110; break;
+    case WL_TYPE_IQ2_S: e = 256; b = 82; break;
     case WL_TYPE_IQ4_XS: e = 256; b = 136; break;
   }
   if (be) *be = e;

@@ -101,6 +101,63 @@ struct BIQ4NL : BlkSmall {
   }
 };
 
+// ---------------------------------------------------------------- IQ3_S and IQ2_S
+// The 16 values at offset k of a block: 32-value sub-block sub = k / 32 and its 8-value groups
+// l = 2 * ((k % 32) / 16) and l + 1. Read byte by byte from the block (Raw keeps its address).
+struct BIqRaw {
+  struct Raw { const uint8_t *b; };
+  __device__ static void load(const uint8_t *blk, int, Raw &r) { r.b = blk; }
+};
+
+// IQ3_S (src/IQuants.cs:112-143): d, qs[64], qh[8], signs[32], scales[4]. y = db * grid byte *
+// sign with db = d * (1 + 2 * the sub-block's scale nibble); grid index = qs byte 2l (values
+// 0-3 of the group) or 2l + 1 (values 4-7) with bit 2l or 2l + 1 of qh[sub] as bit 8.
+struct BIQ3S : BIqRaw {
+  static constexpr int BLOCK = 256, BYTES = 110;
+  __device__ static void dec(const Raw &r, int k, float (&y)[16]) {
+    const uint8_t *b = r.b;
+    const int sub = k / 32, l0 = 2 * ((k % 32) / 16);
+    const float d = half_bits_exact((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+    const int sc = b[106 + sub / 2];
+    const float db = d * (float)(1 + 2 * ((sub & 1) ? sc >> 4 : sc & 0xF));
+    const int h = b[66 + sub];
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      const int l = l0 + g;
+      const int i1 = b[2 + 8 * sub + 2 * l] | ((h << (8 - 2 * l)) & 256);
+      const int i2 = b[2 + 8 * sub + 2 * l + 1] | ((h << (7 - 2 * l)) & 256);
+      const int sg = b[74 + 4 * sub + l];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        y[8 * g + j] = db * (float)iq3s_grid_byte(i1, j) * ((sg >> j) & 1 ? -1.0f : 1.0f);
+        y[8 * g + 4 + j] = db * (float)iq3s_grid_byte(i2, j) * ((sg >> (j + 4)) & 1 ? -1.0f : 1.0f);
+      }
+    }
+  }
+};
+
+// IQ2_S (src/IQuants.cs:199-222): d, qs[32] grid bytes, signs[32], qh[8], scales[8]. y = dl *
+// grid byte * sign, dl = d * (0.5 + nibble) * 0.25 (low nibble for groups 0-1, high for 2-3);
+// grid index = qs byte of the group with bits 2l..2l+1 of qh[sub] as bits 8-9.
+struct BIQ2S : BIqRaw {
+  static constexpr int BLOCK = 256, BYTES = 82;
+  __device__ static void dec(const Raw &r, int k, float (&y)[16]) {
+    const uint8_t *b = r.b;
+    const int sub = k / 32, l0 = 2 * ((k % 32) / 16);
+    const float d = half_bits_exact((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+    const int sc = b[74 + sub], h = b[66 + sub];
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      const int l = l0 + g;
+      const float dl = d * (0.5f + (float)(l < 2 ? sc & 0xF : sc >> 4)) * 0.25f;
+      const int gi = b[2 + 4 * sub + l] | ((h << (8 - 2 * l)) & 0x300);
+      const int sg = b[34 + 4 * sub + l];
+#pragma unroll
+      for (int j = 0; j < 8; j++) y[8 * g + j] = dl * (float)iq2s_grid_byte(gi, j) * ((sg >> j) & 1 ? -1.0f : 1.0f);
+    }
+  }
+};
+
 // ---------------------------------------------------------------- K-quants
 // The 16 values at offset k of a Q2_K/Q3_K block: 128-value half h = k / 128, 2-bit field
 // shift 2j with j = (k % 128) / 32, bytes l0 .. l0 + 15 of the half's 32 qs bytes

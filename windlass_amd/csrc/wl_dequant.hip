@@ -185,7 +185,7 @@ static hipError_t launch(const uint8_t *w, int64_t row_bytes, int64_t row0, int6
 bool dequant_supports(int type) {
   switch (type) {
     case 0: case 1: case 30: case 8: case 12: case 14: case 23: case 16:
-    case 2: case 3: case 6: case 7: case 10: case 11: case 13: case 20: return true;
+    case 2: case 3: case 6: case 7: case 10: case 11: case 13: case 20: case 21: case 22: return true;
   }
   return false;
 }
@@ -209,6 +209,8 @@ static hipError_t dequant_any(int type, const uint8_t *w, int64_t row_bytes, int
     case 11: return launch<DqBlk<BQ3K>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
     case 13: return launch<DqBlk<BQ5K>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
     case 20: return launch<DqBlk<BIQ4NL>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 21: return launch<DqBlk<BIQ3S>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
+    case 22: return launch<DqBlk<BIQ2S>>(w, row_bytes, row0, nrows, cols, dst, ids, tensor_rows, st);
   }
   return hipErrorInvalidValue;
 }

@@ -404,7 +404,7 @@ static hipError_t launch(const uint8_t *w, int64_t row_bytes, int rows, int cols
 bool gemm_supports(int type) {
   switch (type) {
     case 0: case 1: case 2: case 3: case 6: case 7: case 8: case 10: case 11: case 12: case 13: case 14: case 16:
-    case 20: case 23: case 30: return true;
+    case 20: case 21: case 22: case 23: case 30: return true;
   }
   return false;
 }
@@ -440,6 +440,8 @@ hipError_t gemm_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, 
     case 11: return launch<GBlk<BQ3K>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
     case 13: return launch<GBlk<BQ5K>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
     case 20: return launch<GBlk<BIQ4NL>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 21: return launch<GBlk<BIQ3S>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
+    case 22: return launch<GBlk<BIQ2S>>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
   }
   return hipErrorInvalidValue;
 }

@@ -14,7 +14,7 @@ from .backend import GgmlType, layout
 _SCALE_FIELDS = {GgmlType.Q4_0: (0,), GgmlType.Q4_1: (0, 2), GgmlType.Q5_0: (0,), GgmlType.Q5_1: (0, 2),
                  GgmlType.Q8_0: (0,), GgmlType.Q2_K: (80, 82), GgmlType.Q3_K: (108,), GgmlType.Q4_K: (0, 2),
                  GgmlType.Q5_K: (0, 2), GgmlType.Q6_K: (208,), GgmlType.IQ4_NL: (0,), GgmlType.IQ4_XS: (0,),
-                 GgmlType.IQ2_XXS: (0,)}
+                 GgmlType.IQ2_XXS: (0,), GgmlType.IQ3_S: (0,), GgmlType.IQ2_S: (0,)}
 
 
 def scale_fields(t):
