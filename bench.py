@@ -497,7 +497,8 @@ def run_decode_batch(args):
 
 # ggml type id -> name, for --formats
 FORMATS = {12: "q4_K", 13: "q5_K", 14: "q6_K", 10: "q2_K", 11: "q3_K", 2: "q4_0", 3: "q4_1", 6: "q5_0",
-           7: "q5_1", 8: "q8_0", 20: "iq4_nl", 23: "iq4_xs", 16: "iq2_xxs", 1: "f16", 30: "bf16", 0: "f32"}
+           7: "q5_1", 8: "q8_0", 20: "iq4_nl", 23: "iq4_xs", 16: "iq2_xxs", 21: "iq3_s", 22: "iq2_s", 1: "f16",
+           30: "bf16", 0: "f32"}
 
 
 def run_formats(args):
