@@ -46,7 +46,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--batch", type=int, default=1, help="tokens per step (1..8)")
+    ap.add_argument("--batch", type=int, default=1,
+                    help="tokens per step (1..8); with --decode, sequences decoding together (any N)")
     ap.add_argument("--copies", type=int, default=4, help="distinct layer copies to rotate")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
