@@ -221,3 +221,48 @@ def test_gpu_batch_step_rows_equal_single_sequences(gpu, key, n_seq):
                                        c(batch.K[0].data_ptr()), c(batch.V[0].data_ptr())))
     for w in weights.values():
         w.free()
+
+
+_LAYER_NAMES = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("slots", [1, 2])
+@pytest.mark.parametrize("key", [k for k in ("llama-q4_K", "llama-bf16", "qwen2-q6_K-tied", "qwen3-q4_K")
+                                 if k in SPECS])
+def test_gpu_streamed_layers_equal_resident(gpu, key, slots):
+    """LayerStream's streaming mode under the device forward (StageStream): every layer's
+    tensors copied from pinned host memory into HBM slots as the forward reaches them (one slot:
+    each copy waits for the previous layer's last reader; two: the copy of layer l + 1 beside
+    the compute of l) give the resident forward's logits bit for bit and its greedy tokens."""
+    from tiny_model import EMBD, EPS, HEADS, KV_HEADS, LAYERS, build
+    from windlass_amd import DeviceTransformer, ModelConfig, StageStream
+    want, want_logits = None, None
+    dm, weights = device_model(gpu, key)
+    want, want_logits = dm.greedy(PROBE, 6, chunk=8, keep_logits=True)
+    cfg = dm.cfg
+    for w in weights.values():
+        w.free()
+    arch, t = build(key)
+    layers = [{n: (t["blk.%d.%s" % (l, n)].type, t["blk.%d.%s" % (l, n)].rows, t["blk.%d.%s" % (l, n)].cols,
+                   t["blk.%d.%s" % (l, n)].data) for n in _LAYER_NAMES} for l in range(LAYERS)]
+    if any({n: v[:3] for n, v in lt.items()} != {n: v[:3] for n, v in layers[0].items()} for lt in layers):
+        pytest.skip("layers of different formats")
+    stream = StageStream(gpu, layers, slots)
+    dev = torch.device("cuda:0")
+    w2, vectors = dict(stream.weights()), {}
+    resident = []
+    for n, x in t.items():
+        if isinstance(x, np.ndarray):
+            vectors[n] = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev)
+        elif not n.startswith("blk.") and not (n == "output" and x is t["token_embd"]):
+            w2[n] = gpu.upload(x.type, x.data, x.rows, x.cols, name=n)
+            resident.append(w2[n])
+    ds = DeviceTransformer(gpu, cfg, w2, vectors, 64, stream=stream)
+    got, got_logits = ds.greedy(PROBE, 6, chunk=8, keep_logits=True)
+    stream.free()
+    for w in resident:
+        w.free()
+    assert got == want, (got, want)
+    for a, b in zip(got_logits, want_logits):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

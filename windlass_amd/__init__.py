@@ -30,8 +30,8 @@ from ._lib import (ArgumentOutOfRangeError, BackendError, NotSupportedError, Sha
                    library_path, load)
 from .backend import (Context, FastMath, GgmlType, HostBuffer, LayerDesc, QActs, Quants, Stage, Transformer,
                       WeightView, layout)
-from .model import DeviceBatch, DeviceTransformer, ModelConfig
+from .model import DeviceBatch, DeviceTransformer, ModelConfig, StageStream
 
 __all__ = ["ArgumentOutOfRangeError", "BackendError", "NotSupportedError", "ShapeError",
            "library_path", "load", "Context", "FastMath", "GgmlType", "HostBuffer", "LayerDesc", "QActs", "Quants", "Stage",
-           "Transformer", "WeightView", "layout", "DeviceBatch", "DeviceTransformer", "ModelConfig"]
+           "Transformer", "WeightView", "layout", "DeviceBatch", "DeviceTransformer", "ModelConfig", "StageStream"]

@@ -47,9 +47,12 @@ class DeviceTransformer:
     vectors: {name: device float32 tensor} with output_norm, blk.N.attn_norm, blk.N.ffn_norm and
     the optional blk.N.attn_{q,k,v}.bias, blk.N.attn_{q,k}_norm and rope_freqs."""
 
-    def __init__(self, ctx, cfg, weights, vectors, max_positions):
+    def __init__(self, ctx, cfg, weights, vectors, max_positions, stream=None):
+        """stream: a StageStream whose weights() the layer tensors of `weights` come from; the
+        forward then acquires and releases each layer's slot around its layer."""
         import torch
         self.ctx, self.cfg, self.L, self.torch = ctx, cfg, load(), torch
+        self.stream = stream
         self.w, self.v = weights, vectors
         self.embd_w = weights["token_embd"]
         self.head_w = weights.get("output", self.embd_w)
@@ -123,9 +126,15 @@ class DeviceTransformer:
 
     def _layers_and_head(self, x, T, pos0):
         L, h, c = self.L, self.ctx.handle, ctypes.c_void_p
+        if self.stream:
+            self.stream.begin()
         for l, d in enumerate(self.descs):
+            if self.stream:
+                self.stream.acquire(l)
             check(L.wl_layer_dev(h, ctypes.byref(d), c(x.data_ptr()), T, pos0, c(self.K[l].data_ptr()),
                                  c(self.V[l].data_ptr())))
+            if self.stream:
+                self.stream.release(l)
         self.length = pos0 + T
         # Head (src/Transformer.cs:112-125) of the last row
         check(L.wl_rms_norm_dev(h, c(x[T - 1:].data_ptr()), 1, self.cfg.embd, c(self.v["output_norm"].data_ptr()),
@@ -181,6 +190,64 @@ class DeviceTransformer:
     def host_logits(self):
         self.ctx.sync()
         return self.logits[0].cpu().numpy().astype(np.float32)
+
+
+class StageStream:
+    """LayerStream's streaming mode (src/LayerStream.cs:127-181) for DeviceTransformer: each
+    decoder layer's tensors in one pinned host buffer (a stage, tensors at 64-byte aligned
+    offsets as Bind lays them out), `slots` HBM slots; layer l runs from slot l % slots. begin()
+    queues the first layers; acquire(l) makes the compute stream wait for layer l's copy;
+    release(l) records the slot's last reader and queues the copy of layer l + slots into it,
+    which waits for that release. No host wait anywhere, so the copies overlap the compute of
+    the layers before them; one slot streams too (no lookahead)."""
+
+    def __init__(self, ctx, layers, slots=2):
+        """layers: one {name: (GgmlType, rows, cols, raw blocks)} per layer, the same names and
+        shapes in every layer."""
+        from .backend import HostBuffer, layout
+        self.ctx, self.n, self.S = ctx, len(layers), slots
+        self.offs, total = {}, 0
+        for name, (t, rows, cols, _) in layers[0].items():
+            be, bb = layout(t)
+            self.offs[name] = (total, t, rows, cols)
+            total = (total + rows * (cols // be) * bb + 63) // 64 * 64
+        self.host = []
+        for lt in layers:
+            hb = HostBuffer(total)
+            for name, (off, t, rows, cols) in self.offs.items():
+                data = np.ascontiguousarray(lt[name][3], np.uint8).reshape(-1)
+                hb.array[off:off + data.size] = data
+            self.host.append(hb)
+        self.slot = [ctx.stage(total) for _ in range(slots)]
+        self.views = [{name: s.weight(off, t, rows, cols, name=name) for name, (off, t, rows, cols) in self.offs.items()}
+                      for s in self.slot]
+
+    def weights(self):
+        """{blk.l.name: the view of slot l % slots} for DeviceTransformer."""
+        return {"blk.%d.%s" % (l, name): self.views[l % self.S][name] for l in range(self.n) for name in self.offs}
+
+    def begin(self):
+        for l in range(min(self.S, self.n)):
+            self.slot[l].upload_async(self.host[l].array, 0)
+
+    def acquire(self, l):
+        self.slot[l % self.S].ready()
+
+    def release(self, l):
+        s = self.slot[l % self.S]
+        s.release()
+        if l + self.S < self.n:
+            s.upload_async(self.host[l + self.S].array, 0)
+
+    def free(self):
+        self.ctx.sync()
+        for vs in self.views:
+            for v in vs.values():
+                v.free()
+        for s in self.slot:
+            s.free()
+        for hb in self.host:
+            hb.free()
 
 
 class DeviceBatch:
