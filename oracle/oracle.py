@@ -12,6 +12,12 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
+# The same source built -O3 -march=native (vectorised where the semantics allow): an upper bound
+# of what a compiler gets from this CPU code, built on the machine that runs it.
+NATIVE_PATH = os.path.join(HERE, "liboracle_native.so")
+# -O1 with AddressSanitizer and UBSan (make san), loaded only by the sanitizer test's child process.
+SAN_PATH = os.path.join(HERE, "liboracle_san.so")
+_PATHS = {"scalar": (LIB_PATH, "all"), "native": (NATIVE_PATH, "native"), "san": (SAN_PATH, "san")}
 
 F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 = 0, 1, 2, 3, 6, 7, 8
 Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 10, 11, 12, 13, 14
@@ -26,6 +32,7 @@ NAMES = {F32: "f32", F16: "f16", BF16: "bf16", Q4_0: "q4_0", Q4_1: "q4_1", Q5_0:
          IQ3_S: "iq3_s", IQ2_S: "iq2_s"}
 
 _lib = None
+_libs = {}
 
 
 def build():
@@ -33,12 +40,28 @@ def build():
     subprocess.run(["make", "-s", "-C", HERE], check=True)
 
 
+def use(kind):
+    """Route the module's functions to one build: "scalar" (-O2, the default), "native"
+    (-O3 -march=native, built on first use for the CPU this runs on) or "san" (sanitizers)."""
+    global _lib
+    path, target = _PATHS[kind]
+    if not os.path.exists(path):
+        subprocess.run(["make", "-s", "-C", HERE, target], check=True)
+    _lib = _open(path)
+
+
 def lib():
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             build()
-        L = ctypes.CDLL(LIB_PATH)
+        _lib = _open(LIB_PATH)
+    return _lib
+
+
+def _open(path):
+    if path not in _libs:
+        L = ctypes.CDLL(path)
         P, I, I64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
         U64P = ctypes.POINTER(ctypes.c_uint64)
         L.wlo_half_to_float.restype = F
@@ -68,8 +91,8 @@ def lib():
         L.wlo_iq3s_grid.restype = ctypes.POINTER(ctypes.c_uint32)
         L.wlo_ksigns_iq2xs.restype = ctypes.POINTER(ctypes.c_uint8)
         L.wlo_kvalues_iq4nl.restype = ctypes.POINTER(ctypes.c_int8)
-        _lib = L
-    return _lib
+        _libs[path] = L
+    return _libs[path]
 
 
 def _p(a):

@@ -899,6 +899,7 @@ int wlo_swiglu(int gtype, const uint8_t *gate, int64_t grb, int utype, const uin
  * the lower id, optional renormalisation clamped at the smallest fp16 normal. */
 void wlo_route(const float *logits, int n, int k, int renorm, int *sel, float *wts, int *count)
 {
+    if (n <= 0 || k <= 0 || k > n) return;
     float max = -INFINITY;
     for (int i = 0; i < n; i++) if (logits[i] > max) max = logits[i];
     float *p = (float *)malloc(sizeof(float) * (size_t)n);

@@ -134,18 +134,54 @@ def test_tiny_model_config(tmp_path, key):
 
 @pytest.mark.parametrize("md,err", [
     ([("general.architecture", STR, "gpt2")], "architecture"),
-    ([("general.architecture", STR, "qwen3moe"), ("qwen3moe.expert_count", U32, 8)], "experts"),
+    ([("general.architecture", STR, "qwen3moe"), ("qwen3moe.expert_count", U32, 8)], "expert"),
+    ([("general.architecture", STR, "llama"), ("llama.expert_count", U32, 8)], "expert"),
     ([("general.architecture", STR, "llama"), ("llama.embedding_length", U32, 64), ("llama.block_count", U32, 1),
-      ("llama.attention.head_count", U32, 6), ("llama.attention.head_count_kv", U32, 4)], "multiple"),
+      ("llama.attention.head_count", U32, 6), ("llama.attention.head_count_kv", U32, 4)], "divide"),
     ([("general.architecture", STR, "llama"), ("llama.embedding_length", U32, 64), ("llama.block_count", U32, 1),
-      ("llama.attention.head_count", U32, 4), ("llama.rope.scaling.type", STR, "yarn"),
-      ("llama.rope.scaling.factor", F32, 4.0)], "scaling"),
+      ("llama.attention.head_count", U32, 4), ("llama.rope.dimension_count", U32, 7)], "rotary"),
 ])
 def test_model_config_refusals(tmp_path, md, err):
     p = tmp_path / "c.gguf"
     write_gguf(p, md, [])
     with pytest.raises(NotSupportedError, match=err):
         model_config(GgufModelFile.Open(p))
+
+
+def test_other_rope_scaling_is_a_warning(tmp_path):
+    # ModelConfig.From records unimplemented scaling as a warning and runs the model
+    # (src/ModelConfig.cs:71-74)
+    p = tmp_path / "y.gguf"
+    write_gguf(p, [("general.architecture", STR, "llama"), ("llama.embedding_length", U32, 64),
+                   ("llama.block_count", U32, 1), ("llama.attention.head_count", U32, 4),
+                   ("llama.rope.scaling.type", STR, "yarn"), ("llama.rope.scaling.factor", F32, 4.0)], [])
+    c = model_config(GgufModelFile.Open(p))
+    assert c.rope_freq_scale == 1.0 and len(c.warnings) == 1 and "yarn" in c.warnings[0]
+    write_gguf(p, [("general.architecture", STR, "llama"), ("llama.embedding_length", U32, 64),
+                   ("llama.block_count", U32, 1), ("llama.attention.head_count", U32, 4),
+                   ("llama.rope.scaling.type", STR, "yarn"), ("llama.rope.scaling.factor", F32, 1.0)], [])
+    assert model_config(GgufModelFile.Open(p)).warnings == []
+
+
+def test_invalid_utf8_is_replaced(tmp_path):
+    # Encoding.UTF8.GetString (src/Gguf.cs:226) replaces invalid bytes instead of failing
+    p = tmp_path / "u.gguf"
+    write_gguf(p, [("general.architecture", STR, "llama")], [])
+    raw = bytearray(p.read_bytes())
+    i = raw.index(b"llama")
+    raw[i + 1] = 0xFF
+    p.write_bytes(bytes(raw))
+    assert GgufModelFile.Open(p).Metadata["general.architecture"] == "l\ufffdama"
+
+
+def test_counts_larger_than_the_file_are_refused(tmp_path):
+    p = tmp_path / "n.gguf"
+    write_gguf(p, META[:1], [])
+    raw = bytearray(p.read_bytes())
+    raw[8:16] = struct.pack("<q", 1 << 40)
+    p.write_bytes(bytes(raw))
+    with pytest.raises(InvalidDataError):
+        GgufModelFile.Open(p)
 
 
 def test_linear_rope_scaling(tmp_path):

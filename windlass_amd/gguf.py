@@ -1,51 +1,119 @@
-"""GGUF model files (GgufModelFile, src/Gguf.cs:104-270) and ModelConfig.From
-(src/ModelConfig.cs:38-100) for the dense architectures, and the model loaded into HBM for
-DeviceTransformer.
+"""GGUF model files and their model constants, read from ggml's published file format (gguf.md),
+for the device forward: the counterpart of the reference's GgufModelFile (src/Gguf.cs:104-270)
+and ModelConfig.From (src/ModelConfig.cs:38-100).
 
-The reader keeps the reference's checks: the magic, versions 2 and 3, sane counts, a
-power-of-two general.alignment (default 32), 1..4 positive dims, no duplicate tensor, whole
-blocks per row, every tensor inside its file; split models (name-00001-of-0000N.gguf) are read
-part by part and the first part's metadata wins. Tensor bytes are memory-mapped and go to HBM
-unchanged (wl_upload); 1-D tensors (norms, biases, rope_freqs) are decoded to float32 on the GPU
-by the dequant kernels.
+A file is memory-mapped and decoded with a bounds-checked cursor: every field read proves first
+that its bytes lie inside the file, so counts and lengths are limited by what the file can hold
+rather than by fixed caps. Layout (all little-endian):
+
+    u32 magic "GGUF" | u32 version (2 or 3) | u64 tensor count | u64 metadata count
+    metadata: string key, u32 kind, value   (kind 8: u64 length + UTF-8 bytes;
+                                             kind 9: u32 item kind, u64 count, items)
+    tensor infos: string name, u32 n_dims, u64 dims[n_dims] (row length first), u32 ggml type,
+                  u64 offset from the data section
+    data section at the first multiple of general.alignment (default 32, a power of two)
+
+A model split by gguf-split (<base>-00001-of-0000N.gguf) opens from any part; the parts' tensors
+are concatenated in part order and a metadata key keeps the value of the first part that holds
+it. Tensor bytes go to HBM unchanged (wl_upload); 1-D tensors (norms, biases, rope_freqs) are
+decoded to float32 by the GPU's dequant kernels.
 """
 import ctypes
+import mmap
 import os
-import re
 import struct
+from dataclasses import dataclass, field
 
 import numpy as np
 
 from ._lib import NotSupportedError, check, load
 from .backend import GgmlType, layout
 
-MAGIC = 0x46554747  # "GGUF"
-ARCHITECTURES = ("llama", "qwen2", "qwen3", "mixtral", "qwen2moe", "qwen3moe", "granite", "olmo2")
-# GgufType (src/Gguf.cs:12-16): id -> (struct format, size); 8 = string, 9 = array
-_SCALARS = {0: ("<B", 1), 1: ("<b", 1), 2: ("<H", 2), 3: ("<h", 2), 4: ("<I", 4), 5: ("<i", 4), 6: ("<f", 4),
-            7: ("<?", 1), 10: ("<Q", 8), 11: ("<q", 8), 12: ("<d", 8)}
-_NP = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32, 6: np.float32, 7: np.uint8,
-       10: np.uint64, 11: np.int64, 12: np.float64}
-_SPLIT = re.compile(r"^(.*)-(\d{5})-of-(\d{5})\.gguf$", re.IGNORECASE)
+GGUF_MAGIC = b"GGUF"
+DEFAULT_ALIGNMENT = 32
+MAX_DIMS = 4  # GGML_MAX_DIMS
+
+# metadata value kinds (gguf.md "gguf_metadata_value_type") with fixed-size payloads
+_FIXED = {0: np.dtype("<u1"), 1: np.dtype("<i1"), 2: np.dtype("<u2"), 3: np.dtype("<i2"), 4: np.dtype("<u4"),
+          5: np.dtype("<i4"), 6: np.dtype("<f4"), 7: np.dtype("<u1"), 10: np.dtype("<u8"), 11: np.dtype("<i8"),
+          12: np.dtype("<f8")}
+KIND_BOOL, KIND_STRING, KIND_ARRAY = 7, 8, 9
+# smallest encodings, used to bound counts by the bytes that remain
+_MIN_KV = 8 + 4 + 1           # empty key, kind, one-byte value
+_MIN_TENSOR_INFO = 8 + 4 + 8 + 4 + 8
 
 
 class InvalidDataError(ValueError):
     """InvalidDataException: a file that is not a well-formed GGUF model."""
 
 
-class GgufTensor:
-    """GgufTensor (src/Gguf.cs:82-102): Dims[0] is the row length."""
+class _Cursor:
+    """Little-endian reads over a memory-mapped part, each checked against the part's end."""
 
-    def __init__(self, name, dims, t, file_index, offset):
-        self.Name, self.Dims, self.Type, self.FileIndex, self.FileOffset = name, dims, t, file_index, offset
-        self.SizeBytes = 0
+    def __init__(self, buf, path):
+        self.buf, self.path, self.pos = buf, path, 0
+
+    def remaining(self):
+        return len(self.buf) - self.pos
+
+    def _take(self, n, what):
+        if n < 0 or n > self.remaining():
+            raise InvalidDataError("%s: %s needs %d bytes at offset %d, past the end of the file (%d bytes)"
+                                   % (self.path, what, n, self.pos, len(self.buf)))
+        p = self.pos
+        self.pos += n
+        return p
+
+    def u32(self, what):
+        return struct.unpack_from("<I", self.buf, self._take(4, what))[0]
+
+    def u64(self, what):
+        return struct.unpack_from("<Q", self.buf, self._take(8, what))[0]
+
+    def text(self, what):
+        n = self.u64(what + " length")
+        p = self._take(n, what)
+        # invalid UTF-8 is replaced, not refused (token strings of real files carry stray bytes)
+        return bytes(self.buf[p:p + n]).decode("utf-8", errors="replace")
+
+    def fixed(self, kind, count, what):
+        dt = _FIXED[kind]
+        p = self._take(count * dt.itemsize, what)
+        a = np.frombuffer(self.buf, dtype=dt, count=count, offset=p).copy()
+        return a.astype(bool) if kind == KIND_BOOL else a
+
+    def value(self, kind, what):
+        if kind == KIND_STRING:
+            return self.text(what)
+        if kind == KIND_ARRAY:
+            item = self.u32(what + " item kind")
+            n = self.u64(what + " item count")
+            if item == KIND_STRING:
+                if n * 8 > self.remaining():
+                    raise InvalidDataError("%s: %s claims %d strings, more than the file holds" % (self.path, what, n))
+                return [self.text(what) for _ in range(n)]
+            if item not in _FIXED:
+                raise InvalidDataError("%s: %s is an array of kind %d, which GGUF does not define"
+                                       % (self.path, what, item))
+            return self.fixed(item, n, what)
+        if kind not in _FIXED:
+            raise InvalidDataError("%s: %s has value kind %d, which GGUF does not define" % (self.path, what, kind))
+        return self.fixed(kind, 1, what)[0].item()
+
+
+@dataclass
+class GgufTensor:
+    """One tensor of a model: Dims[0] is the row length (src/Gguf.cs:82-102)."""
+    Name: str
+    Dims: list
+    Type: int
+    FileIndex: int
+    FileOffset: int          # absolute, in its part
+    SizeBytes: int = 0
 
     @property
     def ElementCount(self):
-        n = 1
-        for d in self.Dims:
-            n *= d
-        return n
+        return int(np.prod(self.Dims, dtype=np.int64))
 
     @property
     def Cols(self):
@@ -56,122 +124,104 @@ class GgufTensor:
         return self.ElementCount // self.Dims[0]
 
 
-class _Reader:
-    def __init__(self, f, path):
-        self.f, self.path = f, path
+@dataclass
+class _Part:
+    path: str
+    size: int
+    metadata: dict = field(default_factory=dict)
+    tensors: list = field(default_factory=list)
 
-    def read(self, n):
-        b = self.f.read(n)
-        if len(b) != n:
-            raise InvalidDataError("Unexpected end of GGUF header in %s." % self.path)
-        return b
 
-    def scalar(self, fmt, size):
-        return struct.unpack(fmt, self.read(size))[0]
+def _parse_part(path, index):
+    size = os.path.getsize(path)
+    with open(path, "rb") as f:
+        buf = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ) if size else b""
+    try:
+        c = _Cursor(buf, path)
+        if size < 4 or bytes(buf[:4]) != GGUF_MAGIC:
+            raise InvalidDataError("%s does not start with the GGUF magic" % path)
+        c.pos = 4
+        version = c.u32("version")
+        if version not in (2, 3):
+            raise InvalidDataError("%s: GGUF version %d (versions 2 and 3 are read)" % (path, version))
+        n_tensors, n_kv = c.u64("tensor count"), c.u64("metadata count")
+        if n_kv * _MIN_KV + n_tensors * _MIN_TENSOR_INFO > c.remaining():
+            raise InvalidDataError("%s: %d tensors and %d metadata entries cannot fit in %d bytes"
+                                   % (path, n_tensors, n_kv, size))
+        part = _Part(path, size)
+        for i in range(n_kv):
+            key = c.text("metadata key %d" % i)
+            part.metadata.setdefault(key, c.value(c.u32("kind of " + key), key))
+        align = part.metadata.get("general.alignment", DEFAULT_ALIGNMENT)
+        if not isinstance(align, int) or align <= 0 or align & (align - 1):
+            raise InvalidDataError("%s: general.alignment %r is not a power of two" % (path, align))
+        for i in range(n_tensors):
+            name = c.text("tensor name %d" % i)
+            nd = c.u32("dims of " + name)
+            if not 1 <= nd <= MAX_DIMS:
+                raise InvalidDataError("%s: tensor %s has %d dimensions (1..%d allowed)" % (path, name, nd, MAX_DIMS))
+            dims = [c.u64("dim of " + name) for _ in range(nd)]
+            if min(dims) < 1 or max(dims) >= 1 << 62:
+                raise InvalidDataError("%s: tensor %s has dimensions %s" % (path, name, dims))
+            ttype, rel = c.u32("type of " + name), c.u64("offset of " + name)
+            part.tensors.append(GgufTensor(name, dims, ttype, index, rel))
+        data_start = -(-c.pos // align) * align
+    finally:
+        if size:
+            buf.close()
+    for t in part.tensors:
+        if t.Type not in GgmlType._value2member_map_:
+            raise NotSupportedError("%s: tensor %s has ggml type %d, which the GPU path cannot read"
+                                    % (path, t.Name, t.Type))
+        t.Type = GgmlType(t.Type)
+        elems, nbytes = layout(t.Type)
+        if t.Cols % elems:
+            raise InvalidDataError("%s: tensor %s rows of %d values are not whole %s blocks of %d"
+                                   % (path, t.Name, t.Cols, t.Type.name, elems))
+        t.SizeBytes = t.ElementCount // elems * nbytes
+        t.FileOffset += data_start
+        if t.FileOffset + t.SizeBytes > size:
+            raise InvalidDataError("%s: tensor %s (%d bytes at %d) runs past the end of the file (%d bytes)"
+                                   % (path, t.Name, t.SizeBytes, t.FileOffset, size))
+    return part
 
-    def string(self):
-        n = self.scalar("<Q", 8)
-        if n > 0x7FFFFFFF:
-            raise InvalidDataError("GGUF string too long.")
-        return self.read(n).decode("utf-8")
 
-    def value(self, t):
-        if t == 8:
-            return self.string()
-        if t not in _SCALARS:
-            raise InvalidDataError("Unknown GGUF value type %d." % t)
-        return self.scalar(*_SCALARS[t])
-
-    def array(self, t, n):
-        if n < 0 or n > 0x7FFFFFFF:
-            raise InvalidDataError("Bad GGUF array length.")
-        if t == 8:
-            return [self.string() for _ in range(n)]
-        if t not in _NP:
-            raise InvalidDataError("Unsupported GGUF array type %d." % t)
-        a = np.frombuffer(self.read(n * _SCALARS[t][1]), dtype=_NP[t]).copy()
-        return a.astype(bool) if t == 7 else a
+def split_parts(path):
+    """Every part of a gguf-split model named by any one part (<base>-NNNNN-of-MMMMM.gguf), or the
+    path alone."""
+    stem, ext = os.path.splitext(path)
+    bits = stem.rsplit("-", 3)
+    if ext.lower() != ".gguf" or len(bits) != 4 or bits[2] != "of" or not (
+            len(bits[1]) == len(bits[3]) == 5 and bits[1].isdigit() and bits[3].isdigit()):
+        return [path]
+    total = int(bits[3])
+    return ["%s-%05d-of-%05d%s" % (bits[0], i, total, ext) for i in range(1, total + 1)]
 
 
 class GgufModelFile:
     """A GGUF model: Metadata {key: value}, Tensors in file order, TensorsByName."""
 
-    def __init__(self):
-        self.Paths, self.Metadata, self.Tensors, self.TensorsByName = [], {}, [], {}
+    def __init__(self, parts):
+        self.Paths = [p.path for p in parts]
+        self.Metadata, self.Tensors, self.TensorsByName = {}, [], {}
+        for p in parts:
+            for k, v in p.metadata.items():
+                self.Metadata.setdefault(k, v)
+            for t in p.tensors:
+                if t.Name in self.TensorsByName:
+                    raise InvalidDataError("%s: tensor %s appears twice in the model" % (p.path, t.Name))
+                self.TensorsByName[t.Name] = t
+                self.Tensors.append(t)
         self._maps = {}
 
     @staticmethod
     def Open(path):
-        """A .gguf file, or every part of a split model when given any one part (Gguf.cs:119-140)."""
-        path = os.path.abspath(path)
-        parts = [path]
-        m = _SPLIT.match(path)
-        if m:
-            count = int(m.group(3))
-            parts = ["%s-%05d-of-%05d.gguf" % (m.group(1), i, count) for i in range(1, count + 1)]
-            for p in parts:
-                if not os.path.exists(p):
-                    raise FileNotFoundError("Split model part is missing: " + p)
-        g = GgufModelFile()
-        for i, p in enumerate(parts):
-            g._read_header(p, i)
-        return g
-
-    def _read_header(self, path, file_index):
-        self.Paths.append(path)
-        length = os.path.getsize(path)
-        with open(path, "rb") as f:
-            r = _Reader(f, path)
-            if length < 24 or r.scalar("<I", 4) != MAGIC:
-                raise InvalidDataError(path + " is not a GGUF file.")
-            version = r.scalar("<I", 4)
-            if version < 2 or version > 3:
-                raise InvalidDataError("%s: unsupported GGUF version %d." % (path, version))
-            n_tensors, n_kv = r.scalar("<q", 8), r.scalar("<q", 8)
-            if n_tensors < 0 or n_kv < 0 or n_tensors > 1000000 or n_kv > 1000000:
-                raise InvalidDataError(path + ": bad tensor or key count.")
-            alignment = 32
-            for _ in range(n_kv):
-                key = r.string()
-                t = r.scalar("<i", 4)
-                if t == 9:
-                    at = r.scalar("<i", 4)
-                    v = r.array(at, r.scalar("<q", 8))
-                else:
-                    v = r.value(t)
-                if key == "general.alignment":
-                    alignment = int(v)
-                self.Metadata.setdefault(key, v)  # split parts repeat keys; the first part wins
-            if alignment <= 0 or alignment & (alignment - 1):
-                raise InvalidDataError(path + ": general.alignment must be a power of two.")
-            mine = []
-            for _ in range(n_tensors):
-                name = r.string()
-                nd = r.scalar("<I", 4)
-                if nd == 0 or nd > 4:
-                    raise InvalidDataError("Tensor %s has %d dims." % (name, nd))
-                dims = [r.scalar("<q", 8) for _ in range(nd)]
-                if any(d <= 0 for d in dims):
-                    raise InvalidDataError("Tensor %s has a non-positive dim." % name)
-                t = r.scalar("<i", 4)
-                off = r.scalar("<Q", 8)
-                if name in self.TensorsByName or any(x.Name == name for x in mine):
-                    raise InvalidDataError("Duplicate tensor %s." % name)
-                mine.append(GgufTensor(name, dims, t, file_index, off))
-            data = (f.tell() + alignment - 1) // alignment * alignment
-        for t in mine:
-            if t.Type not in GgmlType._value2member_map_:
-                raise NotSupportedError("Tensor %s uses type %d, which Windlass cannot read yet." % (t.Name, t.Type))
-            be, bb = layout(GgmlType(t.Type))
-            if t.Dims[0] % be:
-                raise InvalidDataError("Tensor %s row is not a multiple of the block size." % t.Name)
-            t.Type = GgmlType(t.Type)
-            t.SizeBytes = t.ElementCount // be * bb
-            t.FileOffset += data
-            if t.FileOffset + t.SizeBytes > length:
-                raise InvalidDataError("Tensor %s extends past the end of %s." % (t.Name, path))
-            self.Tensors.append(t)
-            self.TensorsByName[t.Name] = t
+        """A .gguf file, or the whole split model when given any one of its parts."""
+        paths = split_parts(os.path.abspath(str(path)))
+        missing = [p for p in paths if not os.path.exists(p)]
+        if missing:
+            raise FileNotFoundError("part %s of the split model is missing" % missing[0])
+        return GgufModelFile([_parse_part(p, i) for i, p in enumerate(paths)])
 
     def Has(self, key):
         return key in self.Metadata
@@ -180,52 +230,64 @@ class GgufModelFile:
         return self.Metadata.get(key, default)
 
     def data(self, t):
-        """The tensor's raw blocks (a read-only memory map of its file)."""
+        """The tensor's raw blocks (a read-only memory map of its part)."""
         m = self._maps.get(t.FileIndex)
         if m is None:
             m = self._maps[t.FileIndex] = np.memmap(self.Paths[t.FileIndex], dtype=np.uint8, mode="r")
         return m[t.FileOffset:t.FileOffset + t.SizeBytes]
 
 
+# architectures the device forward runs, with their rotary pairing (False: adjacent values,
+# True: NeoX halves); the reference's other architectures are refused by model_config
+DENSE_ARCHS = {"llama": False, "qwen2": True, "qwen3": True, "granite": False}
+KNOWN_ARCHS = set(DENSE_ARCHS) | {"mixtral", "qwen2moe", "qwen3moe", "olmo2"}
+
+
 def model_config(g):
-    """ModelConfig.From (src/ModelConfig.cs:38-100) for the dense models DeviceTransformer runs:
-    llama, qwen2, qwen3, and granite without embedding or logit scales. Other architectures,
-    experts, OLMo 2's post-norms and unimplemented RoPE scaling raise NotSupportedError."""
+    """ModelConfig.From (src/ModelConfig.cs:38-100) for the models the device forward runs:
+    llama, qwen2, qwen3, and granite without embedding or logit scales. Architectures outside the
+    reference's list, expert layers, OLMo 2's post-norms and granite's embedding/logit scales raise
+    NotSupportedError. RoPE scaling other than linear is recorded in `warnings`, as the reference
+    does, and the model runs without it."""
     from .model import ModelConfig
     arch = g.Get("general.architecture", "")
-    if arch not in ARCHITECTURES:
-        raise NotSupportedError("Model architecture '%s' is not supported." % arch)
-    a = arch + "."
-    if int(g.Get(a + "expert_count", 0)) > 0 or arch in ("mixtral", "qwen2moe", "qwen3moe"):
-        raise NotSupportedError("The device forward runs dense models; %s has experts." % arch)
-    if arch == "olmo2":
-        raise NotSupportedError("OLMo 2's post-norms are not on the device forward.")
-    embd = int(g.Get(a + "embedding_length"))
-    heads = int(g.Get(a + "attention.head_count"))
-    kv_heads = int(g.Get(a + "attention.head_count_kv", heads))
-    head_dim = int(g.Get(a + "attention.key_length", embd // heads))
-    rope_dims = int(g.Get(a + "rope.dimension_count", head_dim))
-    if heads % kv_heads:
-        raise NotSupportedError("head_count must be a multiple of head_count_kv.")
-    if rope_dims > head_dim or rope_dims % 2:
-        raise NotSupportedError("Unsupported rope.dimension_count %d." % rope_dims)
-    freq_scale = 1.0
-    scaling, factor = g.Get(a + "rope.scaling.type", "none"), float(g.Get(a + "rope.scaling.factor", 0.0))
+    if arch not in KNOWN_ARCHS:
+        raise NotSupportedError("architecture %r is not one Windlass runs" % arch)
+
+    def md(key, default=None, cast=int):
+        v = g.Get("%s.%s" % (arch, key), default)
+        if v is None:
+            raise InvalidDataError("the model has no %s.%s" % (arch, key))
+        return cast(v)
+
+    f32 = lambda v: float(np.float32(v))  # noqa: E731  (GGUF float keys are read as float32)
+    if arch not in DENSE_ARCHS or md("expert_count", 0) > 0:
+        raise NotSupportedError("%s has expert layers; the device forward runs dense layers" % arch)
+    embd, heads = md("embedding_length"), md("attention.head_count")
+    kv_heads = md("attention.head_count_kv", heads)
+    head_dim = md("attention.key_length", embd // heads)
+    rope_dims = md("rope.dimension_count", head_dim)
+    if kv_heads < 1 or heads % kv_heads:
+        raise NotSupportedError("%d query heads do not divide into %d key/value heads" % (heads, kv_heads))
+    if rope_dims % 2 or rope_dims > head_dim:
+        raise NotSupportedError("rotary dimension count %d must be even and at most the head size %d"
+                                % (rope_dims, head_dim))
+    warnings, freq_scale = [], 1.0
+    scaling, factor = md("rope.scaling.type", "none", str), md("rope.scaling.factor", 0.0, f32)
     if scaling == "linear" and factor > 0:
-        freq_scale = float(np.float32(1.0) / np.float32(factor))
+        freq_scale = f32(np.float32(1.0) / np.float32(factor))
     elif scaling != "none" and factor > 0 and factor != 1.0:
-        raise NotSupportedError("RoPE scaling '%s' is not implemented." % scaling)
+        warnings.append("RoPE scaling %r (factor %g) is not applied; positions past the trained context may "
+                        "degrade" % (scaling, factor))
     attention_scale = residual_scale = 0.0
     if arch == "granite":
-        if float(g.Get(a + "embedding_scale", 0.0)) or float(g.Get(a + "logit_scale", 0.0)):
-            raise NotSupportedError("Granite's embedding and logit scales are not on the device forward.")
-        residual_scale = float(g.Get(a + "residual_scale", 0.0))
-        attention_scale = float(g.Get(a + "attention.scale", 0.0))
-    return ModelConfig(layers=int(g.Get(a + "block_count")), embd=embd, heads=heads, kv_heads=kv_heads,
-                       head_dim=head_dim, rope_dims=rope_dims, neox=arch in ("qwen2", "qwen3"),
-                       rope_base=float(np.float32(g.Get(a + "rope.freq_base", 10000.0))), rope_freq_scale=freq_scale,
-                       eps=float(np.float32(g.Get(a + "attention.layer_norm_rms_epsilon", 1e-5))),
-                       attention_scale=attention_scale, residual_scale=residual_scale)
+        if md("embedding_scale", 0.0, float) or md("logit_scale", 0.0, float):
+            raise NotSupportedError("granite's embedding and logit scales are not on the device forward")
+        residual_scale, attention_scale = md("residual_scale", 0.0, float), md("attention.scale", 0.0, float)
+    return ModelConfig(layers=md("block_count"), embd=embd, heads=heads, kv_heads=kv_heads, head_dim=head_dim,
+                       rope_dims=rope_dims, neox=DENSE_ARCHS[arch], rope_base=md("rope.freq_base", 10000.0, f32),
+                       rope_freq_scale=freq_scale, eps=md("attention.layer_norm_rms_epsilon", 1e-5, f32),
+                       attention_scale=attention_scale, residual_scale=residual_scale, warnings=warnings)
 
 
 def _vector(ctx, g, t, dev):

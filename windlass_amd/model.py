@@ -10,7 +10,7 @@ and feeds it to the next step's embedding (wl_embed_dev_ids), so the host queues
 without waiting and reads the ids once.
 """
 import ctypes
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 
@@ -35,6 +35,7 @@ class ModelConfig:
     eps: float = 1e-5
     attention_scale: float = 0.0  # 0: 1/sqrt(head_dim)
     residual_scale: float = 0.0   # 0: 1
+    warnings: list = field(default_factory=list)  # ModelConfig.Warnings: what the model runs without
 
 
 def _ptr(t):
