@@ -285,6 +285,13 @@ int wl_layer_dev(wl_ctx *ctx, const wl_layer_desc *layer, float *d_x, int32_t T,
 int wl_layer_batch_dev(wl_ctx *ctx, const wl_layer_desc *layer, float *d_x, int32_t N, const int32_t *pos,
                        const int32_t *slot, int32_t slots, int32_t slot_positions, uint16_t *d_K, uint16_t *d_V);
 
+/* ---- Calibration (no counterpart in the reference) ----
+ * A plain streaming read of `bytes` (a multiple of 16) of device memory at d_src by `workgroups`
+ * workgroups of 256 threads (0: eight per CU), stream-ordered on the context. It only loads; the
+ * rate it reaches is the HBM read ceiling the decode GEMVs' roofline fractions are set against.
+ * d_out (one uint32, device) is written only in a case real data does not produce. */
+int wl_read_peak_dev(wl_ctx *ctx, const void *d_src, int64_t bytes, int32_t workgroups, uint32_t *d_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,6 +17,7 @@
 #include "wl_intdot.h"
 #include "wl_layer.h"
 #include "wl_moe.h"
+#include "wl_probe.h"
 
 // Bytes of padding after every weight buffer: the GEMV reads the aligned dwords around
 // 2-byte-aligned fields and may touch up to 16 bytes past the last block.
@@ -1074,4 +1075,14 @@ extern "C" int wl_layer_batch_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x,
   rm.slot = rows + N;
   rm.cap = slot_positions;
   return layer_run(c, L, d_x, N, 0, d_K, d_V, rm, max_n, true);
+}
+
+extern "C" int wl_read_peak_dev(wl_ctx *c, const void *d_src, int64_t bytes, int32_t workgroups, uint32_t *d_out) {
+  if (!c || !d_src || !d_out) return fail(WL_E_ARG, "wl_read_peak_dev: null argument");
+  if (bytes < 16 || bytes % 16) return fail(WL_E_SHAPE, "wl_read_peak_dev: %lld bytes are not whole 16-byte words",
+                                            (long long)bytes);
+  const int wgs = workgroups > 0 ? workgroups : 8 * c->num_cu;
+  WL_HIP(hipSetDevice(c->device), "hipSetDevice");
+  WL_HIP(wl::read_peak_launch(d_src, bytes, wgs, d_out, c->stream), "read_peak_kernel");
+  return WL_OK;
 }
