@@ -285,6 +285,17 @@ int wl_layer_dev(wl_ctx *ctx, const wl_layer_desc *layer, float *d_x, int32_t T,
 int wl_layer_batch_dev(wl_ctx *ctx, const wl_layer_desc *layer, float *d_x, int32_t N, const int32_t *pos,
                        const int32_t *slot, int32_t slots, int32_t slot_positions, uint16_t *d_K, uint16_t *d_V);
 
+/* ---- Allocation-free product (no counterpart in the reference) ----
+ * For callers that cannot allocate device memory: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc. The same operation and results as wl_matmul_dev (bit
+ * for bit: the same kernels), but every kernel's scratch is a static per-GPU array of 32 MiB that
+ * the library resolves in wl_create, so the call allocates nothing. A call that would need more
+ * scratch than that (large GEMMs: T > 8 with T * cols * 2 bytes of bf16 activations near 32 MiB)
+ * returns WL_E_SHAPE before anything is launched. Calls on one GPU share the array: calls that
+ * overlap (other streams, other contexts, other host threads) race. */
+int wl_matmul_dev_noalloc(wl_ctx *ctx, const wl_weight *w, int32_t expert, const float *d_x, int32_t T,
+                          float *d_y);
+
 /* ---- Calibration (no counterpart in the reference) ----
  * A plain streaming read of `bytes` (a multiple of 16) of device memory at d_src by `workgroups`
  * workgroups of 256 threads (0: eight per CU), stream-ordered on the context. It only loads; the

@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/windlass_hip.h"
@@ -169,6 +170,49 @@ static int ensure(wl_ctx *c, int slot, size_t bytes) {
   return WL_OK;
 }
 
+// ---- The allocation-free entry point's scratch ----
+// One file-scope device array per GPU, held until the process ends. In host code `scratch` only
+// names the symbol: its device address on each GPU comes from hipGetSymbolAddress with that GPU
+// current (wl_create, once per device), and only that address is handed to kernels.
+static constexpr size_t kStaticScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices];
+
+// Resolves this device's copy of `scratch` (the device must be current).
+static int resolve_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return fail(WL_E_ARG, "device %d is beyond the library's %d", device,
+                                                       kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return WL_OK;
+  void *p = nullptr;
+  WL_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+  if (!p) return fail(WL_E_DEVICE, "hipGetSymbolAddress(scratch) returned no address");
+  g_scratch_ptr[device] = p;
+  return WL_OK;
+}
+
+static void *static_scratch(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return device >= 0 && device < kMaxDevices ? g_scratch_ptr[device] : nullptr;
+}
+
+// The scratch of one call: the context's growable slot, or (fixed non-null) the static array,
+// whose size bounds what the call may need.
+static int scratch_for(wl_ctx *c, int slot, size_t bytes, void *fixed, void **out) {
+  if (fixed) {
+    if (bytes > kStaticScratchBytes)
+      return fail(WL_E_SHAPE, "this call needs %zu bytes of scratch; the allocation-free entry point has %zu",
+                  bytes, kStaticScratchBytes);
+    *out = fixed;
+    return WL_OK;
+  }
+  if (int rc = ensure(c, slot, bytes)) return rc;
+  *out = c->buf[slot];
+  return WL_OK;
+}
+
 extern "C" int wl_create(int device, wl_ctx **out) {
   if (!out) return fail(WL_E_ARG, "wl_create: out is null");
   *out = nullptr;
@@ -181,6 +225,10 @@ extern "C" int wl_create(int device, wl_ctx **out) {
   hipDeviceProp_t prop;
   c->num_cu = hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0
                   ? prop.multiProcessorCount : 256;
+  if (int rc = resolve_scratch(device)) {
+    delete c;
+    return rc;
+  }
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete c;
@@ -414,13 +462,13 @@ static void operand(const wl_weight *w, int32_t expert, const uint8_t **base, in
 }
 
 // One GEMV launch (plus its combine when rows are split along K) on the context's stream.
-static int gemv(wl_ctx *c, const wl::GemvMat *mats, int nmat, int nm, const float *d_x, int cols, int T) {
+static int gemv(wl_ctx *c, const wl::GemvMat *mats, int nmat, int nm, const float *d_x, int cols, int T,
+                void *fixed = nullptr) {
   const int64_t nf = wl::gemv_scratch_floats(mats, nmat, nm, cols, T);
-  int rc;
-  if (nf > 0 && (rc = ensure(c, S_PART, (size_t)nf * sizeof(float)))) return rc;
-  WL_HIP(wl::gemv_run(mats, nmat, nm, d_x, cols, cols, T, nf > 0 ? (float *)c->buf[S_PART] : nullptr, c->num_cu,
-                      c->stream),
-         "gemv launch");
+  void *part = nullptr;
+  if (nf > 0)
+    if (int rc = scratch_for(c, S_PART, (size_t)nf * sizeof(float), fixed, &part)) return rc;
+  WL_HIP(wl::gemv_run(mats, nmat, nm, d_x, cols, cols, T, (float *)part, c->num_cu, c->stream), "gemv launch");
   return WL_OK;
 }
 
@@ -431,10 +479,11 @@ static bool int_path(const wl_ctx *c, const wl_weight *w) {
 }
 
 // FastMath.Quantize of x [T][cols] into S_QA (Q8_K when k, else Q8_0).
-static int int_quantize(wl_ctx *c, const float *d_x, int T, int cols, int k, wl::QActsDev *qa) {
-  int rc;
-  if ((rc = ensure(c, S_QA, (size_t)wl::qacts_bytes(T, cols, k)))) return rc;
-  *qa = wl::qacts_at(c->buf[S_QA], T, cols, k);
+static int int_quantize(wl_ctx *c, const float *d_x, int T, int cols, int k, wl::QActsDev *qa,
+                        void *fixed = nullptr) {
+  void *buf = nullptr;
+  if (int rc = scratch_for(c, S_QA, (size_t)wl::qacts_bytes(T, cols, k), fixed, &buf)) return rc;
+  *qa = wl::qacts_at(buf, T, cols, k);
   WL_HIP(wl::quantize_launch(d_x, T, cols, k, *qa, c->stream), "quantize launch");
   return WL_OK;
 }
@@ -457,13 +506,13 @@ struct IntActs {
 // (quantized once per call and kind). With up (same type and shape), y = silu(gate) * up per
 // (row, token) instead (SwiGlu).
 static int int_run(wl_ctx *c, const wl_weight *w, const uint8_t *base, const uint8_t *up_base, int64_t rows,
-                   const float *d_x, IntActs &acts, int T, float *d_y) {
+                   const float *d_x, IntActs &acts, int T, float *d_y, void *fixed = nullptr) {
   const int cols = (int)w->cols, k = wl::intdot_needs_k(w->type) ? 1 : 0;
   const int tp = wl::intdot_max_tokens(w->type, cols, up_base ? 2 : 1);
   if (tp < 1) return fail(WL_E_UNSUPPORTED, "integer dot: rows of %d values are too wide", cols);
   int rc;
   if (!acts.made[k]) {
-    if ((rc = int_quantize(c, d_x, T, cols, k, &acts.qa[k]))) return rc;
+    if ((rc = int_quantize(c, d_x, T, cols, k, &acts.qa[k], fixed))) return rc;
     acts.made[k] = true;
   }
   for (int t0 = 0; t0 < T; t0 += tp) {
@@ -483,12 +532,14 @@ static int int_run(wl_ctx *c, const wl_weight *w, const uint8_t *base, const uin
 }
 
 static int intdot_matmul(wl_ctx *c, const wl_weight *w, const uint8_t *base, int64_t rows, const float *d_x, int T,
-                         float *d_y) {
+                         float *d_y, void *fixed = nullptr) {
   IntActs acts;
-  return int_run(c, w, base, nullptr, rows, d_x, acts, T, d_y);
+  return int_run(c, w, base, nullptr, rows, d_x, acts, T, d_y, fixed);
 }
 
-static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float *d_x, int32_t T, float *d_y) {
+// fixed: the static scratch (the allocation-free entry point), or null for the context's slots.
+static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float *d_x, int32_t T, float *d_y,
+                      void *fixed = nullptr) {
   if (!c || !w || !d_x || !d_y) return fail(WL_E_ARG, "matmul: null argument");
   int rc = check_expert(w, expert);
   if (rc) return rc;
@@ -498,11 +549,14 @@ static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float
   const uint8_t *base;
   int64_t rows;
   operand(w, expert, &base, &rows);
-  if (int_path(c, w)) return intdot_matmul(c, w, base, rows, d_x, T, d_y);
+  if (int_path(c, w)) return intdot_matmul(c, w, base, rows, d_x, T, d_y, fixed);
   if (T > 8 && wl::gemm_supports(w->type)) {
-    if ((rc = ensure(c, S_XB, (size_t)wl::gemm_scratch_bytes((int)rows, (int)w->cols, T, c->num_cu)))) return rc;
-    WL_HIP(wl::gemm_launch(w->type, base, w->row_bytes, (int)rows, (int)w->cols, d_x, T, d_y, (int)rows,
-                           c->buf[S_XB], c->num_cu, c->stream),
+    void *xb = nullptr;
+    if ((rc = scratch_for(c, S_XB, (size_t)wl::gemm_scratch_bytes((int)rows, (int)w->cols, T, c->num_cu), fixed,
+                          &xb)))
+      return rc;
+    WL_HIP(wl::gemm_launch(w->type, base, w->row_bytes, (int)rows, (int)w->cols, d_x, T, d_y, (int)rows, xb,
+                           c->num_cu, c->stream),
            "gemm launch");
     return WL_OK;
   }
@@ -510,7 +564,7 @@ static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float
   for (int t0 = 0; t0 < T; t0 += 8) {
     const wl::GemvMat m{base, nullptr, w->row_bytes, (int)rows, w->type, d_y + (int64_t)t0 * rows, (int)rows};
     const int Tp = T - t0 < 8 ? T - t0 : 8;
-    if ((rc = gemv(c, &m, 1, 1, d_x + (int64_t)t0 * w->cols, (int)w->cols, Tp))) return rc;
+    if ((rc = gemv(c, &m, 1, 1, d_x + (int64_t)t0 * w->cols, (int)w->cols, Tp, fixed))) return rc;
   }
   return WL_OK;
 }
@@ -518,6 +572,19 @@ static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float
 extern "C" int wl_matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float *d_x, int32_t T,
                              float *d_y) {
   return matmul_dev(c, w, expert, d_x, T, d_y);
+}
+
+// wl_matmul_dev without any allocation: every kernel's scratch (K-chunk and wave-column
+// partials, the GEMM's bf16 copy of x and its chunk partials, the integer path's quantized
+// activations) is this device's static array, resolved by wl_create. A call needing more
+// than the array holds is refused before anything is launched. The scratch is fully written
+// before it is read, so nothing is cleared; calls that overlap on one GPU share it and race.
+extern "C" int wl_matmul_dev_noalloc(wl_ctx *c, const wl_weight *w, int32_t expert, const float *d_x, int32_t T,
+                                     float *d_y) {
+  if (!c) return fail(WL_E_ARG, "wl_matmul_dev_noalloc: context is null");
+  void *fixed = static_scratch(c->device);
+  if (!fixed) return fail(WL_E_DEVICE, "device %d has no resolved static scratch", c->device);
+  return matmul_dev(c, w, expert, d_x, T, d_y, fixed);
 }
 
 // d_y += (W x) * rs. Up to 8 tokens on the GEMV kernels the add is their final store; otherwise
