@@ -552,7 +552,7 @@ static int matmul_dev(wl_ctx *c, const wl_weight *w, int32_t expert, const float
   if (int_path(c, w)) return intdot_matmul(c, w, base, rows, d_x, T, d_y, fixed);
   if (T > 8 && wl::gemm_supports(w->type)) {
     void *xb = nullptr;
-    if ((rc = scratch_for(c, S_XB, (size_t)wl::gemm_scratch_bytes((int)rows, (int)w->cols, T, c->num_cu), fixed,
+    if ((rc = scratch_for(c, S_XB, (size_t)wl::gemm_scratch_bytes(w->type, (int)rows, (int)w->cols, T, c->num_cu), fixed,
                           &xb)))
       return rc;
     WL_HIP(wl::gemm_launch(w->type, base, w->row_bytes, (int)rows, (int)w->cols, d_x, T, d_y, (int)rows, xb,

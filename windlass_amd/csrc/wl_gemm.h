@@ -8,9 +8,9 @@ namespace wl {
 bool gemm_supports(int type);
 
 // K-chunks of a launch (1 when the output tiles alone fill the device).
-int gemm_chunks(int rows, int cols, int T, int num_cu);
+int gemm_chunks(int type, int rows, int cols, int T, int num_cu);
 // Bytes of scratch gemm_launch needs: x as bf16, then the chunk partials when K is split.
-int64_t gemm_scratch_bytes(int rows, int cols, int T, int num_cu);
+int64_t gemm_scratch_bytes(int type, int rows, int cols, int T, int num_cu);
 
 // y[t * ldy + r] = sum_k W[r][k] * x[t][k] for T rows of x (x is [T][cols] fp32), W rows x cols
 // raw blocks of `type`. The operands enter the matrix cores as bf16 (weights decoded exactly in

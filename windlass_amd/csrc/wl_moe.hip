@@ -56,18 +56,18 @@ __global__ void route_serial_kernel(const float *__restrict__ logits, int T, int
 
 // Routing of one token per wave (n <= 64 * PER experts, k <= 64): lane l holds probabilities l, l + 64,
 // ...; the same values as route_serial_kernel. The maximum ignores NaN like the reference's `>`
-// scan; the softmax denominator is summed in double in index order (values read lane by lane);
-// each of the k rounds picks what the reference's sequential scan picks: the first untaken entry
-// when it is NaN, else the largest untaken non-NaN value, ties to the lower id.
+// scan; the softmax denominator is summed in double in index order. The k picks are the entries
+// of rank < k, an entry's rank being how many entries are larger, or equal at a lower id: what
+// the reference's k rounds of sequential scans pick, in the same order. A NaN probability (then
+// every probability is NaN, through the denominator) takes the scan's choice for NaN: the first
+// untaken entry each round. The wave's probabilities, sort keys and picks pass through LDS (pl:
+// room for n 64-bit keys; rk_i, rk_w: k entries each).
 constexpr int kRouteWaveMax = 64 * 32;
-
-__device__ __forceinline__ bool route_better(float v, int i, float bv, int bi) {
-  return bi < 0 || v > bv || (v == bv && i < bi);
-}
 
 template <int PER>
 __device__ __forceinline__ void route_wave(const float *__restrict__ l, int n, int k, int renorm,
-                                           int *__restrict__ sel, float *__restrict__ wts) {
+                                           int *__restrict__ sel, float *__restrict__ wts, float *__restrict__ pl,
+                                           int *__restrict__ rk_i, float *__restrict__ rk_w) {
   const int lane = threadIdx.x & 63;
   float v[PER];
   float mx = -INFINITY;
@@ -83,113 +83,173 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ l, int n, i
     if (u > mx) mx = u;
   }
 #pragma unroll
-  for (int m = 0; m < PER; m++)
-    if (lane + 64 * m < n) v[m] = (float)exp((double)(v[m] - mx));
-  double sum = 0;  // in index order: entry 64m + j lives in lane j
+  for (int m = 0; m < PER; m++) {
+    const int i = lane + 64 * m;
+    if (i < n) {
+      v[m] = (float)exp((double)(v[m] - mx));
+      pl[i] = v[m];
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  // the denominator in double, entries in index order, read back sixteen at a time so the reads
+  // overlap the dependent adds
+  const float4 *p4 = reinterpret_cast<const float4 *>(pl);
+  double sum = 0;
+  int i = 0;
+  for (; i + 16 <= n; i += 16) {
+    float4 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) q[u] = p4[i / 4 + u];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      sum += (double)q[u].x;
+      sum += (double)q[u].y;
+      sum += (double)q[u].z;
+      sum += (double)q[u].w;
+    }
+  }
+  for (; i < n; i++) sum += (double)pl[i];
+  const float inv = (float)(1.0 / sum);
+  int nan = 0;
 #pragma unroll
   for (int m = 0; m < PER; m++) {
-    const int cnt = n - 64 * m < 64 ? n - 64 * m : 64;
-    for (int j = 0; j < cnt; j++) sum += (double)__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[m]), j));
+    v[m] *= inv;
+    nan |= (int)(lane + 64 * m < n) & (int)(v[m] != v[m]);
   }
-  const float inv = (float)(1.0 / sum);
-#pragma unroll
-  for (int m = 0; m < PER; m++) v[m] *= inv;
-  uint32_t taken = 0;  // bit m: entry lane + 64m chosen
-  float chosen = 0, mine_w = 0.f;  // lane j keeps choice j
-  int mine = 0;
-  for (int j = 0; j < k; j++) {
-    int first = 0x7FFFFFFF, bi = -1;
-    float bv = 0.f;
-#pragma unroll
-    for (int m = 0; m < PER; m++) {
-      const int i = lane + 64 * m;
-      if (i < n && !((taken >> m) & 1)) {
-        if (i < first) first = i;
-        if (v[m] == v[m] && route_better(v[m], i, bv, bi)) {
-          bv = v[m];
-          bi = i;
-        }
-      }
+  if (__any(nan)) {
+    if (lane < k) {
+      sel[lane] = lane;
+      wts[lane] = __builtin_nanf("");
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const int f2 = __shfl_xor(first, o, 64);
-      const int i2 = __shfl_xor(bi, o, 64);
-      const float v2 = __shfl_xor(bv, o, 64);
-      if (f2 < first) first = f2;
-      if (i2 >= 0 && route_better(v2, i2, bv, bi)) {
-        bv = v2;
-        bi = i2;
-      }
-    }
-    // the first untaken entry is a NaN: the reference's scan keeps it
-    float firstv = 0.f;
-#pragma unroll
-    for (int m = 0; m < PER; m++)
-      if (lane + 64 * m == first) firstv = v[m];
-    firstv = __shfl(firstv, first & 63, 64);
-    const int best = (firstv != firstv) ? first : bi;
-    const float bw = best == first ? firstv : bv;
-#pragma unroll
-    for (int m = 0; m < PER; m++)
-      if (lane + 64 * m == best) taken |= 1u << m;
-    if (lane == j) {
-      mine = best;
-      mine_w = bw;
-    }
-    chosen += bw;
+    return;
   }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  // The probabilities are finite and not negative here, so their bit patterns order like the
+  // values; key = (bits << 32) | ~id orders by probability, then by lower id, and an entry's
+  // rank is how many keys exceed its own. The keys replace the probabilities in LDS (pl holds
+  // 2n floats' room).
+  uint64_t *keys = reinterpret_cast<uint64_t *>(pl);
+  uint64_t key[PER];
+  int rank[PER], me[PER];
+#pragma unroll
+  for (int m = 0; m < PER; m++) {
+    me[m] = lane + 64 * m;
+    rank[m] = 0;
+    key[m] = ((uint64_t)__float_as_uint(v[m]) << 32) | (uint32_t)~me[m];
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+  for (int m = 0; m < PER; m++)
+    if (me[m] < n) keys[me[m]] = key[m];
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  const ulonglong2 *k2 = reinterpret_cast<const ulonglong2 *>(keys);
+  int j = 0;
+  for (; j + 8 <= n; j += 8) {
+    ulonglong2 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) q[u] = k2[j / 2 + u];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+      for (int m = 0; m < PER; m++) rank[m] += (int)(q[u].x > key[m]) + (int)(q[u].y > key[m]);
+  }
+  for (; j < n; j++) {
+    const uint64_t q = keys[j];
+#pragma unroll
+    for (int m = 0; m < PER; m++) rank[m] += (int)(q > key[m]);
+  }
+#pragma unroll
+  for (int m = 0; m < PER; m++)
+    if (me[m] < n && rank[m] < k) {
+      rk_i[rank[m]] = me[m];
+      rk_w[rank[m]] = v[m];
+    }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  float chosen = 0;
+  for (int c = 0; c < k; c++) chosen += rk_w[c];  // in pick order, as the reference adds them
   if (lane < k) {
+    float w = rk_w[lane];
     if (renorm) {
       const float div = chosen > WL_MIN_EXPERT_WEIGHT_SUM ? chosen : WL_MIN_EXPERT_WEIGHT_SUM;
-      mine_w /= div;
+      w /= div;
     }
-    sel[lane] = mine;
-    wts[lane] = mine_w;
+    sel[lane] = rk_i[lane];
+    wts[lane] = w;
   }
 }
 
 template <int PER>
 __global__ __launch_bounds__(64) void route_wave_kernel(const float *__restrict__ logits, int n, int k, int renorm,
                                                         int *__restrict__ sel, float *__restrict__ wts) {
+  __shared__ __attribute__((aligned(16))) float lds[128 * PER + 128];
   const int t = blockIdx.x;
-  route_wave<PER>(logits + (int64_t)t * n, n, k, renorm, sel + t * k, wts + t * k);
+  route_wave<PER>(logits + (int64_t)t * n, n, k, renorm, sel + t * k, wts + t * k, lds, (int *)(lds + 128 * PER),
+                  lds + 128 * PER + 64);
 }
 
 // The routing plan from T tokens' k choices, one thread per (token, choice) pair. Pairs are
 // numbered experts ascending, tokens ascending within an expert (the gather order of
 // src/Transformer.cs:271-286); each token's pairs are listed again in ascending expert order for
 // the combine (:289-293).
+constexpr int kPlanMaskExperts = 8192;  // experts the plan's bitmask covers; more use pair scans
+
 __device__ __forceinline__ void plan_pairs(const int *__restrict__ sel, const float *__restrict__ wts, int T, int k,
-                                           MoePlan *__restrict__ plan) {
-  __shared__ int se[MOE_MAX_PAIRS];
-  __shared__ int first_of[MOE_MAX_PAIRS];  // pair a is the lowest-index pair of its expert
-  const int P = T * k, i = threadIdx.x;
+                                           int n, MoePlan *__restrict__ plan) {
+  __shared__ __attribute__((aligned(16))) int se[MOE_MAX_PAIRS];
+  __shared__ int first_of[MOE_MAX_PAIRS];              // pair a is the lowest-index pair of its expert
+  __shared__ uint32_t emask[kPlanMaskExperts / 32];  // experts chosen by any pair
+  const int P = T * k, i = threadIdx.x, nw = (n + 31) / 32;
+  const bool masked = n <= kPlanMaskExperts;
+  if (masked)
+    for (int w = i; w < nw; w += blockDim.x) emask[w] = 0;
   if (i < P) se[i] = sel[i];
   __syncthreads();
   if (i < P) {
-    int f = 1;
-    for (int b = 0; b < i; b++)
-      if (se[b] == se[i]) f = 0;
-    first_of[i] = f;
+    if (masked) {
+      atomicOr(&emask[se[i] >> 5], 1u << (se[i] & 31));
+    } else {
+      int f = 1;
+      for (int b = 0; b < i; b++) f &= (int)(se[b] != se[i]);
+      first_of[i] = f;
+    }
   }
   __syncthreads();
   if (i >= P) return;
-  const int e = se[i], t = i / k, j = i % k;
-  int rank = 0, before = 0, same = 0, slot = 0, pos = 0, nslots = 0;
-  for (int a = 0; a < P; a++) {
-    const int ea = se[a], ta = a / k;
-    if (ea < e || (ea == e && ta < t)) rank++;
-    if (ea == e) {
-      same++;
-      if (ta < t) before++;
+  const int e = se[i], t = i / k, j = i - t * k;
+  // distinct experts below e (the slot) and in all
+  int slot = 0, nslots = 0;
+  if (masked) {
+    for (int w = 0; w < nw; w++) {
+      const uint32_t m = emask[w];
+      const int c = __popc(m);
+      nslots += c;
+      slot += w < (e >> 5) ? c : (w == (e >> 5) ? __popc(m & ((1u << (e & 31)) - 1u)) : 0);
     }
-    if (first_of[a]) {
-      nslots++;
-      if (ea < e) slot++;
+  } else {
+    for (int a = 0; a < P; a++) {
+      nslots += first_of[a];
+      slot += first_of[a] & (int)(se[a] < e);
     }
-    if (ta == t && ea < e) pos++;
   }
+  // pairs before this one in the numbering (experts ascending, tokens ascending), and this
+  // expert's tokens before t and in all
+  int rank = 0, before = 0, same = 0;
+  for (int ta = 0; ta < T; ta++) {
+    const int tb = (int)(ta < t);
+    for (int c = 0; c < k; c++) {
+      const int ea = se[ta * k + c], lt = (int)(ea < e), eq = (int)(ea == e);
+      rank += lt | (eq & tb);
+      same += eq;
+      before += eq & tb;
+    }
+  }
+  int pos = 0;  // this token's pairs of lower experts
+  for (int c = 0; c < k; c++) pos += (int)(se[t * k + c] < e);
   plan->slot_tok[slot][before] = t;
   plan->slot_pair[slot][before] = rank;
   plan->tok_pair[t][j] = rank;
@@ -203,17 +263,21 @@ __device__ __forceinline__ void plan_pairs(const int *__restrict__ sel, const fl
   if (i == 0) plan->nslots = nslots;
 }
 
-// Routing and plan in one workgroup of T waves: wave t routes token t (unless `route` is 0 and
+// Routing and plan in one workgroup of T waves (64 * T threads, at least one per pair): wave t routes token t (unless `route` is 0 and
 // sel/wts already hold the choices), then the pairs are numbered (after the barrier every choice
 // is visible to the workgroup).
 template <int PER>
 __global__ __launch_bounds__(64 * MOE_MAX_T) void route_plan_kernel(const float *__restrict__ logits, int T, int n,
                                                                     int k, int renorm, int route, int *__restrict__ sel,
                                                                     float *__restrict__ wts, MoePlan *__restrict__ plan) {
+  extern __shared__ __attribute__((aligned(16))) float route_lds[];  // per wave: 128 * PER + 128 floats
   const int t = threadIdx.x >> 6;
-  if (route && t < T) route_wave<PER>(logits + (int64_t)t * n, n, k, renorm, sel + t * k, wts + t * k);
+  float *mine = route_lds + t * (128 * PER + 128);
+  if (route && t < T)
+    route_wave<PER>(logits + (int64_t)t * n, n, k, renorm, sel + t * k, wts + t * k, mine, (int *)(mine + 128 * PER),
+                    mine + 128 * PER + 64);
   __syncthreads();
-  plan_pairs(sel, wts, T, k, plan);
+  plan_pairs(sel, wts, T, k, n, plan);
 }
 
 __global__ void combine_kernel(const MoePlan *__restrict__ plan, const float *__restrict__ yd, int T, int k,
@@ -273,17 +337,34 @@ hipError_t route_launch(const float *logits, int T, int n, int k, int renorm, in
   return hipGetLastError();
 }
 
+// Dynamic LDS above 64 KB needs the kernel's limit raised once.
+template <class K>
+static hipError_t raise_route_lds(K *kernel, size_t smem, bool &raised) {
+  if (smem > 65536 && !raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)smem) != hipSuccess)
+      return hipErrorInvalidConfiguration;
+    raised = true;
+  }
+  return hipSuccess;
+}
+
 static hipError_t route_plan_launch(const MoeLaunch &m, hipStream_t st) {
   if (m.ne > kRouteWaveMax) {
     hipError_t e = route_launch(m.logits, m.T, m.ne, m.k, m.renorm, m.sel, m.wts, m.prob, st);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(route_plan_kernel<1>, dim3(1), dim3(64 * MOE_MAX_T), 0, st, m.logits, m.T, m.ne, m.k, m.renorm,
+    hipLaunchKernelGGL(route_plan_kernel<1>, dim3(1), dim3(64 * m.T), 0, st, m.logits, m.T, m.ne, m.k, m.renorm,
                        0, m.sel, m.wts, m.plan);
     return hipGetLastError();
   }
 #define WL_RP(P)                                                                                                  \
-  hipLaunchKernelGGL(route_plan_kernel<P>, dim3(1), dim3(64 * MOE_MAX_T), 0, st, m.logits, m.T, m.ne, m.k, m.renorm, \
-                     1, m.sel, m.wts, m.plan)
+  {                                                                                                                   \
+    static bool raised = false;                                                                                       \
+    const size_t smem = (size_t)(128 * P + 128) * 4 * m.T;                                                             \
+    if (hipError_t e = raise_route_lds(&route_plan_kernel<P>, smem, raised)) return e;                                \
+    hipLaunchKernelGGL(route_plan_kernel<P>, dim3(1), dim3(64 * m.T), smem, st, m.logits, m.T, m.ne, m.k, m.renorm,   \
+                       1, m.sel, m.wts, m.plan);                                                                      \
+  }
   switch (route_per(m.ne)) {
     case 1: WL_RP(1); break;
     case 2: WL_RP(2); break;
