@@ -437,6 +437,20 @@ def run_workloads(ctx, L, stream, layers, host70, only):
                                                          "(MatMulEach: each token's bits equal its one-token result)")
         cpu.append(("llama70b_q4km_layer_T8", lambda: gemv_cpu(LAYER, host70, 8, 3.0, "70B layer (7 GEMVs) at 8 tokens")))
 
+    if want("llama70b_q4km_layer_T8_intdot"):
+        # Transformer.IntDot (--int-dot) at 8 tokens: activations quantized once per call, the
+        # products on the int8 matrix cores, every result FastMath.IntDot's bits
+        ws = [ly.w for ly in layers]
+        ctx.IntDot = True
+        try:
+            ms = time_events(stream, layer_fns(LAYER, ws, 8), 100)
+        finally:
+            ctx.IntDot = False
+        e = gemv_entry(LAYER, 8, ms, len(ws))
+        e["tokens_per_s_per_layer"] = round(8 / (ms * 1e-3), 1)
+        out["llama70b_q4km_layer_T8_intdot"] = dict(e, workload="Llama-3.3-70B Q4_K_M layer, 8 tokens, integer-dot "
+                                                                "path (Q8_K activations, v_mfma_i32_16x16x32_i8)")
+
     for key, t, rows, cols in (("prefill_512_q4k_28672x8192", Q4_K, 28672, 8192),
                                ("prefill_512_q6k_8192x28672", Q6_K, 8192, 28672)):
         if not want(key):

@@ -126,6 +126,30 @@ def test_int_matmul_matches_oracle_bitwise(ctx, t, shape, T):
     w.free()
 
 
+@pytest.mark.parametrize("t", [GgmlType.Q4_K, GgmlType.Q6_K], ids=lambda t: t.name)
+@pytest.mark.parametrize("shape", [(37, 256), (200, 8192), (16, 28672)], ids=lambda s: "%dx%d" % s)
+@pytest.mark.parametrize("T", [2, 8, 20])
+def test_int_matmul_matrix_cores_match_oracle_bitwise(ctx, t, shape, T):
+    # 2..8 tokens of Q4_K / Q6_K run on the int8 matrix cores (20: passes of 8, 8 and 4), each
+    # row's blocks split over four waves; every (row, token) is still FastMath.IntDot's bits, and
+    # a token's bits do not depend on the pass
+    rows, cols = shape
+    data = blocks(t, rows, cols, seed=rows * 3 + cols + int(t))
+    x = np.random.default_rng(T * 7 + cols).standard_normal((T, cols), dtype=np.float32)
+    w = ctx.upload(t, data, rows, cols)
+    ctx.IntDot = True
+    try:
+        y = Transformer.MatMul(w, x, T)
+        y1 = np.stack([Transformer.MatMul(w, x[i:i + 1], 1)[0] for i in (0, T - 1)])
+    finally:
+        ctx.IntDot = False
+    want = oracle_int_matmul(t, data, rows, cols, x)
+    assert np.array_equal(bits(y), bits(want)), "%s %dx%d T=%d: %d of %d differ" % (
+        t.name, rows, cols, T, int((bits(y) != bits(want)).sum()), y.size)
+    assert np.array_equal(bits(y1), bits(y[[0, T - 1]]))
+    w.free()
+
+
 @pytest.mark.parametrize("t", ITYPES, ids=lambda t: t.name)
 def test_int_path_is_off_by_default_and_close_to_float(ctx, t):
     rows, cols, T = 64, 2048, 2

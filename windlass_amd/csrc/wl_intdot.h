@@ -27,8 +27,9 @@ QActsDev qacts_at(void *buf, int T, int cols, int k);
 // through fp16), k = 1 Q8_K (blocks of 256, float d, sums of every 16 quants). Bit-identical.
 hipError_t quantize_launch(const float *x, int T, int cols, int k, QActsDev a, hipStream_t st);
 
-// Tokens one launch can take for a row of `cols` (the staged terms fit the workgroup's LDS);
-// nm = 2 for the SwiGLU pair. 0 when not even one fits.
+// Tokens one launch can take for a row of `cols` (the larger of the matrix-core kernel's and of
+// as many as the VALU kernel's staged terms fit the workgroup's LDS); nm = 2 for the SwiGLU pair.
+// 0 when not even one fits.
 int intdot_max_tokens(int type, int cols, int nm);
 
 // y[t * ldy + r] = FastMath.IntDot(W[r], the activations of token t) (src/FastMath.cs:105-214)
@@ -37,6 +38,14 @@ int intdot_max_tokens(int type, int cols, int nm);
 // reference's operations, and a row's terms are added in block order.
 hipError_t intdot_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, int cols, QActsDev a, int T,
                          float *y, int ldy, int num_cu, hipStream_t st);
+
+// The int8 matrix-core kernel (wl_intmma.hip) for 2..8 tokens of Q4_K or Q6_K: the same
+// results as intdot_launch, bit for bit (exact integer sums, the reference's float terms added
+// in block order). w2 non-null: the SwiGLU pair (nm = 2), y = silu(gate) * up.
+bool intmma_supports(int type, int cols, int T, int nm);
+int intmma_max_tokens(int type, int cols, int nm);  // 0 when the kernel does not take the rows
+hipError_t intmma_launch(int type, const uint8_t *w, const uint8_t *w2, int64_t row_bytes, int rows, int cols,
+                         QActsDev qa, int T, float *y, int ldy, hipStream_t st);
 
 // SwiGlu's gate/up half on the integer kernels, one launch: y = silu(IntDot(gate)) * IntDot(up)
 // per (row, token) (src/Transformer.cs:245-247), both products on the same activations a.

@@ -533,10 +533,11 @@ static hipError_t launch_type(int type, const IntArgs &a, int num_cu, hipStream_
 }
 
 int intdot_max_tokens(int type, int cols, int nm) {
+  const int mm = intmma_max_tokens(type, cols, nm);  // the matrix-core kernel (wl_intmma.hip)
   const int nterm = nterm_of(type, cols);
   for (int tm = 8; tm >= 1; tm /= 2)
-    if (lds_of(nm, tm, nterm) <= (size_t)kIntLds) return tm;
-  return 0;
+    if (lds_of(nm, tm, nterm) <= (size_t)kIntLds) return tm > mm ? tm : mm;
+  return mm;
 }
 
 static hipError_t run(int type, const uint8_t *w, const uint8_t *w2, int64_t row_bytes, int rows, int cols,
@@ -546,6 +547,8 @@ static hipError_t run(int type, const uint8_t *w, const uint8_t *w2, int64_t row
   if (!intdot_supports(type) || !intdot_fits(type, cols) || T > intdot_max_tokens(type, cols, nm))
     return hipErrorInvalidValue;
   if (!qa.q || !qa.d || (intdot_needs_k(type) && !qa.bsums)) return hipErrorInvalidValue;
+  // two or more tokens of Q4_K / Q6_K: the int8 matrix cores, the same bits
+  if (intmma_supports(type, cols, T, nm)) return intmma_launch(type, w, w2, row_bytes, rows, cols, qa, T, y, ldy, st);
   const IntArgs a{w, w2, row_bytes, rows, cols, qa.q, qa.d, qa.bsums, T, y, ldy, nterm_of(type, cols)};
   return nm == 2 ? launch_type<2>(type, a, num_cu, st) : launch_type<1>(type, a, num_cu, st);
 }
