@@ -72,6 +72,12 @@ int wl_can_matmul(int ggml_type);
 /* FastMath.CanIntDot (src/FastMath.cs:27-30): 1 for Q8_0, Q4_0, Q4_K, Q5_K and Q6_K. */
 int wl_can_int_dot(int ggml_type);
 
+/* Fault injection for tests of the error paths (the reference has no counterpart; its
+ * allocations fail with OutOfMemoryException): with n > 0, the n-th device allocation from now
+ * on (a weight upload, a stage, a context's scratch growth) fails once with WL_E_NOMEM, without
+ * allocating; the context stays usable. n = 0 disarms. Process-wide. */
+int wl_debug_fail_alloc(int n);
+
 /* Block geometry, GgmlTypes.TryGetLayout (src/Gguf.cs:30-66). Returns 1 when known. */
 int wl_type_layout(int ggml_type, int *block_elems, int *block_bytes);
 

@@ -114,3 +114,10 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "HERE", str(tmp_path))
     with pytest.raises(windlass_amd.BackendError):
         _lib.load()
+
+
+def test_fault_injection_is_armed_and_disarmed_on_the_host():
+    L = windlass_amd.load()
+    assert L.wl_debug_fail_alloc(-1) == _lib.WL_E_ARG
+    assert L.wl_debug_fail_alloc(3) == 0
+    assert L.wl_debug_fail_alloc(0) == 0

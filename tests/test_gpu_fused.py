@@ -57,8 +57,9 @@ def test_multi_matmul_equals_separate(ctx, types, T, cols):
         w.free()
 
 
-@pytest.mark.parametrize("t", [GgmlType.Q4_K, GgmlType.Q6_K, GgmlType.IQ4_XS], ids=lambda t: t.name)
-@pytest.mark.parametrize("T", [1, 4])
+@pytest.mark.parametrize("t", [GgmlType.Q4_K, GgmlType.Q6_K, GgmlType.IQ4_XS, GgmlType.IQ3_S, GgmlType.IQ2_S],
+                         ids=lambda t: t.name)
+@pytest.mark.parametrize("T", [1, 4, 8])
 @pytest.mark.parametrize("embd", [2048, 12288])
 def test_gate_up_epilogue(ctx, t, T, embd):
     ff = 768

@@ -285,7 +285,7 @@ def test_layer_equals_its_operations(ctx):
 
 
 @pytest.mark.parametrize("t", [GgmlType.Q4_K, GgmlType.Q6_K, GgmlType.Q8_0, GgmlType.Q5_K, GgmlType.IQ4_XS,
-                               GgmlType.F16])
+                               GgmlType.F16, GgmlType.IQ3_S, GgmlType.IQ2_S])
 @pytest.mark.parametrize("rows,cols", [(256, 512), (512, 16384), (300, 2048)])
 @pytest.mark.parametrize("T", [1, 3, 8, 12])
 def test_matmul_add_equals_matmul_then_residual(ctx, t, rows, cols, T):

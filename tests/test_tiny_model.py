@@ -126,14 +126,26 @@ def test_gpu_greedy_tokens_match_cpu(gpu, key):
         w.free()
 
 
+def build_any(key):
+    """tiny_model.build, plus "llama-q4_K_M": llama-q4_K with the Q6_K tensors of llama-q6_K
+    in layer 0's attn_v and layer 1's ffn_down (Q4_K_M mixes the two across layers)."""
+    from tiny_model import build
+    if key != "llama-q4_K_M":
+        return build(key)
+    arch, t = build("llama-q4_K")
+    _, t6 = build("llama-q6_K")
+    for n in ("blk.0.attn_v", "blk.1.ffn_down"):
+        t[n] = t6[n]
+    return arch, t
+
+
 def device_model(ctx, key, max_positions=64):
     """The same model with every activation in HBM (windlass_amd.DeviceTransformer): embedding
     rows, wl_layer_dev per layer (Transformer.Layer, src/Transformer.cs:177-232) over fp16 KV
     caches on the device, the final norm, the output product and greedy sampling on the device
     (src/Engine.cs:356-360). Returns the model and the weights to free."""
-    from tiny_model import EMBD, EPS, HEADS, KV_HEADS, LAYERS, build
-    from windlass_amd import DeviceTransformer, ModelConfig
-    arch, t = build(key)
+    from windlass_amd import DeviceTransformer
+    arch, t = build_any(key)
     dev = torch.device("cuda:0")
     weights, vectors = {}, {}
     for n, x in t.items():
@@ -141,9 +153,14 @@ def device_model(ctx, key, max_positions=64):
             vectors[n] = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev)
         elif not (n == "output" and x is t["token_embd"]):  # a tied head reuses token_embd
             weights[n] = ctx.upload(x.type, x.data, x.rows, x.cols, name=n)
-    cfg = ModelConfig(layers=LAYERS, embd=EMBD, heads=HEADS, kv_heads=KV_HEADS, head_dim=EMBD // HEADS,
-                      neox=arch != "llama", rope_base=500000.0 if arch == "llama" else 1000000.0, eps=float(EPS))
-    return DeviceTransformer(ctx, cfg, weights, vectors, max_positions), weights
+    return DeviceTransformer(ctx, tiny_config(arch), weights, vectors, max_positions), weights
+
+
+def tiny_config(arch):
+    from tiny_model import EMBD, EPS, HEADS, KV_HEADS, LAYERS
+    from windlass_amd import ModelConfig
+    return ModelConfig(layers=LAYERS, embd=EMBD, heads=HEADS, kv_heads=KV_HEADS, head_dim=EMBD // HEADS,
+                       neox=arch != "llama", rope_base=500000.0 if arch == "llama" else 1000000.0, eps=float(EPS))
 
 
 @pytest.mark.gpu
@@ -226,28 +243,14 @@ def test_gpu_batch_step_rows_equal_single_sequences(gpu, key, n_seq):
 _LAYER_NAMES = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("slots", [1, 2])
-@pytest.mark.parametrize("key", [k for k in ("llama-q4_K", "llama-bf16", "qwen2-q6_K-tied", "qwen3-q4_K")
-                                 if k in SPECS])
-def test_gpu_streamed_layers_equal_resident(gpu, key, slots):
-    """LayerStream's streaming mode under the device forward (StageStream): every layer's
-    tensors copied from pinned host memory into HBM slots as the forward reaches them (one slot:
-    each copy waits for the previous layer's last reader; two: the copy of layer l + 1 beside
-    the compute of l) give the resident forward's logits bit for bit and its greedy tokens."""
-    from tiny_model import EMBD, EPS, HEADS, KV_HEADS, LAYERS, build
-    from windlass_amd import DeviceTransformer, ModelConfig, StageStream
-    want, want_logits = None, None
-    dm, weights = device_model(gpu, key)
-    want, want_logits = dm.greedy(PROBE, 6, chunk=8, keep_logits=True)
-    cfg = dm.cfg
-    for w in weights.values():
-        w.free()
-    arch, t = build(key)
+def streamed_model(gpu, key, slots, max_positions=64):
+    """device_model's model with the decoder layers in a StageStream of `slots` HBM slots and
+    the rest resident. Returns the model, the stream and the resident weights to free."""
+    from tiny_model import LAYERS
+    from windlass_amd import DeviceTransformer, StageStream
+    arch, t = build_any(key)
     layers = [{n: (t["blk.%d.%s" % (l, n)].type, t["blk.%d.%s" % (l, n)].rows, t["blk.%d.%s" % (l, n)].cols,
                    t["blk.%d.%s" % (l, n)].data) for n in _LAYER_NAMES} for l in range(LAYERS)]
-    if any({n: v[:3] for n, v in lt.items()} != {n: v[:3] for n, v in layers[0].items()} for lt in layers):
-        pytest.skip("layers of different formats")
     stream = StageStream(gpu, layers, slots)
     dev = torch.device("cuda:0")
     w2, vectors = dict(stream.weights()), {}
@@ -258,7 +261,27 @@ def test_gpu_streamed_layers_equal_resident(gpu, key, slots):
         elif not n.startswith("blk.") and not (n == "output" and x is t["token_embd"]):
             w2[n] = gpu.upload(x.type, x.data, x.rows, x.cols, name=n)
             resident.append(w2[n])
-    ds = DeviceTransformer(gpu, cfg, w2, vectors, 64, stream=stream)
+    return DeviceTransformer(gpu, tiny_config(arch), w2, vectors, max_positions, stream=stream), stream, resident
+
+
+STREAM_KEYS = [k for k in ("llama-q4_K", "llama-bf16", "qwen2-q6_K-tied", "qwen3-q4_K") if k in SPECS] + \
+    ["llama-q4_K_M"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("slots", [1, 2])
+@pytest.mark.parametrize("key", STREAM_KEYS)
+def test_gpu_streamed_layers_equal_resident(gpu, key, slots):
+    """LayerStream's streaming mode under the device forward (StageStream): every layer's
+    tensors copied from pinned host memory into HBM slots as the forward reaches them (one slot:
+    each copy waits for the previous layer's last reader; two: the copy of layer l + 1 beside
+    the compute of l) give the resident forward's logits bit for bit and its greedy tokens;
+    llama-q4_K_M has layers of different formats and sizes in the same slots."""
+    dm, weights = device_model(gpu, key)
+    want, want_logits = dm.greedy(PROBE, 6, chunk=8, keep_logits=True)
+    for w in weights.values():
+        w.free()
+    ds, stream, resident = streamed_model(gpu, key, slots)
     got, got_logits = ds.greedy(PROBE, 6, chunk=8, keep_logits=True)
     stream.free()
     for w in resident:
@@ -266,3 +289,39 @@ def test_gpu_streamed_layers_equal_resident(gpu, key, slots):
     assert got == want, (got, want)
     for a, b in zip(got_logits, want_logits):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("key", ["llama-q4_K", "llama-q4_K_M"])
+def test_gpu_streamed_batch_equals_resident_batch(gpu, key):
+    """DeviceBatch over a streamed model: prompts and stacked steps acquire and release each
+    layer's slot as the single-sequence forward does, so every row equals the resident batch's."""
+    from windlass_amd import DeviceBatch
+    prompts = [PROBE[:5], PROBE[3:11], PROBE[1:3]]
+    dm, weights = device_model(gpu, key, max_positions=32)
+    want, want_seen = DeviceBatch(dm, slots=3, slot_positions=32).greedy(prompts, 4, keep_logits=True)
+    for w in weights.values():
+        w.free()
+    ds, stream, resident = streamed_model(gpu, key, 1, max_positions=32)
+    got, got_seen = DeviceBatch(ds, slots=3, slot_positions=32).greedy(prompts, 4, keep_logits=True)
+    stream.free()
+    for w in resident:
+        w.free()
+    assert got == want, (got, want)
+    for a, b in zip(got_seen, want_seen):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_stage_stream_refuses_layers_with_other_tensors():
+    from windlass_amd import StageStream
+    from windlass_amd._lib import ShapeError
+    from windlass_amd.backend import GgmlType
+
+    class NoCtx:  # the checks run before any device call
+        def stage(self, n):
+            raise AssertionError("no slot expected")
+    q8 = (GgmlType.Q8_0, 2, 32, np.zeros(68, np.uint8))
+    with pytest.raises(ShapeError, match="layer 1 has tensors"):
+        StageStream(NoCtx(), [{"a": q8}, {"b": q8}])
+    with pytest.raises(ShapeError, match="layer 1 a: 60 bytes"):
+        StageStream(NoCtx(), [{"a": q8}, {"a": (GgmlType.Q8_0, 2, 32, np.zeros(60, np.uint8))}])

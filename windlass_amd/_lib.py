@@ -14,6 +14,7 @@ SIGNATURES = {
     "wl_can_decode": (ctypes.c_int, [ctypes.c_int]),
     "wl_can_matmul": (ctypes.c_int, [ctypes.c_int]),
     "wl_can_int_dot": (ctypes.c_int, [ctypes.c_int]),
+    "wl_debug_fail_alloc": (ctypes.c_int, [ctypes.c_int]),
     "wl_type_layout": (ctypes.c_int, [ctypes.c_int, P, P]),
     "wl_create": (ctypes.c_int, [ctypes.c_int, PP]),
     "wl_destroy": (None, [P]),

@@ -3,6 +3,7 @@
 // Host-side only; the kernels live in wl_gemv.hip, wl_dequant.hip, wl_gemm.hip and wl_moe.hip.
 // Every entry point validates shapes on the host before anything is launched, so a kernel
 // never sees an operand that does not match its grid.
+#include <atomic>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -153,6 +154,27 @@ extern "C" int wl_can_matmul(int t) { return wl::gemv_supports(t) ? 1 : 0; }
 
 extern "C" int wl_can_int_dot(int t) { return wl::intdot_supports(t) ? 1 : 0; }
 
+// Fault injection for the error paths: when armed with n > 0, the n-th device allocation from
+// then on (weights, stages, context scratch) reports failure without allocating, once.
+static std::atomic<int> g_fail_alloc{0};
+
+static hipError_t dev_alloc(void **p, size_t bytes) {
+  int n = g_fail_alloc.load();
+  while (n > 0 && !g_fail_alloc.compare_exchange_weak(n, n - 1)) {
+  }
+  if (n == 1) {
+    *p = nullptr;
+    return hipErrorOutOfMemory;
+  }
+  return hipMalloc(p, bytes);
+}
+
+extern "C" int wl_debug_fail_alloc(int n) {
+  if (n < 0) return fail(WL_E_ARG, "wl_debug_fail_alloc: n must be >= 0");
+  g_fail_alloc.store(n);
+  return WL_OK;
+}
+
 static int ensure(wl_ctx *c, int slot, size_t bytes) {
   if (c->cap[slot] >= bytes) return WL_OK;
   if (c->buf[slot]) {
@@ -162,7 +184,7 @@ static int ensure(wl_ctx *c, int slot, size_t bytes) {
     c->cap[slot] = 0;
   }
   size_t want = bytes < 4096 ? 4096 : bytes;
-  if (hipMalloc(&c->buf[slot], want) != hipSuccess) {
+  if (dev_alloc(&c->buf[slot], want) != hipSuccess) {
     c->buf[slot] = nullptr;
     return fail(WL_E_NOMEM, "cannot allocate %zu bytes of device scratch", want);
   }
@@ -296,7 +318,7 @@ extern "C" int wl_upload(wl_ctx *c, int type, const void *blocks, int64_t rows, 
   w->experts = experts;
   w->bytes = (size_t)rows * (size_t)experts * (size_t)row_bytes;
   w->owned = true;
-  if (hipMalloc(&w->dev, w->bytes + kWeightPad) != hipSuccess) {
+  if (dev_alloc((void **)&w->dev, w->bytes + kWeightPad) != hipSuccess) {
     delete w;
     return fail(WL_E_NOMEM, "cannot allocate %zu bytes for a %s weight", (size_t)(rows * experts * row_bytes),
                 type_name(type));
@@ -346,7 +368,7 @@ extern "C" int wl_stage_create(wl_ctx *c, int64_t bytes, wl_stage **out) {
   if (!c->copy) WL_HIP(hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking), "copy stream");
   wl_stage *s = new wl_stage();
   s->bytes = (size_t)bytes;
-  if (hipMalloc(&s->dev, s->bytes + kWeightPad) != hipSuccess) {
+  if (dev_alloc((void **)&s->dev, s->bytes + kWeightPad) != hipSuccess) {
     delete s;
     return fail(WL_E_NOMEM, "cannot allocate a stage of %lld bytes", (long long)bytes);
   }

@@ -125,17 +125,23 @@ class DeviceTransformer:
             raise ShapeError("The prompt and reply need %d positions; the context is %d."
                              % (pos0 + T, self.max_positions))
 
-    def _layers_and_head(self, x, T, pos0):
-        L, h, c = self.L, self.ctx.handle, ctypes.c_void_p
+    def run_layers(self, layer):
+        """layer(l, desc) for every decoder layer in order; with a StageStream, each between the
+        acquire and the release of its slot (the copy of a later layer into the slot waits for
+        that release)."""
         if self.stream:
             self.stream.begin()
         for l, d in enumerate(self.descs):
             if self.stream:
                 self.stream.acquire(l)
-            check(L.wl_layer_dev(h, ctypes.byref(d), c(x.data_ptr()), T, pos0, c(self.K[l].data_ptr()),
-                                 c(self.V[l].data_ptr())))
+            layer(l, d)
             if self.stream:
                 self.stream.release(l)
+
+    def _layers_and_head(self, x, T, pos0):
+        L, h, c = self.L, self.ctx.handle, ctypes.c_void_p
+        self.run_layers(lambda l, d: check(L.wl_layer_dev(h, ctypes.byref(d), c(x.data_ptr()), T, pos0,
+                                                          c(self.K[l].data_ptr()), c(self.V[l].data_ptr()))))
         self.length = pos0 + T
         # Head (src/Transformer.cs:112-125) of the last row
         check(L.wl_rms_norm_dev(h, c(x[T - 1:].data_ptr()), 1, self.cfg.embd, c(self.v["output_norm"].data_ptr()),
@@ -196,36 +202,52 @@ class DeviceTransformer:
 class StageStream:
     """LayerStream's streaming mode (src/LayerStream.cs:127-181) for DeviceTransformer: each
     decoder layer's tensors in one pinned host buffer (a stage, tensors at 64-byte aligned
-    offsets as Bind lays them out), `slots` HBM slots; layer l runs from slot l % slots. begin()
-    queues the first layers; acquire(l) makes the compute stream wait for layer l's copy;
-    release(l) records the slot's last reader and queues the copy of layer l + slots into it,
-    which waits for that release. No host wait anywhere, so the copies overlap the compute of
-    the layers before them; one slot streams too (no lookahead)."""
+    offsets as Bind lays them out), `slots` HBM slots sized to the largest layer; layer l runs
+    from slot l % slots through views of its own tensors (type, shape, offset), so layers of
+    different formats (Q4_K_M's Q4_K and Q6_K attn_v / ffn_down) share the slots. begin() queues
+    the first layers; acquire(l) makes the compute stream wait for layer l's copy; release(l)
+    records the slot's last reader and queues the copy of layer l + slots into it, which waits
+    for that release. No host wait anywhere, so the copies overlap the compute of the layers
+    before them; one slot streams too (no lookahead). Every layer's stage stays in pinned host
+    memory for the object's life: the model must fit host RAM, not HBM."""
 
     def __init__(self, ctx, layers, slots=2):
-        """layers: one {name: (GgmlType, rows, cols, raw blocks)} per layer, the same names and
-        shapes in every layer."""
+        """layers: one {name: (GgmlType, rows, cols, raw blocks)} per layer, the same tensor
+        names in every layer (types and shapes may differ)."""
         from .backend import HostBuffer, layout
+        from ._lib import ShapeError
         self.ctx, self.n, self.S = ctx, len(layers), slots
-        self.offs, total = {}, 0
-        for name, (t, rows, cols, _) in layers[0].items():
-            be, bb = layout(t)
-            self.offs[name] = (total, t, rows, cols)
-            total = (total + rows * (cols // be) * bb + 63) // 64 * 64
-        self.host = []
-        for lt in layers:
+        names = sorted(layers[0]) if layers else []
+        self.offs, totals, self.host = [], [], []
+        for l, lt in enumerate(layers):  # every layer checked before anything is allocated
+            if sorted(lt) != names:
+                raise ShapeError("layer %d has tensors %s; layer 0 has %s" % (l, sorted(lt), names))
+            offs, total = {}, 0
+            for name in names:
+                t, rows, cols, data = lt[name]
+                be, bb = layout(t)
+                nbytes = rows * (cols // be) * bb
+                if cols % be or np.asarray(data).nbytes != nbytes:
+                    raise ShapeError("layer %d %s: %d bytes for %dx%d of type %d" % (
+                        l, name, np.asarray(data).nbytes, rows, cols, int(t)))
+                offs[name] = (total, t, rows, cols)
+                total = (total + nbytes + 63) // 64 * 64
+            self.offs.append(offs)
+            totals.append(max(total, 64))
+        for lt, offs, total in zip(layers, self.offs, totals):
             hb = HostBuffer(total)
-            for name, (off, t, rows, cols) in self.offs.items():
+            for name, (off, t, rows, cols) in offs.items():
                 data = np.ascontiguousarray(lt[name][3], np.uint8).reshape(-1)
                 hb.array[off:off + data.size] = data
             self.host.append(hb)
-        self.slot = [ctx.stage(total) for _ in range(slots)]
-        self.views = [{name: s.weight(off, t, rows, cols, name=name) for name, (off, t, rows, cols) in self.offs.items()}
-                      for s in self.slot]
+        need = max(totals, default=64)
+        self.slot = [ctx.stage(need) for _ in range(slots)]
+        self.views = [{name: self.slot[l % slots].weight(off, t, rows, cols, name=name)
+                       for name, (off, t, rows, cols) in offs.items()} for l, offs in enumerate(self.offs)]
 
     def weights(self):
-        """{blk.l.name: the view of slot l % slots} for DeviceTransformer."""
-        return {"blk.%d.%s" % (l, name): self.views[l % self.S][name] for l in range(self.n) for name in self.offs}
+        """{blk.l.name: layer l's view into slot l % slots} for DeviceTransformer."""
+        return {"blk.%d.%s" % (l, name): v for l, vs in enumerate(self.views) for name, v in vs.items()}
 
     def begin(self):
         for l in range(min(self.S, self.n)):
@@ -303,9 +325,9 @@ class DeviceBatch:
         x = self._buf("x", T, m.cfg.embd)
         toks = (ctypes.c_int32 * T)(*tokens)
         check(m.L.wl_embed_dev(m.ctx.handle, m.embd_w.handle, toks, T, c(x.data_ptr())))
-        for l, d in enumerate(m.descs):
-            check(m.L.wl_layer_dev(m.ctx.handle, ctypes.byref(d), c(x.data_ptr()), T, pos0,
-                                   c(self.K[l, slot].data_ptr()), c(self.V[l, slot].data_ptr())))
+        m.run_layers(lambda l, d: check(m.L.wl_layer_dev(m.ctx.handle, ctypes.byref(d), c(x.data_ptr()), T, pos0,
+                                                         c(self.K[l, slot].data_ptr()),
+                                                         c(self.V[l, slot].data_ptr()))))
         self.length[slot] = pos0 + T
         return self._head(x[T - 1:], 1)
 
@@ -317,9 +339,9 @@ class DeviceBatch:
         sl = (ctypes.c_int32 * N)(*slots)
         x = self._buf("x", N, m.cfg.embd)
         check(m.L.wl_embed_dev_ids(m.ctx.handle, m.embd_w.handle, c(d_ids.data_ptr()), N, c(x.data_ptr())))
-        for l, d in enumerate(m.descs):
-            check(m.L.wl_layer_batch_dev(m.ctx.handle, ctypes.byref(d), c(x.data_ptr()), N, pos, sl, self.slots,
-                                         self.cap, c(self.K[l].data_ptr()), c(self.V[l].data_ptr())))
+        m.run_layers(lambda l, d: check(m.L.wl_layer_batch_dev(m.ctx.handle, ctypes.byref(d), c(x.data_ptr()), N,
+                                                               pos, sl, self.slots, self.cap,
+                                                               c(self.K[l].data_ptr()), c(self.V[l].data_ptr()))))
         for s in slots:
             self.length[s] += 1
         return self._head(x, N)
