@@ -170,7 +170,9 @@ int wl_moe_ffn(wl_ctx *ctx, const float *logits, int32_t k, int32_t renorm,
  * activation blocks (FastMath.Fits, src/FastMath.cs:34) with the integer branch of MatMul
  * (src/Transformer.cs:504-524): the T rows of x are quantized once (FastMath.Quantize), then
  * y[t][r] = FastMath.IntDot(W[r], activations of t) (src/FastMath.cs:105-214), bit-identical to
- * the reference for every T. MoE experts keep the float path. */
+ * the reference for every T. The MoE entries give the experts' gate/up and down products the
+ * same branch (MoeFfn -> SwiGlu -> MatMul, src/Transformer.cs:288,241-251): x quantized once per
+ * pass, the SwiGLU outputs of every (token, expert) pair quantized for down. */
 int wl_set_int_dot(wl_ctx *ctx, int on);
 
 /* FastMath.Quantize (src/FastMath.cs:35-91) of x [T][cols], bit-identical: k = 0 gives Q8_0

@@ -86,6 +86,7 @@ def _open(path):
         L.wlo_matrix.argtypes = [U64P, I, I, I, F, P]
         L.wlo_quantize_row.argtypes = [P, I, I, P, P, P]
         L.wlo_int_dot.argtypes = [I, P, P, P, P, I, P]
+        L.wlo_int_matmul.argtypes = [I, P, I, I, I64, P, I, P, I]
         L.wlo_iq2xxs_grid.restype = ctypes.POINTER(ctypes.c_uint64)
         L.wlo_iq2s_grid.restype = ctypes.POINTER(ctypes.c_uint64)
         L.wlo_iq3s_grid.restype = ctypes.POINTER(ctypes.c_uint32)
@@ -187,13 +188,18 @@ def matmul(t, data, rows, cols, x, T, each_token=False, threads=0):
     return y.reshape(T, rows)
 
 
-def swiglu(gt, gate, ut, up, dt, down, ff, embd, x, T, each_token=False, threads=0):
+def _mode(each_token, int_dot):
+    return (1 if each_token else 0) | (2 if int_dot else 0)
+
+
+def swiglu(gt, gate, ut, up, dt, down, ff, embd, x, T, each_token=False, threads=0, int_dot=False):
+    """int_dot: Transformer.IntDot on (the integer branch for every product it applies to)."""
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
     out = np.empty(T * embd, np.float32)
     gate, up, down = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
     rc = lib().wlo_swiglu(gt, _p(gate), row_bytes(gt, embd), ut, _p(up), row_bytes(ut, embd),
                           dt, _p(down), row_bytes(dt, ff), ff, embd, _p(x), T, _p(out),
-                          int(each_token), threads)
+                          _mode(each_token, int_dot), threads)
     assert rc == 0
     return out.reshape(T, embd)
 
@@ -209,7 +215,7 @@ def route(logits, k, renorm):
 
 
 def moe_ffn(logits, k, renorm, gt, gate, ut, up, dt, down, ff, embd, x, T,
-            each_token=False, threads=0):
+            each_token=False, threads=0, int_dot=False):
     logits = np.ascontiguousarray(logits, np.float32).reshape(T, -1)
     ne = logits.shape[1]
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
@@ -217,7 +223,7 @@ def moe_ffn(logits, k, renorm, gt, gate, ut, up, dt, down, ff, embd, x, T,
     runs = np.zeros(1, np.int32)
     gate, up, down = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
     rc = lib().wlo_moe_ffn(_p(logits), ne, k, int(renorm), gt, _p(gate), ut, _p(up), dt, _p(down),
-                           ff, embd, _p(x), T, _p(out), int(each_token), threads, _p(runs))
+                           ff, embd, _p(x), T, _p(out), _mode(each_token, int_dot), threads, _p(runs))
     assert rc == 0
     return out.reshape(T, embd), int(runs[0])
 
@@ -248,6 +254,19 @@ def int_dot(t, row, q, d, bsums):
     rc = lib().wlo_int_dot(t, _p(row), _p(q), _p(d), _p(bsums), q.size, _p(out))
     assert rc == 0
     return out[0]
+
+
+def int_matmul(t, data, rows, cols, x, threads=0):
+    """Transformer.MatMul's integer branch: every (token, row) FastMath.IntDot on the token's
+    quantized activations."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+    y = np.empty((x.shape[0], rows), np.float32)
+    data = np.ascontiguousarray(data, np.uint8)
+    rc = lib().wlo_int_matmul(int(t), _p(data), rows, cols, row_bytes(int(t), cols), _p(x), x.shape[0], _p(y),
+                              threads)
+    if rc:
+        raise NotImplementedError("oracle has no integer dot for type %d at %d columns" % (t, cols))
+    return y
 
 
 def iq2xxs_grid():

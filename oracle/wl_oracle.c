@@ -872,22 +872,32 @@ static int64_t row_bytes_of(int type, int cols)
     return (int64_t)(cols / be) * bb;
 }
 
+/* MatMul's dispatch (src/Transformer.cs:483-494) under a mode: the integer branch first when
+ * IntDot is on and applies, then MatMulEach or the plain float product. */
+static int matmul_mode(int type, const uint8_t *data, int rows, int cols, int64_t row_bytes,
+                       const float *x, int T, float *y, int mode, int threads)
+{
+    if ((mode & WLO_INT_DOT) && wlo_can_int_dot(type) && wlo_int_fits(type, cols))
+        return wlo_int_matmul(type, data, rows, cols, row_bytes, x, T, y, threads);
+    return wlo_matmul(type, data, rows, cols, row_bytes, x, T, y, mode & WLO_EACH_TOKEN, threads);
+}
+
 /* SwiGlu (src/Transformer.cs:241-251). The exponential is .NET Math.Exp on a double, cast
- * to float; libm exp stands in for it. */
+ * to float; libm exp stands in for it. each_token: the WLO_EACH_TOKEN / WLO_INT_DOT mode. */
 int wlo_swiglu(int gtype, const uint8_t *gate, int64_t grb, int utype, const uint8_t *up, int64_t urb,
                int dtype, const uint8_t *down, int64_t drb, int ff, int embd,
                const float *x, int T, float *out, int each_token, int threads)
 {
     float *g = (float *)malloc(sizeof(float) * (size_t)T * ff);
     float *u = (float *)malloc(sizeof(float) * (size_t)T * ff);
-    int rc = wlo_matmul(gtype, gate, ff, embd, grb, x, T, g, each_token, threads);
-    if (!rc) rc = wlo_matmul(utype, up, ff, embd, urb, x, T, u, each_token, threads);
+    int rc = matmul_mode(gtype, gate, ff, embd, grb, x, T, g, each_token, threads);
+    if (!rc) rc = matmul_mode(utype, up, ff, embd, urb, x, T, u, each_token, threads);
     if (!rc) {
         for (int64_t i = 0; i < (int64_t)T * ff; i++) {
             float a = g[i];
             g[i] = a / (1.0f + (float)exp((double)(-a))) * u[i];
         }
-        rc = wlo_matmul(dtype, down, embd, ff, drb, g, T, out, each_token, threads);
+        rc = matmul_mode(dtype, down, embd, ff, drb, g, T, out, each_token, threads);
     }
     free(g); free(u);
     return rc;
@@ -1165,4 +1175,35 @@ int wlo_int_dot(int t, const uint8_t *b, const int8_t *q, const float *d, const 
     }
     }
     return -1;
+}
+
+int wlo_can_int_dot(int t)
+{
+    return t == WLO_Q8_0 || t == WLO_Q4_0 || t == WLO_Q4_K || t == WLO_Q5_K || t == WLO_Q6_K;
+}
+
+static int int_needs_k(int t) { return t == WLO_Q4_K || t == WLO_Q5_K || t == WLO_Q6_K; }
+
+int wlo_int_fits(int t, int cols) { return cols > 0 && cols % (int_needs_k(t) ? 256 : 32) == 0; }
+
+int wlo_int_matmul(int type, const uint8_t *data, int rows, int cols, int64_t row_bytes,
+                   const float *x, int T, float *y, int threads)
+{
+    if (!wlo_can_int_dot(type) || !wlo_int_fits(type, cols)) return -1;
+    int k = int_needs_k(type), nb = cols / (k ? 256 : 32), nth = n_threads(threads);
+    int8_t *q = (int8_t *)malloc((size_t)T * cols);
+    float *d = (float *)malloc(sizeof(float) * (size_t)T * nb);
+    int16_t *bs = (int16_t *)calloc((size_t)T * (cols / 16), sizeof(int16_t));
+    for (int t = 0; t < T; t++)
+        wlo_quantize_row(x + (int64_t)t * cols, cols, k, q + (int64_t)t * cols, d + (int64_t)t * nb,
+                         bs + (int64_t)t * (cols / 16));
+    int rc = 0;
+    #pragma omp parallel for schedule(dynamic, 32) num_threads(nth)
+    for (int r = 0; r < rows; r++)
+        for (int t = 0; t < T; t++)
+            if (wlo_int_dot(type, data + (int64_t)r * row_bytes, q + (int64_t)t * cols, d + (int64_t)t * nb,
+                            bs + (int64_t)t * (cols / 16), cols, y + (int64_t)t * rows + r))
+                rc = -1;
+    free(q); free(d); free(bs);
+    return rc;
 }

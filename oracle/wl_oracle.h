@@ -63,7 +63,13 @@ void wlo_block(const float *w, int ws, int nr, const float *x, int xs, int nt, i
  * threads <= 0 means every core. Returns 0, -1 unsupported type. */
 int wlo_matmul(int type, const uint8_t *data, int rows, int cols, int64_t row_bytes,
                const float *x, int T, float *y, int each_token, int threads);
-/* SwiGlu (src/Transformer.cs:241-251): out = down(silu(gate x) * (up x)). */
+/* mode for wlo_swiglu / wlo_moe_ffn: bit 0 EachToken (src/Transformer.cs:488), bit 1 IntDot
+ * (src/Transformer.cs:23): each product of a FastMath.CanIntDot type whose rows are whole
+ * activation blocks takes MatMul's integer branch (wlo_int_matmul). */
+#define WLO_EACH_TOKEN 1
+#define WLO_INT_DOT 2
+/* SwiGlu (src/Transformer.cs:241-251): out = down(silu(gate x) * (up x)); each_token is the
+ * mode above. */
 int wlo_swiglu(int gtype, const uint8_t *gate, int64_t g_row_bytes,
                int utype, const uint8_t *up, int64_t u_row_bytes,
                int dtype, const uint8_t *down, int64_t d_row_bytes,
@@ -90,6 +96,14 @@ void wlo_quantize_row(const float *x, int cols, int k, int8_t *q, float *d, int1
 /* FastMath.IntDot (src/FastMath.cs:105-214) for Q8_0 / Q4_K / Q6_K weights. */
 int wlo_int_dot(int type, const uint8_t *b, const int8_t *q, const float *d,
                 const int16_t *bsums, int n, float *out);
+/* FastMath.CanIntDot / NeedsK / Fits (src/FastMath.cs:27-34). */
+int wlo_can_int_dot(int type);
+int wlo_int_fits(int type, int cols);
+/* Transformer.MatMul's integer branch (src/Transformer.cs:504-524): each of the T rows of x
+ * quantized (FastMath.Quantize, Q8_K for the K-quants), then y[t][r] = FastMath.IntDot. Returns
+ * 0, -1 when the type has no integer dot or the rows are not whole activation blocks. */
+int wlo_int_matmul(int type, const uint8_t *data, int rows, int cols, int64_t row_bytes,
+                   const float *x, int T, float *y, int threads);
 
 /* Table data of src/IqTables.cs:9-57 (kmask, ksigns, kvalues, iq2xxs grid). */
 const uint64_t *wlo_iq2xxs_grid(void);

@@ -104,3 +104,54 @@ def test_one_expert_equals_dense(ctx):
     dense = Transformer.SwiGlu(wg, wu, wd, x, T)
     assert runs == 1
     assert np.array_equal(moe.view(np.uint32), dense.view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 8, 11])
+@pytest.mark.parametrize("types", [(12, 12), (12, 14), (8, 8), (13, 14), (2, 8)])
+@pytest.mark.parametrize("shape", [(16, 4, 512, 256), (128, 8, 512, 256)], ids=lambda s: "ne%d_k%d" % s[:2])
+def test_moe_ffn_int_dot_is_bit_identical(ctx, T, types, shape):
+    # Transformer.IntDot on: the experts' gate/up and down take MatMul's integer branch
+    # (src/Transformer.cs:288,241-251,504-524), so every output is the oracle's bits
+    ne, k, embd, ff = shape
+    gt, dt = types
+    gate = blocks(gt, ne * ff, embd, seed=11)
+    up = blocks(gt, ne * ff, embd, seed=12)
+    down = blocks(dt, ne * embd, ff, seed=13)
+    x = np.random.default_rng(14).standard_normal((T, embd), dtype=np.float32)
+    logits = np.random.default_rng(15).standard_normal((T, ne), dtype=np.float32)
+    wg = ctx.upload(gt, gate, ff, embd, experts=ne)
+    wu = ctx.upload(gt, up, ff, embd, experts=ne)
+    wd = ctx.upload(dt, down, embd, ff, experts=ne)
+    ctx.IntDot = True
+    try:
+        got, runs = Transformer.MoeFfn(logits, wg, wu, wd, x, T, k, True)
+    finally:
+        ctx.IntDot = False
+    want, oruns = oracle.moe_ffn(logits, k, True, gt, gate, gt, up, dt, down, ff, embd, x, T, each_token=True,
+                                 int_dot=True)
+    if T <= 8:
+        assert runs == oruns
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), int((got != want).sum())
+    for w in (wg, wu, wd):
+        w.free()
+
+
+def test_moe_int_dot_leaves_other_formats_on_the_float_path(ctx):
+    # IQ4_XS has no integer dot (FastMath.CanIntDot): with IntDot on, its down product stays on
+    # the float kernels while Q4_K gate/up take the integer branch
+    ne, k, embd, ff, T = 16, 4, 512, 256, 3
+    gate, up, down = blocks(12, ne * ff, embd, seed=21), blocks(12, ne * ff, embd, seed=22), blocks(23, ne * embd, ff, 23)
+    x = np.random.default_rng(24).standard_normal((T, embd), dtype=np.float32)
+    logits = np.random.default_rng(25).standard_normal((T, ne), dtype=np.float32)
+    wg, wu = ctx.upload(12, gate, ff, embd, experts=ne), ctx.upload(12, up, ff, embd, experts=ne)
+    wd = ctx.upload(23, down, embd, ff, experts=ne)
+    ctx.IntDot = True
+    try:
+        got, _ = Transformer.MoeFfn(logits, wg, wu, wd, x, T, k, True)
+    finally:
+        ctx.IntDot = False
+    want, _ = oracle.moe_ffn(logits, k, True, 12, gate, 12, up, 23, down, ff, embd, x, T, each_token=True,
+                             int_dot=True)
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.std(want)
+    for w in (wg, wu, wd):
+        w.free()

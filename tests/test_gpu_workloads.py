@@ -231,5 +231,15 @@ def test_qwen3moe_experts(ctx, T):
                                  each_token=True)
     assert runs == oruns
     assert np.max(np.abs(got - want)) <= 1e-4 * np.std(want)
+    # the integer branch (IntDot) at the same shapes: FastMath.IntDot's bits
+    ctx.IntDot = True
+    try:
+        got, runs = Transformer.MoeFfn(logits, wg, wu, wd, x, T, k, True)
+    finally:
+        ctx.IntDot = False
+    want, oruns = oracle.moe_ffn(logits, k, True, int(Q4_K), gate, int(Q4_K), up, int(Q4_K), down, ff, embd, x, T,
+                                 each_token=True, int_dot=True)
+    assert runs == oruns
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     for w in (wg, wu, wd):
         w.free()

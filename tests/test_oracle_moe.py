@@ -104,3 +104,80 @@ def test_quantizer_known_answers():
         assert bs[j] == int(np.sum(q[j * 16:(j + 1) * 16].astype(np.int32)))
     q, d, _ = oracle.quantize_row(np.zeros(256, np.float32), 1)
     assert d[0] == 0 and np.all(q == 0)
+
+
+def _compose_int_matmul(t, data, rows, cols, x):
+    """MatMul's integer branch from the oracle's pinned pieces: FastMath.Quantize of each token
+    (quantize_row), then FastMath.IntDot per (token, row)."""
+    k = t in (oracle.Q4_K, oracle.Q5_K, oracle.Q6_K)
+    rb = oracle.row_bytes(t, cols)
+    y = np.empty((x.shape[0], rows), np.float32)
+    for tok in range(x.shape[0]):
+        q, d, bs = oracle.quantize_row(x[tok], k)
+        for r in range(rows):
+            y[tok, r] = oracle.int_dot(t, data[r * rb:(r + 1) * rb], q, d, bs)
+    return y
+
+
+def _silu_mul(g, u):
+    """SwiGlu's a / (1f + (float)Math.Exp(-a)) * u in float32 (src/Transformer.cs:247)."""
+    g, u = g.astype(np.float32), u.astype(np.float32)
+    e = np.exp(-g.astype(np.float64)).astype(np.float32)
+    return (g / (np.float32(1) + e) * u).astype(np.float32)
+
+
+def test_int_matmul_is_quantize_then_int_dot():
+    r = oracle.Rng(11)
+    for t, cols in ((oracle.Q8_0, 96), (oracle.Q4_K, 512), (oracle.Q6_K, 256), (oracle.Q5_K, 256)):
+        data = oracle.matrix(r, t, 9, cols, 0.1)
+        x = r.normals(3 * cols).reshape(3, cols)
+        got = oracle.int_matmul(t, data, 9, cols, x)
+        assert np.array_equal(got.view(np.uint32), _compose_int_matmul(t, data, 9, cols, x).view(np.uint32)), t
+
+
+def test_swiglu_int_dot_is_its_products_in_the_integer_branch():
+    # Transformer.IntDot on: gate, up and down each take MatMul's integer branch; IQ4_XS has no
+    # integer dot, so its product stays on the float path (src/Transformer.cs:488-492,504)
+    embd, ff, T = 256, 512, 3
+    r = oracle.Rng(12)
+    x = r.normals(T * embd).reshape(T, embd)
+    for gt, dt in ((oracle.Q4_K, oracle.Q6_K), (oracle.Q8_0, oracle.IQ4_XS)):
+        gate, up = oracle.matrix(r, gt, ff, embd, 0.08), oracle.matrix(r, gt, ff, embd, 0.08)
+        down = oracle.matrix(r, dt, embd, ff, 0.06)
+        got = oracle.swiglu(gt, gate, gt, up, dt, down, ff, embd, x, T, each_token=True, int_dot=True)
+        h = _silu_mul(_compose_int_matmul(gt, gate, ff, embd, x), _compose_int_matmul(gt, up, ff, embd, x))
+        if dt == oracle.IQ4_XS:
+            want = oracle.matmul(dt, down, embd, ff, h, T, each_token=True)
+        else:
+            want = _compose_int_matmul(dt, down, embd, ff, h)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (gt, dt)
+
+
+def test_moe_ffn_int_dot_restated():
+    # MoeFfn (src/Transformer.cs:259-294) under IntDot: experts in ascending id, each one's
+    # tokens gathered in token order, SwiGlu on the expert's slices, out[tok] += w * y
+    ne, k, embd, ff, T = 6, 2, 256, 256, 4
+    r = oracle.Rng(13)
+    gt, dt = oracle.Q4_K, oracle.Q6_K
+    gate = oracle.matrix(r, gt, ne * ff, embd, 0.08)
+    up = oracle.matrix(r, gt, ne * ff, embd, 0.08)
+    down = oracle.matrix(r, dt, ne * embd, ff, 0.06)
+    x = r.normals(T * embd).reshape(T, embd)
+    logits = r.normals(T * ne).reshape(T, ne)
+    got, runs = oracle.moe_ffn(logits, k, True, gt, gate, gt, up, dt, down, ff, embd, x, T, int_dot=True)
+    gsz, dsz = ff * oracle.row_bytes(gt, embd), embd * oracle.row_bytes(dt, ff)
+    sel = [oracle.route(logits[t], k, True)[:2] for t in range(T)]
+    want = np.zeros((T, embd), np.float32)
+    used = 0
+    for e in range(ne):
+        pairs = [(t, float(sel[t][1][j])) for t in range(T) for j in range(k) if sel[t][0][j] == e]
+        if not pairs:
+            continue
+        used += 1
+        xe = x[[t for t, _ in pairs]]
+        ye = oracle.swiglu(gt, gate[e * gsz:(e + 1) * gsz], gt, up[e * gsz:(e + 1) * gsz], dt,
+                           down[e * dsz:(e + 1) * dsz], ff, embd, xe, len(pairs), int_dot=True)
+        for i, (t, w) in enumerate(pairs):
+            want[t] = (want[t] + np.float32(w) * ye[i]).astype(np.float32)
+    assert runs == used
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

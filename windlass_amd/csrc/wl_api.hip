@@ -772,9 +772,10 @@ extern "C" int wl_dequant_f32(wl_ctx *c, const wl_weight *w, int64_t row0, int64
 
 // --------------------------------------------------------------------------------- MoE
 
-// scratch layout in S_MOE: sel | wts | prob | plan | h | yd
+// scratch layout in S_MOE: sel | wts | prob | plan | h | yd | qx | qh (the last two: IntDot's
+// quantized activations of x and h, sized for Q8_K, the larger layout)
 struct MoeScratch {
-  size_t sel, wts, prob, plan, h, yd, total;
+  size_t sel, wts, prob, plan, h, yd, qx, qh, total;
 };
 
 static MoeScratch moe_layout(int T, int k, int ne, int ff, int embd) {
@@ -787,6 +788,12 @@ static MoeScratch moe_layout(int T, int k, int ne, int ff, int embd) {
   s.plan = o; o = al(o + sizeof(wl::MoePlan));
   s.h = o; o = al(o + (size_t)T * k * ff * 4);
   s.yd = o; o = al(o + (size_t)T * k * embd * 4);
+  const int64_t qx = wl::qacts_bytes(T, embd, 1) > wl::qacts_bytes(T, embd, 0) ? wl::qacts_bytes(T, embd, 1)
+                                                                                 : wl::qacts_bytes(T, embd, 0);
+  const int64_t qh = wl::qacts_bytes(T * k, ff, 1) > wl::qacts_bytes(T * k, ff, 0) ? wl::qacts_bytes(T * k, ff, 1)
+                                                                                     : wl::qacts_bytes(T * k, ff, 0);
+  s.qx = o; o = al(o + (size_t)qx);
+  s.qh = o; o = al(o + (size_t)qh);
   s.total = o;
   return s;
 }
@@ -845,6 +852,12 @@ static int moe_dev(wl_ctx *c, const float *d_logits, int32_t k, int32_t renorm, 
     m.out = d_out + (int64_t)t0 * embd;
     m.sel = (int *)(b + s.sel); m.wts = (float *)(b + s.wts); m.prob = (float *)(b + s.prob);
     m.plan = (wl::MoePlan *)(b + s.plan); m.h = (float *)(b + s.h); m.yd = (float *)(b + s.yd);
+    // Transformer.IntDot: each product of the experts' SwiGlu whose type and width allow it
+    // takes MatMul's integer branch (src/Transformer.cs:288,241-251,488-524)
+    m.gu_int = c->int_dot && wl::intdot_supports(g->type) && wl::intdot_fits(g->type, embd);
+    m.d_int = c->int_dot && wl::intdot_supports(d->type) && wl::intdot_fits(d->type, ff);
+    m.qx = wl::qacts_at(b + s.qx, Tc, embd, wl::intdot_needs_k(g->type) ? 1 : 0);
+    m.qh = wl::qacts_at(b + s.qh, Tc * k, ff, wl::intdot_needs_k(d->type) ? 1 : 0);
     WL_HIP(wl::moe_launch(m, c->num_cu, c->stream), "moe launch");
   }
   return WL_OK;

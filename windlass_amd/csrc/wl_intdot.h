@@ -47,6 +47,17 @@ int intmma_max_tokens(int type, int cols, int nm);  // 0 when the kernel does no
 hipError_t intmma_launch(int type, const uint8_t *w, const uint8_t *w2, int64_t row_bytes, int rows, int cols,
                          QActsDev qa, int T, float *y, int ldy, hipStream_t st);
 
+struct MoePlan;
+// The integer products of routed experts (MoeFfn's SwiGlu under IntDot, src/Transformer.cs:
+// 288,241-251,504-524), one launch for every slot of the plan: slot s multiplies expert
+// slot_expert[s] of the stacked tensors (estride bytes apart) with its tokens' activations
+// (rows slot_pair of qa when x_by_pair, else slot_tok) into rows slot_pair of y. T: the most
+// tokens a slot may hold (<= 8); slots: the most slots the plan may use. Each (row, token) is
+// FastMath.IntDot's bits, as for intdot_launch. w2 non-null: y = silu(gate) * up.
+hipError_t intdot_moe_launch(int type, const uint8_t *w, const uint8_t *w2, int64_t row_bytes, int64_t estride,
+                             int rows, int cols, QActsDev qa, const MoePlan *plan, int x_by_pair, int T, int slots,
+                             float *y, int ldy, int num_cu, hipStream_t st);
+
 // SwiGlu's gate/up half on the integer kernels, one launch: y = silu(IntDot(gate)) * IntDot(up)
 // per (row, token) (src/Transformer.cs:245-247), both products on the same activations a.
 hipError_t intdot_swiglu_launch(int type, const uint8_t *wg, const uint8_t *wu, int64_t row_bytes, int rows,

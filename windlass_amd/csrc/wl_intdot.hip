@@ -17,6 +17,7 @@
 
 #include "wl_codecs2.h"
 #include "wl_gemv_impl.h"
+#include "wl_moe.h"
 
 #pragma clang fp contract(off)
 
@@ -385,6 +386,12 @@ struct IntArgs {
   float *y;
   int ldy;
   int nterm;  // float terms per row
+  // routed experts: workgroup row y of the grid runs slot y of the plan, on expert
+  // slot_expert of the stacked tensors (estride bytes apart) and the slot's tokens; activation
+  // row of its t-th token slot_pair (x_by_pair) or slot_tok, result row slot_pair
+  const MoePlan *plan;
+  int64_t estride;
+  int x_by_pair;
 };
 
 constexpr int kIntRows = 4;        // rows per group (of each matrix: 4 / NM)
@@ -427,13 +434,30 @@ __global__ __launch_bounds__(64 * kIntMaxWaves) void intdot_kernel(IntArgs a) {
   const int ld = (a.nterm + 3) & ~3;        // LDS row stride: 16-byte aligned rows
   const int slab = NM * R * TM * ld;          // floats of one LDS buffer
   const uint8_t *wm[2] = {a.w, a.w2};
+  int T = a.T, xr[TM], yr[TM];  // tokens; each one's activation and result rows
+#pragma unroll
+  for (int t = 0; t < TM; t++) xr[t] = yr[t] = t;
+  if (a.plan) {
+    const int slot = blockIdx.y;
+    if (slot >= a.plan->nslots) return;  // the whole workgroup: blockIdx.y is uniform
+    T = min(a.plan->slot_ntok[slot], TM);
+    const int64_t eo = (int64_t)a.plan->slot_expert[slot] * a.estride;
+    wm[0] += eo;
+    if (NM == 2) wm[1] += eo;
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+      if (t < T) {
+        yr[t] = a.plan->slot_pair[slot][t];
+        xr[t] = a.x_by_pair ? yr[t] : a.plan->slot_tok[slot][t];
+      }
+  }
 
   auto load_xs = [&](int b, typename IC::Xq(&xs)[TM]) {
 #pragma unroll
     for (int t = 0; t < TM; t++)
-      if (t < a.T)
-        IC::load_x(a.q + (int64_t)t * a.cols, a.d + (int64_t)t * (a.cols / ab),
-                   a.bs ? a.bs + (int64_t)t * (a.cols / 16) : nullptr, b, L, xs[t]);
+      if (t < T)
+        IC::load_x(a.q + (int64_t)xr[t] * a.cols, a.d + (int64_t)xr[t] * (a.cols / ab),
+                   a.bs ? a.bs + (int64_t)xr[t] * (a.cols / 16) : nullptr, b, L, xs[t]);
   };
   typename IC::Xq xs0[TM];
   if (SP && wv * BPW + bslot < nb) load_xs(wv * BPW + bslot, xs0);
@@ -464,7 +488,7 @@ __global__ __launch_bounds__(64 * kIntMaxWaves) void intdot_kernel(IntArgs a) {
         for (int r = 0; r < R; r++)
 #pragma unroll
           for (int t = 0; t < TM; t++) {
-            if (t < a.T) {
+            if (t < T) {
               int si = 0, sm = 0;
               if (live) IC::part(raw[m][r], L, xs[t], si, sm);
               IC::reduce(si, sm);  // every lane takes part (uniform over the wave)
@@ -477,10 +501,10 @@ __global__ __launch_bounds__(64 * kIntMaxWaves) void intdot_kernel(IntArgs a) {
     if (wv == 0) {
       for (int i = lane; i < R * TM; i += 64) {
         const int r = i % R, t = i / R, row = g * R + r;
-        if (t < a.T && row < a.rows) {
+        if (t < T && row < a.rows) {
           float s = sum_in_order(pb + (r * TM + t) * ld, a.nterm);
           if constexpr (NM == 2) s = silu_mul(s, sum_in_order(pb + ((R + r) * TM + t) * ld, a.nterm));
-          a.y[(int64_t)t * a.ldy + row] = s;
+          a.y[(int64_t)yr[t] * a.ldy + row] = s;
         }
       }
     }
@@ -495,40 +519,42 @@ static size_t lds_of(int nm, int tm, int nterm) {
   return sizeof(float) * 2 * kIntRows * tm * ((nterm + 3) & ~3);  // nm matrices of kIntRows / nm rows
 }
 
+// slots: grid rows (the plan's slots that may be used; 1 without a plan)
 template <class IC, int TM, int NM>
-static hipError_t launch_int(const IntArgs &a, int num_cu, hipStream_t st) {
+static hipError_t launch_int(const IntArgs &a, int num_cu, hipStream_t st, int slots = 1) {
   using C = typename IC::C;
   const int bpw = 64 / C::LPB, nb = a.cols / C::BLOCK;
   const int units = (nb + bpw - 1) / bpw;
   const int passes = (units + kIntMaxWaves - 1) / kIntMaxWaves;
   const int nwv = (units + passes - 1) / passes;
   const int ngroups = (a.rows + kIntRows / NM - 1) / (kIntRows / NM);
-  int nwg = (num_cu * 32 + nwv - 1) / nwv;  // about 32 waves per CU
+  int nwg = (num_cu * 32 + nwv * slots - 1) / (nwv * slots);  // about 32 waves per CU over all slots
   if (nwg > ngroups) nwg = ngroups;
+  if (nwg < 1) nwg = 1;
   const size_t smem = lds_of(NM, TM, a.nterm);
   if (passes == 1)
-    hipLaunchKernelGGL((intdot_kernel<IC, TM, NM, true>), dim3(nwg), dim3(64 * nwv), smem, st, a);
+    hipLaunchKernelGGL((intdot_kernel<IC, TM, NM, true>), dim3(nwg, slots), dim3(64 * nwv), smem, st, a);
   else
-    hipLaunchKernelGGL((intdot_kernel<IC, TM, NM, false>), dim3(nwg), dim3(64 * nwv), smem, st, a);
+    hipLaunchKernelGGL((intdot_kernel<IC, TM, NM, false>), dim3(nwg, slots), dim3(64 * nwv), smem, st, a);
   return hipGetLastError();
 }
 
 template <class IC, int NM>
-static hipError_t launch_int_tm(const IntArgs &a, int num_cu, hipStream_t st) {
-  if (a.T <= 1) return launch_int<IC, 1, NM>(a, num_cu, st);
-  if (a.T <= 2) return launch_int<IC, 2, NM>(a, num_cu, st);
-  if (a.T <= 4) return launch_int<IC, 4, NM>(a, num_cu, st);
-  return launch_int<IC, 8, NM>(a, num_cu, st);
+static hipError_t launch_int_tm(const IntArgs &a, int num_cu, hipStream_t st, int slots) {
+  if (a.T <= 1) return launch_int<IC, 1, NM>(a, num_cu, st, slots);
+  if (a.T <= 2) return launch_int<IC, 2, NM>(a, num_cu, st, slots);
+  if (a.T <= 4) return launch_int<IC, 4, NM>(a, num_cu, st, slots);
+  return launch_int<IC, 8, NM>(a, num_cu, st, slots);
 }
 
 template <int NM>
-static hipError_t launch_type(int type, const IntArgs &a, int num_cu, hipStream_t st) {
+static hipError_t launch_type(int type, const IntArgs &a, int num_cu, hipStream_t st, int slots = 1) {
   switch (type) {
-    case 12: return launch_int_tm<IQ4K, NM>(a, num_cu, st);
-    case 13: return launch_int_tm<IQ5K, NM>(a, num_cu, st);
-    case 14: return launch_int_tm<IQ6K, NM>(a, num_cu, st);
-    case 2: return launch_int_tm<IQ40, NM>(a, num_cu, st);
-    default: return launch_int_tm<IQ80, NM>(a, num_cu, st);
+    case 12: return launch_int_tm<IQ4K, NM>(a, num_cu, st, slots);
+    case 13: return launch_int_tm<IQ5K, NM>(a, num_cu, st, slots);
+    case 14: return launch_int_tm<IQ6K, NM>(a, num_cu, st, slots);
+    case 2: return launch_int_tm<IQ40, NM>(a, num_cu, st, slots);
+    default: return launch_int_tm<IQ80, NM>(a, num_cu, st, slots);
   }
 }
 
@@ -549,7 +575,7 @@ static hipError_t run(int type, const uint8_t *w, const uint8_t *w2, int64_t row
   if (!qa.q || !qa.d || (intdot_needs_k(type) && !qa.bsums)) return hipErrorInvalidValue;
   // two or more tokens of Q4_K / Q6_K: the int8 matrix cores, the same bits
   if (intmma_supports(type, cols, T, nm)) return intmma_launch(type, w, w2, row_bytes, rows, cols, qa, T, y, ldy, st);
-  const IntArgs a{w, w2, row_bytes, rows, cols, qa.q, qa.d, qa.bsums, T, y, ldy, nterm_of(type, cols)};
+  const IntArgs a{w, w2, row_bytes, rows, cols, qa.q, qa.d, qa.bsums, T, y, ldy, nterm_of(type, cols), nullptr, 0, 0};
   return nm == 2 ? launch_type<2>(type, a, num_cu, st) : launch_type<1>(type, a, num_cu, st);
 }
 
@@ -561,6 +587,19 @@ hipError_t intdot_launch(int type, const uint8_t *w, int64_t row_bytes, int rows
 hipError_t intdot_swiglu_launch(int type, const uint8_t *wg, const uint8_t *wu, int64_t row_bytes, int rows,
                                 int cols, QActsDev qa, int T, float *y, int ldy, int num_cu, hipStream_t st) {
   return run(type, wg, wu, row_bytes, rows, cols, qa, T, y, ldy, num_cu, st);
+}
+
+hipError_t intdot_moe_launch(int type, const uint8_t *w, const uint8_t *w2, int64_t row_bytes, int64_t estride,
+                             int rows, int cols, QActsDev qa, const MoePlan *plan, int x_by_pair, int T, int slots,
+                             float *y, int ldy, int num_cu, hipStream_t st) {
+  if (rows <= 0 || T <= 0 || slots <= 0) return hipSuccess;
+  const int nm = w2 ? 2 : 1;
+  if (!plan || !intdot_supports(type) || !intdot_fits(type, cols) || T > MOE_MAX_T) return hipErrorInvalidValue;
+  const int nterm = nterm_of(type, cols);
+  if (lds_of(nm, 8, nterm) > (size_t)kIntLds) return hipErrorInvalidValue;  // up to 8 tokens a slot
+  if (!qa.q || !qa.d || (intdot_needs_k(type) && !qa.bsums)) return hipErrorInvalidValue;
+  const IntArgs a{w, w2, row_bytes, rows, cols, qa.q, qa.d, qa.bsums, T, y, ldy, nterm, plan, estride, x_by_pair};
+  return nm == 2 ? launch_type<2>(type, a, num_cu, st, slots) : launch_type<1>(type, a, num_cu, st, slots);
 }
 
 }  // namespace wl

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "wl_intdot.h"
+
 namespace wl {
 
 constexpr int MOE_MAX_T = 8;   // tokens per pass (larger batches run in passes of 8)
@@ -49,6 +51,10 @@ struct MoeLaunch {
   MoePlan *plan;
   float *h;   // [pairs][ff]
   float *yd;  // [pairs][embd]
+  // Transformer.IntDot: gate/up (gu_int) and down (d_int) on the integer kernels, with x
+  // quantized into qx and h into qh
+  int gu_int, d_int;
+  QActsDev qx, qh;
 };
 
 bool moe_supports(int type);

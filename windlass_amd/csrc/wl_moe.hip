@@ -381,16 +381,34 @@ hipError_t moe_launch(const MoeLaunch &m, int num_cu, hipStream_t st) {
   hipError_t err = route_plan_launch(m, st);
   if (err != hipSuccess) return err;
   const int max_slots = m.T * m.k < m.ne ? m.T * m.k : m.ne;
-  MoeGemvArgs gu{};
-  gu.plan = m.plan;
-  gu.w = m.gate; gu.w2 = m.up; gu.row_bytes = m.gu_row_bytes; gu.rows = m.ff; gu.cols = m.embd;
-  gu.x = m.x; gu.ldx = m.embd; gu.x_by_pair = 0; gu.y = m.h; gu.ldy = m.ff;
-  if ((err = launch_moe_type<2>(m.gu_type, gu, m.T, max_slots, num_cu, st)) != hipSuccess) return err;
-  MoeGemvArgs dn{};
-  dn.plan = m.plan;
-  dn.w = m.down; dn.w2 = nullptr; dn.row_bytes = m.d_row_bytes; dn.rows = m.embd; dn.cols = m.ff;
-  dn.x = m.h; dn.ldx = m.ff; dn.x_by_pair = 1; dn.y = m.yd; dn.ldy = m.embd;
-  if ((err = launch_moe_type<1>(m.d_type, dn, m.T, max_slots, num_cu, st)) != hipSuccess) return err;
+  if (m.gu_int) {
+    // MatMul's integer branch for gate and up: the tokens' activations quantized once
+    if ((err = quantize_launch(m.x, m.T, m.embd, intdot_needs_k(m.gu_type) ? 1 : 0, m.qx, st)) != hipSuccess) return err;
+    if ((err = intdot_moe_launch(m.gu_type, m.gate, m.up, m.gu_row_bytes, (int64_t)m.ff * m.gu_row_bytes, m.ff,
+                                 m.embd, m.qx, m.plan, 0, m.T, max_slots, m.h, m.ff, num_cu, st)) != hipSuccess)
+      return err;
+  } else {
+    MoeGemvArgs gu{};
+    gu.plan = m.plan;
+    gu.w = m.gate; gu.w2 = m.up; gu.row_bytes = m.gu_row_bytes; gu.rows = m.ff; gu.cols = m.embd;
+    gu.x = m.x; gu.ldx = m.embd; gu.x_by_pair = 0; gu.y = m.h; gu.ldy = m.ff;
+    if ((err = launch_moe_type<2>(m.gu_type, gu, m.T, max_slots, num_cu, st)) != hipSuccess) return err;
+  }
+  if (m.d_int) {
+    // every pair's row of h quantized (each token's k choices are distinct experts, so all
+    // T * k rows were written)
+    if ((err = quantize_launch(m.h, m.T * m.k, m.ff, intdot_needs_k(m.d_type) ? 1 : 0, m.qh, st)) != hipSuccess)
+      return err;
+    if ((err = intdot_moe_launch(m.d_type, m.down, nullptr, m.d_row_bytes, (int64_t)m.embd * m.d_row_bytes, m.embd,
+                                 m.ff, m.qh, m.plan, 1, m.T, max_slots, m.yd, m.embd, num_cu, st)) != hipSuccess)
+      return err;
+  } else {
+    MoeGemvArgs dn{};
+    dn.plan = m.plan;
+    dn.w = m.down; dn.w2 = nullptr; dn.row_bytes = m.d_row_bytes; dn.rows = m.embd; dn.cols = m.ff;
+    dn.x = m.h; dn.ldx = m.ff; dn.x_by_pair = 1; dn.y = m.yd; dn.ldy = m.embd;
+    if ((err = launch_moe_type<1>(m.d_type, dn, m.T, max_slots, num_cu, st)) != hipSuccess) return err;
+  }
   const int64_t total = (int64_t)m.T * m.embd;
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, m.plan, m.yd, m.T,
                      m.k, m.embd, m.out);
