@@ -274,6 +274,13 @@ typedef struct wl_layer_desc {
   int32_t embd, heads, kv_heads, head_dim, rope_dims, neox;
   double rope_base, rope_freq_scale;
   float eps, attention_scale, residual_scale;
+  /* MoeFfn (src/Transformer.cs:229,259-311) when ffn_gate_inp (the router, [n_expert][embd]) is
+   * set: ffn_gate / ffn_up / ffn_down are then the stacked experts, expert_used of them chosen
+   * per token (weights renormalised when expert_weights_norm). The shared expert
+   * (ffn_*_shexp, qwen2moe) is optional, and so is its gate ffn_gate_inp_shexp ([1][embd]):
+   * without it the shared expert's weight is 1. NULL ffn_gate_inp: the dense SwiGLU FFN. */
+  const wl_weight *ffn_gate_inp, *ffn_gate_shexp, *ffn_up_shexp, *ffn_down_shexp, *ffn_gate_inp_shexp;
+  int32_t expert_used, expert_weights_norm;
 } wl_layer_desc;
 
 /* Transformer.Layer (src/Transformer.cs:177-232) for T tokens at positions pos0.. of one

@@ -77,3 +77,41 @@ def tiny_model_gguf(path, key, context_length=64):
             tensors.append((gname, [x.cols, x.rows], int(x.type), x.data))
     write_gguf(path, md, tensors)
     return arch
+
+
+def tiny_moe_gguf(path, key, context_length=64, omit=None):
+    """The tiny MoE model of tiny_model.build_moe as a GGUF file in TinyMoe's layout
+    (tests/TinyMoe.cs:56-80,129-147): expert keys, stacked expert tensors with dims
+    [cols, rows, experts], the router [embd, n], the shared expert's gate as embd values. omit:
+    a tensor name (without .weight) to leave out."""
+    from tiny_model import EMBD, EPS, HEADS, KV_HEADS, MOE_FF, MOE_SPECS, build_moe
+    layout, _, n, used, layers, _, norm_key, _ = MOE_SPECS[key]
+    arch, t, _ = build_moe(key)
+    a = layout + "."
+    md = [("general.architecture", STR, layout), ("general.name", STR, key),
+          (a + "block_count", U32, layers), (a + "embedding_length", U32, EMBD),
+          (a + "feed_forward_length", U32, MOE_FF),
+          (a + "attention.head_count", U32, HEADS), (a + "attention.head_count_kv", U32, KV_HEADS),
+          (a + "rope.freq_base", F32, 1000000.0 if layout in ("qwen2moe", "qwen3moe") else 500000.0),
+          (a + "attention.layer_norm_rms_epsilon", F32, float(EPS)), (a + "context_length", U32, context_length),
+          (a + "expert_count", U32, n), (a + "expert_used_count", U32, used),
+          (a + "expert_feed_forward_length", U32, MOE_FF)]
+    if layout == "qwen2moe":
+        md.append((a + "expert_shared_feed_forward_length", U32, MOE_FF))
+    if norm_key >= 0:
+        md.append((a + "expert_weights_norm", BOOL, bool(norm_key)))
+    tensors = []
+    for name, x in t.items():
+        if name == omit:
+            continue
+        gname = name if name.endswith(".bias") else name + ".weight"
+        if isinstance(x, np.ndarray):
+            tensors.append((gname, [x.size], 0, np.ascontiguousarray(x, np.float32).view(np.uint8)))
+        elif name.endswith("ffn_gate_inp_shexp"):
+            tensors.append((gname, [x.cols], int(x.type), x.data))
+        elif getattr(x, "experts", 1) > 1 or name.endswith("_exps"):
+            tensors.append((gname, [x.cols, x.rows, x.experts], int(x.type), x.data))
+        elif not (name == "output" and x is t["token_embd"]):
+            tensors.append((gname, [x.cols, x.rows], int(x.type), x.data))
+    write_gguf(path, md, tensors)
+    return arch

@@ -134,8 +134,11 @@ def test_tiny_model_config(tmp_path, key):
 
 @pytest.mark.parametrize("md,err", [
     ([("general.architecture", STR, "gpt2")], "architecture"),
-    ([("general.architecture", STR, "qwen3moe"), ("qwen3moe.expert_count", U32, 8)], "expert"),
-    ([("general.architecture", STR, "llama"), ("llama.expert_count", U32, 8)], "expert"),
+    ([("general.architecture", STR, "qwen3moe")], "expert_count"),
+    ([("general.architecture", STR, "qwen3moe"), ("qwen3moe.expert_count", U32, 8)], "0 experts used"),
+    ([("general.architecture", STR, "mixtral"), ("mixtral.expert_count", U32, 4),
+      ("mixtral.expert_used_count", U32, 5)], "5 experts used per token of 4"),
+    ([("general.architecture", STR, "qwen2"), ("qwen2.expert_count", U32, 8)], "cannot have expert layers"),
     ([("general.architecture", STR, "llama"), ("llama.embedding_length", U32, 64), ("llama.block_count", U32, 1),
       ("llama.attention.head_count", U32, 6), ("llama.attention.head_count_kv", U32, 4)], "divide"),
     ([("general.architecture", STR, "llama"), ("llama.embedding_length", U32, 64), ("llama.block_count", U32, 1),
@@ -190,3 +193,31 @@ def test_linear_rope_scaling(tmp_path):
                    ("llama.block_count", U32, 1), ("llama.attention.head_count", U32, 4),
                    ("llama.rope.scaling.type", STR, "linear"), ("llama.rope.scaling.factor", F32, 4.0)], [])
     assert model_config(GgufModelFile.Open(p)).rope_freq_scale == 0.25
+
+
+@pytest.mark.parametrize("key,norm", [("moe-qwen3moe-q4_K-e8k3-dense1", True), ("moe-qwen2moe-q4_K-e8k2", False),
+                                      ("moe-qwen2moe-q6_K-e4k2-norm1-tied", True), ("moe-mixtral-q8_0-e8k2", True)])
+def test_tiny_moe_model_config(tmp_path, key, norm):
+    # ModelConfig.From's expert keys (src/ModelConfig.cs:73-86): the renormalisation default is
+    # on except for qwen2moe, and the file's expert_weights_norm wins
+    from gguf_writer import tiny_moe_gguf
+    from tiny_model import MOE_SPECS
+    p = tmp_path / "moe.gguf"
+    tiny_moe_gguf(p, key)
+    c = model_config(GgufModelFile.Open(p))
+    _, _, n, used, layers, _, _, _ = MOE_SPECS[key]
+    assert (c.expert_count, c.expert_used, c.expert_weights_norm, c.layers) == (n, used, norm, layers)
+
+
+def test_moe_layer_without_its_experts_is_refused(tmp_path):
+    from gguf_writer import tiny_moe_gguf
+    from windlass_amd.gguf import _check_ffn_layouts
+    p = tmp_path / "moe.gguf"
+    tiny_moe_gguf(p, "moe-qwen2moe-q4_K-e8k2", omit="blk.1.ffn_up_exps")
+    g = GgufModelFile.Open(p)
+    with pytest.raises(NotSupportedError, match="layer 1 lacks ffn_up_exps"):
+        _check_ffn_layouts(g, model_config(g))
+    tiny_moe_gguf(p, "moe-qwen2moe-q4_K-e8k2", omit="blk.0.ffn_gate_inp_shexp")
+    g = GgufModelFile.Open(p)
+    with pytest.raises(NotSupportedError, match="layer 0 lacks ffn_gate_inp_shexp"):
+        _check_ffn_layouts(g, model_config(g))

@@ -127,16 +127,27 @@ def test_gpu_greedy_tokens_match_cpu(gpu, key):
 
 
 def build_any(key):
-    """tiny_model.build, plus "llama-q4_K_M": llama-q4_K with the Q6_K tensors of llama-q6_K
-    in layer 0's attn_v and layer 1's ffn_down (Q4_K_M mixes the two across layers)."""
-    from tiny_model import build
+    """tiny_model.build (and build_moe for the MoE keys), plus "llama-q4_K_M": llama-q4_K with
+    the Q6_K tensors of llama-q6_K in layer 0's attn_v and layer 1's ffn_down (Q4_K_M mixes the
+    two across layers). Returns (arch, tensors, ModelConfig)."""
+    from tiny_model import MOE_SPECS, build, build_moe, moe_norm
+    if key in MOE_SPECS:
+        arch, t, layers = build_moe(key)
+        layout, _, n, used, _, _, norm_key, _ = MOE_SPECS[key]
+        return arch, t, tiny_config(arch, layers, expert_count=n, expert_used=used,
+                                    expert_weights_norm=moe_norm(layout, norm_key))
     if key != "llama-q4_K_M":
-        return build(key)
+        arch, t = build(key)
+        return arch, t, tiny_config(arch)
     arch, t = build("llama-q4_K")
     _, t6 = build("llama-q6_K")
     for n in ("blk.0.attn_v", "blk.1.ffn_down"):
         t[n] = t6[n]
-    return arch, t
+    return arch, t, tiny_config(arch)
+
+
+def upload_tensor(ctx, n, x):
+    return ctx.upload(x.type, x.data, x.rows, x.cols, experts=getattr(x, "experts", 1), name=n)
 
 
 def device_model(ctx, key, max_positions=64):
@@ -145,22 +156,23 @@ def device_model(ctx, key, max_positions=64):
     caches on the device, the final norm, the output product and greedy sampling on the device
     (src/Engine.cs:356-360). Returns the model and the weights to free."""
     from windlass_amd import DeviceTransformer
-    arch, t = build_any(key)
+    arch, t, cfg = build_any(key)
     dev = torch.device("cuda:0")
     weights, vectors = {}, {}
     for n, x in t.items():
         if isinstance(x, np.ndarray):
             vectors[n] = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev)
         elif not (n == "output" and x is t["token_embd"]):  # a tied head reuses token_embd
-            weights[n] = ctx.upload(x.type, x.data, x.rows, x.cols, name=n)
-    return DeviceTransformer(ctx, tiny_config(arch), weights, vectors, max_positions), weights
+            weights[n] = upload_tensor(ctx, n, x)
+    return DeviceTransformer(ctx, cfg, weights, vectors, max_positions), weights
 
 
-def tiny_config(arch):
+def tiny_config(arch, layers=None, **moe):
     from tiny_model import EMBD, EPS, HEADS, KV_HEADS, LAYERS
     from windlass_amd import ModelConfig
-    return ModelConfig(layers=LAYERS, embd=EMBD, heads=HEADS, kv_heads=KV_HEADS, head_dim=EMBD // HEADS,
-                       neox=arch != "llama", rope_base=500000.0 if arch == "llama" else 1000000.0, eps=float(EPS))
+    return ModelConfig(layers=layers or LAYERS, embd=EMBD, heads=HEADS, kv_heads=KV_HEADS, head_dim=EMBD // HEADS,
+                       neox=arch != "llama", rope_base=500000.0 if arch == "llama" else 1000000.0, eps=float(EPS),
+                       **moe)
 
 
 @pytest.mark.gpu
@@ -248,7 +260,7 @@ def streamed_model(gpu, key, slots, max_positions=64):
     the rest resident. Returns the model, the stream and the resident weights to free."""
     from tiny_model import LAYERS
     from windlass_amd import DeviceTransformer, StageStream
-    arch, t = build_any(key)
+    arch, t, cfg = build_any(key)
     layers = [{n: (t["blk.%d.%s" % (l, n)].type, t["blk.%d.%s" % (l, n)].rows, t["blk.%d.%s" % (l, n)].cols,
                    t["blk.%d.%s" % (l, n)].data) for n in _LAYER_NAMES} for l in range(LAYERS)]
     stream = StageStream(gpu, layers, slots)
@@ -261,7 +273,7 @@ def streamed_model(gpu, key, slots, max_positions=64):
         elif not n.startswith("blk.") and not (n == "output" and x is t["token_embd"]):
             w2[n] = gpu.upload(x.type, x.data, x.rows, x.cols, name=n)
             resident.append(w2[n])
-    return DeviceTransformer(gpu, tiny_config(arch), w2, vectors, max_positions, stream=stream), stream, resident
+    return DeviceTransformer(gpu, cfg, w2, vectors, max_positions, stream=stream), stream, resident
 
 
 STREAM_KEYS = [k for k in ("llama-q4_K", "llama-bf16", "qwen2-q6_K-tied", "qwen3-q4_K") if k in SPECS] + \
@@ -325,3 +337,141 @@ def test_stage_stream_refuses_layers_with_other_tensors():
         StageStream(NoCtx(), [{"a": q8}, {"b": q8}])
     with pytest.raises(ShapeError, match="layer 1 a: 60 bytes"):
         StageStream(NoCtx(), [{"a": q8}, {"a": (GgmlType.Q8_0, 2, 32, np.zeros(60, np.uint8))}])
+
+
+# ------------------------------------------------------------------ mixture-of-experts models
+
+def _moe_keys():
+    from tiny_model import MOE_SPECS
+    return sorted(MOE_SPECS)
+
+
+@pytest.mark.parametrize("key", _moe_keys())
+def test_moe_ffn_restatement_matches_oracle(key):
+    """The tiny models' MoE FFN (router, Route, experts' SwiGlu, weighted sum) against the
+    oracle's MoeFfn on the same activations, bit for bit; the shared expert adds
+    sigmoid(gate . x) * SwiGlu_shexp(x) after the routed sum (src/Transformer.cs:296-309)."""
+    import oracle
+    from tiny_model import EMBD, MOE_FF
+    m = Model(key, oracle_matmul)
+    t = m.t
+    p = next("blk.%d." % l for l in range(m.layers) if "blk.%d.ffn_gate_inp" % l in t)
+    xn = np.random.default_rng(3).standard_normal((5, EMBD)).astype(np.float32)
+    r = t[p + "ffn_gate_inp"]
+    logits = oracle.matmul(r.type, r.data, r.rows, r.cols, xn, 5)
+    g, u, d = t[p + "ffn_gate_exps"], t[p + "ffn_up_exps"], t[p + "ffn_down_exps"]
+    want, _ = oracle.moe_ffn(logits, m.used, m.renorm, g.type, g.data, u.type, u.data, d.type, d.data, MOE_FF, EMBD,
+                             xn, 5)
+    if p + "ffn_gate_shexp" in t:
+        sg, su, sd = t[p + "ffn_gate_shexp"], t[p + "ffn_up_shexp"], t[p + "ffn_down_shexp"]
+        sh = oracle.swiglu(sg.type, sg.data, su.type, su.data, sd.type, sd.data, sg.rows, EMBD, xn, 5)
+        gi = t[p + "ffn_gate_inp_shexp"]
+        gl = oracle.matmul(gi.type, gi.data, 1, EMBD, xn, 5)[:, 0]
+        f = (np.float32(1) / (np.float32(1) + np.exp(-gl.astype(np.float64)).astype(np.float32))).astype(np.float32)
+        want = (want + f[:, None] * sh).astype(np.float32)
+    got = m.moe_ffn(p, xn)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_one_expert_moe_equals_its_dense_twin():
+    # tests/MoeTests.cs:151-162: with one expert (weight 1 after renormalisation) a MoE model
+    # is its dense twin, whose ffn_gate/up/down hold that expert
+    key = "moe-qwen3moe-q6_K-e1k1"
+    moe, dense = Model(key, oracle_matmul), Model(key, oracle_matmul)
+    for l in range(dense.layers):
+        p = "blk.%d." % l
+        if p + "ffn_gate_inp" in dense.t:
+            for n in ("gate", "up", "down"):
+                dense.t[p + "ffn_" + n] = dense.t.pop(p + "ffn_%s_exps" % n).expert(0)
+            del dense.t[p + "ffn_gate_inp"]
+    a, la = moe.greedy(PROBE, 4, chunk=8)
+    b, lb = dense.greedy(PROBE, 4, chunk=8)
+    assert a == b
+    for x, y in zip(la, lb):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("key", _moe_keys())
+def test_gpu_moe_device_greedy_tokens_match_cpu(gpu, key):
+    """MoE layers in the device forward (router product, routing plan, experts, shared expert
+    with its sigmoid gate, residual) give the CPU backend's greedy tokens, prompt in chunks of
+    8 and 8 greedy steps; the logits stay within 1e-3 of their spread."""
+    want, want_logits = Model(key, oracle_matmul).greedy(PROBE, 8, chunk=8)
+    dm, weights = device_model(gpu, key)
+    got, got_logits = dm.greedy(PROBE, 8, chunk=8, keep_logits=True)
+    # the whole prompt in one pass: the GEMMs for attention and dense layers, experts in passes of 8
+    whole = dm.greedy(PROBE, 8)
+    for w in weights.values():
+        w.free()
+    for a, b in zip(want_logits, got_logits):
+        assert np.abs(a - b).max() <= 1e-3 * np.std(a), "%s: logits drift from the CPU backend" % key
+    assert got == want, "%s: greedy tokens %s, CPU backend %s" % (key, got, want)
+    assert whole == want, (whole, want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("key", ["moe-qwen2moe-q4_K-e8k2", "moe-qwen3moe-q4_K-e8k3-dense1"])
+def test_gpu_moe_batch_rows_equal_single_sequences(gpu, key):
+    """ForwardBatch over MoE layers: every row of a stacked step is bit-identical to that
+    sequence's own one-token step (the experts' products see one token's activations alone)."""
+    from windlass_amd import DeviceBatch
+    prompts = [PROBE[(3 * i) % 7:(3 * i) % 7 + 3 + (i * 5) % 10] for i in range(5)]
+    dm, weights = device_model(gpu, key, max_positions=32)
+    single = []
+    for p in prompts:
+        dm.length = 0
+        single.append(dm.greedy(p, 4, keep_logits=True))
+    toks, seen = DeviceBatch(dm, slots=5, slot_positions=32).greedy(prompts, 4, keep_logits=True)
+    for w in weights.values():
+        w.free()
+    for i in range(5):
+        assert toks[i] == single[i][0], (i, toks[i], single[i][0])
+        for s in range(5):
+            assert np.array_equal(seen[s][i].view(np.uint32), single[i][1][s].view(np.uint32)), (i, s)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("key", ["moe-qwen2moe-q4_K-e8k2", "moe-qwen3moe-q4_K-e8k3-dense1"])
+def test_gpu_moe_int_dot_greedy_tokens_match_cpu(gpu, key):
+    """--int-dot on a MoE model: every product of an integer-dot format (attention, dense FFN,
+    experts, shared expert) takes MatMul's integer branch on both sides; the F32 router stays
+    float. Same greedy tokens as the CPU backend with the oracle's integer products."""
+    import oracle
+
+    def int_mm(name, w, x):
+        x = np.ascontiguousarray(x, np.float32)
+        if oracle.lib().wlo_can_int_dot(w.type) and oracle.lib().wlo_int_fits(w.type, w.cols):
+            return oracle.int_matmul(w.type, w.data, w.rows, w.cols, x)
+        return oracle_matmul(name, w, x)
+    want, want_logits = Model(key, int_mm).greedy(PROBE, 6, chunk=8)
+    dm, weights = device_model(gpu, key)
+    gpu.IntDot = True
+    try:
+        got, got_logits = dm.greedy(PROBE, 6, chunk=8, keep_logits=True)
+    finally:
+        gpu.IntDot = False
+    for w in weights.values():
+        w.free()
+    for a, b in zip(want_logits, got_logits):
+        assert np.abs(a - b).max() <= 1e-3 * np.std(a), "%s: logits drift from the CPU backend" % key
+    assert got == want, (got, want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("key", ["moe-qwen3moe-q4_K-e8k3-dense1", "moe-qwen2moe-q6_K-e4k2-norm1-tied",
+                                 "moe-mixtral-q8_0-e8k2"])
+def test_gpu_moe_gguf_file_greedy_tokens_match_cpu(gpu, key, tmp_path):
+    """A tiny MoE model written as a GGUF file in the reference's layout (stacked [cols, rows,
+    experts] expert tensors, the router, the shared expert) and loaded by the reader gives the
+    CPU backend's greedy tokens."""
+    from gguf_writer import tiny_moe_gguf
+    from windlass_amd.gguf import load_device_model
+    p = tmp_path / "moe.gguf"
+    tiny_moe_gguf(p, key)
+    want, _ = Model(key, oracle_matmul).greedy(PROBE, 8, chunk=8)
+    dm, weights = load_device_model(gpu, p)
+    got = dm.greedy(PROBE, 8, chunk=8)
+    for w in weights.values():
+        w.free()
+    assert got == want, "%s: greedy tokens %s, CPU backend %s" % (key, got, want)

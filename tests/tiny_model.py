@@ -51,8 +51,94 @@ def vocab_size(arch, spm):
 
 
 class Tensor:
-    def __init__(self, t, rows, cols, data):
-        self.type, self.rows, self.cols, self.data = t, rows, cols, data
+    """rows x cols blocks of type t; experts > 1: that many such matrices stacked (a GGUF
+    [cols, rows, experts] tensor)."""
+
+    def __init__(self, t, rows, cols, data, experts=1):
+        self.type, self.rows, self.cols, self.data, self.experts = t, rows, cols, data, experts
+
+    def expert(self, e):
+        """WeightView.Slice (src/LayerStream.cs:26-34): expert e's rows x cols matrix."""
+        n = self.rows * oracle.row_bytes(self.type, self.cols)
+        return Tensor(self.type, self.rows, self.cols, self.data[e * n:(e + 1) * n])
+
+
+# MoeSpec (tests/TinyMoe.cs:10-37) and the reference's own MoE cases (tests/MoeTests.cs:68-78,
+# 153-156) on this path's formats: (layout, type, experts, used, layers, dense layers, norm key,
+# tied). Embd 256, 4 heads (2 KV), expert / shared / dense FF 256.
+MOE_SPECS = {
+    "moe-llama-q8_0-e4k2": ("llama", 8, 4, 2, 2, (), -1, False),
+    "moe-mixtral-q8_0-e8k2": ("mixtral", 8, 8, 2, 2, (), -1, False),
+    "moe-qwen2moe-q4_K-e8k2": ("qwen2moe", 12, 8, 2, 2, (), -1, False),
+    "moe-qwen2moe-q6_K-e4k2-norm1-tied": ("qwen2moe", 14, 4, 2, 2, (), 1, True),
+    "moe-qwen3moe-q4_K-e8k3-dense1": ("qwen3moe", 12, 8, 3, 3, (1,), -1, False),
+    "moe-qwen3moe-q6_K-e1k1": ("qwen3moe", 14, 1, 1, 2, (), -1, False),
+}
+MOE_FF = 256
+
+
+def moe_norm(layout, norm_key):
+    """ExpertWeightsNorm (src/ModelConfig.cs:83-86): renormalise unless qwen2moe; the key wins."""
+    return norm_key == 1 if norm_key >= 0 else layout != "qwen2moe"
+
+
+def build_moe(key):
+    """TinyMoe.Build (tests/TinyMoe.cs:51-153) with the oracle's Rng and Matrix, in the
+    reference's draw order. Returns (arch, tensors, layers); stacked expert tensors carry
+    experts = N, ffn_gate_inp is the F32 router [N][embd], ffn_gate_inp_shexp a [1][embd] F32
+    row."""
+    layout, t, N, used, layers, dense, norm_key, tied = MOE_SPECS[key]
+    qwen = layout in ("qwen2moe", "qwen3moe")
+    rng = oracle.Rng(SEED)
+    hd = EMBD // HEADS
+    qd, kd, X, H, F = HEADS * hd, KV_HEADS * hd, MOE_FF, MOE_FF, MOE_FF
+    vocab = vocab_size("qwen2" if qwen else "llama", False)
+
+    def mat(rows, cols, rms, ty=t):
+        return Tensor(ty, rows, cols, oracle.matrix(rng, ty, rows, cols, rms))
+
+    def norm(n):
+        return F32(1) + F32(0.2) * rng.normals(n).astype(F32)
+
+    def vec(n, scale):
+        return F32(scale) * rng.normals(n).astype(F32)
+
+    m = {"token_embd": mat(vocab, EMBD, 1.0)}
+    for l in range(layers):
+        p = "blk.%d." % l
+        m[p + "attn_norm"] = norm(EMBD)
+        m[p + "attn_q"] = mat(qd, EMBD, 0.08)
+        m[p + "attn_k"] = mat(kd, EMBD, 0.08)
+        m[p + "attn_v"] = mat(kd, EMBD, 0.08)
+        if layout == "qwen2moe":
+            m[p + "attn_q.bias"] = vec(qd, 0.1)
+            m[p + "attn_k.bias"] = vec(kd, 0.1)
+            m[p + "attn_v.bias"] = vec(kd, 0.1)
+        if layout == "qwen3moe":
+            m[p + "attn_q_norm"] = norm(hd)
+            m[p + "attn_k_norm"] = norm(hd)
+        m[p + "attn_output"] = mat(EMBD, qd, 0.08)
+        m[p + "ffn_norm"] = norm(EMBD)
+        if l in dense:
+            m[p + "ffn_gate"] = mat(F, EMBD, 0.08)
+            m[p + "ffn_up"] = mat(F, EMBD, 0.08)
+            m[p + "ffn_down"] = mat(EMBD, F, 0.06)
+            continue
+        m[p + "ffn_gate_inp"] = mat(N, EMBD, 0.1, oracle.F32)
+        g, u, d = mat(N * X, EMBD, 0.08), mat(N * X, EMBD, 0.08), mat(N * EMBD, X, 0.06)
+        m[p + "ffn_gate_exps"] = Tensor(t, X, EMBD, g.data, N)
+        m[p + "ffn_up_exps"] = Tensor(t, X, EMBD, u.data, N)
+        m[p + "ffn_down_exps"] = Tensor(t, EMBD, X, d.data, N)
+        if layout == "qwen2moe":
+            sg = vec(EMBD, 0.2)
+            m[p + "ffn_gate_inp_shexp"] = Tensor(oracle.F32, 1, EMBD, np.ascontiguousarray(sg, F32).view(np.uint8))
+            m[p + "ffn_gate_shexp"] = mat(H, EMBD, 0.08)
+            m[p + "ffn_up_shexp"] = mat(H, EMBD, 0.08)
+            m[p + "ffn_down_shexp"] = mat(EMBD, H, 0.06)
+    m["output_norm"] = norm(EMBD)
+    m["output"] = m["token_embd"] if tied else mat(vocab, EMBD, 0.08)
+    arch = "qwen2" if layout == "qwen2moe" else "qwen3" if layout == "qwen3moe" else "llama"
+    return arch, m, layers
 
 
 def build(key):
@@ -104,11 +190,24 @@ def rms_norm_rows(x, w):
     return (x * scale * w).astype(F32)
 
 
+def silu_mul(g, u):
+    """SwiGlu's g / (1 + exp(-g)) * u with the exponential in double (src/Transformer.cs:247)."""
+    g = np.asarray(g, F32)
+    e = np.exp(-g.astype(np.float64)).astype(F32)
+    return ((g / (F32(1) + e)).astype(F32) * np.asarray(u, F32)).astype(F32)
+
+
 class Model:
     def __init__(self, key, matmul):
         """matmul(name, tensor, x [T][cols] float32) -> y [T][rows] float32."""
         self.key = key
-        self.arch, self.t = build(key)
+        if key in MOE_SPECS:
+            self.arch, self.t, self.layers = build_moe(key)
+            layout, _, _, self.used, _, _, norm_key, _ = MOE_SPECS[key]
+            self.renorm = moe_norm(layout, norm_key)
+        else:
+            self.arch, self.t = build(key)
+            self.layers = LAYERS
         self.mm = matmul
         self.hd = EMBD // HEADS
         self.base = 500000.0 if self.arch == "llama" else 1000000.0
@@ -116,8 +215,8 @@ class Model:
         self.reset()
 
     def reset(self):
-        self.K = [np.zeros((0, KV_HEADS * self.hd), np.float16) for _ in range(LAYERS)]
-        self.V = [np.zeros((0, KV_HEADS * self.hd), np.float16) for _ in range(LAYERS)]
+        self.K = [np.zeros((0, KV_HEADS * self.hd), np.float16) for _ in range(self.layers)]
+        self.V = [np.zeros((0, KV_HEADS * self.hd), np.float16) for _ in range(self.layers)]
 
     def rope_table(self, pos):
         """RopeTable (src/Transformer.cs:396-414)."""
@@ -174,7 +273,7 @@ class Model:
         emb = t["token_embd"]
         rb = oracle.row_bytes(emb.type, EMBD)
         x = np.stack([oracle.decode(emb.type, emb.data[tok * rb:(tok + 1) * rb], EMBD) for tok in tokens]).astype(F32)
-        for l in range(LAYERS):
+        for l in range(self.layers):
             p = "blk.%d." % l
             xn = rms_norm_rows(x, t[p + "attn_norm"])
             q = self.mm(p + "attn_q", t[p + "attn_q"], xn)
@@ -197,14 +296,46 @@ class Model:
             att = self.attention(l, q, pos0)
             x = (x + self.mm(p + "attn_output", t[p + "attn_output"], att)).astype(F32)
             xn = rms_norm_rows(x, t[p + "ffn_norm"])
-            g = self.mm(p + "ffn_gate", t[p + "ffn_gate"], xn).astype(np.float64)
-            u = self.mm(p + "ffn_up", t[p + "ffn_up"], xn).astype(F32)
-            # silu: g / (1 + exp(-g)) * u, exp in double (src/Transformer.cs:247)
-            h = ((g.astype(F32) / (F32(1) + np.exp(-g).astype(F32))).astype(F32) * u).astype(F32)
-            x = (x + self.mm(p + "ffn_down", t[p + "ffn_down"], h)).astype(F32)
+            if p + "ffn_gate_inp" in t:
+                o = self.moe_ffn(p, xn)
+            else:
+                o = self.swiglu(p + "ffn_", t[p + "ffn_gate"], t[p + "ffn_up"], t[p + "ffn_down"], xn)
+            x = (x + o).astype(F32)
         rows = x if all_logits else x[-1:]
         xn = rms_norm_rows(rows, t["output_norm"])
         return self.mm("output", t["output"], xn)
+
+    def swiglu(self, name, gate, up, down, xn):
+        """SwiGlu (src/Transformer.cs:241-251)."""
+        h = silu_mul(self.mm(name + "gate", gate, xn), self.mm(name + "up", up, xn))
+        return self.mm(name + "down", down, h).astype(F32)
+
+    def moe_ffn(self, p, xn):
+        """MoeFfn (src/Transformer.cs:259-311): the router's logits, Route per token, every chosen
+        expert's SwiGlu on its tokens (experts in ascending id, tokens in order) added with its
+        weight, then the shared expert scaled by sigmoid(ffn_gate_inp_shexp . x)."""
+        t, T = self.t, xn.shape[0]
+        logits = self.mm(p + "ffn_gate_inp", t[p + "ffn_gate_inp"], xn)
+        routes = [oracle.route(logits[i], self.used, self.renorm)[:2] for i in range(T)]
+        out = np.zeros((T, EMBD), F32)
+        gate, up, down = t[p + "ffn_gate_exps"], t[p + "ffn_up_exps"], t[p + "ffn_down_exps"]
+        for e in range(gate.experts):
+            pairs = [(i, routes[i][1][j]) for i in range(T) for j in range(self.used) if routes[i][0][j] == e]
+            if not pairs:
+                continue
+            ye = self.swiglu(p + "ffn_exps%d_" % e, gate.expert(e), up.expert(e), down.expert(e),
+                             xn[[i for i, _ in pairs]])
+            for r, (i, w) in enumerate(pairs):
+                out[i] = (out[i] + F32(w) * ye[r]).astype(F32)
+        if p + "ffn_gate_shexp" in t:
+            sh = self.swiglu(p + "ffn_shexp_", t[p + "ffn_gate_shexp"], t[p + "ffn_up_shexp"],
+                             t[p + "ffn_down_shexp"], xn)
+            f = np.ones(T, F32)
+            if p + "ffn_gate_inp_shexp" in t:
+                gl = self.mm(p + "ffn_gate_inp_shexp", t[p + "ffn_gate_inp_shexp"], xn)[:, 0]
+                f = (F32(1) / (F32(1) + np.exp(-gl.astype(np.float64)).astype(F32))).astype(F32)
+            out = (out + f[:, None] * sh).astype(F32)
+        return out
 
     def greedy(self, prompt, steps, chunk=None):
         """Prompt (in chunks of `chunk` tokens when set), then `steps` greedy tokens (argmax,

@@ -286,7 +286,10 @@ class LayerDesc(ctypes.Structure):
         ("embd", ctypes.c_int32), ("heads", ctypes.c_int32), ("kv_heads", ctypes.c_int32),
         ("head_dim", ctypes.c_int32), ("rope_dims", ctypes.c_int32), ("neox", ctypes.c_int32),
         ("rope_base", ctypes.c_double), ("rope_freq_scale", ctypes.c_double),
-        ("eps", ctypes.c_float), ("attention_scale", ctypes.c_float), ("residual_scale", ctypes.c_float)]
+        ("eps", ctypes.c_float), ("attention_scale", ctypes.c_float), ("residual_scale", ctypes.c_float)] + [
+        (n, ctypes.c_void_p) for n in ("ffn_gate_inp", "ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp",
+                                       "ffn_gate_inp_shexp")] + [
+        ("expert_used", ctypes.c_int32), ("expert_weights_norm", ctypes.c_int32)]
 
 
 class Transformer:

@@ -49,9 +49,10 @@ struct wl_stage {
 // S_PART holds the K-chunk partials of split GEMV rows, S_XB the bf16 copy of x for the GEMM,
 // S_QA the 8-bit activations of the integer path.
 // S_L* are wl_layer_dev's activations (S_LO: wl_matmul_add_dev's product when the add is not
-// the GEMV's own store).
+// the GEMV's own store; S_LR the router's logits and the shared expert's gate, S_LM the MoE
+// FFN's output, S_LS the shared expert's).
 enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB, S_QA, S_ATT,
-       S_LXN, S_LQ, S_LK, S_LV, S_LATT, S_LO, S_LG, S_LU, S_ROWS, S_ARG, S_COUNT };
+       S_LXN, S_LQ, S_LK, S_LV, S_LATT, S_LO, S_LG, S_LU, S_LR, S_LM, S_LS, S_ROWS, S_ARG, S_COUNT };
 
 struct wl_ctx {
   int device;
@@ -1075,11 +1076,26 @@ static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, i
   if (T <= 0 || pos0 < 0 || E <= 0 || H <= 0 || KH <= 0 || H % KH || HD <= 0)
     return fail(WL_E_SHAPE, "wl_layer_dev: bad shape");
   const int QD = H * HD, KD = KH * HD;
-  const int64_t FF = L->ffn_gate->rows;
+  const bool moe = L->ffn_gate_inp != nullptr;
+  const bool shared = moe && L->ffn_gate_shexp;
+  int64_t FF = L->ffn_gate->rows;
   if (L->attn_q->cols != E || L->attn_q->rows != QD || L->attn_k->rows != KD || L->attn_v->rows != KD ||
       L->attn_output->cols != QD || L->attn_output->rows != E || L->ffn_gate->cols != E || L->ffn_up->rows != FF ||
       L->ffn_down->cols != FF || L->ffn_down->rows != E)
     return fail(WL_E_SHAPE, "wl_layer_dev: tensor shapes do not match the layer");
+  if (moe) {
+    // the router's shape here; moe_dev checks the experts and expert_used
+    if (L->ffn_gate_inp->cols != E || L->ffn_gate_inp->rows != L->ffn_gate->experts || L->ffn_gate_inp->experts != 1)
+      return fail(WL_E_SHAPE, "wl_layer_dev: ffn_gate_inp must be %d x %d", (int)L->ffn_gate->experts, E);
+    if (shared) {
+      const wl_weight *sg = L->ffn_gate_shexp, *su = L->ffn_up_shexp, *sd = L->ffn_down_shexp, *si = L->ffn_gate_inp_shexp;
+      if (!su || !sd) return fail(WL_E_ARG, "wl_layer_dev: the shared expert needs gate, up and down");
+      if (sg->cols != E || su->cols != E || su->rows != sg->rows || sd->rows != E || sd->cols != sg->rows ||
+          (si && (si->cols != E || si->rows != 1)))
+        return fail(WL_E_SHAPE, "wl_layer_dev: shared expert tensors have inconsistent shapes");
+      if (sg->rows > FF) FF = sg->rows;  // S_LG / S_LU hold either FFN's rows
+    }
+  }
   const int rd = L->rope_dims > 0 ? L->rope_dims : HD;
   if (rd > HD || rd % 2) return fail(WL_E_SHAPE, "wl_layer_dev: %d rotated of %d per head", rd, HD);
   int rc;
@@ -1134,17 +1150,39 @@ static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, i
   if ((rc = mm(L->attn_output, att, d_x, true))) return rc;
   // feed-forward block
   if ((rc = wl_rms_norm_dev(c, d_x, T, E, L->d_ffn_norm, L->eps, xn))) return rc;
-  // up to 8 rows (or every row with each): gate and up in one GEMV launch with the SiLU
-  // epilogue; a prompt: the two GEMMs, then the SiLU pass
-  const bool fused = L->ffn_gate->type == L->ffn_up->type &&
-                     (T <= 8 || each || int_path(c, L->ffn_gate) || !wl::gemm_supports(L->ffn_gate->type));
-  if (fused) {
-    if ((rc = wl_gate_up_dev(c, L->ffn_gate, L->ffn_up, -1, xn, T, g))) return rc;
-  } else {
-    if ((rc = mm(L->ffn_gate, xn, g, false)) || (rc = mm(L->ffn_up, xn, u, false))) return rc;
-    WL_HIP(wl::silu_mul_launch(g, u, (int64_t)T * FF, c->stream), "silu");
+  // SwiGlu (src/Transformer.cs:241-251) into y (added into y with add): up to 8 rows (or every
+  // row with each) gate and up in one GEMV launch with the SiLU epilogue; a prompt: the two
+  // GEMMs, then the SiLU pass
+  auto swiglu = [&](const wl_weight *wg, const wl_weight *wu, const wl_weight *wd, float *y, bool add) -> int {
+    const bool fused = wg->type == wu->type && (T <= 8 || each || int_path(c, wg) || !wl::gemm_supports(wg->type));
+    int r;
+    if (fused) {
+      if ((r = wl_gate_up_dev(c, wg, wu, -1, xn, T, g))) return r;
+    } else {
+      if ((r = mm(wg, xn, g, false)) || (r = mm(wu, xn, u, false))) return r;
+      WL_HIP(wl::silu_mul_launch(g, u, (int64_t)T * wg->rows, c->stream), "silu");
+    }
+    return mm(wd, g, y, add);
+  };
+  if (!moe) return swiglu(L->ffn_gate, L->ffn_up, L->ffn_down, d_x, true);
+  // MoeFfn (src/Transformer.cs:259-311): router logits, routed experts, the shared expert, then
+  // the residual add (:231)
+  const int ne = (int)L->ffn_gate->experts;
+  if ((rc = ensure(c, S_LR, (size_t)T * (ne > 1 ? ne : 1) * 4)) || (rc = ensure(c, S_LM, (size_t)T * E * 4)) ||
+      (shared && (rc = ensure(c, S_LS, (size_t)T * E * 4))))
+    return rc;
+  float *lg = (float *)c->buf[S_LR], *o = (float *)c->buf[S_LM], *sh = (float *)c->buf[S_LS];
+  if ((rc = mm(L->ffn_gate_inp, xn, lg, false))) return rc;
+  if ((rc = moe_dev(c, lg, L->expert_used, L->expert_weights_norm, L->ffn_gate, L->ffn_up, L->ffn_down, xn, T, o)))
+    return rc;
+  if (shared) {
+    if ((rc = swiglu(L->ffn_gate_shexp, L->ffn_up_shexp, L->ffn_down_shexp, sh, false))) return rc;
+    // the router's logits are used: its buffer takes the shared expert's gate
+    if (L->ffn_gate_inp_shexp && (rc = mm(L->ffn_gate_inp_shexp, xn, lg, false))) return rc;
+    WL_HIP(wl::shared_expert_launch(o, sh, L->ffn_gate_inp_shexp ? lg : nullptr, T, E, c->stream), "shared expert");
   }
-  return mm(L->ffn_down, g, d_x, true);
+  WL_HIP(wl::residual_launch(d_x, o, (int64_t)T * E, rs, c->stream), "residual");
+  return WL_OK;
 }
 
 extern "C" int wl_layer_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,

@@ -32,6 +32,9 @@ hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *
                             int heads, int kv_heads, int hd, int pos0, float scale, float *scratch, float *out,
                             int64_t ldo, const RowMap &rm, int max_n, hipStream_t st);
 hipError_t residual_launch(float *x, const float *o, int64_t n, float rs, hipStream_t st);
+// o [rows][dim] += f_t * sh, f_t = sigmoid(gl[t]) (gl null: 1): MoeFfn's shared expert.
+hipError_t shared_expert_launch(float *o, const float *sh, const float *gl, int64_t rows, int64_t dim,
+                                hipStream_t st);
 // Workgroups per row of the first argmax launch; scratch holds 2 * rows * argmax_parts(n) words.
 int argmax_parts(int64_t n);
 hipError_t argmax_launch(const float *logits, int rows, int64_t n, int *out, float *scratch, hipStream_t st);

@@ -458,6 +458,16 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *__restri
 }
 
 // AddBias (src/Transformer.cs:433-443): y[t][i] += b[i].
+// MoeFfn's shared expert (src/Transformer.cs:296-309): o[t][d] += f_t * sh[t][d], with
+// f_t = 1 / (1 + exp(-gl[t])) (the exponential in double, cast to float) or 1 without a gate.
+__global__ void shared_expert_kernel(float *__restrict__ o, const float *__restrict__ sh, const float *__restrict__ gl,
+                                     int64_t n, int64_t dim) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float f = gl ? 1.0f / (1.0f + (float)exp((double)(-gl[i / dim]))) : 1.0f;
+  o[i] += f * sh[i];
+}
+
 __global__ void bias_kernel(float *__restrict__ y, const float *__restrict__ b, int64_t n, int64_t dim) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] += b[i % dim];
@@ -562,6 +572,14 @@ hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *
   }
   hipLaunchKernelGGL(attention_kernel, dim3(heads, T), dim3(256), 0, st, q, ldq, K, V, kv_dim, heads, kv_heads, hd,
                      pos0, scale, scratch, (int64_t)max_n, out, ldo, rm.pos, rm.slot, rm.cap);
+  return hipGetLastError();
+}
+
+hipError_t shared_expert_launch(float *o, const float *sh, const float *gl, int64_t rows, int64_t dim,
+                                hipStream_t st) {
+  const int64_t n = rows * dim;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(shared_expert_kernel, dim3(blocks_of(n, 256)), dim3(256), 0, st, o, sh, gl, n, dim);
   return hipGetLastError();
 }
 

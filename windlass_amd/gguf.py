@@ -240,15 +240,18 @@ class GgufModelFile:
 # architectures the device forward runs, with their rotary pairing (False: adjacent values,
 # True: NeoX halves); the reference's other architectures are refused by model_config
 DENSE_ARCHS = {"llama": False, "qwen2": True, "qwen3": True, "granite": False}
-KNOWN_ARCHS = set(DENSE_ARCHS) | {"mixtral", "qwen2moe", "qwen3moe", "olmo2"}
+MOE_ARCHS = {"llama": False, "mixtral": False, "qwen2moe": True, "qwen3moe": True}  # may hold expert layers
+KNOWN_ARCHS = set(DENSE_ARCHS) | set(MOE_ARCHS) | {"olmo2"}
 
 
 def model_config(g):
     """ModelConfig.From (src/ModelConfig.cs:38-100) for the models the device forward runs:
-    llama, qwen2, qwen3, and granite without embedding or logit scales. Architectures outside the
-    reference's list, expert layers, OLMo 2's post-norms and granite's embedding/logit scales raise
-    NotSupportedError. RoPE scaling other than linear is recorded in `warnings`, as the reference
-    does, and the model runs without it."""
+    llama, qwen2, qwen3, granite without embedding or logit scales, and the expert models
+    (llama/mixtral, qwen2moe, qwen3moe: expert_count, expert_used_count, expert_weights_norm,
+    whose default renormalises except for qwen2moe). Architectures outside the reference's list,
+    OLMo 2's post-norms and granite's embedding/logit scales raise NotSupportedError. RoPE scaling
+    other than linear is recorded in `warnings`, as the reference does, and the model runs
+    without it."""
     from .model import ModelConfig
     arch = g.Get("general.architecture", "")
     if arch not in KNOWN_ARCHS:
@@ -261,8 +264,21 @@ def model_config(g):
         return cast(v)
 
     f32 = lambda v: float(np.float32(v))  # noqa: E731  (GGUF float keys are read as float32)
-    if arch not in DENSE_ARCHS or md("expert_count", 0) > 0:
-        raise NotSupportedError("%s has expert layers; the device forward runs dense layers" % arch)
+    experts = md("expert_count", 0)
+    if arch not in DENSE_ARCHS and arch not in MOE_ARCHS:
+        raise NotSupportedError("%s is not on the device forward" % arch)
+    if experts > 0 and arch not in MOE_ARCHS:
+        raise NotSupportedError("%s cannot have expert layers here (llama, mixtral, qwen2moe and qwen3moe can)" % arch)
+    if experts <= 0 and arch in ("qwen2moe", "qwen3moe", "mixtral"):
+        raise NotSupportedError("%s without %s.expert_count" % (arch, arch))
+    moe = {}
+    if experts > 0:
+        used = md("expert_used_count", 0)
+        if not 1 <= used <= experts:
+            raise NotSupportedError("%d experts used per token of %d" % (used, experts))
+        norm = g.Get("%s.expert_weights_norm" % arch, None)
+        moe = dict(expert_count=experts, expert_used=used,
+                   expert_weights_norm=bool(norm) if norm is not None else arch != "qwen2moe")
     embd, heads = md("embedding_length"), md("attention.head_count")
     kv_heads = md("attention.head_count_kv", heads)
     head_dim = md("attention.key_length", embd // heads)
@@ -285,9 +301,10 @@ def model_config(g):
             raise NotSupportedError("granite's embedding and logit scales are not on the device forward")
         residual_scale, attention_scale = md("residual_scale", 0.0, float), md("attention.scale", 0.0, float)
     return ModelConfig(layers=md("block_count"), embd=embd, heads=heads, kv_heads=kv_heads, head_dim=head_dim,
-                       rope_dims=rope_dims, neox=DENSE_ARCHS[arch], rope_base=md("rope.freq_base", 10000.0, f32),
-                       rope_freq_scale=freq_scale, eps=md("attention.layer_norm_rms_epsilon", 1e-5, f32),
-                       attention_scale=attention_scale, residual_scale=residual_scale, warnings=warnings)
+                       rope_dims=rope_dims, neox={**DENSE_ARCHS, **MOE_ARCHS}[arch],
+                       rope_base=md("rope.freq_base", 10000.0, f32), rope_freq_scale=freq_scale,
+                       eps=md("attention.layer_norm_rms_epsilon", 1e-5, f32), attention_scale=attention_scale,
+                       residual_scale=residual_scale, warnings=warnings, **moe)
 
 
 def _vector(ctx, g, t, dev):
@@ -317,14 +334,59 @@ def load_device_model(ctx, path, max_positions=None):
     g = GgufModelFile.Open(path)
     cfg = model_config(g)
     dev = torch.device("cuda:%d" % ctx.device)
+    _check_ffn_layouts(g, cfg)
     weights, vectors = {}, {}
     for t in g.Tensors:
         name = t.Name[:-len(".weight")] if t.Name.endswith(".weight") else t.Name
-        if len(t.Dims) == 1:
+        if name.endswith("ffn_gate_inp_shexp"):  # one row of embd values: the shared expert's gate
+            weights[name] = ctx.upload(t.Type, g.data(t), 1, t.ElementCount, name=name)
+        elif len(t.Dims) == 1:
             vectors[name] = _vector(ctx, g, t, dev)
         elif len(t.Dims) == 2:
             weights[name] = ctx.upload(t.Type, g.data(t), t.Rows, t.Cols, name=name)
+        elif len(t.Dims) == 3 and name.endswith("_exps"):  # [cols, rows, experts]: stacked experts
+            weights[name] = ctx.upload(t.Type, g.data(t), t.Dims[1], t.Cols, experts=t.Dims[2], name=name)
         else:
-            raise NotSupportedError("Tensor %s has %d dims; the device forward runs dense layers." % (t.Name, len(t.Dims)))
+            raise NotSupportedError("Tensor %s has %d dims." % (t.Name, len(t.Dims)))
     n = max_positions or int(g.Get(g.Get("general.architecture") + ".context_length", 4096))
     return DeviceTransformer(ctx, cfg, weights, vectors, n), weights
+
+
+def _check_ffn_layouts(g, cfg):
+    """Each layer's feed-forward tensors before anything is uploaded (src/ModelConfig.cs:94-100,
+    128-158): a layer with a router (ffn_gate_inp) in an expert model needs the three stacked
+    expert tensors, [embd, ff, n], [embd, ff, n] and [ff, embd, n], and a router of n x embd;
+    a shared expert needs all three of its matrices (and qwen2moe its gate); other layers need
+    the dense ffn_gate / ffn_up / ffn_down."""
+    have = {t.Name: t for t in g.Tensors}
+    for l in range(cfg.layers):
+        p = "blk.%d." % l
+
+        def need(*names):
+            for n in names:
+                if p + n + ".weight" not in have:
+                    raise NotSupportedError("layer %d lacks %s" % (l, n))
+        if cfg.expert_count > 0 and p + "ffn_gate_inp.weight" in have:
+            need("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps")
+            r = have[p + "ffn_gate_inp.weight"]
+            gt, ut, dt = (have[p + n + ".weight"] for n in ("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"))
+            n, e = cfg.expert_count, cfg.embd
+            if r.Dims != [e, n]:
+                raise NotSupportedError("layer %d: the router is %s, not [%d, %d]" % (l, r.Dims, e, n))
+            ff = gt.Dims[1] if len(gt.Dims) == 3 else -1
+            if gt.Dims != [e, ff, n] or ut.Dims != [e, ff, n] or dt.Dims != [ff, e, n]:
+                raise NotSupportedError("layer %d: expert tensors %s / %s / %s do not stack %d experts of %d x %d"
+                                        % (l, gt.Dims, ut.Dims, dt.Dims, n, ff, e))
+            shared = [p + s + ".weight" in have for s in ("ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp")]
+            if any(shared):
+                need("ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp")
+                if g.Get("general.architecture") == "qwen2moe":
+                    need("ffn_gate_inp_shexp")
+                si = have.get(p + "ffn_gate_inp_shexp.weight")
+                if si is not None and si.ElementCount != e:
+                    raise NotSupportedError("layer %d: the shared expert's gate has %d values, not %d"
+                                            % (l, si.ElementCount, e))
+            elif g.Get("general.architecture") == "qwen2moe":
+                need("ffn_gate_shexp")
+        else:
+            need("ffn_gate", "ffn_up", "ffn_down")

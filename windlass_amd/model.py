@@ -35,6 +35,9 @@ class ModelConfig:
     eps: float = 1e-5
     attention_scale: float = 0.0  # 0: 1/sqrt(head_dim)
     residual_scale: float = 0.0   # 0: 1
+    expert_count: int = 0         # MoE (src/ModelConfig.cs:26-31): experts per MoE layer, 0 for dense
+    expert_used: int = 0          # experts chosen per token
+    expert_weights_norm: bool = True  # renormalise the chosen weights (not qwen2moe by default)
     warnings: list = field(default_factory=list)  # ModelConfig.Warnings: what the model runs without
 
 
@@ -50,7 +53,9 @@ class DeviceTransformer:
 
     def __init__(self, ctx, cfg, weights, vectors, max_positions, stream=None):
         """stream: a StageStream whose weights() the layer tensors of `weights` come from; the
-        forward then acquires and releases each layer's slot around its layer."""
+        forward then acquires and releases each layer's slot around its layer. A layer with
+        blk.N.ffn_gate_inp is a MoE layer: blk.N.ffn_{gate,up,down}_exps (stacked experts), the
+        router, and optionally blk.N.ffn_{gate,up,down}_shexp and ffn_gate_inp_shexp ([1][embd])."""
         import torch
         self.ctx, self.cfg, self.L, self.torch = ctx, cfg, load(), torch
         self.stream = stream
@@ -77,8 +82,21 @@ class DeviceTransformer:
     def _desc(self, l):
         c, p, v = self.cfg, "blk.%d." % l, self.v
         d = LayerDesc()
-        for f in _LAYER_TENSORS:
-            setattr(d, f, self.w[p + f].handle.value)
+        if p + "ffn_gate_inp" in self.w:
+            # a MoE layer (MoeFfn, src/Transformer.cs:229): the stacked experts in the FFN fields
+            if c.expert_used < 1:
+                raise ShapeError("Layer %d has a router but the model has no expert_used_count." % l)
+            names = {f: f for f in _LAYER_TENSORS[:4]}
+            names.update(ffn_gate="ffn_gate_exps", ffn_up="ffn_up_exps", ffn_down="ffn_down_exps")
+            for f, n in names.items():
+                setattr(d, f, self.w[p + n].handle.value)
+            for f in ("ffn_gate_inp", "ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp", "ffn_gate_inp_shexp"):
+                if p + f in self.w:
+                    setattr(d, f, self.w[p + f].handle.value)
+            d.expert_used, d.expert_weights_norm = c.expert_used, int(c.expert_weights_norm)
+        else:
+            for f in _LAYER_TENSORS:
+                setattr(d, f, self.w[p + f].handle.value)
         d.d_attn_norm, d.d_ffn_norm = _ptr(v[p + "attn_norm"]), _ptr(v[p + "ffn_norm"])
         d.d_q_bias, d.d_k_bias, d.d_v_bias = (_ptr(v.get(p + "attn_%s.bias" % q)) for q in "qkv")
         d.d_q_norm, d.d_k_norm = _ptr(v.get(p + "attn_q_norm")), _ptr(v.get(p + "attn_k_norm"))
