@@ -19,4 +19,11 @@ int64_t gemm_scratch_bytes(int type, int rows, int cols, int T, int num_cu);
 hipError_t gemm_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, int cols, const float *x, int T,
                        float *y, int ldy, void *scratch, int num_cu, hipStream_t st);
 
+// The 512-token tiles for Q4_K / Q6_K prompts of 384 tokens and more (wl_gemm_tall.hip):
+// gemm_launch and gemm_scratch_bytes hand such calls to these.
+bool gemm_tall_applies(int type, int T);
+int64_t gemm_tall_scratch_bytes(int rows, int cols, int T, int num_cu);
+hipError_t gemm_tall_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, int cols, const float *x, int T,
+                            float *y, int ldy, void *scratch, int num_cu, hipStream_t st);
+
 }  // namespace wl

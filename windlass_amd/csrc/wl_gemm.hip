@@ -345,199 +345,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WL_GEMM_WPE
 }
 
 
-// ------------------------------------------------------------------ wide tiles (512 tokens)
-// Prompts of 384 tokens and more in the 70B layer's formats (Q4_K, Q6_K) take a workgroup of
-// eight waves that owns a 128 x 512 tile of y: every wave multiplies 64 rows x 128 tokens as
-// above, and each weight is decoded once per 512 tokens, so the decode work per MFMA halves.
-// K walks whole blocks with the eight 32-value steps of a block unrolled: a step's sub-block is
-// a compile-time field of the block (scale and min picked without branches), and the fp16 scales
-// go through the hardware conversion (exact for every finite value; the operands are rounded to
-// bf16 anyway). A thread decodes 8 values of one row per step (quarter q of the sub-block, with
-// the reference DecodeRow's fp32 operations) and stages 32 values of one token.
-constexpr int WBN = 512, WTHREADS = 512;
-
-struct WQ4K {
-  static constexpr int BYTES = 144;
-  struct Raw { uint4 h; uint2 q; };
-  template <int S>
-  __device__ static void load(const uint8_t *blk, int q, Raw &r) {
-    r.h = *reinterpret_cast<const uint4 *>(blk);  // 16-byte aligned
-    r.q = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * (S / 2) + 8 * q);
-  }
-  template <int S>
-  __device__ static void dec(const Raw &r, uint32_t (&o)[4]) {
-    const float d = half_lo(r.h.x), dmin = half_hi(r.h.x);
-    const uint32_t sc[3] = {r.h.y, r.h.z, r.h.w};
-    auto B = [&](int i) { return (sc[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
-    uint32_t scv, mv;  // get_scale_min_k4 of sub-block S (src/Quants.cs:322-330)
-    if constexpr (S < 4) {
-      scv = B(S) & 63;
-      mv = B(S + 4) & 63;
-    } else {
-      scv = (B(S + 4) & 0xF) | ((B(S - 4) >> 6) << 4);
-      mv = (B(S + 4) >> 4) | ((B(S) >> 6) << 4);
-    }
-    const float d1 = d * (float)scv, m1 = dmin * (float)mv;
-    const uint32_t v[2] = {(r.q.x >> (4 * (S & 1))) & 0x0F0F0F0Fu, (r.q.y >> (4 * (S & 1))) & 0x0F0F0F0Fu};
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      float y[4];
-#pragma unroll
-      for (int c = 0; c < 4; c++) y[c] = d1 * (float)((v[i] >> (8 * c)) & 0xFF) - m1;  // src/Quants.cs:345-346
-      o[2 * i] = pk(y[0], y[1]);
-      o[2 * i + 1] = pk(y[2], y[3]);
-    }
-  }
-};
-
-struct WQ6K {
-  static constexpr int BYTES = 210;
-  // ql and qh fields (8 bytes each at offsets that are multiples of 8, so they share the
-  // block's 2-byte misalignment) as aligned dword windows; the dwords holding the scale byte and d
-  struct Raw { uint32_t l[3], h[3], s, dw, sh, ssh; };
-  template <int S>
-  __device__ static void load(const uint8_t *blk, int q, Raw &r) {
-    constexpr int n = S / 4, qq = S % 4;
-    gu32 *a = align4_down(blk);
-    r.sh = misalign4(blk) * 8;
-    const int ol = (64 * n + 32 * (qq & 1) + 8 * q) / 4, oh = (128 + 32 * n + 8 * q) / 4;
-    r.l[0] = a[ol]; r.l[1] = a[ol + 1]; r.l[2] = a[ol + 2];
-    r.h[0] = a[oh]; r.h[1] = a[oh + 1]; r.h[2] = a[oh + 2];
-    const uint8_t *ps = blk + 192 + 8 * n + 2 * qq + (q >> 1);
-    r.s = *align4_down(ps);
-    r.ssh = misalign4(ps) * 8;
-    r.dw = a[208 / 4];
-  }
-  template <int S>
-  __device__ static void dec(const Raw &r, uint32_t (&o)[4]) {
-    constexpr int qq = S % 4;
-    const float d = r.sh ? half_hi(r.dw) : half_lo(r.dw);
-    const float ds = d * (float)(int8_t)(r.s >> r.ssh);
-#pragma unroll
-    for (int i = 0; i < 2; i++) {  // src/Quants.cs:381-392
-      const uint32_t ql = __builtin_amdgcn_alignbit(r.l[i + 1], r.l[i], r.sh);
-      const uint32_t qh = __builtin_amdgcn_alignbit(r.h[i + 1], r.h[i], r.sh);
-      const uint32_t v = ((ql >> (4 * (qq >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * qq)) & 0x03030303u) << 4);
-      float y[4];
-#pragma unroll
-      for (int c = 0; c < 4; c++) y[c] = ds * (float)((int)((v >> (8 * c)) & 0xFF) - 32);
-      o[2 * i] = pk(y[0], y[1]);
-      o[2 * i + 1] = pk(y[2], y[3]);
-    }
-  }
-};
-
-// The shared state of one wide workgroup.
-template <class G>
-struct WideTile {
-  const uint8_t *wr;   // this thread's weight row (clamped to the last row)
-  const uint16_t *xr;  // this thread's token (clamped to the last token)
-  int q;               // quarter of each sub-block the thread decodes
-  int kb;              // first column of the K-chunk
-  typename G::Raw ra[2];  // weight bytes of the steps not yet staged (by step parity)
-  uint4 xs[4];            // x of the next step to stage
-};
-
-// Step S (0..7) of block blk. Buffer S & 1 holds the step's operands (staged before the barrier);
-// after the barrier the threads stage step S + 1 into the other buffer (decode its weights, copy
-// its x, prefetch the weights of step S + 3 and the x of step S + 2) and multiply step S. The
-// other buffer was last read by step S - 1's products, which every thread finished before
-// reaching this barrier, and nothing in the staging depends on the products, so the decode's
-// VALU work can issue between the MFMAs.
-template <class G, int S>
-__device__ __forceinline__ void wide_step(WideTile<G> &t, int blk, int nblk, uint16_t *as_next, uint16_t *bs_next,
-                                          const uint16_t *ar, const uint16_t *br, f32x4_t (&acc)[4][8]) {
-  constexpr int S1 = (S + 1) & 7, S2 = (S + 2) & 7, S3 = (S + 3) & 7, P1 = S1 & 1;
-  const int blk1 = blk + (S + 1) / 8, blk2 = blk + (S + 2) / 8, blk3 = blk + (S + 3) / 8;
-  __syncthreads();
-  if (blk1 < nblk) {
-    uint4 *bd = reinterpret_cast<uint4 *>(bs_next);
-#pragma unroll
-    for (int i = 0; i < 4; i++) bd[i] = t.xs[i];
-    uint32_t o[4];
-    G::template dec<S1>(t.ra[P1], o);
-    *reinterpret_cast<uint4 *>(as_next) = make_uint4(o[0], o[1], o[2], o[3]);
-  }
-  if (blk2 < nblk) {
-    const uint4 *xp = reinterpret_cast<const uint4 *>(t.xr + t.kb + 256 * blk2 + 32 * S2);
-#pragma unroll
-    for (int i = 0; i < 4; i++) t.xs[i] = xp[i];
-  }
-  if (blk3 < nblk) G::template load<S3>(t.wr + (int64_t)(t.kb / 256 + blk3) * G::BYTES, t.q, t.ra[P1]);
-  mfma_step(ar, br, acc);
-}
-
-template <class G>
-__global__ __launch_bounds__(WTHREADS) void gemm_wide_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
-                                                             int rows, int cols, int kc,
-                                                             const uint16_t *__restrict__ xb, int T,
-                                                             float *__restrict__ y, int64_t ldy, int64_t zstride) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][WBN * LDK];
-  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * WBN;
-  const int kb = blockIdx.z * kc, ke = min(cols, kb + kc);
-  y += blockIdx.z * zstride;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int wm = wv >> 2, wn = wv & 3;
-  WideTile<G> t;
-  t.q = tid & 3;
-  t.kb = kb;
-  t.wr = w + (int64_t)min(m0 + (tid >> 2), rows - 1) * row_bytes;
-  t.xr = xb + (int64_t)min(n0 + tid, T - 1) * cols;
-  const int aw = (tid >> 2) * LDK + 8 * t.q, bw = tid * LDK;
-  const int ao = (64 * wm + (lane & 15)) * LDK + 8 * (lane >> 4);
-  const int bo = (128 * wn + (lane & 15)) * LDK + 8 * (lane >> 4);
-
-  f32x4_t acc[4][8];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 8; j++) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  const int nblk = (ke - kb) / 256;
-  if (nblk > 0) {
-    // stage step 0 into buffer 0; steps 1 and 2 in registers
-    const uint8_t *b0 = t.wr + (int64_t)(kb / 256) * G::BYTES;
-    G::template load<0>(b0, t.q, t.ra[0]);
-    G::template load<1>(b0, t.q, t.ra[1]);
-    const uint4 *x0 = reinterpret_cast<const uint4 *>(t.xr + kb);
-    uint4 *bd = reinterpret_cast<uint4 *>(Bs[0] + bw);
-#pragma unroll
-    for (int i = 0; i < 4; i++) bd[i] = x0[i];
-    uint32_t o[4];
-    G::template dec<0>(t.ra[0], o);
-    *reinterpret_cast<uint4 *>(As[0] + aw) = make_uint4(o[0], o[1], o[2], o[3]);
-#pragma unroll
-    for (int i = 0; i < 4; i++) t.xs[i] = x0[4 + i];
-    G::template load<2>(b0, t.q, t.ra[0]);
-  }
-  for (int blk = 0; blk < nblk; blk++) {
-    wide_step<G, 0>(t, blk, nblk, As[1] + aw, Bs[1] + bw, As[0] + ao, Bs[0] + bo, acc);
-    wide_step<G, 1>(t, blk, nblk, As[0] + aw, Bs[0] + bw, As[1] + ao, Bs[1] + bo, acc);
-    wide_step<G, 2>(t, blk, nblk, As[1] + aw, Bs[1] + bw, As[0] + ao, Bs[0] + bo, acc);
-    wide_step<G, 3>(t, blk, nblk, As[0] + aw, Bs[0] + bw, As[1] + ao, Bs[1] + bo, acc);
-    wide_step<G, 4>(t, blk, nblk, As[1] + aw, Bs[1] + bw, As[0] + ao, Bs[0] + bo, acc);
-    wide_step<G, 5>(t, blk, nblk, As[0] + aw, Bs[0] + bw, As[1] + ao, Bs[1] + bo, acc);
-    wide_step<G, 6>(t, blk, nblk, As[1] + aw, Bs[1] + bw, As[0] + ao, Bs[0] + bo, acc);
-    wide_step<G, 7>(t, blk, nblk, As[0] + aw, Bs[0] + bw, As[1] + ao, Bs[1] + bo, acc);
-  }
-
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int r0 = m0 + 64 * wm + 16 * i + 4 * (lane >> 4);
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const int tk = n0 + 128 * wn + 16 * j + (lane & 15);
-      if (tk < T) {
-        float *yp = y + (int64_t)tk * ldy + r0;
-#pragma unroll
-        for (int qd = 0; qd < 4; qd++)
-          if (r0 + qd < rows) yp[qd] = acc[i][j][qd];
-      }
-    }
-  }
-}
-
 // y[t][r] = chunk partials added in chunk order.
 __global__ __launch_bounds__(256) void gemm_combine_kernel(const float *__restrict__ part, int S, int T, int rows,
                                                            float *__restrict__ y, int64_t ldy) {
@@ -557,11 +364,6 @@ __global__ __launch_bounds__(256) void gemm_combine_kernel(const float *__restri
 
 constexpr int kMaxChunks = 8;
 
-// The wide tiles take Q4_K and Q6_K prompts whose last 512-token tile is at least 3/4 full.
-static bool gemm_wide(int type, int T) {
-  return (type == 12 || type == 14) && T >= 384 && (T % WBN == 0 || T % WBN >= 384);
-}
-
 static int split_chunks(int tiles, int target, int cols) {
   if (tiles >= target) return 1;
   int S = (target + tiles - 1) / tiles;
@@ -573,39 +375,29 @@ static int split_chunks(int tiles, int target, int cols) {
 }
 
 // K-chunks: a launch with fewer output tiles than the device holds at once is split along K
-// (in whole 256-blocks): about two workgroups per CU of the 128 x 256 tiles, and one per CU of
-// the wide tiles (whose 100 KB of LDS allow one), unless the tiles already fill 7/8 of the CUs.
+// (in whole 256-blocks): about two workgroups per CU of the 128 x 256 tiles.
 int gemm_chunks(int type, int rows, int cols, int T, int num_cu) {
-  if (gemm_wide(type, T)) {
-    const int tiles = ((rows + BM - 1) / BM) * ((T + WBN - 1) / WBN);
-    return tiles * 8 >= num_cu * 7 ? 1 : split_chunks(tiles, num_cu, cols);
-  }
   return split_chunks(((rows + BM - 1) / BM) * ((T + BN - 1) / BN), 2 * num_cu, cols);
 }
 
 int64_t gemm_scratch_bytes(int type, int rows, int cols, int T, int num_cu) {
+  if (gemm_tall_applies(type, T)) return gemm_tall_scratch_bytes(rows, cols, T, num_cu);
   const int S = gemm_chunks(type, rows, cols, T, num_cu);
   return (int64_t)T * cols * 2 + (S > 1 ? (int64_t)S * T * rows * 4 : 0);
 }
 
-template <class G, bool WIDE = false>
+template <class G>
 static hipError_t launch(const uint8_t *w, int64_t row_bytes, int rows, int cols, const uint16_t *xb, int T,
                          float *y, int ldy, float *part, int S, hipStream_t st) {
   const int kc = (cols / 256 + S - 1) / S * 256;
-  const int bn = WIDE ? WBN : BN;
-  const dim3 grid((rows + BM - 1) / BM, (T + bn - 1) / bn, S);
-  auto go = [&](float *out, int64_t ld, int64_t zs) {
-    if constexpr (WIDE)
-      hipLaunchKernelGGL((gemm_wide_kernel<G>), grid, dim3(WTHREADS), 0, st, w, row_bytes, rows, cols, kc, xb, T, out,
-                         ld, zs);
-    else
-      hipLaunchKernelGGL((gemm_kernel<G>), grid, dim3(256), 0, st, w, row_bytes, rows, cols, kc, xb, T, out, ld, zs);
-  };
+  const dim3 grid((rows + BM - 1) / BM, (T + BN - 1) / BN, S);
   if (S == 1) {
-    go(y, (int64_t)ldy, (int64_t)0);
+    hipLaunchKernelGGL((gemm_kernel<G>), grid, dim3(256), 0, st, w, row_bytes, rows, cols, kc, xb, T, y, (int64_t)ldy,
+                       (int64_t)0);
     return hipGetLastError();
   }
-  go(part, (int64_t)rows, (int64_t)T * rows);
+  hipLaunchKernelGGL((gemm_kernel<G>), grid, dim3(256), 0, st, w, row_bytes, rows, cols, kc, xb, T, part, (int64_t)rows,
+                     (int64_t)T * rows);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   int64_t g = ((int64_t)T * rows + 255) / 256;
@@ -626,6 +418,8 @@ hipError_t gemm_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, 
                        float *y, int ldy, void *scratch, int num_cu, hipStream_t st) {
   if (rows <= 0 || T <= 0) return hipSuccess;
   if (cols <= 0 || cols % 256 || !scratch) return hipErrorInvalidValue;
+  if (gemm_tall_applies(type, T))
+    return gemm_tall_launch(type, w, row_bytes, rows, cols, x, T, y, ldy, scratch, num_cu, st);
   const int64_t n4 = (int64_t)T * cols / 4;
   int64_t g = (n4 + 255) / 256;
   if (g > 4096) g = 4096;
@@ -636,10 +430,6 @@ hipError_t gemm_launch(int type, const uint8_t *w, int64_t row_bytes, int rows, 
   // partials follow the bf16 copy of x (T * cols * 2 bytes, a multiple of 512)
   float *part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + (int64_t)T * cols * 2);
   const int S = gemm_chunks(type, rows, cols, T, num_cu);
-  if (gemm_wide(type, T)) {
-    if (type == 12) return launch<WQ4K, true>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
-    return launch<WQ6K, true>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
-  }
   switch (type) {
     case 8: return launch<GQ80>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
     case 12: return launch<GQ4K>(w, row_bytes, rows, cols, xb, T, y, ldy, part, S, st);
