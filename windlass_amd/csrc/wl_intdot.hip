@@ -30,20 +30,32 @@ bool intdot_fits(int t, int cols) { return cols > 0 && cols % (intdot_needs_k(t)
 
 static int64_t up16(int64_t n) { return (n + 15) / 16 * 16; }
 
+// The matrix-core operand copy (QActsDev::qf/bf/df) of Q8_K activations of 2..8 tokens.
+static bool qacts_mma(int T, int k) { return k && T >= 2 && T <= 8; }
+static int64_t mma_bytes(int cols) { return (int64_t)(cols / 256) * (8 * 16 * 32 + 16 * 16 * 2 + 16 * 4); }
+
 int64_t qacts_bytes(int T, int cols, int k) {
   const int bs = k ? 256 : 32;
-  return up16((int64_t)T * cols) + up16((int64_t)T * (cols / bs) * 4) + (k ? (int64_t)T * (cols / 16) * 2 : 0);
+  return up16((int64_t)T * cols) + up16((int64_t)T * (cols / bs) * 4) + up16(k ? (int64_t)T * (cols / 16) * 2 : 0) +
+         (qacts_mma(T, k) ? mma_bytes(cols) : 0);
 }
 
 QActsDev qacts_at(void *buf, int T, int cols, int k) {
   const int bs = k ? 256 : 32;
   uint8_t *p = static_cast<uint8_t *>(buf);
-  QActsDev a;
+  QActsDev a{};
   a.q = reinterpret_cast<int8_t *>(p);
   p += up16((int64_t)T * cols);
   a.d = reinterpret_cast<float *>(p);
   p += up16((int64_t)T * (cols / bs) * 4);
   a.bsums = k ? reinterpret_cast<int16_t *>(p) : nullptr;
+  p += up16(k ? (int64_t)T * (cols / 16) * 2 : 0);
+  if (qacts_mma(T, k)) {
+    const int64_t nb = cols / 256;
+    a.qf = reinterpret_cast<int8_t *>(p);
+    a.bf = reinterpret_cast<int16_t *>(p + nb * 8 * 16 * 32);
+    a.df = reinterpret_cast<float *>(p + nb * (8 * 16 * 32 + 16 * 16 * 2));
+  }
   return a;
 }
 
@@ -54,15 +66,23 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 }
 
 // Wave w of the grid quantizes activations [256 c, 256 c + 256) of token t (w = t * nchunk + c).
+// With qf (Q8_K of 2..8 tokens), waves of token slots T..15 write that copy's zero slots.
 __global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__ x, int T, int cols, int k,
                                                        int8_t *__restrict__ q, float *__restrict__ d,
-                                                       int16_t *__restrict__ bsums) {
+                                                       int16_t *__restrict__ bsums, int8_t *__restrict__ qf,
+                                                       int16_t *__restrict__ bf, float *__restrict__ df) {
   const int lane = threadIdx.x & 63;
   const int nchunk = (cols + 255) / 256;
   const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (gw >= (int64_t)T * nchunk) return;  // the whole wave
+  if (gw >= (int64_t)(qf ? 16 : T) * nchunk) return;  // the whole wave
   const int t = (int)(gw / nchunk), c = (int)(gw % nchunk);
   const int base = 256 * c + 4 * lane;  // cols is a multiple of 32, so a lane's 4 values are all in or all out
+  if (t >= T) {  // a zero slot of the operand copy
+    reinterpret_cast<uint32_t *>(qf)[((c * 8 + lane / 8) * 16 + t) * 8 + lane % 8] = 0u;
+    if ((lane & 3) == 0) bf[(c * 16 + t) * 16 + lane / 4] = 0;
+    if (lane == 0) df[c * 16 + t] = 0.f;
+    return;
+  }
   const bool in = base < cols;
   const float *xr = x + (int64_t)t * cols;
   float v[4] = {0.f, 0.f, 0.f, 0.f};
@@ -129,17 +149,25 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__
   int s = qi[0] + qi[1] + qi[2] + qi[3];  // bsums: 16 quants = 4 lanes
   s += __shfl_xor(s, 1, 64);
   s += __shfl_xor(s, 2, 64);
-  *qw = pack4(qi[0], qi[1], qi[2], qi[3]);
+  const uint32_t packed = pack4(qi[0], qi[1], qi[2], qi[3]);
+  const float dv = am != 0.f ? 1.f / iscale : 0.f;
+  *qw = packed;
   if ((lane & 3) == 0) bsums[(int64_t)t * (cols / 16) + base / 16] = (int16_t)s;
-  if (lane == 0) d[(int64_t)t * (cols / 256) + c] = am != 0.f ? 1.f / iscale : 0.f;
+  if (lane == 0) d[(int64_t)t * (cols / 256) + c] = dv;
+  if (qf) {  // the same values in the matrix-core operand order
+    reinterpret_cast<uint32_t *>(qf)[((c * 8 + lane / 8) * 16 + t) * 8 + lane % 8] = packed;
+    if ((lane & 3) == 0) bf[(c * 16 + t) * 16 + lane / 4] = (int16_t)s;
+    if (lane == 0) df[c * 16 + t] = dv;
+  }
 }
 
 hipError_t quantize_launch(const float *x, int T, int cols, int k, QActsDev a, hipStream_t st) {
   if (T <= 0 || cols <= 0) return hipSuccess;
   if (cols % (k ? 256 : 32)) return hipErrorInvalidValue;
-  const int64_t waves = (int64_t)T * ((cols + 255) / 256);
+  const bool mma = a.qf && qacts_mma(T, k);
+  const int64_t waves = (int64_t)(mma ? 16 : T) * ((cols + 255) / 256);
   hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, T, cols, k, a.q, a.d,
-                     a.bsums);
+                     a.bsums, mma ? a.qf : nullptr, a.bf, a.df);
   return hipGetLastError();
 }
 

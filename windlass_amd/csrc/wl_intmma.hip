@@ -50,6 +50,12 @@ struct MQ4K {
 #pragma unroll
     for (int j = 0; j < 4; j++) r.q[j] = ld8(blk + 16 + 32 * j + 8 * q4);
   }
+  // the same bytes from a staged copy of the block in LDS (16-byte aligned)
+  __device__ static void load_lds(const uint8_t *blk, int q4, Raw &r) {
+    r.h = *reinterpret_cast<const uint4 *>(blk);
+#pragma unroll
+    for (int j = 0; j < 4; j++) r.q[j] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 8 * q4);
+  }
   __device__ static uint2 operand(const Raw &r, int s) {
     const uint2 v = r.q[s >> 1];
     const int sh = 4 * (s & 1);
@@ -132,15 +138,32 @@ struct MmaArgs {
   int T;
   float *y;
   int ldy;
+  // the same activations in operand order (QActsDev::qf/bf/df), or null
+  const int8_t *qf;
+  const int16_t *bf;
+  const float *df;
 };
 
 // A workgroup owns one 16-row tile (of each matrix); wave w walks the w-th quarter of the row's
 // blocks in order. Wave 0 adds its blocks' terms as it goes; waves 1..3 leave theirs in LDS
 // (the D lanes of the first 8 tokens), and after one barrier wave 0 adds them on in block
 // order: the reference's single `sum +=` chain over the whole row.
-template <class M, int NM>
+// Staged weights (Q4_K): a wave reads its tile's 16 rows x kStageBlocks blocks with coalesced
+// nontemporal 16-byte loads (every byte once; a wave load covers about two rows' contiguous
+// bytes instead of 16 rows' separate lines), one chunk ahead in registers, into its own LDS
+// area, and the lanes take their operand bytes from there.
+constexpr int kStageBlocks = 2;
+constexpr int kStageRow = kStageBlocks * 144 + 16;                          // LDS bytes per row (padded)
+constexpr int kStageChunks = 16 * kStageBlocks * 144 / 16;                  // 16-byte chunks of a stage
+constexpr int kStageLoads = (kStageChunks + 63) / 64;                       // loads per lane
+
+// FRAG: the activations come from the operand-order copy (one 512-byte wave load per run of 32
+// values, 16 tokens' bsums and scales in one 512- and one 64-byte range) instead of the tokens'
+// rows (16 tokens' separate lines per wave load). STG: staged weights (Q4_K).
+template <class M, int NM, bool FRAG, bool STG = false>
 __global__ __launch_bounds__(64 * kMmaWaves) void intmma_kernel(MmaArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t slab[kMmaWaves][NM][16 * kSlab];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[STG ? kMmaWaves : 1][STG ? NM : 1][STG ? 16 * kStageRow : 16];
   extern __shared__ __attribute__((aligned(16))) float4 mma_terms[];  // [3][bw][NM][TERMS][32]
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, q4 = lane >> 4, c16 = lane & 15;
   const int tile = blockIdx.x;  // uniform: the barrier below is reached by every wave
@@ -170,11 +193,20 @@ __global__ __launch_bounds__(64 * kMmaWaves) void intmma_kernel(MmaArgs a) {
   auto fetch = [&](int b, Ops &o) {
 #pragma unroll
     for (int m = 0; m < NM; m++) M::load(wr[m] + (int64_t)b * M::BYTES, q4, o.raw[m]);
+    if constexpr (FRAG) {
 #pragma unroll
-    for (int s = 0; s < 8; s++) o.xs[s] = ld8(xq + (int64_t)b * 256 + 32 * s);
-    o.b0 = *reinterpret_cast<const uint4 *>(xb + (int64_t)b * 16);
-    o.b1 = *reinterpret_cast<const uint4 *>(xb + (int64_t)b * 16 + 8);
-    o.dt = xd[b];
+      for (int s = 0; s < 8; s++) o.xs[s] = ld8(a.qf + (((int64_t)b * 8 + s) * 16 + c16) * 32 + 8 * q4);
+      const int16_t *bb = a.bf + ((int64_t)b * 16 + c16) * 16;
+      o.b0 = *reinterpret_cast<const uint4 *>(bb);
+      o.b1 = *reinterpret_cast<const uint4 *>(bb + 8);
+      o.dt = a.df[(int64_t)b * 16 + c16];
+    } else {
+#pragma unroll
+      for (int s = 0; s < 8; s++) o.xs[s] = ld8(xq + (int64_t)b * 256 + 32 * s);
+      o.b0 = *reinterpret_cast<const uint4 *>(xb + (int64_t)b * 16);
+      o.b1 = *reinterpret_cast<const uint4 *>(xb + (int64_t)b * 16 + 8);
+      o.dt = xd[b];
+    }
   };
   // blocks b and b + 1 in flight: block b's operands were fetched two blocks earlier
   auto body = [&](const Ops &op, float (&tm)[NM][M::TERMS][4]) {
@@ -269,7 +301,92 @@ __global__ __launch_bounds__(64 * kMmaWaves) void intmma_kernel(MmaArgs a) {
           p[(m * M::TERMS + h) * 32] = make_float4(tm[m][h][0], tm[m][h][1], tm[m][h][2], tm[m][h][3]);
     }
   };
-  if (tile * 16 < a.rows && b_lo < b_hi) {
+  if constexpr (STG) {
+    // stage loads: chunk f = 64 i + lane of the 16 x kStageBlocks block region is row f / per,
+    // 16-byte piece f % per of it (per = kStageBlocks * 9)
+    constexpr int per = kStageBlocks * 9;
+    int soff[kStageLoads], lofs[kStageLoads];
+    bool sok[kStageLoads];
+#pragma unroll
+    for (int i = 0; i < kStageLoads; i++) {
+      const int f = 64 * i + lane, r = f / per, c = f % per;
+      sok[i] = f < kStageChunks;
+      const int row = min(tile * 16 + r, a.rows - 1);
+      soff[i] = 0;
+      lofs[i] = r * kStageRow + 16 * c;
+      // row offsets fit 32 bits only per tile; the tile's first row is added once below
+      soff[i] = (row - min(tile * 16, a.rows - 1)) * (int)a.row_bytes + 16 * c;
+    }
+    const int64_t tbase = (int64_t)min(tile * 16, a.rows - 1) * a.row_bytes;
+    u32x4_t sreg[NM][kStageLoads];
+    auto issue = [&](int c0) {  // blocks c0 .. c0 + kStageBlocks - 1 (clamped to the row)
+      const int cb = min(c0, nb - kStageBlocks);
+#pragma unroll
+      for (int m = 0; m < NM; m++) {
+        const uint8_t *base = (m ? a.w2 : a.w) + tbase + (int64_t)cb * 144;
+#pragma unroll
+        for (int i = 0; i < kStageLoads; i++)
+          if (sok[i]) sreg[m][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(base + soff[i]));
+      }
+      return cb;
+    };
+    auto commit = [&]() {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int i = 0; i < kStageLoads; i++)
+          if (sok[i]) *reinterpret_cast<u32x4_t *>(&stage[wv][m][lofs[i]]) = sreg[m][i];
+      asm volatile("" ::: "memory");
+    };
+    struct Xo {
+      uint2 xs[8];
+      uint4 b0, b1;
+      float dt;
+    };
+    auto fetch_x = [&](int b, Xo &o) {
+#pragma unroll
+      for (int s = 0; s < 8; s++) o.xs[s] = ld8(a.qf + (((int64_t)b * 8 + s) * 16 + c16) * 32 + 8 * q4);
+      const int16_t *bb = a.bf + ((int64_t)b * 16 + c16) * 16;
+      o.b0 = *reinterpret_cast<const uint4 *>(bb);
+      o.b1 = *reinterpret_cast<const uint4 *>(bb + 8);
+      o.dt = a.df[(int64_t)b * 16 + c16];
+    };
+    auto block = [&](int b, int cb, const Xo &xo) {
+      Ops op;
+#pragma unroll
+      for (int m = 0; m < NM; m++) M::load_lds(&stage[wv][m][c16 * kStageRow + (b - cb) * 144], q4, op.raw[m]);
+#pragma unroll
+      for (int s = 0; s < 8; s++) op.xs[s] = xo.xs[s];
+      op.b0 = xo.b0;
+      op.b1 = xo.b1;
+      op.dt = xo.dt;
+      float tm[NM][M::TERMS][4];
+      body(op, tm);
+      take(b, tm);
+    };
+    if (tile * 16 < a.rows && b_lo < b_hi) {
+      Xo xr[2];
+      int cb = issue(b_lo);
+      fetch_x(b_lo, xr[0]);
+      if (b_lo + 1 < b_hi) fetch_x(b_lo + 1, xr[1]);
+      for (int c = b_lo; c < b_hi; c += kStageBlocks) {
+        commit();
+        const int cur = cb;
+        if (c + kStageBlocks < b_hi) cb = issue(c + kStageBlocks);
+        {
+          const Xo xo = xr[0];
+          if (c + 2 < b_hi) fetch_x(c + 2, xr[0]);
+          block(c, cur, xo);
+        }
+        if (c + 1 < b_hi) {
+          const Xo xo = xr[1];
+          if (c + 3 < b_hi) fetch_x(c + 3, xr[1]);
+          block(c + 1, cur, xo);
+        }
+      }
+    }
+  } else if (tile * 16 < a.rows && b_lo < b_hi) {
     Ops ring[2];
     fetch(b_lo, ring[0]);
     if (b_lo + 1 < b_hi) fetch(b_lo + 1, ring[1]);
@@ -336,24 +453,32 @@ bool intmma_supports(int type, int cols, int T, int nm) {
 
 int intmma_max_tokens(int type, int cols, int nm) { return intmma_supports(type, cols, 2, nm) ? kMmaTokens : 0; }
 
-template <class M, int NM>
-static hipError_t go(const MmaArgs &a, int grid, size_t smem, hipStream_t st) {
+template <class M, int NM, bool FRAG, bool STG = false>
+static hipError_t go_frag(const MmaArgs &a, int grid, size_t smem, hipStream_t st) {
   static bool raised = false;
   if (smem > 65536 && !raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&intmma_kernel<M, NM>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&intmma_kernel<M, NM, FRAG, STG>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMmaMaxLds) != hipSuccess)
       return hipErrorInvalidConfiguration;
     raised = true;
   }
-  hipLaunchKernelGGL((intmma_kernel<M, NM>), dim3(grid), dim3(64 * kMmaWaves), smem, st, a);
+  hipLaunchKernelGGL((intmma_kernel<M, NM, FRAG, STG>), dim3(grid), dim3(64 * kMmaWaves), smem, st, a);
   return hipGetLastError();
+}
+
+// Q4_K rows of at least one stage take the staged weights (with the operand-order activations).
+template <class M, int NM>
+static hipError_t go(const MmaArgs &a, int grid, size_t smem, hipStream_t st) {
+  if constexpr (M::BYTES == 144)
+    if (a.qf && a.cols / 256 >= kStageBlocks) return go_frag<M, NM, true, true>(a, grid, smem, st);
+  return a.qf ? go_frag<M, NM, true>(a, grid, smem, st) : go_frag<M, NM, false>(a, grid, smem, st);
 }
 
 hipError_t intmma_launch(int type, const uint8_t *w, const uint8_t *w2, int64_t row_bytes, int rows, int cols,
                          QActsDev qa, int T, float *y, int ldy, hipStream_t st) {
   if (rows <= 0) return hipSuccess;
   if (!intmma_supports(type, cols, T, w2 ? 2 : 1) || !qa.q || !qa.d || !qa.bsums) return hipErrorInvalidValue;
-  const MmaArgs a{w, w2, row_bytes, rows, cols, qa.q, qa.d, qa.bsums, T, y, ldy};
+  const MmaArgs a{w, w2, row_bytes, rows, cols, qa.q, qa.d, qa.bsums, T, y, ldy, qa.qf, qa.bf, qa.df};
   const int grid = (rows + 15) / 16;
   const size_t smem = mma_lds(type, cols, w2 ? 2 : 1);
   hipError_t e = hipSuccess;
