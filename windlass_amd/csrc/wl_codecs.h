@@ -280,17 +280,20 @@ struct Q80 {
     }
   }
 
+  // Two accumulators (even and odd values, as the reference's DotRow keeps two partial sums,
+  // src/Quants.cs:86-97): independent multiply-add chains issue without the wait a chain of
+  // dependent v_fma_mix_f32 needs on gfx950.
   __device__ static float dot(const W &w, const Xs &x) {
-    float a = 0.f;
+    float a = 0.f, b = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       a = fma_lo(w.p[2 * i], x.v[4 * i + 0], a);
+      b = fma_lo(w.p[2 * i + 1], x.v[4 * i + 1], b);
       a = fma_hi(w.p[2 * i], x.v[4 * i + 2], a);
-      a = fma_lo(w.p[2 * i + 1], x.v[4 * i + 1], a);
-      a = fma_hi(w.p[2 * i + 1], x.v[4 * i + 3], a);
+      b = fma_hi(w.p[2 * i + 1], x.v[4 * i + 3], b);
     }
     // d * sum(q*x) = d * (sum((q+128)*x) - 128*sum(x))   (src/Quants.cs:93-94)
-    return w.d * __builtin_fmaf(-128.f, x.s, a);
+    return w.d * __builtin_fmaf(-128.f, x.s, a + b);
   }
 };
 
@@ -373,28 +376,32 @@ struct IQ4XS {
     }
   }
 
+  // Two accumulators (the low and the high nibbles' values): independent chains issue without
+  // the wait a chain of dependent v_fma_mix_f32 needs on gfx950.
   __device__ static float dot(const W &w, const Xs &x) {
-    float a = 0.f;
+    float a = 0.f, b = 0.f;
     if constexpr (NEED_LDS) {
 #pragma unroll
       for (int k = 0; k < 16; k++) {
         a = fma_lo(w.p[k], x.v[k], a);
-        a = fma_hi(w.p[k], x.v[16 + k], a);
+        b = fma_hi(w.p[k], x.v[16 + k], b);
       }
     } else {
 #pragma unroll
-      for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float *xv = x.v + 16 * h + 4 * i;
-          a = fma_lo(w.p[8 * h + 2 * i], xv[0], a);
-          a = fma_hi(w.p[8 * h + 2 * i], xv[2], a);
-          a = fma_lo(w.p[8 * h + 2 * i + 1], xv[1], a);
-          a = fma_hi(w.p[8 * h + 2 * i + 1], xv[3], a);
-        }
+      for (int i = 0; i < 4; i++) {
+        const float *xa = x.v + 4 * i, *xb = x.v + 16 + 4 * i;
+        a = fma_lo(w.p[2 * i], xa[0], a);
+        b = fma_lo(w.p[8 + 2 * i], xb[0], b);
+        a = fma_hi(w.p[2 * i], xa[2], a);
+        b = fma_hi(w.p[8 + 2 * i], xb[2], b);
+        a = fma_lo(w.p[2 * i + 1], xa[1], a);
+        b = fma_lo(w.p[8 + 2 * i + 1], xb[1], b);
+        a = fma_hi(w.p[2 * i + 1], xa[3], a);
+        b = fma_hi(w.p[8 + 2 * i + 1], xb[3], b);
+      }
     }
     // dl * sum(kv*x) = dl * (sum((kv+128)*x) - 128*sum(x))
-    return w.dl * __builtin_fmaf(-128.f, x.s, a);
+    return w.dl * __builtin_fmaf(-128.f, x.s, a + b);
   }
 
   // byte b -> fp16 pair (kvalues[b & 15] + 128, kvalues[b >> 4] + 128) as subnormals
@@ -454,22 +461,33 @@ struct IQ2XXS {
     }
   }
 
+  // Two accumulators (groups 0, 2 and groups 1, 3): independent chains issue without the wait a
+  // chain of dependent v_fma_mix_f32 needs on gfx950.
   __device__ static float dot(const W &w, const Xs &x) {
-    float a = 0.f;
+    float a = 0.f, b = 0.f;
 #pragma unroll
-    for (int l = 0; l < 4; l++) {
-      const float *xv = x.v + 8 * l;
-      // pairs (0,2) (1,3) (4,6) (5,7) of the group, as init_lds lays them out
-      a = fma_lo(w.p[4 * l + 0], xv[0], a);
-      a = fma_hi(w.p[4 * l + 0], xv[2], a);
-      a = fma_lo(w.p[4 * l + 1], xv[1], a);
-      a = fma_hi(w.p[4 * l + 1], xv[3], a);
-      a = fma_lo(w.p[4 * l + 2], xv[4], a);
-      a = fma_hi(w.p[4 * l + 2], xv[6], a);
-      a = fma_lo(w.p[4 * l + 3], xv[5], a);
-      a = fma_hi(w.p[4 * l + 3], xv[7], a);
+    for (int l = 0; l < 4; l += 2) {
+      const float *xa = x.v + 8 * l, *xb = x.v + 8 * (l + 1);
+      const uint32_t *pa = w.p + 4 * l, *pb = w.p + 4 * (l + 1);
+      // pairs (0,2) (1,3) (4,6) (5,7) of each group, as init_lds lays them out
+      a = fma_lo(pa[0], xa[0], a);
+      b = fma_lo(pb[0], xb[0], b);
+      a = fma_hi(pa[0], xa[2], a);
+      b = fma_hi(pb[0], xb[2], b);
+      a = fma_lo(pa[1], xa[1], a);
+      b = fma_lo(pb[1], xb[1], b);
+      a = fma_hi(pa[1], xa[3], a);
+      b = fma_hi(pb[1], xb[3], b);
+      a = fma_lo(pa[2], xa[4], a);
+      b = fma_lo(pb[2], xb[4], b);
+      a = fma_hi(pa[2], xa[6], a);
+      b = fma_hi(pb[2], xb[6], b);
+      a = fma_lo(pa[3], xa[5], a);
+      b = fma_lo(pb[3], xb[5], b);
+      a = fma_hi(pa[3], xa[7], a);
+      b = fma_hi(pb[3], xb[7], b);
     }
-    return w.db * a;
+    return w.db * (a + b);
   }
 
   // The grid entries as their 8 value bytes and the 128 sign patterns (ksigns_iq2xs: index plus
