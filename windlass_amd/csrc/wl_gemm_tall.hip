@@ -242,19 +242,44 @@ struct TallState {
   f32x16_t acc[RM / 32][4];
 };
 
-// Product K (0..NK-1) of a step, then the decode piece that slot carries: values 0..15 of step
-// s + 2 in slots 0..15 (three VALU instructions each), their bf16 pairs in slots 16..23, and the
-// preparation of step s + 3's decode from slot 24 on. A scheduling barrier after each slot keeps
-// this order, so every v_mfma is followed by at most a few independent VALU instructions, which
-// issue while the matrix core works.
-template <class G, int RM, int S, int K, bool DEC2, bool DEC3>
+// What a step loads for the steps after it, issued from the product slots.
+struct StepMem {
+  const XView *xv;
+  int s;                 // this step's index in the row
+  const uint16_t *ar;    // step s + 1's A tile in LDS (with the lane's offset)
+  const uint8_t *wnext;  // the next block's bytes (weights of a half-block ahead), or null
+};
+
+// Product K (0..NK-1) of a step, then the work that slot carries:
+//   slots 0..7    the next step's B fragment K (x_frag), and value K of step s + 2's decode
+//   slots 8..15   the next step's A fragment K - 8 (LDS), and value K
+//   slots 16..23  the bf16 pairs; slot 16 the L2 prefetch, slot 17 a half-block's weight bytes,
+//                 slot 23 the decoded values to LDS
+//   slots 24..    the preparation of step s + 3's decode
+// A scheduling barrier after each slot keeps this order, so every v_mfma is followed by one
+// memory instruction and a few independent VALU instructions, which issue while the matrix core
+// works, instead of the step opening with sixteen memory instructions and no product.
+template <class G, int RM, int S, int K, bool HAS1, bool DEC2, bool DEC3, bool LAST>
 __device__ __forceinline__ void step_products(TallState<G, RM> &st, int h, float (&y)[16], uint32_t (&o)[8],
-                                              uint16_t *a_out) {
+                                              uint16_t *a_out, const StepMem &mem) {
   constexpr int NK = 2 * (RM / 32) * 4;
-  static_assert(NK >= 24 + G::NPREP, "decode slots");
+  static_assert(NK >= 24 + G::NPREP && NK >= 8 + 2 * (RM / 32), "decode and load slots");
   if constexpr (K < NK) {
     constexpr int u = K / ((RM / 32) * 4), i = (K / 4) % (RM / 32), jj = K % 4;
     mfma_acc(st.acc[i][jj], st.af[S & 1][u][i], st.b[S & 1][jj][u]);
+    if constexpr (HAS1 && K < 8) st.b[(S + 1) & 1][K >> 1][K & 1] = x_frag(*mem.xv, K >> 1, mem.s + 1, K & 1);
+    if constexpr (HAS1 && K >= 8 && K < 8 + 2 * (RM / 32)) {
+      constexpr int un = (K - 8) / (RM / 32), in = (K - 8) % (RM / 32);
+      st.af[(S + 1) & 1][un][in] = *reinterpret_cast<const uint4 *>(mem.ar + 32 * in * TLDK + 16 * un);
+    }
+    if constexpr (K == 16) {
+      if constexpr (DEC3) st.pf[S & 3] = x_prefetch(*mem.xv, mem.s + 3);
+      asm volatile("" ::"v"(st.pf[(S + 2) & 3]));  // the prefetch issued two steps ago
+    }
+    if constexpr (K == 17 && !LAST) {
+      if constexpr (S == 1) G::template load<0>(mem.wnext, h, st.raw[0]);
+      if constexpr (S == 5) G::template load<1>(mem.wnext, h, st.raw[1]);
+    }
     if constexpr (DEC2 && K < 16) y[K] = G::template value<K>(st.dec[S & 1]);
     if constexpr (DEC2 && K >= 16 && K < 24) o[K - 16] = pk2(y[2 * (K - 16)], y[2 * (K - 16) + 1]);
     if constexpr (DEC2 && K == 23) {  // the decoded values of step s + 2 to LDS
@@ -267,20 +292,19 @@ __device__ __forceinline__ void step_products(TallState<G, RM> &st, int h, float
       G::template prep<S3, K - 24>(st.raw[S3 / 4], h, st.dec[(S + 1) & 1]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    step_products<G, RM, S, K + 1, DEC2, DEC3>(st, h, y, o, a_out);
+    step_products<G, RM, S, K + 1, HAS1, DEC2, DEC3, LAST>(st, h, y, o, a_out, mem);
   }
 }
 
-// Step S (0..7) of block blk. Going in, the step's A operands are in registers (af[S & 1], read
-// from LDS before the last barrier), its B operands are loaded or in flight (b[S & 1]), and the
-// decode state of step s + 2 is ready (dec[S & 1]). The step issues the next step's B loads, an
-// L2 prefetch of step s + 3's x slice, the weight bytes of a half-block four steps ahead (at
-// S = 1 and 5) and the reads of step s + 1's A operands from LDS buffer (S + 1) & 3, then the
-// products with the decode pieces between them (step s + 2 into buffer (S + 2) & 3, step
-// s + 3's preparation), and ends at the barrier. Buffer (S + 1) & 3 was written during step
-// s - 1 and made visible by the barrier that ended it; buffer (S + 2) & 3 was last read during
-// step s - 1, before that barrier, so one barrier per step orders every LDS write against its
-// reads, and the reads have the whole step to arrive.
+// Step S (0..7) of block blk. Going in, the step's A operands are in registers (af[S & 1]), its B
+// operands are loaded or in flight (b[S & 1]), and the decode state of step s + 2 is ready
+// (dec[S & 1]). Between its products the step loads the next step's B fragments and A operands
+// (from LDS buffer (S + 1) & 3), prefetches step s + 3's x slice into L2, loads the weight bytes
+// of a half-block four steps ahead (at S = 1 and 5), decodes step s + 2 into buffer (S + 2) & 3
+// and prepares step s + 3's decode; it ends at the barrier. Buffer (S + 1) & 3 was written
+// during step s - 1 and made visible by the barrier that ended it; buffer (S + 2) & 3 held step
+// s - 2's operands, read during step s - 3, so one barrier per step orders every LDS write
+// against its reads.
 // LAST: the row's last block (steps past its end are not prepared).
 template <class G, int RM, int S, bool LAST>
 __device__ __forceinline__ void tall_step(TallState<G, RM> &st, uint16_t (*As)[128 * TLDK], int blk,
@@ -289,32 +313,11 @@ __device__ __forceinline__ void tall_step(TallState<G, RM> &st, uint16_t (*As)[1
   constexpr bool HAS1 = !(LAST && S == 7);  // step s + 1 exists
   constexpr bool HAS2 = !(LAST && S >= 6);  // step s + 2 exists
   constexpr bool HAS3 = !(LAST && S >= 5);  // step s + 3 exists
-  const int s = s0 + 8 * blk + S;           // this step's index in the row
-  if constexpr (HAS1) {
-#pragma unroll
-    for (int jj = 0; jj < 4; jj++)
-#pragma unroll
-      for (int u = 0; u < 2; u++) st.b[S1 & 1][jj][u] = x_frag(xv, jj, s + 1, u);
-  }
-  if constexpr (HAS3) st.pf[S & 3] = x_prefetch(xv, s + 3);
-  asm volatile("" ::"v"(st.pf[(S + 2) & 3]));  // the prefetch issued two steps ago
-  if constexpr (S == 1 && !LAST) {
-    G::template load<0>(wblk0 + (blk + 1) * G::BYTES, h, st.raw[0]);
-  } else if constexpr (S == 5 && !LAST) {
-    G::template load<1>(wblk0 + (blk + 1) * G::BYTES, h, st.raw[1]);
-  }
-  if constexpr (HAS1) {  // step s + 1's A operands: written during step s - 1, visible since its barrier
-    const uint16_t *ar = As[S1 & 3] + ao;
-#pragma unroll
-    for (int u = 0; u < 2; u++)
-#pragma unroll
-      for (int i = 0; i < RM / 32; i++)
-        st.af[S1 & 1][u][i] = *reinterpret_cast<const uint4 *>(ar + 32 * i * TLDK + 16 * u);
-  }
+  StepMem mem{&xv, s0 + 8 * blk + S, As[S1 & 3] + ao, wblk0 + (blk + 1) * G::BYTES};
   float y[16];
   uint32_t o[8];
   __builtin_amdgcn_sched_barrier(0);
-  step_products<G, RM, S, 0, HAS2, HAS3>(st, h, y, o, As[S2 & 3] + aw);
+  step_products<G, RM, S, 0, HAS1, HAS2, HAS3, LAST>(st, h, y, o, As[S2 & 3] + aw, mem);
   if constexpr (HAS1) __syncthreads();
 }
 
