@@ -211,13 +211,12 @@ struct TallArgs {
 typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
 
 // The wave's view of x: a buffer resource over xf, the byte offset of its first fragment block,
-// and the per-lane offsets of a fragment load and of the L2 prefetch.
+// and the per-lane offset of a fragment load.
 struct XView {
   __amdgpu_buffer_rsrc_t rs;
   int base;     // bytes: first token block * nsteps * 2048
   int stride;   // bytes between token blocks: nsteps * 2048
   int vlane;    // lane * 16
-  int vpf;      // prefetch lane: token block l/16, half (l/8)%2, 128-byte line l%8
 };
 
 // Fragment (token block jj of the wave, step s, half u) into registers.
@@ -226,19 +225,12 @@ __device__ __forceinline__ uint4 x_frag(const XView &xv, int jj, int s, int u) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// One dword of every 128-byte line of the wave's slice of step s: the lines reach L2 before the
-// step's fragment loads ask for them. The result is consumed (opaquely) two steps later.
-__device__ __forceinline__ uint32_t x_prefetch(const XView &xv, int s) {
-  return __builtin_amdgcn_raw_buffer_load_b32(xv.rs, xv.vpf, xv.base + s * 2048, 0);
-}
-
 template <class G, int RM>
 struct TallState {
   typename G::Raw raw[2];   // by phase: raw[0] steps 0-3 of a block, raw[1] steps 4-7
   typename G::Dec dec[2];   // the decode state of steps s + 2 (dec[S & 1]) and s + 3
   uint4 b[2][4][2];         // B fragments by step parity, token block of 32, half of the step
   uint4 af[2][2][RM / 32];  // A fragments by step parity, half of the step, row tile of 32
-  uint32_t pf[4];           // L2 prefetch results, by step mod 4
   f32x16_t acc[RM / 32][4];
 };
 
@@ -253,8 +245,8 @@ struct StepMem {
 // Product K (0..NK-1) of a step, then the work that slot carries:
 //   slots 0..7    the next step's B fragment K (x_frag), and value K of step s + 2's decode
 //   slots 8..15   the next step's A fragment K - 8 (LDS), and value K
-//   slots 16..23  the bf16 pairs; slot 16 the L2 prefetch, slot 17 a half-block's weight bytes,
-//                 slot 23 the decoded values to LDS
+//   slots 16..23  the bf16 pairs; slot 17 a half-block's weight bytes, slot 23 the decoded values
+//                 to LDS
 //   slots 24..    the preparation of step s + 3's decode
 // A scheduling barrier after each slot keeps this order, so every v_mfma is followed by one
 // memory instruction and a few independent VALU instructions, which issue while the matrix core
@@ -271,10 +263,6 @@ __device__ __forceinline__ void step_products(TallState<G, RM> &st, int h, float
     if constexpr (HAS1 && K >= 8 && K < 8 + 2 * (RM / 32)) {
       constexpr int un = (K - 8) / (RM / 32), in = (K - 8) % (RM / 32);
       st.af[(S + 1) & 1][un][in] = *reinterpret_cast<const uint4 *>(mem.ar + 32 * in * TLDK + 16 * un);
-    }
-    if constexpr (K == 16) {
-      if constexpr (DEC3) st.pf[S & 3] = x_prefetch(*mem.xv, mem.s + 3);
-      asm volatile("" ::"v"(st.pf[(S + 2) & 3]));  // the prefetch issued two steps ago
     }
     if constexpr (K == 17 && !LAST) {
       if constexpr (S == 1) G::template load<0>(mem.wnext, h, st.raw[0]);
@@ -299,7 +287,7 @@ __device__ __forceinline__ void step_products(TallState<G, RM> &st, int h, float
 // Step S (0..7) of block blk. Going in, the step's A operands are in registers (af[S & 1]), its B
 // operands are loaded or in flight (b[S & 1]), and the decode state of step s + 2 is ready
 // (dec[S & 1]). Between its products the step loads the next step's B fragments and A operands
-// (from LDS buffer (S + 1) & 3), prefetches step s + 3's x slice into L2, loads the weight bytes
+// (from LDS buffer (S + 1) & 3), loads the weight bytes
 // of a half-block four steps ahead (at S = 1 and 5), decodes step s + 2 into buffer (S + 2) & 3
 // and prepares step s + 3's decode; it ends at the barrier. Buffer (S + 1) & 3 was written
 // during step s - 1 and made visible by the barrier that ended it; buffer (S + 2) & 3 held step
@@ -377,9 +365,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // decoder role: row tid % 128 of the tile, values 16h .. 16h+15 of each step (h = tid / 128);
-  // eight consecutive lanes write eight consecutive 80-byte LDS rows, one bank set each
-  const int ar = tid & 127, h = tid >> 7;
+  // decoder role: row tid / 2 of the tile, values 16h .. 16h+15 of each step (h = tid % 2). The
+  // two lanes of a row read adjacent 16-byte pieces of its block, so a wave's weight load touches
+  // 32 rows' lines instead of 64: the texture unit, which also carries every B fragment, spends
+  // its time per line.
+  const int ar = tid >> 1, h = tid & 1;
   const uint8_t *wblk0 = p.w + (int64_t)min(m0 + ar, p.rows - 1) * p.row_bytes + (int64_t)(kb / 256) * G::BYTES;
   const int aw = ar * TLDK + 16 * h;
   const int ao = (lane & 31) * TLDK + 8 * (lane >> 5);
@@ -393,7 +383,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   xv.stride = nsteps * 2048;
   xv.base = jfirst * xv.stride;
   xv.vlane = lane * 16;
-  xv.vpf = (lane >> 4) * xv.stride + ((lane >> 3) & 1) * 1024 + (lane & 7) * 128;
   const int s0 = kb / TK;
 
   TallState<G, RM> st;
@@ -411,15 +400,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   if (nblk > 0) {
     // steps 0 and 1 decoded into buffers 0 and 1, step 2's decode prepared, step 0's operands in
-    // registers, the x slices of steps 1 and 2 prefetched into L2
+    // registers
     G::template load<0>(wblk0, h, st.raw[0]);
     G::template load<1>(wblk0, h, st.raw[1]);
 #pragma unroll
     for (int jj = 0; jj < 4; jj++)
 #pragma unroll
       for (int u = 0; u < 2; u++) st.b[0][jj][u] = x_frag(xv, jj, s0, u);
-    st.pf[2] = x_prefetch(xv, s0 + 1);
-    st.pf[3] = x_prefetch(xv, s0 + 2);
     decode_step<G, 0>(st.raw[0], h, As[0] + aw);
     decode_step<G, 1>(st.raw[0], h, As[1] + aw);
     prep_all<G, 2, 0>(st.raw[0], h, st.dec[0]);
