@@ -182,17 +182,30 @@ struct TQ6K {
 // xf + (j * nsteps + s) * 128: half u (columns 16u .. 16u+15 of the step), lane l holds token
 // 32j + l%32, columns 32s + 16u + 8(l/32) .. +7 as bf16 (round to nearest even). Tokens past T
 // repeat token T - 1 (their results are never stored).
+// One workgroup per (token block j, 8 steps): the 32 tokens' 256 columns come in as 1 KB rows
+// (a wave reads one row's 256 floats), go through LDS as bf16, and leave as the 8 fragments
+// (j, s0 .. s0+7), 16 KB contiguous in xf.
+constexpr int FRAG_ROW = 64 + 2;  // uint2 per LDS row: 256 bf16 and a 16-byte pad
 __global__ __launch_bounds__(256) void to_frag_kernel(const float *__restrict__ x, int T, int cols,
-                                                      uint4 *__restrict__ xf, int64_t n) {
-  const int nsteps = cols / TK;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int l = (int)(i & 63), u = (int)((i >> 6) & 1);
-    const int64_t f = i >> 7;
-    const int s = (int)(f % nsteps), j = (int)(f / nsteps);
-    const int t = min(32 * j + (l & 31), T - 1);
-    const float4 *p = reinterpret_cast<const float4 *>(x + (int64_t)t * cols + TK * s + 16 * u + 8 * (l >> 5));
-    const float4 a = p[0], b = p[1];
-    xf[i] = make_uint4(pk2(a.x, a.y), pk2(a.z, a.w), pk2(b.x, b.y), pk2(b.z, b.w));
+                                                      uint4 *__restrict__ xf) {
+  __shared__ uint2 lds[32 * FRAG_ROW];
+  const int nsteps = cols / TK, groups = nsteps / 8;
+  const int j = blockIdx.x / groups, s0 = (blockIdx.x % groups) * 8;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const int r = 4 * k + (tid >> 6), c = tid & 63;
+    const int t = min(32 * j + r, T - 1);
+    const float4 v = reinterpret_cast<const float4 *>(x + (int64_t)t * cols + TK * s0)[c];
+    lds[r * FRAG_ROW + c] = make_uint2(pk2(v.x, v.y), pk2(v.z, v.w));
+  }
+  __syncthreads();
+  uint4 *o = xf + ((int64_t)j * nsteps + s0) * 128;
+#pragma unroll
+  for (int m = 0; m < 4; m++) {
+    const int i = tid + 256 * m;  // fragment i / 128 of the 8; piece q = (i / 32) % 4, token l = i % 32
+    const int f = i >> 7, q = (i >> 5) & 3, l = i & 31;
+    o[i] = *reinterpret_cast<const uint4 *>(&lds[l * FRAG_ROW + 8 * f + 2 * q]);
   }
 }
 
@@ -452,14 +465,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
 }
 
+// y = the S chunk partials added in chunk order. V = 4: rows, ldy and y's address are multiples of
+// 4 floats, and each thread adds four adjacent outputs with 16-byte loads and stores.
+template <int V>
 __global__ __launch_bounds__(256) void tall_combine_kernel(const float *__restrict__ part, int S, int T, int rows,
                                                            float *__restrict__ y, int64_t ldy) {
-  const int64_t plane = (int64_t)T * rows;
+  typedef float fv_t __attribute__((ext_vector_type(V)));
+  const int64_t plane = (int64_t)T * rows / V, rv = rows / V;
+  const fv_t *pv = reinterpret_cast<const fv_t *>(part);
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < plane; i += (int64_t)gridDim.x * blockDim.x) {
-    float s = part[i];
-    for (int c = 1; c < S; c++) s += part[c * plane + i];  // chunk order
-    const int64_t t = i / rows, r = i % rows;
-    y[t * ldy + r] = s;
+    fv_t s = pv[i];
+    for (int c = 1; c < S; c++) s += pv[c * plane + i];  // chunk order
+    const int64_t t = i / rv, r = i % rv;
+    *reinterpret_cast<fv_t *>(y + t * ldy + r * V) = s;
   }
 }
 
@@ -505,10 +523,8 @@ hipError_t gemm_tall_launch(int type, const uint8_t *w, int64_t row_bytes, int r
   if (cols <= 0 || cols % 256 || !scratch) return hipErrorInvalidValue;
   const TallPlan pl = tall_plan(rows, cols, T, num_cu);
   const int64_t nfrag = (int64_t)((T + 31) / 32) * (cols / TK) * 128;
-  int64_t g = (nfrag + 255) / 256;
-  if (g > 8192) g = 8192;
   uint4 *xf = reinterpret_cast<uint4 *>(scratch);
-  hipLaunchKernelGGL(to_frag_kernel, dim3((unsigned)g), dim3(256), 0, st, x, T, cols, xf, nfrag);
+  hipLaunchKernelGGL(to_frag_kernel, dim3((unsigned)((T + 31) / 32 * (cols / 256))), dim3(256), 0, st, x, T, cols, xf);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   float *part = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + nfrag * 16);
@@ -539,9 +555,15 @@ hipError_t gemm_tall_launch(int type, const uint8_t *w, int64_t row_bytes, int r
   else hipLaunchKernelGGL((gemm_tall_kernel<TQ6K, 128>), grid, block, 0, st, a);
   e = hipGetLastError();
   if (e != hipSuccess || pl.S == 1) return e;
-  int64_t gc = ((int64_t)T * rows + 255) / 256;
+  const bool v4 = rows % 4 == 0 && ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
+  int64_t gc = ((int64_t)T * rows / (v4 ? 4 : 1) + 255) / 256;
   if (gc > 8192) gc = 8192;
-  hipLaunchKernelGGL(tall_combine_kernel, dim3((unsigned)gc), dim3(256), 0, st, part, pl.S, T, rows, y, (int64_t)ldy);
+  if (v4)
+    hipLaunchKernelGGL(tall_combine_kernel<4>, dim3((unsigned)gc), dim3(256), 0, st, part, pl.S, T, rows, y,
+                       (int64_t)ldy);
+  else
+    hipLaunchKernelGGL(tall_combine_kernel<1>, dim3((unsigned)gc), dim3(256), 0, st, part, pl.S, T, rows, y,
+                       (int64_t)ldy);
   return hipGetLastError();
 }
 
