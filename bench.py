@@ -471,6 +471,16 @@ def run_workloads(ctx, L, stream, layers, host70, only):
                                 % ("Q4_K" if t == Q4_K else "Q6_K", rows, cols, cols)}
         for w in ws:
             w.free()
+        # the vendor library on the same product with dense bf16 operands already in HBM (no
+        # decode, no fp32 x): W [rows x cols] @ X^T [cols x T], both contiguous
+        wb = torch.randn(rows, cols, device=dev, dtype=torch.bfloat16)
+        xt = x.t().contiguous().to(torch.bfloat16)
+        ms_v = time_events(stream, lambda i: torch.matmul(wb, xt), 20, warm=3)
+        out[key]["vendor_bf16_gemm"] = {
+            "us": round(ms_v * 1e3, 1), "tflops": round(flops / (ms_v * 1e-3) / 1e12, 1),
+            "what": "torch.matmul (hipBLASLt) of dense bf16 W [%d x %d] and X^T [%d x 512], same stream and "
+                    "timing" % (rows, cols, cols)}
+        del wb, xt
 
         def pre_cpu(t=t, rows=rows, cols=cols, host=host):
             oracle = _oracle()

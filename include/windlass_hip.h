@@ -212,6 +212,13 @@ int wl_gate_up_dev(wl_ctx *ctx, const wl_weight *gate, const wl_weight *up, int3
 /* wl_dequant_f32 into a device buffer. */
 int wl_dequant_dev(wl_ctx *ctx, const wl_weight *w, int64_t row0, int64_t nrows, float *d_dst);
 
+/* How the MoE entries run (no counterpart in the reference, whose MoeFfn is one host loop):
+ * on = 1 (the default) routes, plans, runs gate/up and down and combines in one launch where
+ * the shapes allow it (Q4_K/Q6_K experts, hidden and FFN up to 2048, up to 64 token-expert
+ * pairs per pass, up to 256 experts, float products); on = 0 always runs the launch chain
+ * (route+plan, gate/up, down, combine). Both give the same bits. */
+int wl_set_moe_one_launch(wl_ctx *ctx, int on);
+
 /* wl_moe_ffn on device buffers (logits, x, out in HBM). */
 int wl_moe_ffn_dev(wl_ctx *ctx, const float *d_logits, int32_t k, int32_t renorm,
                    const wl_weight *gate_exps, const wl_weight *up_exps,

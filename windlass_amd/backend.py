@@ -144,6 +144,17 @@ class Context:
         check(self._lib.wl_set_int_dot(self.handle, int(bool(on))))
         self._int_dot = bool(on)
 
+    @property
+    def MoeOneLaunch(self):
+        """Whether the MoE entries may run as one launch (the default) or always as the launch
+        chain (route+plan, gate/up, down, combine). Both give the same bits."""
+        return getattr(self, "_moe_one", True)
+
+    @MoeOneLaunch.setter
+    def MoeOneLaunch(self, on):
+        check(self._lib.wl_set_moe_one_launch(self.handle, int(bool(on))))
+        self._moe_one = bool(on)
+
     def upload(self, t, blocks, rows, cols, experts=1, name="weight"):
         """Raw GGUF blocks to HBM, unchanged (LayerStream.Bind, src/LayerStream.cs:182-203)."""
         return WeightView(self, t, blocks, rows, cols, experts, name)

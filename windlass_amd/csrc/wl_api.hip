@@ -47,12 +47,13 @@ struct wl_stage {
 };
 
 // S_PART holds the K-chunk partials of split GEMV rows, S_XB the bf16 copy of x for the GEMM,
-// S_QA the 8-bit activations of the integer path.
+// S_QA the 8-bit activations of the integer path, S_MSYNC the one-launch MoE's counters
+// (allocated and zeroed once; every launch leaves them zero).
 // S_L* are wl_layer_dev's activations (S_LO: wl_matmul_add_dev's product when the add is not
 // the GEMV's own store; S_LR the router's logits and the shared expert's gate, S_LM the MoE
 // FFN's output, S_LS the shared expert's).
 enum { S_X = 0, S_Y, S_H, S_MOE, S_OUT, S_AUX, S_PART, S_XB, S_QA, S_ATT,
-       S_LXN, S_LQ, S_LK, S_LV, S_LATT, S_LO, S_LG, S_LU, S_LR, S_LM, S_LS, S_ROWS, S_ARG, S_COUNT };
+       S_LXN, S_LQ, S_LK, S_LV, S_LATT, S_LO, S_LG, S_LU, S_LR, S_LM, S_LS, S_ROWS, S_ARG, S_MSYNC, S_COUNT };
 
 struct wl_ctx {
   int device;
@@ -60,6 +61,8 @@ struct wl_ctx {
   hipStream_t stream;
   hipStream_t copy;  // stage uploads (default priority), created on first use
   int int_dot;  // Transformer.IntDot (src/Transformer.cs:23)
+  int moe_chain;  // wl_set_moe_one_launch(0): the MoE entries always run the launch chain
+  unsigned moe_launches;  // one-launch MoE launches so far (their counter sets alternate)
   // growable scratch (device)
   void *buf[S_COUNT];
   size_t cap[S_COUNT];
@@ -839,6 +842,10 @@ static int moe_dev(wl_ctx *c, const float *d_logits, int32_t k, int32_t renorm, 
   int rc = moe_check(g, u, d, k);
   if (rc) return rc;
   const int ne = g->experts, ff = (int)g->rows, embd = (int)g->cols;
+  if (!c->buf[S_MSYNC]) {
+    if ((rc = ensure(c, S_MSYNC, sizeof(wl::MoeSync)))) return rc;
+    WL_HIP(wl::moe_sync_init((wl::MoeSync *)c->buf[S_MSYNC], c->stream), "moe counters");
+  }
   for (int t0 = 0; t0 < T; t0 += wl::MOE_MAX_T) {
     const int Tc = T - t0 < wl::MOE_MAX_T ? T - t0 : wl::MOE_MAX_T;
     MoeScratch s = moe_layout(Tc, k, ne, ff, embd);
@@ -861,6 +868,8 @@ static int moe_dev(wl_ctx *c, const float *d_logits, int32_t k, int32_t renorm, 
     m.d_int = c->int_dot && wl::intdot_supports(d->type) && wl::intdot_fits(d->type, ff);
     m.qx = wl::qacts_at(b + s.qx, Tc, embd, wl::intdot_needs_k(g->type) ? 1 : 0);
     m.qh = wl::qacts_at(b + s.qh, Tc * k, ff, wl::intdot_needs_k(d->type) ? 1 : 0);
+    m.sync = c->moe_chain ? nullptr : (wl::MoeSync *)c->buf[S_MSYNC];
+    m.parity = (int)(c->moe_launches++ & 1);
     WL_HIP(wl::moe_launch(m, c->num_cu, c->stream), "moe launch");
   }
   return WL_OK;
@@ -901,12 +910,26 @@ extern "C" int wl_moe_ffn(wl_ctx *c, const float *logits, int32_t k, int32_t ren
     }
   }
   WL_HIP(hipMemcpyAsync(out, c->buf[S_OUT], xb, hipMemcpyDeviceToHost, c->stream), "copy out");
+  unsigned err = 0;
+  wl::MoeSync *sy = (wl::MoeSync *)c->buf[S_MSYNC];
+  WL_HIP(hipMemcpyAsync(&err, &sy->err[0], sizeof(err), hipMemcpyDeviceToHost, c->stream), "copy moe status");
   WL_HIP(hipStreamSynchronize(c->stream), "moe");
+  if (err) {
+    WL_HIP(hipMemsetAsync(&sy->err[0], 0, sizeof(err), c->stream), "clear moe status");
+    WL_HIP(hipStreamSynchronize(c->stream), "moe");
+    return fail(WL_E_DEVICE, "moe: a workgroup of the one-launch MoE gave up waiting for its inputs");
+  }
   if (expert_runs) *expert_runs = runs;
   return WL_OK;
 }
 
 // ----------------------------------------------------------------------------- integer path
+
+extern "C" int wl_set_moe_one_launch(wl_ctx *c, int on) {
+  if (!c) return fail(WL_E_ARG, "wl_set_moe_one_launch: null context");
+  c->moe_chain = on ? 0 : 1;
+  return WL_OK;
+}
 
 extern "C" int wl_set_int_dot(wl_ctx *c, int on) {
   if (!c) return fail(WL_E_ARG, "wl_set_int_dot: null context");

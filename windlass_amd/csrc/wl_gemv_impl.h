@@ -159,7 +159,16 @@ struct CsSlots {
 // GS groups (and after the last) one barrier, then wave 0 finishes the buffered groups while
 // the other waves go on into the other buffer. g and the slot state are uniform over the
 // workgroup, so every wave takes the same branches.
-template <int TM, int R, int NM>
+// A store another workgroup reads in the same launch (WT): written through to the device's
+// point of coherence (an agent-scope store), so the reader needs no cache write-back from the
+// writer. Otherwise a plain store.
+template <bool WT, class V>
+__device__ __forceinline__ void put(V *p, V v) {
+  if constexpr (WT) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = v;
+}
+
+template <int TM, int R, int NM, bool WT = false>
 __device__ __forceinline__ void cs_finish(const float (&acc)[NM][R][TM], int g, int gstride, int ngroups,
                                           CsSlots &st, float *part, const CsRows &W, const CsIO &io) {
   constexpr int V = NM * R * TM;
@@ -199,7 +208,7 @@ __device__ __forceinline__ void cs_finish(const float (&acc)[NM][R][TM], int g, 
             s = silu_mul(s, s1);
           }
         }
-        io.y[o] = io.add ? add_scaled(io.y[o], s, io.rs) : s;
+        put<WT>(&io.y[o], io.add ? add_scaled(io.y[o], s, io.rs) : s);
       }
     }
   }
@@ -209,7 +218,7 @@ __device__ __forceinline__ void cs_finish(const float (&acc)[NM][R][TM], int g, 
 }
 
 // SP: passes whose x slices stay in registers (0: x read per row group; 1 or 2 only for TM 1).
-template <class C, int TM, int R, int NM, int SP>
+template <class C, int TM, int R, int NM, int SP, bool WT = false>
 __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int cols, int g0, int gstride,
                                         uint8_t *lds_raw) {
   constexpr int V = NM * R * TM;
@@ -291,8 +300,90 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
         }
       }
     }
-    cs_finish<TM, R, NM>(acc, g, gstride, ngroups, st, part, W, io);
+    cs_finish<TM, R, NM, WT>(acc, g, gstride, ngroups, st, part, W, io);
   }
+}
+
+// Row group g of W (R rows of each of the NM matrices, all cols up to one wave-column: 64 / LPB
+// blocks) by one wave, with nothing shared with the other waves of its workgroup: the lanes'
+// partials as cs_gemv forms them (the same unpack and dot), folded by the same tree and added
+// across nothing (one wave), so each result has cs_gemv's bits for a one-wave workgroup.
+// cs_group_load issues the group's weight loads (they may be in flight across other work);
+// cs_group_finish takes them from there. `part` is the wave's own LDS scratch of NM * R * TM
+// floats. WT: agent-scope stores (read by another workgroup in the same launch).
+template <class C, int R, int NM>
+__device__ __forceinline__ void cs_group_load(const CsRows &W, int cols, int g, typename C::Raw (&raw)[NM][R]) {
+  const int lane = threadIdx.x & 63;
+  const int b = lane / C::LPB;
+  if (b < cols / C::BLOCK) cs_load<C, R, NM>(W, g, b, C::lane(lane % C::LPB), raw);
+}
+
+template <class C, int TM, int R, int NM, bool WT>
+__device__ __forceinline__ void cs_group_finish(const CsRows &W, const CsIO &io, int cols, int g, float *part,
+                                                const typename C::Raw (&raw)[NM][R]) {
+  constexpr int V = NM * R * TM;
+  constexpr int LOW = 6 - ilog2(V);
+  static_assert(!C::NEED_LDS, "codecs with LDS tables run through cs_gemv");
+  const Lds &lds = *reinterpret_cast<const Lds *>(part);  // unused by these codecs
+  const int lane = threadIdx.x & 63;
+  const int sub = lane % C::LPB, b = lane / C::LPB;
+  const typename C::Lane L = C::lane(sub);
+  float acc[NM][R][TM];
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+      for (int t = 0; t < TM; t++) acc[m][r][t] = 0.f;
+  if (b < cols / C::BLOCK) {
+    typename C::W wv[NM][R];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int r = 0; r < R; r++) C::unpack(raw[m][r], L, lds, wv[m][r]);
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+      if (t < io.T) {
+        const float *xr = io.x + (int64_t)(io.xrow ? io.xrow[t] : t) * io.ldx;
+        typename C::Xs xs;
+        C::load_x(xr + (int64_t)b * C::BLOCK, L, xs);
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+          for (int r = 0; r < R; r++) acc[m][r][t] += C::dot(wv[m][r], xs);
+      }
+    }
+  }
+  float vals[V];
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+      for (int r = 0; r < R; r++) vals[(m * TM + t) * R + r] = acc[m][r][t];
+  const float q = exch_reduce<V, 5>(vals, lane);
+  if ((lane & ((1 << LOW) - 1)) == 0) part[lane >> LOW] = q;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (int i = lane; i < R * TM; i += 64) {
+    const int r = i % R, t = i / R;
+    const int row = g * R + r;
+    if (t < io.T && row < W.rows) {
+      float v = part[t * R + r];
+      if constexpr (NM == 2) v = silu_mul(v, part[(TM + t) * R + r]);
+      put<WT>(&io.y[(int64_t)(io.yrow ? io.yrow[t] : t) * io.ldy + row], v);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();  // part is reused by the wave's next group
+}
+
+template <class C, int TM, int R, int NM, bool WT>
+__device__ __forceinline__ void cs_group_wave(const CsRows &W, const CsIO &io, int cols, int g, float *part) {
+  typename C::Raw raw[NM][R];
+  cs_group_load<C, R, NM>(W, cols, g, raw);
+  cs_group_finish<C, TM, R, NM, WT>(W, io, cols, g, part, raw);
 }
 
 }  // namespace wl

@@ -24,6 +24,26 @@ struct MoePlan {
   float comb_w[MOE_MAX_T][MOE_MAX_K];
 };
 
+// Counters of the one-launch MoE (moe_fused_*), two sets used by alternate launches: a launch
+// clears the set the next one uses. The flag every workgroup polls is replicated on 64 cache
+// lines and the arrivals spread over 16 counters, because the device serialises atomics and
+// polls on one address (about 11 ns each). `err` is sticky: a wait that ran out of patience
+// (never expected; the workgroup goes on without its inputs and the host reports it).
+constexpr int MOE_SYNC_REP = 64;      // replicas of the polled flag
+constexpr int MOE_SYNC_SUB = 16;      // arrival counters
+constexpr int MOE_SYNC_LINE = 32;     // words per 128-byte line
+constexpr int MOE_SYNC_MAX_G = 8192;  // row groups of the down projection
+struct MoeSyncSet {
+  unsigned arrive[MOE_SYNC_SUB * MOE_SYNC_LINE];
+  unsigned top[MOE_SYNC_LINE];
+  unsigned h_ready[MOE_SYNC_REP * MOE_SYNC_LINE];
+};
+struct MoeSync {
+  MoeSyncSet set[2];
+  unsigned d_done[MOE_SYNC_MAX_G];  // per down row group; the combining wave clears its own
+  unsigned err[MOE_SYNC_LINE];
+};
+
 struct MoeGemvArgs {
   const MoePlan *plan;
   const uint8_t *w, *w2;
@@ -55,11 +75,17 @@ struct MoeLaunch {
   // quantized into qx and h into qh
   int gu_int, d_int;
   QActsDev qx, qh;
+  // counters of the one-launch path (zeroed once when allocated), or null for the launch chain;
+  // parity: this launch's set (alternates between launches)
+  MoeSync *sync;
+  int parity;
 };
 
 bool moe_supports(int type);
 hipError_t route_launch(const float *logits, int T, int n, int k, int renorm, int *sel, float *wts, float *prob,
                         hipStream_t st);
 hipError_t moe_launch(const MoeLaunch &m, int num_cu, hipStream_t st);
+// Zeroes a MoeSync once after its allocation (a kernel, so it may sit in a captured stream).
+hipError_t moe_sync_init(MoeSync *s, hipStream_t st);
 
 }  // namespace wl

@@ -11,6 +11,8 @@
 //   4. moe_down        grouped decode GEMV of each pair's hidden row with its expert's down;
 //   5. combine_kernel  out[t] = sum over t's experts, ascending, of w * y (:289-293).
 // Only the chosen experts are read (tests/MoeTests.cs:164-181).
+#include <climits>
+
 #include "wl_moe_launch.h"
 
 #pragma clang fp contract(off)
@@ -64,7 +66,7 @@ __global__ void route_serial_kernel(const float *__restrict__ logits, int T, int
 // room for n 64-bit keys; rk_i, rk_w: k entries each).
 constexpr int kRouteWaveMax = 64 * 32;
 
-template <int PER>
+template <int PER, bool WT = false>
 __device__ __forceinline__ void route_wave(const float *__restrict__ l, int n, int k, int renorm,
                                            int *__restrict__ sel, float *__restrict__ wts, float *__restrict__ pl,
                                            int *__restrict__ rk_i, float *__restrict__ rk_w) {
@@ -119,8 +121,8 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ l, int n, i
   }
   if (__any(nan)) {
     if (lane < k) {
-      sel[lane] = lane;
-      wts[lane] = __builtin_nanf("");
+      put<WT>(&sel[lane], lane);
+      put<WT>(&wts[lane], __builtin_nanf(""));
     }
     return;
   }
@@ -178,8 +180,8 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ l, int n, i
       const float div = chosen > WL_MIN_EXPERT_WEIGHT_SUM ? chosen : WL_MIN_EXPERT_WEIGHT_SUM;
       w /= div;
     }
-    sel[lane] = rk_i[lane];
-    wts[lane] = w;
+    put<WT>(&sel[lane], rk_i[lane]);
+    put<WT>(&wts[lane], w);
   }
 }
 
@@ -198,16 +200,21 @@ __global__ __launch_bounds__(64) void route_wave_kernel(const float *__restrict_
 // the combine (:289-293).
 constexpr int kPlanMaskExperts = 8192;  // experts the plan's bitmask covers; more use pair scans
 
+template <bool WT = false>
 __device__ __forceinline__ void plan_pairs(const int *__restrict__ sel, const float *__restrict__ wts, int T, int k,
                                            int n, MoePlan *__restrict__ plan) {
-  __shared__ __attribute__((aligned(16))) int se[MOE_MAX_PAIRS];
+  // se: the choices, then INT_MAX up to a multiple of 4 (no expert is above or equal to it);
+  // emask: experts chosen by any pair, cleared to a multiple of 4 words. Both are read 16 bytes
+  // at a time so the reads of a scan are in flight together.
+  __shared__ __attribute__((aligned(16))) int se[MOE_MAX_PAIRS + 4];
   __shared__ int first_of[MOE_MAX_PAIRS];              // pair a is the lowest-index pair of its expert
-  __shared__ uint32_t emask[kPlanMaskExperts / 32];  // experts chosen by any pair
-  const int P = T * k, i = threadIdx.x, nw = (n + 31) / 32;
+  __shared__ __attribute__((aligned(16))) uint32_t emask[kPlanMaskExperts / 32];
+  const int P = T * k, P4 = (P + 3) & ~3, i = threadIdx.x, nw = (n + 31) / 32, nw4 = (nw + 3) & ~3;
   const bool masked = n <= kPlanMaskExperts;
   if (masked)
-    for (int w = i; w < nw; w += blockDim.x) emask[w] = 0;
+    for (int w = i; w < nw4; w += blockDim.x) emask[w] = 0;
   if (i < P) se[i] = sel[i];
+  else if (i < P4) se[i] = INT_MAX;
   __syncthreads();
   if (i < P) {
     if (masked) {
@@ -224,11 +231,17 @@ __device__ __forceinline__ void plan_pairs(const int *__restrict__ sel, const fl
   // distinct experts below e (the slot) and in all
   int slot = 0, nslots = 0;
   if (masked) {
-    for (int w = 0; w < nw; w++) {
-      const uint32_t m = emask[w];
-      const int c = __popc(m);
-      nslots += c;
-      slot += w < (e >> 5) ? c : (w == (e >> 5) ? __popc(m & ((1u << (e & 31)) - 1u)) : 0);
+    const uint4 *m4 = reinterpret_cast<const uint4 *>(emask);
+    for (int w0 = 0; w0 < nw4; w0 += 4) {
+      const uint4 q = m4[w0 >> 2];
+      const uint32_t mv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int w = w0 + u;
+        const int c = __popc(mv[u]);
+        nslots += c;
+        slot += w < (e >> 5) ? c : (w == (e >> 5) ? __popc(mv[u] & ((1u << (e & 31)) - 1u)) : 0);
+      }
     }
   } else {
     for (int a = 0; a < P; a++) {
@@ -236,31 +249,38 @@ __device__ __forceinline__ void plan_pairs(const int *__restrict__ sel, const fl
       slot += first_of[a] & (int)(se[a] < e);
     }
   }
-  // pairs before this one in the numbering (experts ascending, tokens ascending), and this
-  // expert's tokens before t and in all
-  int rank = 0, before = 0, same = 0;
-  for (int ta = 0; ta < T; ta++) {
-    const int tb = (int)(ta < t);
-    for (int c = 0; c < k; c++) {
-      const int ea = se[ta * k + c], lt = (int)(ea < e), eq = (int)(ea == e);
+  // pairs before this one in the numbering (experts ascending, tokens ascending), this expert's
+  // tokens before t and in all, and this token's pairs of lower experts; pair a is (token ta,
+  // choice c)
+  int rank = 0, before = 0, same = 0, pos = 0, ta = 0, c = 0;
+  const int4 *s4 = reinterpret_cast<const int4 *>(se);
+  for (int a0 = 0; a0 < P4; a0 += 4) {
+    const int4 q = s4[a0 >> 2];
+    const int ev[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int ea = ev[u], tb = (int)(ta < t), lt = (int)(ea < e), eq = (int)(ea == e);
       rank += lt | (eq & tb);
       same += eq;
       before += eq & tb;
+      pos += lt & (int)(ta == t);
+      if (++c == k) {
+        c = 0;
+        ta++;
+      }
     }
   }
-  int pos = 0;  // this token's pairs of lower experts
-  for (int c = 0; c < k; c++) pos += (int)(se[t * k + c] < e);
-  plan->slot_tok[slot][before] = t;
-  plan->slot_pair[slot][before] = rank;
-  plan->tok_pair[t][j] = rank;
-  plan->tok_w[t][j] = wts[i];
-  plan->comb_pair[t][pos] = rank;
-  plan->comb_w[t][pos] = wts[i];
+  put<WT>(&plan->slot_tok[slot][before], t);
+  put<WT>(&plan->slot_pair[slot][before], rank);
+  put<WT>(&plan->tok_pair[t][j], rank);
+  put<WT>(&plan->tok_w[t][j], wts[i]);
+  put<WT>(&plan->comb_pair[t][pos], rank);
+  put<WT>(&plan->comb_w[t][pos], wts[i]);
   if (before == 0) {
-    plan->slot_expert[slot] = e;
-    plan->slot_ntok[slot] = same;
+    put<WT>(&plan->slot_expert[slot], e);
+    put<WT>(&plan->slot_ntok[slot], same);
   }
-  if (i == 0) plan->nslots = nslots;
+  if (i == 0) put<WT>(&plan->nslots, nslots);
 }
 
 // Routing and plan in one workgroup of T waves (64 * T threads, at least one per pair): wave t routes token t (unless `route` is 0 and
@@ -288,6 +308,381 @@ __global__ void combine_kernel(const MoePlan *__restrict__ plan, const float *__
   float o = 0.f;
   for (int j = 0; j < k; j++) o += plan->comb_w[t][j] * yd[(int64_t)plan->comb_pair[t][j] * embd + d];
   out[i] = o;
+}
+
+// ------------------------------------------------------------------ one launch for the layer
+// Route, plan, gate/up, down and the combine in one launch of G workgroups of eight waves, G no
+// more than the device holds at once, so every workgroup is eventually resident while the
+// others wait (a bounded wait in any case):
+//   phase 1  every workgroup routes the T tokens itself (route_group: route_wave's results
+//            with 512 / T threads per token) and numbers the pairs into its LDS; workgroup 0
+//            also stores the plan for the host;
+//   phase 2  the waves take the gate/up row groups i = gw, gw + 8G, ... of the chosen slots
+//            (gw the wave's index in the grid; slot i / groups, group i % groups) and write h;
+//            then a grid barrier (16 arrival counters, a count of the complete ones, a flag
+//            on 64 replicas);
+//   phase 3  the down row groups the same way, writing yd; the wave that finishes a row group's
+//            last slot (a per-group count) adds the tokens' pairs for its rows in ascending
+//            expert order, as combine_kernel does, and clears the count.
+// Each row group is computed by cs_group_wave, whose results are cs_gemv's for a one-wave
+// workgroup, as the launch chain runs these shapes: the same bits. Stores another workgroup
+// reads are agent-scope (written through to the point of coherence). Readers of h acquire once
+// per CU after the barrier (the polling wave's acquire; the others follow it through the
+// workgroup barrier); the combine reads yd with agent-scope loads, since a cache
+// invalidation per row group would throw away the lines every other wave's weight reads share.
+// Every wait is bounded (kMoeSpin polls); one that runs out sets `err`.
+struct MoeFusedArgs {
+  const float *logits;
+  int T, ne, k, renorm;
+  MoePlan *plan;
+  const uint8_t *gate, *up, *down;
+  int64_t gu_row_bytes, d_row_bytes, gu_stride, d_stride;  // bytes per row, per expert
+  int ff, embd;
+  const float *x;
+  float *h, *yd, *out;
+  MoeSync *sync;
+  int parity, max_slots;
+};
+
+constexpr int kMoeSpin = 1 << 18;
+constexpr int kMoeWaves = 8;
+
+// Polls *p until it reaches v, then acquires (one cache invalidation, not one per poll). False
+// when the patience runs out (err set).
+__device__ __forceinline__ bool moe_wait_ge(unsigned *p, unsigned v, MoeSync *sy) {
+  for (int i = 0; i < kMoeSpin; i++) {
+    if (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= v) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      return true;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if ((threadIdx.x & 63) == 0) atomicOr(&sy->err[0], 1u);
+  return false;
+}
+
+// One atomic add by the wave's lane 0 once the wave's stores have completed (the
+// cross-workgroup ones are agent-scope, so completion is visibility); the old value goes to
+// every lane of the wave.
+__device__ __forceinline__ unsigned moe_arrive(unsigned *p) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  unsigned old = 0;
+  if ((threadIdx.x & 63) == 0) old = atomicAdd(p, 1u);
+  return __builtin_amdgcn_readfirstlane(old);
+}
+
+// Routing of the T tokens by the whole workgroup: G = 512 / T' threads per token (T' = T
+// rounded up to a power of two), the same results as route_wave.
+//   - The softmax denominator: when every nonzero probability is at least 2^-20, each partial
+//     sum of up to 256 of them is a multiple of 2^-43 below 2^9, exact in double, so the sum
+//     does not depend on the order and a tree adds it; otherwise one thread adds in index
+//     order, as the reference does.
+//   - The ranks: an entry's rank (keys above its own) is counted over S slices of the keys by
+//     S threads and added in LDS (integers: exact).
+constexpr int kRouteMaxN = 256;
+struct RouteLds {
+  float p[kMoeWaves][kRouteMaxN];     // probabilities by group (a group's rows: G / 64 waves)
+  __attribute__((aligned(16))) uint64_t key[kMoeWaves][kRouteMaxN];
+  int rank[kMoeWaves][kRouteMaxN];
+  double dsum[kMoeWaves * 64 / 64];   // per wave
+  float fmax[kMoeWaves];
+  int rk_i[kMoeWaves][MOE_MAX_K];
+  float rk_w[kMoeWaves][MOE_MAX_K];
+  int inexact, nan[kMoeWaves];
+};
+
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float u = __shfl_xor(v, o, 64);
+    if (u > v) v = u;
+  }
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ void route_group(const float *__restrict__ logits, int T, int n, int k, int renorm, int *__restrict__ sel,
+                            float *__restrict__ wts, RouteLds &L) {
+  const int tid = threadIdx.x, Tp = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8;
+  const int gs = 64 * kMoeWaves / Tp, grp = tid / gs, li = tid % gs, wv = tid >> 6;
+  const int wpg = gs / 64, w0 = grp * wpg;  // the group's waves
+  const bool act = grp < T;
+  const float *l = logits + (int64_t)(act ? grp : 0) * n;
+  constexpr int PM = kRouteMaxN / 64;
+  float v[PM];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int m = 0; m < PM; m++) {
+    const int e = li + gs * m;
+    v[m] = act && e < n ? l[e] : -INFINITY;
+    if (v[m] > mx) mx = v[m];  // NaN never wins, as in the reference's scan
+  }
+  mx = wave_max_f(mx);
+  if ((tid & 63) == 0) L.fmax[wv] = mx;
+  if (tid == 0) L.inexact = 0;
+  __syncthreads();
+  mx = L.fmax[w0];
+  for (int j = 1; j < wpg; j++) {
+    const float u = L.fmax[w0 + j];
+    if (u > mx) mx = u;
+  }
+  double part = 0;
+  int inexact = 0;
+#pragma unroll
+  for (int m = 0; m < PM; m++) {
+    const int e = li + gs * m;
+    if (act && e < n) {
+      v[m] = (float)exp((double)(v[m] - mx));
+      L.p[grp][e] = v[m];
+      part += (double)v[m];
+      inexact |= (int)(v[m] != 0.f && !(v[m] >= 0x1p-20f));  // tiny, or NaN
+    }
+  }
+  if (inexact) L.inexact = 1;
+  part = wave_sum_d(part);
+  if ((tid & 63) == 0) L.dsum[wv] = part;
+  __syncthreads();
+  double sum = 0;
+  if (!L.inexact) {  // uniform over the workgroup
+    for (int j = 0; j < wpg; j++) sum += L.dsum[w0 + j];
+  } else {  // index order, one thread per group, the result through LDS
+    __syncthreads();  // every wave has read its partial sums' slot before it is reused
+    if (li == 0 && act) {
+      for (int e = 0; e < n; e++) sum += (double)L.p[grp][e];
+      L.dsum[w0] = sum;
+    }
+    __syncthreads();
+    sum = L.dsum[w0];
+  }
+  const float inv = (float)(1.0 / sum);
+  int nan = 0;
+#pragma unroll
+  for (int m = 0; m < PM; m++) {
+    const int e = li + gs * m;
+    if (act && e < n) {
+      v[m] *= inv;
+      nan |= (int)(v[m] != v[m]);
+      // finite and not negative unless NaN: the bits order like the values; ties to the lower id
+      L.key[grp][e] = ((uint64_t)__float_as_uint(v[m]) << 32) | (uint32_t)~e;
+      L.rank[grp][e] = 0;
+    }
+  }
+  nan = __any(nan);
+  if ((tid & 63) == 0) L.nan[wv] = nan;
+  __syncthreads();
+  nan = 0;
+  for (int j = 0; j < wpg; j++) nan |= L.nan[w0 + j];
+  // ranks: the n keys of the group in S slices; unit u = (entry e, slice u / n)
+  int np = 1;
+  while (np < n) np <<= 1;
+  const int S = gs > np ? gs / np : 1, span = (n + S - 1) / S;
+  if (!nan && act) {
+    for (int u = li; u < n * S; u += gs) {
+      const int e = u % n, sl = u / n, j0 = sl * span, j1 = min(n, j0 + span);
+      const uint64_t me = L.key[grp][e];
+      int c = 0, j = j0;
+      for (; j + 8 <= j1 && !(j & 1); j += 8) {  // eight keys per round, the LDS reads in flight together
+        const ulonglong2 *k2 = reinterpret_cast<const ulonglong2 *>(&L.key[grp][j]);
+        ulonglong2 q[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) q[u] = k2[u];
+#pragma unroll
+        for (int u = 0; u < 4; u++) c += (int)(q[u].x > me) + (int)(q[u].y > me);
+      }
+      for (; j < j1; j++) c += (int)(L.key[grp][j] > me);
+      if (S == 1) L.rank[grp][e] = c;
+      else atomicAdd(&L.rank[grp][e], c);
+    }
+  }
+  __syncthreads();
+  if (!nan && act) {
+#pragma unroll
+    for (int m = 0; m < PM; m++) {
+      const int e = li + gs * m;
+      if (e < n) {
+        const int r = L.rank[grp][e];
+        if (r < k) {
+          L.rk_i[grp][r] = e;
+          L.rk_w[grp][r] = v[m];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (act && li < k) {
+    if (nan) {  // every probability is NaN (through the denominator): the scan's first k entries
+      sel[grp * k + li] = li;
+      wts[grp * k + li] = __builtin_nanf("");
+    } else {
+      float chosen = 0;
+      for (int c = 0; c < k; c++) chosen += L.rk_w[grp][c];  // in pick order, as the reference adds them
+      float w = L.rk_w[grp][li];
+      if (renorm) {
+        const float div = chosen > WL_MIN_EXPERT_WEIGHT_SUM ? chosen : WL_MIN_EXPERT_WEIGHT_SUM;
+        w /= div;
+      }
+      sel[grp * k + li] = L.rk_i[grp][li];
+      wts[grp * k + li] = w;
+    }
+  }
+  __syncthreads();
+}
+
+template <class CG, class CD, int TM>
+__global__ __launch_bounds__(64 * kMoeWaves) void moe_fused_kernel(MoeFusedArgs a) {
+  __shared__ RouteLds s_route;
+  __shared__ int s_sel[MOE_MAX_PAIRS];
+  __shared__ float s_wts[MOE_MAX_PAIRS];
+  __shared__ MoePlan s_plan;
+  __shared__ float s_part[kMoeWaves][64];
+  constexpr int RG = TM == 1 ? CG::R1 / 2 : 2, RD = TM == 1 ? CD::R1 : 4;
+  MoeSync *sy = a.sync;
+  MoeSyncSet &S = sy->set[a.parity];
+  const int w = blockIdx.x, G = gridDim.x, tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), gw = w * kMoeWaves + wv, NW = G * kMoeWaves;
+
+  {  // the other set, for the next launch (the previous launch, which used it, has ended)
+    unsigned *o = reinterpret_cast<unsigned *>(&sy->set[a.parity ^ 1]);
+    const int n = (int)(sizeof(MoeSyncSet) / sizeof(unsigned));
+    for (int i = w * 64 * kMoeWaves + tid; i < n; i += G * 64 * kMoeWaves) o[i] = 0;
+  }
+
+  // phase 1: the routing and the plan, in this workgroup's LDS
+  route_group(a.logits, a.T, a.ne, a.k, a.renorm, s_sel, s_wts, s_route);
+  plan_pairs(s_sel, s_wts, a.T, a.k, a.ne, &s_plan);
+  __syncthreads();
+  const MoePlan &pl = s_plan;
+  if (w == 0) {  // the plan for the host (expert runs)
+    const int *src = reinterpret_cast<const int *>(&s_plan);
+    int *dst = reinterpret_cast<int *>(a.plan);
+    for (int i = tid; i < (int)(sizeof(MoePlan) / 4); i += 64 * kMoeWaves) dst[i] = src[i];
+  }
+  const int nslots = min(pl.nslots, a.max_slots);
+
+  // phase 2: gate/up
+  const int ggu = (a.ff + RG - 1) / RG;
+  for (int i = gw; i < nslots * ggu; i += NW) {
+    const int s = i / ggu, g = i % ggu;
+    const int64_t eoff = (int64_t)pl.slot_expert[s] * a.gu_stride;
+    const CsRows W{a.gate + eoff, a.up + eoff, a.gu_row_bytes, a.ff};
+    const CsIO io{a.x, pl.slot_tok[s], a.embd, a.h, pl.slot_pair[s], a.ff, pl.slot_ntok[s]};
+    cs_group_wave<CG, TM, RG, 2, true>(W, io, a.embd, g, s_part[wv]);
+  }
+  // this wave's first down row group: one dword of each of its weights' 128-byte lines, read
+  // across the barrier so the lines are in the caches when phase 3 reads them
+  const int gd = (a.embd + RD - 1) / RD;
+  uint32_t touch = 0;
+  {
+    const int lpr = (int)((a.d_row_bytes + 127) / 128);  // lines per row
+    if (gw < nslots * gd && lane < RD * lpr) {
+      const int r = min((gw % gd) * RD + lane / lpr, a.embd - 1);
+      const int64_t off = min((int64_t)(lane % lpr) * 128, a.d_row_bytes - 4);
+      const uint8_t *row = a.down + (int64_t)pl.slot_expert[gw / gd] * a.d_stride + (int64_t)r * a.d_row_bytes;
+      touch = *reinterpret_cast<const uint32_t *>(row + (off & ~(int64_t)3));
+    }
+  }
+  __syncthreads();
+  if (wv == 0) {  // grid barrier
+    const int nsub = G < MOE_SYNC_SUB ? G : MOE_SYNC_SUB, sub = w % nsub;
+    const unsigned per = (unsigned)((G - sub + nsub - 1) / nsub);
+    if (moe_arrive(&S.arrive[sub * MOE_SYNC_LINE]) == per - 1 && moe_arrive(&S.top[0]) == (unsigned)nsub - 1)
+      __hip_atomic_store(&S.h_ready[lane * MOE_SYNC_LINE], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    moe_wait_ge(&S.h_ready[(w % MOE_SYNC_REP) * MOE_SYNC_LINE], 1u, sy);  // acquires for the CU
+  }
+  __syncthreads();
+
+  // phase 3: down, and the combine of each row group by the wave that finishes its last slot
+  for (int i = gw; i < nslots * gd; i += NW) {
+    const int s = i / gd, g = i % gd;
+    const int64_t eoff = (int64_t)pl.slot_expert[s] * a.d_stride;
+    const CsRows W{a.down + eoff, nullptr, a.d_row_bytes, a.embd};
+    const CsIO io{a.h, pl.slot_pair[s], a.ff, a.yd, pl.slot_pair[s], a.embd, pl.slot_ntok[s]};
+    if (i == gw) asm volatile("" ::"v"(touch));  // the prefetch has landed (long ago)
+    cs_group_wave<CD, TM, RD, 1, true>(W, io, a.ff, g, s_part[wv]);
+    if (moe_arrive(&sy->d_done[g]) == (unsigned)nslots - 1) {
+      // the other slots' rows come from other workgroups: agent-scope loads, which see them at
+      // the point of coherence, rather than a cache invalidation under everyone's weight reads
+      for (int q = lane; q < RD * a.T; q += 64) {
+        const int t = q / RD, r = g * RD + q % RD;
+        if (r < a.embd) {
+          float o = 0.f;
+          for (int j = 0; j < a.k; j++)
+            o += pl.comb_w[t][j] * __hip_atomic_load(&a.yd[(int64_t)pl.comb_pair[t][j] * a.embd + r], __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+          a.out[(int64_t)t * a.embd + r] = o;
+        }
+      }
+      if (lane == 0) sy->d_done[g] = 0;
+    }
+  }
+}
+
+__global__ void moe_sync_init_kernel(unsigned *p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
+}
+
+hipError_t moe_sync_init(MoeSync *s, hipStream_t st) {
+  hipLaunchKernelGGL(moe_sync_init_kernel, dim3(1), dim3(256), 0, st, reinterpret_cast<unsigned *>(s),
+                     (int)(sizeof(MoeSync) / sizeof(unsigned)));
+  return hipGetLastError();
+}
+
+// The grid: one workgroup per CU (the barrier needs every workgroup resident in the end; the
+// kernel is checked once to fit at least one per CU).
+template <class CG, class CD, int TM>
+static hipError_t moe_fused_go(const MoeFusedArgs &a, int num_cu, hipStream_t st) {
+  static int fits = -1;  // per instantiation
+  if (fits < 0) {
+    int n = 0;
+    fits = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, moe_fused_kernel<CG, CD, TM>, 64 * kMoeWaves, 0) ==
+               hipSuccess && n >= 1;
+  }
+  if (!fits) return hipErrorInvalidConfiguration;
+  const int g = num_cu;
+  hipLaunchKernelGGL((moe_fused_kernel<CG, CD, TM>), dim3((unsigned)g), dim3(64 * kMoeWaves), 0, st, a);
+  return hipGetLastError();
+}
+
+template <class CG, class CD>
+static hipError_t moe_fused_tm(const MoeFusedArgs &a, int num_cu, hipStream_t st) {
+  if (a.T <= 1) return moe_fused_go<CG, CD, 1>(a, num_cu, st);
+  if (a.T <= 2) return moe_fused_go<CG, CD, 2>(a, num_cu, st);
+  if (a.T <= 4) return moe_fused_go<CG, CD, 4>(a, num_cu, st);
+  return moe_fused_go<CG, CD, 8>(a, num_cu, st);
+}
+
+// Formats and shapes of the one-launch path: gate/up and down in one wave-column each (embd and
+// ff up to 2048, whole 256-blocks), Q4_K/Q6_K experts, up to 64 (token, choice) pairs and 256
+// experts, float products (IntDot keeps the chain).
+static bool moe_fused_applies(const MoeLaunch &m) {
+  int pg, wg, pd, wd;
+  cs_shape(m.embd, &pg, &wg);
+  cs_shape(m.ff, &pd, &wd);
+  const bool types = (m.gu_type == 12 || m.gu_type == 14) && (m.d_type == 12 || m.d_type == 14) &&
+                     !(m.gu_type == 14 && m.d_type == 12);
+  return m.sync && !m.gu_int && !m.d_int && types && pg == 1 && wg == 1 && pd == 1 && wd == 1 &&
+         m.T * m.k <= 64 && m.T <= kMoeWaves && m.ne <= kRouteMaxN && m.embd / 2 <= MOE_SYNC_MAX_G;
+}
+
+static hipError_t moe_fused_launch(const MoeLaunch &m, int num_cu, hipStream_t st) {
+  MoeFusedArgs a{};
+  a.logits = m.logits; a.T = m.T; a.ne = m.ne; a.k = m.k; a.renorm = m.renorm;
+  a.plan = m.plan;
+  a.gate = m.gate; a.up = m.up; a.down = m.down;
+  a.gu_row_bytes = m.gu_row_bytes; a.d_row_bytes = m.d_row_bytes;
+  a.gu_stride = (int64_t)m.ff * m.gu_row_bytes; a.d_stride = (int64_t)m.embd * m.d_row_bytes;
+  a.ff = m.ff; a.embd = m.embd;
+  a.x = m.x; a.h = m.h; a.yd = m.yd; a.out = m.out;
+  a.sync = m.sync; a.parity = m.parity & 1;
+  a.max_slots = m.T * m.k < m.ne ? m.T * m.k : m.ne;
+  if (m.gu_type == 12 && m.d_type == 12) return moe_fused_tm<Q4K, Q4K>(a, num_cu, st);
+  if (m.gu_type == 12) return moe_fused_tm<Q4K, Q6K>(a, num_cu, st);
+  return moe_fused_tm<Q6K, Q6K>(a, num_cu, st);
 }
 
 // The codecs of this unit and the lookup over every unit.
@@ -378,6 +773,7 @@ static hipError_t route_plan_launch(const MoeLaunch &m, hipStream_t st) {
 }
 
 hipError_t moe_launch(const MoeLaunch &m, int num_cu, hipStream_t st) {
+  if (moe_fused_applies(m)) return moe_fused_launch(m, num_cu, st);
   hipError_t err = route_plan_launch(m, st);
   if (err != hipSuccess) return err;
   const int max_slots = m.T * m.k < m.ne ? m.T * m.k : m.ne;
