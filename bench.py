@@ -369,8 +369,10 @@ def run_workloads(ctx, L, stream, layers, host70, only):
         ms_copy = time_events(cur, lambda i: b.copy_(a), 10, warm=2)
         out["copy_peak"] = {"read_gbs": max(reads.values()), "read_gbs_by_workgroups": reads,
                             "torch_copy_gbs": round(8 * n / (ms_copy * 1e-3) / 1e9, 1),
-                            "method": "wl_read_peak_dev: 16-byte loads only over 4 GiB, 256-thread workgroups, "
-                                      "HIP events over 10 launches per grid size; torch copy_ counts read + write"}
+                            "method": "wl_read_peak_dev: nontemporal 16-byte loads only over 4 GiB, each 256-thread "
+                                      "workgroup over one contiguous chunk with eight loads in flight per thread, best "
+                                      "of five grid sizes, HIP events over 10 launches each; torch copy_ counts read + "
+                                      "write"}
         del a, b, sink
         torch.cuda.empty_cache()
 

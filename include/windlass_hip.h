@@ -320,7 +320,8 @@ int wl_matmul_dev_noalloc(wl_ctx *ctx, const wl_weight *w, int32_t expert, const
 
 /* ---- Calibration (no counterpart in the reference) ----
  * A plain streaming read of `bytes` (a multiple of 16) of device memory at d_src by `workgroups`
- * workgroups of 256 threads (0: eight per CU), stream-ordered on the context. It only loads; the
+ * workgroups of 256 threads (0: eight per CU), each over one contiguous chunk with nontemporal
+ * 16-byte loads, stream-ordered on the context. It only loads; the
  * rate it reaches is the HBM read ceiling the decode GEMVs' roofline fractions are set against.
  * d_out (one uint32, device) is written only in a case real data does not produce. */
 int wl_read_peak_dev(wl_ctx *ctx, const void *d_src, int64_t bytes, int32_t workgroups, uint32_t *d_out);
