@@ -95,7 +95,7 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
 struct TQ4K {
   static constexpr int BYTES = 144, NPREP = 3;
   struct Raw { uint4 hdr, q[2]; };
-  struct Dec { float d1, m1; uint32_t v[4]; };
+  struct Dec { float d1, nm1; uint32_t v[4]; };
   template <int PH>
   __device__ static void load(const uint8_t *blk, int h, Raw &r) {
     r.hdr = *reinterpret_cast<const uint4 *>(blk);  // blocks are 16-byte aligned
@@ -117,7 +117,7 @@ struct TQ4K {
         mv = (B(S + 4) >> 4) | ((B(S) >> 6) << 4);
       }
       o.d1 = d * (float)scv;
-      o.m1 = dmin * (float)mv;
+      o.nm1 = -(dmin * (float)mv);
     } else {
       const uint4 q = r.q[(S / 2) & 1];
       const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
@@ -125,9 +125,13 @@ struct TQ4K {
       for (int i = 2 * (PART - 1); i < 2 * PART; i++) o.v[i] = opaque((qq[i] >> (4 * (S & 1))) & 0x0F0F0F0Fu);
     }
   }
+  // d1 * q - m1 (src/Quants.cs:345-346) as one fma with the same bits: d1 = d * sc and m1 =
+  // dmin * m are products of an fp16 and a 6-bit integer (at most 17 significant bits, exact in
+  // fp32), so d1 * q (q < 16) is exact too and the reference's one rounding is the subtraction's,
+  // the fma's. Non-finite scales give the same infinities and NaNs.
   template <int I>
   __device__ static float value(const Dec &o) {
-    return o.d1 * (float)((o.v[I / 4] >> (8 * (I % 4))) & 0xFF) - o.m1;  // src/Quants.cs:345-346
+    return __builtin_fmaf(o.d1, (float)((o.v[I / 4] >> (8 * (I % 4))) & 0xFF), o.nm1);
   }
 };
 
