@@ -310,7 +310,8 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
 // across nothing (one wave), so each result has cs_gemv's bits for a one-wave workgroup.
 // cs_group_load issues the group's weight loads (they may be in flight across other work);
 // cs_group_finish takes them from there. `part` is the wave's own LDS scratch of NM * R * TM
-// floats. WT: agent-scope stores (read by another workgroup in the same launch).
+// floats. WT: agent-scope stores (read by another workgroup in the same launch). Results go to
+// io.y[yrow * ldy + row - row0] (row0: where io.y's rows start, e.g. an LDS tile of the group).
 template <class C, int R, int NM>
 __device__ __forceinline__ void cs_group_load(const CsRows &W, int cols, int g, typename C::Raw (&raw)[NM][R]) {
   const int lane = threadIdx.x & 63;
@@ -320,7 +321,7 @@ __device__ __forceinline__ void cs_group_load(const CsRows &W, int cols, int g, 
 
 template <class C, int TM, int R, int NM, bool WT>
 __device__ __forceinline__ void cs_group_finish(const CsRows &W, const CsIO &io, int cols, int g, float *part,
-                                                const typename C::Raw (&raw)[NM][R]) {
+                                                const typename C::Raw (&raw)[NM][R], int row0 = 0) {
   constexpr int V = NM * R * TM;
   constexpr int LOW = 6 - ilog2(V);
   static_assert(!C::NEED_LDS, "codecs with LDS tables run through cs_gemv");
@@ -372,7 +373,7 @@ __device__ __forceinline__ void cs_group_finish(const CsRows &W, const CsIO &io,
     if (t < io.T && row < W.rows) {
       float v = part[t * R + r];
       if constexpr (NM == 2) v = silu_mul(v, part[(TM + t) * R + r]);
-      put<WT>(&io.y[(int64_t)(io.yrow ? io.yrow[t] : t) * io.ldy + row], v);
+      put<WT>(&io.y[(int64_t)(io.yrow ? io.yrow[t] : t) * io.ldy + row - row0], v);
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -380,10 +381,11 @@ __device__ __forceinline__ void cs_group_finish(const CsRows &W, const CsIO &io,
 }
 
 template <class C, int TM, int R, int NM, bool WT>
-__device__ __forceinline__ void cs_group_wave(const CsRows &W, const CsIO &io, int cols, int g, float *part) {
+__device__ __forceinline__ void cs_group_wave(const CsRows &W, const CsIO &io, int cols, int g, float *part,
+                                              int row0 = 0) {
   typename C::Raw raw[NM][R];
   cs_group_load<C, R, NM>(W, cols, g, raw);
-  cs_group_finish<C, TM, R, NM, WT>(W, io, cols, g, part, raw);
+  cs_group_finish<C, TM, R, NM, WT>(W, io, cols, g, part, raw, row0);
 }
 
 }  // namespace wl

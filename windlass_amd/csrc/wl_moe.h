@@ -32,7 +32,6 @@ struct MoePlan {
 constexpr int MOE_SYNC_REP = 64;      // replicas of the polled flag
 constexpr int MOE_SYNC_SUB = 16;      // arrival counters
 constexpr int MOE_SYNC_LINE = 32;     // words per 128-byte line
-constexpr int MOE_SYNC_MAX_G = 8192;  // row groups of the down projection
 struct MoeSyncSet {
   unsigned arrive[MOE_SYNC_SUB * MOE_SYNC_LINE];
   unsigned top[MOE_SYNC_LINE];
@@ -40,7 +39,6 @@ struct MoeSyncSet {
 };
 struct MoeSync {
   MoeSyncSet set[2];
-  unsigned d_done[MOE_SYNC_MAX_G];  // per down row group; the combining wave clears its own
   unsigned err[MOE_SYNC_LINE];
 };
 

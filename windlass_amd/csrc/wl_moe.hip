@@ -321,16 +321,14 @@ __global__ void combine_kernel(const MoePlan *__restrict__ plan, const float *__
 //            (gw the wave's index in the grid; slot i / groups, group i % groups) and write h;
 //            then a grid barrier (16 arrival counters, a count of the complete ones, a flag
 //            on 64 replicas);
-//   phase 3  the down row groups the same way, writing yd; the wave that finishes a row group's
-//            last slot (a per-group count) adds the tokens' pairs for its rows in ascending
-//            expert order, as combine_kernel does, and clears the count.
+//   phase 3  workgroup w takes the down row groups w, w + G, ...; its waves take the slots of a
+//            group in turn, the slots' rows meet in LDS, and the workgroup adds the tokens'
+//            pairs for each row in ascending expert order, as combine_kernel does.
 // Each row group is computed by cs_group_wave, whose results are cs_gemv's for a one-wave
-// workgroup, as the launch chain runs these shapes: the same bits. Stores another workgroup
-// reads are agent-scope (written through to the point of coherence). Readers of h acquire once
-// per CU after the barrier (the polling wave's acquire; the others follow it through the
-// workgroup barrier); the combine reads yd with agent-scope loads, since a cache
-// invalidation per row group would throw away the lines every other wave's weight reads share.
-// Every wait is bounded (kMoeSpin polls); one that runs out sets `err`.
+// workgroup, as the launch chain runs these shapes: the same bits. h crosses workgroups: it is
+// stored at agent scope (written through to the point of coherence), and its readers acquire
+// once per CU after the barrier (the polling wave's acquire; the others follow it through the
+// workgroup barrier). Every wait is bounded (kMoeSpin polls); one that runs out sets `err`.
 struct MoeFusedArgs {
   const float *logits;
   int T, ne, k, renorm;
@@ -540,6 +538,7 @@ __global__ __launch_bounds__(64 * kMoeWaves) void moe_fused_kernel(MoeFusedArgs 
   __shared__ float s_wts[MOE_MAX_PAIRS];
   __shared__ MoePlan s_plan;
   __shared__ float s_part[kMoeWaves][64];
+  __shared__ float s_yd[MOE_MAX_PAIRS * 8];  // a down row group's rows (up to 8) of every pair
   constexpr int RG = TM == 1 ? CG::R1 / 2 : 2, RD = TM == 1 ? CD::R1 : 4;
   MoeSync *sy = a.sync;
   MoeSyncSet &S = sy->set[a.parity];
@@ -573,16 +572,16 @@ __global__ __launch_bounds__(64 * kMoeWaves) void moe_fused_kernel(MoeFusedArgs 
     const CsIO io{a.x, pl.slot_tok[s], a.embd, a.h, pl.slot_pair[s], a.ff, pl.slot_ntok[s]};
     cs_group_wave<CG, TM, RG, 2, true>(W, io, a.embd, g, s_part[wv]);
   }
-  // this wave's first down row group: one dword of each of its weights' 128-byte lines, read
-  // across the barrier so the lines are in the caches when phase 3 reads them
+  // this wave's first down row group (group w, slot wv): one dword of each of its weights'
+  // 128-byte lines, read across the barrier so the lines are in the caches when phase 3 reads them
   const int gd = (a.embd + RD - 1) / RD;
   uint32_t touch = 0;
   {
     const int lpr = (int)((a.d_row_bytes + 127) / 128);  // lines per row
-    if (gw < nslots * gd && lane < RD * lpr) {
-      const int r = min((gw % gd) * RD + lane / lpr, a.embd - 1);
+    if (w < gd && wv < nslots && lane < RD * lpr) {
+      const int r = min(w * RD + lane / lpr, a.embd - 1);
       const int64_t off = min((int64_t)(lane % lpr) * 128, a.d_row_bytes - 4);
-      const uint8_t *row = a.down + (int64_t)pl.slot_expert[gw / gd] * a.d_stride + (int64_t)r * a.d_row_bytes;
+      const uint8_t *row = a.down + (int64_t)pl.slot_expert[wv] * a.d_stride + (int64_t)r * a.d_row_bytes;
       touch = *reinterpret_cast<const uint32_t *>(row + (off & ~(int64_t)3));
     }
   }
@@ -596,29 +595,27 @@ __global__ __launch_bounds__(64 * kMoeWaves) void moe_fused_kernel(MoeFusedArgs 
   }
   __syncthreads();
 
-  // phase 3: down, and the combine of each row group by the wave that finishes its last slot
-  for (int i = gw; i < nslots * gd; i += NW) {
-    const int s = i / gd, g = i % gd;
-    const int64_t eoff = (int64_t)pl.slot_expert[s] * a.d_stride;
-    const CsRows W{a.down + eoff, nullptr, a.d_row_bytes, a.embd};
-    const CsIO io{a.h, pl.slot_pair[s], a.ff, a.yd, pl.slot_pair[s], a.embd, pl.slot_ntok[s]};
-    if (i == gw) asm volatile("" ::"v"(touch));  // the prefetch has landed (long ago)
-    cs_group_wave<CD, TM, RD, 1, true>(W, io, a.ff, g, s_part[wv]);
-    if (moe_arrive(&sy->d_done[g]) == (unsigned)nslots - 1) {
-      // the other slots' rows come from other workgroups: agent-scope loads, which see them at
-      // the point of coherence, rather than a cache invalidation under everyone's weight reads
-      for (int q = lane; q < RD * a.T; q += 64) {
-        const int t = q / RD, r = g * RD + q % RD;
-        if (r < a.embd) {
-          float o = 0.f;
-          for (int j = 0; j < a.k; j++)
-            o += pl.comb_w[t][j] * __hip_atomic_load(&a.yd[(int64_t)pl.comb_pair[t][j] * a.embd + r], __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-          a.out[(int64_t)t * a.embd + r] = o;
-        }
-      }
-      if (lane == 0) sy->d_done[g] = 0;
+  // phase 3: row groups g = w, w + G, ... of the down rows; wave v takes the slots v, v + 8, ...,
+  // the slots' rows of the group meet in LDS, and the workgroup adds the tokens' pairs for each
+  // row in ascending expert order, as combine_kernel does
+  for (int g = w; g < gd; g += G) {
+    for (int s = wv; s < nslots; s += kMoeWaves) {
+      if (g == w && s == wv) asm volatile("" ::"v"(touch));  // the prefetch has landed (long ago)
+      const int64_t eoff = (int64_t)pl.slot_expert[s] * a.d_stride;
+      const CsRows W{a.down + eoff, nullptr, a.d_row_bytes, a.embd};
+      const CsIO io{a.h, pl.slot_pair[s], a.ff, s_yd, pl.slot_pair[s], RD, pl.slot_ntok[s]};
+      cs_group_wave<CD, TM, RD, 1, false>(W, io, a.ff, g, s_part[wv], g * RD);
     }
+    __syncthreads();
+    for (int q = tid; q < RD * a.T; q += 64 * kMoeWaves) {
+      const int t = q / RD, r = q % RD;
+      if (g * RD + r < a.embd) {
+        float o = 0.f;
+        for (int j = 0; j < a.k; j++) o += pl.comb_w[t][j] * s_yd[pl.comb_pair[t][j] * RD + r];
+        a.out[(int64_t)t * a.embd + g * RD + r] = o;
+      }
+    }
+    __syncthreads();  // s_yd is the next group's
   }
 }
 
@@ -666,7 +663,7 @@ static bool moe_fused_applies(const MoeLaunch &m) {
   const bool types = (m.gu_type == 12 || m.gu_type == 14) && (m.d_type == 12 || m.d_type == 14) &&
                      !(m.gu_type == 14 && m.d_type == 12);
   return m.sync && !m.gu_int && !m.d_int && types && pg == 1 && wg == 1 && pd == 1 && wd == 1 &&
-         m.T * m.k <= 64 && m.T <= kMoeWaves && m.ne <= kRouteMaxN && m.embd / 2 <= MOE_SYNC_MAX_G;
+         m.T * m.k <= 64 && m.T <= kMoeWaves && m.ne <= kRouteMaxN;
 }
 
 static hipError_t moe_fused_launch(const MoeLaunch &m, int num_cu, hipStream_t st) {
