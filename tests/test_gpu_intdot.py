@@ -127,12 +127,14 @@ def test_int_matmul_matches_oracle_bitwise(ctx, t, shape, T):
 
 
 @pytest.mark.parametrize("t", [GgmlType.Q4_K, GgmlType.Q6_K], ids=lambda t: t.name)
-@pytest.mark.parametrize("shape", [(37, 256), (200, 8192), (16, 28672)], ids=lambda s: "%dx%d" % s)
-@pytest.mark.parametrize("T", [2, 8, 20])
+@pytest.mark.parametrize("shape", [(37, 256), (48, 1280), (40, 2816), (200, 8192), (16, 28672)],
+                         ids=lambda s: "%dx%d" % s)
+@pytest.mark.parametrize("T", [2, 5, 8, 20])
 def test_int_matmul_matrix_cores_match_oracle_bitwise(ctx, t, shape, T):
-    # 2..8 tokens of Q4_K / Q6_K run on the int8 matrix cores (20: passes of 8, 8 and 4), each
-    # row's blocks split over four waves; every (row, token) is still FastMath.IntDot's bits, and
-    # a token's bits do not depend on the pass
+    # 2..8 tokens of Q4_K / Q6_K run on the int8 matrix cores (20: passes of 8, 8 and 4), a row's
+    # blocks taken by the workgroup's waves in rounds (5 and 11 blocks: a last round that only
+    # some waves have); every (row, token) is still FastMath.IntDot's bits, and a token's bits do
+    # not depend on the pass
     rows, cols = shape
     data = blocks(t, rows, cols, seed=rows * 3 + cols + int(t))
     x = np.random.default_rng(T * 7 + cols).standard_normal((T, cols), dtype=np.float32)

@@ -520,7 +520,7 @@ static wl::QActsDev int_tokens(const wl::QActsDev &qa, int t0, int cols, int k) 
   // the matrix-core operand copy holds every token from 0 (it exists for one pass of at most 8)
   return wl::QActsDev{qa.q + (int64_t)t0 * cols, qa.d + (int64_t)t0 * (cols / ab),
                       qa.bsums ? qa.bsums + (int64_t)t0 * (cols / 16) : nullptr, t0 ? nullptr : qa.qf,
-                      t0 ? nullptr : qa.bf, t0 ? nullptr : qa.df};
+                      t0 ? nullptr : qa.df};
 }
 
 // Activations quantized for the integer kernels, made at most once per call and kind.

@@ -20,10 +20,9 @@ struct QActsDev {
   float *d;
   int16_t *bsums;
   // Q8_K of at most 8 tokens, also in the matrix-core kernel's operand order (16 token slots,
-  // slots past T zero): per 256-block b, qf[b][run s][slot t][32 quants], bf[b][t][16 bsums],
-  // df[b][t]; so one wave load of a run's B operand reads 512 contiguous bytes. Null otherwise.
+  // slots past T zero): per 256-block b, qf[b][run s][slot t][32 quants] and df[b][t]; so one
+  // wave load of a run's B operand reads 512 contiguous bytes. Null otherwise.
   int8_t *qf;
-  int16_t *bf;
   float *df;
 };
 int64_t qacts_bytes(int T, int cols, int k);

@@ -30,9 +30,9 @@ bool intdot_fits(int t, int cols) { return cols > 0 && cols % (intdot_needs_k(t)
 
 static int64_t up16(int64_t n) { return (n + 15) / 16 * 16; }
 
-// The matrix-core operand copy (QActsDev::qf/bf/df) of Q8_K activations of 2..8 tokens.
+// The matrix-core operand copy (QActsDev::qf/df) of Q8_K activations of 2..8 tokens.
 static bool qacts_mma(int T, int k) { return k && T >= 2 && T <= 8; }
-static int64_t mma_bytes(int cols) { return (int64_t)(cols / 256) * (8 * 16 * 32 + 16 * 16 * 2 + 16 * 4); }
+static int64_t mma_bytes(int cols) { return (int64_t)(cols / 256) * (8 * 16 * 32 + 16 * 4); }
 
 int64_t qacts_bytes(int T, int cols, int k) {
   const int bs = k ? 256 : 32;
@@ -53,8 +53,7 @@ QActsDev qacts_at(void *buf, int T, int cols, int k) {
   if (qacts_mma(T, k)) {
     const int64_t nb = cols / 256;
     a.qf = reinterpret_cast<int8_t *>(p);
-    a.bf = reinterpret_cast<int16_t *>(p + nb * 8 * 16 * 32);
-    a.df = reinterpret_cast<float *>(p + nb * (8 * 16 * 32 + 16 * 16 * 2));
+    a.df = reinterpret_cast<float *>(p + nb * 8 * 16 * 32);
   }
   return a;
 }
@@ -70,7 +69,7 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 __global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__ x, int T, int cols, int k,
                                                        int8_t *__restrict__ q, float *__restrict__ d,
                                                        int16_t *__restrict__ bsums, int8_t *__restrict__ qf,
-                                                       int16_t *__restrict__ bf, float *__restrict__ df) {
+                                                       float *__restrict__ df) {
   const int lane = threadIdx.x & 63;
   const int nchunk = (cols + 255) / 256;
   const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -79,7 +78,6 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__
   const int base = 256 * c + 4 * lane;  // cols is a multiple of 32, so a lane's 4 values are all in or all out
   if (t >= T) {  // a zero slot of the operand copy
     reinterpret_cast<uint32_t *>(qf)[((c * 8 + lane / 8) * 16 + t) * 8 + lane % 8] = 0u;
-    if ((lane & 3) == 0) bf[(c * 16 + t) * 16 + lane / 4] = 0;
     if (lane == 0) df[c * 16 + t] = 0.f;
     return;
   }
@@ -156,7 +154,6 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__
   if (lane == 0) d[(int64_t)t * (cols / 256) + c] = dv;
   if (qf) {  // the same values in the matrix-core operand order
     reinterpret_cast<uint32_t *>(qf)[((c * 8 + lane / 8) * 16 + t) * 8 + lane % 8] = packed;
-    if ((lane & 3) == 0) bf[(c * 16 + t) * 16 + lane / 4] = (int16_t)s;
     if (lane == 0) df[c * 16 + t] = dv;
   }
 }
@@ -167,7 +164,7 @@ hipError_t quantize_launch(const float *x, int T, int cols, int k, QActsDev a, h
   const bool mma = a.qf && qacts_mma(T, k);
   const int64_t waves = (int64_t)(mma ? 16 : T) * ((cols + 255) / 256);
   hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, T, cols, k, a.q, a.d,
-                     a.bsums, mma ? a.qf : nullptr, a.bf, a.df);
+                     a.bsums, mma ? a.qf : nullptr, a.df);
   return hipGetLastError();
 }
 

@@ -3,19 +3,29 @@
 // Transformer.MatMul's integer branch (src/Transformer.cs:504-524) for several tokens at once,
 // as ForwardBatch runs it (one FastMath.IntDot per (row, token), src/FastMath.cs:105-214). The
 // integer sums of FastMath.IntDot are exact, so they may come from any order of products: here
-// v_mfma_i32_16x16x32_i8 forms them for 16 rows x 16 tokens x one 32-value run at a time, with
-// the weight quants as the A operand and the tokens' 8-bit activations as B. Each row's
-// scale terms and the float term of every block are the reference's, and the terms of a row's
-// blocks are added in block order, as the reference's `sum +=` does: every (row, token) result is
+// v_mfma_i32_16x16x32_i8 forms them for 16 rows x 16 columns x one 32-value run at a time, with
+// the weight quants as the A operand and the tokens' 8-bit activations as B. Each row's scale
+// terms and the float term of every block are the reference's, and the terms of a row's blocks
+// are added in block order, as the reference's `sum +=` does: every (row, token) result is
 // bit-identical to FastMath.IntDot, whatever the token count, and to the one-token integer kernel
 // (wl_intdot.hip).
 //
 // Operand layout of v_mfma_i32_16x16x32_i8: lane l holds A[row l%16][k 8*(l/16) .. +7] and
-// B[k 8*(l/16) .. +7][token l%16]; the result holds D[row 4*(l/16) + i][token l%16], i < 4. So a
-// lane loads the weight bytes of row l%16 (the "A row") and the activations of token l%16, and
-// its results are rows 4*(l/16) .. +3 of that token (its "D rows"). Each block's per-row scales
-// reach the D rows through a small LDS slab per wave: every A lane decodes two sub-blocks'
-// (scale, min) of its row, and every D lane reads the rows it owns.
+// B[k 8*(l/16) .. +7][column l%16]; the result holds D[row 4*(l/16) + i][column l%16], i < 4. So
+// a lane loads the weight bytes of row l%16 (its "A row") and one column's activations, and its
+// results are rows 4*(l/16) .. +3 of that column (its "D rows"). Each block's per-row scales reach
+// the D rows through a small LDS slab per wave: the A lanes decode their row's scales into it,
+// and the D lanes read the rows they own.
+//
+// Sums the matrix cores take over from the VALU (all exact in int32):
+//   Q4_K  summ = sum_s m_s * (bsums of sub-block s) = sum_k m_s(k) * x_k: one more product per run
+//         with every A byte the run's min, accumulated over the block's eight runs;
+//   Q6_K  acc_g = sum (q - 32) x = sum q x + sum (-32) x: a second product per run with every A
+//         byte -32, accumulated onto the first.
+// Q6_K's scale groups are 16 values, two per run: columns 0..7 carry tokens 0..7 with the run's
+// first group (the other group's B bytes read a zero slot) and columns 8..15 the same tokens with
+// the second group, so one product serves both groups and a lane adds its partner column's
+// scaled sums (integers, any order) to complete a half's `part`.
 #include "wl_device.h"
 #include "wl_gemv_impl.h"
 #include "wl_intdot.h"
@@ -26,9 +36,8 @@ namespace wl {
 
 typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kMmaWaves = 4;     // waves per workgroup: one 16-row tile, its blocks in four parts
-constexpr int kMmaTokens = 8;    // tokens per launch (of the MFMA's 16 columns)
-constexpr int kSlab = 20;        // dwords per row in the scale slab
+constexpr int kMmaTokens = 8;  // tokens per launch (of the MFMA's 16 columns)
+constexpr int kSlab = 20;      // dwords per row in the scale slab
 
 __device__ __forceinline__ i32x4_t mma(uint2 a, uint2 b, i32x4_t c) {
   return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)__builtin_bit_cast(uint64_t, a),
@@ -39,11 +48,10 @@ __device__ __forceinline__ uint2 ld8(const void *p) { return *reinterpret_cast<c
 
 // ------------------------------------------------------------------------------------ Q4_K
 // A lane (q4 = l/16, row l%16) of block b: qs bytes 32j + 8 q4 .. +8 (j < 4) of its row are the
-// A operands of sub-blocks 2j (low nibbles) and 2j + 1 (high nibbles). Its slab entries are the
-// (scale, min) of sub-blocks 2 q4 and 2 q4 + 1 (get_scale_min_k4, src/Quants.cs:321-330) and
-// the row's (d, dmin).
+// A operands of sub-blocks 2j (low nibbles) and 2j + 1 (high nibbles); the header gives the
+// sub-blocks' 6-bit scales and mins (get_scale_min_k4, src/Quants.cs:321-330).
 struct MQ4K {
-  static constexpr int BYTES = 144, SUBS = 8, TERMS = 1;
+  static constexpr int BYTES = 144, TERMS = 1;
   struct Raw { uint4 h; uint2 q[4]; };
   __device__ static void load(const uint8_t *blk, int q4, Raw &r) {
     r.h = *reinterpret_cast<const uint4 *>(blk);
@@ -56,35 +64,36 @@ struct MQ4K {
 #pragma unroll
     for (int j = 0; j < 4; j++) r.q[j] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 8 * q4);
   }
+  // the B slot of lane (q4, c16): its column's token (slots 8..15 are zero, their results unused)
+  __device__ static int slot(int, int c16) { return c16; }
   __device__ static uint2 operand(const Raw &r, int s) {
     const uint2 v = r.q[s >> 1];
     const int sh = 4 * (s & 1);
     return make_uint2((v.x >> sh) & 0x0F0F0F0Fu, (v.y >> sh) & 0x0F0F0F0Fu);
   }
-  // slab row: dwords 0..7 scales, 8..15 mins, 16 the (d, dmin) halves
+  // the eight mins as bytes: sub-blocks 0..3 are the low 6 bits of header bytes 8..11, 4..7 the
+  // high nibbles of bytes 12..15 with the top two bits of bytes 8..11
+  __device__ static void mins(const Raw &r, uint32_t &m03, uint32_t &m47) {
+    m03 = r.h.z & 0x3F3F3F3Fu;
+    m47 = ((r.h.w >> 4) & 0x0F0F0F0Fu) | ((r.h.z >> 2) & 0x30303030u);
+  }
+  // slab row: dwords 0..7 the scales of sub-blocks 0..7, 8 the (d, dmin) halves; lane q4 writes
+  // sub-blocks 2 q4 and 2 q4 + 1 (scales 0..3: the low 6 bits of header bytes 4..7; 4..7: the
+  // low nibbles of bytes 12..15 with the top two bits of bytes 4..7)
   __device__ static void stage(const Raw &r, int q4, uint32_t *row) {
-    uint32_t sc[2], mn[2];
-#pragma unroll
-    for (int e = 0; e < 2; e++) {
-      const int s = 2 * q4 + e, k = 8 * (s & 3);
-      const uint32_t Y = (r.h.y >> k) & 0xFF, Z = (r.h.z >> k) & 0xFF, W = (r.h.w >> k) & 0xFF;
-      sc[e] = s < 4 ? (Y & 63) : ((W & 0xF) | ((Y >> 6) << 4));
-      mn[e] = s < 4 ? (Z & 63) : ((W >> 4) | ((Z >> 6) << 4));
-    }
-    *reinterpret_cast<uint2 *>(row + 2 * q4) = make_uint2(sc[0], sc[1]);
-    *reinterpret_cast<uint2 *>(row + 8 + 2 * q4) = make_uint2(mn[0], mn[1]);
-    if (q4 == 0) row[16] = r.h.x;
+    const uint32_t sb = q4 < 2 ? (r.h.y & 0x3F3F3F3Fu) : ((r.h.w & 0x0F0F0F0Fu) | ((r.h.y >> 2) & 0x30303030u));
+    const int k = 16 * (q4 & 1);
+    *reinterpret_cast<uint2 *>(row + 2 * q4) = make_uint2((sb >> k) & 0xFF, (sb >> (k + 8)) & 0xFF);
+    if (q4 == 0) row[8] = r.h.x;
   }
 };
 
 // ------------------------------------------------------------------------------------ Q6_K
 // A lane (q4, row) of block b, half hh, 32-value run s' (values 128 hh + 32 s' + 8 q4 .. +8):
 // quants ((ql >> 4 (s' >> 1)) & 15) | (((qh >> 2 s') & 3) << 4) from ql bytes
-// 64 hh + 32 (s' & 1) + 8 q4 and qh bytes 128 + 32 hh + 8 q4 (src/Quants.cs:381-392). A run holds
-// two scale groups of 16 values (lanes q4 < 2 and q4 >= 2), so each run is two products whose B
-// operand keeps one group's activations. Slab: the 16 int8 scales as ints, and d.
+// 64 hh + 32 (s' & 1) + 8 q4 and qh bytes 128 + 32 hh + 8 q4 (src/Quants.cs:381-392).
 struct MQ6K {
-  static constexpr int BYTES = 210, SUBS = 16, TERMS = 2;
+  static constexpr int BYTES = 210, TERMS = 2;
   struct Raw { uint32_t l[2][2][3], h[2][3], s, d, sh; };  // aligned dword windows (2-byte-aligned blocks)
   __device__ static void load(const uint8_t *blk, int q4, Raw &r) {
     gu32 *a = align4_down(blk);
@@ -108,6 +117,10 @@ struct MQ6K {
     // one extra dword for the scale window when the block is at 2 mod 4
     r.s = __builtin_amdgcn_alignbit(a[(192 + 4 * q4) / 4 + 1], r.s, r.sh);
   }
+  // A run's values 0..15 (lanes q4 < 2) are one scale group and 16..31 (q4 >= 2) the next:
+  // column c16 < 8 is token c16 with the first group, c16 >= 8 token c16 - 8 with the second;
+  // a lane whose values belong to the other group reads a zero slot (8..15: at most 8 tokens)
+  __device__ static int slot(int q4, int c16) { return ((q4 >= 2) == (c16 >= 8)) ? (c16 & 7) : (c16 | 8); }
   __device__ static uint2 win(const uint32_t (&w)[3], uint32_t sh) {
     return make_uint2(__builtin_amdgcn_alignbit(w[1], w[0], sh), __builtin_amdgcn_alignbit(w[2], w[1], sh));
   }
@@ -118,12 +131,16 @@ struct MQ6K {
     return make_uint2(((ql.x >> s1) & 0x0F0F0F0Fu) | (((qh.x >> s2) & 0x03030303u) << 4),
                       ((ql.y >> s1) & 0x0F0F0F0Fu) | (((qh.y >> s2) & 0x03030303u) << 4));
   }
-  // slab row: dwords 0..15 the scales (sign-extended), 16 the d half
+  // slab row: group g = 2 sp + s of half hh (scale byte 8 hh + g, sign-extended) at dword
+  // 8 hh + 4 s + sp, so the four scales a D lane of group s needs per half are one 16-byte read;
+  // 16 the d half. Lane q4 holds scale bytes 4 q4 .. +3: half q4 >> 1, g = 4 (q4 & 1) + e.
   __device__ static void stage(const Raw &r, int q4, uint32_t *row) {
     const uint32_t s = r.s;
-    *reinterpret_cast<uint4 *>(row + 4 * q4) =
-        make_uint4((uint32_t)(int)(int8_t)(s & 0xFF), (uint32_t)(int)(int8_t)((s >> 8) & 0xFF),
-                   (uint32_t)(int)(int8_t)((s >> 16) & 0xFF), (uint32_t)(int)(int8_t)(s >> 24));
+    const int o = 8 * (q4 >> 1) + 2 * (q4 & 1);
+    const uint32_t e0 = (uint32_t)(int)(int8_t)(s & 0xFF), e1 = (uint32_t)(int)(int8_t)((s >> 8) & 0xFF),
+                   e2 = (uint32_t)(int)(int8_t)((s >> 16) & 0xFF), e3 = (uint32_t)(int)(int8_t)(s >> 24);
+    *reinterpret_cast<uint2 *>(row + o) = make_uint2(e0, e2);      // s = 0: sp, sp + 1
+    *reinterpret_cast<uint2 *>(row + o + 4) = make_uint2(e1, e3);  // s = 1
     if (q4 == 0) row[16] = r.sh ? (r.d >> 16) : (r.d & 0xFFFF);
   }
 };
@@ -132,364 +149,266 @@ struct MmaArgs {
   const uint8_t *w, *w2;  // w2: the up matrix of the SwiGLU pair (NM = 2)
   int64_t row_bytes;
   int rows, cols;
-  const int8_t *q;  // token t's quants at q + t * cols
-  const float *d;   // token t's block scales at d + t * (cols / 256)
-  const int16_t *bs;
+  // the activations in operand order (QActsDev::qf/df): per 256-block b, qf[b][run][slot][32]
+  // and df[b][slot], slots past T zero; or null, and the tokens' rows q [T][cols], d [T][cols/256]
+  const int8_t *qf;
+  const float *df;
+  const int8_t *q;
+  const float *d;
   int T;
   float *y;
   int ldy;
-  // the same activations in operand order (QActsDev::qf/bf/df), or null
-  const int8_t *qf;
-  const int16_t *bf;
-  const float *df;
 };
 
-// A workgroup owns one 16-row tile (of each matrix); wave w walks the w-th quarter of the row's
-// blocks in order. Wave 0 adds its blocks' terms as it goes; waves 1..3 leave theirs in LDS
-// (the D lanes of the first 8 tokens), and after one barrier wave 0 adds them on in block
-// order: the reference's single `sum +=` chain over the whole row.
-// Staged weights (Q4_K): a wave reads its tile's 16 rows x kStageBlocks blocks with coalesced
-// nontemporal 16-byte loads (every byte once; a wave load covers about two rows' contiguous
-// bytes instead of 16 rows' separate lines), one chunk ahead in registers, into its own LDS
-// area, and the lanes take their operand bytes from there.
-constexpr int kStageBlocks = 2;
-constexpr int kStageRow = kStageBlocks * 144 + 16;                          // LDS bytes per row (padded)
-constexpr int kStageChunks = 16 * kStageBlocks * 144 / 16;                  // 16-byte chunks of a stage
-constexpr int kStageLoads = (kStageChunks + 63) / 64;                       // loads per lane
+// A workgroup owns one 16-row tile (of each matrix). Its W waves take the row's blocks in rounds:
+// in round r wave w takes block r W + w, its loads issued one round ahead. Each block's terms
+// (for the 8 token columns: 16 rows x 8 tokens x TERMS floats per matrix) go to an LDS ring of
+// two rounds; after the round's barrier every wave adds the round's terms, in block order, for
+// its share of the (row, token) pairs: the reference's single `sum +=` chain over the whole row.
+// Staged Q4_K weights: a wave reads its block's 16 rows x 144 bytes (per matrix) with three
+// coalesced nontemporal 16-byte loads per lane, one round ahead, into its own LDS area, and the
+// lanes take their operand bytes from there (a wave load covers about seven rows' contiguous
+// bytes, where an operand load touches sixteen rows' lines).
+constexpr int kStgRow = 176;                       // LDS bytes per staged row (reads of the 16 rows in distinct banks)
+constexpr int kStgChunks = 16 * 144 / 16;          // 16-byte pieces of a 16-row block
+constexpr int kStgLoads = (kStgChunks + 63) / 64;  // loads per lane
 
-// FRAG: the activations come from the operand-order copy (one 512-byte wave load per run of 32
-// values, 16 tokens' bsums and scales in one 512- and one 64-byte range) instead of the tokens'
-// rows (16 tokens' separate lines per wave load). STG: staged weights (Q4_K).
-template <class M, int NM, bool FRAG, bool STG = false>
-__global__ __launch_bounds__(64 * kMmaWaves) void intmma_kernel(MmaArgs a) {
-  __shared__ __attribute__((aligned(16))) uint32_t slab[kMmaWaves][NM][16 * kSlab];
-  __shared__ __attribute__((aligned(16))) uint8_t stage[STG ? kMmaWaves : 1][STG ? NM : 1][STG ? 16 * kStageRow : 16];
-  extern __shared__ __attribute__((aligned(16))) float4 mma_terms[];  // [3][bw][NM][TERMS][32]
+// FRAG: the operand-order copy (one 512-byte wave load per run); otherwise the tokens' rows.
+// STG: staged weights (Q4_K).
+template <class M, int NM, int W, bool FRAG, bool STG>
+__global__ __launch_bounds__(64 * W) void intmma_kernel(MmaArgs a) {
+  constexpr int MH = NM * M::TERMS;
+  static_assert(!STG || M::BYTES == 144, "staging is laid out for Q4_K blocks");
+  __shared__ __attribute__((aligned(16))) uint32_t slab[W][NM][16 * kSlab];
+  __shared__ __attribute__((aligned(16))) float4 terms[2][W][MH][32];
+  __shared__ __attribute__((aligned(16))) uint8_t stg[STG ? W : 1][STG ? NM : 1][STG ? 16 * kStgRow : 16];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, q4 = lane >> 4, c16 = lane & 15;
-  const int tile = blockIdx.x;  // uniform: the barrier below is reached by every wave
-  const int nb = a.cols / 256, bw = (nb + kMmaWaves - 1) / kMmaWaves;
-  const int b_lo = min(nb, wv * bw), b_hi = min(nb, b_lo + bw);
-  const int dl = q4 * 8 + c16;  // D lane index among the first 8 tokens' lanes
+  const int tile = blockIdx.x;  // uniform: the barriers below are reached by every wave
+  const int nb = a.cols / 256, nr = (nb + W - 1) / W;
   const int arow = min(tile * 16 + c16, a.rows - 1);  // rows past the end re-read the last row
-  const int tok = min(c16, a.T - 1);                    // tokens past T re-read the last token
   const uint8_t *wr[2] = {a.w + (int64_t)arow * a.row_bytes, NM == 2 ? a.w2 + (int64_t)arow * a.row_bytes : nullptr};
-  const int8_t *xq = a.q + (int64_t)tok * a.cols + 8 * q4;
-  const float *xd = a.d + (int64_t)tok * nb;
-  const int16_t *xb = a.bs + (int64_t)tok * (a.cols / 16);
+  // FRAG: slot M::slot's quants at xq + (8 b + run) * 512, its scale at xd + 16 b; rows: token
+  // tok's at xq + 256 b + 32 run and xd + b, and a lane of the other Q6_K group takes zeros
+  const int slot = M::slot(q4, c16), tok = min(c16 & 7, a.T - 1);
+  const bool xzero = !FRAG && slot >= 8 && M::TERMS == 2;
+  const int8_t *xq = FRAG ? a.qf + slot * 32 + 8 * q4 : a.q + (int64_t)tok * a.cols + 8 * q4;
+  const float *xd = FRAG ? a.df + (c16 & 7) : a.d + (int64_t)tok * (a.cols / 256);
+  const int dl = q4 * 8 + c16;                                 // D lane among the token columns (c16 < 8)
 
-  float sum[NM][4];
+  // staging: piece f = 64 i + lane of a block's 16 rows is row f / 9, bytes 16 (f % 9) ..
+  int soff[kStgLoads], lofs[kStgLoads];
+  bool sok[kStgLoads];
 #pragma unroll
-  for (int m = 0; m < NM; m++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) sum[m][i] = 0.f;
+  for (int i = 0; i < kStgLoads; i++) {
+    const int f = 64 * i + lane, r = f / 9, c = f % 9;
+    sok[i] = STG && f < kStgChunks;
+    soff[i] = (min(tile * 16 + r, a.rows - 1) - tile * 16) * (int)a.row_bytes + 16 * c;  // tile*16 < rows
+    lofs[i] = r * kStgRow + 16 * c;
+  }
+  const int64_t tbase = (int64_t)tile * 16 * a.row_bytes;
 
-  // a block's operands: the weight bytes of the tile's rows, the token's quants, bsums and scale
-  struct Ops {
-    typename M::Raw raw[NM];
+  struct Xo {
     uint2 xs[8];
-    uint4 b0, b1;
     float dt;
   };
-  auto fetch = [&](int b, Ops &o) {
-#pragma unroll
-    for (int m = 0; m < NM; m++) M::load(wr[m] + (int64_t)b * M::BYTES, q4, o.raw[m]);
+  auto fetch_x = [&](int b, Xo &o) {
     if constexpr (FRAG) {
 #pragma unroll
-      for (int s = 0; s < 8; s++) o.xs[s] = ld8(a.qf + (((int64_t)b * 8 + s) * 16 + c16) * 32 + 8 * q4);
-      const int16_t *bb = a.bf + ((int64_t)b * 16 + c16) * 16;
-      o.b0 = *reinterpret_cast<const uint4 *>(bb);
-      o.b1 = *reinterpret_cast<const uint4 *>(bb + 8);
-      o.dt = a.df[(int64_t)b * 16 + c16];
+      for (int s = 0; s < 8; s++) o.xs[s] = ld8(xq + ((int64_t)b * 8 + s) * 512);
+      o.dt = xd[(int64_t)b * 16];
     } else {
 #pragma unroll
-      for (int s = 0; s < 8; s++) o.xs[s] = ld8(xq + (int64_t)b * 256 + 32 * s);
-      o.b0 = *reinterpret_cast<const uint4 *>(xb + (int64_t)b * 16);
-      o.b1 = *reinterpret_cast<const uint4 *>(xb + (int64_t)b * 16 + 8);
+      for (int s = 0; s < 8; s++) o.xs[s] = xzero ? make_uint2(0u, 0u) : ld8(xq + (int64_t)b * 256 + 32 * s);
       o.dt = xd[b];
     }
   };
-  // blocks b and b + 1 in flight: block b's operands were fetched two blocks earlier
-  auto body = [&](const Ops &op, float (&tm)[NM][M::TERMS][4]) {
-    const typename M::Raw(&cur)[NM] = op.raw;
-    const uint2(&xs)[8] = op.xs;
-    const uint4 b0 = op.b0, b1 = op.b1;
-    const float dt = op.dt;
-    // the slab of this block (the wave's own region; a wave barrier orders it)
+  struct Ops {
+    typename M::Raw raw[STG ? 1 : NM];
+    u32x4_t sg[STG ? NM : 1][kStgLoads];
+    Xo x;
+  };
+  auto fetch = [&](int b, Ops &o) {
+    if constexpr (STG) {
 #pragma unroll
-    for (int m = 0; m < NM; m++) M::stage(cur[m], q4, &slab[wv][m][c16 * kSlab]);
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    // bsums of the token: 16 int16 of the block
-    const uint32_t bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-    int bsum[16];
+      for (int m = 0; m < NM; m++) {
+        const uint8_t *base = (m ? a.w2 : a.w) + tbase + (int64_t)b * 144;
 #pragma unroll
-    for (int g = 0; g < 8; g++) {
-      bsum[2 * g] = (int)(int16_t)(bv[g] & 0xFFFF);
-      bsum[2 * g + 1] = (int)(int16_t)(bv[g] >> 16);
+        for (int i = 0; i < kStgLoads; i++)
+          if (sok[i]) o.sg[m][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(base + soff[i]));
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < NM; m++) M::load(wr[m] + (int64_t)b * M::BYTES, q4, o.raw[m]);
     }
+    fetch_x(b, o.x);
+  };
+  // one block's terms into ring slot buf
+  auto body = [&](const Ops &op, int buf) {
+    const Xo &xo = op.x;
+    typename M::Raw sraw[STG ? NM : 1];
+    if constexpr (STG) {
+      // the staged pieces to this wave's LDS area (its previous block's reads are done: one
+      // wave's LDS accesses complete in order), then each lane's operand bytes from there
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int i = 0; i < kStgLoads; i++)
+          if (sok[i]) *reinterpret_cast<u32x4_t *>(&stg[wv][m][lofs[i]]) = op.sg[m][i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int m = 0; m < NM; m++) M::load_lds(&stg[wv][m][c16 * kStgRow], q4, sraw[m]);
+    }
+    const typename M::Raw *raw = STG ? sraw : op.raw;
+#pragma unroll
+    for (int m = 0; m < NM; m++) M::stage(raw[m], q4, &slab[wv][m][c16 * kSlab]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const i32x4_t zero = {0, 0, 0, 0};
 #pragma unroll
     for (int m = 0; m < NM; m++) {
       if constexpr (M::TERMS == 1) {
-        // Q4_K: sumi = sum_s sc_s a_s, summ = sum_s m_s (bsums of the sub-block), one term
-        i32x4_t acc[8];
+        // Q4_K: sumi = sum_s sc_s a_s (VALU), summ by the matrix cores
+        i32x4_t acc[8], accm = zero;
+        uint32_t m03, m47;
+        M::mins(raw[m], m03, m47);
 #pragma unroll
-        for (int s = 0; s < 8; s++) acc[s] = mma(M::operand(cur[m], s), xs[s], i32x4_t{0, 0, 0, 0});
+        for (int s = 0; s < 8; s++) {
+          acc[s] = mma(M::operand(raw[m], s), xo.xs[s], zero);
+          const uint32_t mb = __builtin_amdgcn_perm(s < 4 ? m03 : m47, s < 4 ? m03 : m47, 0x01010101u * (s & 3));
+          accm = mma(make_uint2(mb, mb), xo.xs[s], accm);
+        }
+        float tm[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const uint32_t *row = &slab[wv][m][(4 * q4 + i) * kSlab];
           const uint4 s0 = *reinterpret_cast<const uint4 *>(row), s1 = *reinterpret_cast<const uint4 *>(row + 4);
-          const uint4 m0 = *reinterpret_cast<const uint4 *>(row + 8), m1 = *reinterpret_cast<const uint4 *>(row + 12);
-          const uint32_t dd = row[16];
+          const uint32_t dd = row[8];
           const int sc[8] = {(int)s0.x, (int)s0.y, (int)s0.z, (int)s0.w, (int)s1.x, (int)s1.y, (int)s1.z, (int)s1.w};
-          const int mn[8] = {(int)m0.x, (int)m0.y, (int)m0.z, (int)m0.w, (int)m1.x, (int)m1.y, (int)m1.z, (int)m1.w};
-          int sumi = 0, summ = 0;
+          int sumi = 0;
 #pragma unroll
-          for (int s = 0; s < 8; s++) {
-            // 24-bit products (sc, m < 64; |a| < 2^16; |bsum pair| < 2^12): exact, full rate
-            sumi += __mul24(sc[s], acc[s][i]);
-            summ += __mul24(mn[s], bsum[2 * s] + bsum[2 * s + 1]);
-          }
+          for (int s = 0; s < 8; s++) sumi += __mul24(sc[s], acc[s][i]);  // sc < 64, |a| < 2^16: exact
           const float d = half_lo(dd), dmin = half_hi(dd);
-          tm[m][0][i] = dt * (d * (float)sumi - dmin * (float)summ);  // src/FastMath.cs:155
+          tm[i] = xo.dt * (d * (float)sumi - dmin * (float)accm[i]);  // src/FastMath.cs:155
         }
+        if (c16 < 8) terms[buf][wv][m][dl] = make_float4(tm[0], tm[1], tm[2], tm[3]);
       } else {
-        // Q6_K: per half, eight groups of 16: acc_g = sum q x - 32 sum x; part = sum_g sc_g acc_g
+        // Q6_K: per half, the group sums of (q - 32) x; part = sum_g sc_g acc_g
+        const uint2 m32 = make_uint2(0xE0E0E0E0u, 0xE0E0E0E0u);  // int8 -32
+        i32x4_t acc[2][4];
 #pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
-          i32x4_t acc[8];
+        for (int hh = 0; hh < 2; hh++)
 #pragma unroll
           for (int sp = 0; sp < 4; sp++) {
-            const uint2 wop = M::operand(cur[m], hh, sp), x = xs[4 * hh + sp];
-            const uint2 zero = make_uint2(0u, 0u);
-            acc[2 * sp] = mma(wop, q4 < 2 ? x : zero, i32x4_t{0, 0, 0, 0});
-            acc[2 * sp + 1] = mma(wop, q4 < 2 ? zero : x, i32x4_t{0, 0, 0, 0});
+            const uint2 x = xo.xs[4 * hh + sp];
+            acc[hh][sp] = mma(m32, x, mma(M::operand(raw[m], hh, sp), x, zero));
           }
+        const int gs = c16 >> 3;  // this column's group within each run
+        float tm[2][4];
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const uint32_t *row = &slab[wv][m][(4 * q4 + i) * kSlab];
-            const uint4 sv = *reinterpret_cast<const uint4 *>(row + 8 * hh),
-                        sw = *reinterpret_cast<const uint4 *>(row + 8 * hh + 4);
-            const int sc[8] = {(int)sv.x, (int)sv.y, (int)sv.z, (int)sv.w, (int)sw.x, (int)sw.y, (int)sw.z, (int)sw.w};
-            int part = 0;
+        for (int i = 0; i < 4; i++) {
+          const uint32_t *row = &slab[wv][m][(4 * q4 + i) * kSlab];
+          const float f = xo.dt * half_lo(row[16]);
 #pragma unroll
-            for (int g = 0; g < 8; g++)  // |sc| <= 128, |acc - 32 bsum| < 2^18: 24-bit products, exact
-              part += __mul24(sc[g], acc[g][i] - 32 * bsum[8 * hh + g]);
-            const float d = half_lo(row[16]);
-            tm[m][hh][i] = dt * d * (float)part;  // src/FastMath.cs:209
+          for (int hh = 0; hh < 2; hh++) {
+            const uint4 sv = *reinterpret_cast<const uint4 *>(row + 8 * hh + 4 * gs);
+            // |sc| <= 128, |acc| < 2^17: 24-bit products, exact
+            int p = __mul24((int)sv.x, acc[hh][0][i]) + __mul24((int)sv.y, acc[hh][1][i]) +
+                    __mul24((int)sv.z, acc[hh][2][i]) + __mul24((int)sv.w, acc[hh][3][i]);
+            p += __builtin_amdgcn_update_dpp(0, p, 0x128, 0xF, 0xF, false);  // column c16 ^ 8: the other groups
+            tm[hh][i] = f * (float)p;                                          // src/FastMath.cs:209
           }
         }
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  };
-  // wave 0 adds a block's terms to the running sums; the others keep them for wave 0
-  auto take = [&](int b, const float (&tm)[NM][M::TERMS][4]) {
-    if (wv == 0) {
-#pragma unroll
-      for (int m = 0; m < NM; m++)
-#pragma unroll
-        for (int h = 0; h < M::TERMS; h++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) sum[m][i] += tm[m][h][i];
-    } else if (c16 < 8) {
-      float4 *p = mma_terms + (((int64_t)(wv - 1) * bw + (b - b_lo)) * NM * M::TERMS) * 32 + dl;
-#pragma unroll
-      for (int m = 0; m < NM; m++)
-#pragma unroll
-        for (int h = 0; h < M::TERMS; h++)
-          p[(m * M::TERMS + h) * 32] = make_float4(tm[m][h][0], tm[m][h][1], tm[m][h][2], tm[m][h][3]);
-    }
-  };
-  if constexpr (STG) {
-    // stage loads: chunk f = 64 i + lane of the 16 x kStageBlocks block region is row f / per,
-    // 16-byte piece f % per of it (per = kStageBlocks * 9)
-    constexpr int per = kStageBlocks * 9;
-    int soff[kStageLoads], lofs[kStageLoads];
-    bool sok[kStageLoads];
-#pragma unroll
-    for (int i = 0; i < kStageLoads; i++) {
-      const int f = 64 * i + lane, r = f / per, c = f % per;
-      sok[i] = f < kStageChunks;
-      const int row = min(tile * 16 + r, a.rows - 1);
-      soff[i] = 0;
-      lofs[i] = r * kStageRow + 16 * c;
-      // row offsets fit 32 bits only per tile; the tile's first row is added once below
-      soff[i] = (row - min(tile * 16, a.rows - 1)) * (int)a.row_bytes + 16 * c;
-    }
-    const int64_t tbase = (int64_t)min(tile * 16, a.rows - 1) * a.row_bytes;
-    u32x4_t sreg[NM][kStageLoads];
-    auto issue = [&](int c0) {  // blocks c0 .. c0 + kStageBlocks - 1 (clamped to the row)
-      const int cb = min(c0, nb - kStageBlocks);
-#pragma unroll
-      for (int m = 0; m < NM; m++) {
-        const uint8_t *base = (m ? a.w2 : a.w) + tbase + (int64_t)cb * 144;
-#pragma unroll
-        for (int i = 0; i < kStageLoads; i++)
-          if (sok[i]) sreg[m][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(base + soff[i]));
-      }
-      return cb;
-    };
-    auto commit = [&]() {
-      asm volatile("" ::: "memory");
-#pragma unroll
-      for (int m = 0; m < NM; m++)
-#pragma unroll
-        for (int i = 0; i < kStageLoads; i++)
-          if (sok[i]) *reinterpret_cast<u32x4_t *>(&stage[wv][m][lofs[i]]) = sreg[m][i];
-      asm volatile("" ::: "memory");
-    };
-    struct Xo {
-      uint2 xs[8];
-      uint4 b0, b1;
-      float dt;
-    };
-    auto fetch_x = [&](int b, Xo &o) {
-#pragma unroll
-      for (int s = 0; s < 8; s++) o.xs[s] = ld8(a.qf + (((int64_t)b * 8 + s) * 16 + c16) * 32 + 8 * q4);
-      const int16_t *bb = a.bf + ((int64_t)b * 16 + c16) * 16;
-      o.b0 = *reinterpret_cast<const uint4 *>(bb);
-      o.b1 = *reinterpret_cast<const uint4 *>(bb + 8);
-      o.dt = a.df[(int64_t)b * 16 + c16];
-    };
-    auto block = [&](int b, int cb, const Xo &xo) {
-      Ops op;
-#pragma unroll
-      for (int m = 0; m < NM; m++) M::load_lds(&stage[wv][m][c16 * kStageRow + (b - cb) * 144], q4, op.raw[m]);
-#pragma unroll
-      for (int s = 0; s < 8; s++) op.xs[s] = xo.xs[s];
-      op.b0 = xo.b0;
-      op.b1 = xo.b1;
-      op.dt = xo.dt;
-      float tm[NM][M::TERMS][4];
-      body(op, tm);
-      take(b, tm);
-    };
-    if (tile * 16 < a.rows && b_lo < b_hi) {
-      Xo xr[2];
-      int cb = issue(b_lo);
-      fetch_x(b_lo, xr[0]);
-      if (b_lo + 1 < b_hi) fetch_x(b_lo + 1, xr[1]);
-      for (int c = b_lo; c < b_hi; c += kStageBlocks) {
-        commit();
-        const int cur = cb;
-        if (c + kStageBlocks < b_hi) cb = issue(c + kStageBlocks);
-        {
-          const Xo xo = xr[0];
-          if (c + 2 < b_hi) fetch_x(c + 2, xr[0]);
-          block(c, cur, xo);
-        }
-        if (c + 1 < b_hi) {
-          const Xo xo = xr[1];
-          if (c + 3 < b_hi) fetch_x(c + 3, xr[1]);
-          block(c + 1, cur, xo);
+        if (c16 < 8) {
+          terms[buf][wv][2 * m][dl] = make_float4(tm[0][0], tm[0][1], tm[0][2], tm[0][3]);
+          terms[buf][wv][2 * m + 1][dl] = make_float4(tm[1][0], tm[1][1], tm[1][2], tm[1][3]);
         }
       }
     }
-  } else if (tile * 16 < a.rows && b_lo < b_hi) {
-    Ops ring[2];
-    fetch(b_lo, ring[0]);
-    if (b_lo + 1 < b_hi) fetch(b_lo + 1, ring[1]);
-    for (int b = b_lo; b < b_hi; b += 2) {
-      {
-        const Ops op = ring[0];
-        if (b + 2 < b_hi) fetch(b + 2, ring[0]);
-        float tm[NM][M::TERMS][4];
-        body(op, tm);
-        take(b, tm);
-      }
-      if (b + 1 < b_hi) {
-        const Ops op = ring[1];
-        if (b + 3 < b_hi) fetch(b + 3, ring[1]);
-        float tm[NM][M::TERMS][4];
-        body(op, tm);
-        take(b + 1, tm);
-      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // the slab is the next block's
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  // the chain: lane l of wave w owns pair p = l W + w < 128 (D lane p / 4, row offset p % 4)
+  const int p = lane * W + wv;
+  const bool owner = p < 128;
+  float sum[NM];
+#pragma unroll
+  for (int m = 0; m < NM; m++) sum[m] = 0.f;
+  auto drain = [&](int r, int buf) {
+    if (owner) {
+      const float *t = reinterpret_cast<const float *>(&terms[buf][0][0][0]);
+      for (int w = 0; w < W && r * W + w < nb; w++)
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+          for (int h = 0; h < M::TERMS; h++) sum[m] += t[((w * MH) + m * M::TERMS + h) * 128 + p];
+    }
+  };
+
+  Ops o0, o1;
+  if (wv < nb) fetch(wv, o0);
+  for (int r = 0; r < nr; r += 2) {
+    {
+      const int b = r * W + wv;
+      if (b + W < nb) fetch(b + W, o1);
+      if (b < nb) body(o0, 0);
+      __syncthreads();
+      drain(r, 0);
+    }
+    if (r + 1 < nr) {
+      const int b = (r + 1) * W + wv;
+      if (b + W < nb) fetch(b + W, o0);
+      if (b < nb) body(o1, 1);
+      __syncthreads();
+      drain(r + 1, 1);
     }
   }
-  __syncthreads();
-  if (wv != 0 || tile * 16 >= a.rows) return;
-  // the other quarters' terms, in block order
-  if (c16 < 8)
-    for (int b = min(nb, bw); b < nb; b++) {
-      const float4 *p = mma_terms + (int64_t)(b - bw) * NM * M::TERMS * 32 + dl;
-#pragma unroll
-      for (int m = 0; m < NM; m++)
-#pragma unroll
-        for (int h = 0; h < M::TERMS; h++) {
-          const float4 v = p[(m * M::TERMS + h) * 32];
-          sum[m][0] += v.x;
-          sum[m][1] += v.y;
-          sum[m][2] += v.z;
-          sum[m][3] += v.w;
-        }
-    }
-  if (c16 < a.T) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int row = tile * 16 + 4 * q4 + i;
-      if (row < a.rows) {
-        float v = sum[0][i];
-        if constexpr (NM == 2) v = silu_mul(v, sum[1][i]);
-        a.y[(int64_t)c16 * a.ldy + row] = v;
-      }
+  if (owner) {
+    const int d = p >> 2, t = d & 7;
+    const int row = tile * 16 + 4 * (d >> 3) + (p & 3);
+    if (t < a.T && row < a.rows) {
+      float v = sum[0];
+      if constexpr (NM == 2) v = silu_mul(v, sum[1]);
+      a.y[(int64_t)t * a.ldy + row] = v;
     }
   }
 }
 
-// The staged terms of waves 1..3 are the launch's dynamic LDS; rows longer than this allows
-// (more than about 200 K of Q6_K values) take the VALU kernel.
-constexpr size_t kMmaMaxLds = 96 * 1024;
-
-static size_t mma_lds(int type, int cols, int nm) {
-  const int bw = (cols / 256 + kMmaWaves - 1) / kMmaWaves;
-  return (size_t)(kMmaWaves - 1) * bw * nm * (type == 14 ? 2 : 1) * 32 * sizeof(float4);
-}
-
-bool intmma_supports(int type, int cols, int T, int nm) {
-  return (type == 12 || type == 14) && cols > 0 && cols % 256 == 0 && T >= 2 && T <= kMmaTokens &&
-         mma_lds(type, cols, nm) <= kMmaMaxLds;
+bool intmma_supports(int type, int cols, int T, int) {
+  return (type == 12 || type == 14) && cols > 0 && cols % 256 == 0 && T >= 2 && T <= kMmaTokens;
 }
 
 int intmma_max_tokens(int type, int cols, int nm) { return intmma_supports(type, cols, 2, nm) ? kMmaTokens : 0; }
 
-template <class M, int NM, bool FRAG, bool STG = false>
-static hipError_t go_frag(const MmaArgs &a, int grid, size_t smem, hipStream_t st) {
-  static bool raised = false;
-  if (smem > 65536 && !raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&intmma_kernel<M, NM, FRAG, STG>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMmaMaxLds) != hipSuccess)
-      return hipErrorInvalidConfiguration;
-    raised = true;
-  }
-  hipLaunchKernelGGL((intmma_kernel<M, NM, FRAG, STG>), dim3(grid), dim3(64 * kMmaWaves), smem, st, a);
-  return hipGetLastError();
-}
+// Four waves per workgroup: a 70B layer's 8192-row down matrix is 512 tiles, two per CU; six or
+// eight waves (more blocks per round) measured slower, and they split a Q4_K row of 32 blocks
+// unevenly.
+constexpr int kMmaWaves = 4;
 
-// Q4_K rows of at least one stage take the staged weights (with the operand-order activations).
+// Q4_K with the operand-order activations takes the staged weights.
 template <class M, int NM>
-static hipError_t go(const MmaArgs &a, int grid, size_t smem, hipStream_t st) {
-  if constexpr (M::BYTES == 144)
-    if (a.qf && a.cols / 256 >= kStageBlocks) return go_frag<M, NM, true, true>(a, grid, smem, st);
-  return a.qf ? go_frag<M, NM, true>(a, grid, smem, st) : go_frag<M, NM, false>(a, grid, smem, st);
+static hipError_t go(const MmaArgs &a, int grid, hipStream_t st) {
+  constexpr int W = kMmaWaves;
+  constexpr bool STG = M::BYTES == 144;
+  if (a.qf)
+    hipLaunchKernelGGL((intmma_kernel<M, NM, W, true, STG>), dim3(grid), dim3(64 * W), 0, st, a);
+  else
+    hipLaunchKernelGGL((intmma_kernel<M, NM, W, false, false>), dim3(grid), dim3(64 * W), 0, st, a);
+  return hipGetLastError();
 }
 
 hipError_t intmma_launch(int type, const uint8_t *w, const uint8_t *w2, int64_t row_bytes, int rows, int cols,
                          QActsDev qa, int T, float *y, int ldy, hipStream_t st) {
   if (rows <= 0) return hipSuccess;
-  if (!intmma_supports(type, cols, T, w2 ? 2 : 1) || !qa.q || !qa.d || !qa.bsums) return hipErrorInvalidValue;
-  const MmaArgs a{w, w2, row_bytes, rows, cols, qa.q, qa.d, qa.bsums, T, y, ldy, qa.qf, qa.bf, qa.df};
+  if (!intmma_supports(type, cols, T, w2 ? 2 : 1) || !qa.q || !qa.d || (qa.qf && !qa.df)) return hipErrorInvalidValue;
+  const MmaArgs a{w, w2, row_bytes, rows, cols, qa.qf, qa.df, qa.q, qa.d, T, y, ldy};
   const int grid = (rows + 15) / 16;
-  const size_t smem = mma_lds(type, cols, w2 ? 2 : 1);
-  hipError_t e = hipSuccess;
-  if (type == 12) {
-    if (w2) e = go<MQ4K, 2>(a, grid, smem, st);
-    else e = go<MQ4K, 1>(a, grid, smem, st);
-  } else {
-    if (w2) e = go<MQ6K, 2>(a, grid, smem, st);
-    else e = go<MQ6K, 1>(a, grid, smem, st);
-  }
-  return e;
+  if (type == 12) return w2 ? go<MQ4K, 2>(a, grid, st) : go<MQ4K, 1>(a, grid, st);
+  return w2 ? go<MQ6K, 2>(a, grid, st) : go<MQ6K, 1>(a, grid, st);
 }
 
 }  // namespace wl
