@@ -349,23 +349,23 @@ __global__ __launch_bounds__(64 * W) void intmma_kernel(MmaArgs a) {
     }
   };
 
+  // round r: its block's operands were fetched a round earlier; those of round r + 1 go to the
+  // set that round r - 1 used. Every fetch is issued (past the row's end it re-reads the last
+  // block), so the load counter's waits are the same on every path: a conditional fetch makes
+  // the compiler wait for all loads in flight, the prefetched ones too. (Two rounds in flight
+  // measured the same.)
+  auto round = [&](int r, const Ops &cur, Ops &nxt) {
+    const int b = r * W + wv;
+    fetch(min(b + W, nb - 1), nxt);
+    if (b < nb) body(cur, r & 1);
+    __syncthreads();
+    drain(r, r & 1);
+  };
   Ops o0, o1;
-  if (wv < nb) fetch(wv, o0);
+  fetch(min(wv, nb - 1), o0);
   for (int r = 0; r < nr; r += 2) {
-    {
-      const int b = r * W + wv;
-      if (b + W < nb) fetch(b + W, o1);
-      if (b < nb) body(o0, 0);
-      __syncthreads();
-      drain(r, 0);
-    }
-    if (r + 1 < nr) {
-      const int b = (r + 1) * W + wv;
-      if (b + W < nb) fetch(b + W, o0);
-      if (b < nb) body(o1, 1);
-      __syncthreads();
-      drain(r + 1, 1);
-    }
+    round(r, o0, o1);
+    if (r + 1 < nr) round(r + 1, o1, o0);
   }
   if (owner) {
     const int d = p >> 2, t = d & 7;
