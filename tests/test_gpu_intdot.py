@@ -152,6 +152,37 @@ def test_int_matmul_matrix_cores_match_oracle_bitwise(ctx, t, shape, T):
     w.free()
 
 
+@pytest.mark.parametrize("T", [2, 5, 8])
+def test_int_qkv_in_one_launch_matches_each_matrix(ctx, T):
+    # q, k (Q4_K) and v (Q6_K) reading the same x run as one matrix-core launch under IntDot;
+    # each output is its matrix's own integer matmul, bit for bit (row counts not multiples of 16)
+    lib = load()
+    cols = 2816
+    shapes = [(GgmlType.Q4_K, 200), (GgmlType.Q4_K, 40), (GgmlType.Q6_K, 37)]
+    host = [blocks(t, rows, cols, seed=60 + i) for i, (t, rows) in enumerate(shapes)]
+    ws = [ctx.upload(t, h, rows, cols) for (t, rows), h in zip(shapes, host)]
+    x = np.random.default_rng(T + 90).standard_normal((T, cols), dtype=np.float32)
+    dx = torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0")
+    ys = [torch.empty((T, rows), dtype=torch.float32, device="cuda:0") for _, rows in shapes]
+    torch.cuda.synchronize()
+    ctx.IntDot = True
+    try:
+        arr_w = (ctypes.c_void_p * 3)(*[w.handle for w in ws])
+        arr_y = (ctypes.c_void_p * 3)(*[y.data_ptr() for y in ys])
+        assert lib.wl_matmul_multi_dev(ctx.handle, 3, arr_w, ctypes.c_void_p(dx.data_ptr()), T, arr_y) == 0
+        ctx.sync()
+        each = [Transformer.MatMul(w, x, T) for w in ws]
+    finally:
+        ctx.IntDot = False
+    for (t, rows), h, y, e in zip(shapes, host, ys, each):
+        got = y.cpu().numpy()
+        assert np.array_equal(bits(got), bits(e)), (t.name, rows, int((bits(got) != bits(e)).sum()))
+        want = oracle_int_matmul(t, h, rows, cols, x)
+        assert np.array_equal(bits(got), bits(want))
+    for w in ws:
+        w.free()
+
+
 @pytest.mark.parametrize("t", ITYPES, ids=lambda t: t.name)
 def test_int_path_is_off_by_default_and_close_to_float(ctx, t):
     rows, cols, T = 64, 2048, 2

@@ -671,8 +671,26 @@ extern "C" int wl_matmul_multi_dev(wl_ctx *c, int32_t n, const wl_weight *const 
     same = same && ws[i]->type == ws[0]->type;
     mixed_ok = mixed_ok && wl::gemv_mixed_supports(ws[i]->type);
   }
-  bool any_int = false;
-  for (int i = 0; i < n; i++) any_int = any_int || int_path(c, ws[i]);
+  bool any_int = false, all_int = true;
+  int types[wl::GEMV_MAX_MATS];
+  for (int i = 0; i < n; i++) {
+    any_int = any_int || int_path(c, ws[i]);
+    all_int = all_int && int_path(c, ws[i]);
+    types[i] = ws[i]->type;
+  }
+  const int cols = (int)ws[0]->cols;
+  if (all_int && n > 1 && wl::intmma_multi_supports(types, n, cols, T)) {
+    // every matrix on the int8 matrix cores in one launch, on activations quantized once
+    wl::QActsDev qa;
+    if (int rc = int_quantize(c, d_x, T, cols, 1, &qa)) return rc;
+    wl::MmaMat mats[3];
+    for (int i = 0; i < n; i++) {
+      const int rows = (int)(ws[i]->rows * ws[i]->experts);
+      mats[i] = wl::MmaMat{ws[i]->dev, ws[i]->row_bytes, rows, ws[i]->type, d_ys[i], rows};
+    }
+    WL_HIP(wl::intmma_multi_launch(mats, n, cols, qa, T, c->stream), "int dot launch");
+    return WL_OK;
+  }
   if (any_int) {
     // the integer matrices share the activations; the others take the float path one by one
     IntActs acts;

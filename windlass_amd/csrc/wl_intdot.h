@@ -51,6 +51,17 @@ bool intmma_supports(int type, int cols, int T, int nm);
 int intmma_max_tokens(int type, int cols, int nm);  // 0 when the kernel does not take the rows
 hipError_t intmma_launch(int type, const uint8_t *w, const uint8_t *w2, int64_t row_bytes, int rows, int cols,
                          QActsDev qa, int T, float *y, int ldy, hipStream_t st);
+// Up to three matrices of `cols` columns that read the same activations, in one launch (each
+// result as intmma_launch gives it).
+struct MmaMat {
+  const uint8_t *w;
+  int64_t row_bytes;
+  int rows, type;
+  float *y;
+  int ldy;
+};
+bool intmma_multi_supports(const int *types, int n, int cols, int T);
+hipError_t intmma_multi_launch(const MmaMat *mats, int n, int cols, QActsDev qa, int T, hipStream_t st);
 
 struct MoePlan;
 // The integer products of routed experts (MoeFfn's SwiGlu under IntDot, src/Transformer.cs:

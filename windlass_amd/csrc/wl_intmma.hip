@@ -163,8 +163,9 @@ struct MmaArgs {
 // A workgroup owns one 16-row tile (of each matrix). Its W waves take the row's blocks in rounds:
 // in round r wave w takes block r W + w, its loads issued one round ahead. Each block's terms
 // (for the 8 token columns: 16 rows x 8 tokens x TERMS floats per matrix) go to an LDS ring of
-// two rounds; after the round's barrier every wave adds the round's terms, in block order, for
-// its share of the (row, token) pairs: the reference's single `sum +=` chain over the whole row.
+// two groups of RPS rounds; after a group's barrier every wave adds the group's terms, in block
+// order, for its share of the (row, token) pairs: the reference's single `sum +=` chain over
+// the whole row.
 // Staged Q4_K weights: a wave reads its block's 16 rows x 144 bytes (per matrix) with three
 // coalesced nontemporal 16-byte loads per lane, one round ahead, into its own LDS area, and the
 // lanes take their operand bytes from there (a wave load covers about seven rows' contiguous
@@ -175,15 +176,23 @@ constexpr int kStgLoads = (kStgChunks + 63) / 64;  // loads per lane
 
 // FRAG: the operand-order copy (one 512-byte wave load per run); otherwise the tokens' rows.
 // STG: staged weights (Q4_K).
-template <class M, int NM, int W, bool FRAG, bool STG>
-__global__ __launch_bounds__(64 * W) void intmma_kernel(MmaArgs a) {
-  constexpr int MH = NM * M::TERMS;
+// The kernel's LDS: the scale slabs, the terms ring of two groups of RPS rounds (MH floats per
+// (row, token) and block: matrices x terms per block), and the staged weights.
+template <int W, int NM, int MH, int RPS, bool STG>
+struct MmaLds {
+  uint32_t slab[W][NM][16 * kSlab];
+  float4 terms[2 * RPS][W][MH][32];
+  uint8_t stg[STG ? W : 1][STG ? NM : 1][STG ? 16 * kStgRow : 16];
+};
+
+// Tile `tile` of a (every wave of the workgroup calls it: it holds workgroup barriers).
+template <class M, int NM, int W, bool FRAG, bool STG, int RPS, class L>
+__device__ __forceinline__ void mma_tile(const MmaArgs &a, const int tile, L &lds) {
   static_assert(!STG || M::BYTES == 144, "staging is laid out for Q4_K blocks");
-  __shared__ __attribute__((aligned(16))) uint32_t slab[W][NM][16 * kSlab];
-  __shared__ __attribute__((aligned(16))) float4 terms[2][W][MH][32];
-  __shared__ __attribute__((aligned(16))) uint8_t stg[STG ? W : 1][STG ? NM : 1][STG ? 16 * kStgRow : 16];
+  auto &slab = lds.slab;
+  auto &terms = lds.terms;
+  auto &stg = lds.stg;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, q4 = lane >> 4, c16 = lane & 15;
-  const int tile = blockIdx.x;  // uniform: the barriers below are reached by every wave
   const int nb = a.cols / 256, nr = (nb + W - 1) / W;
   const int arow = min(tile * 16 + c16, a.rows - 1);  // rows past the end re-read the last row
   const uint8_t *wr[2] = {a.w + (int64_t)arow * a.row_bytes, NM == 2 ? a.w2 + (int64_t)arow * a.row_bytes : nullptr};
@@ -338,14 +347,14 @@ __global__ __launch_bounds__(64 * W) void intmma_kernel(MmaArgs a) {
   float sum[NM];
 #pragma unroll
   for (int m = 0; m < NM; m++) sum[m] = 0.f;
-  auto drain = [&](int r, int buf) {
+  auto drain = [&](int r) {
     if (owner) {
-      const float *t = reinterpret_cast<const float *>(&terms[buf][0][0][0]);
       for (int w = 0; w < W && r * W + w < nb; w++)
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
-          for (int h = 0; h < M::TERMS; h++) sum[m] += t[((w * MH) + m * M::TERMS + h) * 128 + p];
+          for (int h = 0; h < M::TERMS; h++)
+            sum[m] += reinterpret_cast<const float *>(&terms[r % (2 * RPS)][w][m * M::TERMS + h][0])[p];
     }
   };
 
@@ -357,9 +366,11 @@ __global__ __launch_bounds__(64 * W) void intmma_kernel(MmaArgs a) {
   auto round = [&](int r, const Ops &cur, Ops &nxt) {
     const int b = r * W + wv;
     fetch(min(b + W, nb - 1), nxt);
-    if (b < nb) body(cur, r & 1);
-    __syncthreads();
-    drain(r, r & 1);
+    if (b < nb) body(cur, r % (2 * RPS));
+    if (r % RPS == RPS - 1 || r + 1 == nr) {  // uniform
+      __syncthreads();
+      for (int q = r - r % RPS; q <= r; q++) drain(q);
+    }
   };
   Ops o0, o1;
   fetch(min(wv, nb - 1), o0);
@@ -376,6 +387,39 @@ __global__ __launch_bounds__(64 * W) void intmma_kernel(MmaArgs a) {
       a.y[(int64_t)t * a.ldy + row] = v;
     }
   }
+}
+
+template <class M, int NM, int W, bool FRAG, bool STG>
+__global__ __launch_bounds__(64 * W) void intmma_kernel(MmaArgs a) {
+  // rounds per barrier: the ring holds two groups of RPS rounds (64 KB for one Q6_K matrix or
+  // 32 KB for the SwiGLU pair, whose workgroups need room for two per CU); 1, 2, 4 and 8
+  // measured 242, 238, 228 and 250 us (the pair at 8: one workgroup per CU) for a 70B layer
+  constexpr int RPS = NM == 2 ? 4 : 8;
+  __shared__ MmaLds<W, NM, NM * M::TERMS, RPS, STG> lds;
+  mma_tile<M, NM, W, FRAG, STG, RPS>(a, blockIdx.x, lds);
+}
+
+// Several matrices that read the same activations (q, k and v) in one launch: the workgroups
+// of matrix i are tiles tile_end[i - 1] .. tile_end[i] - 1; each takes its format's body.
+// Launched apart, k and v (1024 rows: 64 tiles each) leave most of the device idle.
+struct MmaMulti {
+  MmaArgs seg[3];
+  int type[3], tile_end[3];
+};
+
+template <int W, bool FRAG>
+__global__ __launch_bounds__(64 * W) void intmma_multi_kernel(MmaMulti mm) {
+  constexpr int RPS = 4;  // one workgroup's LDS fits three per CU
+  __shared__ MmaLds<W, 1, 2, RPS, FRAG> lds;
+  const int bid = blockIdx.x;  // uniform: the segment and its branch are the workgroup's
+  const int i = bid < mm.tile_end[0] ? 0 : bid < mm.tile_end[1] ? 1 : 2;
+  const MmaArgs a = i == 0 ? mm.seg[0] : i == 1 ? mm.seg[1] : mm.seg[2];
+  const int type = i == 0 ? mm.type[0] : i == 1 ? mm.type[1] : mm.type[2];
+  const int tile = bid - (i == 0 ? 0 : i == 1 ? mm.tile_end[0] : mm.tile_end[1]);
+  if (type == 12)
+    mma_tile<MQ4K, 1, W, FRAG, FRAG, RPS>(a, tile, lds);
+  else
+    mma_tile<MQ6K, 1, W, FRAG, false, RPS>(a, tile, lds);
 }
 
 bool intmma_supports(int type, int cols, int T, int) {
@@ -409,6 +453,36 @@ hipError_t intmma_launch(int type, const uint8_t *w, const uint8_t *w2, int64_t 
   const int grid = (rows + 15) / 16;
   if (type == 12) return w2 ? go<MQ4K, 2>(a, grid, st) : go<MQ4K, 1>(a, grid, st);
   return w2 ? go<MQ6K, 2>(a, grid, st) : go<MQ6K, 1>(a, grid, st);
+}
+
+bool intmma_multi_supports(const int *types, int n, int cols, int T) {
+  if (n < 1 || n > 3) return false;
+  for (int i = 0; i < n; i++)
+    if (!intmma_supports(types[i], cols, T, 1)) return false;
+  return true;
+}
+
+hipError_t intmma_multi_launch(const MmaMat *mats, int n, int cols, QActsDev qa, int T, hipStream_t st) {
+  int types[3];
+  for (int i = 0; i < n && i < 3; i++) types[i] = mats[i].type;
+  if (!intmma_multi_supports(types, n, cols, T) || !qa.q || !qa.d || (qa.qf && !qa.df)) return hipErrorInvalidValue;
+  MmaMulti mm{};
+  int tiles = 0;
+  for (int i = 0; i < 3; i++) {
+    const MmaMat &m = mats[i < n ? i : n - 1];
+    const int rows = i < n ? m.rows : 0;  // past n: empty segments
+    mm.seg[i] = MmaArgs{m.w, nullptr, m.row_bytes, rows > 0 ? rows : 1, cols, qa.qf, qa.df, qa.q, qa.d, T, m.y, m.ldy};
+    mm.type[i] = m.type;
+    tiles += (rows + 15) / 16;
+    mm.tile_end[i] = tiles;
+  }
+  if (tiles == 0) return hipSuccess;
+  constexpr int W = kMmaWaves;
+  if (qa.qf)
+    hipLaunchKernelGGL((intmma_multi_kernel<W, true>), dim3(tiles), dim3(64 * W), 0, st, mm);
+  else
+    hipLaunchKernelGGL((intmma_multi_kernel<W, false>), dim3(tiles), dim3(64 * W), 0, st, mm);
+  return hipGetLastError();
 }
 
 }  // namespace wl
