@@ -52,14 +52,10 @@ __device__ __forceinline__ uint2 ld8(const void *p) { return *reinterpret_cast<c
 // sub-blocks' 6-bit scales and mins (get_scale_min_k4, src/Quants.cs:321-330).
 struct MQ4K {
   static constexpr int BYTES = 144, TERMS = 1;
+  static constexpr int SCH = 9, SROW = 176;  // staging: 16-byte pieces per row, LDS bytes per row
   struct Raw { uint4 h; uint2 q[4]; };
-  __device__ static void load(const uint8_t *blk, int q4, Raw &r) {
-    r.h = *reinterpret_cast<const uint4 *>(blk);
-#pragma unroll
-    for (int j = 0; j < 4; j++) r.q[j] = ld8(blk + 16 + 32 * j + 8 * q4);
-  }
-  // the same bytes from a staged copy of the block in LDS (16-byte aligned)
-  __device__ static void load_lds(const uint8_t *blk, int q4, Raw &r) {
+  // the lane's bytes from a staged copy of the block in LDS (16-byte aligned)
+  __device__ static void load_lds(const uint8_t *blk, const uint8_t *, int q4, Raw &r) {
     r.h = *reinterpret_cast<const uint4 *>(blk);
 #pragma unroll
     for (int j = 0; j < 4; j++) r.q[j] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 8 * q4);
@@ -94,10 +90,15 @@ struct MQ4K {
 // 64 hh + 32 (s' & 1) + 8 q4 and qh bytes 128 + 32 hh + 8 q4 (src/Quants.cs:381-392).
 struct MQ6K {
   static constexpr int BYTES = 210, TERMS = 2;
+  // staging: 224 bytes from the dword at or below the block's start (the block and its offset
+  // of 0 or 2 bytes); LDS rows of 240 bytes put the 16 rows' reads in distinct banks
+  static constexpr int SCH = 14, SROW = 240;
   struct Raw { uint32_t l[2][2][3], h[2][3], s, d, sh; };  // aligned dword windows (2-byte-aligned blocks)
-  __device__ static void load(const uint8_t *blk, int q4, Raw &r) {
-    gu32 *a = align4_down(blk);
-    r.sh = misalign4(blk) * 8;
+  // the lane's dword windows from a staged copy in LDS whose first dword is the one at or below
+  // the global block gblk's start; sh = the block's offset in bits (0 or 16)
+  __device__ static void load_lds(const uint8_t *row, const uint8_t *gblk, int q4, Raw &r) {
+    const uint32_t *a = reinterpret_cast<const uint32_t *>(row);
+    r.sh = misalign4(gblk) * 8;
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
 #pragma unroll
@@ -112,10 +113,8 @@ struct MQ6K {
       r.h[hh][1] = a[o + 1];
       r.h[hh][2] = a[o + 2];
     }
-    r.s = a[(192 + 4 * q4) / 4];
     r.d = a[208 / 4];
-    // one extra dword for the scale window when the block is at 2 mod 4
-    r.s = __builtin_amdgcn_alignbit(a[(192 + 4 * q4) / 4 + 1], r.s, r.sh);
+    r.s = __builtin_amdgcn_alignbit(a[(192 + 4 * q4) / 4 + 1], a[(192 + 4 * q4) / 4], r.sh);
   }
   // A run's values 0..15 (lanes q4 < 2) are one scale group and 16..31 (q4 >= 2) the next:
   // column c16 < 8 is token c16 with the first group, c16 >= 8 token c16 - 8 with the second;
@@ -166,29 +165,25 @@ struct MmaArgs {
 // two groups of RPS rounds; after a group's barrier every wave adds the group's terms, in block
 // order, for its share of the (row, token) pairs: the reference's single `sum +=` chain over
 // the whole row.
-// Staged Q4_K weights: a wave reads its block's 16 rows x 144 bytes (per matrix) with three
-// coalesced nontemporal 16-byte loads per lane, one round ahead, into its own LDS area, and the
-// lanes take their operand bytes from there (a wave load covers about seven rows' contiguous
-// bytes, where an operand load touches sixteen rows' lines).
-constexpr int kStgRow = 176;                       // LDS bytes per staged row (reads of the 16 rows in distinct banks)
-constexpr int kStgChunks = 16 * 144 / 16;          // 16-byte pieces of a 16-row block
-constexpr int kStgLoads = (kStgChunks + 63) / 64;  // loads per lane
+// Staged weights: a wave reads its block's 16 rows (per matrix) with coalesced nontemporal
+// 16-byte loads, one round ahead, into its own LDS area, and the lanes take their operand bytes
+// from there. A wave load covers about four to seven rows' contiguous bytes, where an operand
+// load touches sixteen rows' lines: for Q6_K's 2-byte-aligned windows the L1 cache's accesses
+// (TCP_TOTAL_CACHE_ACCESSES) were 694 per block and wave, close to one per cycle.
 
 // FRAG: the operand-order copy (one 512-byte wave load per run); otherwise the tokens' rows.
-// STG: staged weights (Q4_K).
 // The kernel's LDS: the scale slabs, the terms ring of two groups of RPS rounds (MH floats per
 // (row, token) and block: matrices x terms per block), and the staged weights.
-template <int W, int NM, int MH, int RPS, bool STG>
+template <int W, int NM, int MH, int RPS, int SROW>
 struct MmaLds {
   uint32_t slab[W][NM][16 * kSlab];
   float4 terms[2 * RPS][W][MH][32];
-  uint8_t stg[STG ? W : 1][STG ? NM : 1][STG ? 16 * kStgRow : 16];
+  uint8_t stg[W][NM][16 * SROW];
 };
 
 // Tile `tile` of a (every wave of the workgroup calls it: it holds workgroup barriers).
-template <class M, int NM, int W, bool FRAG, bool STG, int RPS, class L>
+template <class M, int NM, int W, bool FRAG, int RPS, class L>
 __device__ __forceinline__ void mma_tile(const MmaArgs &a, const int tile, L &lds) {
-  static_assert(!STG || M::BYTES == 144, "staging is laid out for Q4_K blocks");
   auto &slab = lds.slab;
   auto &terms = lds.terms;
   auto &stg = lds.stg;
@@ -205,14 +200,16 @@ __device__ __forceinline__ void mma_tile(const MmaArgs &a, const int tile, L &ld
   const int dl = q4 * 8 + c16;                                 // D lane among the token columns (c16 < 8)
 
   // staging: piece f = 64 i + lane of a block's 16 rows is row f / 9, bytes 16 (f % 9) ..
-  int soff[kStgLoads], lofs[kStgLoads];
-  bool sok[kStgLoads];
+  // piece f = 64 i + lane is row f / SCH, bytes 16 (f % SCH) .. of the row's staged range
+  constexpr int SCH = M::SCH, SCHUNKS = 16 * M::SCH, SLOADS = (SCHUNKS + 63) / 64;
+  int soff[SLOADS], lofs[SLOADS];
+  bool sok[SLOADS];
 #pragma unroll
-  for (int i = 0; i < kStgLoads; i++) {
-    const int f = 64 * i + lane, r = f / 9, c = f % 9;
-    sok[i] = STG && f < kStgChunks;
+  for (int i = 0; i < SLOADS; i++) {
+    const int f = 64 * i + lane, r = f / SCH, c = f % SCH;
+    sok[i] = f < SCHUNKS;
     soff[i] = (min(tile * 16 + r, a.rows - 1) - tile * 16) * (int)a.row_bytes + 16 * c;  // tile*16 < rows
-    lofs[i] = r * kStgRow + 16 * c;
+    lofs[i] = r * M::SROW + 16 * c;
   }
   const int64_t tbase = (int64_t)tile * 16 * a.row_bytes;
 
@@ -232,44 +229,41 @@ __device__ __forceinline__ void mma_tile(const MmaArgs &a, const int tile, L &ld
     }
   };
   struct Ops {
-    typename M::Raw raw[STG ? 1 : NM];
-    u32x4_t sg[STG ? NM : 1][kStgLoads];
+    u32x4_t sg[NM][SLOADS];
     Xo x;
   };
   auto fetch = [&](int b, Ops &o) {
-    if constexpr (STG) {
 #pragma unroll
-      for (int m = 0; m < NM; m++) {
-        const uint8_t *base = (m ? a.w2 : a.w) + tbase + (int64_t)b * 144;
+    for (int m = 0; m < NM; m++) {
+      const uint8_t *base = (m ? a.w2 : a.w) + tbase + (int64_t)b * M::BYTES;
 #pragma unroll
-        for (int i = 0; i < kStgLoads; i++)
-          if (sok[i]) o.sg[m][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(base + soff[i]));
-      }
-    } else {
-#pragma unroll
-      for (int m = 0; m < NM; m++) M::load(wr[m] + (int64_t)b * M::BYTES, q4, o.raw[m]);
+      for (int i = 0; i < SLOADS; i++)
+        if (sok[i]) {
+          // Q6_K blocks start 2-byte aligned: pieces from the dword at or below the row's block
+          // start (16 c keeps the low bits), dword-aligned loads
+          const uint8_t *p = base + soff[i];
+          if constexpr (M::BYTES % 4 != 0) p -= misalign4(p);
+          o.sg[m][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a4_t *>(p));
+        }
     }
     fetch_x(b, o.x);
   };
+
   // one block's terms into ring slot buf
-  auto body = [&](const Ops &op, int buf) {
-    const Xo &xo = op.x;
-    typename M::Raw sraw[STG ? NM : 1];
-    if constexpr (STG) {
-      // the staged pieces to this wave's LDS area (its previous block's reads are done: one
-      // wave's LDS accesses complete in order), then each lane's operand bytes from there
+  auto body = [&](const Ops &op, const Xo &xo, int buf, int b) {
+    // the staged pieces to this wave's LDS area (its previous block's reads are done: one
+    // wave's LDS accesses complete in order), then each lane's operand bytes from there
 #pragma unroll
-      for (int m = 0; m < NM; m++)
+    for (int m = 0; m < NM; m++)
 #pragma unroll
-        for (int i = 0; i < kStgLoads; i++)
-          if (sok[i]) *reinterpret_cast<u32x4_t *>(&stg[wv][m][lofs[i]]) = op.sg[m][i];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      for (int i = 0; i < SLOADS; i++)
+        if (sok[i]) *reinterpret_cast<u32x4_t *>(&stg[wv][m][lofs[i]]) = op.sg[m][i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    typename M::Raw raw[NM];
 #pragma unroll
-      for (int m = 0; m < NM; m++) M::load_lds(&stg[wv][m][c16 * kStgRow], q4, sraw[m]);
-    }
-    const typename M::Raw *raw = STG ? sraw : op.raw;
+    for (int m = 0; m < NM; m++) M::load_lds(&stg[wv][m][c16 * M::SROW], wr[m] + (int64_t)b * M::BYTES, q4, raw[m]);
 #pragma unroll
     for (int m = 0; m < NM; m++) M::stage(raw[m], q4, &slab[wv][m][c16 * kSlab]);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -366,7 +360,7 @@ __device__ __forceinline__ void mma_tile(const MmaArgs &a, const int tile, L &ld
   auto round = [&](int r, const Ops &cur, Ops &nxt) {
     const int b = r * W + wv;
     fetch(min(b + W, nb - 1), nxt);
-    if (b < nb) body(cur, r % (2 * RPS));
+    if (b < nb) body(cur, cur.x, r % (2 * RPS), b);
     if (r % RPS == RPS - 1 || r + 1 == nr) {  // uniform
       __syncthreads();
       for (int q = r - r % RPS; q <= r; q++) drain(q);
@@ -389,14 +383,23 @@ __device__ __forceinline__ void mma_tile(const MmaArgs &a, const int tile, L &ld
   }
 }
 
-template <class M, int NM, int W, bool FRAG, bool STG>
+// Rounds per barrier: the most of 8, 4, 2, 1 whose ring leaves the workgroup's LDS within
+// 80 KB (two workgroups per CU). For a 70B layer, one barrier per 1, 2, 4 and 8 rounds measured
+// 242, 238, 228 and 250 us (the SwiGLU pair at 8: one workgroup per CU).
+constexpr int rounds_per_barrier(int fixed_bytes, int bytes_per_round) {
+  return fixed_bytes + 8 * bytes_per_round <= 80 * 1024   ? 8
+         : fixed_bytes + 4 * bytes_per_round <= 80 * 1024 ? 4
+         : fixed_bytes + 2 * bytes_per_round <= 80 * 1024 ? 2
+                                                          : 1;
+}
+
+template <class M, int NM, int W, bool FRAG>
 __global__ __launch_bounds__(64 * W) void intmma_kernel(MmaArgs a) {
-  // rounds per barrier: the ring holds two groups of RPS rounds (64 KB for one Q6_K matrix or
-  // 32 KB for the SwiGLU pair, whose workgroups need room for two per CU); 1, 2, 4 and 8
-  // measured 242, 238, 228 and 250 us (the pair at 8: one workgroup per CU) for a 70B layer
-  constexpr int RPS = NM == 2 ? 4 : 8;
-  __shared__ MmaLds<W, NM, NM * M::TERMS, RPS, STG> lds;
-  mma_tile<M, NM, W, FRAG, STG, RPS>(a, blockIdx.x, lds);
+  constexpr int MH = NM * M::TERMS;
+  constexpr int RPS = rounds_per_barrier(sizeof(MmaLds<W, NM, MH, 1, M::SROW>) - 2 * W * MH * 512,
+                                         2 * W * MH * 512);
+  __shared__ MmaLds<W, NM, MH, RPS, M::SROW> lds;
+  mma_tile<M, NM, W, FRAG, RPS>(a, blockIdx.x, lds);
 }
 
 // Several matrices that read the same activations (q, k and v) in one launch: the workgroups
@@ -410,16 +413,16 @@ struct MmaMulti {
 template <int W, bool FRAG>
 __global__ __launch_bounds__(64 * W) void intmma_multi_kernel(MmaMulti mm) {
   constexpr int RPS = 4;  // one workgroup's LDS fits three per CU
-  __shared__ MmaLds<W, 1, 2, RPS, FRAG> lds;
+  __shared__ MmaLds<W, 1, 2, RPS, MQ6K::SROW> lds;
   const int bid = blockIdx.x;  // uniform: the segment and its branch are the workgroup's
   const int i = bid < mm.tile_end[0] ? 0 : bid < mm.tile_end[1] ? 1 : 2;
   const MmaArgs a = i == 0 ? mm.seg[0] : i == 1 ? mm.seg[1] : mm.seg[2];
   const int type = i == 0 ? mm.type[0] : i == 1 ? mm.type[1] : mm.type[2];
   const int tile = bid - (i == 0 ? 0 : i == 1 ? mm.tile_end[0] : mm.tile_end[1]);
   if (type == 12)
-    mma_tile<MQ4K, 1, W, FRAG, FRAG, RPS>(a, tile, lds);
+    mma_tile<MQ4K, 1, W, FRAG, RPS>(a, tile, lds);
   else
-    mma_tile<MQ6K, 1, W, FRAG, false, RPS>(a, tile, lds);
+    mma_tile<MQ6K, 1, W, FRAG, RPS>(a, tile, lds);
 }
 
 bool intmma_supports(int type, int cols, int T, int) {
@@ -433,15 +436,13 @@ int intmma_max_tokens(int type, int cols, int nm) { return intmma_supports(type,
 // unevenly.
 constexpr int kMmaWaves = 4;
 
-// Q4_K with the operand-order activations takes the staged weights.
 template <class M, int NM>
 static hipError_t go(const MmaArgs &a, int grid, hipStream_t st) {
   constexpr int W = kMmaWaves;
-  constexpr bool STG = M::BYTES == 144;
   if (a.qf)
-    hipLaunchKernelGGL((intmma_kernel<M, NM, W, true, STG>), dim3(grid), dim3(64 * W), 0, st, a);
+    hipLaunchKernelGGL((intmma_kernel<M, NM, W, true>), dim3(grid), dim3(64 * W), 0, st, a);
   else
-    hipLaunchKernelGGL((intmma_kernel<M, NM, W, false, false>), dim3(grid), dim3(64 * W), 0, st, a);
+    hipLaunchKernelGGL((intmma_kernel<M, NM, W, false>), dim3(grid), dim3(64 * W), 0, st, a);
   return hipGetLastError();
 }
 
