@@ -65,9 +65,38 @@ static int plan_grid(GemvParams &p, RowsOf rows_of, int nwv, int num_cu) {
   return nwg;
 }
 
+// Codecs whose one-token launches of one matrix set take smaller row groups when the matrices
+// are too small to give each SIMD four waves (the 4096-wide matrices of an 8B layer: o is 512
+// row groups of 8, one wave per SIMD; in 2-row groups 8.4 -> 6.5 us, q/k/v in 4-row groups
+// 9.0 -> 8.0 us). A row's sum does not depend on the grouping, so the bits are the same. Q8_0
+// 4096x4096 measured slower in 2-row groups.
+template <class C>
+inline constexpr bool kSmallGroups = false;
+template <>
+inline constexpr bool kSmallGroups<Q4K> = true;
+template <>
+inline constexpr bool kSmallGroups<Q6K> = true;
+
+template <class C, int TM, int R, int NM>
+static hipError_t launch_r(GemvParams &p, int split, int num_cu, hipStream_t st);
+
 template <class C, int TM, int NM>
 static hipError_t launch_one(GemvParams &p, int split, int num_cu, hipStream_t st) {
   constexpr int R = rows_per_group<C, TM, NM>();
+  if constexpr (TM == 1 && NM == 1 && kSmallGroups<C> && R >= 4) {
+    int passes, nwv;
+    cs_shape(p.cols, &passes, &nwv);
+    int64_t waves = 0;
+    for (int i = 0; i < p.nseg; i++) waves += (int64_t)((p.seg[i].rows + R - 1) / R) * nwv;
+    const int64_t want = (int64_t)num_cu * 16;  // four waves per SIMD
+    if (waves * 4 <= want) return launch_r<C, TM, R / 4, NM>(p, split, num_cu, st);
+    if (waves * 2 <= want) return launch_r<C, TM, R / 2, NM>(p, split, num_cu, st);
+  }
+  return launch_r<C, TM, R, NM>(p, split, num_cu, st);
+}
+
+template <class C, int TM, int R, int NM>
+static hipError_t launch_r(GemvParams &p, int split, int num_cu, hipStream_t st) {
   int passes, nwv;
   cs_shape(p.cols, &passes, &nwv);
   const int nwg = plan_grid(p, [](int) { return R; }, nwv, num_cu);
