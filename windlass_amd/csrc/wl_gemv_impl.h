@@ -218,7 +218,9 @@ __device__ __forceinline__ void cs_finish(const float (&acc)[NM][R][TM], int g, 
 }
 
 // SP: passes whose x slices stay in registers (0: x read per row group; 1 or 2 only for TM 1).
-template <class C, int TM, int R, int NM, int SP, bool WT = false>
+// PIPE (one token, one pass): the next row group's weights are loaded while the current one is
+// computed; the same sums in the same order.
+template <class C, int TM, int R, int NM, int SP, bool WT = false, bool PIPE = false>
 __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int cols, int g0, int gstride,
                                         uint8_t *lds_raw) {
   constexpr int V = NM * R * TM;
@@ -251,6 +253,46 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
   if constexpr (C::NEED_LDS) {
     C::init_lds(*reinterpret_cast<Lds *>(lds_raw));
     __syncthreads();
+  }
+
+  if constexpr (PIPE) {
+    static_assert(TM == 1 && SP == 1, "the pipelined loop is for one token in one pass");
+    // Every load is issued (past the last group it re-reads the last one; a lane past the
+    // row's blocks reads block 0 and adds nothing), so the load counter's waits stay exact: a
+    // conditional load makes the compiler wait for every load in flight.
+    const int b = wv * BPW + bslot;
+    const bool bok = b < nb;
+    const int bl = bok ? b : 0;
+    typename C::Raw ra[NM][R], rb[NM][R];
+    auto group = [&](int g, const typename C::Raw(&raw)[NM][R]) {
+      float acc[NM][R][TM];
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[m][r][0] = 0.f;
+      if (bok) {
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            typename C::W w;
+            C::unpack(raw[m][r], L, lds, w);
+            acc[m][r][0] += C::dot(w, xs0[0]);
+          }
+      }
+      cs_finish<TM, R, NM, WT>(acc, g, gstride, ngroups, st, part, W, io);
+    };
+    if (g0 < ngroups) {
+      cs_load<C, R, NM>(W, g0, bl, L, ra);
+      for (int g = g0; g < ngroups; g += 2 * gstride) {
+        cs_load<C, R, NM>(W, min(g + gstride, ngroups - 1), bl, L, rb);
+        group(g, ra);
+        if (g + gstride >= ngroups) break;  // uniform over the workgroup
+        cs_load<C, R, NM>(W, min(g + 2 * gstride, ngroups - 1), bl, L, ra);
+        group(g + gstride, rb);
+      }
+    }
+    return;
   }
 
   for (int g = g0; g < ngroups; g += gstride) {

@@ -22,17 +22,17 @@ __device__ __forceinline__ int find_seg(const GemvParams &p) {
 
 // split: the segment writes partials; for the SwiGLU pair the up partial follows the gate
 // partial at out + T * ldo.
-template <class C, int TM, int R, int NM, int SP>
+template <class C, int TM, int R, int NM, int SP, bool PIPE = false>
 __device__ __forceinline__ void run_seg(const GemvParams &p, const GemvSeg &s, int split) {
   const CsRows W{s.w, s.w2, s.row_bytes, s.rows};
   float *y2 = (NM == 2 && split) ? s.out + (int64_t)p.T * s.ldo : nullptr;
   const CsIO io{p.x + s.col0, nullptr, p.ldx, s.out, nullptr, s.ldo, p.T, y2, split ? 0 : s.add, s.rs};
-  cs_gemv<C, TM, R, NM, SP>(W, io, p.cols, (int)blockIdx.x - s.wg_begin, s.nwg, wl_dyn_lds);
+  cs_gemv<C, TM, R, NM, SP, false, PIPE>(W, io, p.cols, (int)blockIdx.x - s.wg_begin, s.nwg, wl_dyn_lds);
 }
 
-template <class C, int TM, int R, int NM, int SP>
+template <class C, int TM, int R, int NM, int SP, bool PIPE = false>
 __global__ __launch_bounds__(64 * kMaxWaves) void gemv_kernel(GemvParams p, int split) {
-  run_seg<C, TM, R, NM, SP>(p, p.seg[find_seg(p)], split);
+  run_seg<C, TM, R, NM, SP, PIPE>(p, p.seg[find_seg(p)], split);
 }
 
 // Rows per group: V = NM*R*TM partials per lane go through the exchange butterfly.
@@ -80,9 +80,28 @@ inline constexpr bool kSmallGroups<Q6K> = true;
 template <class C, int TM, int R, int NM>
 static hipError_t launch_r(GemvParams &p, int split, int num_cu, hipStream_t st);
 
+// Q6_K single matrices of one token (the 70B down projection's chunks) in 2-row groups with the
+// next group's weights loaded during the current one's work: 47.5 -> 45.9 us for the 70B down
+// (the same loop for Q4_K, the q/k/v launch or larger groups was slower).
+template <class C>
+inline constexpr bool kPipelined = false;
+template <>
+inline constexpr bool kPipelined<Q6K> = true;
+
 template <class C, int TM, int NM>
 static hipError_t launch_one(GemvParams &p, int split, int num_cu, hipStream_t st) {
   constexpr int R = rows_per_group<C, TM, NM>();
+  if constexpr (kPipelined<C> && TM == 1 && NM == 1) {
+    int passes, nwv;
+    cs_shape(p.cols, &passes, &nwv);
+    if (passes == 1) {
+      const int nwg = plan_grid(p, [](int) { return 2; }, nwv, num_cu);
+      if (nwg == 0) return hipSuccess;
+      const size_t smem = cs_lds_bytes<C, 1, 2, 1>(nwv);
+      hipLaunchKernelGGL((gemv_kernel<C, 1, 2, 1, 1, true>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
+      return hipGetLastError();
+    }
+  }
   if constexpr (TM == 1 && NM == 1 && kSmallGroups<C> && R >= 4) {
     int passes, nwv;
     cs_shape(p.cols, &passes, &nwv);
