@@ -123,8 +123,11 @@ __device__ __forceinline__ uint32_t misalign4(const void *p) {
 typedef const __attribute__((address_space(1))) uint32_t gu32;
 
 // The dword-aligned address at or below p, in the global address space.
+// (Clearing the low bits is one VALU instruction on the address's low dword; subtracting the
+// misalignment was a 64-bit subtraction with borrow. 70B down 46.9 -> 45.7 us, Q8_0 4096x4096
+// 7.63 -> 7.38 us.)
 __device__ __forceinline__ gu32 *align4_down(const uint8_t *p) {
-  return (gu32 *)(p - misalign4(p));
+  return (gu32 *)(reinterpret_cast<uintptr_t>(p) & ~(uintptr_t)3);
 }
 
 // One weight dword (nontemporal as ldw16).
