@@ -64,6 +64,23 @@ def test_batch_rows_equal_single_token_bitwise(ctx, t, cols):
     w.free()
 
 
+@pytest.mark.parametrize("t", [GgmlType.Q4_K, GgmlType.Q6_K], ids=lambda t: t.name)
+@pytest.mark.parametrize("rows", [1, 2, 3, 17])
+@pytest.mark.parametrize("cols", [4096, 28672])
+def test_few_rows_one_token_equals_batch_rows(ctx, t, rows, cols):
+    # a handful of rows: the one-token launch takes its smallest row groups (and, for one Q6_K
+    # matrix, the loop that loads the next group early, re-reading the last group at the end);
+    # each token alone still gives the batch's bits, and the tolerance bar holds
+    data = blocks(t, rows, cols, seed=rows * 7 + cols)
+    w = ctx.upload(t, data, rows, cols)
+    x = np.random.default_rng(rows).standard_normal((3, cols), dtype=np.float32)
+    y1 = np.stack([Transformer.MatMul(w, x[i:i + 1], 1)[0] for i in range(3)])
+    yb = Transformer.MatMul(w, x, 3)
+    assert np.array_equal(yb.view(np.uint32), y1.view(np.uint32))
+    tol_check(y1, x, decoded(t, data, rows, cols), what="gpu %s %dx%d" % (t.name, rows, cols))
+    w.free()
+
+
 def test_more_than_eight_tokens(ctx):
     # T > 8 runs the bf16 MFMA GEMM: within the stated bf16 bound of the fp32 result
     t, rows, cols, T = GgmlType.Q4_K, 64, 1024, 19
