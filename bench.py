@@ -125,20 +125,24 @@ def main():
     out = torch.empty((T, HIDDEN), device=dev)
     stream = torch.cuda.ExternalStream(ctx.stream, device=dev)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    # every call's arguments built once, outside the timed loop: the host only enqueues
+    hc, px, pq, po, ph, pout = ctx.handle, P(x), P(yq), P(yo), P(h), P(out)
+    ys = (ctypes.c_void_p * 3)(yq.data_ptr(), yk.data_ptr(), yv.data_ptr())
+    for ly in layers:
+        ly.qkv = (ctypes.c_void_p * 3)(ly.w["q"].handle.value, ly.w["k"].handle.value, ly.w["v"].handle.value)
+    mm_multi, mm, gu = L.wl_matmul_multi_dev, L.wl_matmul_dev, L.wl_gate_up_dev
 
     def qkv(ly):
-        ws = (ctypes.c_void_p * 3)(ly.w["q"].handle.value, ly.w["k"].handle.value, ly.w["v"].handle.value)
-        ys = (ctypes.c_void_p * 3)(yq.data_ptr(), yk.data_ptr(), yv.data_ptr())
-        check(L.wl_matmul_multi_dev(ctx.handle, 3, ws, P(x), T, ys))
+        check(mm_multi(hc, 3, ly.qkv, px, T, ys))
 
     def o_proj(ly):   # the attention output stands in as yq (attention is not on this path)
-        check(L.wl_matmul_dev(ctx.handle, ly.w["o"].handle, -1, P(yq), T, P(yo)))
+        check(mm(hc, ly.w["o"].handle, -1, pq, T, po))
 
     def gate_up(ly):
-        check(L.wl_gate_up_dev(ctx.handle, ly.w["gate"].handle, ly.w["up"].handle, -1, P(yo), T, P(h)))
+        check(gu(hc, ly.w["gate"].handle, ly.w["up"].handle, -1, po, T, ph))
 
     def down(ly):
-        check(L.wl_matmul_dev(ctx.handle, ly.w["down"].handle, -1, P(h), T, P(out)))
+        check(mm(hc, ly.w["down"].handle, -1, ph, T, pout))
 
     def step(i):
         ly = layers[i % len(layers)]
@@ -336,6 +340,25 @@ def gemv_cpu(mats, host, T, budget_s, what):
                       % (what, reps, thr)}
 
 
+def intdot_cpu(mats, host, T, budget_s, what):
+    """The oracle's integer branch of Transformer.MatMul (FastMath.Quantize per token, then
+    FastMath.IntDot per row and token) over every matrix of a workload, best of repeated passes."""
+    oracle = _oracle()
+    rng = np.random.default_rng(98)
+    xs = {c: rng.standard_normal((T, c), dtype=np.float32) for _, _, _, c in mats}
+    thr = cpu_threads()
+
+    def one():
+        for n, t, r, c in mats:
+            oracle.int_matmul(t, host[n], r, c, xs[c], threads=thr)
+    best, reps = best_of(one, budget_s)
+    b = gemv_bytes(mats, T)
+    return {"value": round(b / best / 1e9, 3), "unit": "GB/s", "cores": thr, "kind": "port",
+            "ms": round(best * 1e3, 3),
+            "sample": "%s, best of %d passes, C restatement of Transformer.MatMul's integer branch "
+                      "(FastMath.Quantize + IntDot, -O2 scalar), %d threads" % (what, reps, thr)}
+
+
 def run_workloads(ctx, L, stream, layers, host70, only):
     """The other measured workloads (GPU legs), each with algorithmic bytes or flops, µs per
     launch set, achieved rate and fraction of peak. Returns the results and the CPU-baseline
@@ -452,6 +475,8 @@ def run_workloads(ctx, L, stream, layers, host70, only):
         e["tokens_per_s_per_layer"] = round(8 / (ms * 1e-3), 1)
         out["llama70b_q4km_layer_T8_intdot"] = dict(e, workload="Llama-3.3-70B Q4_K_M layer, 8 tokens, integer-dot "
                                                                 "path (Q8_K activations, v_mfma_i32_16x16x32_i8)")
+        cpu.append(("llama70b_q4km_layer_T8_intdot",
+                    lambda: intdot_cpu(LAYER, host70, 8, 3.0, "70B layer (7 GEMVs) at 8 tokens, integer dot")))
 
     for key, t, rows, cols in (("prefill_512_q4k_28672x8192", Q4_K, 28672, 8192),
                                ("prefill_512_q6k_8192x28672", Q6_K, 8192, 28672)):
@@ -520,6 +545,8 @@ def run_workloads(ctx, L, stream, layers, host70, only):
             w.free()
         cpu.append(("%s_T1" % key, lambda h=host, t=t: gemv_cpu(
             [("w", t, 8192, 28672)], {"w": h}, 1, 1.5, "8192 x 28672 at batch 1 (decode + Block)")))
+        cpu.append(("%s_T8" % key, lambda h=host, t=t: gemv_cpu(
+            [("w", t, 8192, 28672)], {"w": h}, 8, 2.0, "8192 x 28672 at 8 tokens (decode + Block)")))
 
     if want("qwen3moe_experts"):
         ne, k, embd, ff = 128, 8, 2048, 768

@@ -52,6 +52,18 @@ extern "C" {
 #define WL_TYPE_IQ2_S 22
 #define WL_TYPE_IQ4_XS 23
 #define WL_TYPE_BF16 30
+/* Ids the file format lays out (wl_type_layout) that no GPU path decodes: wl_upload refuses them. */
+#define WL_TYPE_Q8_1 9
+#define WL_TYPE_Q8_K 15
+#define WL_TYPE_IQ2_XS 17
+#define WL_TYPE_IQ3_XXS 18
+#define WL_TYPE_IQ1_S 19
+#define WL_TYPE_I8 24
+#define WL_TYPE_I16 25
+#define WL_TYPE_I32 26
+#define WL_TYPE_I64 27
+#define WL_TYPE_F64 28
+#define WL_TYPE_IQ1_M 29
 
 typedef struct wl_ctx wl_ctx;       /* one per model: a HIP stream plus scratch buffers */
 typedef struct wl_weight wl_weight; /* raw GGUF blocks of one tensor in HBM (WeightView, src/LayerStream.cs:15-35) */
@@ -89,7 +101,10 @@ void wl_destroy(wl_ctx *ctx);
 /* The hipStream_t the context launches on, as void*. */
 void *wl_stream(wl_ctx *ctx);
 
-/* Waits for every launch queued on the context. */
+/* Waits for every launch queued on the context. Also the point where asynchronous failures of
+ * those launches are reported: WL_E_DEVICE when a one-launch MoE (wl_moe_ffn_dev, the MoE layers
+ * of wl_layer_dev / wl_layer_batch_dev) gave up one of its bounded waits since the last
+ * synchronizing call on this context (its output is wrong). Each failure is reported once. */
 int wl_sync(wl_ctx *ctx);
 
 /* Copies raw GGUF blocks unchanged to HBM: LayerStream.Bind's view of one tensor
@@ -159,7 +174,9 @@ int wl_route(wl_ctx *ctx, const float *logits, int32_t T, int32_t n, int32_t k, 
 /* MoeFfn (src/Transformer.cs:259-294) given the router logits [T][n_expert]: route, run each
  * chosen expert's SwiGLU on its tokens, weighted sum. gate/up/down are stacked expert tensors
  * ([n_expert][ff][embd], [n_expert][ff][embd], [n_expert][embd][ff]). expert_runs (may be
- * NULL) receives the number of distinct experts computed (Transformer.ExpertRuns, :27). */
+ * NULL) receives the number of distinct experts computed (Transformer.ExpertRuns, :27).
+ * Synchronous: WL_E_DEVICE when a one-launch MoE on this context gave up one of its bounded
+ * waits since the last synchronizing call (as wl_sync reports it). */
 int wl_moe_ffn(wl_ctx *ctx, const float *logits, int32_t k, int32_t renorm,
                const wl_weight *gate_exps, const wl_weight *up_exps, const wl_weight *down_exps,
                const float *x, int32_t T, float *out, int32_t *expert_runs);
@@ -219,7 +236,15 @@ int wl_dequant_dev(wl_ctx *ctx, const wl_weight *w, int64_t row0, int64_t nrows,
  * (route+plan, gate/up, down, combine). Both give the same bits. */
 int wl_set_moe_one_launch(wl_ctx *ctx, int on);
 
-/* wl_moe_ffn on device buffers (logits, x, out in HBM). */
+/* Fault injection for the one-launch MoE's error path (no counterpart in the reference): the
+ * polls each of its bounded waits makes before it gives up (sets the context's sticky status,
+ * reported by the next wl_sync or wl_moe_ffn) and goes on. 0 gives up at once, so the status is
+ * set on every such launch while every kernel still exits normally; polls < 0 restores the
+ * default. */
+int wl_debug_moe_patience(wl_ctx *ctx, int32_t polls);
+
+/* wl_moe_ffn on device buffers (logits, x, out in HBM). Asynchronous: a one-launch failure is
+ * reported by the next wl_sync. */
 int wl_moe_ffn_dev(wl_ctx *ctx, const float *d_logits, int32_t k, int32_t renorm,
                    const wl_weight *gate_exps, const wl_weight *up_exps,
                    const wl_weight *down_exps, const float *d_x, int32_t T, float *d_out);

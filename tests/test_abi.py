@@ -85,9 +85,15 @@ def test_type_queries_match_reference_layouts():
         assert L.wl_can_decode(t) == 1
     for t in want:
         assert L.wl_can_matmul(t) == 1
-    # Q8_1, Q8_K (activation formats) and the I-quants whose grids have no source here
-    for t in (9, 15, 17, 18, 19, 29):
+    # laid out by the format but not multiplied here: Q8_1, Q8_K (activation formats), the
+    # I-quants whose grids have no source here, integer and f64 tensors
+    other = {9: (32, 36), 15: (256, 292), 17: (256, 74), 18: (256, 98), 19: (256, 50), 29: (256, 56),
+             24: (1, 1), 25: (1, 2), 26: (1, 4), 27: (1, 8), 28: (1, 8)}
+    for t, lay in other.items():
+        assert windlass_amd.layout(t) == lay
         assert L.wl_can_decode(t) == 0 and L.wl_can_matmul(t) == 0
+    for t in (4, 5, 31, 99, -1):
+        assert L.wl_type_layout(t, None, None) == 0
     assert windlass_amd.Quants.CanDecode(windlass_amd.GgmlType.Q4_K)
     assert L.wl_version() >= 100
 

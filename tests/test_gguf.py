@@ -101,6 +101,31 @@ def test_unknown_tensor_type_is_not_supported(tmp_path):
         GgufModelFile.Open(p)
 
 
+# GgmlTypes.TryGetLayout (src/Gguf.cs:30-66) ids the GPU path does not multiply
+OTHER_LAYOUTS = {9: (32, 36), 15: (256, 292), 17: (256, 74), 18: (256, 98), 19: (256, 50), 29: (256, 56),
+                 24: (1, 1), 25: (1, 2), 26: (1, 4), 27: (1, 8), 28: (1, 8)}
+
+
+@pytest.mark.parametrize("tid", sorted(OTHER_LAYOUTS))
+def test_laid_out_types_are_read_and_refused_on_upload(tmp_path, tid):
+    # the reader opens a file holding any type the format lays out (ReadHeader, src/Gguf.cs:187-196):
+    # its tensor's size follows the layout; only uploading it is refused
+    from windlass_amd.backend import WeightView
+    be, bb = OTHER_LAYOUTS[tid]
+    cols, rows = 256, 2
+    data = np.arange(rows * cols // be * bb, dtype=np.uint8)
+    p = tmp_path / "o.gguf"
+    write_gguf(p, META[:1], [("w", [cols, rows], tid, data), ("a.weight", [256, 2], int(GgmlType.Q4_K),
+                                                            np.zeros(288, np.uint8))])
+    g = GgufModelFile.Open(p)
+    w, a = g.Tensors
+    assert int(w.Type) == tid and not isinstance(w.Type, GgmlType)
+    assert (w.Rows, w.Cols, w.SizeBytes) == (rows, cols, data.size)
+    assert np.array_equal(g.data(w), data) and a.Type == GgmlType.Q4_K
+    with pytest.raises(NotSupportedError):
+        WeightView(None, w.Type, g.data(w), rows, cols)
+
+
 def test_split_model_parts(tmp_path):
     rng = np.random.default_rng(3)
     ts = _tensors(rng)

@@ -243,3 +243,50 @@ def test_qwen3moe_experts(ctx, T):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     for w in (wg, wu, wd):
         w.free()
+
+
+def silu_f32(g, u):
+    """g / (1 + exp(-g)) * u in float32 with the exponential in double (src/Transformer.cs:247),
+    as the kernels' epilogue computes it."""
+    g, u = np.asarray(g, np.float32), np.asarray(u, np.float32)
+    with np.errstate(over="ignore"):
+        e = np.exp(-g.astype(np.float64)).astype(np.float32)
+    return (g / (np.float32(1) + e)) * u
+
+
+def test_int_dot_layer_70b_T8(ctx):
+    """The integer-dot leg of the layer benchmark (--int-dot, 8 tokens) through the launches it
+    times: q/k/v in one wl_matmul_multi_dev call (8192/1024/1024 x 8192 on the int8 matrix cores),
+    o, the gate/up pair with SiLU (28672 x 8192) and down (8192 x 28672, Q6_K). Every product is
+    FastMath.IntDot's bits over the whole matrix (oracle.int_matmul); h is silu(g) * u on those
+    bits (its exponential in double may round differently in the last place of a float in rare
+    cases: at most 1 ulp, and rare)."""
+    run = LayerRun(ctx, LLAMA70B, seed=0x57494E44 + 77)
+    T = 8
+    rng = np.random.default_rng(0x1D07)
+    x = rng.standard_normal((T, 8192), dtype=np.float32)
+    xo = rng.standard_normal((T, 8192), dtype=np.float32)
+    xd = rng.standard_normal((T, 28672), dtype=np.float32)
+    ctx.IntDot = True
+    try:
+        qkv = run.qkv(x)
+        yo = run.single("o", xo)
+        h = run.gate_up(x)
+        yd = run.single("down", xd)
+    finally:
+        ctx.IntDot = False
+    try:
+        for n, y, xx in (("q", qkv[0], x), ("k", qkv[1], x), ("v", qkv[2], x), ("o", yo, xo), ("down", yd, xd)):
+            t, r, c = run.shape[n]
+            print("int-dot %s: %d x %d %s" % (n, r, c, t.name), flush=True)
+            want = oracle.int_matmul(t, run.host[n], r, c, xx)
+            assert same_bits(y, want), "%s: %d of %d differ" % (n, int((y != want).sum()), y.size)
+        t, r, c = run.shape["gate"]
+        g = oracle.int_matmul(t, run.host["gate"], r, c, x)
+        u = oracle.int_matmul(t, run.host["up"], r, c, x)
+        want = silu_f32(g, u)
+        hb, wb = h.view(np.int32).astype(np.int64), want.view(np.int32).astype(np.int64)
+        off = np.abs(hb - wb)
+        assert off.max() <= 1 and int((off > 0).sum()) <= 8, (int(off.max()), int((off > 0).sum()))
+    finally:
+        run.free()

@@ -475,3 +475,25 @@ def test_gpu_moe_gguf_file_greedy_tokens_match_cpu(gpu, key, tmp_path):
     for w in weights.values():
         w.free()
     assert got == want, "%s: greedy tokens %s, CPU backend %s" % (key, got, want)
+
+
+@pytest.mark.gpu
+def test_gpu_moe_wait_given_up_surfaces_in_the_device_forward(gpu):
+    """A one-launch MoE layer whose bounded wait gives up (forced from the host: no patience)
+    fails the device forward at its next sync with BackendError, once; with the default patience
+    the same model again gives the CPU backend's greedy tokens."""
+    from windlass_amd._lib import BackendError
+    key = "moe-qwen2moe-q4_K-e8k2"
+    want, _ = Model(key, oracle_matmul).greedy(PROBE, 4, chunk=8)
+    dm, weights = device_model(gpu, key)
+    gpu.debug_moe_patience(0)
+    try:
+        with pytest.raises(BackendError, match="gave up"):
+            dm.greedy(PROBE, 4, chunk=8)
+        gpu.sync()
+    finally:
+        gpu.debug_moe_patience(-1)
+    got = dm.greedy(PROBE, 4, chunk=8)
+    for w in weights.values():
+        w.free()
+    assert got == want, (got, want)

@@ -66,3 +66,35 @@ def test_noalloc_refuses_more_scratch_than_it_has():
         ctx.sync()
         assert float(dy.abs().sum()) == 0.0   # nothing ran
         w.free()
+
+
+@pytest.mark.parametrize("case", [CASES[1], CASES[2], CASES[3], CASES[4]], ids=["k_chunks", "down_T1", "gemm", "intdot"])
+def test_noalloc_allocates_nothing_on_a_fresh_context(case):
+    # With the next device allocation armed to fail, the allocation-free entry runs first on a
+    # fresh context (no scratch slot grown yet) and succeeds; the armed failure is then still
+    # pending (the next ordinary allocation takes it), so the entry allocated nothing.
+    from windlass_amd._lib import BackendError
+    t, rows, cols, T, intdot = case
+    L = load()
+    with Context(0) as ctx:
+        ctx.IntDot = intdot
+        data = blocks(t, rows, cols, seed=rows + cols + T)
+        w = ctx.upload(t, data, rows, cols)
+        x = np.random.default_rng(T).standard_normal((T, cols), dtype=np.float32)
+        dx = torch.from_numpy(x).to("cuda:0")
+        yb = torch.full((T, rows), np.nan, device="cuda:0")
+        ya = torch.full((T, rows), np.nan, device="cuda:0")
+        torch.cuda.synchronize()
+        check(L.wl_debug_fail_alloc(1))
+        try:
+            check(L.wl_matmul_dev_noalloc(ctx.handle, w.handle, -1, _p(dx), T, _p(yb)))
+            ctx.sync()
+            with pytest.raises(BackendError):
+                ctx.upload(t, data[:w.RowBytes], 1, cols)
+        finally:
+            check(L.wl_debug_fail_alloc(0))
+        check(L.wl_matmul_dev(ctx.handle, w.handle, -1, _p(dx), T, _p(ya)))
+        ctx.sync()
+        a, b = ya.cpu().numpy(), yb.cpu().numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        w.free()

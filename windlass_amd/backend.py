@@ -155,6 +155,11 @@ class Context:
         check(self._lib.wl_set_moe_one_launch(self.handle, int(bool(on))))
         self._moe_one = bool(on)
 
+    def debug_moe_patience(self, polls):
+        """Fault injection: the polls of the one-launch MoE's bounded waits (0: each gives up at
+        once, and the next sync raises BackendError); a negative value restores the default."""
+        check(self._lib.wl_debug_moe_patience(self.handle, int(polls)))
+
     def upload(self, t, blocks, rows, cols, experts=1, name="weight"):
         """Raw GGUF blocks to HBM, unchanged (LayerStream.Bind, src/LayerStream.cs:182-203)."""
         return WeightView(self, t, blocks, rows, cols, experts, name)

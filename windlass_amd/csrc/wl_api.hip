@@ -63,6 +63,8 @@ struct wl_ctx {
   int int_dot;  // Transformer.IntDot (src/Transformer.cs:23)
   int moe_chain;  // wl_set_moe_one_launch(0): the MoE entries always run the launch chain
   unsigned moe_launches;  // one-launch MoE launches so far (their counter sets alternate)
+  bool moe_unchecked;     // one-launch MoE launches since the err word was last read
+  int moe_spin = wl::MOE_SPIN;  // polls of the one-launch MoE's bounded waits
   // growable scratch (device)
   void *buf[S_COUNT];
   size_t cap[S_COUNT];
@@ -142,6 +144,19 @@ extern "C" int wl_type_layout(int t, int *be, int *bb) {
     case WL_TYPE_IQ3_S: e = 256; b = 110; break;
     case WL_TYPE_IQ2_S: e = 256; b = 82; break;
     case WL_TYPE_IQ4_XS: e = 256; b = 136; break;
+    // known to the file format but not multiplied here (activation formats, integer and f64
+    // tensors, the I-quants whose grids have no source provenance): a reader can still lay out
+    // their tensors; wl_upload refuses them
+    case WL_TYPE_Q8_1: e = 32; b = 36; break;
+    case WL_TYPE_Q8_K: e = 256; b = 292; break;
+    case WL_TYPE_IQ2_XS: e = 256; b = 74; break;
+    case WL_TYPE_IQ3_XXS: e = 256; b = 98; break;
+    case WL_TYPE_IQ1_S: e = 256; b = 50; break;
+    case WL_TYPE_IQ1_M: e = 256; b = 56; break;
+    case WL_TYPE_I8: e = 1; b = 1; break;
+    case WL_TYPE_I16: e = 1; b = 2; break;
+    case WL_TYPE_I32: e = 1; b = 4; break;
+    case WL_TYPE_I64: case WL_TYPE_F64: e = 1; b = 8; break;
   }
   if (be) *be = e;
   if (bb) *bb = b;
@@ -283,10 +298,28 @@ extern "C" void wl_destroy(wl_ctx *c) {
 
 extern "C" void *wl_stream(wl_ctx *c) { return c ? (void *)c->stream : nullptr; }
 
+// After the stream has drained: the one-launch MoE's sticky err word, set when one of its
+// bounded waits ran out (that launch's output is then wrong). Read once per run of such launches
+// and cleared, so each failure is reported once, by the first synchronizing call after it.
+static int moe_status(wl_ctx *c) {
+  if (!c->moe_unchecked || !c->buf[S_MSYNC]) return WL_OK;
+  c->moe_unchecked = false;
+  unsigned err = 0;
+  wl::MoeSync *sy = (wl::MoeSync *)c->buf[S_MSYNC];
+  WL_HIP(hipMemcpyAsync(&err, &sy->err[0], sizeof(err), hipMemcpyDeviceToHost, c->stream), "copy moe status");
+  WL_HIP(hipStreamSynchronize(c->stream), "moe status");
+  if (!err) return WL_OK;
+  static const unsigned zero = 0;
+  WL_HIP(hipMemcpyAsync(&sy->err[0], &zero, sizeof(zero), hipMemcpyHostToDevice, c->stream), "clear moe status");
+  WL_HIP(hipStreamSynchronize(c->stream), "clear moe status");
+  return fail(WL_E_DEVICE, "moe: a workgroup of the one-launch MoE gave up waiting for its inputs; that call's "
+                           "output is wrong");
+}
+
 extern "C" int wl_sync(wl_ctx *c) {
   if (!c) return fail(WL_E_ARG, "context is null");
   WL_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-  return WL_OK;
+  return moe_status(c);
 }
 
 // F32, F16 and BF16 rows have one-value blocks in GGUF, but the GPU kernels read them in runs
@@ -887,8 +920,16 @@ static int moe_dev(wl_ctx *c, const float *d_logits, int32_t k, int32_t renorm, 
     m.qx = wl::qacts_at(b + s.qx, Tc, embd, wl::intdot_needs_k(g->type) ? 1 : 0);
     m.qh = wl::qacts_at(b + s.qh, Tc * k, ff, wl::intdot_needs_k(d->type) ? 1 : 0);
     m.sync = c->moe_chain ? nullptr : (wl::MoeSync *)c->buf[S_MSYNC];
-    m.parity = (int)(c->moe_launches++ & 1);
+    m.parity = (int)(c->moe_launches & 1);
+    m.spin = c->moe_spin;
+    // only a one-launch launch uses a counter set (and clears the other for the next one), so
+    // only it moves the parity; a chain launch in between leaves the sets as they are
+    const bool one = wl::moe_uses_one_launch(m);
     WL_HIP(wl::moe_launch(m, c->num_cu, c->stream), "moe launch");
+    if (one) {
+      c->moe_launches++;
+      c->moe_unchecked = true;
+    }
   }
   return WL_OK;
 }
@@ -928,16 +969,15 @@ extern "C" int wl_moe_ffn(wl_ctx *c, const float *logits, int32_t k, int32_t ren
     }
   }
   WL_HIP(hipMemcpyAsync(out, c->buf[S_OUT], xb, hipMemcpyDeviceToHost, c->stream), "copy out");
-  unsigned err = 0;
-  wl::MoeSync *sy = (wl::MoeSync *)c->buf[S_MSYNC];
-  WL_HIP(hipMemcpyAsync(&err, &sy->err[0], sizeof(err), hipMemcpyDeviceToHost, c->stream), "copy moe status");
   WL_HIP(hipStreamSynchronize(c->stream), "moe");
-  if (err) {
-    WL_HIP(hipMemsetAsync(&sy->err[0], 0, sizeof(err), c->stream), "clear moe status");
-    WL_HIP(hipStreamSynchronize(c->stream), "moe");
-    return fail(WL_E_DEVICE, "moe: a workgroup of the one-launch MoE gave up waiting for its inputs");
-  }
+  if ((rc = moe_status(c))) return rc;
   if (expert_runs) *expert_runs = runs;
+  return WL_OK;
+}
+
+extern "C" int wl_debug_moe_patience(wl_ctx *c, int32_t polls) {
+  if (!c) return fail(WL_E_ARG, "wl_debug_moe_patience: null context");
+  c->moe_spin = polls < 0 ? wl::MOE_SPIN : polls;
   return WL_OK;
 }
 

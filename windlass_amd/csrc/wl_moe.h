@@ -74,14 +74,22 @@ struct MoeLaunch {
   int gu_int, d_int;
   QActsDev qx, qh;
   // counters of the one-launch path (zeroed once when allocated), or null for the launch chain;
-  // parity: this launch's set (alternates between launches)
+  // parity: this launch's set (alternates between one-launch launches); spin: polls a bounded
+  // wait makes before it gives up and sets the sticky err word
   MoeSync *sync;
   int parity;
+  int spin;
 };
+
+// Polls of the one-launch MoE's bounded waits (each poll sleeps about 64 clocks).
+constexpr int MOE_SPIN = 1 << 18;
 
 bool moe_supports(int type);
 hipError_t route_launch(const float *logits, int T, int n, int k, int renorm, int *sel, float *wts, float *prob,
                         hipStream_t st);
+// Whether moe_launch runs m as the one launch (and so uses m.sync's set m.parity and clears
+// the other set for the next one-launch launch), rather than the launch chain.
+bool moe_uses_one_launch(const MoeLaunch &m);
 hipError_t moe_launch(const MoeLaunch &m, int num_cu, hipStream_t st);
 // Zeroes a MoeSync once after its allocation (a kernel, so it may sit in a captured stream).
 hipError_t moe_sync_init(MoeSync *s, hipStream_t st);

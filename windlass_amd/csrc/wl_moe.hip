@@ -328,7 +328,7 @@ __global__ void combine_kernel(const MoePlan *__restrict__ plan, const float *__
 // workgroup, as the launch chain runs these shapes: the same bits. h crosses workgroups: it is
 // stored at agent scope (written through to the point of coherence), and its readers acquire
 // once per CU after the barrier (the polling wave's acquire; the others follow it through the
-// workgroup barrier). Every wait is bounded (kMoeSpin polls); one that runs out sets `err`.
+// workgroup barrier). Every wait is bounded (a.spin polls); one that runs out sets `err`.
 struct MoeFusedArgs {
   const float *logits;
   int T, ne, k, renorm;
@@ -339,16 +339,15 @@ struct MoeFusedArgs {
   const float *x;
   float *h, *yd, *out;
   MoeSync *sync;
-  int parity, max_slots;
+  int parity, max_slots, spin;
 };
 
-constexpr int kMoeSpin = 1 << 18;
 constexpr int kMoeWaves = 8;
 
 // Polls *p until it reaches v, then acquires (one cache invalidation, not one per poll). False
-// when the patience runs out (err set).
-__device__ __forceinline__ bool moe_wait_ge(unsigned *p, unsigned v, MoeSync *sy) {
-  for (int i = 0; i < kMoeSpin; i++) {
+// when the patience (spin polls) runs out (err set).
+__device__ __forceinline__ bool moe_wait_ge(unsigned *p, unsigned v, MoeSync *sy, int spin) {
+  for (int i = 0; i < spin; i++) {
     if (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= v) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       return true;
@@ -359,11 +358,10 @@ __device__ __forceinline__ bool moe_wait_ge(unsigned *p, unsigned v, MoeSync *sy
   return false;
 }
 
-// One atomic add by the wave's lane 0 once the wave's stores have completed (the
-// cross-workgroup ones are agent-scope, so completion is visibility); the old value goes to
-// every lane of the wave.
+// One atomic add by the wave's lane 0; the old value goes to every lane of the wave. The
+// caller has made the workgroup's stores visible at agent scope first (every wave's agent-scope
+// release fence before the workgroup barrier that precedes the arrival).
 __device__ __forceinline__ unsigned moe_arrive(unsigned *p) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   unsigned old = 0;
   if ((threadIdx.x & 63) == 0) old = atomicAdd(p, 1u);
   return __builtin_amdgcn_readfirstlane(old);
@@ -585,13 +583,16 @@ __global__ __launch_bounds__(64 * kMoeWaves) void moe_fused_kernel(MoeFusedArgs 
       touch = *reinterpret_cast<const uint32_t *>(row + (off & ~(int64_t)3));
     }
   }
+  // every wave's h stores complete at agent scope (the fence waits for them) before the
+  // workgroup barrier, so wave 0's arrival below follows all of them
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
   if (wv == 0) {  // grid barrier
     const int nsub = G < MOE_SYNC_SUB ? G : MOE_SYNC_SUB, sub = w % nsub;
     const unsigned per = (unsigned)((G - sub + nsub - 1) / nsub);
     if (moe_arrive(&S.arrive[sub * MOE_SYNC_LINE]) == per - 1 && moe_arrive(&S.top[0]) == (unsigned)nsub - 1)
       __hip_atomic_store(&S.h_ready[lane * MOE_SYNC_LINE], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    moe_wait_ge(&S.h_ready[(w % MOE_SYNC_REP) * MOE_SYNC_LINE], 1u, sy);  // acquires for the CU
+    moe_wait_ge(&S.h_ready[(w % MOE_SYNC_REP) * MOE_SYNC_LINE], 1u, sy, a.spin);  // acquires for the CU
   }
   __syncthreads();
 
@@ -656,7 +657,7 @@ static hipError_t moe_fused_tm(const MoeFusedArgs &a, int num_cu, hipStream_t st
 // Formats and shapes of the one-launch path: gate/up and down in one wave-column each (embd and
 // ff up to 2048, whole 256-blocks), Q4_K/Q6_K experts, up to 64 (token, choice) pairs and 256
 // experts, float products (IntDot keeps the chain).
-static bool moe_fused_applies(const MoeLaunch &m) {
+bool moe_uses_one_launch(const MoeLaunch &m) {
   int pg, wg, pd, wd;
   cs_shape(m.embd, &pg, &wg);
   cs_shape(m.ff, &pd, &wd);
@@ -675,7 +676,7 @@ static hipError_t moe_fused_launch(const MoeLaunch &m, int num_cu, hipStream_t s
   a.gu_stride = (int64_t)m.ff * m.gu_row_bytes; a.d_stride = (int64_t)m.embd * m.d_row_bytes;
   a.ff = m.ff; a.embd = m.embd;
   a.x = m.x; a.h = m.h; a.yd = m.yd; a.out = m.out;
-  a.sync = m.sync; a.parity = m.parity & 1;
+  a.sync = m.sync; a.parity = m.parity & 1; a.spin = m.spin < 0 ? 0 : m.spin;
   a.max_slots = m.T * m.k < m.ne ? m.T * m.k : m.ne;
   if (m.gu_type == 12 && m.d_type == 12) return moe_fused_tm<Q4K, Q4K>(a, num_cu, st);
   if (m.gu_type == 12) return moe_fused_tm<Q4K, Q6K>(a, num_cu, st);
@@ -770,7 +771,7 @@ static hipError_t route_plan_launch(const MoeLaunch &m, hipStream_t st) {
 }
 
 hipError_t moe_launch(const MoeLaunch &m, int num_cu, hipStream_t st) {
-  if (moe_fused_applies(m)) return moe_fused_launch(m, num_cu, st);
+  if (moe_uses_one_launch(m)) return moe_fused_launch(m, num_cu, st);
   hipError_t err = route_plan_launch(m, st);
   if (err != hipSuccess) return err;
   const int max_slots = m.T * m.k < m.ne ? m.T * m.k : m.ne;

@@ -170,14 +170,18 @@ def _parse_part(path, index):
         if size:
             buf.close()
     for t in part.tensors:
-        if t.Type not in GgmlType._value2member_map_:
-            raise NotSupportedError("%s: tensor %s has ggml type %d, which the GPU path cannot read"
-                                    % (path, t.Name, t.Type))
-        t.Type = GgmlType(t.Type)
-        elems, nbytes = layout(t.Type)
+        # every id the format lays out (GgmlTypes.TryGetLayout, src/Gguf.cs:30-66) is read; ids
+        # the GPU path does not multiply stay plain ints and are refused when uploaded
+        try:
+            elems, nbytes = layout(t.Type)
+        except ValueError:
+            raise NotSupportedError("%s: tensor %s uses ggml type %d, which Windlass cannot read yet"
+                                    % (path, t.Name, t.Type)) from None
+        if t.Type in GgmlType._value2member_map_:
+            t.Type = GgmlType(t.Type)
         if t.Cols % elems:
             raise InvalidDataError("%s: tensor %s rows of %d values are not whole %s blocks of %d"
-                                   % (path, t.Name, t.Cols, t.Type.name, elems))
+                                   % (path, t.Name, t.Cols, getattr(t.Type, "name", "type %d" % t.Type), elems))
         t.SizeBytes = t.ElementCount // elems * nbytes
         t.FileOffset += data_start
         if t.FileOffset + t.SizeBytes > size:
@@ -317,7 +321,7 @@ def _vector(ctx, g, t, dev):
         return out
     if t.ElementCount % 32:
         raise NotSupportedError("Vector %s: %d %s values are not whole blocks of 32." % (t.Name, t.ElementCount,
-                                                                                        t.Type.name))
+                                                                                        getattr(t.Type, "name", t.Type)))
     w = ctx.upload(t.Type, g.data(t), 1, t.ElementCount, name=t.Name)
     out = torch.empty(t.ElementCount, device=dev)
     check(load().wl_dequant_dev(ctx.handle, w.handle, 0, 1, ctypes.c_void_p(out.data_ptr())))
