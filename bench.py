@@ -179,7 +179,11 @@ def main():
     layer_bytes = algo_bytes(LAYER, T)
     gbs = layer_bytes / (ms_layer * 1e-3) / 1e9
 
-    # per-launch durations (HIP events on the same stream), rotating copies
+    # per-launch durations (HIP events on the launch stream around 200 back-to-back calls of one
+    # launch, rotating the copies). Events between the calls of a step would add 4-7 us to each
+    # bracketed launch. Alone, the gate/up pair (264 MB per copy) streams from HBM as in a step;
+    # the four copies of q/k/v (198 MB) and o (151 MB) fit in the 256 MB Infinity Cache, so their
+    # figures here are optimistic, and the step time above is what the layer takes.
     def time_launch(fn, reps=200):
         with torch.cuda.stream(stream):
             for i in range(10):
@@ -235,6 +239,8 @@ def main():
         "tokens_per_s_80_layers": round(1000.0 * T / (LAYERS * ms_layer), 2),
         "layer_algorithmic_bytes": layer_bytes,
         "per_launch_ms": {k: round(v, 5) for k, v in per.items()},
+        "per_launch_note": "each launch timed alone over the 4 rotating copies: q/k/v and o then partly hit the "
+                           "256 MB Infinity Cache; ms_per_step is the layer",
         "per_launch_gbs": {k: round(launch_bytes[k] / (per[k] * 1e-3) / 1e9, 1) for k in per},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic,

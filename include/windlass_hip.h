@@ -313,7 +313,19 @@ typedef struct wl_layer_desc {
    * without it the shared expert's weight is 1. NULL ffn_gate_inp: the dense SwiGLU FFN. */
   const wl_weight *ffn_gate_inp, *ffn_gate_shexp, *ffn_up_shexp, *ffn_down_shexp, *ffn_gate_inp_shexp;
   int32_t expert_used, expert_weights_norm;
+  /* OLMo 2's post-norms (ModelConfig.PostNorms, src/Transformer.cs:182,224-230): when both are
+   * set there are no pre-norms (d_attn_norm / d_ffn_norm are not read: q/k/v and the FFN read x
+   * itself), and each branch's output is RMS-normed with these before its residual add. */
+  const float *d_post_attention_norm, *d_post_ffw_norm;
+  /* ModelConfig.QkNormFull (OLMo 2, :192-196): d_q_norm / d_k_norm cover the whole q and k rows
+   * (heads * head_dim, kv_heads * head_dim values) instead of one head. */
+  int32_t qk_norm_full;
 } wl_layer_desc;
+
+/* x[i] *= s for n floats of device memory, in place, stream-ordered: Granite's embedding scale
+ * on the embedding rows (src/Transformer.cs:94,150) and its logit scale, as the reciprocal
+ * 1f / LogitScale, on the logits (:123). */
+int wl_scale_dev(wl_ctx *ctx, float *d_x, int64_t n, float s);
 
 /* Transformer.Layer (src/Transformer.cs:177-232) for T tokens at positions pos0.. of one
  * sequence: x [T][embd] (device) is updated in place and the tokens' keys and values go to

@@ -115,3 +115,34 @@ def tiny_moe_gguf(path, key, context_length=64, omit=None):
             tensors.append((gname, [x.cols, x.rows], int(x.type), x.data))
     write_gguf(path, md, tensors)
     return arch
+
+
+def tiny_arch_gguf(path, key, context_length=512):
+    """A tiny Granite or OLMo 2 model of tiny_arch.build_arch as a GGUF file with TinyArchs' keys
+    (tests/TinyArchs.cs:38-59): rope.dimension_count except for OLMo 2, Granite's scale keys only
+    when set."""
+    from tiny_arch import ROPE_BASE, build_arch, spec
+    from tiny_model import EMBD, EPS, FF, HEADS, KV_HEADS
+    s = spec(key)
+    arch, t, layers = build_arch(key)
+    a = arch + "."
+    md = [("general.architecture", STR, arch), ("general.name", STR, "tiny-" + key),
+          (a + "block_count", U32, layers), (a + "context_length", U32, context_length),
+          (a + "embedding_length", U32, EMBD), (a + "feed_forward_length", U32, FF),
+          (a + "attention.head_count", U32, HEADS), (a + "attention.head_count_kv", U32, KV_HEADS),
+          (a + "attention.layer_norm_rms_epsilon", F32, float(EPS)), (a + "rope.freq_base", F32, ROPE_BASE)]
+    if arch != "olmo2":
+        md.append((a + "rope.dimension_count", U32, EMBD // HEADS))
+    if arch == "granite":
+        for k, v in (("embedding_scale", s["es"]), ("residual_scale", s["rs"]), ("attention.scale", s["as_"]),
+                     ("logit_scale", s["ls"])):
+            if v:
+                md.append((a + k, F32, v))
+    tensors = []
+    for n, x in t.items():
+        if isinstance(x, np.ndarray):
+            tensors.append((n + ".weight", [x.size], 0, np.ascontiguousarray(x, np.float32).view(np.uint8)))
+        elif not (n == "output" and x is t["token_embd"]):
+            tensors.append((n + ".weight", [x.cols, x.rows], int(x.type), x.data))
+    write_gguf(path, md, tensors)
+    return arch

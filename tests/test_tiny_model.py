@@ -131,6 +131,14 @@ def build_any(key):
     the Q6_K tensors of llama-q6_K in layer 0's attn_v and layer 1's ffn_down (Q4_K_M mixes the
     two across layers). Returns (arch, tensors, ModelConfig)."""
     from tiny_model import MOE_SPECS, build, build_moe, moe_norm
+    if key.startswith("arch-"):  # Granite / OLMo 2 (tests/tiny_arch.py)
+        from tiny_arch import arch_config, build_arch
+        from tiny_model import EMBD, EPS, HEADS, KV_HEADS
+        from windlass_amd import ModelConfig
+        arch, t, layers = build_arch(key)
+        c = dict(arch_config(key), layers=layers)
+        return arch, t, ModelConfig(embd=EMBD, heads=HEADS, kv_heads=KV_HEADS, head_dim=EMBD // HEADS,
+                                    eps=float(EPS), **c)
     if key in MOE_SPECS:
         arch, t, layers = build_moe(key)
         layout, _, n, used, _, _, norm_key, _ = MOE_SPECS[key]

@@ -201,17 +201,27 @@ class Model:
     def __init__(self, key, matmul):
         """matmul(name, tensor, x [T][cols] float32) -> y [T][rows] float32."""
         self.key = key
+        # Granite's scales (0: not set) and OLMo 2's post-norms / whole-row q/k norms
+        self.es = self.rs = self.kq = self.ls = 0.0
+        self.post = self.qkfull = False
         if key in MOE_SPECS:
             self.arch, self.t, self.layers = build_moe(key)
             layout, _, _, self.used, _, _, norm_key, _ = MOE_SPECS[key]
             self.renorm = moe_norm(layout, norm_key)
+        elif key.startswith("arch-"):
+            from tiny_arch import arch_config, build_arch
+            self.arch, self.t, self.layers = build_arch(key)
+            c = arch_config(key)
+            self.es, self.rs, self.kq, self.ls = (c["embedding_scale"], c["residual_scale"], c["attention_scale"],
+                                                  c["logit_scale"])
+            self.post, self.qkfull = c["post_norms"], c["qk_norm_full"]
         else:
             self.arch, self.t = build(key)
             self.layers = LAYERS
         self.mm = matmul
         self.hd = EMBD // HEADS
-        self.base = 500000.0 if self.arch == "llama" else 1000000.0
-        self.neox = self.arch != "llama"
+        self.base = 500000.0 if self.arch in ("llama", "granite", "olmo2") else 1000000.0
+        self.neox = self.arch not in ("llama", "granite")
         self.reset()
 
     def reset(self):
@@ -248,7 +258,8 @@ class Model:
         """Attention (src/Transformer.cs:351-393): fp16 keys/values, softmax with a double sum."""
         T = q.shape[0]
         hd, group = self.hd, HEADS // KV_HEADS
-        scale = F32(1) / F32(np.sqrt(hd))
+        # AttentionScale when set (src/Transformer.cs:354)
+        scale = F32(self.kq) if self.kq else F32(1) / F32(np.sqrt(hd))
         K = self.K[l].astype(F32)
         V = self.V[l].astype(F32)
         out = np.zeros((T, HEADS * hd), F32)
@@ -273,9 +284,12 @@ class Model:
         emb = t["token_embd"]
         rb = oracle.row_bytes(emb.type, EMBD)
         x = np.stack([oracle.decode(emb.type, emb.data[tok * rb:(tok + 1) * rb], EMBD) for tok in tokens]).astype(F32)
+        if self.es:  # EmbeddingScale (src/Transformer.cs:94)
+            x = (x * F32(self.es)).astype(F32)
+        rs = F32(self.rs or 1.0)
         for l in range(self.layers):
             p = "blk.%d." % l
-            xn = rms_norm_rows(x, t[p + "attn_norm"])
+            xn = x if self.post else rms_norm_rows(x, t[p + "attn_norm"])
             q = self.mm(p + "attn_q", t[p + "attn_q"], xn)
             k = self.mm(p + "attn_k", t[p + "attn_k"], xn)
             v = self.mm(p + "attn_v", t[p + "attn_v"], xn)
@@ -283,7 +297,10 @@ class Model:
                 q = (q + t[p + "attn_q.bias"]).astype(F32)
                 k = (k + t[p + "attn_k.bias"]).astype(F32)
                 v = (v + t[p + "attn_v.bias"]).astype(F32)
-            if p + "attn_q_norm" in t:
+            if self.qkfull:  # QkNormFull: the whole q and k rows (src/Transformer.cs:192-196)
+                q = rms_norm_rows(q, t[p + "attn_q_norm"])
+                k = rms_norm_rows(k, t[p + "attn_k_norm"])
+            elif p + "attn_q_norm" in t:
                 q = rms_norm_rows(q.reshape(T * HEADS, hd), t[p + "attn_q_norm"]).reshape(T, HEADS * hd)
                 k = rms_norm_rows(k.reshape(T * KV_HEADS, hd), t[p + "attn_k_norm"]).reshape(T, KV_HEADS * hd)
             q, k = q.copy(), k.copy()
@@ -294,16 +311,24 @@ class Model:
             self.K[l] = np.concatenate([self.K[l][:pos0], k.astype(np.float16)])
             self.V[l] = np.concatenate([self.V[l][:pos0], v.astype(np.float16)])
             att = self.attention(l, q, pos0)
-            x = (x + self.mm(p + "attn_output", t[p + "attn_output"], att)).astype(F32)
-            xn = rms_norm_rows(x, t[p + "ffn_norm"])
+            o = self.mm(p + "attn_output", t[p + "attn_output"], att)
+            if self.post:  # post_attention_norm (src/Transformer.cs:224)
+                o = rms_norm_rows(o, t[p + "post_attention_norm"])
+            x = (x + (o * rs).astype(F32)).astype(F32)  # x += o * rs (:225)
+            xn = x if self.post else rms_norm_rows(x, t[p + "ffn_norm"])
             if p + "ffn_gate_inp" in t:
                 o = self.moe_ffn(p, xn)
             else:
                 o = self.swiglu(p + "ffn_", t[p + "ffn_gate"], t[p + "ffn_up"], t[p + "ffn_down"], xn)
-            x = (x + o).astype(F32)
+            if self.post:  # post_ffw_norm (:230)
+                o = rms_norm_rows(o, t[p + "post_ffw_norm"])
+            x = (x + (o * rs).astype(F32)).astype(F32)
         rows = x if all_logits else x[-1:]
         xn = rms_norm_rows(rows, t["output_norm"])
-        return self.mm("output", t["output"], xn)
+        logits = self.mm("output", t["output"], xn)
+        if self.ls:  # LogitScale: logits *= 1f / scale (:123)
+            logits = (logits * (F32(1) / F32(self.ls))).astype(F32)
+        return logits
 
     def swiglu(self, name, gate, up, down, xn):
         """SwiGlu (src/Transformer.cs:241-251)."""

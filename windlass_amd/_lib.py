@@ -27,6 +27,7 @@ SIGNATURES = {
     "wl_kv_store_dev": (ctypes.c_int, [P, P, P, I32, I32, P, P, I32]),
     "wl_attention_dev": (ctypes.c_int, [P, P, I32, I32, I32, I32, P, P, I32, ctypes.c_float, P]),
     "wl_residual_dev": (ctypes.c_int, [P, P, P, I64, ctypes.c_float]),
+    "wl_scale_dev": (ctypes.c_int, [P, P, I64, ctypes.c_float]),
     "wl_argmax_dev": (ctypes.c_int, [P, P, I32, I64, P]),
     "wl_embed_dev_ids": (ctypes.c_int, [P, P, P, I32, P]),
     "wl_layer_batch_dev": (ctypes.c_int, [P, P, P, I32, P, P, I32, I32, P, P]),

@@ -305,7 +305,9 @@ class LayerDesc(ctypes.Structure):
         ("eps", ctypes.c_float), ("attention_scale", ctypes.c_float), ("residual_scale", ctypes.c_float)] + [
         (n, ctypes.c_void_p) for n in ("ffn_gate_inp", "ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp",
                                        "ffn_gate_inp_shexp")] + [
-        ("expert_used", ctypes.c_int32), ("expert_weights_norm", ctypes.c_int32)]
+        ("expert_used", ctypes.c_int32), ("expert_weights_norm", ctypes.c_int32)] + [
+        (n, ctypes.c_void_p) for n in ("d_post_attention_norm", "d_post_ffw_norm")] + [
+        ("qk_norm_full", ctypes.c_int32)]
 
 
 class Transformer:

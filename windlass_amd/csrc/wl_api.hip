@@ -1075,6 +1075,13 @@ extern "C" int wl_attention_dev(wl_ctx *c, const float *d_q, int32_t T, int32_t 
   return WL_OK;
 }
 
+extern "C" int wl_scale_dev(wl_ctx *c, float *d_x, int64_t n, float s) {
+  if (!c || !d_x) return fail(WL_E_ARG, "wl_scale_dev: null argument");
+  if (n < 0) return fail(WL_E_SHAPE, "wl_scale_dev: n = %lld", (long long)n);
+  WL_HIP(wl::scale_launch(d_x, n, s, c->stream), "scale");
+  return WL_OK;
+}
+
 extern "C" int wl_residual_dev(wl_ctx *c, float *d_x, const float *d_o, int64_t n, float rs) {
   if (!c || !d_x || !d_o) return fail(WL_E_ARG, "wl_residual_dev: null argument");
   WL_HIP(wl::residual_launch(d_x, d_o, n, rs, c->stream), "residual");
@@ -1152,8 +1159,10 @@ extern "C" int wl_embed_dev_ids(wl_ctx *c, const wl_weight *embd, const int32_t 
 static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
                      uint16_t *d_V, const wl::RowMap &rm, int max_n, bool each) {
   if (!c || !L || !d_x || !d_K || !d_V) return fail(WL_E_ARG, "wl_layer_dev: null argument");
+  // OLMo 2 (src/Transformer.cs:182,224-230): post-norms instead of pre-norms
+  const bool post = L->d_post_attention_norm || L->d_post_ffw_norm;
   if (!L->attn_q || !L->attn_k || !L->attn_v || !L->attn_output || !L->ffn_gate || !L->ffn_up || !L->ffn_down ||
-      !L->d_attn_norm || !L->d_ffn_norm)
+      (post ? !(L->d_post_attention_norm && L->d_post_ffw_norm) : !(L->d_attn_norm && L->d_ffn_norm)))
     return fail(WL_E_ARG, "wl_layer_dev: a required tensor is missing");
   const int E = L->embd, H = L->heads, KH = L->kv_heads, HD = L->head_dim;
   if (T <= 0 || pos0 < 0 || E <= 0 || H <= 0 || KH <= 0 || H % KH || HD <= 0)
@@ -1204,24 +1213,29 @@ static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, i
     }
     return WL_OK;
   };
-  // attention block
-  if ((rc = wl_rms_norm_dev(c, d_x, T, E, L->d_attn_norm, L->eps, xn))) return rc;
+  // attention block (x itself is the input under post-norms: OLMo 2 has no pre-norm)
+  const float *ain = post ? d_x : xn;
+  if (!post && (rc = wl_rms_norm_dev(c, d_x, T, E, L->d_attn_norm, L->eps, xn))) return rc;
   if (T <= 8 || each) {
     for (int t0 = 0; t0 < T; t0 += 8) {  // q, k, v in one launch per 8 rows
       const int n = T - t0 < 8 ? T - t0 : 8;
       const wl_weight *ws[3] = {L->attn_q, L->attn_k, L->attn_v};
       float *ys[3] = {q + (int64_t)t0 * QD, k + (int64_t)t0 * KD, v + (int64_t)t0 * KD};
-      if ((rc = wl_matmul_multi_dev(c, 3, ws, xn + (int64_t)t0 * E, n, ys))) return rc;
+      if ((rc = wl_matmul_multi_dev(c, 3, ws, ain + (int64_t)t0 * E, n, ys))) return rc;
     }
-  } else if ((rc = mm(L->attn_q, xn, q, false)) || (rc = mm(L->attn_k, xn, k, false)) ||
-             (rc = mm(L->attn_v, xn, v, false))) {
+  } else if ((rc = mm(L->attn_q, ain, q, false)) || (rc = mm(L->attn_k, ain, k, false)) ||
+             (rc = mm(L->attn_v, ain, v, false))) {
     return rc;
   }
   if (L->d_q_bias) WL_HIP(wl::bias_launch(q, L->d_q_bias, T, QD, c->stream), "q bias");
   if (L->d_k_bias) WL_HIP(wl::bias_launch(k, L->d_k_bias, T, KD, c->stream), "k bias");
   if (L->d_v_bias) WL_HIP(wl::bias_launch(v, L->d_v_bias, T, KD, c->stream), "v bias");
-  if (L->d_q_norm && (rc = wl_rms_norm_dev(c, q, (int64_t)T * H, HD, L->d_q_norm, L->eps, q))) return rc;
-  if (L->d_k_norm && (rc = wl_rms_norm_dev(c, k, (int64_t)T * KH, HD, L->d_k_norm, L->eps, k))) return rc;
+  // q/k norms per head (qwen3) or over the whole rows (QkNormFull, OLMo 2: src/Transformer.cs:192-201)
+  const bool full = L->qk_norm_full != 0;
+  if (L->d_q_norm && (rc = wl_rms_norm_dev(c, q, full ? T : (int64_t)T * H, full ? QD : HD, L->d_q_norm, L->eps, q)))
+    return rc;
+  if (L->d_k_norm && (rc = wl_rms_norm_dev(c, k, full ? T : (int64_t)T * KH, full ? KD : HD, L->d_k_norm, L->eps, k)))
+    return rc;
   const double fs = L->rope_freq_scale != 0.0 ? L->rope_freq_scale : 1.0;
   WL_HIP(wl::rope_kv_launch(q, k, v, T, H, KH, HD, rd, L->neox, pos0, L->rope_base, fs, L->d_rope_freqs, d_K, d_V,
                             rm, c->stream),
@@ -1230,9 +1244,20 @@ static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, i
   WL_HIP(wl::attention_launch(q, QD, T, d_K, d_V, KD, H, KH, HD, pos0, scale, (float *)c->buf[S_ATT], att, QD, rm,
                               max_n, c->stream),
          "attention");
-  if ((rc = mm(L->attn_output, att, d_x, true))) return rc;
+  if (post) {
+    // o = RmsNorm(W_o att), then x += o * rs (src/Transformer.cs:223-225)
+    if ((rc = ensure(c, S_LM, (size_t)T * E * 4))) return rc;
+    float *o = (float *)c->buf[S_LM];
+    if ((rc = mm(L->attn_output, att, o, false)) ||
+        (rc = wl_rms_norm_dev(c, o, T, E, L->d_post_attention_norm, L->eps, o)))
+      return rc;
+    WL_HIP(wl::residual_launch(d_x, o, (int64_t)T * E, rs, c->stream), "residual");
+  } else if ((rc = mm(L->attn_output, att, d_x, true))) {
+    return rc;
+  }
   // feed-forward block
-  if ((rc = wl_rms_norm_dev(c, d_x, T, E, L->d_ffn_norm, L->eps, xn))) return rc;
+  const float *fin = post ? d_x : xn;
+  if (!post && (rc = wl_rms_norm_dev(c, d_x, T, E, L->d_ffn_norm, L->eps, xn))) return rc;
   // SwiGlu (src/Transformer.cs:241-251) into y (added into y with add): up to 8 rows (or every
   // row with each) gate and up in one GEMV launch with the SiLU epilogue; a prompt: the two
   // GEMMs, then the SiLU pass
@@ -1240,14 +1265,24 @@ static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, i
     const bool fused = wg->type == wu->type && (T <= 8 || each || int_path(c, wg) || !wl::gemm_supports(wg->type));
     int r;
     if (fused) {
-      if ((r = wl_gate_up_dev(c, wg, wu, -1, xn, T, g))) return r;
+      if ((r = wl_gate_up_dev(c, wg, wu, -1, fin, T, g))) return r;
     } else {
-      if ((r = mm(wg, xn, g, false)) || (r = mm(wu, xn, u, false))) return r;
+      if ((r = mm(wg, fin, g, false)) || (r = mm(wu, fin, u, false))) return r;
       WL_HIP(wl::silu_mul_launch(g, u, (int64_t)T * wg->rows, c->stream), "silu");
     }
     return mm(wd, g, y, add);
   };
-  if (!moe) return swiglu(L->ffn_gate, L->ffn_up, L->ffn_down, d_x, true);
+  if (!moe && !post) return swiglu(L->ffn_gate, L->ffn_up, L->ffn_down, d_x, true);
+  if (!moe) {
+    // the FFN's output RMS-normed before the residual add (src/Transformer.cs:229-231)
+    if ((rc = ensure(c, S_LM, (size_t)T * E * 4))) return rc;
+    float *o = (float *)c->buf[S_LM];
+    if ((rc = swiglu(L->ffn_gate, L->ffn_up, L->ffn_down, o, false)) ||
+        (rc = wl_rms_norm_dev(c, o, T, E, L->d_post_ffw_norm, L->eps, o)))
+      return rc;
+    WL_HIP(wl::residual_launch(d_x, o, (int64_t)T * E, rs, c->stream), "residual");
+    return WL_OK;
+  }
   // MoeFfn (src/Transformer.cs:259-311): router logits, routed experts, the shared expert, then
   // the residual add (:231)
   const int ne = (int)L->ffn_gate->experts;
@@ -1255,15 +1290,16 @@ static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, i
       (shared && (rc = ensure(c, S_LS, (size_t)T * E * 4))))
     return rc;
   float *lg = (float *)c->buf[S_LR], *o = (float *)c->buf[S_LM], *sh = (float *)c->buf[S_LS];
-  if ((rc = mm(L->ffn_gate_inp, xn, lg, false))) return rc;
-  if ((rc = moe_dev(c, lg, L->expert_used, L->expert_weights_norm, L->ffn_gate, L->ffn_up, L->ffn_down, xn, T, o)))
+  if ((rc = mm(L->ffn_gate_inp, fin, lg, false))) return rc;
+  if ((rc = moe_dev(c, lg, L->expert_used, L->expert_weights_norm, L->ffn_gate, L->ffn_up, L->ffn_down, fin, T, o)))
     return rc;
   if (shared) {
     if ((rc = swiglu(L->ffn_gate_shexp, L->ffn_up_shexp, L->ffn_down_shexp, sh, false))) return rc;
     // the router's logits are used: its buffer takes the shared expert's gate
-    if (L->ffn_gate_inp_shexp && (rc = mm(L->ffn_gate_inp_shexp, xn, lg, false))) return rc;
+    if (L->ffn_gate_inp_shexp && (rc = mm(L->ffn_gate_inp_shexp, fin, lg, false))) return rc;
     WL_HIP(wl::shared_expert_launch(o, sh, L->ffn_gate_inp_shexp ? lg : nullptr, T, E, c->stream), "shared expert");
   }
+  if (post && (rc = wl_rms_norm_dev(c, o, T, E, L->d_post_ffw_norm, L->eps, o))) return rc;
   WL_HIP(wl::residual_launch(d_x, o, (int64_t)T * E, rs, c->stream), "residual");
   return WL_OK;
 }

@@ -32,6 +32,8 @@ hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *
                             int heads, int kv_heads, int hd, int pos0, float scale, float *scratch, float *out,
                             int64_t ldo, const RowMap &rm, int max_n, hipStream_t st);
 hipError_t residual_launch(float *x, const float *o, int64_t n, float rs, hipStream_t st);
+// x[i] *= s
+hipError_t scale_launch(float *x, int64_t n, float s, hipStream_t st);
 // o [rows][dim] += f_t * sh, f_t = sigmoid(gl[t]) (gl null: 1): MoeFfn's shared expert.
 hipError_t shared_expert_launch(float *o, const float *sh, const float *gl, int64_t rows, int64_t dim,
                                 hipStream_t st);

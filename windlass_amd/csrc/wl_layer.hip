@@ -384,6 +384,13 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float *__r
   }
 }
 
+// x[i] *= s: the embedding scale (src/Transformer.cs:94,150) and the logit scale's reciprocal
+// (:123).
+__global__ void scale_kernel(float *__restrict__ x, int64_t n, float s) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] *= s;
+}
+
 // x[i] += o[i] * rs (src/Transformer.cs:224,231).
 __global__ void residual_kernel(float *__restrict__ x, const float *__restrict__ o, int64_t n, float rs) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -580,6 +587,12 @@ hipError_t shared_expert_launch(float *o, const float *sh, const float *gl, int6
   const int64_t n = rows * dim;
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(shared_expert_kernel, dim3(blocks_of(n, 256)), dim3(256), 0, st, o, sh, gl, n, dim);
+  return hipGetLastError();
+}
+
+hipError_t scale_launch(float *x, int64_t n, float s, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(scale_kernel, dim3(blocks_of(n, 256)), dim3(256), 0, st, x, n, s);
   return hipGetLastError();
 }
 

@@ -243,19 +243,19 @@ class GgufModelFile:
 
 # architectures the device forward runs, with their rotary pairing (False: adjacent values,
 # True: NeoX halves); the reference's other architectures are refused by model_config
-DENSE_ARCHS = {"llama": False, "qwen2": True, "qwen3": True, "granite": False}
+DENSE_ARCHS = {"llama": False, "qwen2": True, "qwen3": True, "granite": False, "olmo2": True}
 MOE_ARCHS = {"llama": False, "mixtral": False, "qwen2moe": True, "qwen3moe": True}  # may hold expert layers
-KNOWN_ARCHS = set(DENSE_ARCHS) | set(MOE_ARCHS) | {"olmo2"}
+KNOWN_ARCHS = set(DENSE_ARCHS) | set(MOE_ARCHS)
 
 
 def model_config(g):
-    """ModelConfig.From (src/ModelConfig.cs:38-100) for the models the device forward runs:
-    llama, qwen2, qwen3, granite without embedding or logit scales, and the expert models
-    (llama/mixtral, qwen2moe, qwen3moe: expert_count, expert_used_count, expert_weights_norm,
-    whose default renormalises except for qwen2moe). Architectures outside the reference's list,
-    OLMo 2's post-norms and granite's embedding/logit scales raise NotSupportedError. RoPE scaling
-    other than linear is recorded in `warnings`, as the reference does, and the model runs
-    without it."""
+    """ModelConfig.From (src/ModelConfig.cs:38-100) for every architecture the reference runs:
+    llama, qwen2, qwen3, granite (its embedding, residual, attention and logit scales), OLMo 2
+    (post-norms, q/k norms over the whole rows, NeoX RoPE) and the expert models (llama/mixtral,
+    qwen2moe, qwen3moe: expert_count, expert_used_count, expert_weights_norm, whose default
+    renormalises except for qwen2moe). Architectures outside the reference's list raise
+    NotSupportedError. RoPE scaling other than linear is recorded in `warnings`, as the reference
+    does, and the model runs without it."""
     from .model import ModelConfig
     arch = g.Get("general.architecture", "")
     if arch not in KNOWN_ARCHS:
@@ -299,16 +299,24 @@ def model_config(g):
     elif scaling != "none" and factor > 0 and factor != 1.0:
         warnings.append("RoPE scaling %r (factor %g) is not applied; positions past the trained context may "
                         "degrade" % (scaling, factor))
-    attention_scale = residual_scale = 0.0
-    if arch == "granite":
-        if md("embedding_scale", 0.0, float) or md("logit_scale", 0.0, float):
-            raise NotSupportedError("granite's embedding and logit scales are not on the device forward")
-        residual_scale, attention_scale = md("residual_scale", 0.0, float), md("attention.scale", 0.0, float)
+    scales = dict.fromkeys(("embedding_scale", "residual_scale", "attention_scale", "logit_scale"), 0.0)
+    if arch == "granite":  # 0 = not set (src/ModelConfig.cs:56-62)
+        for k in scales:
+            scales[k] = md("attention.scale" if k == "attention_scale" else k, 0.0, f32)
+    olmo = arch == "olmo2"
+    if olmo:  # q/k norms over the whole rows (src/ModelConfig.cs:105-108)
+        qd, kd = heads * head_dim, kv_heads * head_dim
+        have = {t.Name: t for t in g.Tensors}
+        for l in range(md("block_count")):
+            qn, kn = have.get("blk.%d.attn_q_norm.weight" % l), have.get("blk.%d.attn_k_norm.weight" % l)
+            if qn is not None and kn is not None and (qn.ElementCount != qd or kn.ElementCount != kd):
+                raise NotSupportedError("Layer %d: attn_q_norm/attn_k_norm must cover the whole Q and K vectors "
+                                        "(%d and %d)." % (l, qd, kd))
     return ModelConfig(layers=md("block_count"), embd=embd, heads=heads, kv_heads=kv_heads, head_dim=head_dim,
                        rope_dims=rope_dims, neox={**DENSE_ARCHS, **MOE_ARCHS}[arch],
                        rope_base=md("rope.freq_base", 10000.0, f32), rope_freq_scale=freq_scale,
-                       eps=md("attention.layer_norm_rms_epsilon", 1e-5, f32), attention_scale=attention_scale,
-                       residual_scale=residual_scale, warnings=warnings, **moe)
+                       eps=md("attention.layer_norm_rms_epsilon", 1e-5, f32), warnings=warnings,
+                       post_norms=olmo, qk_norm_full=olmo, **scales, **moe)
 
 
 def _vector(ctx, g, t, dev):
@@ -370,6 +378,12 @@ def _check_ffn_layouts(g, cfg):
             for n in names:
                 if p + n + ".weight" not in have:
                     raise NotSupportedError("layer %d lacks %s" % (l, n))
+        # RequiredLayerTensors, or OLMo 2's (src/ModelConfig.cs:112-115)
+        if cfg.post_norms:
+            need("attn_q", "attn_k", "attn_v", "attn_output", "attn_q_norm", "attn_k_norm", "post_attention_norm",
+                 "post_ffw_norm")
+        else:
+            need("attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_norm")
         if cfg.expert_count > 0 and p + "ffn_gate_inp.weight" in have:
             need("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps")
             r = have[p + "ffn_gate_inp.weight"]

@@ -38,6 +38,10 @@ class ModelConfig:
     expert_count: int = 0         # MoE (src/ModelConfig.cs:26-31): experts per MoE layer, 0 for dense
     expert_used: int = 0          # experts chosen per token
     expert_weights_norm: bool = True  # renormalise the chosen weights (not qwen2moe by default)
+    embedding_scale: float = 0.0  # Granite: embedding rows times this (0: none)
+    logit_scale: float = 0.0      # Granite: logits divided by this, as 1f / scale (0: none)
+    post_norms: bool = False      # OLMo 2: no pre-norms; each branch's output RMS-normed before its add
+    qk_norm_full: bool = False    # OLMo 2: q/k norms over the whole rows, not per head
     warnings: list = field(default_factory=list)  # ModelConfig.Warnings: what the model runs without
 
 
@@ -48,8 +52,9 @@ def _ptr(t):
 class DeviceTransformer:
     """weights: {GGUF tensor name: WeightView} with token_embd, output (absent when tied to
     token_embd) and blk.N.{attn_q,attn_k,attn_v,attn_output,ffn_gate,ffn_up,ffn_down};
-    vectors: {name: device float32 tensor} with output_norm, blk.N.attn_norm, blk.N.ffn_norm and
-    the optional blk.N.attn_{q,k,v}.bias, blk.N.attn_{q,k}_norm and rope_freqs."""
+    vectors: {name: device float32 tensor} with output_norm, blk.N.attn_norm, blk.N.ffn_norm (or,
+    with post_norms, blk.N.post_attention_norm and blk.N.post_ffw_norm) and the optional
+    blk.N.attn_{q,k,v}.bias, blk.N.attn_{q,k}_norm and rope_freqs."""
 
     def __init__(self, ctx, cfg, weights, vectors, max_positions, stream=None):
         """stream: a StageStream whose weights() the layer tensors of `weights` come from; the
@@ -97,7 +102,12 @@ class DeviceTransformer:
         else:
             for f in _LAYER_TENSORS:
                 setattr(d, f, self.w[p + f].handle.value)
-        d.d_attn_norm, d.d_ffn_norm = _ptr(v[p + "attn_norm"]), _ptr(v[p + "ffn_norm"])
+        if c.post_norms:
+            d.d_post_attention_norm = _ptr(v[p + "post_attention_norm"])
+            d.d_post_ffw_norm = _ptr(v[p + "post_ffw_norm"])
+        else:
+            d.d_attn_norm, d.d_ffn_norm = _ptr(v[p + "attn_norm"]), _ptr(v[p + "ffn_norm"])
+        d.qk_norm_full = int(c.qk_norm_full)
         d.d_q_bias, d.d_k_bias, d.d_v_bias = (_ptr(v.get(p + "attn_%s.bias" % q)) for q in "qkv")
         d.d_q_norm, d.d_k_norm = _ptr(v.get(p + "attn_q_norm")), _ptr(v.get(p + "attn_k_norm"))
         d.d_rope_freqs = _ptr(v.get("rope_freqs"))
@@ -122,7 +132,20 @@ class DeviceTransformer:
         x = self._rows(T)
         toks = (ctypes.c_int32 * T)(*tokens)
         check(self.L.wl_embed_dev(self.ctx.handle, self.embd_w.handle, toks, T, ctypes.c_void_p(x.data_ptr())))
+        self.embed_scale(x, T)
         return self._layers_and_head(x, T, pos0)
+
+    def embed_scale(self, x, T):
+        """x *= EmbeddingScale on the embedding rows (src/Transformer.cs:94,150), when set."""
+        if self.cfg.embedding_scale:
+            check(self.L.wl_scale_dev(self.ctx.handle, ctypes.c_void_p(x.data_ptr()), T * self.cfg.embd,
+                                      ctypes.c_float(self.cfg.embedding_scale)))
+
+    def logit_scale(self, lg, n):
+        """logits *= 1f / LogitScale (src/Transformer.cs:123), when set."""
+        if self.cfg.logit_scale:
+            inv = np.float32(1) / np.float32(self.cfg.logit_scale)
+            check(self.L.wl_scale_dev(self.ctx.handle, ctypes.c_void_p(lg.data_ptr()), n, ctypes.c_float(inv)))
 
     def forward_ids(self, d_ids, pos0):
         """forward() with the token ids in device memory (an int32 tensor, e.g. a sampled token):
@@ -132,6 +155,7 @@ class DeviceTransformer:
         x = self._rows(T)
         check(self.L.wl_embed_dev_ids(self.ctx.handle, self.embd_w.handle, ctypes.c_void_p(d_ids.data_ptr()), T,
                                       ctypes.c_void_p(x.data_ptr())))
+        self.embed_scale(x, T)
         return self._layers_and_head(x, T, pos0)
 
     def _check(self, T, pos0):
@@ -165,6 +189,7 @@ class DeviceTransformer:
         check(L.wl_rms_norm_dev(h, c(x[T - 1:].data_ptr()), 1, self.cfg.embd, c(self.v["output_norm"].data_ptr()),
                                 ctypes.c_float(self.cfg.eps), c(self._xn.data_ptr())))
         check(L.wl_matmul_dev(h, self.head_w.handle, -1, c(self._xn.data_ptr()), 1, c(self.logits.data_ptr())))
+        self.logit_scale(self.logits, self.vocab)
         return self.logits
 
     def sample(self):
@@ -331,6 +356,7 @@ class DeviceBatch:
             n = min(8, rows - r0)
             check(m.L.wl_matmul_dev(m.ctx.handle, m.head_w.handle, -1, c(xn[r0:].data_ptr()), n,
                                     c(lg[r0:].data_ptr())))
+        m.logit_scale(lg, rows * m.vocab)
         return lg
 
     def prefill(self, slot, tokens):
@@ -343,6 +369,7 @@ class DeviceBatch:
         x = self._buf("x", T, m.cfg.embd)
         toks = (ctypes.c_int32 * T)(*tokens)
         check(m.L.wl_embed_dev(m.ctx.handle, m.embd_w.handle, toks, T, c(x.data_ptr())))
+        m.embed_scale(x, T)
         m.run_layers(lambda l, d: check(m.L.wl_layer_dev(m.ctx.handle, ctypes.byref(d), c(x.data_ptr()), T, pos0,
                                                          c(self.K[l, slot].data_ptr()),
                                                          c(self.V[l, slot].data_ptr()))))
@@ -357,6 +384,7 @@ class DeviceBatch:
         sl = (ctypes.c_int32 * N)(*slots)
         x = self._buf("x", N, m.cfg.embd)
         check(m.L.wl_embed_dev_ids(m.ctx.handle, m.embd_w.handle, c(d_ids.data_ptr()), N, c(x.data_ptr())))
+        m.embed_scale(x, N)
         m.run_layers(lambda l, d: check(m.L.wl_layer_batch_dev(m.ctx.handle, ctypes.byref(d), c(x.data_ptr()), N,
                                                                pos, sl, self.slots, self.cap,
                                                                c(self.K[l].data_ptr()), c(self.V[l].data_ptr()))))
