@@ -70,8 +70,9 @@ def test_route_ties_and_nan_vs_oracle(ctx, n):
 # serial kernel and plan separately
 @pytest.mark.parametrize("T", [1, 8, 11])
 # (gate/up, down) formats; Q5_0 and Q3_K experts are the reference's own MoE cases
-# (tests/MoeTests.cs:73-77)
-@pytest.mark.parametrize("types", [(12, 12), (12, 14), (6, 6), (11, 11), (13, 14), (2, 8), (1, 30)])
+# (tests/MoeTests.cs:73-77); IQ3_S / IQ2_S experts through their LDS-table codecs
+@pytest.mark.parametrize("types", [(12, 12), (12, 14), (6, 6), (11, 11), (13, 14), (2, 8), (1, 30), (21, 22),
+                                   (22, 21)])
 @pytest.mark.parametrize("shape", [(16, 4, 512, 256), (128, 8, 512, 256), (2100, 2, 256, 256)],
                          ids=lambda s: "ne%d_k%d" % s[:2])
 def test_moe_ffn_vs_oracle(ctx, T, types, shape):

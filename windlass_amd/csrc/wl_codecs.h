@@ -34,11 +34,24 @@ namespace wl {
 constexpr float kTwo24 = 16777216.f;
 constexpr float kTwo20 = 1048576.f;
 
-// LDS tables some codecs use; filled once per workgroup by init_lds.
+// LDS tables some codecs use; filled once per workgroup by init_lds. A launch runs one codec, so
+// the formats' tables share the space.
 struct Lds {
-  uint2 grid8[256];   // IQ2_XXS grid entries: 8 value bytes (8, 25 or 43)
-  uint2 signs8[128];  // IQ2_XXS sign patterns: 8 bytes, 0x80 where the value is negated
-  uint32_t iq4[256];  // IQ4_XS qs byte -> (kvalue[low nibble] + 128, kvalue[high nibble] + 128) as fp16 pair
+  union {
+    struct {
+      uint2 grid8[256];   // IQ2_XXS grid entries: 8 value bytes (8, 25 or 43)
+      uint2 signs8[128];  // IQ2_XXS sign patterns: 8 bytes, 0x80 where the value is negated
+    };
+    uint32_t iq4[256];    // IQ4_XS qs byte -> (kvalue[low nibble] + 128, kvalue[high nibble] + 128) as fp16 pair
+    struct {
+      uint2 grid2s[1024];  // IQ2_S grid entries: 8 value bytes
+      uint2 sgn2s[256];    // a sign byte -> 8 bytes, 0x80 where the value is negated
+    };
+    struct {
+      uint32_t grid3s[512];  // IQ3_S grid entries: 4 value bytes (odd, 1..15)
+      uint2 sgn3s[256];      // as sgn2s
+    };
+  };
 };
 
 // ---------------------------------------------------------------------------- Q4_K

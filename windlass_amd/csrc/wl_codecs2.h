@@ -489,4 +489,181 @@ typedef FWide<0> F32w;
 typedef FWide<1> F16w;
 typedef FWide<2> BF16w;
 
+
+// A sign byte's 8 bits as 8 bytes, 0x80 where the bit is set (the fp16 sign bit of a value byte
+// placed below it): one LDS table of the 256 patterns.
+__device__ inline void init_sign_bytes(uint2 *t) {
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) {
+    uint32_t m[8];
+    for (int j = 0; j < 8; j++) m[j] = ((i >> j) & 1) ? 0x80u : 0u;
+    t[i] = make_uint2(m[0] | m[1] << 8 | m[2] << 16 | m[3] << 24, m[4] | m[5] << 8 | m[6] << 16 | m[7] << 24);
+  }
+}
+
+// Eight signed values as four fp16 pairs from value bytes g and sign bytes sg (0x80 / 0x00): the
+// pairs (0,2) (1,3) (4,6) (5,7), each value a subnormal with its sign.
+__device__ __forceinline__ void signed_pairs(uint2 g, uint2 sg, uint32_t *p) {
+  p[0] = __builtin_amdgcn_perm(sg.x, g.x, 0x06020400u);
+  p[1] = __builtin_amdgcn_perm(sg.x, g.x, 0x07030501u);
+  p[2] = __builtin_amdgcn_perm(sg.y, g.y, 0x06020400u);
+  p[3] = __builtin_amdgcn_perm(sg.y, g.y, 0x07030501u);
+}
+
+// The dot of one group of 8 (pairs as signed_pairs lays them out) onto chain acc.
+__device__ __forceinline__ float group_dot(const uint32_t *p, const float *x, float acc) {
+  acc = fma_lo(p[0], x[0], acc);
+  acc = fma_hi(p[0], x[2], acc);
+  acc = fma_lo(p[1], x[1], acc);
+  acc = fma_hi(p[1], x[3], acc);
+  acc = fma_lo(p[2], x[4], acc);
+  acc = fma_hi(p[2], x[6], acc);
+  acc = fma_lo(p[3], x[5], acc);
+  return fma_hi(p[3], x[7], acc);
+}
+
+// The byte at p (any alignment) from its aligned dword.
+__device__ __forceinline__ uint32_t ld_byte(const uint8_t *p) {
+  return (ldw4(align4_down(p)) >> (8 * misalign4(p))) & 0xFF;
+}
+
+// -------------------------------------------------------------------------- IQ2_S
+// block_iq2_s (82 B, src/IQuants.cs:199-222): d f16 | 32 grid bytes | 32 sign bytes | qh[8] |
+// scales[8]. Lane slice: sub-block ib = sub (32 values): grid bytes 4ib.. with two index bits
+// each from qh[ib] (10-bit index into the 1024-entry grid), sign bytes 4ib.., and the scales
+// byte ib (groups 0, 1: low nibble; 2, 3: high), db = d * (0.5 + s) * 0.25.
+struct IQ2S {
+  static constexpr int BLOCK = 256, BYTES = 82, LPB = 8, NEED_LDS = 1, R1 = 8, SP2 = 1;
+  struct Lane { int ib; };
+  struct Xs { float v[32]; };
+  struct Raw { uint32_t dw, g[2], s[2], qh, sc; uint32_t dsh, sh; };
+  struct W { uint32_t p[16]; float db0, db1; };
+
+  __device__ static Lane lane(int sub) { return Lane{sub}; }
+
+  __device__ static void load_x(const float *xb, const Lane &L, Xs &x) {
+    ld_x16(xb + 32 * L.ib, x.v);
+    ld_x16(xb + 32 * L.ib + 16, x.v + 16);
+#pragma unroll
+    for (int i = 0; i < 32; i++) x.v[i] *= kTwo24;
+  }
+
+  __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
+    r.dw = ldw4(align4_down(blk));
+    r.dsh = misalign4(blk) & 2;
+    const uint8_t *pg = blk + 2 + 4 * L.ib;  // the sign bytes follow 32 bytes later: the same alignment
+    gu32 *a = align4_down(pg), *b = align4_down(pg + 32);
+    r.sh = misalign4(pg) * 8;
+    r.g[0] = ldw4(a);
+    r.g[1] = ldw4(a + 1);
+    r.s[0] = ldw4(b);
+    r.s[1] = ldw4(b + 1);
+    r.qh = ld_byte(blk + 66 + L.ib);
+    r.sc = ld_byte(blk + 74 + L.ib);
+  }
+
+  __device__ static void unpack(const Raw &r, const Lane &, const Lds &lds, W &w) {
+    const float d = half_lo(r.dsh ? (r.dw >> 16) : r.dw);
+    w.db0 = d * (0.5f + (float)(r.sc & 0xF)) * 0.25f;  // src/IQuants.cs:210-211
+    w.db1 = d * (0.5f + (float)(r.sc >> 4)) * 0.25f;
+    const uint32_t g4 = __builtin_amdgcn_alignbit(r.g[1], r.g[0], r.sh);
+    const uint32_t s4 = __builtin_amdgcn_alignbit(r.s[1], r.s[0], r.sh);
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+      const uint32_t gi = ((g4 >> (8 * l)) & 0xFF) | (((r.qh >> (2 * l)) & 3) << 8);  // :215
+      signed_pairs(lds.grid2s[gi], lds.sgn2s[(s4 >> (8 * l)) & 0xFF], w.p + 4 * l);
+    }
+  }
+
+  // groups 0, 1 (scale db0) on one chain and 2, 3 (db1) on the other, interleaved
+  __device__ static float dot(const W &w, const Xs &x) {
+    float a = 0.f, b = 0.f;
+    a = group_dot(w.p, x.v, a);
+    b = group_dot(w.p + 8, x.v + 16, b);
+    a = group_dot(w.p + 4, x.v + 8, a);
+    b = group_dot(w.p + 12, x.v + 24, b);
+    return __builtin_fmaf(w.db1, b, w.db0 * a);
+  }
+
+  __device__ static void init_lds(Lds &lds) {
+    for (int i = threadIdx.x; i < 1024; i += blockDim.x) {
+      uint32_t b[8];
+      for (int j = 0; j < 8; j++) b[j] = iq2s_grid_byte(i, j);
+      lds.grid2s[i] = make_uint2(b[0] | b[1] << 8 | b[2] << 16 | b[3] << 24, b[4] | b[5] << 8 | b[6] << 16 | b[7] << 24);
+    }
+    init_sign_bytes(lds.sgn2s);
+  }
+};
+
+// -------------------------------------------------------------------------- IQ3_S
+// block_iq3_s (110 B, src/IQuants.cs:112-143): d f16 | qs[64] | qh[8] | signs[32] | scales[4].
+// Lane slice: sub-block ib = sub: grid indices qs[8ib..] with a ninth bit each from qh[ib]
+// (512-entry grid of 4 values), sign bytes 4ib.. (one per 8 values), and the nibble ib & 1 of
+// scales[ib / 2], db = d * (1 + 2 s).
+struct IQ3S {
+  static constexpr int BLOCK = 256, BYTES = 110, LPB = 8, NEED_LDS = 1, R1 = 8, SP2 = 1;
+  struct Lane { int ib; };
+  struct Xs { float v[32]; };
+  struct Raw { uint32_t dw, q[3], s[2], qh, sc; uint32_t dsh, sh; };
+  struct W { uint32_t p[16]; float db; };
+
+  __device__ static Lane lane(int sub) { return Lane{sub}; }
+
+  __device__ static void load_x(const float *xb, const Lane &L, Xs &x) {
+    ld_x16(xb + 32 * L.ib, x.v);
+    ld_x16(xb + 32 * L.ib + 16, x.v + 16);
+#pragma unroll
+    for (int i = 0; i < 32; i++) x.v[i] *= kTwo24;
+  }
+
+  __device__ static void load(const uint8_t *blk, const Lane &L, Raw &r) {
+    r.dw = ldw4(align4_down(blk));
+    r.dsh = misalign4(blk) & 2;
+    const uint8_t *pq = blk + 2 + 8 * L.ib, *ps = blk + 74 + 4 * L.ib;  // both at the block's alignment
+    gu32 *a = align4_down(pq), *b = align4_down(ps);
+    r.sh = misalign4(pq) * 8;
+    r.q[0] = ldw4(a);
+    r.q[1] = ldw4(a + 1);
+    r.q[2] = ldw4(a + 2);
+    r.s[0] = ldw4(b);
+    r.s[1] = ldw4(b + 1);
+    r.qh = ld_byte(blk + 66 + L.ib);
+    r.sc = ld_byte(blk + 106 + L.ib / 2) >> (4 * (L.ib & 1));
+  }
+
+  __device__ static void unpack(const Raw &r, const Lane &, const Lds &lds, W &w) {
+    const float d = half_lo(r.dsh ? (r.dw >> 16) : r.dw);
+    w.db = d * (float)(1 + 2 * (int)(r.sc & 0xF));  // src/IQuants.cs:121-122
+    const uint32_t q03 = __builtin_amdgcn_alignbit(r.q[1], r.q[0], r.sh);
+    const uint32_t q47 = __builtin_amdgcn_alignbit(r.q[2], r.q[1], r.sh);
+    const uint32_t s4 = __builtin_amdgcn_alignbit(r.s[1], r.s[0], r.sh);
+    const uint32_t h = r.qh;
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+      const uint32_t qw = l < 2 ? q03 : q47;
+      const uint32_t i1 = ((qw >> (16 * (l & 1))) & 0xFF) | ((h << (8 - 2 * l)) & 256);      // :130
+      const uint32_t i2 = ((qw >> (16 * (l & 1) + 8)) & 0xFF) | ((h << (7 - 2 * l)) & 256);  // :131
+      signed_pairs(make_uint2(lds.grid3s[i1], lds.grid3s[i2]), lds.sgn3s[(s4 >> (8 * l)) & 0xFF], w.p + 4 * l);
+    }
+  }
+
+  // groups 0, 2 and 1, 3 on two chains
+  __device__ static float dot(const W &w, const Xs &x) {
+    float a = 0.f, b = 0.f;
+    a = group_dot(w.p, x.v, a);
+    b = group_dot(w.p + 4, x.v + 8, b);
+    a = group_dot(w.p + 8, x.v + 16, a);
+    b = group_dot(w.p + 12, x.v + 24, b);
+    return w.db * (a + b);
+  }
+
+  __device__ static void init_lds(Lds &lds) {
+    for (int i = threadIdx.x; i < 512; i += blockDim.x) {
+      uint32_t g = 0;
+      for (int j = 0; j < 4; j++) g |= iq3s_grid_byte(i, j) << (8 * j);
+      lds.grid3s[i] = g;
+    }
+    init_sign_bytes(lds.sgn3s);
+  }
+};
+
 }  // namespace wl

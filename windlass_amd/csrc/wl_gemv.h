@@ -48,10 +48,6 @@ struct GemvParams {
 };
 
 bool gemv_supports(int type);
-// IQ3_S and IQ2_S: the generic kernel over the exact block decoders (wl_gemv_generic.hip).
-bool gemv_generic_supports(int type);
-hipError_t gemv_generic_run(const GemvMat *mats, int nmat, int nm, const float *x, int ldx, int cols, int T,
-                            hipStream_t st);
 bool gemv_mixed_supports(int type);
 
 // K-chunks a row of `cols` values is split into when nmat matrices share a launch (1: no split).

@@ -246,7 +246,6 @@ hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int l
     }
     return hipSuccess;
   }
-  if (same && gemv_generic_supports(mats[0].type)) return gemv_generic_run(mats, nmat, nm, x, ldx, cols, T, st);
   {
     const hipError_t e = gemv_batch_run(mats, nmat, nm, x, ldx, cols, T, scratch, num_cu, st);
     if (e != hipErrorNotSupported) return e;
@@ -318,7 +317,7 @@ hipError_t gemv_run(const GemvMat *mats, int nmat, int nm, const float *x, int l
   return hipGetLastError();
 }
 
-bool gemv_supports(int type) { return gemv_ops(type) != nullptr || gemv_generic_supports(type); }
+bool gemv_supports(int type) { return gemv_ops(type) != nullptr; }
 
 bool gemv_mixed_supports(int type) { return type == 12 || type == 14 || type == 8; }
 
