@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--int-dot", action="store_true",
                     help="the integer-dot kernels (Transformer.IntDot, --int-dot): 8-bit activations, "
                          "FastMath.IntDot per row; no CPU baseline")
+    ap.add_argument("--float-mma", action="store_true",
+                    help="the float products on the matrix cores (wl_set_float_mma: fp16 MFMA on an "
+                         "exact two-part split of x, as an engine started with --batch N runs them)")
     ap.add_argument("--formats", action="store_true",
                     help="instead of the layer: the decode GEMV of every GGUF format at the 70B FFN "
                          "shapes (28672x8192 and 8192x28672), one token and eight, one JSON line")
@@ -114,6 +117,7 @@ def main():
     host = {n: synth.blocks(t, r, c, rng) for n, t, r, c in LAYER}
     ctx = Context(0)
     ctx.IntDot = args.int_dot
+    ctx.FloatMma = args.float_mma
     layers = [Layer(ctx, host) for _ in range(args.copies)]
     dev = torch.device("cuda:0")
     x = torch.from_numpy(synth.activations(rng, T, HIDDEN)).to(dev)
@@ -158,7 +162,7 @@ def main():
 
     # the other workloads first (GPU parts only; their CPU baselines run after the timed region)
     work, work_cpu = {}, []
-    if not args.no_workloads and not args.int_dot and T == 1:
+    if not args.no_workloads and not args.int_dot and not args.float_mma and T == 1:
         only = [k for k in args.only_workloads.split(",") if k]
         work, work_cpu = run_workloads(ctx, L, stream, layers, host, only)
 
@@ -205,7 +209,8 @@ def main():
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("%s_T%d%s" % (dom, T, "_int" if args.int_dot else ""))
+        kind = "_int" if args.int_dot else "_fmma" if args.float_mma else ""
+        traffic = json.load(open(tpath)).get("%s_T%d%s" % (dom, T, kind))
 
     for ly in layers:
         ly.free()
@@ -233,7 +238,9 @@ def main():
         "config": {"workload": "Llama-3.3-70B Q4_K_M decoder layer, 7 GEMVs (q,k,o,gate,up Q4_K; v,down Q6_K)",
                    "hidden": HIDDEN, "ffn": FFN, "heads": HEADS, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM,
                    "batch": T, "layer_copies": args.copies, "matrix_calls_per_layer": 4,
-                   "kernels": "int-dot (8-bit activations)" if args.int_dot else "fp32 decode GEMV"},
+                   "kernels": "int-dot (8-bit activations)" if args.int_dot else
+                   "fp32 decode GEMV on fp16 MFMA (x in two exact fp16 parts)" if args.float_mma else
+                   "fp32 decode GEMV"},
         "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "ms_per_layer": round(ms_layer, 5),
         "tokens_per_s_80_layers": round(1000.0 * T / (LAYERS * ms_layer), 2),
@@ -483,6 +490,23 @@ def run_workloads(ctx, L, stream, layers, host70, only):
                                                                 "path (Q8_K activations, v_mfma_i32_16x16x32_i8)")
         cpu.append(("llama70b_q4km_layer_T8_intdot",
                     lambda: intdot_cpu(LAYER, host70, 8, 3.0, "70B layer (7 GEMVs) at 8 tokens, integer dot")))
+
+    if want("llama70b_q4km_layer_T8_fmma"):
+        # ForwardBatch's float products on the matrix cores (wl_set_float_mma): fp16 MFMA on the
+        # exact two-part split of x, each token's bits independent of the batch
+        ws = [ly.w for ly in layers]
+        ctx.FloatMma = True
+        try:
+            ms = time_events(stream, layer_fns(LAYER, ws, 8), 100)
+        finally:
+            ctx.FloatMma = False
+        e = gemv_entry(LAYER, 8, ms, len(ws))
+        e["tokens_per_s_per_layer"] = round(8 / (ms * 1e-3), 1)
+        out["llama70b_q4km_layer_T8_fmma"] = dict(e, workload="Llama-3.3-70B Q4_K_M layer, 8 tokens, float products "
+                                                              "on the matrix cores (v_mfma_f32_16x16x32_f16, x split "
+                                                              "into two fp16 parts)")
+        cpu.append(("llama70b_q4km_layer_T8_fmma",
+                    lambda: gemv_cpu(LAYER, host70, 8, 3.0, "70B layer (7 GEMVs) at 8 tokens")))
 
     for key, t, rows, cols in (("prefill_512_q4k_28672x8192", Q4_K, 28672, 8192),
                                ("prefill_512_q6k_8192x28672", Q6_K, 8192, 28672)):

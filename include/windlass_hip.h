@@ -192,6 +192,18 @@ int wl_moe_ffn(wl_ctx *ctx, const float *logits, int32_t k, int32_t renorm,
  * pass, the SwiGLU outputs of every (token, expert) pair quantized for down. */
 int wl_set_int_dot(wl_ctx *ctx, int on);
 
+/* The float arithmetic of ForwardBatch (src/Transformer.cs:127-170; MatMulEach, :544-561) on the
+ * matrix cores, for an engine started with --batch N (EngineOptions.Batch, src/Engine.cs:21,65;
+ * src/Program.cs:213). Off by default. When on, every float decode GEMV of Q4_K and Q6_K weights
+ * (wl_matmul(_dev), the fused q/k/v and SwiGLU entries, the layer entries; 1-8 tokens per pass)
+ * runs on fp16 MFMA with each token's x split exactly into two fp16 parts: results within the
+ * float bar of the reference's DotRow, and a token's bits are the same whatever the number of
+ * tokens in the call, so a batched sequence gets the bits it gets alone in the same mode. The
+ * bits differ from the default (VALU) arithmetic's in the last places; switch it per context
+ * before decoding, not between steps of one sequence. Other formats, the integer branch and
+ * the MoE experts are unchanged. */
+int wl_set_float_mma(wl_ctx *ctx, int on);
+
 /* FastMath.Quantize (src/FastMath.cs:35-91) of x [T][cols], bit-identical: k = 0 gives Q8_0
  * activations (q int8 [T][cols], d [T][cols/32] rounded through fp16; bsums unused, may be
  * NULL), k = 1 Q8_K (d [T][cols/256], bsums int16 [T][cols/16], the sums of every 16 quants).

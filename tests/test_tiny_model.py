@@ -505,3 +505,36 @@ def test_gpu_moe_wait_given_up_surfaces_in_the_device_forward(gpu):
     for w in weights.values():
         w.free()
     assert got == want, (got, want)
+
+
+FMMA_KEYS = ["llama-q4_K", "llama-q6_K"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("key", FMMA_KEYS)
+def test_gpu_float_mma_batch_rows_equal_single_sequences(gpu, key):
+    """With the float products on the matrix cores (wl_set_float_mma) ForwardBatch's promise
+    still holds in that mode: every stacked row equals the sequence's own one-token step, bit
+    for bit, and the greedy tokens are the CPU backend's."""
+    from windlass_amd import DeviceBatch
+    gpu.FloatMma = True
+    try:
+        prompts = [PROBE[i:i + 3 + 2 * i] for i in range(5)]
+        dm, weights = device_model(gpu, key, max_positions=32)
+        single = []
+        for p in prompts:
+            dm.length = 0
+            single.append(dm.greedy(p, 4, keep_logits=True))
+        batch = DeviceBatch(dm, slots=5, slot_positions=32)
+        toks, seen = batch.greedy(prompts, 4, keep_logits=True)
+        for i in range(5):
+            assert toks[i] == single[i][0], (i, toks[i], single[i][0])
+            for s in range(5):
+                assert np.array_equal(seen[s][i].view(np.uint32), single[i][1][s].view(np.uint32)), (i, s)
+        want, _ = Model(key, oracle_matmul).greedy(PROBE, 8, chunk=8)
+        dm.length = 0
+        assert dm.greedy(PROBE, 8, chunk=8) == want
+        for w in weights.values():
+            w.free()
+    finally:
+        gpu.FloatMma = False

@@ -48,6 +48,7 @@ SIGNATURES = {
     "wl_route": (ctypes.c_int, [P, P, I32, I32, I32, I32, P, P]),
     "wl_moe_ffn": (ctypes.c_int, [P, P, I32, I32, P, P, P, P, I32, P, P]),
     "wl_set_int_dot": (ctypes.c_int, [P, ctypes.c_int]),
+    "wl_set_float_mma": (ctypes.c_int, [P, ctypes.c_int]),
     "wl_set_moe_one_launch": (ctypes.c_int, [P, ctypes.c_int]),
     "wl_debug_moe_patience": (ctypes.c_int, [P, ctypes.c_int32]),
     "wl_quantize": (ctypes.c_int, [P, P, I32, I32, I32, P, P, P]),

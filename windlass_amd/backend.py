@@ -145,6 +145,18 @@ class Context:
         self._int_dot = bool(on)
 
     @property
+    def FloatMma(self):
+        """ForwardBatch's float products (src/Transformer.cs:127-170) on the matrix cores: Q4_K
+        and Q6_K decode GEMVs of 1-8 tokens on fp16 MFMA with x split exactly into two fp16
+        parts, a token's bits independent of the batch. Off by default."""
+        return getattr(self, "_float_mma", False)
+
+    @FloatMma.setter
+    def FloatMma(self, on):
+        check(self._lib.wl_set_float_mma(self.handle, int(bool(on))))
+        self._float_mma = bool(on)
+
+    @property
     def MoeOneLaunch(self):
         """Whether the MoE entries may run as one launch (the default) or always as the launch
         chain (route+plan, gate/up, down, combine). Both give the same bits."""

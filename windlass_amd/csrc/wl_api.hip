@@ -14,6 +14,7 @@
 
 #include "../../include/windlass_hip.h"
 #include "wl_dequant.h"
+#include "wl_fmma.h"
 #include "wl_gemm.h"
 #include "wl_gemv.h"
 #include "wl_intdot.h"
@@ -61,6 +62,7 @@ struct wl_ctx {
   hipStream_t stream;
   hipStream_t copy;  // stage uploads (default priority), created on first use
   int int_dot;  // Transformer.IntDot (src/Transformer.cs:23)
+  int float_mma;  // wl_set_float_mma: Q4_K / Q6_K decode GEMVs of 1-8 tokens on the matrix cores
   int moe_chain;  // wl_set_moe_one_launch(0): the MoE entries always run the launch chain
   unsigned moe_launches;  // one-launch MoE launches so far (their counter sets alternate)
   bool moe_unchecked;     // one-launch MoE launches since the err word was last read
@@ -521,8 +523,27 @@ static void operand(const wl_weight *w, int32_t expert, const uint8_t **base, in
 }
 
 // One GEMV launch (plus its combine when rows are split along K) on the context's stream.
+// With float_mma on, the Q4_K / Q6_K matrices take the matrix-core GEMV (a matrix set it does
+// not take as a whole runs one matrix at a time, each on the path its format takes), so a
+// matrix's arithmetic depends only on its format and the switch, never on T.
 static int gemv(wl_ctx *c, const wl::GemvMat *mats, int nmat, int nm, const float *d_x, int cols, int T,
                 void *fixed = nullptr) {
+  if (c->float_mma) {
+    if (wl::fmma_applies(mats, nmat, nm, cols)) {
+      const int64_t nf = wl::fmma_scratch_floats(mats, nmat, nm, cols, T);
+      void *part = nullptr;
+      if (int rc = scratch_for(c, S_PART, (size_t)nf * sizeof(float), fixed, &part)) return rc;
+      WL_HIP(wl::fmma_run(mats, nmat, nm, d_x, cols, cols, T, (float *)part, c->num_cu, c->stream), "gemv launch");
+      return WL_OK;
+    }
+    bool any = false;
+    for (int i = 0; i < nmat; i++) any = any || wl::fmma_applies(&mats[i], 1, nm, cols);
+    if (any && nmat > 1) {
+      for (int i = 0; i < nmat; i++)
+        if (int rc = gemv(c, &mats[i], 1, nm, d_x, cols, T, fixed)) return rc;
+      return WL_OK;
+    }
+  }
   const int64_t nf = wl::gemv_scratch_floats(mats, nmat, nm, cols, T);
   void *part = nullptr;
   if (nf > 0)
@@ -986,6 +1007,12 @@ extern "C" int wl_debug_moe_patience(wl_ctx *c, int32_t polls) {
 extern "C" int wl_set_moe_one_launch(wl_ctx *c, int on) {
   if (!c) return fail(WL_E_ARG, "wl_set_moe_one_launch: null context");
   c->moe_chain = on ? 0 : 1;
+  return WL_OK;
+}
+
+extern "C" int wl_set_float_mma(wl_ctx *c, int on) {
+  if (!c) return fail(WL_E_ARG, "wl_set_float_mma: null context");
+  c->float_mma = on ? 1 : 0;
   return WL_OK;
 }
 
