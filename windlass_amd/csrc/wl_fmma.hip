@@ -204,7 +204,7 @@ struct FQ4K {
 // (q - 32) sl and (q - 32) sh for the two accumulators.
 struct FQ6K {
   static constexpr int BYTES = 210;
-  struct Raw { Win<16> l1, l2, qh; Win<8> sc; uint32_t dw; };
+  struct Raw { Win<16> l1, l2, qh; Win<8> sc; uint32_t dw; };  // sc: the half's 8 scales
 
   __device__ static int prep_offset(int sb, int e) { return 256 * sb + 128 * (e >> 2) + 32 * (e & 3); }
   // lane (sb, e): group g = e % 4 of half hh = e / 4, 32 values -> quarters 2hh + ih, MFMAs 2g + p
@@ -271,6 +271,7 @@ struct FQ6K {
         Cl = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl, Cl, 0, 0, 0);
         Ch = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh, Ch, 0, 0, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);  // one group's operands live at a time
     }
     const float d = half_lo(r.l1.sh ? (r.dw >> 16) : r.dw);
 #pragma unroll
@@ -279,46 +280,86 @@ struct FQ6K {
 };
 
 // ------------------------------------------------------------------------------------ kernel
-// The tiles of one matrix (pair) in this workgroup's unit: wave wv takes tiles wgx * 8 + wv,
-// + nwg * 8, ...; the next super-block's weights are loaded while the current one is computed
-// (every load issued, the last super-block re-read, so the load counters' waits stay exact).
+// Loads in flight per wave: PF work items (one matrix's super-block) ahead of the one computed,
+// as many as the register budget (128 VGPRs, four waves per SIMD) holds without spilling.
+#ifndef WL_FMMA_PF_Q4K
+#define WL_FMMA_PF_Q4K 1
+#endif
+#ifndef WL_FMMA_PF_Q6K
+#define WL_FMMA_PF_Q6K 1
+#endif
 template <class C, int NM>
-__device__ __forceinline__ void fmma_tiles(const BatchArgs &a, const BatchMat &M, int wgx, int nwg,
-                                           const uint8_t *lds, const float *inv) {
+constexpr int fmma_ahead() {
+  return NM == 2 ? 1 : C::BYTES == 144 ? WL_FMMA_PF_Q4K : WL_FMMA_PF_Q6K;
+}
+
+template <class C>
+__device__ __forceinline__ void fmma_prep(const BatchArgs &a, uint8_t *lds, float *inv) {
+  const int wv = threadIdx.x >> 6, u = blockIdx.y;
+  const int n = a.cols - u * FM_UNIT < FM_UNIT ? a.cols - u * FM_UNIT : FM_UNIT;
+  if (wv < a.T) {
+    const float iv = prep_token<C>(a.x + (int64_t)wv * a.ldx + (int64_t)u * FM_UNIT, n, wv, lds);
+    if ((threadIdx.x & 63) == 0) inv[wv] = iv;
+  } else {
+    prep_zero(wv, lds);
+  }
+}
+
+// One workgroup's work: the tokens' x parts of its unit into LDS, then the tiles of one matrix
+// (pair): wave wv takes tiles wgx * 8 + wv, + nwg * 8, .... The unit's items (super-block b,
+// matrix m, in that order) are computed with the loads of the next PF items in flight; the
+// first tile's first loads are issued before the x parts are prepared.
+template <class C, int NM>
+__device__ __forceinline__ void fmma_body(const BatchArgs &a, const BatchMat &M, int wgx, int nwg, uint8_t *lds,
+                                          float *inv) {
+  constexpr int PF = fmma_ahead<C, NM>();
+  // a ring of PF + 1 load buffers; a loop body of K items keeps every buffer's role and every
+  // item's matrix fixed at compile time. Past the last item the last one is re-read (valid
+  // memory, unused), so every load is issued and the load counters' waits stay exact.
+  constexpr int K = (PF + 1) % NM == 0 ? PF + 1 : (PF + 1) * NM;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int q = lane >> 4, rr = lane & 15, u = blockIdx.y;
   const int rem = (a.cols - u * FM_UNIT) / 256;
-  const int nsb = rem < 8 ? rem : 8;
-  const int ntiles = (M.rows + 15) / 16;
-  for (int tile = wgx * FM_WAVES + wv; tile < ntiles; tile += nwg * FM_WAVES) {
+  const int nsb = rem < 8 ? rem : 8, NI = nsb * NM;
+  const int ntiles = (M.rows + 15) / 16, first = wgx * FM_WAVES + wv;
+  const uint8_t *wr[NM];
+  auto rows_of = [&](int tile) {
     const int row = min(tile * 16 + rr, M.rows - 1);
-    const uint8_t *wr[NM];
     wr[0] = M.w + (int64_t)row * M.row_bytes + (int64_t)u * 8 * C::BYTES;
     if constexpr (NM == 2) wr[1] = M.w2 + (int64_t)row * M.row_bytes + (int64_t)u * 8 * C::BYTES;
+  };
+  typename C::Raw rg[PF + 1];
+  auto preload = [&]() {
+#pragma unroll
+    for (int i = 0; i < PF; i++) {
+      const int j = i < NI ? i : NI - 1;
+      C::load(wr[i % NM] + (int64_t)(j / NM) * C::BYTES, q, rg[i]);
+    }
+  };
+  if (first < ntiles) {
+    rows_of(first);
+    preload();
+  }
+  fmma_prep<C>(a, lds, inv);
+  __syncthreads();
+  for (int tile = first; tile < ntiles; tile += nwg * FM_WAVES) {
+    if (tile != first) {
+      rows_of(tile);
+      preload();
+    }
     ff4 acc[NM];
 #pragma unroll
     for (int m = 0; m < NM; m++) acc[m] = ff4{0.f, 0.f, 0.f, 0.f};
-    typename C::Raw ra, rb;
-    C::load(wr[0], q, ra);
-    if constexpr (NM == 1) {
 #pragma unroll 1
-      for (int b = 0; b < nsb; b += 2) {
-        const int b1 = b + 1 < nsb ? b + 1 : nsb - 1, b2 = b + 2 < nsb ? b + 2 : nsb - 1;
-        C::load(wr[0] + (int64_t)b1 * C::BYTES, q, rb);
-        C::step(ra, q, rr, lds, b, acc[0]);
-        if (b + 1 >= nsb) break;  // uniform
-        C::load(wr[0] + (int64_t)b2 * C::BYTES, q, ra);
-        C::step(rb, q, rr, lds, b + 1, acc[0]);
-      }
-    } else {
-      // gate and up of a super-block in turn, each loaded during the other's work
-#pragma unroll 1
-      for (int b = 0; b < nsb; b++) {
-        const int b1 = b + 1 < nsb ? b + 1 : nsb - 1;
-        C::load(wr[1] + (int64_t)b * C::BYTES, q, rb);
-        C::step(ra, q, rr, lds, b, acc[0]);
-        C::load(wr[0] + (int64_t)b1 * C::BYTES, q, ra);
-        C::step(rb, q, rr, lds, b, acc[1]);
+    for (int base = 0; base < NI; base += K) {
+#pragma unroll
+      for (int k = 0; k < K; k++) {
+        const int i = base + k;
+        if (i < NI) {  // uniform
+          const int j = i + PF < NI ? i + PF : NI - 1;
+          C::load(wr[(k + PF) % NM] + (int64_t)(j / NM) * C::BYTES, q, rg[(k + PF) % (PF + 1)]);
+          C::step(rg[k % (PF + 1)], q, rr, lds, i / NM, acc[k % NM]);
+        }
       }
     }
     const int r = tile * 16 + rr;
@@ -334,18 +375,6 @@ __device__ __forceinline__ void fmma_tiles(const BatchArgs &a, const BatchMat &M
   }
 }
 
-template <class C>
-__device__ __forceinline__ void fmma_prep(const BatchArgs &a, uint8_t *lds, float *inv) {
-  const int wv = threadIdx.x >> 6, u = blockIdx.y;
-  const int n = a.cols - u * FM_UNIT < FM_UNIT ? a.cols - u * FM_UNIT : FM_UNIT;
-  if (wv < a.T) {
-    const float iv = prep_token<C>(a.x + (int64_t)wv * a.ldx + (int64_t)u * FM_UNIT, n, wv, lds);
-    if ((threadIdx.x & 63) == 0) inv[wv] = iv;
-  } else {
-    prep_zero(wv, lds);
-  }
-}
-
 // KINDS: the formats present (1: Q4_K, 2: Q6_K, 3: both, the fused q/k/v of a Q4_K_M layer);
 // a kernel holds only the codecs it needs, so each stays within its register budget.
 template <int NM, int KINDS>
@@ -355,14 +384,11 @@ __global__ __launch_bounds__(64 * FM_WAVES) __attribute__((amdgpu_waves_per_eu(4
   const int mi = batch_mat(a);
   const BatchMat &M = a.m[mi];
   const int wgx = (int)blockIdx.x - M.wg_begin, nwg = batch_nwg(a, mi);
-  const bool q4 = KINDS == 1 || (KINDS == 3 && M.type == 12);
-  if (q4) fmma_prep<FQ4K>(a, lds, inv);
-  else fmma_prep<FQ6K>(a, lds, inv);
-  __syncthreads();
+  const bool q4 = KINDS == 1 || (KINDS == 3 && M.type == 12);  // uniform over the workgroup
   if constexpr (KINDS & 1)
-    if (q4) fmma_tiles<FQ4K, NM>(a, M, wgx, nwg, lds, inv);
+    if (q4) fmma_body<FQ4K, NM>(a, M, wgx, nwg, lds, inv);
   if constexpr ((KINDS & 2) != 0)
-    if (!q4) fmma_tiles<FQ6K, NM>(a, M, wgx, nwg, lds, inv);
+    if (!q4) fmma_body<FQ6K, NM>(a, M, wgx, nwg, lds, inv);
 }
 
 template <int NM, int KINDS>

@@ -330,7 +330,7 @@ static __global__ __launch_bounds__(256) void batch_combine_kernel(BatchArgs a) 
 
 // Workgroups per matrix along x: about WL_BATCH_WPC waves per CU over all columns, split over
 // the matrices in proportion to their row groups. Returns the grid's x size.
-static int plan_batch(BatchArgs &a, int R, int num_cu) {
+static inline int plan_batch(BatchArgs &a, int R, int num_cu) {
   int total = 0;
   for (int i = 0; i < a.nmat; i++) total += (a.m[i].rows + R - 1) / R;
   const int target = (num_cu * WL_BATCH_WPC / kBatchWaves + a.u - 1) / a.u;
