@@ -847,6 +847,7 @@ def run_decode_batch(args):
              "up": "ffn_up", "down": "ffn_down"}
     L = windlass_amd.load()
     ctx = Context(0)
+    ctx.FloatMma = args.float_mma
     dev = torch.device("cuda:0")
 
     def norm():
@@ -888,7 +889,7 @@ def run_decode_batch(args):
             "data": "synthetic seeded GGUF blocks; random prompt ids; random-init norms",
             "config": {"workload": "Llama-3.3-70B Q4_K_M: %d layers, vocab 128256, %d sequences, prompt %d each, "
                                    "then %d timed stacked steps" % (args.layers, N, args.prompt, args.tokens),
-                       "batch": N},
+                       "batch": N, "float_mma": bool(args.float_mma)},
             "tokens_per_s_per_sequence": round(1.0 / per_step, 2), "ms_per_layer": round(per_step * 1e3 / args.layers, 4)}
     print(json.dumps(line), flush=True)
     for w in weights.values():

@@ -6,6 +6,8 @@ the CPU with the C oracle and the library's CPU-side entry points only.
 import os
 import sys
 
+import pytest
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 for p in (ROOT, os.path.join(ROOT, "oracle")):
     if p not in sys.path:
@@ -14,3 +16,20 @@ for p in (ROOT, os.path.join(ROOT, "oracle")):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X GPU and the built HIP library")
+
+
+_TORCH_FIRST = []
+
+
+@pytest.hookimpl(tryfirst=True)
+def pytest_runtest_setup(item):
+    """In a process that runs GPU tests, torch's HIP runtime initialises the GPU before the
+    library's first call does (a torch tensor is made on cuda:0 before the first GPU test's
+    fixtures run): torch's device initialisation after the library's has failed with
+    "No HIP GPUs are available"."""
+    if item.get_closest_marker("gpu") is None or _TORCH_FIRST:
+        return
+    _TORCH_FIRST.append(True)
+    import torch
+    if torch.cuda.device_count() > 0:
+        torch.zeros(1, device="cuda:0")

@@ -359,8 +359,8 @@ __device__ __forceinline__ bool moe_wait_ge(unsigned *p, unsigned v, MoeSync *sy
 }
 
 // One atomic add by the wave's lane 0; the old value goes to every lane of the wave. The
-// caller has made the workgroup's stores visible at agent scope first (every wave's agent-scope
-// release fence before the workgroup barrier that precedes the arrival).
+// caller has made the workgroup's stores visible at agent scope first (every wave waits for its
+// agent-scope stores to complete before the workgroup barrier that precedes the arrival).
 __device__ __forceinline__ unsigned moe_arrive(unsigned *p) {
   unsigned old = 0;
   if ((threadIdx.x & 63) == 0) old = atomicAdd(p, 1u);
@@ -570,6 +570,13 @@ __global__ __launch_bounds__(64 * kMoeWaves) void moe_fused_kernel(MoeFusedArgs 
     const CsIO io{a.x, pl.slot_tok[s], a.embd, a.h, pl.slot_pair[s], a.ff, pl.slot_ntok[s]};
     cs_group_wave<CG, TM, RG, 2, true>(W, io, a.embd, g, s_part[wv]);
   }
+  // every wave's h stores (agent-scope stores, written through to the point of coherence) have
+  // completed before the workgroup barrier, so wave 0's arrival below follows all of them: the
+  // wave waits for its outstanding memory operations (gfx9's vmcnt counts stores), which is the
+  // whole of an agent-scope release for such stores (no cache write-back: nothing the other
+  // workgroups read was stored through the cache)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt and lgkmcnt not waited for
   // this wave's first down row group (group w, slot wv): one dword of each of its weights'
   // 128-byte lines, read across the barrier so the lines are in the caches when phase 3 reads them
   const int gd = (a.embd + RD - 1) / RD;
@@ -583,9 +590,6 @@ __global__ __launch_bounds__(64 * kMoeWaves) void moe_fused_kernel(MoeFusedArgs 
       touch = *reinterpret_cast<const uint32_t *>(row + (off & ~(int64_t)3));
     }
   }
-  // every wave's h stores complete at agent scope (the fence waits for them) before the
-  // workgroup barrier, so wave 0's arrival below follows all of them
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
   if (wv == 0) {  // grid barrier
     const int nsub = G < MOE_SYNC_SUB ? G : MOE_SYNC_SUB, sub = w % nsub;
