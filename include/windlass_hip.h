@@ -367,6 +367,21 @@ int wl_layer_batch_dev(wl_ctx *ctx, const wl_layer_desc *layer, float *d_x, int3
 int wl_matmul_dev_noalloc(wl_ctx *ctx, const wl_weight *w, int32_t expert, const float *d_x, int32_t T,
                           float *d_y);
 
+/* ---- Replayed step (no counterpart in the reference; it serves the per-token loop of
+ * src/Engine.cs:198-203, one Model.Forward per generated token) ----
+ * wl_capture_begin starts recording the context's stream; every _dev call until wl_capture_end
+ * is recorded, not run, and wl_capture_end returns the recording as one graph. wl_graph_launch
+ * replays it on the context's stream: the same kernels with the same arguments (the same device
+ * buffers, the same weights), enqueued by one host call. A call that would grow the context's
+ * scratch during a capture fails with WL_E_ARG (run the same calls once before capturing), and
+ * the MoE entries take their launch chain while capturing (the same bits as one launch).
+ * Host-buffer entries synchronise and must not be called while capturing. */
+typedef struct wl_graph wl_graph;
+int wl_capture_begin(wl_ctx *ctx);
+int wl_capture_end(wl_ctx *ctx, wl_graph **out);
+int wl_graph_launch(wl_ctx *ctx, const wl_graph *g);
+int wl_graph_free(wl_graph *g);
+
 /* ---- Calibration (no counterpart in the reference) ----
  * A plain streaming read of `bytes` (a multiple of 16) of device memory at d_src by `workgroups`
  * workgroups of 256 threads (0: eight per CU), each over one contiguous chunk with nontemporal

@@ -28,10 +28,10 @@ failure). There is no CPU fallback: without the built library every call raises.
 """
 from ._lib import (ArgumentOutOfRangeError, BackendError, NotSupportedError, ShapeError,
                    library_path, load)
-from .backend import (Context, FastMath, GgmlType, HostBuffer, LayerDesc, QActs, Quants, Stage, Transformer,
-                      WeightView, layout)
+from .backend import (Context, FastMath, GgmlType, Graph, HostBuffer, LayerDesc, QActs, Quants, Stage,
+                      Transformer, WeightView, layout)
 from .model import DeviceBatch, DeviceTransformer, ModelConfig, StageStream
 
 __all__ = ["ArgumentOutOfRangeError", "BackendError", "NotSupportedError", "ShapeError",
-           "library_path", "load", "Context", "FastMath", "GgmlType", "HostBuffer", "LayerDesc", "QActs", "Quants", "Stage",
+           "library_path", "load", "Context", "FastMath", "GgmlType", "Graph", "HostBuffer", "LayerDesc", "QActs", "Quants", "Stage",
            "Transformer", "WeightView", "layout", "DeviceBatch", "DeviceTransformer", "ModelConfig", "StageStream"]

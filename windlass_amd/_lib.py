@@ -61,6 +61,10 @@ SIGNATURES = {
     "wl_moe_ffn_dev": (ctypes.c_int, [P, P, I32, I32, P, P, P, P, I32, P]),
     "wl_read_peak_dev": (ctypes.c_int, [P, P, I64, I32, P]),
     "wl_matmul_dev_noalloc": (ctypes.c_int, [P, P, I32, P, I32, P]),
+    "wl_capture_begin": (ctypes.c_int, [P]),
+    "wl_capture_end": (ctypes.c_int, [P, P]),
+    "wl_graph_launch": (ctypes.c_int, [P, P]),
+    "wl_graph_free": (ctypes.c_int, [P]),
 }
 
 WL_E_UNSUPPORTED, WL_E_SHAPE, WL_E_DEVICE, WL_E_ARG, WL_E_NOMEM = -1, -2, -3, -4, -5

@@ -180,6 +180,46 @@ class Context:
         """A LayerStream slot of nbytes in HBM (src/LayerStream.cs:36-124)."""
         return Stage(self, nbytes)
 
+    def capture(self, fn):
+        """Records the _dev calls fn() makes on this context into a Graph instead of running
+        them (wl_capture_begin / wl_capture_end); Graph.launch() replays them with one host call,
+        as the engine's per-token loop would (src/Engine.cs:198-203). A failure inside fn ends
+        the recording and is raised."""
+        check(self._lib.wl_capture_begin(self.handle))
+        try:
+            fn()
+        except BaseException:
+            g = ctypes.c_void_p()
+            self._lib.wl_capture_end(self.handle, ctypes.byref(g))
+            if g.value:
+                self._lib.wl_graph_free(g)
+            raise
+        g = ctypes.c_void_p()
+        check(self._lib.wl_capture_end(self.handle, ctypes.byref(g)))
+        return Graph(self, g)
+
+
+class Graph:
+    """A recorded run of _dev calls: the same kernels on the same buffers at every launch()."""
+
+    def __init__(self, ctx, handle):
+        self.ctx = ctx
+        self.handle = handle
+
+    def launch(self):
+        check(load().wl_graph_launch(self.ctx.handle, self.handle))
+
+    def free(self):
+        if self.handle:
+            check(load().wl_graph_free(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
 
 class HostBuffer:
     """Pinned host memory as a uint8 numpy array (the slot buffers LayerStream reads stages

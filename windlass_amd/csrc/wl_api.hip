@@ -64,6 +64,7 @@ struct wl_ctx {
   int int_dot;  // Transformer.IntDot (src/Transformer.cs:23)
   int float_mma;  // wl_set_float_mma: Q4_K / Q6_K decode GEMVs of 1-8 tokens on the matrix cores
   int moe_chain;  // wl_set_moe_one_launch(0): the MoE entries always run the launch chain
+  bool capturing = false;  // between wl_capture_begin and wl_capture_end
   unsigned moe_launches;  // one-launch MoE launches so far (their counter sets alternate)
   bool moe_unchecked;     // one-launch MoE launches since the err word was last read
   int moe_spin = wl::MOE_SPIN;  // polls of the one-launch MoE's bounded waits
@@ -198,6 +199,9 @@ extern "C" int wl_debug_fail_alloc(int n) {
 
 static int ensure(wl_ctx *c, int slot, size_t bytes) {
   if (c->cap[slot] >= bytes) return WL_OK;
+  if (c->capturing)
+    return fail(WL_E_ARG, "a captured call needs %zu bytes of scratch slot %d, which holds %zu: run the same calls "
+                "once before the capture", bytes, slot, c->cap[slot]);
   if (c->buf[slot]) {
     hipStreamSynchronize(c->stream);
     hipFree(c->buf[slot]);
@@ -940,7 +944,9 @@ static int moe_dev(wl_ctx *c, const float *d_logits, int32_t k, int32_t renorm, 
     m.d_int = c->int_dot && wl::intdot_supports(d->type) && wl::intdot_fits(d->type, ff);
     m.qx = wl::qacts_at(b + s.qx, Tc, embd, wl::intdot_needs_k(g->type) ? 1 : 0);
     m.qh = wl::qacts_at(b + s.qh, Tc * k, ff, wl::intdot_needs_k(d->type) ? 1 : 0);
-    m.sync = c->moe_chain ? nullptr : (wl::MoeSync *)c->buf[S_MSYNC];
+    // a captured graph replays fixed arguments, and the one launch's counter sets alternate
+    // from call to call: captures take the launch chain (the same bits)
+    m.sync = c->moe_chain || c->capturing ? nullptr : (wl::MoeSync *)c->buf[S_MSYNC];
     m.parity = (int)(c->moe_launches & 1);
     m.spin = c->moe_spin;
     // only a one-launch launch uses a counter set (and clears the other for the next one), so
@@ -1371,4 +1377,49 @@ extern "C" int wl_read_peak_dev(wl_ctx *c, const void *d_src, int64_t bytes, int
   WL_HIP(hipSetDevice(c->device), "hipSetDevice");
   WL_HIP(wl::read_peak_launch(d_src, bytes, wgs, d_out, c->stream), "read_peak_kernel");
   return WL_OK;
+}
+
+// ------------------------------------------------------------------------------ graphs
+// A run of _dev calls captured once from the context's stream and replayed as one graph launch:
+// the host enqueues one command instead of one per kernel.
+struct wl_graph {
+  hipGraphExec_t exec;
+};
+
+extern "C" int wl_capture_begin(wl_ctx *c) {
+  if (!c) return fail(WL_E_ARG, "wl_capture_begin: null context");
+  if (c->capturing) return fail(WL_E_ARG, "wl_capture_begin: the context is already capturing");
+  WL_HIP(hipSetDevice(c->device), "hipSetDevice");
+  WL_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  c->capturing = true;
+  return WL_OK;
+}
+
+extern "C" int wl_capture_end(wl_ctx *c, wl_graph **out) {
+  if (!c || !out) return fail(WL_E_ARG, "wl_capture_end: null argument");
+  *out = nullptr;
+  if (!c->capturing) return fail(WL_E_ARG, "wl_capture_end: the context is not capturing");
+  c->capturing = false;
+  hipGraph_t g = nullptr;
+  WL_HIP(hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture (a call during the capture failed or synchronised)");
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) return fail(WL_E_DEVICE, "hipGraphInstantiate: %s", hipGetErrorString(e));
+  *out = new wl_graph{exec};
+  return WL_OK;
+}
+
+extern "C" int wl_graph_launch(wl_ctx *c, const wl_graph *g) {
+  if (!c || !g) return fail(WL_E_ARG, "wl_graph_launch: null argument");
+  if (c->capturing) return fail(WL_E_ARG, "wl_graph_launch: the context is capturing");
+  WL_HIP(hipGraphLaunch(g->exec, c->stream), "hipGraphLaunch");
+  return WL_OK;
+}
+
+extern "C" int wl_graph_free(wl_graph *g) {
+  if (!g) return WL_OK;
+  const hipError_t e = hipGraphExecDestroy(g->exec);
+  delete g;
+  return e == hipSuccess ? WL_OK : fail(WL_E_DEVICE, "hipGraphExecDestroy: %s", hipGetErrorString(e));
 }
