@@ -66,6 +66,9 @@ struct Q4K {
     int j, h, sh;
     bool jlo;
     uint32_t m1, m2;
+    // the header permute: t1 = bytes (b, b+1) of scales 0-3 and of scales 4-7, t3 = bytes
+    // (b, b+1) of scales 8-11 twice, b = 2j (j < 2) or 2j - 4
+    uint32_t selA, selW, mA, mB, mC, mD;
   };
   struct Xs { float lo[16], hi[16], slo, shi; };
   struct Raw { uint4 hdr, q; };
@@ -79,6 +82,13 @@ struct Q4K {
     L.jlo = L.j < 2;
     L.m1 = L.jlo ? 0x3F3F3F3Fu : 0x0F0F0F0Fu;
     L.m2 = L.jlo ? 0u : 0x30303030u;
+    const uint32_t b = L.jlo ? 2 * L.j : 2 * L.j - 4;
+    L.selA = b | (b + 1) << 8 | (b + 4) << 16 | (b + 5) << 24;
+    L.selW = b | (b + 1) << 8 | b << 16 | (b + 1) << 24;
+    L.mA = L.jlo ? 0x3F3F3F3Fu : 0u;
+    L.mB = L.jlo ? 0u : 0x30303030u;
+    L.mC = L.jlo ? 0u : 0x00000F0Fu;
+    L.mD = L.jlo ? 0u : 0x0F0F0000u;
     return L;
   }
 
@@ -102,18 +112,18 @@ struct Q4K {
 
   __device__ static void unpack(const Raw &r, const Lane &L, const Lds &, W &w) {
     const uint4 h = r.hdr;
-    // The 6-bit scale and min of sub-blocks 2j and 2j+1 (get_scale_min_k4,
-    // src/Quants.cs:321-330): sub-blocks 0-3 are the low 6 bits of bytes 0-7; 4-7 take their
-    // low 4 bits from bytes 8-11 and the top two from the top of bytes 0-7. The lane's j is
-    // fixed, so both cases are one masked form with lane-constant masks.
-    const uint32_t P = L.jlo ? h.y : h.w;
-    const uint32_t Q = L.jlo ? h.z : (h.w >> 4);
-    const uint32_t S = ((P & L.m1) | ((h.y >> 2) & L.m2)) >> L.sh;
-    const uint32_t M = ((Q & L.m1) | ((h.z >> 2) & L.m2)) >> L.sh;
-    w.fs1 = (float)(S & 0xFF);
-    w.fs2 = (float)((S >> 8) & 0xFF);
-    w.fm1 = (float)(M & 0xFF);
-    w.fm2 = (float)((M >> 8) & 0xFF);
+    // The 6-bit scales and mins of sub-blocks 2j and 2j+1 (get_scale_min_k4,
+    // src/Quants.cs:321-330) as the four bytes of one word: sub-blocks 0-3 are the low 6 bits
+    // of bytes 0-7; 4-7 take their low 4 bits from bytes 8-11 and the top two from the top of
+    // bytes 0-7. Two byte permutes with lane-constant selectors gather the lane's bytes, and
+    // lane-constant masks keep what each case takes; each byte then converts on its own.
+    const uint32_t t1 = __builtin_amdgcn_perm(h.z, h.y, L.selA);
+    const uint32_t t3 = __builtin_amdgcn_perm(h.w, h.w, L.selW);
+    const uint32_t W4 = (t1 & L.mA) | ((t1 >> 2) & L.mB) | (t3 & L.mC) | ((t3 >> 4) & L.mD);
+    w.fs1 = (float)(W4 & 0xFF);
+    w.fs2 = (float)((W4 >> 8) & 0xFF);
+    w.fm1 = (float)((W4 >> 16) & 0xFF);
+    w.fm2 = (float)(W4 >> 24);
     w.d = half_lo(h.x);
     w.dmin = half_hi(h.x);
     const uint32_t qq[4] = {r.q.x, r.q.y, r.q.z, r.q.w};

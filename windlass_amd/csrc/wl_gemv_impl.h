@@ -141,12 +141,16 @@ inline size_t cs_lds_bytes(int nwv) {
 template <class C, int R, int NM>
 __device__ __forceinline__ void cs_load(const CsRows &W, int g, int b, const typename C::Lane &L,
                                         typename C::Raw (&raw)[NM][R]) {
+  // the row's base is uniform and the lane's offset a 32-bit value, so the loads can take a
+  // scalar base address with a vector offset (no 64-bit address arithmetic per row)
+  const uint32_t off = (uint32_t)b * (uint32_t)C::BYTES;
 #pragma unroll
   for (int m = 0; m < NM; m++)
 #pragma unroll
     for (int r = 0; r < R; r++) {
       const int row = min(g * R + r, W.rows - 1);
-      C::load((m ? W.w2 : W.w) + (int64_t)row * W.row_bytes + (int64_t)b * C::BYTES, L, raw[m][r]);
+      const uint8_t *rowp = (m ? W.w2 : W.w) + (int64_t)row * W.row_bytes;
+      C::load(rowp + off, L, raw[m][r]);
     }
 }
 
