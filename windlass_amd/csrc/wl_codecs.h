@@ -168,7 +168,7 @@ struct Q4K {
 #endif
 struct Q6K {
   static constexpr int BLOCK = 256, BYTES = 210, LPB = 8, NEED_LDS = 0, R1 = WL_Q6K_R1, SP2 = WL_Q6K_SP2;
-  struct Lane { int hh, g, s; };
+  struct Lane { int hh, g, s; uint32_t ssel; };
   struct Xs { float v[4][8]; float s[4]; };
   // the aligned dwords around each 2-byte-aligned field, and the byte shift (0 or 16)
   struct Raw { uint32_t l1[3], l2[3], h[3], sc[3], dw; uint32_t sh; };
@@ -179,6 +179,7 @@ struct Q6K {
     L.hh = sub >> 2;
     L.g = sub & 3;
     L.s = L.g >> 1;
+    L.ssel = (uint32_t)L.s | (uint32_t)(L.s + 2) << 8 | (uint32_t)(L.s + 4) << 16 | (uint32_t)(L.s + 6) << 24;
     return L;
   }
 
@@ -216,10 +217,11 @@ struct Q6K {
   __device__ static void unpack(const Raw &r, const Lane &L, const Lds &, W &w) {
     const uint2 ql1 = field(r.l1, r.sh), ql2 = field(r.l2, r.sh), qh = field(r.h, r.sh), sc = field(r.sc, r.sh);
     const float d = half_lo(r.sh ? (r.dw >> 16) : r.dw);
-    // signed scale bytes s, s+2 (first dword) and s+4, s+6 (second dword)
-    const int s = L.s;
-    const float scs[4] = {(float)(int8_t)(sc.x >> (8 * s)), (float)(int8_t)(sc.x >> (8 * s + 16)),
-                          (float)(int8_t)(sc.y >> (8 * s)), (float)(int8_t)(sc.y >> (8 * s + 16))};
+    // signed scale bytes s, s+2 (first dword) and s+4, s+6 (second dword), gathered into one
+    // word by a byte permute with a lane-constant selector
+    const uint32_t sg = __builtin_amdgcn_perm(sc.y, sc.x, L.ssel);
+    const float scs[4] = {(float)(int8_t)sg, (float)(int8_t)(sg >> 8), (float)(int8_t)(sg >> 16),
+                          (float)(int8_t)(sg >> 24)};
 #pragma unroll
     for (int k = 0; k < 4; k++) w.dq[k] = d * scs[k];
     const uint32_t L1[2] = {ql1.x, ql1.y}, L2[2] = {ql2.x, ql2.y}, QH[2] = {qh.x, qh.y};
@@ -234,8 +236,8 @@ struct Q6K {
       const uint32_t q4[4] = {a, b, c, e};
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        w.p[k][2 * i + 0] = q4[k] & 0x00FF00FFu;         // bytes 0, 2 as subnormal halves
-        w.p[k][2 * i + 1] = (q4[k] >> 8) & 0x00FF00FFu;  // bytes 1, 3
+        w.p[k][2 * i + 0] = q4[k] & 0x00FF00FFu;                          // bytes 0, 2 as subnormal halves
+        w.p[k][2 * i + 1] = __builtin_amdgcn_perm(q4[k], q4[k], 0x0C030C01u);  // bytes 1, 3 (zero-filled)
       }
     }
   }
@@ -299,7 +301,7 @@ struct Q80 {
       // int8 q + 128 as an unsigned byte, then bytes 0,2 / 1,3 as subnormal halves
       const uint32_t v = __builtin_amdgcn_alignbit(hi, lo, 16) ^ 0x80808080u;
       w.p[2 * i] = v & 0x00FF00FFu;
-      w.p[2 * i + 1] = (v >> 8) & 0x00FF00FFu;
+      w.p[2 * i + 1] = __builtin_amdgcn_perm(v, v, 0x0C030C01u);  // bytes 1, 3 (zero-filled)
     }
   }
 
