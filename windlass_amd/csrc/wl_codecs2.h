@@ -123,7 +123,7 @@ typedef Q32<24, 8, 4, true> Q51;
 // IQ4_NL (src/IQuants.cs:45-58): y = d * kvalues[n], through IQ4_XS's LDS table of
 // (kvalue[low] + 128, kvalue[high] + 128) fp16 pairs indexed by a whole qs byte.
 struct IQ4NL {
-  static constexpr int BLOCK = 32, BYTES = 18, LPB = 1, NEED_LDS = 1, R1 = 4, SP2 = 1;
+  static constexpr int BLOCK = 32, BYTES = 18, LPB = 1, NEED_LDS = 2, R1 = 4, SP2 = 1;
   struct Lane {};
   struct Xs { float v[32]; float s; };
   typedef Raw32<18> Raw;

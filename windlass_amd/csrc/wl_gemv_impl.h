@@ -130,10 +130,21 @@ struct CsIO {
 #endif
 constexpr int GS = WL_GEMV_GROUPS_PER_SYNC;
 
-// Dynamic LDS of a launch: the codec tables, then the double-buffered wave partials.
+// Dynamic LDS of a launch: the codec tables (NEED_LDS 1), then the double-buffered wave partials.
+template <class C>
+constexpr size_t dyn_table_bytes() {
+  return C::NEED_LDS == 1 ? sizeof(Lds) : 0;
+}
 template <class C, int TM, int R, int NM>
 inline size_t cs_lds_bytes(int nwv) {
-  return (C::NEED_LDS ? sizeof(Lds) : 0) + sizeof(float) * 2 * GS * nwv * NM * R * TM;
+  return dyn_table_bytes<C>() + sizeof(float) * 2 * GS * nwv * NM * R * TM;
+}
+
+// The codec's tables: static LDS (NEED_LDS 2) or the start of the dynamic LDS.
+template <class C>
+__device__ __forceinline__ Lds &tables_of(uint8_t *lds_raw) {
+  if constexpr (C::NEED_LDS == 2) return codec_lds();
+  else return *reinterpret_cast<Lds *>(lds_raw);
 }
 
 // The weights of row group g for block column b: R rows of each of the NM matrices. Rows past
@@ -231,8 +242,8 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
   static_assert((1 << ilog2(V)) == V && V <= 64, "partials per lane must be a power of two <= 64");
   static_assert(SP == 0 || TM == 1, "stationary x slices are for one token");
   constexpr int BPW = 64 / C::LPB;
-  const Lds &lds = *reinterpret_cast<const Lds *>(lds_raw);
-  float *part = reinterpret_cast<float *>(lds_raw + (C::NEED_LDS ? sizeof(Lds) : 0));
+  const Lds &lds = tables_of<C>(lds_raw);
+  float *part = reinterpret_cast<float *>(lds_raw + dyn_table_bytes<C>());
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
   const int sub = lane % C::LPB, bslot = lane / C::LPB;
   const typename C::Lane L = C::lane(sub);
@@ -255,7 +266,7 @@ __device__ __forceinline__ void cs_gemv(const CsRows &W, const CsIO &io, int col
   }
 
   if constexpr (C::NEED_LDS) {
-    C::init_lds(*reinterpret_cast<Lds *>(lds_raw));
+    C::init_lds(tables_of<C>(lds_raw));
     __syncthreads();
   }
 

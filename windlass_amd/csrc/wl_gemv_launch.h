@@ -175,7 +175,7 @@ constexpr int xs_u4() {
 
 template <class C, int TM>
 __host__ __device__ constexpr size_t batch_lds_bytes() {
-  return (C::NEED_LDS ? sizeof(Lds) : 0) + (size_t)TM * xs_u4<C>() * 64 * 16;
+  return dyn_table_bytes<C>() + (size_t)TM * xs_u4<C>() * 64 * 16;
 }
 
 #ifndef WL_BATCH_WAVES
@@ -196,14 +196,14 @@ template <class C, int TM, int R, int NM>
 __device__ __forceinline__ void batch_body(const BatchArgs &a, const BatchMat &M, int wgx, int nwg) {
   constexpr int V = NM * R * TM, LOW = 6 - ilog2(V), BPW = 64 / C::LPB, NX = xs_u4<C>();
   static_assert((1 << ilog2(V)) == V && V <= 64, "partials per lane must be a power of two <= 64");
-  const Lds &lds = *reinterpret_cast<const Lds *>(wl_dyn_lds);
-  uint4 *xl = reinterpret_cast<uint4 *>(wl_dyn_lds + (C::NEED_LDS ? sizeof(Lds) : 0));  // [TM][NX][64]
+  const Lds &lds = tables_of<C>(wl_dyn_lds);
+  uint4 *xl = reinterpret_cast<uint4 *>(wl_dyn_lds + dyn_table_bytes<C>());  // [TM][NX][64]
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int c = blockIdx.y, nb = a.cols / C::BLOCK;
   const int sub = lane % C::LPB, b = c * BPW + lane / C::LPB;
   const bool live = b < nb;
   const typename C::Lane L = C::lane(sub);
-  if constexpr (C::NEED_LDS) C::init_lds(*reinterpret_cast<Lds *>(wl_dyn_lds));
+  if constexpr (C::NEED_LDS) C::init_lds(tables_of<C>(wl_dyn_lds));
   // stage: wave w prepares tokens w, w + kBatchWaves, ... as the one-token launch prepares its slice
   for (int t = wv; t < TM; t += kBatchWaves) {
     if (t < a.T && live) {
