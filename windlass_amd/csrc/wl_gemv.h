@@ -41,6 +41,7 @@ struct GemvSeg {
 struct GemvParams {
   GemvSeg seg[GEMV_MAX_SEGS];
   int nseg;
+  int ileave;  // the segments' workgroups interleaved in runs of 8 (set by the launch's grid plan)
   int cols;  // columns of every segment
   const float *x;
   int ldx;

@@ -12,7 +12,12 @@ namespace wl {
 
 extern "C" __shared__ uint8_t wl_dyn_lds[];
 
+// The launch's workgroup w belongs to segment find_seg(p): segments in consecutive ranges, or
+// (ILV, a launch whose grid plan set ileave) in runs of 8 taken in turn, so that workgroup j of
+// every segment is dispatched at about the same time and on the same XCD (j % 8).
+template <bool ILV = false>
 __device__ __forceinline__ int find_seg(const GemvParams &p) {
+  if constexpr (ILV) return ((int)blockIdx.x >> 3) % p.nseg;
   int si = 0;
 #pragma unroll
   for (int i = 1; i < GEMV_MAX_SEGS; i++)
@@ -22,17 +27,18 @@ __device__ __forceinline__ int find_seg(const GemvParams &p) {
 
 // split: the segment writes partials; for the SwiGLU pair the up partial follows the gate
 // partial at out + T * ldo.
-template <class C, int TM, int R, int NM, int SP, bool PIPE = false>
+template <class C, int TM, int R, int NM, int SP, bool PIPE = false, bool ILV = false>
 __device__ __forceinline__ void run_seg(const GemvParams &p, const GemvSeg &s, int split) {
   const CsRows W{s.w, s.w2, s.row_bytes, s.rows};
   float *y2 = (NM == 2 && split) ? s.out + (int64_t)p.T * s.ldo : nullptr;
   const CsIO io{p.x + s.col0, nullptr, p.ldx, s.out, nullptr, s.ldo, p.T, y2, split ? 0 : s.add, s.rs};
-  cs_gemv<C, TM, R, NM, SP, false, PIPE>(W, io, p.cols, (int)blockIdx.x - s.wg_begin, s.nwg, wl_dyn_lds);
+  const int local = ILV ? ((int)blockIdx.x / (8 * p.nseg)) * 8 + ((int)blockIdx.x & 7) : (int)blockIdx.x - s.wg_begin;
+  cs_gemv<C, TM, R, NM, SP, false, PIPE>(W, io, p.cols, local, s.nwg, wl_dyn_lds);
 }
 
-template <class C, int TM, int R, int NM, int SP, bool PIPE = false>
+template <class C, int TM, int R, int NM, int SP, bool PIPE = false, bool ILV = false>
 __global__ __launch_bounds__(64 * kMaxWaves) void gemv_kernel(GemvParams p, int split) {
-  run_seg<C, TM, R, NM, SP, PIPE>(p, p.seg[find_seg(p)], split);
+  run_seg<C, TM, R, NM, SP, PIPE, ILV>(p, p.seg[find_seg<ILV>(p)], split);
 }
 
 // Rows per group: V = NM*R*TM partials per lane go through the exchange butterfly.
@@ -56,12 +62,19 @@ static int plan_grid(GemvParams &p, RowsOf rows_of, int nwv, int num_cu) {
   int nwg = 0;
   for (int i = 0; i < p.nseg; i++) {
     int n = (int)(((int64_t)target * groups[i] + total - 1) / total);
+    // a multiple of the 8 XCDs (the dispatcher deals workgroup w to XCD w % 8)
+    n = (n + 7) & ~7;
     if (n < 1) n = 1;
     if (n > groups[i]) n = groups[i];
     p.seg[i].wg_begin = nwg;
     p.seg[i].nwg = n;
     nwg += n;
   }
+  // Segments of equal grids (the K-chunks of a split row) interleaved in runs of 8: row group g
+  // of every chunk is then computed at about the same time on one XCD, whose L2 serves the
+  // 128-byte line two neighbouring chunks share once.
+  p.ileave = p.nseg > 1 && p.seg[0].nwg % 8 == 0;
+  for (int i = 1; i < p.nseg; i++) p.ileave = p.ileave && p.seg[i].nwg == p.seg[0].nwg;
   return nwg;
 }
 
@@ -98,7 +111,11 @@ static hipError_t launch_one(GemvParams &p, int split, int num_cu, hipStream_t s
       const int nwg = plan_grid(p, [](int) { return 2; }, nwv, num_cu);
       if (nwg == 0) return hipSuccess;
       const size_t smem = cs_lds_bytes<C, 1, 2, 1>(nwv);
-      hipLaunchKernelGGL((gemv_kernel<C, 1, 2, 1, 1, true>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
+      // the K-chunks of a split row (equal segments) interleaved: see plan_grid
+      if (p.ileave)
+        hipLaunchKernelGGL((gemv_kernel<C, 1, 2, 1, 1, true, true>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
+      else
+        hipLaunchKernelGGL((gemv_kernel<C, 1, 2, 1, 1, true>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
       return hipGetLastError();
     }
   }
