@@ -7,6 +7,12 @@
 
 namespace wl {
 
+// their 4096-column chunks end inside 128-byte lines: split rows interleave their K-chunks
+template <>
+inline constexpr bool kInterleaved<IQ3S> = true;
+template <>
+inline constexpr bool kInterleaved<IQ2S> = true;
+
 const GemvOps *gemv_ops_k(int type) {
   static constexpr GemvOps q2k = gemv_ops_of<Q2K>(), q3k = gemv_ops_of<Q3K>(), q5k = gemv_ops_of<Q5K>(),
                            iq3s = gemv_ops_of<IQ3S>(), iq2s = gemv_ops_of<IQ2S>();

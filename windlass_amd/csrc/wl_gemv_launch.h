@@ -101,6 +101,16 @@ inline constexpr bool kPipelined = false;
 template <>
 inline constexpr bool kPipelined<Q6K> = true;
 
+// Codecs whose one-token split rows run with the K-chunks interleaved (plan_grid): those whose
+// 4096-column chunks do not end on 128-byte lines, where it measured faster (8192 x 28672, one
+// token: IQ2_XXS 32.3 -> 30.2 us, IQ2_S 49.6 -> 46.8, IQ3_S 50.1 -> 49.4; Q6_K through the
+// pipelined path; Q2_K 38.3 -> 42.6 and Q3_K within noise, so not those). The translation unit
+// that owns a codec sets it.
+template <class C>
+inline constexpr bool kInterleaved = false;
+template <>
+inline constexpr bool kInterleaved<IQ2XXS> = true;
+
 template <class C, int TM, int NM>
 static hipError_t launch_one(GemvParams &p, int split, int num_cu, hipStream_t st) {
   constexpr int R = rows_per_group<C, TM, NM>();
@@ -138,6 +148,12 @@ static hipError_t launch_r(GemvParams &p, int split, int num_cu, hipStream_t st)
   const int nwg = plan_grid(p, [](int) { return R; }, nwv, num_cu);
   if (nwg == 0) return hipSuccess;
   const size_t smem = cs_lds_bytes<C, TM, R, NM>(nwv);
+  if constexpr (kInterleaved<C> && TM == 1 && NM == 1) {
+    if (passes == 1 && p.ileave) {  // the K-chunks of a split row interleaved: see plan_grid
+      hipLaunchKernelGGL((gemv_kernel<C, 1, R, 1, 1, false, true>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
+      return hipGetLastError();
+    }
+  }
   if (TM == 1 && passes == 1)
     hipLaunchKernelGGL((gemv_kernel<C, TM, R, NM, TM == 1 ? 1 : 0>), dim3(nwg), dim3(64 * nwv), smem, st, p, split);
   else if (TM == 1 && passes == 2 && C::SP2)
