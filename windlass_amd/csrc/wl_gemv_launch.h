@@ -371,6 +371,10 @@ static inline int plan_batch(BatchArgs &a, int R, int num_cu) {
   for (int i = 0; i < a.nmat; i++) {
     const int groups = (a.m[i].rows + R - 1) / R;
     int n = (int)(((int64_t)target * groups + total - 1) / total);
+    // a multiple of the 8 XCDs: workgroup (x, c) is dispatched as x + c * gx and dealt to XCD
+    // (x + c * gx) % 8, so the wave-columns c of a row set x then share one L2, where the
+    // 128-byte line two neighbouring columns share is fetched once
+    n = (n + 7) & ~7;
     const int most = (groups + kBatchWaves - 1) / kBatchWaves;
     if (n > most) n = most;
     if (n < 1) n = 1;
