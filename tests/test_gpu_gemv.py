@@ -81,6 +81,25 @@ def test_few_rows_one_token_equals_batch_rows(ctx, t, rows, cols):
     w.free()
 
 
+# Rows cut into 7 K-chunks whose workgroups run interleaved (equal chunk grids in multiples of 8:
+# 512 rows give 64-256 row groups per chunk, 4,099 Q6_K rows 2,050 two-row groups with a ragged
+# last one; Q2_K keeps consecutive chunk ranges): each token alone equals the batch's rows bit for
+# bit (the chunks are still added in chunk order), and the tolerance bar holds.
+@pytest.mark.parametrize("t,rows", [(GgmlType.Q6_K, 512), (GgmlType.Q6_K, 4099), (GgmlType.IQ2_XXS, 512),
+                                    (GgmlType.IQ2_S, 512), (GgmlType.IQ3_S, 512), (GgmlType.Q2_K, 512)],
+                         ids=lambda v: v.name if hasattr(v, "name") else str(v))
+def test_interleaved_chunks(ctx, t, rows):
+    cols = 28672
+    data = blocks(t, rows, cols, seed=rows + int(t))
+    w = ctx.upload(t, data, rows, cols)
+    x = np.random.default_rng(rows).standard_normal((3, cols), dtype=np.float32)
+    y1 = np.stack([Transformer.MatMul(w, x[i:i + 1], 1)[0] for i in range(3)])
+    yb = Transformer.MatMul(w, x, 3)
+    w.free()
+    assert np.array_equal(yb.view(np.uint32), y1.view(np.uint32))
+    tol_check(y1, x, decoded(t, data, rows, cols), what="gpu %s %dx%d" % (t.name, rows, cols))
+
+
 def test_more_than_eight_tokens(ctx):
     # T > 8 runs the bf16 MFMA GEMM: within the stated bf16 bound of the fp32 result
     t, rows, cols, T = GgmlType.Q4_K, 64, 1024, 19
