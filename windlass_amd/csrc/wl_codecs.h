@@ -332,12 +332,15 @@ struct Q80 {
 };
 
 // -------------------------------------------------------------------------- IQ4_XS
-// Lane slice: sub-block ib = sub (32 values, 16 bytes of qs).
-#ifndef WL_IQ4XS_LDS
-#define WL_IQ4XS_LDS 1
-#endif
-struct IQ4XS {
-  static constexpr int BLOCK = 256, BYTES = 136, LPB = 8, NEED_LDS = WL_IQ4XS_LDS ? 2 : 0, R1 = 8, SP2 = 1;
+// Lane slice: sub-block ib = sub (32 values, 16 bytes of qs). Word k of a lane's W holds the
+// values of qs byte k, kvalue[low nibble] + 128 and kvalue[high nibble] + 128 (values k and
+// 16 + k), as two fp16 subnormals. TABLE: the word is read from an LDS table indexed by the
+// byte (the one-token launches); otherwise it is looked up in registers (byte permutes over the
+// 16 kvalues; the batched launches, whose LDS carries the tokens' x). Both build the same words
+// and share the dot, so a token's bits do not depend on which launch computed it.
+template <bool TABLE>
+struct IQ4XSc {
+  static constexpr int BLOCK = 256, BYTES = 136, LPB = 8, NEED_LDS = TABLE ? 2 : 0, R1 = 8, SP2 = 1;
   struct Lane { int ib; };
   struct Xs { float v[32]; float s; };
   struct Raw { uint2 hdr, q01, q23; };
@@ -392,20 +395,19 @@ struct IQ4XS {
     const int ls = (int)((hdr.y >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xF) | (int)(((scales_h >> (2 * ib)) & 3) << 4);
     w.dl = d * (float)(ls - 32);  // src/IQuants.cs:71-72
     const uint32_t qq[4] = {r.q01.x, r.q01.y, r.q23.x, r.q23.y};
-    if constexpr (NEED_LDS) {
-      // qs byte k: its low nibble is value k, its high nibble value 16+k; one table read gives both
+    if constexpr (TABLE) {
 #pragma unroll
       for (int k = 0; k < 16; k++) w.p[k] = lds.iq4[(qq[k >> 2] >> (8 * (k & 3))) & 0xFF];
     } else {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        // qs byte 4i+k: low nibble -> value 4i+k, high nibble -> value 16+4i+k
+        // the low nibbles' and the high nibbles' values of qs bytes 4i .. 4i+3, then byte b of
+        // each into word 4i + b: [low value, 0, high value, 0]
         const uint32_t lo = lookup(qq[i] & 0x0F0F0F0Fu);
         const uint32_t hi = lookup((qq[i] >> 4) & 0x0F0F0F0Fu);
-        w.p[2 * i] = lo & 0x00FF00FFu;
-        w.p[2 * i + 1] = (lo >> 8) & 0x00FF00FFu;
-        w.p[8 + 2 * i] = hi & 0x00FF00FFu;
-        w.p[8 + 2 * i + 1] = (hi >> 8) & 0x00FF00FFu;
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+          w.p[4 * i + b] = __builtin_amdgcn_perm(hi, lo, (uint32_t)b | 0x0C00u | (uint32_t)(4 + b) << 16 | 0x0C000000u);
       }
     }
   }
@@ -414,25 +416,10 @@ struct IQ4XS {
   // the wait a chain of dependent v_fma_mix_f32 needs on gfx950.
   __device__ static float dot(const W &w, const Xs &x) {
     float a = 0.f, b = 0.f;
-    if constexpr (NEED_LDS) {
 #pragma unroll
-      for (int k = 0; k < 16; k++) {
-        a = fma_lo(w.p[k], x.v[k], a);
-        b = fma_hi(w.p[k], x.v[16 + k], b);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float *xa = x.v + 4 * i, *xb = x.v + 16 + 4 * i;
-        a = fma_lo(w.p[2 * i], xa[0], a);
-        b = fma_lo(w.p[8 + 2 * i], xb[0], b);
-        a = fma_hi(w.p[2 * i], xa[2], a);
-        b = fma_hi(w.p[8 + 2 * i], xb[2], b);
-        a = fma_lo(w.p[2 * i + 1], xa[1], a);
-        b = fma_lo(w.p[8 + 2 * i + 1], xb[1], b);
-        a = fma_hi(w.p[2 * i + 1], xa[3], a);
-        b = fma_hi(w.p[8 + 2 * i + 1], xb[3], b);
-      }
+    for (int k = 0; k < 16; k++) {
+      a = fma_lo(w.p[k], x.v[k], a);
+      b = fma_hi(w.p[k], x.v[16 + k], b);
     }
     // dl * sum(kv*x) = dl * (sum((kv+128)*x) - 128*sum(x))
     return w.dl * __builtin_fmaf(-128.f, x.s, a + b);
@@ -444,6 +431,8 @@ struct IQ4XS {
       lds.iq4[i] = (uint32_t)(kKvaluesIq4nl[i & 15] + 128) | (uint32_t)(kKvaluesIq4nl[i >> 4] + 128) << 16;
   }
 };
+using IQ4XS = IQ4XSc<true>;    // one-token launches, the MoE experts
+using IQ4XSR = IQ4XSc<false>;  // the batched launches
 
 // ------------------------------------------------------------------------- IQ2_XXS
 // Lane slice: sub-block ib32 = sub: four groups of 8 values, each a grid entry (8 bytes of

@@ -122,8 +122,11 @@ typedef Q32<24, 8, 4, true> Q51;
 
 // IQ4_NL (src/IQuants.cs:45-58): y = d * kvalues[n], through IQ4_XS's LDS table of
 // (kvalue[low] + 128, kvalue[high] + 128) fp16 pairs indexed by a whole qs byte.
-struct IQ4NL {
-  static constexpr int BLOCK = 32, BYTES = 18, LPB = 1, NEED_LDS = 2, R1 = 4, SP2 = 1;
+// TABLE: the words of the qs bytes from the LDS table (one-token launches); otherwise looked up
+// in registers into the same words (the batched launches), as IQ4_XS does.
+template <bool TABLE>
+struct IQ4NLc {
+  static constexpr int BLOCK = 32, BYTES = 18, LPB = 1, NEED_LDS = TABLE ? 2 : 0, R1 = 4, SP2 = 1;
   struct Lane {};
   struct Xs { float v[32]; float s; };
   typedef Raw32<18> Raw;
@@ -144,8 +147,19 @@ struct IQ4NL {
   __device__ static void unpack(const Raw &r, const Lane &, const Lds &lds, W &w) {
     w.d = half_lo(r.w.dw(0));
     const uint32_t q[4] = {r.at(2, 0), r.at(2, 1), r.at(2, 2), r.at(2, 3)};
+    if constexpr (TABLE) {
 #pragma unroll
-    for (int k = 0; k < 16; k++) w.p[k] = lds.iq4[(q[k >> 2] >> (8 * (k & 3))) & 0xFF];
+      for (int k = 0; k < 16; k++) w.p[k] = lds.iq4[(q[k >> 2] >> (8 * (k & 3))) & 0xFF];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t lo = IQ4XS::lookup(q[i] & 0x0F0F0F0Fu);
+        const uint32_t hi = IQ4XS::lookup((q[i] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+          w.p[4 * i + b] = __builtin_amdgcn_perm(hi, lo, (uint32_t)b | 0x0C00u | (uint32_t)(4 + b) << 16 | 0x0C000000u);
+      }
+    }
   }
   __device__ static float dot(const W &w, const Xs &x) {
     float a = 0.f;
@@ -158,6 +172,8 @@ struct IQ4NL {
   }
   __device__ static void init_lds(Lds &lds) { IQ4XS::init_lds(lds); }
 };
+using IQ4NL = IQ4NLc<true>;    // one-token launches, the MoE experts
+using IQ4NLR = IQ4NLc<false>;  // the batched launches
 
 // ------------------------------------------------------------------ Q2_K and Q3_K
 // Lane slice: run r = sub of the block, i.e. 128-value half kk = sub / 4 and 2-bit field

@@ -177,7 +177,7 @@ static hipError_t launch_batch_mixed_tm(BatchArgs a, int num_cu, hipStream_t st)
 // The codecs of this unit and the lookup over every unit.
 const GemvOps *gemv_ops_base(int type) {
   static constexpr GemvOps q4k = gemv_ops_of<Q4K>(), q6k = gemv_ops_of<Q6K>(), q80 = gemv_ops_of<Q80>(),
-                           iq4xs = gemv_ops_of<IQ4XS>(), iq2xxs = gemv_ops_of<IQ2XXS>();
+                           iq4xs = gemv_ops_of2<IQ4XS, IQ4XSR>(), iq2xxs = gemv_ops_of<IQ2XXS>();
   switch (type) {
     case 12: return &q4k;
     case 14: return &q6k;

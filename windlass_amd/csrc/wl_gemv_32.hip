@@ -8,7 +8,7 @@ namespace wl {
 
 const GemvOps *gemv_ops_32(int type) {
   static constexpr GemvOps q40 = gemv_ops_of<Q40>(), q41 = gemv_ops_of<Q41>(), q50 = gemv_ops_of<Q50>(),
-                           q51 = gemv_ops_of<Q51>(), iq4nl = gemv_ops_of<IQ4NL>();
+                           q51 = gemv_ops_of<Q51>(), iq4nl = gemv_ops_of2<IQ4NL, IQ4NLR>();
   switch (type) {
     case 2: return &q40;
     case 3: return &q41;

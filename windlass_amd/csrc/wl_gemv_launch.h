@@ -435,6 +435,12 @@ template <class C>
 constexpr GemvOps gemv_ops_of() {
   return GemvOps{{&launch_tm<C, 1>, &launch_tm<C, 2>}, {&launch_batch<C, 1>, &launch_batch<C, 2>}};
 }
+// A codec whose batched launches take another codec of the same values (CB builds the same
+// weight words and shares C's dot, so every token's bits are the same).
+template <class C, class CB>
+constexpr GemvOps gemv_ops_of2() {
+  return GemvOps{{&launch_tm<C, 1>, &launch_tm<C, 2>}, {&launch_batch<CB, 1>, &launch_batch<CB, 2>}};
+}
 
 // Each codec-owning unit: the ops of a format it holds, or nullptr.
 const GemvOps *gemv_ops_base(int type);  // wl_gemv.hip
