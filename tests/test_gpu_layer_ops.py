@@ -218,16 +218,25 @@ def test_shape_errors(ctx):
         check(L.wl_rms_norm_dev(ctx.handle, P(x), 2, 0, P(x), 1e-5, P(x)))
 
 
-def test_layer_equals_its_operations(ctx):
+@pytest.mark.parametrize("T,pos0,cap,HD,rd,neox", [
+    (3, 5, 16, 64, 32, 1),       # three tokens: RoPE + KV store, then attention
+    (1, 5, 16, 64, 32, 1),       # one token: RoPE and the KV store inside the attention launch
+    (1, 0, 16, 64, 32, 1),       # the first token: no cached position
+    (1, 255, 512, 128, 64, 1),   # 256 positions, the token the last of the one chunk
+    (1, 256, 512, 64, 64, 0),    # 257 positions: the token alone in the second chunk
+    (1, 300, 512, 128, 128, 0),  # two chunks, every dim rotated, adjacent pairs
+])
+def test_layer_equals_its_operations(ctx, T, pos0, cap, HD, rd, neox):
     """wl_layer_dev is the operations above in Transformer.Layer's order (src/Transformer.cs:177-232):
     the same layer run one operation at a time through the C ABI gives the same bits, with every
     option the tiny models leave out (partial RoPE, frequency factors, biases, per-head q/k
-    norms, residual and attention scales) and cached positions before the rows."""
+    norms, residual and attention scales) and cached positions before the rows. One token takes
+    the attention launch that rotates q and k and stores the caches itself."""
     from windlass_amd import LayerDesc
     L, h = load(), ctx.handle
-    rng = np.random.default_rng(11)
-    E, H, KH, HD, FF, T, pos0, cap = 256, 4, 2, 64, 512, 3, 5, 16
-    QD, KD, rd, rs, asc = H * HD, KH * HD, 32, 0.5, 0.1
+    rng = np.random.default_rng(11 + T + pos0)
+    E, H, KH, FF = 256, 4, 2, 512
+    QD, KD, rs, asc = H * HD, KH * HD, 0.5, 0.1
     mats = {"attn_q": (GgmlType.Q4_K, QD, E), "attn_k": (GgmlType.Q8_0, KD, E), "attn_v": (GgmlType.Q6_K, KD, E),
             "attn_output": (GgmlType.Q4_K, E, QD), "ffn_gate": (GgmlType.Q4_K, FF, E),
             "ffn_up": (GgmlType.Q4_K, FF, E), "ffn_down": (GgmlType.Q6_K, E, FF)}
@@ -244,7 +253,7 @@ def test_layer_equals_its_operations(ctx):
     d.d_attn_norm, d.d_ffn_norm = v["attn_norm"].data_ptr(), v["ffn_norm"].data_ptr()
     d.d_q_bias, d.d_k_bias, d.d_v_bias = (v[k].data_ptr() for k in ("q_bias", "k_bias", "v_bias"))
     d.d_q_norm, d.d_k_norm, d.d_rope_freqs = v["q_norm"].data_ptr(), v["k_norm"].data_ptr(), v["freqs"].data_ptr()
-    d.embd, d.heads, d.kv_heads, d.head_dim, d.rope_dims, d.neox = E, H, KH, HD, rd, 1
+    d.embd, d.heads, d.kv_heads, d.head_dim, d.rope_dims, d.neox = E, H, KH, HD, rd, neox
     d.rope_base, d.rope_freq_scale, d.eps, d.attention_scale, d.residual_scale = 10000.0, 0.5, 1e-6, asc, rs
     xa, Ka, Va = dev(x0), dev(cache), dev(cache)
     check(L.wl_layer_dev(h, ctypes.byref(d), P(xa), T, pos0, P(Ka), P(Va)))
@@ -267,7 +276,7 @@ def test_layer_equals_its_operations(ctx):
     check(L.wl_rms_norm_dev(h, P(q), T * H, HD, P(v["q_norm"]), c(1e-6), P(q)))
     check(L.wl_rms_norm_dev(h, P(k), T * KH, HD, P(v["k_norm"]), c(1e-6), P(k)))
     for y, nh in ((q, H), (k, KH)):
-        check(L.wl_rope_dev(h, P(y), T, nh, HD, rd, 1, pos0, None, 10000.0, 0.5, P(v["freqs"])))
+        check(L.wl_rope_dev(h, P(y), T, nh, HD, rd, neox, pos0, None, 10000.0, 0.5, P(v["freqs"])))
     check(L.wl_kv_store_dev(h, P(k), P(vv), T, KD, P(Kb), P(Vb), pos0))
     check(L.wl_attention_dev(h, P(q), T, H, KH, HD, P(Kb), P(Vb), pos0, c(asc), P(att)))
     check(L.wl_matmul_dev(h, w["attn_output"].handle, -1, P(att), T, P(o)))

@@ -1269,14 +1269,12 @@ static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, i
     return rc;
   if (L->d_k_norm && (rc = wl_rms_norm_dev(c, k, full ? T : (int64_t)T * KH, full ? KD : HD, L->d_k_norm, L->eps, k)))
     return rc;
+  // RoPE, the fp16 KV store and attention (one launch for a token or batch rows on their own slots)
   const double fs = L->rope_freq_scale != 0.0 ? L->rope_freq_scale : 1.0;
-  WL_HIP(wl::rope_kv_launch(q, k, v, T, H, KH, HD, rd, L->neox, pos0, L->rope_base, fs, L->d_rope_freqs, d_K, d_V,
-                            rm, c->stream),
-         "rope and kv store");
   const float scale = L->attention_scale != 0.f ? L->attention_scale : 1.0f / (float)sqrt((double)HD);
-  WL_HIP(wl::attention_launch(q, QD, T, d_K, d_V, KD, H, KH, HD, pos0, scale, (float *)c->buf[S_ATT], att, QD, rm,
-                              max_n, c->stream),
-         "attention");
+  WL_HIP(wl::rope_attention_launch(q, k, v, T, H, KH, HD, rd, L->neox, pos0, L->rope_base, fs, L->d_rope_freqs, d_K,
+                                   d_V, rm, scale, (float *)c->buf[S_ATT], att, max_n, c->stream),
+         "rope, kv store and attention");
   if (post) {
     // o = RmsNorm(W_o att), then x += o * rs (src/Transformer.cs:223-225)
     if ((rc = ensure(c, S_LM, (size_t)T * E * 4))) return rc;

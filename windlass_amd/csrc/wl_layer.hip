@@ -114,14 +114,19 @@ __global__ __launch_bounds__(1024) void rms_norm_kernel(const float *x, int64_t 
 }
 
 // The angle of rotated pair i at a position: RopeTable's running product in double
-// (src/Transformer.cs:396-414) repeated up to pair i, so every thread gets the bits the
-// sequential table has, divided by the pair's frequency factor when the model has them
-// (rope_freqs.weight).
-__device__ __forceinline__ void rope_cs(int p, int i, double theta_scale, double freq_scale,
+// (src/Transformer.cs:396-414) taken to step i, divided by the pair's frequency factor when the
+// model has them (rope_freqs.weight, `half` of them). The product is the same sequence for every
+// pair, so a wave runs it once for all its lanes (the trip count `half` is uniform) and each lane
+// keeps the value after its own i steps: every lane gets the bits the sequential table has
+// without a divergent loop of up to 63 dependent multiplies per lane.
+__device__ __forceinline__ void rope_cs(int p, int i, int half, double theta_scale, double freq_scale,
                                         const float *__restrict__ freqs, float &c, float &s) {
-  double theta = (double)p * freq_scale;
-  for (int k = 0; k < i; k++) theta *= theta_scale;
-  const double a = freqs ? theta / (double)freqs[i] : theta;
+  double theta = (double)p * freq_scale, mine = theta;
+  for (int k = 1; k < half; k++) {
+    theta *= theta_scale;
+    if (k == i) mine = theta;
+  }
+  const double a = freqs && i < half ? mine / (double)freqs[i] : mine;
   c = (float)cos(a);
   s = (float)sin(a);
 }
@@ -154,11 +159,12 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(float *__restrict__ q, in
   const int npairs = (H + KH) * half;
   const int p = pos ? pos[t] : pos0 + t;
   const int64_t crow = (slot ? (int64_t)slot[t] * cap + p : (int64_t)(pos0 + t)) * KD;
+  float c = 0.f, s = 0.f;  // every lane runs the angle product (uniform trip count)
+  if (half > 0) rope_cs(p, it < npairs ? it % half : 0, half, theta_scale, freq_scale, freqs, c, s);
   if (it < npairs) {
     const int head = it / half, i = it % half;
-    float c, s, y0, y1;
+    float y0, y1;
     int a, b;
-    rope_cs(p, i, theta_scale, freq_scale, freqs, c, s);
     if (head < H) {
       rope_pair(q + (int64_t)t * ldq + (int64_t)head * hd, i, n, neox, c, s, y0, y1, a, b);
     } else {
@@ -244,116 +250,236 @@ __global__ __launch_bounds__(256) void attention_kernel(const float *__restrict_
   }
 }
 
-// Attention for head dims that are a multiple of 8 (src/Transformer.cs:351-393): one workgroup
-// of 256 threads per (query head, chunk of kAttP positions, row). Thread j holds the key of
-// position j0 + j in registers (uint4 loads) and forms its score with the reference's four
-// partial sums; the chunk's values are staged in LDS meanwhile. When a row's positions fit one
-// chunk the workgroup finishes it with the reference's arithmetic (maximum, exp in double,
-// the double sum, p = e * inv, each output value adding its positions in order). A longer row
-// leaves per-chunk partials (unnormalised sums, chunk maximum, double sum) that
-// attention_combine_kernel rescales and adds in chunk order.
+// Wave-wide reductions through DPP: lanes xor 1 and xor 2 (quad permutes), rotations by 4 and
+// 8 within each row of 16 lanes, then lane 0 of each row, combined as (r0 + r1) + (r2 + r3).
+// The result is uniform. Every lane of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp64(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  return __builtin_bit_cast(double, (uint64_t)dpp32<CTRL>((uint32_t)(b >> 32)) << 32 | dpp32<CTRL>((uint32_t)b));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ double lane_d(double v, int l) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+  return __builtin_bit_cast(double, (uint64_t)hi << 32 | lo);
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, dpp32<0xB1>(__builtin_bit_cast(uint32_t, v))));   // quad_perm 1,0,3,2
+  v = fmaxf(v, __builtin_bit_cast(float, dpp32<0x4E>(__builtin_bit_cast(uint32_t, v))));   // quad_perm 2,3,0,1
+  v = fmaxf(v, __builtin_bit_cast(float, dpp32<0x124>(__builtin_bit_cast(uint32_t, v))));  // row_ror 4
+  v = fmaxf(v, __builtin_bit_cast(float, dpp32<0x128>(__builtin_bit_cast(uint32_t, v))));  // row_ror 8
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+  v += dpp64<0xB1>(v);
+  v += dpp64<0x4E>(v);
+  v += dpp64<0x124>(v);
+  v += dpp64<0x128>(v);
+  return (lane_d(v, 0) + lane_d(v, 16)) + (lane_d(v, 32) + lane_d(v, 48));
+}
+
+// One rounding of f16(w.lo) * x: v_fma_mix_f32 with a +0 addend equals the product except that
+// an exact -0 product comes out +0. The sums it feeds start at +0 and cannot become -0 (in
+// round-to-nearest x + y is -0 only when both are -0), so adding +0 or -0 leaves them as they are.
+__device__ __forceinline__ float mul_lo(uint32_t w, float x) { return __builtin_fmaf(half_lo(w), x, 0.0f); }
+__device__ __forceinline__ float mul_hi(uint32_t w, float x) { return __builtin_fmaf(half_hi(w), x, 0.0f); }
+
+// Attention for head dims of 64 and 128 (src/Transformer.cs:351-393): one workgroup of 256
+// threads per (query head, chunk of kAttP positions, row). Thread j loads the key of position
+// j0 + j with uint4 loads (every lane loads, rows past the chunk clamped to its last) and forms
+// its score with the reference's four partial sums; the chunk's values are staged in LDS
+// meanwhile. When a row's positions fit one chunk the workgroup finishes it with the
+// reference's arithmetic (maximum, exp in double, the double sum, p = e * inv, each output value
+// adding its positions in order). A longer row leaves per-chunk partials (unnormalised sums,
+// chunk maximum, double sum) that attention_combine_kernel rescales and adds in chunk order.
+//
+// With ROPE the row's own key and value are this step's: rows whose earlier positions are all
+// cached (one token of a sequence, or batch rows on distinct slots). Each workgroup rotates its
+// query head itself (rope_cs / rope_pair: the bits rope_qkv_kernel gives), the chunk holding the
+// row's position rotates the new key and rounds key and value to fp16 (to_half) for that
+// position, and the first query head of each KV group stores them to the caches. Nothing in the
+// launch reads those cache rows, so the separate RoPE + KV store launch goes away.
 constexpr int kAttP = 256;
 
-__device__ __forceinline__ float half_lo16(uint32_t w) { return h2f((uint16_t)(w & 0xffffu)); }
-__device__ __forceinline__ float half_hi16(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
+struct RopeArgs {
+  const float *k = nullptr, *v = nullptr;  // the rows' keys (not rotated) and values [T][kv_dim]
+  int n = 0, neox = 0;                     // rotated dims per head, NeoX pairing
+  double theta_scale = 0.0, freq_scale = 1.0;
+  const float *freqs = nullptr;
+  uint16_t *Kc = nullptr, *Vc = nullptr;  // the caches the rows' keys and values go to
+};
 
-template <int HD>
-__global__ __launch_bounds__(256) void attention_chunk_kernel(const float *__restrict__ q, int64_t ldq,
-                                                              const uint16_t *__restrict__ K,
-                                                              const uint16_t *__restrict__ V, int kv_dim, int heads,
-                                                              int kv_heads, int pos0, float scale,
+template <int HD, bool ROPE>
+__global__ __launch_bounds__(256, 2) void attention_chunk_kernel(const float *__restrict__ q, int64_t ldq,
+                                                              const uint16_t *K, const uint16_t *V, int kv_dim,
+                                                              int heads, int kv_heads, int pos0, float scale,
                                                               float *__restrict__ part, int max_chunks,
                                                               float *__restrict__ out, int64_t ldo,
                                                               const int *__restrict__ pos,
-                                                              const int *__restrict__ slot, int64_t cap) {
+                                                              const int *__restrict__ slot, int64_t cap, RopeArgs ra) {
   constexpr int U = HD / 8;  // uint4 per key row
   __shared__ uint4 vs4[kAttP * U];
-  __shared__ float qs[HD];
-  __shared__ float es[kAttP];
+  __shared__ __attribute__((aligned(16))) float qs[HD];
+  __shared__ __attribute__((aligned(16))) float ps[kAttP];
   __shared__ float shf[4];
-  __shared__ double shd[16];
-  const int h = blockIdx.x, c = blockIdx.y, t = blockIdx.z;
+  __shared__ double shd[4];
+  __shared__ __attribute__((aligned(16))) float kn[ROPE ? HD : 4];
+  __shared__ __attribute__((aligned(16))) uint16_t kh[ROPE ? HD : 8], vh[ROPE ? HD : 8];
+  const int h = blockIdx.x, c = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
   const int kvh = h / (heads / kv_heads);
-  const int n = pos ? pos[t] + 1 : pos0 + t + 1, j0 = c * kAttP;
+  const int p = pos ? pos[t] : pos0 + t, n = p + 1, j0 = c * kAttP;
   if (j0 >= n) return;  // uniform over the workgroup
-  if (slot) {  // row t reads its own sequence's slot
+  int64_t crow = p;     // the row's cache row
+  if (slot) {           // row t reads its own sequence's slot
     K += (int64_t)slot[t] * cap * kv_dim;
     V += (int64_t)slot[t] * cap * kv_dim;
+    crow += (int64_t)slot[t] * cap;
   }
   const int cnt = n - j0 < kAttP ? n - j0 : kAttP;
+  const int cnt16 = (cnt + 15) & ~15;
   const int nch = (n + kAttP - 1) / kAttP;
-  const int tid = threadIdx.x;
-  uint4 kr[U], vr[U];  // zeroed first: partly written arrays are otherwise kept in scratch
-#pragma unroll
-  for (int u = 0; u < U; u++) kr[u] = vr[u] = make_uint4(0, 0, 0, 0);
-  if (tid < cnt) {
-    const uint4 *kp = reinterpret_cast<const uint4 *>(K + (int64_t)(j0 + tid) * kv_dim + (int64_t)kvh * HD);
+  const bool fresh = ROPE && c == nch - 1;  // the chunk holds the row's position, cnt - 1
+  const int nold = fresh ? cnt - 1 : cnt;   // positions read from the caches
+  float qv = 0.f, kv = 0.f, vv = 0.f;
+  if (tid < HD) qv = q[(int64_t)t * ldq + (int64_t)h * HD + tid];
+  if (fresh) {
+    const int64_t r = (int64_t)t * kv_dim + (int64_t)kvh * HD;
+    if (tid < HD)
+      kv = ra.k[r + tid];
+    else if (tid < 2 * HD)
+      vv = ra.v[r + tid - HD];
+  }
+  // Loads skip what no position needs by uniform branches (a wave's keys, a step of 256/U value
+  // rows); within them every lane loads, rows past the chunk clamped to its last cached one.
+  uint4 kr[U], vr[U];
+  if (__builtin_amdgcn_readfirstlane(tid) - (__builtin_amdgcn_readfirstlane(tid) & 63) < nold) {
+    const int row = tid < nold ? tid : nold - 1;
+    const uint4 *kp = reinterpret_cast<const uint4 *>(K + (int64_t)(j0 + row) * kv_dim + (int64_t)kvh * HD);
 #pragma unroll
     for (int u = 0; u < U; u++) kr[u] = kp[u];
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; u++) kr[u] = make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
-  for (int u = 0; u < U; u++) {  // the chunk's values: element e of [cnt][U] uint4
-    const int e = u * 256 + tid, row = e / U, col = e % U;
-    if (row < cnt) vr[u] = reinterpret_cast<const uint4 *>(V + (int64_t)(j0 + row) * kv_dim + (int64_t)kvh * HD)[col];
+  for (int u = 0; u < U; u++) {  // the chunk's values: element e of [rows][U] uint4
+    const int e = u * 256 + tid, r = e / U, col = e % U, rc = r < nold ? r : nold - 1;
+    vr[u] = make_uint4(0, 0, 0, 0);
+    if (u * (256 / U) < nold)
+      vr[u] = reinterpret_cast<const uint4 *>(V + (int64_t)(j0 + rc) * kv_dim + (int64_t)kvh * HD)[col];
   }
-  const float *qp = q + (int64_t)t * ldq + (int64_t)h * HD;
-  for (int i = tid; i < HD; i += 256) qs[i] = qp[i];
-  __syncthreads();
-  float d = -INFINITY;
-  if (tid < cnt) {
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const uint4 w = kr[u];
-      const float *qq = qs + 8 * u;
-      s0 += qq[0] * half_lo16(w.x);
-      s1 += qq[1] * half_hi16(w.x);
-      s2 += qq[2] * half_lo16(w.y);
-      s3 += qq[3] * half_hi16(w.y);
-      s0 += qq[4] * half_lo16(w.z);
-      s1 += qq[5] * half_hi16(w.z);
-      s2 += qq[6] * half_lo16(w.w);
-      s3 += qq[7] * half_hi16(w.w);
+  float ac = 0.f, as = 0.f;  // cos and sin of pair tid's angle, computed while the loads are in flight
+  if (ROPE && tid < 64) rope_cs(p, tid, ra.n / 2, ra.theta_scale, ra.freq_scale, ra.freqs, ac, as);  // wave 0
+  if (tid < HD) qs[tid] = qv;
+  if (fresh) {
+    if (tid < HD)
+      kn[tid] = kv;
+    else if (tid < 2 * HD)
+      vh[tid - HD] = to_half(vv);
+  }
+  if (ROPE) {
+    __syncthreads();
+    if (tid < ra.n / 2) {
+      float y0, y1;
+      int a, b;
+      rope_pair(qs, tid, ra.n, ra.neox, ac, as, y0, y1, a, b);
+      if (fresh) {
+        rope_pair(kn, tid, ra.n, ra.neox, ac, as, y0, y1, a, b);
+        kh[a] = to_half(y0);
+        kh[b] = to_half(y1);
+      }
+    } else if (fresh && tid >= ra.n && tid < HD) {  // key columns past the rotated ones
+      kh[tid] = to_half(kn[tid]);
     }
-    d = ((s0 + s1) + (s2 + s3)) * scale;
   }
+  __syncthreads();
+  if (fresh) {
+    if (h % (heads / kv_heads) == 0 && tid < HD) {
+      const int64_t o = crow * kv_dim + (int64_t)kvh * HD + tid;
+      ra.Kc[o] = kh[tid];
+      ra.Vc[o] = vh[tid];
+    }
+    if (tid == cnt - 1) {
+#pragma unroll
+      for (int u = 0; u < U; u++) kr[u] = reinterpret_cast<const uint4 *>(kh)[u];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++) {  // values first (frees their registers); rows cnt..cnt16-1 as zeros, p = 0 there
+    const int e = u * 256 + tid, r = e / U;
+    if (r < cnt16) {
+      uint4 w = r < nold ? vr[u] : make_uint4(0, 0, 0, 0);
+      if (fresh && r == cnt - 1) w = reinterpret_cast<const uint4 *>(vh)[e % U];
+      vs4[e] = w;
+    }
+  }
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
   for (int u = 0; u < U; u++) {
-    const int e = u * 256 + tid;
-    if (e / U < cnt) vs4[e] = vr[u];
+    const uint4 w = kr[u];
+    const float4 qa = reinterpret_cast<const float4 *>(qs)[2 * u], qb = reinterpret_cast<const float4 *>(qs)[2 * u + 1];
+    s0 += mul_lo(w.x, qa.x);
+    s1 += mul_hi(w.x, qa.y);
+    s2 += mul_lo(w.y, qa.z);
+    s3 += mul_hi(w.y, qa.w);
+    s0 += mul_lo(w.z, qb.x);
+    s1 += mul_hi(w.z, qb.y);
+    s2 += mul_lo(w.w, qb.z);
+    s3 += mul_hi(w.w, qb.w);
   }
-  const float mx = block_max_f(d, shf);
+  const float d = tid < cnt ? ((s0 + s1) + (s2 + s3)) * scale : -INFINITY;
+  const int wv = tid >> 6;
+  {
+    const float m = wave_max_f(d);
+    if ((tid & 63) == 0) shf[wv] = m;
+  }
+  __syncthreads();
+  const float mx = fmaxf(fmaxf(shf[0], shf[1]), fmaxf(shf[2], shf[3]));
   float e = 0.f;
   double sum = 0.0;
   if (tid < cnt) {
     e = (float)exp((double)(d - mx));
     sum = (double)e;
   }
-  es[tid] = e;
-  sum = block_sum_d(sum, shd);  // also orders the writes of es and vs4 before the reads below
-  const uint16_t *vs = reinterpret_cast<const uint16_t *>(vs4);
-  if (nch == 1) {
-    const float inv = (float)(1.0 / sum);
-    for (int dd = tid; dd < HD; dd += 256) {
-      float o = 0.f;
-#pragma unroll 8
-      for (int j = 0; j < cnt; j++) {  // unrolled: eight positions' LDS reads in flight
-        const float p = es[j] * inv;
-        o += p * h2f(vs[j * HD + dd]);
-      }
-      out[(int64_t)t * ldo + (int64_t)h * HD + dd] = o;
-    }
-    return;
+  {
+    const double s = wave_sum_d(sum);
+    if ((tid & 63) == 0) shd[wv] = s;
   }
-  // record: HD unnormalised sums, the chunk maximum, a pad, the double sum
+  __syncthreads();
+  sum = ((shd[0] + shd[1]) + shd[2]) + shd[3];
+  ps[tid] = nch == 1 ? e * (float)(1.0 / sum) : e;  // zero past cnt
+  __syncthreads();  // also orders the writes of vs4 before the reads below
   float *rec = part + (((int64_t)t * heads + h) * max_chunks + c) * (HD + 4);
-  for (int dd = tid; dd < HD; dd += 256) {
+  if (tid < HD) {
+    // each output value adds its positions in order, 16 at a time: the 16 values and p's are
+    // read first, then the products and sums
+    const uint16_t *vc = reinterpret_cast<const uint16_t *>(vs4) + tid;
+    const float4 *p4 = reinterpret_cast<const float4 *>(ps);
     float o = 0.f;
-#pragma unroll 8
-    for (int j = 0; j < cnt; j++) o += es[j] * h2f(vs[j * HD + dd]);
-    rec[dd] = o;
+    for (int j = 0; j < cnt16; j += 16) {
+      const float4 pa = p4[j / 4], pb = p4[j / 4 + 1], pc = p4[j / 4 + 2], pd = p4[j / 4 + 3];
+      uint32_t w[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) w[i] = vc[(j + i) * HD];
+      const float pp[16] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w,
+                            pc.x, pc.y, pc.z, pc.w, pd.x, pd.y, pd.z, pd.w};
+#pragma unroll
+      for (int i = 0; i < 16; i++) o += mul_lo(w[i], pp[i]);
+    }
+    if (nch == 1)
+      out[(int64_t)t * ldo + (int64_t)h * HD + tid] = o;
+    else
+      rec[tid] = o;  // record: HD unnormalised sums, the chunk maximum, a pad, the double sum
   }
-  if (tid == 0) {
+  if (nch > 1 && tid == 0) {
     rec[HD] = mx;
     *reinterpret_cast<double *>(rec + HD + 2) = sum;
   }
@@ -553,13 +679,14 @@ int64_t attention_scratch_floats(int T, int heads, int hd, int kv_dim, int max_n
   return chunks > 1 ? (int64_t)T * heads * chunks * (hd + 4) : 0;
 }
 
-template <int HD>
+template <int HD, bool ROPE>
 static hipError_t attention_chunked_launch(const float *q, int64_t ldq, int T, const uint16_t *K, const uint16_t *V,
                                            int kv_dim, int heads, int kv_heads, int pos0, float scale, float *part,
-                                           float *out, int64_t ldo, const RowMap &rm, int max_n, hipStream_t st) {
+                                           float *out, int64_t ldo, const RowMap &rm, int max_n, const RopeArgs &ra,
+                                           hipStream_t st) {
   const int chunks = (max_n + kAttP - 1) / kAttP;
-  hipLaunchKernelGGL(attention_chunk_kernel<HD>, dim3(heads, chunks, T), dim3(256), 0, st, q, ldq, K, V, kv_dim,
-                     heads, kv_heads, pos0, scale, part, chunks, out, ldo, rm.pos, rm.slot, rm.cap);
+  hipLaunchKernelGGL((attention_chunk_kernel<HD, ROPE>), dim3(heads, chunks, T), dim3(256), 0, st, q, ldq, K, V,
+                     kv_dim, heads, kv_heads, pos0, scale, part, chunks, out, ldo, rm.pos, rm.slot, rm.cap, ra);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || chunks == 1) return e;
   hipLaunchKernelGGL(attention_combine_kernel<HD>, dim3(heads, T), dim3(HD), 0, st, part, chunks, heads, pos0, out,
@@ -572,14 +699,45 @@ hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *
                             int64_t ldo, const RowMap &rm, int max_n, hipStream_t st) {
   if (T <= 0) return hipSuccess;
   if (attention_chunked(hd, kv_dim, K, V)) {
-    return hd == 64 ? attention_chunked_launch<64>(q, ldq, T, K, V, kv_dim, heads, kv_heads, pos0, scale, scratch,
-                                                   out, ldo, rm, max_n, st)
-                    : attention_chunked_launch<128>(q, ldq, T, K, V, kv_dim, heads, kv_heads, pos0, scale, scratch,
-                                                    out, ldo, rm, max_n, st);
+    const RopeArgs none;
+    return hd == 64 ? attention_chunked_launch<64, false>(q, ldq, T, K, V, kv_dim, heads, kv_heads, pos0, scale,
+                                                          scratch, out, ldo, rm, max_n, none, st)
+                    : attention_chunked_launch<128, false>(q, ldq, T, K, V, kv_dim, heads, kv_heads, pos0, scale,
+                                                           scratch, out, ldo, rm, max_n, none, st);
   }
   hipLaunchKernelGGL(attention_kernel, dim3(heads, T), dim3(256), 0, st, q, ldq, K, V, kv_dim, heads, kv_heads, hd,
                      pos0, scale, scratch, (int64_t)max_n, out, ldo, rm.pos, rm.slot, rm.cap);
   return hipGetLastError();
+}
+
+hipError_t rope_attention_launch(float *q, float *k, const float *v, int T, int H, int KH, int hd, int n, int neox,
+                                 int pos0, double base, double freq_scale, const float *freqs, uint16_t *Kc,
+                                 uint16_t *Vc, const RowMap &rm, float scale, float *scratch, float *out, int max_n,
+                                 hipStream_t st) {
+  if (T <= 0) return hipSuccess;
+  const int kv_dim = KH * hd;
+  const bool own = rm.pos ? rm.slot != nullptr : T == 1;  // every row's earlier positions are cached
+  if (!own || !attention_chunked(hd, kv_dim, Kc, Vc)) {
+    hipError_t e = rope_kv_launch(q, k, v, T, H, KH, hd, n, neox, pos0, base, freq_scale, freqs, Kc, Vc, rm, st);
+    if (e != hipSuccess) return e;
+    return attention_launch(q, (int64_t)H * hd, T, Kc, Vc, kv_dim, H, KH, hd, pos0, scale, scratch, out,
+                            (int64_t)H * hd, rm, max_n, st);
+  }
+  RopeArgs ra;
+  ra.k = k;
+  ra.v = v;
+  ra.n = n;
+  ra.neox = neox;
+  ra.theta_scale = pow(base, -2.0 / n);
+  ra.freq_scale = freq_scale;
+  ra.freqs = freqs;
+  ra.Kc = Kc;
+  ra.Vc = Vc;
+  const int64_t ld = (int64_t)H * hd;
+  return hd == 64 ? attention_chunked_launch<64, true>(q, ld, T, Kc, Vc, kv_dim, H, KH, pos0, scale, scratch, out, ld,
+                                                       rm, max_n, ra, st)
+                  : attention_chunked_launch<128, true>(q, ld, T, Kc, Vc, kv_dim, H, KH, pos0, scale, scratch, out,
+                                                        ld, rm, max_n, ra, st);
 }
 
 hipError_t shared_expert_launch(float *o, const float *sh, const float *gl, int64_t rows, int64_t dim,
