@@ -218,6 +218,9 @@ def test_shape_errors(ctx):
         check(L.wl_rms_norm_dev(ctx.handle, P(x), 2, 0, P(x), 1e-5, P(x)))
 
 
+_FREQS = {}
+
+
 @pytest.mark.parametrize("T,pos0,cap,HD,rd,neox", [
     (3, 5, 16, 64, 32, 1),       # three tokens: RoPE + KV store, then attention
     (1, 5, 16, 64, 32, 1),       # one token: RoPE and the KV store inside the attention launch
@@ -231,7 +234,26 @@ def test_layer_equals_its_operations(ctx, T, pos0, cap, HD, rd, neox):
     the same layer run one operation at a time through the C ABI gives the same bits, with every
     option the tiny models leave out (partial RoPE, frequency factors, biases, per-head q/k
     norms, residual and attention scales) and cached positions before the rows. One token takes
-    the attention launch that rotates q and k and stores the caches itself."""
+    the attention launch that rotates q and k (angles from the context's table by position) and
+    stores the caches itself."""
+    layer_vs_operations(ctx, T, pos0, cap, HD, rd, neox)
+
+
+def test_rope_table_follows_the_setting(ctx):
+    """The context's RoPE angles by position (RopeTable's cache) are refilled when the setting
+    changes, and an entry made with frequency factors whose values have since changed under the
+    same pointer is not used: tokens at new and already-seen positions under two bases, two factor
+    tensors and rewritten factors each equal the operations run one at a time."""
+    for pos0, base, fseed in ((7, 10000.0, 0), (8, 10000.0, 0), (7, 500000.0, 0), (8, 10000.0, 1), (9, 500000.0, 1),
+                              (7, 10000.0, 0), (8, 10000.0, 0)):
+        layer_vs_operations(ctx, 1, pos0, 16, 64, 64, 0, base=base, fseed=fseed)
+    _FREQS[(0, 64)].mul_(1.5)  # the same tensor, other values: positions 7 and 8 are in the table
+    torch.cuda.synchronize()
+    for pos0 in (7, 8):
+        layer_vs_operations(ctx, 1, pos0, 16, 64, 64, 0, base=10000.0, fseed=0)
+
+
+def layer_vs_operations(ctx, T, pos0, cap, HD, rd, neox, base=10000.0, fseed=None):
     from windlass_amd import LayerDesc
     L, h = load(), ctx.handle
     rng = np.random.default_rng(11 + T + pos0)
@@ -242,9 +264,12 @@ def test_layer_equals_its_operations(ctx, T, pos0, cap, HD, rd, neox):
             "ffn_up": (GgmlType.Q4_K, FF, E), "ffn_down": (GgmlType.Q6_K, E, FF)}
     w = {n: ctx.upload(t, blocks(t, r, c, seed=i), r, c, name=n) for i, (n, (t, r, c)) in enumerate(mats.items())}
     vec = lambda n, s=0.2, base=1.0: dev((base + s * rng.standard_normal(n)).astype(F32))  # noqa: E731
+    frng = rng if fseed is None else np.random.default_rng(100 + fseed)
     v = {"attn_norm": vec(E), "ffn_norm": vec(E), "q_bias": vec(QD, 0.1, 0.0), "k_bias": vec(KD, 0.1, 0.0),
          "v_bias": vec(KD, 0.1, 0.0), "q_norm": vec(HD), "k_norm": vec(HD),
-         "freqs": dev((1 + 3 * rng.random(rd // 2)).astype(F32))}
+         "freqs": dev((1 + 3 * frng.random(rd // 2)).astype(F32))}
+    if fseed is not None:  # the same factor tensor (one device pointer) for every call with this seed
+        v["freqs"] = _FREQS.setdefault((fseed, rd), v["freqs"])
     x0 = rng.standard_normal((T, E), dtype=F32)
     cache = rng.standard_normal((cap, KD), dtype=F32).astype(np.float16).view(np.int16)
     d = LayerDesc()
@@ -254,7 +279,7 @@ def test_layer_equals_its_operations(ctx, T, pos0, cap, HD, rd, neox):
     d.d_q_bias, d.d_k_bias, d.d_v_bias = (v[k].data_ptr() for k in ("q_bias", "k_bias", "v_bias"))
     d.d_q_norm, d.d_k_norm, d.d_rope_freqs = v["q_norm"].data_ptr(), v["k_norm"].data_ptr(), v["freqs"].data_ptr()
     d.embd, d.heads, d.kv_heads, d.head_dim, d.rope_dims, d.neox = E, H, KH, HD, rd, neox
-    d.rope_base, d.rope_freq_scale, d.eps, d.attention_scale, d.residual_scale = 10000.0, 0.5, 1e-6, asc, rs
+    d.rope_base, d.rope_freq_scale, d.eps, d.attention_scale, d.residual_scale = base, 0.5, 1e-6, asc, rs
     xa, Ka, Va = dev(x0), dev(cache), dev(cache)
     check(L.wl_layer_dev(h, ctypes.byref(d), P(xa), T, pos0, P(Ka), P(Va)))
     # the same, one operation at a time
@@ -276,7 +301,7 @@ def test_layer_equals_its_operations(ctx, T, pos0, cap, HD, rd, neox):
     check(L.wl_rms_norm_dev(h, P(q), T * H, HD, P(v["q_norm"]), c(1e-6), P(q)))
     check(L.wl_rms_norm_dev(h, P(k), T * KH, HD, P(v["k_norm"]), c(1e-6), P(k)))
     for y, nh in ((q, H), (k, KH)):
-        check(L.wl_rope_dev(h, P(y), T, nh, HD, rd, neox, pos0, None, 10000.0, 0.5, P(v["freqs"])))
+        check(L.wl_rope_dev(h, P(y), T, nh, HD, rd, neox, pos0, None, base, 0.5, P(v["freqs"])))
     check(L.wl_kv_store_dev(h, P(k), P(vv), T, KD, P(Kb), P(Vb), pos0))
     check(L.wl_attention_dev(h, P(q), T, H, KH, HD, P(Kb), P(Vb), pos0, c(asc), P(att)))
     check(L.wl_matmul_dev(h, w["attn_output"].handle, -1, P(att), T, P(o)))

@@ -3,6 +3,7 @@
 // Host-side only; the kernels live in wl_gemv.hip, wl_dequant.hip, wl_gemm.hip and wl_moe.hip.
 // Every entry point validates shapes on the host before anything is launched, so a kernel
 // never sees an operand that does not match its grid.
+#include <algorithm>
 #include <atomic>
 #include <hip/hip_runtime.h>
 
@@ -11,6 +12,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/windlass_hip.h"
 #include "wl_dequant.h"
@@ -79,6 +81,17 @@ struct wl_ctx {
   hipEvent_t rows_ev[kRowRing] = {};
   bool rows_used[kRowRing] = {};
   int rows_next = 0;
+  // RopeTable's cache (src/Transformer.cs:396-414): cos/sin of the rotated pairs by position for
+  // one RoPE setting, filled on first use of a position and reused by every layer after it; a
+  // setting change refills it
+  struct {
+    float4 *dev = nullptr;  // [cap][wl::kRopePairs]
+    int64_t cap = 0;        // positions
+    std::vector<uint8_t> have;
+    int n = 0;
+    double base = 0.0, fs = 0.0;
+    const float *freqs = nullptr;
+  } rope;
 };
 
 static thread_local std::string g_err;
@@ -292,6 +305,7 @@ extern "C" void wl_destroy(wl_ctx *c) {
   for (void *&b : c->buf)
     if (b) hipFree(b);
   if (c->rows_host) hipHostFree(c->rows_host);
+  if (c->rope.dev) hipFree(c->rope.dev);
   for (hipEvent_t &e : c->rows_ev)
     if (e) hipEventDestroy(e);
   hipStreamDestroy(c->stream);
@@ -1189,8 +1203,59 @@ extern "C" int wl_embed_dev_ids(wl_ctx *c, const wl_weight *embd, const int32_t 
 // rows' positions and cache slots (a batch step) and the most positions a row attends to;
 // each: every product in GEMV passes of at most 8 rows, so a row's bits do not depend on the
 // batch (ForwardBatch's EachToken, src/Transformer.cs:127-170).
+// The rows' RoPE angles in the context's table: positions hpos[0..T-1] (host values), or pos0 ..
+// pos0 + T - 1 when hpos is null. Missing positions are filled by one launch over their range,
+// queued before the caller's launches that read them.
+static int rope_angles(wl_ctx *c, const int32_t *hpos, int T, int pos0, int n, double base, double fs,
+                       const float *freqs, const float4 **tab) {
+  auto &R = c->rope;
+  if (R.n != n || R.base != base || R.fs != fs || R.freqs != freqs) {
+    std::fill(R.have.begin(), R.have.end(), (uint8_t)0);
+    R.n = n;
+    R.base = base;
+    R.fs = fs;
+    R.freqs = freqs;
+  }
+  int top = 0, lo = -1, hi = -1;
+  for (int i = 0; i < T; i++) {
+    const int p = hpos ? hpos[i] : pos0 + i;
+    if (p + 1 > top) top = p + 1;
+  }
+  if (top > R.cap) {
+    if (c->capturing)
+      return fail(WL_E_ARG, "a captured call needs RoPE angles of %d positions, the table holds %lld: run the same "
+                  "calls once before the capture", top, (long long)R.cap);
+    const int64_t cap = ((int64_t)top + 4095) / 4096 * 4096;
+    if (R.dev) {
+      hipStreamSynchronize(c->stream);
+      hipFree(R.dev);
+      R.dev = nullptr;
+      R.cap = 0;
+    }
+    void *d = nullptr;
+    if (dev_alloc(&d, (size_t)cap * wl::kRopePairs * sizeof(float4)) != hipSuccess)
+      return fail(WL_E_NOMEM, "cannot allocate the RoPE table of %lld positions", (long long)cap);
+    R.dev = (float4 *)d;
+    R.cap = cap;
+    R.have.assign((size_t)cap, 0);
+  }
+  for (int i = 0; i < T; i++) {
+    const int p = hpos ? hpos[i] : pos0 + i;
+    if (!R.have[p]) {
+      lo = lo < 0 || p < lo ? p : lo;
+      hi = p > hi ? p : hi;
+    }
+  }
+  if (hi >= 0) {
+    WL_HIP(wl::rope_table_launch(R.dev, lo, hi - lo + 1, n, base, fs, freqs, c->stream), "rope table");
+    for (int p = lo; p <= hi; p++) R.have[p] = 1;
+  }
+  *tab = R.dev;
+  return WL_OK;
+}
+
 static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
-                     uint16_t *d_V, const wl::RowMap &rm, int max_n, bool each) {
+                     uint16_t *d_V, const wl::RowMap &rm, const int32_t *hpos, int max_n, bool each) {
   if (!c || !L || !d_x || !d_K || !d_V) return fail(WL_E_ARG, "wl_layer_dev: null argument");
   // OLMo 2 (src/Transformer.cs:182,224-230): post-norms instead of pre-norms
   const bool post = L->d_post_attention_norm || L->d_post_ffw_norm;
@@ -1269,11 +1334,16 @@ static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, i
     return rc;
   if (L->d_k_norm && (rc = wl_rms_norm_dev(c, k, full ? T : (int64_t)T * KH, full ? KD : HD, L->d_k_norm, L->eps, k)))
     return rc;
-  // RoPE, the fp16 KV store and attention (one launch for a token or batch rows on their own slots)
+  // RoPE, the fp16 KV store and attention (one launch for a token or batch rows on their own slots,
+  // with the positions' angles from the context's table)
   const double fs = L->rope_freq_scale != 0.0 ? L->rope_freq_scale : 1.0;
   const float scale = L->attention_scale != 0.f ? L->attention_scale : 1.0f / (float)sqrt((double)HD);
-  WL_HIP(wl::rope_attention_launch(q, k, v, T, H, KH, HD, rd, L->neox, pos0, L->rope_base, fs, L->d_rope_freqs, d_K,
-                                   d_V, rm, scale, (float *)c->buf[S_ATT], att, max_n, c->stream),
+  const float4 *tab = nullptr;
+  if (wl::rope_attention_fused(T, rm, HD, KH, rd, d_K, d_V) &&
+      (rc = rope_angles(c, hpos, T, pos0, rd, L->rope_base, fs, L->d_rope_freqs, &tab)))
+    return rc;
+  WL_HIP(wl::rope_attention_launch(q, k, v, T, H, KH, HD, rd, L->neox, pos0, L->rope_base, fs, L->d_rope_freqs, tab,
+                                   d_K, d_V, rm, scale, (float *)c->buf[S_ATT], att, max_n, c->stream),
          "rope, kv store and attention");
   if (post) {
     // o = RmsNorm(W_o att), then x += o * rs (src/Transformer.cs:223-225)
@@ -1337,7 +1407,7 @@ static int layer_run(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, i
 
 extern "C" int wl_layer_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
                             uint16_t *d_V) {
-  return layer_run(c, L, d_x, T, pos0, d_K, d_V, wl::RowMap{}, pos0 + T, false);
+  return layer_run(c, L, d_x, T, pos0, d_K, d_V, wl::RowMap{}, nullptr, pos0 + T, false);
 }
 
 // Transformer.ForwardBatch's layer (src/Transformer.cs:127-170): N rows, each the next token of
@@ -1364,7 +1434,7 @@ extern "C" int wl_layer_batch_dev(wl_ctx *c, const wl_layer_desc *L, float *d_x,
   rm.pos = rows;
   rm.slot = rows + N;
   rm.cap = slot_positions;
-  return layer_run(c, L, d_x, N, 0, d_K, d_V, rm, max_n, true);
+  return layer_run(c, L, d_x, N, 0, d_K, d_V, rm, pos, max_n, true);
 }
 
 extern "C" int wl_read_peak_dev(wl_ctx *c, const void *d_src, int64_t bytes, int32_t workgroups, uint32_t *d_out) {

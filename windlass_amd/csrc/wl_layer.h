@@ -31,15 +31,24 @@ int64_t attention_scratch_floats(int T, int heads, int hd, int kv_dim, int max_n
 hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *K, const uint16_t *V, int kv_dim,
                             int heads, int kv_heads, int hd, int pos0, float scale, float *scratch, float *out,
                             int64_t ldo, const RowMap &rm, int max_n, hipStream_t st);
+// RoPE angles by position (RopeTable): tab [positions][kRopePairs] of (cos, sin, the frequency
+// factor used, 0), the pairs of n rotated dims at positions lo .. lo + count - 1 written by one
+// launch. Readers check the factor against the model's and take the angle again on a mismatch.
+constexpr int kRopePairs = 64;
+hipError_t rope_table_launch(float4 *tab, int lo, int count, int n, double base, double freq_scale,
+                             const float *freqs, hipStream_t st);
+// Whether rope_attention_launch runs as one launch (and then reads the table) for these rows.
+bool rope_attention_fused(int T, const RowMap &rm, int hd, int kv_heads, int n, const uint16_t *Kc,
+                          const uint16_t *Vc);
 // rope_kv_launch then attention_launch (q [T][H*hd] rotated, k rotated and both caches written,
 // out [T][H*hd]) for rows whose earlier positions are all cached: one token of a sequence, or
-// batch rows (rm) on distinct slots. Where the chunked attention kernel applies this is one
-// launch (the RoPE and the cache stores inside it; q and k are then left as they were), with
-// the same output and cache bits; otherwise the two launches.
+// batch rows (rm) on distinct slots. Where rope_attention_fused holds this is one launch (the
+// RoPE, with the rows' positions' angles from tab, and the cache stores inside it; q and k are
+// then left as they were), with the same output and cache bits; otherwise the two launches.
 hipError_t rope_attention_launch(float *q, float *k, const float *v, int T, int H, int KH, int hd, int n, int neox,
-                                 int pos0, double base, double freq_scale, const float *freqs, uint16_t *Kc,
-                                 uint16_t *Vc, const RowMap &rm, float scale, float *scratch, float *out, int max_n,
-                                 hipStream_t st);
+                                 int pos0, double base, double freq_scale, const float *freqs, const float4 *tab,
+                                 uint16_t *Kc, uint16_t *Vc, const RowMap &rm, float scale, float *scratch,
+                                 float *out, int max_n, hipStream_t st);
 hipError_t residual_launch(float *x, const float *o, int64_t n, float rs, hipStream_t st);
 // x[i] *= s
 hipError_t scale_launch(float *x, int64_t n, float s, hipStream_t st);

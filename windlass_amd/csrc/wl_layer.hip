@@ -143,6 +143,19 @@ __device__ __forceinline__ void rope_pair(float *o, int i, int n, int neox, floa
   o[b] = y1;
 }
 
+// RopeTable (src/Transformer.cs:396-414, computed once per position and reused by every layer):
+// (cos, sin, the pair's frequency factor used, 0) of the rotated pairs at positions lo, lo + 1,
+// ..., one wave per position, lane i pair i. A reader compares the factor with the model's (its
+// values may have changed under the same pointer) and takes the angle again on a mismatch.
+__global__ __launch_bounds__(64) void rope_table_kernel(float4 *__restrict__ tab, int lo, int half,
+                                                        double theta_scale, double freq_scale,
+                                                        const float *__restrict__ freqs) {
+  const int p = lo + (int)blockIdx.x, i = threadIdx.x;
+  float c, s;
+  rope_cs(p, i, half, theta_scale, freq_scale, freqs, c, s);
+  if (i < half) tab[(int64_t)p * kRopePairs + i] = make_float4(c, s, freqs ? freqs[i] : 1.f, 0.f);
+}
+
 // RoPE on q (H heads) and k (KH heads) of row t, and ToHalf of the row's keys and values into
 // cache row pos0 + t, or row pos[t] of slot slot[t] (slots of cap positions) for a batch step
 // (src/Transformer.cs:204-215,342-348). Work items of a row: one per rotated pair of every q and
@@ -303,10 +316,11 @@ __device__ __forceinline__ float mul_hi(uint32_t w, float x) { return __builtin_
 //
 // With ROPE the row's own key and value are this step's: rows whose earlier positions are all
 // cached (one token of a sequence, or batch rows on distinct slots). Each workgroup rotates its
-// query head itself (rope_cs / rope_pair: the bits rope_qkv_kernel gives), the chunk holding the
-// row's position rotates the new key and rounds key and value to fp16 (to_half) for that
-// position, and the first query head of each KV group stores them to the caches. Nothing in the
-// launch reads those cache rows, so the separate RoPE + KV store launch goes away.
+// query head itself (rope_pair with the position's angles from the table rope_table_kernel
+// fills: the bits rope_qkv_kernel gives), the chunk holding the row's position rotates the new
+// key and rounds key and value to fp16 (to_half) for that position, and the first query head of
+// each KV group stores them to the caches. Nothing in the launch reads those cache rows, so the
+// separate RoPE + KV store launch goes away.
 constexpr int kAttP = 256;
 
 struct RopeArgs {
@@ -314,6 +328,7 @@ struct RopeArgs {
   int n = 0, neox = 0;                     // rotated dims per head, NeoX pairing
   double theta_scale = 0.0, freq_scale = 1.0;
   const float *freqs = nullptr;
+  const float4 *tab = nullptr;            // angles by position: [position][kRopePairs] (rope_table_kernel)
   uint16_t *Kc = nullptr, *Vc = nullptr;  // the caches the rows' keys and values go to
 };
 
@@ -349,7 +364,15 @@ __global__ __launch_bounds__(256, 2) void attention_chunk_kernel(const float *__
   const bool fresh = ROPE && c == nch - 1;  // the chunk holds the row's position, cnt - 1
   const int nold = fresh ? cnt - 1 : cnt;   // positions read from the caches
   float qv = 0.f, kv = 0.f, vv = 0.f;
+  float2 cs = make_float2(0.f, 0.f);  // cos and sin of pair tid's angle at the row's position
   if (tid < HD) qv = q[(int64_t)t * ldq + (int64_t)h * HD + tid];
+  if (ROPE && tid < ra.n / 2) {
+    const float4 a = ra.tab[(int64_t)p * kRopePairs + tid];
+    cs = make_float2(a.x, a.y);
+    // an entry made with other frequency factors than the model's now: the angle again here
+    if (ra.freqs && __float_as_uint(a.z) != __float_as_uint(ra.freqs[tid]))
+      rope_cs(p, tid, ra.n / 2, ra.theta_scale, ra.freq_scale, ra.freqs, cs.x, cs.y);
+  }
   if (fresh) {
     const int64_t r = (int64_t)t * kv_dim + (int64_t)kvh * HD;
     if (tid < HD)
@@ -376,8 +399,6 @@ __global__ __launch_bounds__(256, 2) void attention_chunk_kernel(const float *__
     if (u * (256 / U) < nold)
       vr[u] = reinterpret_cast<const uint4 *>(V + (int64_t)(j0 + rc) * kv_dim + (int64_t)kvh * HD)[col];
   }
-  float ac = 0.f, as = 0.f;  // cos and sin of pair tid's angle, computed while the loads are in flight
-  if (ROPE && tid < 64) rope_cs(p, tid, ra.n / 2, ra.theta_scale, ra.freq_scale, ra.freqs, ac, as);  // wave 0
   if (tid < HD) qs[tid] = qv;
   if (fresh) {
     if (tid < HD)
@@ -390,9 +411,9 @@ __global__ __launch_bounds__(256, 2) void attention_chunk_kernel(const float *__
     if (tid < ra.n / 2) {
       float y0, y1;
       int a, b;
-      rope_pair(qs, tid, ra.n, ra.neox, ac, as, y0, y1, a, b);
+      rope_pair(qs, tid, ra.n, ra.neox, cs.x, cs.y, y0, y1, a, b);
       if (fresh) {
-        rope_pair(kn, tid, ra.n, ra.neox, ac, as, y0, y1, a, b);
+        rope_pair(kn, tid, ra.n, ra.neox, cs.x, cs.y, y0, y1, a, b);
         kh[a] = to_half(y0);
         kh[b] = to_half(y1);
       }
@@ -710,14 +731,27 @@ hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *
   return hipGetLastError();
 }
 
+hipError_t rope_table_launch(float4 *tab, int lo, int count, int n, double base, double freq_scale,
+                             const float *freqs, hipStream_t st) {
+  if (count <= 0 || n / 2 > kRopePairs) return count <= 0 ? hipSuccess : hipErrorInvalidValue;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)count), dim3(64), 0, st, tab, lo, n / 2, pow(base, -2.0 / n),
+                     freq_scale, freqs);
+  return hipGetLastError();
+}
+
+bool rope_attention_fused(int T, const RowMap &rm, int hd, int kv_heads, int n, const uint16_t *Kc,
+                          const uint16_t *Vc) {
+  const bool own = rm.pos ? rm.slot != nullptr : T == 1;  // every row's earlier positions are cached
+  return own && n / 2 <= kRopePairs && attention_chunked(hd, kv_heads * hd, Kc, Vc);
+}
+
 hipError_t rope_attention_launch(float *q, float *k, const float *v, int T, int H, int KH, int hd, int n, int neox,
-                                 int pos0, double base, double freq_scale, const float *freqs, uint16_t *Kc,
-                                 uint16_t *Vc, const RowMap &rm, float scale, float *scratch, float *out, int max_n,
-                                 hipStream_t st) {
+                                 int pos0, double base, double freq_scale, const float *freqs, const float4 *tab,
+                                 uint16_t *Kc, uint16_t *Vc, const RowMap &rm, float scale, float *scratch,
+                                 float *out, int max_n, hipStream_t st) {
   if (T <= 0) return hipSuccess;
   const int kv_dim = KH * hd;
-  const bool own = rm.pos ? rm.slot != nullptr : T == 1;  // every row's earlier positions are cached
-  if (!own || !attention_chunked(hd, kv_dim, Kc, Vc)) {
+  if (!rope_attention_fused(T, rm, hd, KH, n, Kc, Vc) || !tab) {
     hipError_t e = rope_kv_launch(q, k, v, T, H, KH, hd, n, neox, pos0, base, freq_scale, freqs, Kc, Vc, rm, st);
     if (e != hipSuccess) return e;
     return attention_launch(q, (int64_t)H * hd, T, Kc, Vc, kv_dim, H, KH, hd, pos0, scale, scratch, out,
@@ -731,6 +765,7 @@ hipError_t rope_attention_launch(float *q, float *k, const float *v, int T, int 
   ra.theta_scale = pow(base, -2.0 / n);
   ra.freq_scale = freq_scale;
   ra.freqs = freqs;
+  ra.tab = tab;
   ra.Kc = Kc;
   ra.Vc = Vc;
   const int64_t ld = (int64_t)H * hd;
