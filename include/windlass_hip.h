@@ -344,7 +344,11 @@ int wl_scale_dev(wl_ctx *ctx, float *d_x, int64_t n, float s);
  * rows pos0.. of the fp16 caches d_K / d_V [positions][kv_heads * head_dim]. Every activation
  * stays in HBM (the context's scratch); stream-ordered, no host wait. Up to 8 tokens the
  * products are the decode GEMVs (o and down add into x in their own store); more tokens take
- * the GEMMs. The caches must hold pos0 + T positions: the library cannot check their size. */
+ * the GEMMs. The caches must hold pos0 + T positions: the library cannot check their size.
+ * Like the reference's RopeTable (src/Transformer.cs:396-414) the context keeps the RoPE angles
+ * of the positions it has seen, for the last setting (rope dims, base, frequency scale,
+ * rope_freqs pointer); each entry records the frequency factors it was made with, and an entry
+ * whose factors no longer match the tensor's values is computed again. */
 int wl_layer_dev(wl_ctx *ctx, const wl_layer_desc *layer, float *d_x, int32_t T, int32_t pos0, uint16_t *d_K,
                  uint16_t *d_V);
 
