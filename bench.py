@@ -316,10 +316,18 @@ def gemv_bytes(mats, T):
     return sum(mat_bytes(t, r, c) + 4 * T * (c + r) for _, t, r, c in mats)
 
 
-def time_events(stream, fn, reps, warm=5):
-    """Average ms per fn(i) call, HIP events on the library's stream around reps calls."""
+def time_events(stream, fn, reps, warm=5, settle=0.2):
+    """Average ms per fn(i) call, HIP events on the library's stream around reps calls, after
+    `settle` seconds of untimed calls (the clocks settle under sustained load; a workload's
+    host-side set-up leaves the GPU idle before it) and `warm` more."""
     import torch
     with torch.cuda.stream(stream):
+        t0, n = time.time(), 0
+        while time.time() - t0 < settle:
+            for _ in range(20):
+                fn(n)
+                n += 1
+            stream.synchronize()
         for i in range(warm):
             fn(i)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
