@@ -151,6 +151,29 @@ def test_attention(ctx, heads, kv_heads, hd, T, pos0):
     assert (err <= 2e-6 * np.abs(want).max(axis=1)).all(), err
 
 
+@pytest.mark.parametrize("heads,kv_heads,hd", [(8, 2, 128), (4, 1, 64), (16, 1, 128)])
+@pytest.mark.parametrize("p", [1, 100, 255, 256, 300, 700])
+@pytest.mark.parametrize("qs", [1.0, 30.0])  # 30: a wide softmax, many tiny probabilities
+def test_attention_row_bits_independent_of_kernel(ctx, heads, kv_heads, hd, p, qs):
+    """A row's attention has the same bits whichever kernel computes it: one token at position p
+    (the per-head kernel up to 256 positions, the KV-group kernel past them) against the same row
+    as the second of two prompt rows (the row-tiled kernel), so a batch row's bits do not depend on
+    the other rows' lengths."""
+    rng = np.random.default_rng(p * 31 + hd + int(qs))
+    kd, n = kv_heads * hd, p + 1
+    K, V = fp16_cache(rng, n, kd), fp16_cache(rng, n, kd)
+    q = (qs * rng.standard_normal((2, heads * hd))).astype(F32)
+    scale = F32(1) / F32(math.sqrt(hd))
+    dq, dq1, dK, dV = dev(q), dev(q[1:2].copy()), dev(K.view(np.int16)), dev(V.view(np.int16))
+    out2 = torch.empty((2, heads * hd), device=DEV)
+    out1 = torch.empty((1, heads * hd), device=DEV)
+    L = load()
+    check(L.wl_attention_dev(ctx.handle, P(dq), 2, heads, kv_heads, hd, P(dK), P(dV), p - 1, float(scale), P(out2)))
+    check(L.wl_attention_dev(ctx.handle, P(dq1), 1, heads, kv_heads, hd, P(dK), P(dV), p, float(scale), P(out1)))
+    a, b = host(ctx, out1).view(np.uint32), host(ctx, out2)[1:2].view(np.uint32)
+    assert np.array_equal(a, b), np.argwhere(a != b)[:8]
+
+
 def test_residual(ctx):
     rng = np.random.default_rng(5)
     x, o = rng.standard_normal(1001, dtype=F32), rng.standard_normal(1001, dtype=F32)

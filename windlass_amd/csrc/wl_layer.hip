@@ -322,6 +322,7 @@ __device__ __forceinline__ float mul_hi(uint32_t w, float x) { return __builtin_
 // each KV group stores them to the caches. Nothing in the launch reads those cache rows, so the
 // separate RoPE + KV store launch goes away.
 constexpr int kAttP = 256;
+constexpr int kAttGroup = 16;  // query heads per KV head that attention_group_kernel takes
 #ifndef WL_ATT_ROWS
 #define WL_ATT_ROWS 16
 #endif
@@ -349,6 +350,7 @@ __global__ __launch_bounds__(256, 2) void attention_chunk_kernel(const float *__
   __shared__ __attribute__((aligned(16))) float ps[kAttP];
   __shared__ float shf[4];
   __shared__ double shd[4];
+  __shared__ double esd[kAttP];
   __shared__ __attribute__((aligned(16))) float kn[ROPE ? HD : 4];
   __shared__ __attribute__((aligned(16))) uint16_t kh[ROPE ? HD : 8], vh[ROPE ? HD : 8];
   const int h = blockIdx.x, c = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
@@ -473,12 +475,19 @@ __global__ __launch_bounds__(256, 2) void attention_chunk_kernel(const float *__
     e = (float)exp((double)(d - mx));
     sum = (double)e;
   }
-  {
-    const double s = wave_sum_d(sum);
-    if ((tid & 63) == 0) shd[wv] = s;
+  // the denominator as wave_attend forms it (lane l adds positions l, l + 64, l + 128, l + 192 in
+  // that order, then the wave's DPP sum), so every attention kernel gives a row the same bits
+  esd[tid] = sum;
+  __syncthreads();
+  if (wv == 0) {
+    double s4 = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) s4 += esd[tid + 64 * i];
+    s4 = wave_sum_d(s4);
+    if (tid == 0) shd[0] = s4;
   }
   __syncthreads();
-  sum = ((shd[0] + shd[1]) + shd[2]) + shd[3];
+  sum = shd[0];
   ps[tid] = nch == 1 ? e * (float)(1.0 / sum) : e;  // zero past cnt
   __syncthreads();  // also orders the writes of vs4 before the reads below
   float *rec = part + (((int64_t)t * heads + h) * max_chunks + c) * (HD + 4);
@@ -504,6 +513,98 @@ __global__ __launch_bounds__(256, 2) void attention_chunk_kernel(const float *__
       rec[tid] = o;  // record: HD unnormalised sums, the chunk maximum, a pad, the double sum
   }
   if (nch > 1 && tid == 0) {
+    rec[HD] = mx;
+    *reinterpret_cast<double *>(rec + HD + 2) = sum;
+  }
+}
+
+// One row of one query head against a chunk staged in LDS (keys in rows of KS uint4, values in
+// rows of HD/8 uint4), by one wave, every lane active: the reference's four partial sums per
+// score (positions lane + 64 i), the maximum, exp in double, the denominator in double, p = e *
+// inv, each output value adding its positions in order (lane l adds columns 2l and 2l + 1). A
+// row of one chunk writes orow; a longer row writes its chunk's record (HD unnormalised sums,
+// the chunk maximum, a pad, the double sum) for attention_combine_kernel. qw: the row's query
+// (HD floats in LDS); pw: the wave's own kAttP floats of LDS.
+template <int HD, int KS>
+__device__ __forceinline__ void wave_attend(const uint4 *__restrict__ ks4, const uint4 *__restrict__ vs4,
+                                            const float *qw, float *pw, int cnt, int nch, float scale, int lane,
+                                            float *__restrict__ orow, float *__restrict__ rec) {
+  constexpr int U = HD / 8;
+  // scores of positions lane + 64 i
+  float d[4];
+  {
+    float s[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) s[i][0] = s[i][1] = s[i][2] = s[i][3] = 0.f;
+    const float4 *q4 = reinterpret_cast<const float4 *>(qw);
+#pragma unroll 4
+    for (int u = 0; u < U; u++) {
+      const float4 qa = q4[2 * u], qb = q4[2 * u + 1];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int j = lane + 64 * i < cnt ? lane + 64 * i : cnt - 1;
+        const uint4 k = ks4[j * KS + u];
+        s[i][0] += mul_lo(k.x, qa.x);
+        s[i][1] += mul_hi(k.x, qa.y);
+        s[i][2] += mul_lo(k.y, qa.z);
+        s[i][3] += mul_hi(k.y, qa.w);
+        s[i][0] += mul_lo(k.z, qb.x);
+        s[i][1] += mul_hi(k.z, qb.y);
+        s[i][2] += mul_lo(k.w, qb.z);
+        s[i][3] += mul_hi(k.w, qb.w);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      d[i] = lane + 64 * i < cnt ? ((s[i][0] + s[i][1]) + (s[i][2] + s[i][3])) * scale : -INFINITY;
+  }
+  const float mx = wave_max_f(fmaxf(fmaxf(d[0], d[1]), fmaxf(d[2], d[3])));
+  float e[4];
+  double sum = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    e[i] = 0.f;
+    if (lane + 64 * i < cnt) {
+      e[i] = (float)exp((double)(d[i] - mx));
+      sum += (double)e[i];
+    }
+  }
+  sum = wave_sum_d(sum);
+  const float inv = (float)(1.0 / sum);
+#pragma unroll
+  for (int i = 0; i < 4; i++) pw[lane + 64 * i] = nch == 1 ? e[i] * inv : e[i];
+  // the wave's own LDS writes before its reads (no other wave reads pw)
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  float o0 = 0.f, o1 = 0.f;
+  if (2 * lane < HD) {
+    const uint32_t *vc = reinterpret_cast<const uint32_t *>(vs4) + lane;  // columns 2 lane, 2 lane + 1
+    const float4 *p4 = reinterpret_cast<const float4 *>(pw);
+    int j = 0;
+    for (; j + 4 <= cnt; j += 4) {
+      const float4 pj = p4[j / 4];
+      const uint32_t v0 = vc[(j + 0) * (HD / 2)], v1 = vc[(j + 1) * (HD / 2)], v2 = vc[(j + 2) * (HD / 2)],
+                     v3 = vc[(j + 3) * (HD / 2)];
+      o0 += mul_lo(v0, pj.x);
+      o1 += mul_hi(v0, pj.x);
+      o0 += mul_lo(v1, pj.y);
+      o1 += mul_hi(v1, pj.y);
+      o0 += mul_lo(v2, pj.z);
+      o1 += mul_hi(v2, pj.z);
+      o0 += mul_lo(v3, pj.w);
+      o1 += mul_hi(v3, pj.w);
+    }
+    for (; j < cnt; j++) {
+      const uint32_t v = vc[j * (HD / 2)];
+      const float pj = pw[j];
+      o0 += mul_lo(v, pj);
+      o1 += mul_hi(v, pj);
+    }
+    if (nch == 1)
+      *reinterpret_cast<float2 *>(orow + 2 * lane) = make_float2(o0, o1);
+    else  // record: HD unnormalised sums, the chunk maximum, a pad, the double sum
+      *reinterpret_cast<float2 *>(rec + 2 * lane) = make_float2(o0, o1);
+  }
+  if (nch > 1 && lane == 0) {
     rec[HD] = mx;
     *reinterpret_cast<double *>(rec + HD + 2) = sum;
   }
@@ -553,87 +654,96 @@ __global__ __launch_bounds__(64 * RW) void attention_rows_kernel(const float *__
   const int n = pos0 + t + 1;
   if (t >= T || j0 >= n) return;  // uniform over the wave; no barrier follows
   const int cnt = n - j0 < kAttP ? n - j0 : kAttP, nch = (n + kAttP - 1) / kAttP;
-  // scores of positions lane + 64 i
-  float d[4];
-  {
-    float s[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) s[i][0] = s[i][1] = s[i][2] = s[i][3] = 0.f;
-    const float4 *q4 = reinterpret_cast<const float4 *>(qs[w]);
-#pragma unroll 4
-    for (int u = 0; u < U; u++) {
-      const float4 qa = q4[2 * u], qb = q4[2 * u + 1];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int j = lane + 64 * i < cnt ? lane + 64 * i : cnt - 1;
-        const uint4 k = ks4[j * KS + u];
-        s[i][0] += mul_lo(k.x, qa.x);
-        s[i][1] += mul_hi(k.x, qa.y);
-        s[i][2] += mul_lo(k.y, qa.z);
-        s[i][3] += mul_hi(k.y, qa.w);
-        s[i][0] += mul_lo(k.z, qb.x);
-        s[i][1] += mul_hi(k.z, qb.y);
-        s[i][2] += mul_lo(k.w, qb.z);
-        s[i][3] += mul_hi(k.w, qb.w);
+  wave_attend<HD, KS>(ks4, vs4, qs[w], ps[w], cnt, nch, scale, lane, out + (int64_t)t * ldo + (int64_t)h * HD,
+                      part + (((int64_t)t * heads + h) * max_chunks + c) * (HD + 4));
+}
+
+// Attention for decode rows (one token of a sequence, or batch rows on their own slots; head
+// dims 64 and 128, at most 16 query heads per KV head): one workgroup of G = heads / kv_heads
+// waves per (KV head, chunk of kAttP positions, row). The chunk's keys and values are staged in
+// LDS once for the G query heads that read them (one workgroup per query head loaded them G
+// times), wave g computing query head kvh * G + g with wave_attend.
+// With ROPE the row's own key and value are this step's (every earlier position of the row is
+// cached): each wave rotates its query head with the position's angles from the table
+// (rope_table_kernel; an entry made with other frequency factors is taken again with rope_cs),
+// and in the chunk holding the row's position wave 0 rotates the new key, rounds key and value to
+// fp16 (to_half) into the staged chunk and stores them to the caches. Nothing in the launch reads
+// those cache rows, so the RoPE + KV store launch goes away; q and k stay as they were.
+template <int HD, bool ROPE>
+__global__ __launch_bounds__(1024) void attention_group_kernel(const float *__restrict__ q, int64_t ldq,
+                                                               const uint16_t *K, const uint16_t *V, int kv_dim,
+                                                               int heads, int kv_heads, int pos0, float scale,
+                                                               float *__restrict__ part, int max_chunks,
+                                                               float *__restrict__ out, int64_t ldo,
+                                                               const int *__restrict__ pos,
+                                                               const int *__restrict__ slot, int64_t cap, RopeArgs ra) {
+  constexpr int U = HD / 8, KS = U + 1;  // uint4 per key row; per padded LDS key row
+  __shared__ uint4 ks4[kAttP * KS];
+  __shared__ uint4 vs4[kAttP * U];
+  __shared__ __attribute__((aligned(16))) float qs[kAttGroup][HD];
+  __shared__ __attribute__((aligned(16))) float ps[kAttGroup][kAttP];
+  __shared__ __attribute__((aligned(16))) float kn[ROPE ? HD : 4];
+  const int kvh = blockIdx.x, c = blockIdx.y, t = blockIdx.z, tid = threadIdx.x, lane = tid & 63;
+  const int G = heads / kv_heads, g = __builtin_amdgcn_readfirstlane(tid >> 6), h = kvh * G + g;
+  const int p = pos ? pos[t] : pos0 + t, n = p + 1, j0 = c * kAttP;
+  if (j0 >= n) return;  // uniform over the workgroup
+  int64_t crow = p;     // the row's cache row
+  if (slot) {           // row t reads its own sequence's slot
+    K += (int64_t)slot[t] * cap * kv_dim;
+    V += (int64_t)slot[t] * cap * kv_dim;
+    crow += (int64_t)slot[t] * cap;
+  }
+  const int cnt = n - j0 < kAttP ? n - j0 : kAttP, nch = (n + kAttP - 1) / kAttP;
+  const bool fresh = ROPE && c == nch - 1;  // the chunk holds the row's position, cnt - 1
+  const int nold = fresh ? cnt - 1 : cnt;   // positions read from the caches
+  const uint16_t *Kb = K + (int64_t)j0 * kv_dim + (int64_t)kvh * HD;
+  const uint16_t *Vb = V + (int64_t)j0 * kv_dim + (int64_t)kvh * HD;
+  for (int e = tid; e < nold * U; e += 64 * G) {
+    const int r = e / U, col = e % U;
+    ks4[r * KS + col] = reinterpret_cast<const uint4 *>(Kb + (int64_t)r * kv_dim)[col];
+    vs4[e] = reinterpret_cast<const uint4 *>(Vb + (int64_t)r * kv_dim)[col];
+  }
+  const float *qp = q + (int64_t)t * ldq + (int64_t)h * HD;
+  for (int i = lane; i < HD; i += 64) qs[g][i] = qp[i];
+  if (ROPE) {
+    const int64_t r = (int64_t)t * kv_dim + (int64_t)kvh * HD;
+    float2 cs = make_float2(0.f, 0.f);
+    if (lane < ra.n / 2) {
+      const float4 a = ra.tab[(int64_t)p * kRopePairs + lane];
+      cs = make_float2(a.x, a.y);
+      if (ra.freqs && __float_as_uint(a.z) != __float_as_uint(ra.freqs[lane]))
+        rope_cs(p, lane, ra.n / 2, ra.theta_scale, ra.freq_scale, ra.freqs, cs.x, cs.y);
+    }
+    if (fresh && g == 0)
+      for (int i = lane; i < HD; i += 64) kn[i] = ra.k[r + i];
+    // the wave's own LDS writes (qs[g], kn) come before its reads below: one wave's LDS
+    // operations run in order
+    uint16_t *kh = reinterpret_cast<uint16_t *>(ks4 + (cnt - 1) * KS);
+    uint16_t *vh = reinterpret_cast<uint16_t *>(vs4 + (cnt - 1) * U);
+    if (lane < ra.n / 2) {
+      float y0, y1;
+      int a, b;
+      rope_pair(qs[g], lane, ra.n, ra.neox, cs.x, cs.y, y0, y1, a, b);
+      if (fresh && g == 0) {
+        rope_pair(kn, lane, ra.n, ra.neox, cs.x, cs.y, y0, y1, a, b);
+        kh[a] = to_half(y0);
+        kh[b] = to_half(y1);
       }
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      d[i] = lane + 64 * i < cnt ? ((s[i][0] + s[i][1]) + (s[i][2] + s[i][3])) * scale : -INFINITY;
-  }
-  const float mx = wave_max_f(fmaxf(fmaxf(d[0], d[1]), fmaxf(d[2], d[3])));
-  float e[4];
-  double sum = 0.0;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    e[i] = 0.f;
-    if (lane + 64 * i < cnt) {
-      e[i] = (float)exp((double)(d[i] - mx));
-      sum += (double)e[i];
+    if (fresh && g == 0) {
+      for (int i = ra.n + lane; i < HD; i += 64) kh[i] = to_half(kn[i]);  // key columns past the rotated ones
+      for (int i = lane; i < HD; i += 64) vh[i] = to_half(ra.v[r + i]);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's kh / vh writes done
+      const int64_t o = crow * kv_dim + (int64_t)kvh * HD;
+      for (int i = lane; i < HD; i += 64) {
+        ra.Kc[o + i] = kh[i];
+        ra.Vc[o + i] = vh[i];
+      }
     }
   }
-  sum = wave_sum_d(sum);
-  const float inv = (float)(1.0 / sum);
-#pragma unroll
-  for (int i = 0; i < 4; i++) ps[w][lane + 64 * i] = nch == 1 ? e[i] * inv : e[i];
-  // the wave's own LDS writes before its reads (no other wave reads ps[w])
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-  float o0 = 0.f, o1 = 0.f;
-  if (2 * lane < HD) {
-    const uint32_t *vc = reinterpret_cast<const uint32_t *>(vs4) + lane;  // columns 2 lane, 2 lane + 1
-    const float4 *p4 = reinterpret_cast<const float4 *>(ps[w]);
-    int j = 0;
-    for (; j + 4 <= cnt; j += 4) {
-      const float4 pj = p4[j / 4];
-      const uint32_t v0 = vc[(j + 0) * (HD / 2)], v1 = vc[(j + 1) * (HD / 2)], v2 = vc[(j + 2) * (HD / 2)],
-                     v3 = vc[(j + 3) * (HD / 2)];
-      o0 += mul_lo(v0, pj.x);
-      o1 += mul_hi(v0, pj.x);
-      o0 += mul_lo(v1, pj.y);
-      o1 += mul_hi(v1, pj.y);
-      o0 += mul_lo(v2, pj.z);
-      o1 += mul_hi(v2, pj.z);
-      o0 += mul_lo(v3, pj.w);
-      o1 += mul_hi(v3, pj.w);
-    }
-    for (; j < cnt; j++) {
-      const uint32_t v = vc[j * (HD / 2)];
-      const float pj = ps[w][j];
-      o0 += mul_lo(v, pj);
-      o1 += mul_hi(v, pj);
-    }
-    if (nch == 1) {
-      *reinterpret_cast<float2 *>(out + (int64_t)t * ldo + (int64_t)h * HD + 2 * lane) = make_float2(o0, o1);
-    } else {  // record: HD unnormalised sums, the chunk maximum, a pad, the double sum
-      float *rec = part + (((int64_t)t * heads + h) * max_chunks + c) * (HD + 4);
-      *reinterpret_cast<float2 *>(rec + 2 * lane) = make_float2(o0, o1);
-    }
-  }
-  if (nch > 1 && lane == 0) {
-    float *rec = part + (((int64_t)t * heads + h) * max_chunks + c) * (HD + 4);
-    rec[HD] = mx;
-    *reinterpret_cast<double *>(rec + HD + 2) = sum;
-  }
+  __syncthreads();
+  wave_attend<HD, KS>(ks4, vs4, qs[g], ps[g], cnt, nch, scale, lane, out + (int64_t)t * ldo + (int64_t)h * HD,
+                      part + (((int64_t)t * heads + h) * max_chunks + c) * (HD + 4));
 }
 
 // Rows longer than one chunk: m = the largest chunk maximum, each chunk weighted by
@@ -860,6 +970,26 @@ static hipError_t attention_chunked_launch(const float *q, int64_t ldq, int T, c
   return hipGetLastError();
 }
 
+// The decode rows' kernel (attention_group_kernel) and, for rows longer than one chunk, the combine.
+template <int HD, bool ROPE>
+static hipError_t attention_group_launch(const float *q, int64_t ldq, int T, const uint16_t *K, const uint16_t *V,
+                                         int kv_dim, int heads, int kv_heads, int pos0, float scale, float *part,
+                                         float *out, int64_t ldo, const RowMap &rm, int max_n, const RopeArgs &ra,
+                                         hipStream_t st) {
+  const int chunks = (max_n + kAttP - 1) / kAttP, G = heads / kv_heads;
+  hipLaunchKernelGGL((attention_group_kernel<HD, ROPE>), dim3(kv_heads, chunks, T), dim3(64 * G), 0, st, q, ldq, K, V,
+                     kv_dim, heads, kv_heads, pos0, scale, part, chunks, out, ldo, rm.pos, rm.slot, rm.cap, ra);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || chunks == 1) return e;
+  hipLaunchKernelGGL(attention_combine_kernel<HD>, dim3(heads, T), dim3(HD), (size_t)chunks * 12, st, part, chunks,
+                     heads, pos0, out, ldo, rm.pos);
+  return hipGetLastError();
+}
+
+// Rows whose earlier positions are all cached and not written by another row of the call: one
+// token of a sequence, or batch rows on distinct slots.
+static bool own_rows(int T, const RowMap &rm) { return rm.pos ? rm.slot != nullptr : T == 1; }
+
 hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *K, const uint16_t *V, int kv_dim,
                             int heads, int kv_heads, int hd, int pos0, float scale, float *scratch, float *out,
                             int64_t ldo, const RowMap &rm, int max_n, hipStream_t st) {
@@ -884,6 +1014,13 @@ hipError_t attention_launch(const float *q, int64_t ldq, int T, const uint16_t *
                          chunks, heads, pos0, out, ldo, (const int *)nullptr);
     return hipGetLastError();
   }
+  if (own_rows(T, rm) && max_n > kAttP && heads / kv_heads <= kAttGroup && attention_chunked(hd, kv_dim, K, V)) {
+    const RopeArgs none;
+    return hd == 64 ? attention_group_launch<64, false>(q, ldq, T, K, V, kv_dim, heads, kv_heads, pos0, scale, scratch,
+                                                        out, ldo, rm, max_n, none, st)
+                    : attention_group_launch<128, false>(q, ldq, T, K, V, kv_dim, heads, kv_heads, pos0, scale,
+                                                         scratch, out, ldo, rm, max_n, none, st);
+  }
   if (attention_chunked(hd, kv_dim, K, V)) {
     const RopeArgs none;
     return hd == 64 ? attention_chunked_launch<64, false>(q, ldq, T, K, V, kv_dim, heads, kv_heads, pos0, scale,
@@ -906,8 +1043,7 @@ hipError_t rope_table_launch(float4 *tab, int lo, int count, int n, double base,
 
 bool rope_attention_fused(int T, const RowMap &rm, int hd, int kv_heads, int n, const uint16_t *Kc,
                           const uint16_t *Vc) {
-  const bool own = rm.pos ? rm.slot != nullptr : T == 1;  // every row's earlier positions are cached
-  return own && n / 2 <= kRopePairs && attention_chunked(hd, kv_heads * hd, Kc, Vc);
+  return own_rows(T, rm) && n / 2 <= kRopePairs && attention_chunked(hd, kv_heads * hd, Kc, Vc);
 }
 
 hipError_t rope_attention_launch(float *q, float *k, const float *v, int T, int H, int KH, int hd, int n, int neox,
@@ -934,6 +1070,11 @@ hipError_t rope_attention_launch(float *q, float *k, const float *v, int T, int 
   ra.Kc = Kc;
   ra.Vc = Vc;
   const int64_t ld = (int64_t)H * hd;
+  if (max_n > kAttP && H / KH <= kAttGroup)  // past one chunk: each KV head's chunk loaded once for its heads
+    return hd == 64 ? attention_group_launch<64, true>(q, ld, T, Kc, Vc, kv_dim, H, KH, pos0, scale, scratch, out, ld,
+                                                       rm, max_n, ra, st)
+                    : attention_group_launch<128, true>(q, ld, T, Kc, Vc, kv_dim, H, KH, pos0, scale, scratch, out,
+                                                        ld, rm, max_n, ra, st);
   return hd == 64 ? attention_chunked_launch<64, true>(q, ld, T, Kc, Vc, kv_dim, H, KH, pos0, scale, scratch, out, ld,
                                                        rm, max_n, ra, st)
                   : attention_chunked_launch<128, true>(q, ld, T, Kc, Vc, kv_dim, H, KH, pos0, scale, scratch, out,
