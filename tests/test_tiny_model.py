@@ -260,6 +260,30 @@ def test_gpu_batch_step_rows_equal_single_sequences(gpu, key, n_seq):
         w.free()
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("key", [k for k in ("llama-q4_K", "qwen3-q4_K") if k in SPECS])
+def test_gpu_long_batch_rows_equal_single_sequences(gpu, key):
+    """The same promise past one 256-position attention chunk: prompts of 250, 254 and 300 tokens
+    (the prompt rows' kernel with chunk partials), then stacked steps that cross 256 positions
+    (the KV-group kernel with RoPE and the KV store inside it, in each sequence's own slot) give
+    every row the bits of its sequence's own one-token steps."""
+    from windlass_amd import DeviceBatch
+    prompts = [[PROBE[(5 * i + j) % len(PROBE)] for j in range(n)] for i, n in enumerate((250, 254, 300))]
+    dm, weights = device_model(gpu, key, max_positions=320)
+    single = []
+    for p in prompts:
+        dm.length = 0
+        single.append(dm.greedy(p, 4, keep_logits=True))
+    batch = DeviceBatch(dm, slots=3, slot_positions=320)
+    toks, seen = batch.greedy(prompts, 4, keep_logits=True)
+    for i in range(3):
+        assert toks[i] == single[i][0], (i, toks[i], single[i][0])
+        for s in range(5):
+            assert np.array_equal(seen[s][i].view(np.uint32), single[i][1][s].view(np.uint32)), (i, s)
+    for w in weights.values():
+        w.free()
+
+
 _LAYER_NAMES = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
 
 
