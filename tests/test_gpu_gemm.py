@@ -19,11 +19,13 @@ pytestmark = pytest.mark.gpu
 
 # rows x cols x T: tile edges in rows (128) and tokens (256), K from one 256-block up. Launches
 # with fewer output tiles than CUs split K into chunks (all but the first two shapes below on a
-# 256-CU device); 4224 x 512 x 2000 has 264 tiles and runs unsplit. Q4_K and Q6_K prompts of 384
+# 256-CU device); 4224 x 512 x 2000 has 264 tiles and runs unsplit. Q4_K and Q6_K prompts of 128
 # tokens and more take the 512-token tiles: 4224 x 512 x 2000 (four token tiles, the last 464
-# tokens), 200 x 1024 x 400 (split K, ragged rows), 130 x 2048 x 1000 (two token tiles, split K).
+# tokens), 200 x 1024 x 400 (split K, ragged rows), 130 x 2048 x 1000 (two token tiles, split K),
+# 1000 x 4096 x 129 and 64 x 512 x 300 (one partly filled tile), 200 x 1024 x 600 (a second tile
+# of 88 tokens).
 SHAPES = [(128, 256, 128), (4224, 512, 2000), (200, 1024, 37), (300, 2048, 9), (64, 512, 300),
-          (1000, 4096, 129), (200, 1024, 400), (130, 2048, 1000)]
+          (1000, 4096, 129), (200, 1024, 400), (130, 2048, 1000), (200, 1024, 600)]
 
 
 @pytest.fixture(scope="module")
