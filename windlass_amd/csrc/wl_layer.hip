@@ -263,42 +263,6 @@ __global__ __launch_bounds__(256) void attention_kernel(const float *__restrict_
   }
 }
 
-// Wave-wide reductions through DPP: lanes xor 1 and xor 2 (quad permutes), rotations by 4 and
-// 8 within each row of 16 lanes, then lane 0 of each row, combined as (r0 + r1) + (r2 + r3).
-// The result is uniform. Every lane of the wave must be active.
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
-}
-template <int CTRL>
-__device__ __forceinline__ double dpp64(double v) {
-  const uint64_t b = __builtin_bit_cast(uint64_t, v);
-  return __builtin_bit_cast(double, (uint64_t)dpp32<CTRL>((uint32_t)(b >> 32)) << 32 | dpp32<CTRL>((uint32_t)b));
-}
-__device__ __forceinline__ float lane_f(float v, int l) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
-}
-__device__ __forceinline__ double lane_d(double v, int l) {
-  const uint64_t b = __builtin_bit_cast(uint64_t, v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
-  return __builtin_bit_cast(double, (uint64_t)hi << 32 | lo);
-}
-__device__ __forceinline__ float wave_max_f(float v) {
-  v = fmaxf(v, __builtin_bit_cast(float, dpp32<0xB1>(__builtin_bit_cast(uint32_t, v))));   // quad_perm 1,0,3,2
-  v = fmaxf(v, __builtin_bit_cast(float, dpp32<0x4E>(__builtin_bit_cast(uint32_t, v))));   // quad_perm 2,3,0,1
-  v = fmaxf(v, __builtin_bit_cast(float, dpp32<0x124>(__builtin_bit_cast(uint32_t, v))));  // row_ror 4
-  v = fmaxf(v, __builtin_bit_cast(float, dpp32<0x128>(__builtin_bit_cast(uint32_t, v))));  // row_ror 8
-  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
-}
-__device__ __forceinline__ double wave_sum_d(double v) {
-  v += dpp64<0xB1>(v);
-  v += dpp64<0x4E>(v);
-  v += dpp64<0x124>(v);
-  v += dpp64<0x128>(v);
-  return (lane_d(v, 0) + lane_d(v, 16)) + (lane_d(v, 32) + lane_d(v, 48));
-}
-
 // One rounding of f16(w.lo) * x: v_fma_mix_f32 with a +0 addend equals the product except that
 // an exact -0 product comes out +0. The sums it feeds start at +0 and cannot become -0 (in
 // round-to-nearest x + y is -0 only when both are -0), so adding +0 or -0 leaves them as they are.

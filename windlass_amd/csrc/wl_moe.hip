@@ -387,20 +387,8 @@ struct RouteLds {
   int inexact, nan[kMoeWaves];
 };
 
-__device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const float u = __shfl_xor(v, o, 64);
-    if (u > v) v = u;
-  }
-  return v;
-}
-
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+// wave_max_f / wave_sum_d (wl_device.h): DPP wave reductions. The maximum is exact in any order
+// (no NaN reaches it); the denominator's tree only runs when its sum is exact (below).
 
 __device__ void route_group(const float *__restrict__ logits, int T, int n, int k, int renorm, int *__restrict__ sel,
                             float *__restrict__ wts, RouteLds &L) {
