@@ -45,6 +45,17 @@ __device__ float block_max_f(float v, float *sh) {
   return s;
 }
 
+// Block-wide sum of doubles for rms_norm_kernel: each wave's DPP sum (wave_sum_d), then the
+// waves' sums in order; one barrier (sh is not reused).
+__device__ __forceinline__ double block_sum_dpp(double v, double *sh) {
+  v = wave_sum_d(v);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double s = 0.0;
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += sh[i];
+  return s;
+}
+
 // RmsNormRows (src/Transformer.cs:446-457): one workgroup per row. Each thread squares and adds
 // its values in double (float4 loads when the row allows), then a tree over the workgroup.
 // Enough threads that a thread holds a few loads at most: the row's latency is one or two
@@ -77,7 +88,7 @@ __global__ __launch_bounds__(1024) void rms_norm_kernel(const float *x, int64_t 
     s += (double)xb.y * (double)xb.y;
     s += (double)xb.z * (double)xb.z;
     s += (double)xb.w * (double)xb.w;
-    s = block_sum_d(s, sh);
+    s = block_sum_dpp(s, sh);
     const float mean = (float)(s / (double)dim);
     const float scale = 1.0f / (float)sqrt((double)(mean + eps));
     if (i0 < dim)
@@ -99,7 +110,7 @@ __global__ __launch_bounds__(1024) void rms_norm_kernel(const float *x, int64_t 
   } else {
     for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) s += (double)xr[i] * (double)xr[i];
   }
-  s = block_sum_d(s, sh);  // every read of x precedes the writes below (in place)
+  s = block_sum_dpp(s, sh);  // every read of x precedes the writes below (in place)
   const float mean = (float)(s / (double)dim);
   const float scale = 1.0f / (float)sqrt((double)(mean + eps));
   if (vec) {
