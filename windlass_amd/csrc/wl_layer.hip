@@ -517,6 +517,7 @@ __device__ __forceinline__ void wave_attend(const uint4 *__restrict__ ks4, const
       const float4 qa = q4[2 * u], qb = q4[2 * u + 1];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
+        if (64 * i >= cnt) break;  // uniform: no position of this slot is in the row
         const int j = lane + 64 * i < cnt ? lane + 64 * i : cnt - 1;
         const uint4 k = ks4[j * KS + u];
         s[i][0] += mul_lo(k.x, qa.x);
